@@ -1,0 +1,273 @@
+"""Benchmark of the MI355X matmul / attention dispatch path.
+
+Default run (the driver's contract): one JSON line for BASELINE.json's metric
+on configs[1], the int8 x int8 -> i32 matmul M=N=K=4096 (A row-major, B
+column-major), one step = one dispatch over inputs resident in HBM. The line
+also carries the other two figures the metric names (fp16 4096^3 TFLOP/s and
+M=1 GEMV HBM GB/s), the roofline of the dominant kernel measured with HIP
+events on the stream it runs on, and the CPU baseline (the C oracle on the
+host cores, labelled "port": IREE is not installable here).
+
+--suite prints one JSON line per BASELINE config (C1..C5 and the C3 sweep).
+--tune times every compiled MFMA macro-tile on the 4096^3 shapes.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_I8_TOPS = 5000.0      # dense int8 MFMA, MI355X published
+PEAK_F16_TFLOPS = 2500.0   # dense fp16 MFMA, MI355X published
+PEAK_HBM_GBS = 8000.0      # HBM3E, MI355X published
+ROTATE_BYTES = 600 << 20   # > 2 x 256 MiB Infinity Cache
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--suite", action="store_true")
+    p.add_argument("--tune", action="store_true")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    return p.parse_args()
+
+
+def timed(fn, steps, warmup):
+    """Average ms per call of fn() over `steps` calls, HIP events on the
+    current stream (the stream every op is enqueued on)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def rotating(make, count):
+    """`count` independent copies of a device tensor, to rotate through."""
+    return [make() for _ in range(count)]
+
+
+def cpu_baseline_i8(a, bt, threads):
+    import oracle
+    t0 = time.perf_counter()
+    oracle.matmul_i8(a, bt, b_transposed=True, threads=threads)
+    dt = time.perf_counter() - t0
+    m, k = a.shape
+    n = bt.shape[0]
+    return 2.0 * m * n * k / dt / 1e12, dt
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU: every GPU box "
+                          "here has one, and the path shards without exchange "
+                          "(see the design notes); run with --gpus 1"}))
+        sys.exit(2)
+    import torch
+    import __graft_entry__ as entry
+    pkg = entry.load_package()
+    from importlib import import_module
+    inputs = import_module(entry.PKG_NAME + ".inputs")
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    if args.tune:
+        return tune(pkg, inputs, dev, args)
+    if args.suite:
+        return suite(pkg, inputs, dev, args)
+
+    # ---- headline: C2 int8 4096^3 ----
+    m = n = k = 4096
+    a, bt = inputs.c2_matmul_i8(m, n, k)
+    a_d, bt_d = a.to(dev), bt.to(dev)
+    c_d = torch.empty(m, n, dtype=torch.int32, device=dev)
+    plan = pkg.plan(pkg.make_desc(pkg.ELEM_I8, pkg.ELEM_I8, pkg.ELEM_I32, m, n,
+                                  k, pkg.B_TRANSPOSED))
+    step = lambda: pkg.matmul(a_d, bt_d, c_d, b_transposed=True)  # noqa: E731
+    ms = timed(step, args.steps, args.warmup)
+    ops = 2.0 * m * n * k
+    tops = ops / (ms * 1e-3) / 1e12
+
+    # ---- fp16 4096^3 (B transposed: the TN MFMA path) ----
+    g = torch.Generator().manual_seed(0)
+    x16 = (torch.randn(m, k, generator=g) * 0.02).half().to(dev)
+    w16 = (torch.randn(n, k, generator=g) * 0.02).half().to(dev)
+    y16 = torch.empty(m, n, dtype=torch.float16, device=dev)
+    ms16 = timed(lambda: pkg.matmul(x16, w16, y16, b_transposed=True),
+                 args.steps, args.warmup)
+    tflops16 = ops / (ms16 * 1e-3) / 1e12
+
+    # ---- GEMV M=1, N=K=4096 f16, rotating weights past the MALL ----
+    wbytes = 4096 * 4096 * 2
+    copies = max(2, ROTATE_BYTES // wbytes + 1)
+    ws = rotating(lambda: (torch.randn(4096, 4096, device=dev) * 0.02).half(),
+                  copies)
+    xv = torch.randn(1, 4096, device=dev).half()
+    yv = torch.empty(1, 4096, dtype=torch.float16, device=dev)
+    it = [0]
+
+    def gemv_step():
+        pkg.matmul(xv, ws[it[0] % copies], yv)
+        it[0] += 1
+    msv = timed(gemv_step, max(args.steps, 4 * copies), args.warmup)
+    gemv_bytes = wbytes + 4096 * 2 * 2
+    gemv_gbs = gemv_bytes / (msv * 1e-3) / 1e9
+    del ws
+
+    out = {
+        "metric": "int8/fp16 matmul TOPS/TFLOPS + % MFMA peak at 4096^3; "
+                  "GEMV HBM GB/s",
+        "value": round(tops, 1),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "i8",
+        "data": "synthetic (seeded torch generators, BASELINE configs[1])",
+        "config": {"workload": "C2 int8 matmul M=N=K=4096, A row-major, "
+                               "B column-major, i32 out",
+                   "kernel": plan.config_name.decode()},
+        "roofline": {"bound": "mfma", "achieved": round(tops, 1),
+                     "peak": PEAK_I8_TOPS, "unit": "TOPS",
+                     "frac": round(tops / PEAK_I8_TOPS, 4), "traffic": None},
+        "extra": {
+            "fp16_4096_tflops": round(tflops16, 1),
+            "fp16_4096_frac_peak": round(tflops16 / PEAK_F16_TFLOPS, 4),
+            "fp16_4096_layout": "B [N,K] (transposed), f32 acc, f16 out",
+            "gemv_m1_4096_gbs": round(gemv_gbs, 1),
+            "gemv_m1_4096_frac_hbm": round(gemv_gbs / PEAK_HBM_GBS, 4),
+            "gemv_rotating_copies": copies,
+        },
+    }
+    if not args.no_cpu_baseline:
+        threads = min(16, os.cpu_count() or 1)
+        cpu_tops, dt = cpu_baseline_i8(a.numpy(), bt.numpy(), threads)
+        out["cpu_baseline"] = {
+            "value": round(cpu_tops, 4), "unit": "TOPS", "cores": threads,
+            "kind": "port",
+            "sample": f"the full C2 4096^3 int8 matmul once ({dt:.1f} s) by "
+                      "the C oracle (OpenMP, -O3 AVX2); IREE llvm-cpu is not "
+                      "installable without network"}
+    print(json.dumps(out), flush=True)
+
+
+def suite(pkg, inputs, dev, args):
+    import torch
+    steps, warm = args.steps, args.warmup
+
+    def emit(name, ms, flops, nbytes, bound, extra=None):
+        rec = {"config": name, "ms": round(ms, 5),
+               "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+               "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1), "bound": bound}
+        peak = PEAK_HBM_GBS if bound == "hbm" else (
+            PEAK_I8_TOPS if "i8" in name else PEAK_F16_TFLOPS)
+        rec["frac"] = round((rec["gbs"] if bound == "hbm" else rec["tflops"])
+                            / peak, 4)
+        if extra:
+            rec.update(extra)
+        print(json.dumps(rec), flush=True)
+
+    a, b = (t.to(dev) for t in inputs.c1_matmul_f16())
+    c = torch.empty(128, 512, dtype=torch.float16, device=dev)
+    ms = timed(lambda: pkg.matmul(a, b, c), steps, warm)
+    emit("C1 f16 128x512x256", ms, 2 * 128 * 512 * 256, 458752, "latency")
+
+    a, bt = (t.to(dev) for t in inputs.c2_matmul_i8())
+    c = torch.empty(4096, 4096, dtype=torch.int32, device=dev)
+    ms = timed(lambda: pkg.matmul(a, bt, c, b_transposed=True), steps, warm)
+    emit("C2 i8 4096^3", ms, 2 * 4096 ** 3, 100663296, "mfma")
+    del a, bt, c
+
+    for m in (1, 16, 128, 2048):
+        for n, k in ((4096, 4096), (11008, 4096), (4096, 11008)):
+            x, w = inputs.c3_linear_f16(m, n, k)
+            wbytes = n * k * 2
+            copies = max(1, min(24, ROTATE_BYTES // wbytes + 1)) if m <= 16 else 1
+            ws = [w.to(dev)] + [w.to(dev).clone() for _ in range(copies - 1)]
+            x = x.to(dev)
+            y = torch.empty(m, n, dtype=torch.float16, device=dev)
+            it = [0]
+
+            def step():
+                pkg.matmul(x, ws[it[0] % copies], y)
+                it[0] += 1
+            ms = timed(step, max(steps, 3 * copies), warm)
+            fam = pkg.plan(pkg.make_desc(0, 0, 0, m, n, k, 0)).config_name.decode()
+            emit(f"C3 f16 M={m} N={n} K={k}", ms, 2 * m * n * k,
+                 2 * (m * k + k * n + m * n), "hbm" if m <= 16 else "mfma",
+                 {"kernel": fam, "rotating_copies": copies})
+            del ws
+
+    q, k_, v = (t.to(dev) for t in inputs.c4_attention_f16())
+    o = torch.empty_like(q)
+    ms = timed(lambda: pkg.attention(q, k_, v, o, causal=True), steps, warm)
+    emit("C4 attention causal B1 H32 S2048 D128", ms,
+         4 * 32 * 2048 * 2048 * 128 / 2, 4 * q.numel() * 2, "mfma")
+    del q, k_, v, o
+
+    for m in (1, 512):
+        x, w, s = inputs.c5_w8a16(m)
+        wbytes = w.numel()
+        copies = max(1, min(24, ROTATE_BYTES // wbytes + 1)) if m == 1 else 1
+        ws = [w.to(dev)] + [w.to(dev).clone() for _ in range(copies - 1)]
+        x, s = x.to(dev), s.to(dev)
+        y = torch.empty(m, w.shape[1], dtype=torch.float16, device=dev)
+        it = [0]
+
+        def step():
+            pkg.quantized_matmul(x, ws[it[0] % copies], s, y)
+            it[0] += 1
+        ms = timed(step, max(steps, 3 * copies), warm)
+        n, k = w.shape[1], w.shape[0]
+        emit(f"C5 w8a16 M={m} N={n} K={k}", ms, 2 * m * n * k,
+             n * k + 2 * n + 2 * m * k + 2 * m * n, "hbm" if m == 1 else "mfma",
+             {"rotating_copies": copies})
+        del ws
+
+
+def tune(pkg, inputs, dev, args):
+    import torch
+    m = n = k = 4096
+    g = torch.Generator().manual_seed(0)
+    a8 = torch.randint(-128, 128, (m, k), generator=g).to(torch.int8).to(dev)
+    b8 = torch.randint(-128, 128, (n, k), generator=g).to(torch.int8).to(dev)
+    a16 = torch.randn(m, k, generator=g).half().to(dev)
+    b16 = torch.randn(n, k, generator=g).half().to(dev)
+    for cfg in pkg.tn_configs():
+        if cfg.a_elem == pkg.ELEM_I8:
+            a, b = a8, b8
+            c = torch.empty(m, n, dtype=torch.int32, device=dev)
+        else:
+            a, b = a16, b16
+            c = torch.empty(m, n, dtype=torch.float32 if cfg.c_elem == pkg.ELEM_F32
+                            else torch.float16, device=dev)
+        ms = timed(lambda: pkg.matmul_tn_config(cfg.index, a, b, c),
+                   args.steps, args.warmup)
+        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        peak = PEAK_I8_TOPS if cfg.a_elem == pkg.ELEM_I8 else PEAK_F16_TFLOPS
+        print(json.dumps({"config": cfg.name, "ms": round(ms, 4),
+                          "tflops_or_tops": round(tf, 1),
+                          "frac": round(tf / peak, 4)}), flush=True)
+
+
+if __name__ == "__main__":
+    main()

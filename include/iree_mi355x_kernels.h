@@ -1,0 +1,140 @@
+// MI355X (gfx950) matmul / attention dispatch kernels: the C-ABI boundary.
+//
+// This header replaces the Hexagon HMX micro-kernel ABI
+// (plugins/runtime/hexagon/dsp/ukernel/hmx/api.h:16-67) for whole dispatches.
+// The reference lowers one linalg.matmul dispatch into a sequence of
+// pack / acc_clear / mma / acc_read / unpack calls per 32x32 HMX tile
+// (CG/Transforms/HexagonExpandHmxMatmul.cpp:100-343, emitted as calls by
+// CG/Conversion/HexagonHmxToLLVM.cpp:22-227). On MI355X the tile loop, the
+// staging (the VTCM plan) and the K loop live inside one HIP kernel, so the
+// callable unit is the whole matmul: each entry point below computes what one
+// matched dispatch region computes.
+//
+// Conventions (all entry points):
+//  * Pointers are device pointers to caller-owned buffers; sizes, leading
+//    dimensions (in elements) and counts are int64_t.
+//  * `stream` is a hipStream_t (NULL = the legacy default stream). Work is
+//    enqueued and the call returns without waiting; calls on different
+//    streams are independent unless they share a workspace.
+//  * Return value is an iree_mi355x_status_t; preconditions are checked on
+//    the host before anything is launched, so an error never leaves work
+//    behind. The reference ABI has no error channel (its preconditions are
+//    proven at compile time by HexagonVerifyHmxRuntimeABI.cpp:84-360); here
+//    the same checks return a status instead.
+//  * Zero-sized M or N is a no-op; K == 0 writes C_init (or zeros).
+#ifndef IREE_MI355X_KERNELS_H_
+#define IREE_MI355X_KERNELS_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum iree_mi355x_status_e {
+  IREE_MI355X_OK = 0,
+  // Null pointer, negative extent, leading dimension smaller than the row,
+  // unknown flag bit.
+  IREE_MI355X_INVALID_ARGUMENT = 1,
+  // A pointer or leading dimension breaks an alignment the kernel needs.
+  IREE_MI355X_MISALIGNED = 2,
+  // The shape/layout/flag combination has no kernel.
+  IREE_MI355X_UNSUPPORTED = 3,
+  // hipLaunchKernel (or another HIP call) failed.
+  IREE_MI355X_LAUNCH_FAILED = 4,
+  // No HIP device is visible.
+  IREE_MI355X_NO_DEVICE = 5,
+  // The caller-provided workspace is smaller than the query returned.
+  IREE_MI355X_WORKSPACE_TOO_SMALL = 6,
+} iree_mi355x_status_t;
+
+// Matmul flags: the linalg.matmul indexing-map variants the plugin matcher
+// accepts (ContractionStrategy.cpp:152-168 accepts an MxN output with either
+// B map; CG/Transforms/HexagonConvertMatmulToHmx.cpp:51-70 packs both).
+// B is stored [N, K] (indexing map (d1, d2), "column-major B").
+#define IREE_MI355X_MATMUL_B_TRANSPOSED 0x1u
+// DPS accumulate: C_out = C_init + A.B, as the HMX unpack adds the tile into
+// the init (UK/hmx.c:328-357,426-450). Without it C is overwritten, which is
+// the same result for a zero-filled init.
+#define IREE_MI355X_MATMUL_ACCUMULATE 0x2u
+// f16 matmul only: write f32 C instead of f16.
+#define IREE_MI355X_MATMUL_OUT_F32 0x4u
+
+// Attention flags.
+#define IREE_MI355X_ATTENTION_CAUSAL 0x1u
+
+// f16 x f16 matmul with f32 accumulation (inputs widened with arith.extf, as
+// in examples/matmul/matmul.mlir:1-14), f16 or f32 output rounded once at the
+// end (RNE).
+//   a: [M, K] row-major, lda >= K
+//   b: [K, N] row-major (ldb >= N) or [N, K] with B_TRANSPOSED (ldb >= K)
+//   c: [M, N] row-major, ldc >= N; f16, or f32 with OUT_F32
+// M == 1..16 dispatches to the HBM-streaming GEMV kernel.
+// Replaces iree_hexagon_hmx_pack_f16 / pack_transposed_f16 / mma_f16 /
+// acc_read_f16 / unpack_acc_f16_to_{f16,f32} (UK/api.h:28-67) as sequenced
+// by HexagonExpandHmxMatmul.cpp:286-331.
+int iree_mi355x_matmul_f16(const void *a, const void *b, void *c, int64_t m,
+                           int64_t n, int64_t k, int64_t lda, int64_t ldb,
+                           int64_t ldc, uint32_t flags, void *workspace,
+                           size_t workspace_bytes, void *stream);
+
+// i8 x i8 -> i32 matmul, exact (linalg.matmul i8,i8->i32 or
+// linalg.quantized_matmul with zero points 0). Same layouts and flags as
+// iree_mi355x_matmul_f16 except OUT_F32. The reference has no accelerator
+// kernel for it (ContractionStrategy.cpp:138-150, int8 TODO at :141); it runs
+// the generic HVX path, whose semantics this keeps bit for bit.
+int iree_mi355x_matmul_i8(const int8_t *a, const int8_t *b, int32_t *c,
+                          int64_t m, int64_t n, int64_t k, int64_t lda,
+                          int64_t ldb, int64_t ldc, uint32_t flags,
+                          void *stream);
+
+// W8A16 linear: y[m,n] = f16((sum_k f32(x[m,k]) * f32(w[k,n])) * f32(s[n])),
+// zero point 0, dequantization fused into the kernel.
+//   x: [M, K] f16 row-major; w: [K, N] int8 (or [N, K] with B_TRANSPOSED);
+//   scale: [N] f16; y: [M, N] f16.
+// No reference kernel matches a dequant-fused matmul (repo-wide); semantics
+// follow the CPU path of the same linalg form.
+int iree_mi355x_w8a16_matmul(const void *x, const int8_t *w, const void *scale,
+                             void *y, int64_t m, int64_t n, int64_t k,
+                             int64_t ldx, int64_t ldw, int64_t ldy,
+                             uint32_t flags, void *workspace,
+                             size_t workspace_bytes, void *stream);
+
+// Fused attention forward, f16 in/out, f32 scores and softmax:
+//   o = softmax(q k^T * scale + mask) v
+// q: [B, H, Sq, D], k/v: [B, H, Skv, D], o: [B, H, Sq, D], all contiguous.
+// CAUSAL masks key j for query i when j > i (top-left aligned).
+// head_dim must be 64 or 128. The reference decomposes attention into
+// batch_matmul + softmax generics (examples/attention_layer/
+// attention_layer.mlir:48-105) or, for iree_linalg_ext.attention, into an
+// online-softmax loop (CG/Pipelines/LoweringPipelines.cpp:561-595); this is
+// that online-softmax loop as one kernel.
+int iree_mi355x_attention_f16(const void *q, const void *k, const void *v,
+                              void *o, int64_t batch, int64_t heads,
+                              int64_t seq_q, int64_t seq_kv, int64_t head_dim,
+                              float scale, uint32_t flags, void *stream);
+
+// Workspace a matmul_f16 / w8a16_matmul call of this shape needs (split-K
+// partials and arrival counters), 0 if none. Mirrors the scratch query of the
+// reference's caller-scratch matmul, hexkl_matmul_f16f16_f32_scratch_bytes
+// (CG/Conversion/HexagonRuntimeLinking.h:35-38). Passing workspace == NULL
+// makes the library use its own per-device workspace (allocated once, grown on
+// demand); a caller workspace must be zero-filled before its first use and is
+// left zero-filled in its counter region after every call.
+size_t iree_mi355x_matmul_workspace_bytes(int64_t m, int64_t n, int64_t k,
+                                          uint32_t flags);
+
+// Last error message recorded on this thread (empty string if none).
+const char *iree_mi355x_last_error(void);
+
+// Library version string and the number of visible devices (0 without GPU);
+// neither launches work.
+const char *iree_mi355x_version(void);
+int iree_mi355x_device_count(void);
+
+#ifdef __cplusplus
+}  // extern "C"
+#endif
+
+#endif  // IREE_MI355X_KERNELS_H_

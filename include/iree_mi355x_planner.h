@@ -1,0 +1,104 @@
+// Dispatch classification and gfx950 tile planning for matched matmul
+// dispatches. Host-only: no HIP call, usable without a GPU.
+//
+// Replaces the reference's HMX strategy selection and VTCM tile search:
+//  * iree_mi355x_classify_matmul  <- isHmxCandidateContraction /
+//    hasHmxElementTypes / isHmxLowerableMatmul / selectHmxStrategy
+//    (CG/Strategy/Planning/Strategies/ContractionStrategy.cpp:133-213),
+//    extended to the int8 and W8A16 dispatches HMX does not take (:141);
+//  * iree_mi355x_plan_matmul      <- selectHmxTileSizes + planVTCMTiling
+//    (CG/Strategy/Planning/VTCMPlanning.cpp:156-329) with the 2 MiB VTCM
+//    budget (CG/Pipelines/TranslationPipeline.cpp:28-34) replaced by the
+//    160 KiB LDS of one gfx950 CU, and the candidates by the compiled MFMA
+//    macro-tiles. The ranking keeps the reference's order (in budget, least
+//    global traffic, fewest tiles, larger N) with one key added first: the
+//    per-CU critical-path work ceil(tiles / CUs) * BM * BN, since 256 CUs run
+//    the tiles in parallel where the DSP ran them in sequence
+//    (RT/dsp/command_buffer.c:670-719). A measured table (autotuner) is
+//    consulted before the ranking.
+#ifndef IREE_MI355X_PLANNER_H_
+#define IREE_MI355X_PLANNER_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum iree_mi355x_elem_e {
+  IREE_MI355X_ELEM_F16 = 0,
+  IREE_MI355X_ELEM_I8 = 1,
+  IREE_MI355X_ELEM_I32 = 2,
+  IREE_MI355X_ELEM_F32 = 3,
+} iree_mi355x_elem_t;
+
+typedef enum iree_mi355x_family_e {
+  IREE_MI355X_FAMILY_NONE = 0,     // not a dispatch this library takes
+  IREE_MI355X_FAMILY_MFMA_TN = 1,  // LDS-DMA MFMA macro-tile kernel
+  IREE_MI355X_FAMILY_GENERAL = 2,  // bounds-checked MFMA kernel, any shape
+  IREE_MI355X_FAMILY_GEMV = 3,     // HBM-streaming skinny kernel (M <= 4)
+} iree_mi355x_family_t;
+
+typedef struct iree_mi355x_matmul_desc_t {
+  int32_t a_elem, b_elem, c_elem;  // iree_mi355x_elem_t
+  int64_t m, n, k;
+  uint32_t flags;            // IREE_MI355X_MATMUL_* (kernels header)
+  int32_t a_aligned16;       // A base and row pitch are 16-byte aligned
+  int32_t b_aligned16;       // B base and row pitch are 16-byte aligned
+  int32_t has_scale;         // per-column f16 scale (W8A16)
+  int64_t lds_budget_bytes;  // per-workgroup LDS budget (default 160 KiB)
+  int32_t num_cus;           // CUs the tiles spread over (default 256)
+} iree_mi355x_matmul_desc_t;
+
+typedef struct iree_mi355x_matmul_plan_t {
+  int32_t family;        // iree_mi355x_family_t
+  int32_t config_index;  // MFMA_TN: index into the compiled config table
+  char config_name[64];
+  int64_t tile_m, tile_n, tile_k;  // workgroup macro-tile (the VTCM tile)
+  int64_t lds_bytes;               // LDS per workgroup
+  int64_t workgroups;
+  int32_t threads;                 // threads per workgroup
+  int32_t splits;                  // GEMV K splits
+  int64_t workspace_bytes;
+  int64_t traffic_bytes;           // modeled global->LDS bytes of the plan
+  int32_t from_tuned_table;        // 1 if a measured entry chose it
+} iree_mi355x_matmul_plan_t;
+
+// Fills defaults: both operands assumed 16-byte aligned, no scale, 160 KiB
+// LDS, 256 CUs.
+void iree_mi355x_matmul_desc_init(iree_mi355x_matmul_desc_t *desc,
+                                  int32_t a_elem, int32_t b_elem,
+                                  int32_t c_elem, int64_t m, int64_t n,
+                                  int64_t k, uint32_t flags);
+
+// Which kernel family takes the dispatch (FAMILY_NONE for element types no
+// kernel computes). Mirrors the HMX eligibility rules, see above.
+int32_t iree_mi355x_classify_matmul(const iree_mi355x_matmul_desc_t *desc);
+
+// Full plan: family, macro-tile, resources. Returns 0 (IREE_MI355X_OK) or
+// IREE_MI355X_UNSUPPORTED.
+int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *desc,
+                            iree_mi355x_matmul_plan_t *plan);
+
+// The compiled MFMA_TN configurations (for the autotuner and the library
+// export table): name, macro-tile and LDS bytes of entry `index`.
+int iree_mi355x_tn_config_count(void);
+int iree_mi355x_tn_config_info(int index, const char **name, int32_t *a_elem,
+                               int32_t *c_elem, int64_t *tile_m,
+                               int64_t *tile_n, int64_t *tile_k,
+                               int64_t *lds_bytes, int32_t *threads);
+
+// Launch one compiled MFMA_TN configuration by index on an eligible shape
+// (autotuner entry). Same argument meaning as iree_mi355x_matmul_f16/_i8;
+// returns IREE_MI355X_UNSUPPORTED if the shape does not tile exactly.
+int iree_mi355x_matmul_tn_config(int index, const void *a, const void *b,
+                                 void *c, int64_t m, int64_t n, int64_t k,
+                                 int64_t lda, int64_t ldb, int64_t ldc,
+                                 uint32_t flags, void *stream);
+
+#ifdef __cplusplus
+}  // extern "C"
+#endif
+
+#endif  // IREE_MI355X_PLANNER_H_

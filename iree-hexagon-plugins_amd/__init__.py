@@ -1,0 +1,402 @@
+"""MI355X (gfx950) matmul / attention dispatch library: Python host binding.
+
+A thin ctypes layer over ``lib/libiree_mi355x.so``, the C-ABI declared in
+``include/iree_mi355x_kernels.h``, ``include/iree_mi355x_planner.h`` and
+``include/iree_mi355x_executable_library.h``. Device buffers are torch tensors
+(torch is the device-memory and stream plumbing); every op enqueues on the
+current torch stream and returns without synchronizing.
+
+There is no fallback: if the native library is missing the import of a
+binding raises, and every call goes to the HIP kernels.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import struct
+from dataclasses import dataclass
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libiree_mi355x.so")
+
+# Status codes (iree_mi355x_status_t).
+OK = 0
+INVALID_ARGUMENT = 1
+MISALIGNED = 2
+UNSUPPORTED = 3
+LAUNCH_FAILED = 4
+NO_DEVICE = 5
+WORKSPACE_TOO_SMALL = 6
+STATUS_NAMES = {
+    OK: "OK", INVALID_ARGUMENT: "INVALID_ARGUMENT", MISALIGNED: "MISALIGNED",
+    UNSUPPORTED: "UNSUPPORTED", LAUNCH_FAILED: "LAUNCH_FAILED",
+    NO_DEVICE: "NO_DEVICE", WORKSPACE_TOO_SMALL: "WORKSPACE_TOO_SMALL",
+}
+
+# Flags.
+B_TRANSPOSED = 0x1
+ACCUMULATE = 0x2
+OUT_F32 = 0x4
+CAUSAL = 0x1
+
+# Element kinds (iree_mi355x_elem_t) and kernel families.
+ELEM_F16, ELEM_I8, ELEM_I32, ELEM_F32 = 0, 1, 2, 3
+FAMILY_NONE, FAMILY_MFMA_TN, FAMILY_GENERAL, FAMILY_GEMV = 0, 1, 2, 3
+FAMILY_NAMES = {FAMILY_NONE: "none", FAMILY_MFMA_TN: "mfma_tn",
+                FAMILY_GENERAL: "general", FAMILY_GEMV: "gemv"}
+
+EXECUTABLE_LIBRARY_VERSION = 0x4D490001
+
+# Every symbol the C-ABI headers declare (checked by the CPU tests).
+EXPORTED_SYMBOLS = (
+    "iree_mi355x_matmul_f16", "iree_mi355x_matmul_i8",
+    "iree_mi355x_w8a16_matmul", "iree_mi355x_attention_f16",
+    "iree_mi355x_matmul_workspace_bytes", "iree_mi355x_last_error",
+    "iree_mi355x_version", "iree_mi355x_device_count",
+    "iree_mi355x_matmul_desc_init", "iree_mi355x_classify_matmul",
+    "iree_mi355x_plan_matmul", "iree_mi355x_tn_config_count",
+    "iree_mi355x_tn_config_info", "iree_mi355x_matmul_tn_config",
+    "iree_mi355x_executable_library_query",
+)
+
+
+class MI355XError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        self.status = status
+        super().__init__(f"{STATUS_NAMES.get(status, status)}: {message}")
+
+
+class MatmulDesc(ctypes.Structure):
+    _fields_ = [("a_elem", ctypes.c_int32), ("b_elem", ctypes.c_int32),
+                ("c_elem", ctypes.c_int32), ("m", ctypes.c_int64),
+                ("n", ctypes.c_int64), ("k", ctypes.c_int64),
+                ("flags", ctypes.c_uint32), ("a_aligned16", ctypes.c_int32),
+                ("b_aligned16", ctypes.c_int32), ("has_scale", ctypes.c_int32),
+                ("lds_budget_bytes", ctypes.c_int64),
+                ("num_cus", ctypes.c_int32)]
+
+
+class MatmulPlan(ctypes.Structure):
+    _fields_ = [("family", ctypes.c_int32), ("config_index", ctypes.c_int32),
+                ("config_name", ctypes.c_char * 64), ("tile_m", ctypes.c_int64),
+                ("tile_n", ctypes.c_int64), ("tile_k", ctypes.c_int64),
+                ("lds_bytes", ctypes.c_int64), ("workgroups", ctypes.c_int64),
+                ("threads", ctypes.c_int32), ("splits", ctypes.c_int32),
+                ("workspace_bytes", ctypes.c_int64),
+                ("traffic_bytes", ctypes.c_int64),
+                ("from_tuned_table", ctypes.c_int32)]
+
+
+class DispatchState(ctypes.Structure):
+    _fields_ = [("constant_count", ctypes.c_uint32),
+                ("constants", ctypes.POINTER(ctypes.c_uint32)),
+                ("binding_count", ctypes.c_uint32),
+                ("binding_ptrs", ctypes.POINTER(ctypes.c_void_p)),
+                ("binding_lengths", ctypes.POINTER(ctypes.c_size_t)),
+                ("stream", ctypes.c_void_p)]
+
+
+DISPATCH_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p,
+                               ctypes.POINTER(DispatchState))
+
+
+class DispatchAttrs(ctypes.Structure):
+    _fields_ = [("flags", ctypes.c_uint64), ("lds_bytes", ctypes.c_uint64),
+                ("threads", ctypes.c_uint64)]
+
+
+class ExportTable(ctypes.Structure):
+    _fields_ = [("count", ctypes.c_uint32),
+                ("ptrs", ctypes.POINTER(ctypes.c_void_p)),
+                ("attrs", ctypes.POINTER(DispatchAttrs)),
+                ("names", ctypes.POINTER(ctypes.c_char_p))]
+
+
+class ImportTable(ctypes.Structure):
+    _fields_ = [("count", ctypes.c_uint32),
+                ("symbols", ctypes.POINTER(ctypes.c_char_p))]
+
+
+class LibraryHeader(ctypes.Structure):
+    _fields_ = [("version", ctypes.c_uint32), ("name", ctypes.c_char_p)]
+
+
+class Library(ctypes.Structure):
+    _fields_ = [("header", ctypes.POINTER(LibraryHeader)),
+                ("imports", ImportTable), ("exports", ExportTable)]
+
+
+_lib = None
+
+
+def _share_hip_runtime() -> None:
+    # torch ships its own libamdhip64; importing it first makes the native
+    # library bind to that same runtime, so one process has one HIP runtime
+    # and torch's device pointers and streams are valid in both.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
+def library():
+    """Load (once) and return the native library; raise if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"native library {LIB_PATH} is not built; run "
+            "`python -c 'import __graft_entry__ as g; g.build()'`")
+    _share_hip_runtime()
+    lib = ctypes.CDLL(LIB_PATH)
+    p, i64, u32, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_uint32, ctypes.c_size_t
+    lib.iree_mi355x_matmul_f16.argtypes = [p, p, p, i64, i64, i64, i64, i64,
+                                           i64, u32, p, sz, p]
+    lib.iree_mi355x_matmul_i8.argtypes = [p, p, p, i64, i64, i64, i64, i64,
+                                          i64, u32, p]
+    lib.iree_mi355x_w8a16_matmul.argtypes = [p, p, p, p, i64, i64, i64, i64,
+                                             i64, i64, u32, p, sz, p]
+    lib.iree_mi355x_attention_f16.argtypes = [p, p, p, p, i64, i64, i64, i64,
+                                              i64, ctypes.c_float, u32, p]
+    lib.iree_mi355x_matmul_workspace_bytes.restype = sz
+    lib.iree_mi355x_matmul_workspace_bytes.argtypes = [i64, i64, i64, u32]
+    lib.iree_mi355x_last_error.restype = ctypes.c_char_p
+    lib.iree_mi355x_version.restype = ctypes.c_char_p
+    lib.iree_mi355x_matmul_desc_init.restype = None
+    lib.iree_mi355x_matmul_desc_init.argtypes = [
+        ctypes.POINTER(MatmulDesc), ctypes.c_int32, ctypes.c_int32,
+        ctypes.c_int32, i64, i64, i64, u32]
+    lib.iree_mi355x_classify_matmul.argtypes = [ctypes.POINTER(MatmulDesc)]
+    lib.iree_mi355x_plan_matmul.argtypes = [ctypes.POINTER(MatmulDesc),
+                                            ctypes.POINTER(MatmulPlan)]
+    lib.iree_mi355x_tn_config_info.argtypes = [
+        ctypes.c_int, ctypes.POINTER(ctypes.c_char_p),
+        ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
+        ctypes.POINTER(i64), ctypes.POINTER(i64), ctypes.POINTER(i64),
+        ctypes.POINTER(i64), ctypes.POINTER(ctypes.c_int32)]
+    lib.iree_mi355x_matmul_tn_config.argtypes = [ctypes.c_int, p, p, p, i64,
+                                                 i64, i64, i64, i64, i64, u32,
+                                                 p]
+    lib.iree_mi355x_executable_library_query.restype = ctypes.c_void_p
+    lib.iree_mi355x_executable_library_query.argtypes = [u32, p]
+    _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    return library().iree_mi355x_last_error().decode()
+
+
+def _check(status: int) -> None:
+    if status != OK:
+        raise MI355XError(status, last_error())
+
+
+# ------------------------------------------------------------------ planner --
+
+def make_desc(a_elem, b_elem, c_elem, m, n, k, flags=0, *, has_scale=False,
+              aligned=True, lds_budget_bytes=None) -> MatmulDesc:
+    d = MatmulDesc()
+    library().iree_mi355x_matmul_desc_init(ctypes.byref(d), a_elem, b_elem,
+                                           c_elem, m, n, k, flags)
+    d.has_scale = int(has_scale)
+    d.a_aligned16 = d.b_aligned16 = int(aligned)
+    if lds_budget_bytes is not None:
+        d.lds_budget_bytes = lds_budget_bytes
+    return d
+
+
+def classify(desc: MatmulDesc) -> int:
+    return library().iree_mi355x_classify_matmul(ctypes.byref(desc))
+
+
+def plan(desc: MatmulDesc) -> MatmulPlan:
+    out = MatmulPlan()
+    _check(library().iree_mi355x_plan_matmul(ctypes.byref(desc),
+                                             ctypes.byref(out)))
+    return out
+
+
+@dataclass
+class TnConfig:
+    index: int
+    name: str
+    a_elem: int
+    c_elem: int
+    tile_m: int
+    tile_n: int
+    tile_k: int
+    lds_bytes: int
+    threads: int
+
+
+def tn_configs() -> list[TnConfig]:
+    lib = library()
+    out = []
+    for i in range(lib.iree_mi355x_tn_config_count()):
+        name = ctypes.c_char_p()
+        ae, ce, th = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+        tm, tn, tk, lds = (ctypes.c_int64() for _ in range(4))
+        _check(lib.iree_mi355x_tn_config_info(
+            i, ctypes.byref(name), ctypes.byref(ae), ctypes.byref(ce),
+            ctypes.byref(tm), ctypes.byref(tn), ctypes.byref(tk),
+            ctypes.byref(lds), ctypes.byref(th)))
+        out.append(TnConfig(i, name.value.decode(), ae.value, ce.value,
+                            tm.value, tn.value, tk.value, lds.value, th.value))
+    return out
+
+
+# ----------------------------------------------------------- library table --
+
+def executable_library(version: int = EXECUTABLE_LIBRARY_VERSION):
+    """The export table (or None if `version` does not match)."""
+    addr = library().iree_mi355x_executable_library_query(version, None)
+    if not addr:
+        return None
+    return ctypes.cast(addr, ctypes.POINTER(Library)).contents
+
+
+def export_names() -> list[str]:
+    lib = executable_library()
+    return [lib.exports.names[i].decode() for i in range(lib.exports.count)]
+
+
+def call_export(name: str, constants, bindings, binding_lengths, stream=None):
+    """Invoke an export's dispatch function; returns the status code."""
+    lib = executable_library()
+    names = export_names()
+    idx = names.index(name)
+    fn = DISPATCH_FN(lib.exports.ptrs[idx])
+    consts = (ctypes.c_uint32 * len(constants))(*constants)
+    ptrs = (ctypes.c_void_p * len(bindings))(*bindings)
+    lens = (ctypes.c_size_t * len(binding_lengths))(*binding_lengths)
+    state = DispatchState(len(constants), consts, len(bindings), ptrs, lens,
+                          stream)
+    return fn(None, ctypes.byref(state))
+
+
+def matmul_constants(m, n, k, lda, ldb, ldc, flags):
+    words = []
+    for v in (m, n, k, lda, ldb, ldc):
+        words += [v & 0xFFFFFFFF, (v >> 32) & 0xFFFFFFFF]
+    return words + [flags]
+
+
+def attention_constants(batch, heads, seq_q, seq_kv, head_dim, scale, flags):
+    scale_bits = struct.unpack("<I", struct.pack("<f", scale))[0]
+    return [batch, heads, seq_q, seq_kv, head_dim, scale_bits, flags]
+
+
+# --------------------------------------------------------------- operators --
+
+def _stream_ptr(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def _require(t, dtype, name):
+    import torch
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise TypeError(f"{name} must be a device tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be 2-D with unit column stride")
+
+
+def matmul(a, b, c=None, *, b_transposed=False, accumulate=False,
+           out_dtype=None, stream=None):
+    """linalg.matmul dispatch: C = [C +] A . B on the MI355X kernels.
+
+    f16 inputs accumulate in f32 and write f16 (or f32 with
+    out_dtype=torch.float32); int8 inputs accumulate exactly into int32.
+    ``b_transposed``: B is stored [N, K].
+    """
+    import torch
+    lib = library()
+    if a.dtype == torch.int8:
+        _require(a, torch.int8, "a")
+        _require(b, torch.int8, "b")
+        out_dtype = torch.int32
+    else:
+        _require(a, torch.float16, "a")
+        _require(b, torch.float16, "b")
+        out_dtype = out_dtype or torch.float16
+    m, k = a.shape
+    n = b.shape[0] if b_transposed else b.shape[1]
+    if (b.shape[1] if b_transposed else b.shape[0]) != k:
+        raise ValueError("contraction extents differ")
+    if c is None:
+        if accumulate:
+            raise ValueError("accumulate needs an init tensor c")
+        c = torch.empty((m, n), dtype=out_dtype, device=a.device)
+    else:
+        _require(c, out_dtype, "c")
+    flags = (B_TRANSPOSED if b_transposed else 0) | (ACCUMULATE if accumulate else 0)
+    s = _stream_ptr(stream)
+    if a.dtype == torch.int8:
+        _check(lib.iree_mi355x_matmul_i8(a.data_ptr(), b.data_ptr(),
+                                         c.data_ptr(), m, n, k, a.stride(0),
+                                         b.stride(0), c.stride(0), flags, s))
+    else:
+        if out_dtype == torch.float32:
+            flags |= OUT_F32
+        _check(lib.iree_mi355x_matmul_f16(a.data_ptr(), b.data_ptr(),
+                                          c.data_ptr(), m, n, k, a.stride(0),
+                                          b.stride(0), c.stride(0), flags,
+                                          None, 0, s))
+    return c
+
+
+def quantized_matmul(x, w, scale, y=None, *, w_transposed=False, stream=None):
+    """W8A16 linear: y = f16((x . w_int8) * scale[n]), zero point 0."""
+    import torch
+    lib = library()
+    _require(x, torch.float16, "x")
+    _require(w, torch.int8, "w")
+    m, k = x.shape
+    n = w.shape[0] if w_transposed else w.shape[1]
+    if scale.dtype != torch.float16 or scale.numel() != n or not scale.is_contiguous():
+        raise ValueError("scale must be a contiguous f16 vector of N")
+    if y is None:
+        y = torch.empty((m, n), dtype=torch.float16, device=x.device)
+    _check(lib.iree_mi355x_w8a16_matmul(
+        x.data_ptr(), w.data_ptr(), scale.data_ptr(), y.data_ptr(), m, n, k,
+        x.stride(0), w.stride(0), y.stride(0),
+        B_TRANSPOSED if w_transposed else 0, None, 0, _stream_ptr(stream)))
+    return y
+
+
+def attention(q, k, v, o=None, *, causal=True, scale=None, stream=None):
+    """Fused attention forward on [B, H, S, D] f16 tensors (contiguous)."""
+    import torch
+    lib = library()
+    for t, nm in ((q, "q"), (k, "k"), (v, "v")):
+        if t.dtype != torch.float16 or not t.is_cuda or not t.is_contiguous() or t.dim() != 4:
+            raise TypeError(f"{nm} must be a contiguous [B,H,S,D] f16 device tensor")
+    b, h, sq, d = q.shape
+    skv = k.shape[2]
+    if scale is None:
+        scale = d ** -0.5
+    if o is None:
+        o = torch.empty_like(q)
+    _check(lib.iree_mi355x_attention_f16(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), b, h, sq, skv,
+        d, float(scale), CAUSAL if causal else 0, _stream_ptr(stream)))
+    return o
+
+
+def matmul_tn_config(index, a, b, c, *, stream=None):
+    """Run one compiled MFMA_TN configuration (autotuner entry point)."""
+    m, k = a.shape
+    n = b.shape[0]
+    flags = B_TRANSPOSED
+    import torch
+    if c.dtype == torch.float32 and a.dtype == torch.float16:
+        flags |= OUT_F32
+    _check(library().iree_mi355x_matmul_tn_config(
+        index, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, a.stride(0),
+        b.stride(0), c.stride(0), flags, _stream_ptr(stream)))
+    return c

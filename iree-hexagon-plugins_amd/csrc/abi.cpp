@@ -1,0 +1,307 @@
+// C-ABI entry points (include/iree_mi355x_kernels.h): host-side argument
+// checks, kernel selection and launch.
+//
+// The reference proves its kernels' preconditions at compile time
+// (CG/Transforms/HexagonVerifyHmxRuntimeABI.cpp:84-360: placement, row-major
+// layout, 64/128/2048-byte alignment, extents that fit) and its kernels have
+// no error channel (UK/api.h). Here every check runs on the host before
+// launch and reports an iree_mi355x_status_t; nothing is launched on error.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "../../include/iree_mi355x_kernels.h"
+#include "../../include/iree_mi355x_planner.h"
+#include "kernels_internal.h"
+
+namespace ihp {
+
+static thread_local char g_last_error[512];
+
+int fail(int status, const char *fmt, ...) {
+  va_list args;
+  va_start(args, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, args);
+  va_end(args);
+  return status;
+}
+
+static int ok() {
+  g_last_error[0] = 0;
+  return IREE_MI355X_OK;
+}
+
+static bool aligned(const void *p, size_t a) {
+  return ((uintptr_t)p % a) == 0;
+}
+
+static const int64_t kMaxExtent = (int64_t)1 << 31;
+
+// Library-owned workspace, one per device, zero-filled when (re)allocated.
+// Calls that share it must be ordered (same stream or synchronized).
+struct DeviceWorkspace {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+};
+static std::mutex g_ws_mutex;
+static std::vector<DeviceWorkspace> g_ws;
+
+static int library_workspace(size_t need, void **out) {
+  *out = nullptr;
+  if (need == 0)
+    return IREE_MI355X_OK;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess)
+    return fail(IREE_MI355X_NO_DEVICE, "hipGetDevice failed");
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  if ((int)g_ws.size() <= dev)
+    g_ws.resize(dev + 1);
+  DeviceWorkspace &ws = g_ws[dev];
+  if (ws.bytes < need) {
+    size_t grow = need < ((size_t)64 << 20) ? ((size_t)64 << 20) : need;
+    if (ws.ptr) {
+      // Work queued on any stream may still use the old buffer.
+      if (hipDeviceSynchronize() != hipSuccess || hipFree(ws.ptr) != hipSuccess)
+        return fail(IREE_MI355X_LAUNCH_FAILED, "workspace release failed");
+      ws.ptr = nullptr;
+      ws.bytes = 0;
+    }
+    if (hipMalloc(&ws.ptr, grow) != hipSuccess)
+      return fail(IREE_MI355X_LAUNCH_FAILED, "workspace hipMalloc(%zu) failed",
+                  grow);
+    if (hipMemset(ws.ptr, 0, grow) != hipSuccess)
+      return fail(IREE_MI355X_LAUNCH_FAILED, "workspace hipMemset failed");
+    ws.bytes = grow;
+  }
+  *out = ws.ptr;
+  return IREE_MI355X_OK;
+}
+
+static int launch_status(hipError_t e, const char *what) {
+  if (e != hipSuccess)
+    return fail(IREE_MI355X_LAUNCH_FAILED, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+// Shared shape / stride checks for the three matmul entry points.
+static int check_matmul(const char *who, const void *a, const void *b,
+                        void *c, int64_t m, int64_t n, int64_t k, int64_t lda,
+                        int64_t ldb, int64_t ldc, uint32_t flags,
+                        uint32_t allowed_flags, size_t a_elem, size_t b_elem,
+                        size_t c_elem) {
+  if (flags & ~allowed_flags)
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: unknown flag bits 0x%x", who,
+                flags & ~allowed_flags);
+  if (m < 0 || n < 0 || k < 0)
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: negative extent", who);
+  if (m >= kMaxExtent || n >= kMaxExtent || k >= kMaxExtent)
+    return fail(IREE_MI355X_UNSUPPORTED, "%s: extent >= 2^31", who);
+  if (m == 0 || n == 0)
+    return IREE_MI355X_OK;
+  const bool bt = flags & IREE_MI355X_MATMUL_B_TRANSPOSED;
+  if (!c || (k > 0 && (!a || !b)))
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: null pointer", who);
+  if (lda < k || ldb < (bt ? k : n) || ldc < n || lda < 0 || ldb < 0)
+    return fail(IREE_MI355X_INVALID_ARGUMENT,
+                "%s: leading dimension smaller than the row", who);
+  if ((a && !aligned(a, a_elem)) || (b && !aligned(b, b_elem)) ||
+      !aligned(c, c_elem))
+    return fail(IREE_MI355X_MISALIGNED,
+                "%s: pointer not aligned to its element size", who);
+  return IREE_MI355X_OK;
+}
+
+}  // namespace ihp
+
+using namespace ihp;
+
+extern "C" {
+
+const char *iree_mi355x_last_error(void) { return g_last_error; }
+
+const char *iree_mi355x_version(void) { return "iree-mi355x 0.1 gfx950"; }
+
+int iree_mi355x_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess)
+    return 0;
+  return n;
+}
+
+size_t iree_mi355x_matmul_workspace_bytes(int64_t m, int64_t n, int64_t k,
+                                          uint32_t flags) {
+  if (m <= 0 || n <= 0 || k <= 0 || m > kGemvMaxRows ||
+      (flags & IREE_MI355X_MATMUL_B_TRANSPOSED))
+    return 0;
+  size_t f16b = gemv_workspace_bytes(m, n, k, 2);
+  size_t i8b = gemv_workspace_bytes(m, n, k, 1);
+  return f16b > i8b ? f16b : i8b;
+}
+
+int iree_mi355x_matmul_f16(const void *a, const void *b, void *c, int64_t m,
+                           int64_t n, int64_t k, int64_t lda, int64_t ldb,
+                           int64_t ldc, uint32_t flags, void *workspace,
+                           size_t workspace_bytes, void *stream) {
+  const bool out_f32 = flags & IREE_MI355X_MATMUL_OUT_F32;
+  int st = check_matmul("matmul_f16", a, b, c, m, n, k, lda, ldb, ldc, flags,
+                        IREE_MI355X_MATMUL_B_TRANSPOSED |
+                            IREE_MI355X_MATMUL_ACCUMULATE |
+                            IREE_MI355X_MATMUL_OUT_F32,
+                        2, 2, out_f32 ? 4 : 2);
+  if (st != IREE_MI355X_OK || m == 0 || n == 0)
+    return st == IREE_MI355X_OK ? ok() : st;
+  MatmulArgs args{a, b, c, m, n, k, lda, ldb, ldc,
+                  (flags & IREE_MI355X_MATMUL_B_TRANSPOSED) ? 1 : 0,
+                  (flags & IREE_MI355X_MATMUL_ACCUMULATE) ? 1 : 0, stream};
+  iree_mi355x_matmul_desc_t desc;
+  iree_mi355x_matmul_desc_init(&desc, IREE_MI355X_ELEM_F16,
+                               IREE_MI355X_ELEM_F16,
+                               out_f32 ? IREE_MI355X_ELEM_F32
+                                       : IREE_MI355X_ELEM_F16,
+                               m, n, k, flags);
+  desc.a_aligned16 = aligned(a, 16) && (lda * 2) % 16 == 0;
+  desc.b_aligned16 = aligned(b, 16) && (ldb * 2) % 16 == 0;
+  iree_mi355x_matmul_plan_t plan;
+  if (iree_mi355x_plan_matmul(&desc, &plan) != IREE_MI355X_OK)
+    return fail(IREE_MI355X_UNSUPPORTED, "matmul_f16: no plan");
+  switch (plan.family) {
+    case IREE_MI355X_FAMILY_GEMV: {
+      void *ws = workspace;
+      if (plan.workspace_bytes > 0) {
+        if (ws && workspace_bytes < plan.workspace_bytes)
+          return fail(IREE_MI355X_WORKSPACE_TOO_SMALL,
+                      "matmul_f16: workspace %zu < %zu", workspace_bytes,
+                      (size_t)plan.workspace_bytes);
+        if (!ws && (st = library_workspace(plan.workspace_bytes, &ws)) !=
+                       IREE_MI355X_OK)
+          return st;
+      }
+      return launch_status(launch_gemv(args, 2, nullptr, out_f32, ws),
+                           "gemv_f16");
+    }
+    case IREE_MI355X_FAMILY_MFMA_TN: {
+      int count = 0;
+      const TnConfig *cfgs = tn_configs(&count);
+      return launch_status(cfgs[plan.config_index].launch(args),
+                           cfgs[plan.config_index].name);
+    }
+    default:
+      return launch_status(
+          launch_general(args, out_f32 ? kGeneralF16F32 : kGeneralF16F16,
+                         nullptr),
+          "gemm_general_f16");
+  }
+}
+
+int iree_mi355x_matmul_i8(const int8_t *a, const int8_t *b, int32_t *c,
+                          int64_t m, int64_t n, int64_t k, int64_t lda,
+                          int64_t ldb, int64_t ldc, uint32_t flags,
+                          void *stream) {
+  int st = check_matmul("matmul_i8", a, b, c, m, n, k, lda, ldb, ldc, flags,
+                        IREE_MI355X_MATMUL_B_TRANSPOSED |
+                            IREE_MI355X_MATMUL_ACCUMULATE,
+                        1, 1, 4);
+  if (st != IREE_MI355X_OK || m == 0 || n == 0)
+    return st == IREE_MI355X_OK ? ok() : st;
+  MatmulArgs args{a, b, c, m, n, k, lda, ldb, ldc,
+                  (flags & IREE_MI355X_MATMUL_B_TRANSPOSED) ? 1 : 0,
+                  (flags & IREE_MI355X_MATMUL_ACCUMULATE) ? 1 : 0, stream};
+  iree_mi355x_matmul_desc_t desc;
+  iree_mi355x_matmul_desc_init(&desc, IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_I8,
+                               IREE_MI355X_ELEM_I32, m, n, k, flags);
+  desc.a_aligned16 = aligned(a, 16) && lda % 16 == 0;
+  desc.b_aligned16 = aligned(b, 16) && ldb % 16 == 0;
+  iree_mi355x_matmul_plan_t plan;
+  if (iree_mi355x_plan_matmul(&desc, &plan) != IREE_MI355X_OK)
+    return fail(IREE_MI355X_UNSUPPORTED, "matmul_i8: no plan");
+  if (plan.family == IREE_MI355X_FAMILY_MFMA_TN) {
+    int count = 0;
+    const TnConfig *cfgs = tn_configs(&count);
+    return launch_status(cfgs[plan.config_index].launch(args),
+                         cfgs[plan.config_index].name);
+  }
+  return launch_status(launch_general(args, kGeneralI8I32, nullptr),
+                       "gemm_general_i8");
+}
+
+int iree_mi355x_w8a16_matmul(const void *x, const int8_t *w, const void *scale,
+                             void *y, int64_t m, int64_t n, int64_t k,
+                             int64_t ldx, int64_t ldw, int64_t ldy,
+                             uint32_t flags, void *workspace,
+                             size_t workspace_bytes, void *stream) {
+  int st = check_matmul("w8a16_matmul", x, w, y, m, n, k, ldx, ldw, ldy, flags,
+                        IREE_MI355X_MATMUL_B_TRANSPOSED, 2, 1, 2);
+  if (st != IREE_MI355X_OK || m == 0 || n == 0)
+    return st == IREE_MI355X_OK ? ok() : st;
+  if (!scale)
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "w8a16_matmul: null scale");
+  if (!aligned(scale, 2))
+    return fail(IREE_MI355X_MISALIGNED, "w8a16_matmul: scale misaligned");
+  MatmulArgs args{x, w, y, m, n, k, ldx, ldw, ldy,
+                  (flags & IREE_MI355X_MATMUL_B_TRANSPOSED) ? 1 : 0, 0, stream};
+  iree_mi355x_matmul_desc_t desc;
+  iree_mi355x_matmul_desc_init(&desc, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_I8,
+                               IREE_MI355X_ELEM_F16, m, n, k, flags);
+  desc.a_aligned16 = aligned(x, 16) && (ldx * 2) % 16 == 0;
+  desc.b_aligned16 = aligned(w, 16) && ldw % 16 == 0;
+  desc.has_scale = 1;
+  iree_mi355x_matmul_plan_t plan;
+  if (iree_mi355x_plan_matmul(&desc, &plan) != IREE_MI355X_OK)
+    return fail(IREE_MI355X_UNSUPPORTED, "w8a16_matmul: no plan");
+  if (plan.family == IREE_MI355X_FAMILY_GEMV) {
+    void *ws = workspace;
+    if (plan.workspace_bytes > 0) {
+      if (ws && workspace_bytes < plan.workspace_bytes)
+        return fail(IREE_MI355X_WORKSPACE_TOO_SMALL,
+                    "w8a16_matmul: workspace %zu < %zu", workspace_bytes,
+                    (size_t)plan.workspace_bytes);
+      if (!ws && (st = library_workspace(plan.workspace_bytes, &ws)) !=
+                     IREE_MI355X_OK)
+        return st;
+    }
+    return launch_status(launch_gemv(args, 1, scale, 0, ws), "gemv_w8a16");
+  }
+  return launch_status(launch_general(args, kGeneralW8A16, scale),
+                       "gemm_general_w8a16");
+}
+
+int iree_mi355x_attention_f16(const void *q, const void *k, const void *v,
+                              void *o, int64_t batch, int64_t heads,
+                              int64_t seq_q, int64_t seq_kv, int64_t head_dim,
+                              float scale, uint32_t flags, void *stream) {
+  if (flags & ~IREE_MI355X_ATTENTION_CAUSAL)
+    return fail(IREE_MI355X_INVALID_ARGUMENT,
+                "attention_f16: unknown flag bits 0x%x", flags);
+  if (batch < 0 || heads < 0 || seq_q < 0 || seq_kv < 0 || head_dim < 0)
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "attention_f16: negative extent");
+  if (!std::isfinite(scale))
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "attention_f16: scale not finite");
+  if (batch == 0 || heads == 0 || seq_q == 0)
+    return ok();
+  if (head_dim != 64 && head_dim != 128)
+    return fail(IREE_MI355X_UNSUPPORTED,
+                "attention_f16: head_dim %lld (64 or 128 supported)",
+                (long long)head_dim);
+  if (!q || !o || (seq_kv > 0 && (!k || !v)))
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "attention_f16: null pointer");
+  if (!aligned(q, 16) || !aligned(o, 16) || (k && !aligned(k, 16)) ||
+      (v && !aligned(v, 16)))
+    return fail(IREE_MI355X_MISALIGNED,
+                "attention_f16: q/k/v/o must be 16-byte aligned");
+  const int64_t q_blocks = (seq_q + 127) / 128;
+  if (batch * heads * q_blocks >= kMaxExtent || seq_q >= kMaxExtent ||
+      seq_kv >= kMaxExtent || batch * heads * (seq_q > seq_kv ? seq_q : seq_kv) *
+                                      head_dim >= ((int64_t)1 << 62))
+    return fail(IREE_MI355X_UNSUPPORTED, "attention_f16: problem too large");
+  return launch_status(
+      launch_attention(q, k, v, o, batch, heads, seq_q, seq_kv, head_dim, scale,
+                       (flags & IREE_MI355X_ATTENTION_CAUSAL) ? 1 : 0, stream),
+      "attention_fwd");
+}
+
+}  // extern "C"

@@ -1,0 +1,133 @@
+// Device-side helpers shared by the gfx950 kernels: vector types, MFMA
+// wrappers, direct global->LDS loads, wait counters and the XCD-aware
+// workgroup order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ihp {
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+#define IHP_LDS __attribute__((address_space(3)))
+
+// One 32x32 MFMA over a 32-byte K slab per lane pair (16 bytes per lane):
+//   f16: v_mfma_f32_32x32x16_f16  (K = 16 halves)
+//   i8 : v_mfma_i32_32x32x32_i8   (K = 32 bytes)
+// Operand lane layout: lane l supplies row (l % 32) and the 16-byte K chunk
+// (l / 32) of the slab. The product pairs A and B elements at the same
+// (lane group, element) position, so any K assignment used identically for
+// A and B gives the same sum. Output: lane l holds column (l % 32); register r
+// holds row 8*(r/4) + 4*(l/32) + (r%4).
+template <typename T>
+struct Mfma32;
+
+template <>
+struct Mfma32<f16> {
+  typedef f32x16 Acc;
+  typedef float AccScalar;
+  static __device__ __forceinline__ Acc mma(i32x4 a, i32x4 b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(
+        __builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+        0);
+  }
+};
+
+template <>
+struct Mfma32<int8_t> {
+  typedef i32x16 Acc;
+  typedef int AccScalar;
+  static __device__ __forceinline__ Acc mma(i32x4 a, i32x4 b, Acc c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+  }
+};
+
+// 16x16 MFMA over a 64-byte K slab (16 bytes per lane, 4 lane groups):
+//   f16: v_mfma_f32_16x16x32_f16, i8: v_mfma_i32_16x16x64_i8.
+// Lane l supplies row (l % 16) and K chunk (l / 16). Output: lane l holds
+// column (l % 16); register r holds row 4*(l/16) + r.
+template <typename T>
+struct Mfma16;
+
+template <>
+struct Mfma16<f16> {
+  typedef f32x4 Acc;
+  static __device__ __forceinline__ Acc mma(i32x4 a, i32x4 b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(
+        __builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+        0);
+  }
+};
+
+template <>
+struct Mfma16<int8_t> {
+  typedef i32x4 Acc;
+  static __device__ __forceinline__ Acc mma(i32x4 a, i32x4 b, Acc c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+  }
+};
+
+// 16-byte direct global->LDS copy (global_load_lds_dwordx4). Lane i of the
+// wave writes lds_wave_base + 16*i; lds_wave_base must be wave-uniform.
+__device__ __forceinline__ void global_to_lds_16(const void *gptr,
+                                                 IHP_LDS void *lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(gptr, lds_wave_base, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] | vmcnt[5:4] << 14, other
+// counters left at their maximum so they are not waited on).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) |
+                             (0xF << 8));
+}
+
+// Workgroup barrier without the memory fence __syncthreads() adds: the fence
+// makes the compiler emit s_waitcnt vmcnt(0) first, which would drain every
+// in-flight global->LDS prefetch. Callers wait on exactly the counters they
+// need (wait_vmcnt / wait_lgkmcnt0) before it; the "memory" clobber keeps the
+// compiler from moving memory accesses across it.
+__device__ __forceinline__ void block_barrier() {
+  asm volatile("s_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ void wait_lgkmcnt0() {
+  __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4) | (0x0 << 8));
+}
+
+__device__ __forceinline__ i32x4 lds_read_16(const IHP_LDS char *p) {
+  return *(const IHP_LDS i32x4 *)p;
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs (each with its own
+// L2). Renumber them so that consecutive logical tile ids share an XCD, then
+// walk tiles in GROUP_M-row bands so an XCD's tiles reuse the same A row
+// panels and B column panels from its L2.
+__device__ __forceinline__ void xcd_tile_order(int wg, int num_wg,
+                                               int tiles_m, int tiles_n,
+                                               int group_m, int *tm, int *tn) {
+  constexpr int kXcds = 8;
+  int logical = wg;
+  if (num_wg % kXcds == 0)
+    logical = (wg % kXcds) * (num_wg / kXcds) + wg / kXcds;
+  int per_group = group_m * tiles_n;
+  int group = logical / per_group;
+  int first_m = group * group_m;
+  int rows = tiles_m - first_m < group_m ? tiles_m - first_m : group_m;
+  int in_group = logical - group * per_group;
+  *tm = first_m + in_group % rows;
+  *tn = in_group / rows;
+}
+
+}  // namespace ihp

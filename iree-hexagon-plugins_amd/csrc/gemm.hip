@@ -1,0 +1,350 @@
+// gfx950 matmul kernels for the linalg.matmul / quantized_matmul dispatch.
+//
+// The reference stages VTCM tiles of A and B with double-buffered DMA
+// (CG/Transforms/HexagonPipelineVTCMTransfers.cpp:388-524), packs them into
+// 32x32 HMX tiles (UK/hmx.c:123-143,246-275) and issues one 32x32x32 HMX MMA
+// per K step into an accumulator that is read back once per output tile
+// (CG/Transforms/HexagonExpandHmxMatmul.cpp:286-331). Here:
+//  * the VTCM tile becomes a BM x BN workgroup macro-tile whose A and B K-slabs
+//    are copied straight from HBM into LDS (global_load_lds_dwordx4, no VGPR
+//    round trip) through a STAGES-deep ring of LDS buffers;
+//  * the HMX pack becomes an XOR swizzle of 16-byte chunks applied on the
+//    global side of that copy, so MFMA operand reads from LDS are
+//    bank-conflict free and no separate pack pass exists;
+//  * the HMX MMA becomes v_mfma_{f32_32x32x16_f16, i32_32x32x32_i8} on
+//    per-wave 32x32 fragments with f32/i32 accumulators held in registers for
+//    the whole K loop (the reference reads its accumulator out as f16,
+//    HexagonConvertMatmulToHmx.cpp:592-596; this keeps full precision);
+//  * the unpack (add into the DPS init, UK/hmx.c:328-357) is the epilogue.
+#include "device_common.h"
+#include "kernels_internal.h"
+
+namespace ihp {
+
+// ----------------------------------------------------------------------------
+// Fast path: A [M,K] and B [N,K], both K-contiguous ("TN"), every extent a
+// multiple of the macro-tile, 16-byte aligned rows.
+// ----------------------------------------------------------------------------
+
+template <int CH>
+__device__ __forceinline__ int chunk_swizzle(int row) {
+  // 16-byte chunk permutation of a staged row of CH chunks. Rows are grouped
+  // so that 8 consecutive rows cover all 32 banks of one 128-byte bank line.
+  return (row / (8 / CH)) % CH;
+}
+
+template <typename T, typename OutT, int BM, int BN, int BKB, int WM, int WN,
+          int STAGES>
+__global__ __launch_bounds__(64 * WM *WN, 1) void gemm_tn_lds_kernel(
+    const T *__restrict__ A, const T *__restrict__ B, OutT *__restrict__ C,
+    int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
+    int accumulate) {
+  typedef Mfma32<T> MF;
+  typedef typename MF::Acc Acc;
+  constexpr int NT = 64 * WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 32, FN = WTN / 32;
+  constexpr int CH = BKB / 16;
+  constexpr int ROWS_PER_WAVE = 64 / CH;
+  constexpr int ROWS_PER_PASS = NT / CH;
+  constexpr int A_PASSES = BM / ROWS_PER_PASS;
+  constexpr int B_PASSES = BN / ROWS_PER_PASS;
+  constexpr int LOADS_PER_STAGE = A_PASSES + B_PASSES;
+  constexpr int A_BYTES = BM * BKB;
+  constexpr int STAGE_BYTES = (BM + BN) * BKB;
+  constexpr int KSTEPS = BKB / 32;
+  static_assert(BM % ROWS_PER_PASS == 0 && BN % ROWS_PER_PASS == 0, "tile");
+  static_assert(FM >= 1 && FN >= 1 && CH >= 2 && CH <= 8, "tile");
+  static_assert(KSTEPS % 2 == 0, "fragment double buffer parity");
+  static_assert(STAGES >= 2 && (STAGES - 2) * LOADS_PER_STAGE < 64,
+                "vmcnt range");
+
+  __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  int tm, tn;
+  xcd_tile_order(blockIdx.x, gridDim.x, M / BM, N / BN, 4, &tm, &tn);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+
+  // Copy side: lane -> (row in the wave's slab, physical chunk); the global
+  // chunk it fetches is the logical chunk that belongs in that slot. The
+  // address is a wave-uniform base plus a 32-bit lane offset.
+  const int ld_row = lane / CH;
+  const int ld_chunk = (lane % CH) ^ chunk_swizzle<CH>(ld_row);
+  const int64_t lda_b = lda * (int64_t)sizeof(T);
+  const int64_t ldb_b = ldb * (int64_t)sizeof(T);
+  const uint32_t a_lane =
+      (uint32_t)((wave * ROWS_PER_WAVE + ld_row) * lda_b + ld_chunk * 16);
+  const uint32_t b_lane =
+      (uint32_t)((wave * ROWS_PER_WAVE + ld_row) * ldb_b + ld_chunk * 16);
+  const char *a_base = (const char *)A + m0 * lda_b;
+  const char *b_base = (const char *)B + n0 * ldb_b;
+  IHP_LDS char *lds = (IHP_LDS char *)smem;
+
+  auto load_stage = [&](int kt, int slot) {
+    const int64_t kb = (int64_t)kt * BKB;
+    IHP_LDS char *dst = lds + slot * STAGE_BYTES + wave * ROWS_PER_WAVE * BKB;
+#pragma unroll
+    for (int p = 0; p < A_PASSES; ++p)
+      global_to_lds_16(a_base + kb + (int64_t)p * ROWS_PER_PASS * lda_b +
+                           a_lane,
+                       dst + p * ROWS_PER_PASS * BKB);
+#pragma unroll
+    for (int p = 0; p < B_PASSES; ++p)
+      global_to_lds_16(b_base + kb + (int64_t)p * ROWS_PER_PASS * ldb_b +
+                           b_lane,
+                       dst + A_BYTES + p * ROWS_PER_PASS * BKB);
+  };
+
+  // Read side: lane reads row (lane % 32) of each 32-row fragment, logical
+  // chunk 2*ks + lane/32 of the staged row.
+  const int rd_row = lane & 31;
+  const int rd_sw = chunk_swizzle<CH>(rd_row) ^ (lane >> 5);
+  int koff[KSTEPS];
+#pragma unroll
+  for (int ks = 0; ks < KSTEPS; ++ks)
+    koff[ks] = ((2 * ks) ^ rd_sw) * 16;
+  const int a_rd = (wm * WTM + rd_row) * BKB;
+  const int b_rd = A_BYTES + (wn * WTN + rd_row) * BKB;
+
+  auto read_frags = [&](int slot, int ks, i32x4 *af, i32x4 *bf) {
+    const IHP_LDS char *st = lds + slot * STAGE_BYTES;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      af[i] = lds_read_16(st + a_rd + i * 32 * BKB + koff[ks]);
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      bf[j] = lds_read_16(st + b_rd + j * 32 * BKB + koff[ks]);
+  };
+
+  Acc acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        acc[i][j][r] = 0;
+
+  const int nk = (int)(((int64_t)K * sizeof(T)) / BKB);
+  // Prologue: fill every slot of the ring, wait for stage 0.
+#pragma unroll
+  for (int s = 0; s < STAGES; ++s)
+    if (s < nk)
+      load_stage(s, s);
+  if (STAGES - 1 < nk)
+    wait_vmcnt<(STAGES - 1) * LOADS_PER_STAGE>();
+  else
+    wait_vmcnt<0>();
+  block_barrier();
+
+  i32x4 af[2][FM], bf[2][FN];
+  read_frags(0, 0, af[0], bf[0]);
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const int slot = kt % STAGES;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      const int cur = ks & 1, nxt = cur ^ 1;
+      if (ks + 1 < KSTEPS) {
+        read_frags(slot, ks + 1, af[nxt], bf[nxt]);
+      } else if (kt + 1 < nk) {
+        // Stage handoff: stage kt+1 must have landed for every wave, and
+        // every wave must be done reading stage kt before its slot is
+        // refilled with stage kt+STAGES.
+        if (kt + STAGES - 1 < nk)
+          wait_vmcnt<(STAGES - 2) * LOADS_PER_STAGE>();
+        else
+          wait_vmcnt<0>();
+        wait_lgkmcnt0();
+        block_barrier();
+        if (kt + STAGES < nk)
+          load_stage(kt + STAGES, slot);
+        read_frags((kt + 1) % STAGES, 0, af[nxt], bf[nxt]);
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = MF::mma(af[cur][i], bf[cur][j], acc[i][j]);
+    }
+  }
+
+  // Epilogue: C_out = [C_init +] acc, one rounding for f16 outputs.
+  const int col_l = lane & 31;
+  const int row_l = 4 * (lane >> 5);
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    OutT *crow = C + (m0 + wm * WTM + i * 32 + row_l) * ldc + n0 + wn * WTN +
+                 col_l;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        store_out(crow + (8 * (r >> 2) + (r & 3)) * ldc + j * 32,
+                  acc[i][j][r], accumulate);
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
+// General path: any extents, strides and B layout; bounds-checked element
+// loads staged through registers into LDS (B converted to the MFMA input type
+// on the way, which is where W8A16 dequantizes), 64x64 tiles, 4 waves of
+// 32x32 fragments, optional per-column scale in the epilogue.
+// ----------------------------------------------------------------------------
+
+template <typename TA, typename TB, typename OutT, bool kScale>
+__global__ __launch_bounds__(256) void gemm_general_kernel(
+    const TA *__restrict__ A, const TB *__restrict__ B, OutT *__restrict__ C,
+    const f16 *__restrict__ scale, int M, int N, int K, int64_t lda,
+    int64_t ldb, int64_t ldc, int b_transposed, int accumulate) {
+  // MFMA input type: f16 unless both operands are int8.
+  typedef typename MfmaInput<TA, TB>::type TM;
+  typedef Mfma32<TM> MF;
+  constexpr int KE = 64 / (int)sizeof(TM);  // K elements per 64-byte slab
+  constexpr int ROWB = 64 + 16;             // padded staged row (bytes)
+  __shared__ __attribute__((aligned(16))) char As[64 * ROWB];
+  __shared__ __attribute__((aligned(16))) char Bs[64 * ROWB];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t m0 = (int64_t)blockIdx.y * 64, n0 = (int64_t)blockIdx.x * 64;
+  typename MF::Acc acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    acc[r] = 0;
+
+  constexpr int EPT = 16 / (int)sizeof(TM);  // elements per thread per slab
+  const int ld_r = tid / 4, ld_c = (tid % 4) * EPT;
+
+  for (int k0 = 0; k0 < K; k0 += KE) {
+    {  // A rows
+      TM *dst = (TM *)(As + ld_r * ROWB) + ld_c;
+      const int64_t m = m0 + ld_r;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const int k = k0 + ld_c + e;
+        dst[e] = (m < M && k < K) ? (TM)A[m * lda + k] : (TM)0;
+      }
+    }
+    if (b_transposed) {  // B rows are N
+      TM *dst = (TM *)(Bs + ld_r * ROWB) + ld_c;
+      const int64_t n = n0 + ld_r;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const int k = k0 + ld_c + e;
+        dst[e] = (n < N && k < K) ? (TM)B[n * ldb + k] : (TM)0;
+      }
+    } else {  // B [K,N]: n fastest across threads, staged transposed
+      const int nn = tid & 63, kq = tid >> 6;
+      constexpr int KPT = KE / 4;
+      TM *dst = (TM *)(Bs + nn * ROWB) + kq * KPT;
+      const int64_t n = n0 + nn;
+#pragma unroll
+      for (int e = 0; e < KPT; ++e) {
+        const int k = k0 + kq * KPT + e;
+        dst[e] = (n < N && k < K) ? (TM)B[(int64_t)k * ldb + n] : (TM)0;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int ch = 2 * ks + (lane >> 5);
+      i32x4 af = *(const i32x4 *)(As + (wm * 32 + (lane & 31)) * ROWB + ch * 16);
+      i32x4 bf = *(const i32x4 *)(Bs + (wn * 32 + (lane & 31)) * ROWB + ch * 16);
+      acc = MF::mma(af, bf, acc);
+    }
+    __syncthreads();
+  }
+
+  const int64_t col = n0 + wn * 32 + (lane & 31);
+  if (col >= N)
+    return;
+  float s = 1.0f;
+  if (kScale)
+    s = (float)scale[col];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int64_t row = m0 + wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+    if (row < M) {
+      if (kScale)
+        store_out(C + row * ldc + col, (float)acc[r] * s, accumulate);
+      else
+        store_out(C + row * ldc + col, acc[r], accumulate);
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Host launchers.
+// ----------------------------------------------------------------------------
+
+template <typename T, typename OutT, int BM, int BN, int BKB, int WM, int WN,
+          int STAGES>
+static hipError_t launch_tn(const MatmulArgs &a) {
+  const int tiles = (int)((a.m / BM) * (a.n / BN));
+  hipLaunchKernelGGL(
+      (gemm_tn_lds_kernel<T, OutT, BM, BN, BKB, WM, WN, STAGES>), dim3(tiles),
+      dim3(64 * WM * WN), 0, (hipStream_t)a.stream, (const T *)a.a,
+      (const T *)a.b, (OutT *)a.c, (int)a.m, (int)a.n, (int)a.k, a.lda, a.ldb,
+      a.ldc, a.accumulate);
+  return hipGetLastError();
+}
+
+#define IHP_TN_CONFIG(NAME, T, OUT, BM, BN, BKB, WM, WN, ST)                   \
+  {NAME, sizeof(T) == 1 ? kElemI8 : kElemF16, sizeof(OUT) == 4, BM, BN,       \
+   BKB / (int)sizeof(T), 64 * WM * WN, ST, (BM + BN) * BKB * ST,              \
+   &launch_tn<T, OUT, BM, BN, BKB, WM, WN, ST>}
+
+// Every compiled fast-path configuration. The planner picks among these by
+// name or by its LDS-budget ranking; the autotuner times them.
+// Names: <types>_tn_<BM>x<BN>x<BK in elements>_w<wave grid>_s<LDS stages>.
+static const TnConfig kTnConfigs[] = {
+    IHP_TN_CONFIG("i8_tn_256x256x128_w2x2_s2", int8_t, int32_t, 256, 256, 128, 2, 2, 2),
+    IHP_TN_CONFIG("i8_tn_256x256x64_w2x2_s3", int8_t, int32_t, 256, 256, 64, 2, 2, 3),
+    IHP_TN_CONFIG("i8_tn_256x128x128_w2x2_s2", int8_t, int32_t, 256, 128, 128, 2, 2, 2),
+    IHP_TN_CONFIG("i8_tn_128x128x128_w2x2_s3", int8_t, int32_t, 128, 128, 128, 2, 2, 3),
+    IHP_TN_CONFIG("f16_tn_256x256x64_w2x2_s2", f16, f16, 256, 256, 128, 2, 2, 2),
+    IHP_TN_CONFIG("f16_tn_256x256x32_w2x2_s3", f16, f16, 256, 256, 64, 2, 2, 3),
+    IHP_TN_CONFIG("f16_tn_256x128x64_w2x2_s2", f16, f16, 256, 128, 128, 2, 2, 2),
+    IHP_TN_CONFIG("f16_tn_128x128x64_w2x2_s3", f16, f16, 128, 128, 128, 2, 2, 3),
+    IHP_TN_CONFIG("f16f32_tn_256x256x64_w2x2_s2", f16, float, 256, 256, 128, 2, 2, 2),
+    IHP_TN_CONFIG("f16f32_tn_128x128x64_w2x2_s3", f16, float, 128, 128, 128, 2, 2, 3),
+};
+
+const TnConfig *tn_configs(int *count) {
+  *count = (int)(sizeof(kTnConfigs) / sizeof(kTnConfigs[0]));
+  return kTnConfigs;
+}
+
+template <typename TA, typename TB, typename OutT, bool kScale>
+static hipError_t launch_general_t(const MatmulArgs &a, const void *scale) {
+  dim3 grid((unsigned)((a.n + 63) / 64), (unsigned)((a.m + 63) / 64));
+  hipLaunchKernelGGL((gemm_general_kernel<TA, TB, OutT, kScale>), grid,
+                     dim3(256), 0, (hipStream_t)a.stream, (const TA *)a.a,
+                     (const TB *)a.b, (OutT *)a.c, (const f16 *)scale,
+                     (int)a.m, (int)a.n, (int)a.k, a.lda, a.ldb, a.ldc,
+                     a.b_transposed, a.accumulate);
+  return hipGetLastError();
+}
+
+hipError_t launch_general(const MatmulArgs &a, GeneralKind kind,
+                          const void *scale) {
+  switch (kind) {
+    case kGeneralF16F16:
+      return launch_general_t<f16, f16, f16, false>(a, nullptr);
+    case kGeneralF16F32:
+      return launch_general_t<f16, f16, float, false>(a, nullptr);
+    case kGeneralI8I32:
+      return launch_general_t<int8_t, int8_t, int32_t, false>(a, nullptr);
+    case kGeneralW8A16:
+      return launch_general_t<f16, int8_t, f16, true>(a, scale);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace ihp

@@ -1,0 +1,98 @@
+// Internal interface between the C-ABI layer (abi.cpp), the planner and the
+// HIP kernel translation units. Not installed; the public boundary is
+// include/iree_mi355x_*.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace ihp {
+
+enum ElemKind { kElemF16 = 0, kElemI8 = 1 };
+
+// One matmul launch: C[M,N] = [C +] A[M,K] . B (B [K,N] or [N,K]).
+struct MatmulArgs {
+  const void *a;
+  const void *b;
+  void *c;
+  int64_t m, n, k;
+  int64_t lda, ldb, ldc;
+  int b_transposed;
+  int accumulate;
+  void *stream;
+};
+
+typedef hipError_t (*TnLaunchFn)(const MatmulArgs &);
+
+// A compiled fast-path (TN, LDS-DMA) GEMM configuration.
+struct TnConfig {
+  const char *name;
+  int elem;      // ElemKind of A and B
+  int out_f32;   // f16 path: f32 output (i8 path: always i32)
+  int bm, bn;    // macro-tile
+  int bk;        // K elements per LDS stage
+  int threads;   // workgroup size
+  int stages;    // LDS ring depth
+  int lds_bytes; // static LDS per workgroup
+  TnLaunchFn launch;
+};
+
+const TnConfig *tn_configs(int *count);
+
+enum GeneralKind {
+  kGeneralF16F16 = 0,
+  kGeneralF16F32 = 1,
+  kGeneralI8I32 = 2,
+  kGeneralW8A16 = 3,
+};
+hipError_t launch_general(const MatmulArgs &a, GeneralKind kind,
+                          const void *scale);
+
+// Skinny (M <= kGemvMaxRows) matmul with B [K,N] row-major: split-K streaming
+// kernel with an in-kernel last-arriver reduction over `splits` partials.
+constexpr int kGemvMaxRows = 4;
+struct GemvPlan {
+  int splits;          // K split count (grid y)
+  int cols_per_wg;     // output columns per workgroup
+  int k_chunk;         // rows of W per workgroup
+  int64_t col_blocks;  // grid x
+};
+GemvPlan gemv_plan(int64_t m, int64_t n, int64_t k, int w_bytes);
+size_t gemv_workspace_bytes(int64_t m, int64_t n, int64_t k, int w_bytes);
+// w_bytes = 2: f16 weights (scale == NULL); 1: int8 weights with f16 scale.
+hipError_t launch_gemv(const MatmulArgs &a, int w_bytes, const void *scale,
+                       int out_f32, void *workspace);
+
+hipError_t launch_attention(const void *q, const void *k, const void *v,
+                            void *o, int64_t batch, int64_t heads,
+                            int64_t seq_q, int64_t seq_kv, int64_t head_dim,
+                            float scale, int causal, void *stream);
+
+#ifdef __HIP_DEVICE_COMPILE__
+#define IHP_HD __device__
+#else
+#define IHP_HD __host__ __device__
+#endif
+
+template <typename TA, typename TB>
+struct MfmaInput {
+  typedef _Float16 type;
+};
+template <>
+struct MfmaInput<int8_t, int8_t> {
+  typedef int8_t type;
+};
+
+__device__ __forceinline__ void store_out(float *p, float v, int acc) {
+  *p = acc ? *p + v : v;
+}
+__device__ __forceinline__ void store_out(_Float16 *p, float v, int acc) {
+  *p = (_Float16)(acc ? (float)*p + v : v);
+}
+__device__ __forceinline__ void store_out(int32_t *p, int v, int acc) {
+  // two's-complement wrap, like the i32 adds of the CPU path
+  *p = acc ? (int32_t)((uint32_t)*p + (uint32_t)v) : v;
+}
+
+}  // namespace ihp

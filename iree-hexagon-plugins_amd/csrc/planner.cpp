@@ -1,0 +1,299 @@
+// Dispatch classification and gfx950 macro-tile planning (host only).
+// See include/iree_mi355x_planner.h for the reference functions each entry
+// point replaces.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <tuple>
+
+#include "../../include/iree_mi355x_kernels.h"
+#include "../../include/iree_mi355x_planner.h"
+#include "kernels_internal.h"
+
+namespace ihp {
+
+int fail(int status, const char *fmt, ...);
+
+namespace {
+
+constexpr int64_t kDefaultLdsBudget = 160 * 1024;
+constexpr int32_t kDefaultCus = 256;
+
+// Measured choices (bench.py --tune writes the candidates' timings; the
+// winners are recorded here). Keyed by element types, exact shape and flags.
+struct TunedEntry {
+  int32_t a_elem, c_elem;
+  int64_t m, n, k;
+  uint32_t flags;
+  const char *config;
+};
+const TunedEntry kTuned[] = {
+    {0, 0, 0, 0, 0, 0, nullptr},  // sentinel
+};
+
+int elem_bytes(int32_t e) {
+  switch (e) {
+    case IREE_MI355X_ELEM_I8:
+      return 1;
+    case IREE_MI355X_ELEM_F16:
+      return 2;
+    default:
+      return 4;
+  }
+}
+
+bool types_supported(const iree_mi355x_matmul_desc_t &d) {
+  const bool f16 = d.a_elem == IREE_MI355X_ELEM_F16 &&
+                   d.b_elem == IREE_MI355X_ELEM_F16 &&
+                   (d.c_elem == IREE_MI355X_ELEM_F16 ||
+                    d.c_elem == IREE_MI355X_ELEM_F32) &&
+                   !d.has_scale;
+  const bool i8 = d.a_elem == IREE_MI355X_ELEM_I8 &&
+                  d.b_elem == IREE_MI355X_ELEM_I8 &&
+                  d.c_elem == IREE_MI355X_ELEM_I32 && !d.has_scale;
+  const bool w8a16 = d.a_elem == IREE_MI355X_ELEM_F16 &&
+                     d.b_elem == IREE_MI355X_ELEM_I8 &&
+                     d.c_elem == IREE_MI355X_ELEM_F16 && d.has_scale;
+  return f16 || i8 || w8a16;
+}
+
+bool gemv_eligible(const iree_mi355x_matmul_desc_t &d) {
+  if (d.m < 1 || d.m > kGemvMaxRows || d.k < 1 ||
+      (d.flags & IREE_MI355X_MATMUL_B_TRANSPOSED) || !d.b_aligned16)
+    return false;
+  const int cols = 16 / elem_bytes(d.b_elem);
+  if (d.n % cols != 0)
+    return false;
+  // int8 weights only in the W8A16 form; f16 with f16 or f32 output.
+  if (d.b_elem == IREE_MI355X_ELEM_I8)
+    return d.has_scale;
+  return true;
+}
+
+// TN (both operands K-contiguous) candidates that tile the shape exactly.
+bool tn_fits(const iree_mi355x_matmul_desc_t &d, const TnConfig &c) {
+  if (!(d.flags & IREE_MI355X_MATMUL_B_TRANSPOSED) || !d.a_aligned16 ||
+      !d.b_aligned16 || d.has_scale)
+    return false;
+  const int want_elem = d.a_elem == IREE_MI355X_ELEM_I8 ? kElemI8 : kElemF16;
+  if (c.elem != want_elem || d.a_elem != d.b_elem)
+    return false;
+  if (want_elem == kElemF16 && c.out_f32 != (d.c_elem == IREE_MI355X_ELEM_F32))
+    return false;
+  return d.m % c.bm == 0 && d.n % c.bn == 0 && d.k % c.bk == 0 && d.k > 0;
+}
+
+}  // namespace
+}  // namespace ihp
+
+using namespace ihp;
+
+extern "C" {
+
+void iree_mi355x_matmul_desc_init(iree_mi355x_matmul_desc_t *desc,
+                                  int32_t a_elem, int32_t b_elem,
+                                  int32_t c_elem, int64_t m, int64_t n,
+                                  int64_t k, uint32_t flags) {
+  memset(desc, 0, sizeof(*desc));
+  desc->a_elem = a_elem;
+  desc->b_elem = b_elem;
+  desc->c_elem = c_elem;
+  desc->m = m;
+  desc->n = n;
+  desc->k = k;
+  desc->flags = flags;
+  desc->a_aligned16 = 1;
+  desc->b_aligned16 = 1;
+  desc->lds_budget_bytes = kDefaultLdsBudget;
+  desc->num_cus = kDefaultCus;
+}
+
+int32_t iree_mi355x_classify_matmul(const iree_mi355x_matmul_desc_t *d) {
+  if (!d || !types_supported(*d) || d->m < 0 || d->n < 0 || d->k < 0)
+    return IREE_MI355X_FAMILY_NONE;
+  if (gemv_eligible(*d))
+    return IREE_MI355X_FAMILY_GEMV;
+  int count = 0;
+  const TnConfig *cfgs = tn_configs(&count);
+  for (int i = 0; i < count; ++i)
+    if (tn_fits(*d, cfgs[i]) && cfgs[i].lds_bytes <= d->lds_budget_bytes)
+      return IREE_MI355X_FAMILY_MFMA_TN;
+  return IREE_MI355X_FAMILY_GENERAL;
+}
+
+int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
+                            iree_mi355x_matmul_plan_t *plan) {
+  if (!d || !plan)
+    return IREE_MI355X_INVALID_ARGUMENT;
+  memset(plan, 0, sizeof(*plan));
+  plan->config_index = -1;
+  const int32_t family = iree_mi355x_classify_matmul(d);
+  plan->family = family;
+  if (family == IREE_MI355X_FAMILY_NONE)
+    return IREE_MI355X_UNSUPPORTED;
+  const int64_t budget =
+      d->lds_budget_bytes > 0 ? d->lds_budget_bytes : kDefaultLdsBudget;
+  const int64_t cus = d->num_cus > 0 ? d->num_cus : kDefaultCus;
+
+  if (family == IREE_MI355X_FAMILY_GEMV) {
+    const int wb = elem_bytes(d->b_elem);
+    GemvPlan g = gemv_plan(d->m, d->n, d->k, wb);
+    snprintf(plan->config_name, sizeof(plan->config_name), "gemv_%s_r%lld",
+             wb == 1 ? "w8a16" : "f16", (long long)d->m);
+    plan->tile_m = d->m;
+    plan->tile_n = g.cols_per_wg;
+    plan->tile_k = g.k_chunk;
+    plan->workgroups = g.col_blocks * g.splits;
+    plan->threads = 256;
+    plan->splits = g.splits;
+    plan->workspace_bytes = (int64_t)gemv_workspace_bytes(d->m, d->n, d->k, wb);
+    plan->traffic_bytes = d->n * d->k * wb + d->m * d->k * 2;
+    return IREE_MI355X_OK;
+  }
+
+  if (family == IREE_MI355X_FAMILY_MFMA_TN) {
+    int count = 0;
+    const TnConfig *cfgs = tn_configs(&count);
+    int best = -1;
+    // A measured entry wins when it fits.
+    for (const TunedEntry &t : kTuned) {
+      if (!t.config || t.a_elem != d->a_elem || t.c_elem != d->c_elem || t.m != d->m ||
+          t.n != d->n || t.k != d->k || t.flags != d->flags)
+        continue;
+      for (int i = 0; i < count; ++i)
+        if (strcmp(cfgs[i].name, t.config) == 0 && tn_fits(*d, cfgs[i]) &&
+            cfgs[i].lds_bytes <= budget) {
+          best = i;
+          plan->from_tuned_table = 1;
+        }
+    }
+    // Otherwise rank: (over budget, per-CU critical work, traffic, tiles, -N).
+    std::tuple<int, int64_t, int64_t, int64_t, int64_t> best_rank;
+    const int64_t eb = elem_bytes(d->a_elem);
+    if (best < 0) {
+      for (int i = 0; i < count; ++i) {
+        const TnConfig &c = cfgs[i];
+        if (!tn_fits(*d, c) || c.lds_bytes > budget)
+          continue;
+        const int64_t tiles = (d->m / c.bm) * (d->n / c.bn);
+        const int64_t critical = ((tiles + cus - 1) / cus) * c.bm * c.bn;
+        const int64_t traffic =
+            eb * (d->m * d->k * (d->n / c.bn) + d->n * d->k * (d->m / c.bm));
+        auto rank = std::make_tuple(0, critical, traffic, tiles,
+                                    -(int64_t)c.bn);
+        if (best < 0 || rank < best_rank) {
+          best = i;
+          best_rank = rank;
+        }
+      }
+    }
+    if (best < 0)
+      return IREE_MI355X_UNSUPPORTED;
+    const TnConfig &c = cfgs[best];
+    plan->config_index = best;
+    snprintf(plan->config_name, sizeof(plan->config_name), "%s", c.name);
+    plan->tile_m = c.bm;
+    plan->tile_n = c.bn;
+    plan->tile_k = c.bk;
+    plan->lds_bytes = c.lds_bytes;
+    plan->workgroups = (d->m / c.bm) * (d->n / c.bn);
+    plan->threads = c.threads;
+    plan->traffic_bytes =
+        eb * (d->m * d->k * (d->n / c.bn) + d->n * d->k * (d->m / c.bm));
+    return IREE_MI355X_OK;
+  }
+
+  // General kernel: 64x64 tiles, 256 threads, 10 KiB LDS.
+  snprintf(plan->config_name, sizeof(plan->config_name), "general_64x64");
+  plan->tile_m = 64;
+  plan->tile_n = 64;
+  plan->tile_k = 64 / (d->a_elem == IREE_MI355X_ELEM_I8 &&
+                               d->b_elem == IREE_MI355X_ELEM_I8
+                           ? 1
+                           : 2);
+  plan->lds_bytes = 2 * 64 * 80;
+  plan->workgroups = ((d->m + 63) / 64) * ((d->n + 63) / 64);
+  plan->threads = 256;
+  const int64_t ab = elem_bytes(d->a_elem), bb = elem_bytes(d->b_elem);
+  plan->traffic_bytes = ab * d->m * d->k * ((d->n + 63) / 64) +
+                        bb * d->n * d->k * ((d->m + 63) / 64);
+  return IREE_MI355X_OK;
+}
+
+int iree_mi355x_tn_config_count(void) {
+  int count = 0;
+  tn_configs(&count);
+  return count;
+}
+
+int iree_mi355x_tn_config_info(int index, const char **name, int32_t *a_elem,
+                               int32_t *c_elem, int64_t *tile_m,
+                               int64_t *tile_n, int64_t *tile_k,
+                               int64_t *lds_bytes, int32_t *threads) {
+  int count = 0;
+  const TnConfig *cfgs = tn_configs(&count);
+  if (index < 0 || index >= count)
+    return IREE_MI355X_INVALID_ARGUMENT;
+  const TnConfig &c = cfgs[index];
+  if (name)
+    *name = c.name;
+  if (a_elem)
+    *a_elem = c.elem == kElemI8 ? IREE_MI355X_ELEM_I8 : IREE_MI355X_ELEM_F16;
+  if (c_elem)
+    *c_elem = c.elem == kElemI8 ? IREE_MI355X_ELEM_I32
+                                : (c.out_f32 ? IREE_MI355X_ELEM_F32
+                                             : IREE_MI355X_ELEM_F16);
+  if (tile_m)
+    *tile_m = c.bm;
+  if (tile_n)
+    *tile_n = c.bn;
+  if (tile_k)
+    *tile_k = c.bk;
+  if (lds_bytes)
+    *lds_bytes = c.lds_bytes;
+  if (threads)
+    *threads = c.threads;
+  return IREE_MI355X_OK;
+}
+
+int iree_mi355x_matmul_tn_config(int index, const void *a, const void *b,
+                                 void *c, int64_t m, int64_t n, int64_t k,
+                                 int64_t lda, int64_t ldb, int64_t ldc,
+                                 uint32_t flags, void *stream) {
+  int count = 0;
+  const TnConfig *cfgs = tn_configs(&count);
+  if (index < 0 || index >= count)
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "tn_config: bad index %d", index);
+  const TnConfig &cfg = cfgs[index];
+  iree_mi355x_matmul_desc_t d;
+  const int32_t ae = cfg.elem == kElemI8 ? IREE_MI355X_ELEM_I8
+                                         : IREE_MI355X_ELEM_F16;
+  const int32_t ce = cfg.elem == kElemI8
+                         ? IREE_MI355X_ELEM_I32
+                         : (cfg.out_f32 ? IREE_MI355X_ELEM_F32
+                                        : IREE_MI355X_ELEM_F16);
+  iree_mi355x_matmul_desc_init(&d, ae, ae, ce, m, n, k, flags);
+  const int64_t eb = elem_bytes(ae);
+  d.a_aligned16 = a && ((uintptr_t)a % 16 == 0) && (lda * eb) % 16 == 0;
+  d.b_aligned16 = b && ((uintptr_t)b % 16 == 0) && (ldb * eb) % 16 == 0;
+  if (flags & ~(IREE_MI355X_MATMUL_B_TRANSPOSED | IREE_MI355X_MATMUL_ACCUMULATE |
+                IREE_MI355X_MATMUL_OUT_F32))
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "tn_config: unknown flags");
+  if (!c || (uintptr_t)c % elem_bytes(ce) != 0 || lda < k || ldb < k ||
+      ldc < n || m >= ((int64_t)1 << 31) || n >= ((int64_t)1 << 31) ||
+      k >= ((int64_t)1 << 31))
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "tn_config: bad arguments");
+  if (!tn_fits(d, cfg))
+    return fail(IREE_MI355X_UNSUPPORTED, "tn_config %s: shape does not tile",
+                cfg.name);
+  MatmulArgs args{a, b, c, m, n, k, lda, ldb, ldc, 1,
+                  (flags & IREE_MI355X_MATMUL_ACCUMULATE) ? 1 : 0, stream};
+  hipError_t e = cfg.launch(args);
+  if (e != hipSuccess)
+    return fail(IREE_MI355X_LAUNCH_FAILED, "%s: %s", cfg.name,
+                hipGetErrorString(e));
+  return IREE_MI355X_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,106 @@
+/*
+ * CPU oracle for the MI355X matmul / attention dispatch path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the checker
+ * (or the timed CPU baseline), never as the thing measured or shipped.
+ *
+ * Every routine restates the semantics of the reference's CPU path for the
+ * dispatch it mirrors; each function cites the reference file:line it follows.
+ * Half-precision values are passed as raw IEEE binary16 bit patterns
+ * (uint16_t) because gcc 11 has no _Float16 on x86-64.
+ *
+ * Parity pins (checked in tests/test_oracle.py):
+ *   half conversions      exhaustive vs numpy float16
+ *   matmul_i8             brute force int64 numpy, closed-form overflow bound
+ *   matmul_f16            torch.matmul(a.float(), b.float()) (the reference
+ *                         micro model), exact small-integer cases, identity
+ *   w8a16                 per-element-dequant form, exact power-of-two cases
+ *   attention             torch F.scaled_dot_product_attention (the reference
+ *                         micro attention model) in f32, causal invariants
+ *   select_hmx_tile_sizes reference lit goldens
+ *   choose_static_tiling  brute-force divisor search
+ *   hmx_pack              reference closed form on the UK test cases
+ */
+#ifndef IHP_ORACLE_H_
+#define IHP_ORACLE_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* IEEE binary16 <-> binary32, round-to-nearest-even. */
+float oracle_f16_to_f32(uint16_t h);
+uint16_t oracle_f32_to_f16(float f);
+void oracle_f16_to_f32_array(const uint16_t *src, float *dst, int64_t n);
+void oracle_f32_to_f16_array(const float *src, uint16_t *dst, int64_t n);
+
+/* Bits of the `flags` argument, same values as the product ABI. */
+#define ORACLE_B_TRANSPOSED 1u /* B stored [N,K] (indexing map (d1,d2)) */
+#define ORACLE_ACCUMULATE 2u   /* C_out = C_init + A.B (DPS init is read) */
+#define ORACLE_OUT_F32 4u      /* f32 output, else f16 */
+
+/* linalg.matmul f16 x f16 with f32 accumulation (arith.extf on the inputs),
+ * C_out = C_init + sum_k A[m,k]*B[k,n], summed in k order in f32.
+ * examples/matmul/matmul.mlir:1-14, UK/hmx.c:328-357 (add into init). */
+int oracle_matmul_f16(const uint16_t *a, const uint16_t *b, void *c,
+                      int64_t m, int64_t n, int64_t k, int64_t lda,
+                      int64_t ldb, int64_t ldc, uint32_t flags, int threads);
+
+/* i8 x i8 -> i32 exact integer matmul (linalg.matmul / quantized_matmul with
+ * zero points 0). */
+int oracle_matmul_i8(const int8_t *a, const int8_t *b, int32_t *c, int64_t m,
+                     int64_t n, int64_t k, int64_t lda, int64_t ldb,
+                     int64_t ldc, uint32_t flags, int threads);
+
+/* W8A16 linear: y[m,n] = f16( (sum_k f32(x[m,k]) * f32(w[k,n])) * f32(s[n]) ),
+ * zero point 0, w stored [K,N] (or [N,K] with ORACLE_B_TRANSPOSED). */
+int oracle_w8a16(const uint16_t *x, const int8_t *w, const uint16_t *scale,
+                 uint16_t *y, int64_t m, int64_t n, int64_t k, int64_t ldx,
+                 int64_t ldw, int64_t ldy, uint32_t flags, int threads);
+
+/* softmax(Q K^T * scale + mask) V with f32 scores/softmax, f16 in/out.
+ * Layout [B,H,S,D] contiguous. Causal mask is top-left aligned (key j is
+ * masked for query i when j > i), as torch's is_causal.
+ * IT/models/micro/attention-4x1024x128-f16/model.py (F.sdpa),
+ * CG/Pipelines/LoweringPipelines.cpp:561-595 (online attention). */
+int oracle_attention_f16(const uint16_t *q, const uint16_t *k,
+                         const uint16_t *v, uint16_t *o, int64_t batch,
+                         int64_t heads, int64_t seq_q, int64_t seq_kv,
+                         int64_t head_dim, float scale, int causal,
+                         int threads);
+
+/* chooseStaticTilingFactor, CG/Strategy/Planning/Strategies/
+ * StrategySupport.cpp:38-69. dynamic bound is passed as INT64_MIN. */
+int64_t oracle_choose_static_tiling_factor(int64_t static_bound,
+                                           int64_t preferred,
+                                           int64_t multiple_of);
+
+/* selectHmxTileSizes restricted to a 2-D matmul root (one M, N, K; no batch),
+ * CG/Strategy/Planning/VTCMPlanning.cpp:156-260 with the budget plumbing of
+ * CG/Strategy/KernelDispatch.cpp:14-26 (flag budget halved when double
+ * buffering, doubled back by the search).
+ *   ranges      {M, N, K} static extents or upper bounds
+ *   elem_bytes  {A, B, C} element sizes in bytes
+ *   b_transposed  B indexed (d1, d2) instead of (d2, d1)
+ *   budget_flag_bytes  --iree-hexagon-vtcm-tile-budget-bytes
+ * Returns 1 and writes tiles[3] = {m, n, k} if a tile is chosen, 0 if the
+ * search finds none (the planner then falls back to hexagon-mlir). */
+int oracle_select_hmx_tile_sizes(const int64_t ranges[3],
+                                 const int64_t elem_bytes[3], int b_transposed,
+                                 int64_t budget_flag_bytes,
+                                 int double_buffering, int64_t hmx_m,
+                                 int64_t hmx_n, int64_t tiles[3]);
+
+/* iree_hexagon_hmx_pack_f16 closed form (UK/test/test_support.c:194-215):
+ * packed[tile][(r/2)*64 + 2c + (r&1)] = src[r][c], zero padded. */
+void oracle_hmx_pack_f16(uint16_t *dest, const uint16_t *src,
+                         uint32_t src_stride, uint32_t rows, uint32_t cols,
+                         uint32_t row_tiles, uint32_t col_tiles);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* IHP_ORACLE_H_ */

@@ -1,0 +1,139 @@
+"""Writes the committed golden fixtures under tests/golden/.
+
+Nothing here imports or runs the reference. The fixtures are:
+  * matmul_*.npz    the reference's micro/hmx matmul models
+                    (IT/models/micro/hmx/*/model.{yaml,py}): same shapes, seeds
+                    and generators (IT/stages/importing.py:218-262), expected
+                    output = torch.matmul(a.float(), b.float()) as in their
+                    model.py, tolerances copied from their model.yaml;
+  * attention_*.npz F.scaled_dot_product_attention in f32 on small shapes (the
+                    function of IT/models/micro/attention-4x1024x128-f16);
+  * matmul_i8.npz   int8 x int8 with an int64 numpy product;
+  * tile_search.json the VTCM tile-search goldens of
+                    plugins/compiler/hexagon/test/codegen/strategy/
+                    hexagon_vtcm_planning_hmx.mlir, transcribed as data;
+  * hmx_pack.npz    the UK pack test cases (UK/test/pack_test.c:98-103) with
+                    the closed-form layout of UK/test/test_support.c:194-240.
+Run: python tests/golden/make_golden.py
+"""
+import json
+import os
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def normal(shape, seed, dtype=torch.float16):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g, dtype=torch.float32).to(dtype)
+
+
+MATMUL_CASES = [
+    # name, (M, K), (K, N), atol, rtol, rel_l2 %   (from each model.yaml)
+    ("small_prime_17x19x23", (17, 23), (23, 19), 5e-2, 5e-3, 0.05),
+    ("ragged_m_65x64x64", (65, 64), (64, 64), 5e-2, 5e-3, 0.05),
+    ("ragged_n_64x65x64", (64, 64), (64, 65), 5e-2, 5e-3, 0.05),
+    ("ragged_k_64x64x65", (64, 65), (65, 64), 1.5e-1, 5e-3, 0.05),
+    ("square_32x32x32", (32, 32), (32, 32), 5e-2, 5e-3, 0.05),
+]
+
+
+def write_matmuls():
+    for name, ashape, bshape, atol, rtol, rel in MATMUL_CASES:
+        a = normal(ashape, 0)
+        b = normal(bshape, 1)
+        out = torch.matmul(a.float(), b.float())
+        np.savez(os.path.join(HERE, f"matmul_{name}.npz"), a=a.numpy(),
+                 b=b.numpy(), expected=out.numpy(),
+                 tol=np.array([atol, rtol, rel]))
+
+
+def write_attention():
+    for name, shape, causal in (("b1h2s128d64_causal", (1, 2, 128, 64), True),
+                                ("b1h2s128d64", (1, 2, 128, 64), False),
+                                ("b1h1s160d128_causal", (1, 1, 160, 128), True)):
+        q, k, v = (normal(shape, s) for s in range(3))
+        out = F.scaled_dot_product_attention(q.float(), k.float(), v.float(),
+                                             is_causal=causal)
+        np.savez(os.path.join(HERE, f"attention_{name}.npz"), q=q.numpy(),
+                 k=k.numpy(), v=v.numpy(), expected=out.numpy(),
+                 causal=np.array(causal), tol=np.array([5e-2, 5e-2, 1.0]))
+
+
+def write_i8():
+    g = torch.Generator().manual_seed(0)
+    a = torch.randint(-128, 128, (37, 91), generator=g).to(torch.int8)
+    g = torch.Generator().manual_seed(1)
+    bt = torch.randint(-128, 128, (53, 91), generator=g).to(torch.int8)
+    expected = a.numpy().astype(np.int64) @ bt.numpy().astype(np.int64).T
+    np.savez(os.path.join(HERE, "matmul_i8.npz"), a=a.numpy(), bt=bt.numpy(),
+             expected=expected.astype(np.int32))
+
+
+def write_tile_search():
+    # (line, M, N, K, elem bytes A/B/C, B transposed, expected vtcm or None)
+    cases = [
+        {"line": "37-44", "m": 52, "n": 896, "k": 7680, "elem_bytes": [2, 2, 4],
+         "b_transposed": True, "expected": [52, 32, 7680]},
+        {"line": "57-64", "m": 128, "n": 2560, "k": 9728, "elem_bytes": [2, 2, 2],
+         "b_transposed": True, "expected": [128, 32, 9728]},
+        {"line": "77-84", "m": 64, "n": 64, "k": 32768, "elem_bytes": [2, 2, 2],
+         "b_transposed": True, "expected": None,
+         "note": "HMX search capped; the lit result [4, 8, 32768] comes from "
+                 "the un-vendored hexagon-mlir determineTileSizes fallback"},
+        {"line": "94-104", "m": 32, "n": 32, "k": 128, "elem_bytes": [2, 2, 4],
+         "b_transposed": False, "expected": [32, 32, 128]},
+        {"line": "114-123", "m": 1024, "n": 1024, "k": 2048,
+         "elem_bytes": [2, 2, 4], "b_transposed": False,
+         "expected": [64, 128, 2048]},
+        {"line": "133-142", "m": 1024, "n": 1024, "k": 2048,
+         "elem_bytes": [2, 2, 4], "b_transposed": False,
+         "expected": [64, 128, 2048]},
+    ]
+    with open(os.path.join(HERE, "tile_search.json"), "w") as f:
+        json.dump({"source": "plugins/compiler/hexagon/test/codegen/strategy/"
+                             "hexagon_vtcm_planning_hmx.mlir",
+                   "budget_flag_bytes": 2 * 1024 * 1024,
+                   "double_buffering": True, "cases": cases}, f, indent=1)
+
+
+def pack_closed_form(src, stride, rows, cols, row_tiles, col_tiles):
+    out = np.zeros(row_tiles * col_tiles * 1024, np.float16)
+    flat = src.reshape(-1)
+    for r in range(rows):
+        for c in range(cols):
+            t = (r // 32) * col_tiles + c // 32
+            tr, tc = r % 32, c % 32
+            out[t * 1024 + (tr // 2) * 64 + 2 * tc + (tr & 1)] = flat[r * stride + c]
+    return out
+
+
+def pack_source(rows, cols, stride):
+    # UK/test/pack_test.c:input_value; the stride padding holds a marker that
+    # must never reach the packed tiles.
+    src = np.full((rows, stride), 99.0, np.float16)
+    for r in range(rows):
+        for c in range(cols):
+            src[r, c] = np.float16(((r * 7 + c * 3) % 23 - 11) / 4.0)
+    return src
+
+
+def write_pack():
+    full = pack_source(32, 32, 32)
+    ragged = pack_source(35, 37, 41)
+    np.savez(os.path.join(HERE, "hmx_pack.npz"),
+             full_src=full, full_packed=pack_closed_form(full, 32, 32, 32, 1, 1),
+             ragged_src=ragged,
+             ragged_packed=pack_closed_form(ragged, 41, 35, 37, 3, 3))
+
+
+if __name__ == "__main__":
+    write_matmuls()
+    write_attention()
+    write_i8()
+    write_tile_search()
+    write_pack()
+    print("wrote", sorted(os.listdir(HERE)))

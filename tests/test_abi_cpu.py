@@ -1,0 +1,197 @@
+"""C-ABI boundary without a GPU: the library loads, exports what the headers
+declare, classifies and plans dispatches, and rejects bad arguments on the
+host before anything is launched."""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+
+def header_functions():
+    names = set()
+    for path in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(path).read()
+        text = re.sub(r"//[^\n]*", "", text)
+        for m in re.finditer(r"\b(iree_mi355x_\w+)\s*\(", text):
+            names.add(m.group(1))
+    return names
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    lib = pkg.library()
+    declared = header_functions()
+    assert declared == set(pkg.EXPORTED_SYMBOLS)
+    for name in declared:
+        assert getattr(lib, name) is not None
+
+
+def test_version_and_no_device_here(pkg):
+    lib = pkg.library()
+    assert b"gfx950" in lib.iree_mi355x_version()
+    assert lib.iree_mi355x_device_count() >= 0
+
+
+def test_executable_library_table(pkg):
+    assert ctypes.sizeof(pkg.DispatchAttrs) == 24
+    lib = pkg.executable_library()
+    assert lib.header.contents.version == pkg.EXECUTABLE_LIBRARY_VERSION
+    assert lib.imports.count == 0
+    assert pkg.export_names() == ["matmul_f16", "matmul_i8", "w8a16_matmul",
+                                  "attention_f16"]
+    for i in range(lib.exports.count):
+        attrs = lib.exports.attrs[i]
+        assert attrs.flags & 1  # RESOURCES_VALID
+        assert 0 < attrs.lds_bytes <= 160 * 1024
+        assert attrs.threads == 256
+    # any other version: NULL, like the reference's exact-version rule
+    assert pkg.executable_library(0x48580001) is None
+    assert pkg.executable_library(pkg.EXECUTABLE_LIBRARY_VERSION + 1) is None
+
+
+F16, I8, I32, F32 = 0, 1, 2, 3
+
+
+@pytest.mark.parametrize("case,family,config", [
+    ((I8, I8, I32, 4096, 4096, 4096, 1), 1, "i8_tn_256x256x128_w2x2_s2"),
+    ((F16, F16, F16, 4096, 4096, 4096, 1), 1, "f16_tn_256x256x64_w2x2_s2"),
+    ((F16, F16, F32, 4096, 4096, 4096, 1), 1, "f16f32_tn_256x256x64_w2x2_s2"),
+    ((F16, F16, F16, 2048, 4096, 4096, 1), 1, "f16_tn_256x128x64_w2x2_s2"),
+    ((F16, F16, F16, 128, 512, 256, 0), 2, "general_64x64"),
+    ((F16, F16, F16, 17, 19, 23, 1), 2, "general_64x64"),
+    ((F16, F16, F16, 1, 4096, 4096, 0), 3, "gemv_f16_r1"),
+    ((F16, F16, F16, 4, 11008, 4096, 0), 3, "gemv_f16_r4"),
+    ((F16, F16, F16, 5, 4096, 4096, 0), 2, "general_64x64"),
+    ((I8, I8, I32, 1, 4096, 4096, 0), 2, "general_64x64"),
+])
+def test_planner_classification(pkg, case, family, config):
+    a, b, c, m, n, k, flags = case
+    d = pkg.make_desc(a, b, c, m, n, k, flags)
+    assert pkg.classify(d) == family
+    p = pkg.plan(d)
+    assert p.family == family
+    assert p.config_name.decode() == config
+
+
+def test_planner_w8a16_and_unsupported_types(pkg):
+    d = pkg.make_desc(F16, I8, F16, 1, 11008, 4096, 0, has_scale=True)
+    p = pkg.plan(d)
+    assert p.family == pkg.FAMILY_GEMV and p.tile_n == 512
+    assert p.workspace_bytes > 0 and p.splits > 1
+    d = pkg.make_desc(F16, I8, F16, 512, 11008, 4096, 0, has_scale=True)
+    assert pkg.classify(d) == pkg.FAMILY_GENERAL
+    for bad in ((F32, F32, F32), (I8, F16, F16), (F16, F16, I32), (I8, I8, F16)):
+        d = pkg.make_desc(*bad, 64, 64, 64, 0)
+        assert pkg.classify(d) == pkg.FAMILY_NONE
+        with pytest.raises(pkg.MI355XError):
+            pkg.plan(d)
+
+
+def test_planner_lds_budget_and_alignment(pkg):
+    # a budget below every macro-tile's LDS leaves the general kernel
+    d = pkg.make_desc(I8, I8, I32, 4096, 4096, 4096, 1, lds_budget_bytes=32 * 1024)
+    assert pkg.classify(d) == pkg.FAMILY_GENERAL
+    d = pkg.make_desc(I8, I8, I32, 4096, 4096, 4096, 1, aligned=False)
+    assert pkg.classify(d) == pkg.FAMILY_GENERAL
+    d = pkg.make_desc(I8, I8, I32, 4096, 4096, 4096, 1, lds_budget_bytes=100 * 1024)
+    p = pkg.plan(d)
+    assert p.lds_bytes <= 100 * 1024 and p.family == pkg.FAMILY_MFMA_TN
+
+
+def test_planner_ranking_prefers_least_traffic(pkg):
+    # 4096^3: every candidate has the same per-CU work; 256x256 moves least
+    d = pkg.make_desc(I8, I8, I32, 4096, 4096, 4096, 1)
+    p = pkg.plan(d)
+    assert (p.tile_m, p.tile_n) == (256, 256)
+    assert p.traffic_bytes == 4096 * 4096 * (16 + 16)
+    assert p.workgroups == 256
+
+
+def test_tn_config_table(pkg):
+    cfgs = pkg.tn_configs()
+    assert len(cfgs) >= 8
+    for c in cfgs:
+        assert c.lds_bytes <= 160 * 1024
+        assert c.tile_m % 32 == 0 and c.tile_n % 32 == 0
+        assert c.threads == 256
+
+
+def test_workspace_query(pkg):
+    lib = pkg.library()
+    assert lib.iree_mi355x_matmul_workspace_bytes(1, 4096, 4096, 0) > 0
+    assert lib.iree_mi355x_matmul_workspace_bytes(1, 4096, 4096, 1) == 0
+    assert lib.iree_mi355x_matmul_workspace_bytes(2048, 4096, 4096, 0) == 0
+
+
+# Argument validation: every call below fails on the host, so no GPU is needed.
+FAKE = 0x10000  # 64 KiB aligned, never dereferenced
+
+
+def call_f16(lib, a=FAKE, b=FAKE, c=FAKE, m=64, n=64, k=64, lda=64, ldb=64,
+             ldc=64, flags=0):
+    return lib.iree_mi355x_matmul_f16(a, b, c, m, n, k, lda, ldb, ldc, flags,
+                                      None, 0, None)
+
+
+def test_matmul_argument_errors(pkg):
+    lib = pkg.library()
+    assert call_f16(lib, m=-1) == pkg.INVALID_ARGUMENT
+    assert call_f16(lib, a=None) == pkg.INVALID_ARGUMENT
+    assert call_f16(lib, c=None) == pkg.INVALID_ARGUMENT
+    assert call_f16(lib, lda=32) == pkg.INVALID_ARGUMENT
+    assert call_f16(lib, ldc=63) == pkg.INVALID_ARGUMENT
+    assert call_f16(lib, flags=0x80) == pkg.INVALID_ARGUMENT
+    assert "unknown flag" in pkg.last_error()
+    assert call_f16(lib, a=FAKE + 1) == pkg.MISALIGNED
+    assert call_f16(lib, c=FAKE + 1, flags=pkg.OUT_F32) == pkg.MISALIGNED
+    assert call_f16(lib, m=1 << 31) == pkg.UNSUPPORTED
+    # empty output: a no-op that succeeds without touching the device
+    assert call_f16(lib, m=0) == pkg.OK
+    assert call_f16(lib, n=0, a=None, b=None) == pkg.OK
+    assert lib.iree_mi355x_matmul_i8(FAKE, FAKE, FAKE + 2, 8, 8, 8, 8, 8, 8, 0,
+                                     None) == pkg.MISALIGNED
+    assert lib.iree_mi355x_matmul_i8(FAKE, FAKE, FAKE, 8, 8, 8, 8, 8, 8,
+                                     pkg.OUT_F32, None) == pkg.INVALID_ARGUMENT
+    assert lib.iree_mi355x_w8a16_matmul(FAKE, FAKE, None, FAKE, 1, 64, 64, 64,
+                                        64, 64, 0, None, 0,
+                                        None) == pkg.INVALID_ARGUMENT
+
+
+def test_attention_argument_errors(pkg):
+    lib = pkg.library()
+    att = lib.iree_mi355x_attention_f16
+    assert att(FAKE, FAKE, FAKE, FAKE, 1, 1, 128, 128, 96, 0.1, 1,
+               None) == pkg.UNSUPPORTED
+    assert att(FAKE, FAKE, FAKE, FAKE, 1, 1, 128, 128, 128, float("nan"), 1,
+               None) == pkg.INVALID_ARGUMENT
+    assert att(FAKE + 8, FAKE, FAKE, FAKE, 1, 1, 128, 128, 128, 0.1, 1,
+               None) == pkg.MISALIGNED
+    assert att(FAKE, FAKE, FAKE, FAKE, 1, 1, 128, 128, 128, 0.1, 4,
+               None) == pkg.INVALID_ARGUMENT
+    assert att(None, FAKE, FAKE, FAKE, 1, 1, 128, 128, 128, 0.1, 1,
+               None) == pkg.INVALID_ARGUMENT
+    assert att(FAKE, FAKE, FAKE, FAKE, 0, 1, 128, 128, 128, 0.1, 1,
+               None) == pkg.OK
+
+
+def test_dispatch_rejects_short_bindings(pkg):
+    consts = pkg.matmul_constants(64, 64, 64, 64, 64, 64, 0)
+    full = [64 * 64 * 2] * 3
+    short = [64 * 64 * 2, 64 * 64 * 2 - 2, 64 * 64 * 2]
+    assert pkg.call_export("matmul_f16", consts, [FAKE] * 3,
+                           short) == pkg.INVALID_ARGUMENT
+    assert "binding 1" in pkg.last_error()
+    # transposed B is [N,K]: the same byte count here, a different span formula
+    consts_t = pkg.matmul_constants(64, 32, 64, 64, 64, 32, pkg.B_TRANSPOSED)
+    assert pkg.call_export("matmul_f16", consts_t, [FAKE] * 3,
+                           [64 * 64 * 2, 32 * 64 * 2 - 2, 64 * 32 * 2]) \
+        == pkg.INVALID_ARGUMENT
+    assert pkg.call_export("matmul_i8", consts[:5], [FAKE] * 3,
+                           full) == pkg.INVALID_ARGUMENT
+    att = pkg.attention_constants(1, 2, 128, 128, 64, 0.125, 1)
+    q = 1 * 2 * 128 * 64 * 2
+    assert pkg.call_export("attention_f16", att, [FAKE] * 4,
+                           [q, q, q - 2, q]) == pkg.INVALID_ARGUMENT

@@ -1,0 +1,337 @@
+"""Parity of the gfx950 kernels with the CPU oracle, through the C-ABI.
+
+Bars: int8 -> i32 bit-exact; f16 max|y - y_cpu| / max|y_cpu| <= 2e-3 (the
+BASELINE fp16 rule), plus the reference's allclose + relative-L2 recipe with
+each micro model's tolerances (IT/stages/checking.py:46-132).
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN
+
+pytestmark = pytest.mark.gpu
+
+FP16_BOUND = 2e-3
+
+
+def fp16_ok(oracle, got, ref, bound=FP16_BOUND):
+    err = oracle.fp16_parity(got, ref)
+    assert err <= bound, f"fp16 parity {err:.3e} > {bound}"
+    return err
+
+
+def canary_out(shape, dtype, dev, fill):
+    """Output view inside a larger buffer whose margins hold `fill`."""
+    m, n = shape
+    pad = 64
+    buf = torch.full((m + 2, n + pad), fill, dtype=dtype, device=dev)
+    return buf, buf[1:m + 1, :n]
+
+
+def check_canary(buf, m, n, fill):
+    host = buf.cpu()
+    inner = torch.zeros_like(host, dtype=torch.bool)
+    inner[1:m + 1, :n] = True
+    assert bool((host[~inner] == fill).all()), "write outside the output view"
+
+
+# ------------------------------------------------------------ f16 matmul ----
+
+def test_c1_matmul_f16(pkg, oracle, inputs, dev):
+    a, b = inputs.c1_matmul_f16()
+    c = pkg.matmul(a.to(dev), b.to(dev))
+    ref = oracle.matmul_f16(a.numpy(), b.numpy())
+    fp16_ok(oracle, c.cpu().numpy(), ref)
+    rel, _, close = oracle.compare_arrays(ref, c.cpu().numpy(), 5e-2, 5e-3)
+    assert close and rel < 0.05
+
+
+@pytest.mark.parametrize("name", ["small_prime_17x19x23", "ragged_m_65x64x64",
+                                  "ragged_n_64x65x64", "ragged_k_64x64x65",
+                                  "square_32x32x32"])
+@pytest.mark.parametrize("transposed", [False, True])
+def test_matmul_f16_micro_models(pkg, oracle, dev, name, transposed):
+    d = np.load(os.path.join(GOLDEN, f"matmul_{name}.npz"))
+    atol, rtol, rel_l2 = d["tol"]
+    a = torch.from_numpy(d["a"]).to(dev)
+    b = torch.from_numpy(d["b"])
+    if transposed:
+        b = b.t().contiguous()
+    m, n = d["expected"].shape
+    buf, c = canary_out((m, n), torch.float32, dev, -7.0)
+    pkg.matmul(a, b.to(dev), c, b_transposed=transposed,
+               out_dtype=torch.float32)
+    got = c.cpu().numpy()
+    check_canary(buf, m, n, -7.0)
+    rel, _, close = oracle.compare_arrays(d["expected"], got, atol, rtol)
+    assert close and rel <= rel_l2
+    fp16_ok(oracle, got, d["expected"], 1e-5)
+
+
+@pytest.mark.parametrize("shape", [(256, 256, 64), (512, 512, 256),
+                                   (512, 256, 1024), (256, 768, 512)])
+def test_matmul_f16_tn_configs(pkg, oracle, dev, shape):
+    m, n, k = shape
+    g = torch.Generator().manual_seed(m + n + k)
+    a = torch.randn(m, k, generator=g).half()
+    bt = torch.randn(n, k, generator=g).half()
+    ref16 = oracle.matmul_f16(a.numpy(), bt.numpy(), b_transposed=True)
+    ref32 = oracle.matmul_f16(a.numpy(), bt.numpy(), b_transposed=True,
+                              out_f32=True)
+    ran = 0
+    for cfg in pkg.tn_configs():
+        if cfg.a_elem != pkg.ELEM_F16:
+            continue
+        if m % cfg.tile_m or n % cfg.tile_n or k % cfg.tile_k:
+            continue
+        out32 = cfg.c_elem == pkg.ELEM_F32
+        c = torch.empty(m, n, dtype=torch.float32 if out32 else torch.float16,
+                        device=dev)
+        pkg.matmul_tn_config(cfg.index, a.to(dev), bt.to(dev), c)
+        fp16_ok(oracle, c.cpu().numpy(), ref32 if out32 else ref16)
+        ran += 1
+    assert ran > 0
+
+
+def test_matmul_f16_accumulate(pkg, oracle, dev):
+    g = torch.Generator().manual_seed(3)
+    for m, n, k, bt in ((512, 512, 256, True), (100, 70, 90, False)):
+        a = torch.randn(m, k, generator=g).half()
+        b = torch.randn(n, k, generator=g).half() if bt else torch.randn(
+            k, n, generator=g).half()
+        init = torch.randn(m, n, generator=g)
+        c = init.to(dev).clone()
+        pkg.matmul(a.to(dev), b.to(dev), c, b_transposed=bt, accumulate=True,
+                   out_dtype=torch.float32)
+        ref = oracle.matmul_f16(a.numpy(), b.numpy(), init.numpy(),
+                                b_transposed=bt, out_f32=True)
+        fp16_ok(oracle, c.cpu().numpy(), ref)
+        c16 = init.half().to(dev)
+        pkg.matmul(a.to(dev), b.to(dev), c16, b_transposed=bt, accumulate=True)
+        ref16 = oracle.matmul_f16(a.numpy(), b.numpy(), init.half().numpy(),
+                                  b_transposed=bt)
+        fp16_ok(oracle, c16.cpu().numpy(), ref16)
+
+
+@pytest.mark.parametrize("m,n,k", [(2048, 4096, 4096), (128, 11008, 4096),
+                                   (16, 4096, 11008)])
+def test_c3_linear_sweep(pkg, oracle, inputs, dev, m, n, k):
+    x, w = inputs.c3_linear_f16(m, n, k)
+    y = pkg.matmul(x.to(dev), w.to(dev))
+    rows = min(m, 256)  # oracle on a row slice keeps the test short
+    ref = oracle.matmul_f16(x[:rows].numpy(), w.numpy())
+    fp16_ok(oracle, y[:rows].cpu().numpy(), ref)
+
+
+def test_c3_linear_transposed_weights_full(pkg, oracle, inputs, dev):
+    x, w = inputs.c3_linear_f16(2048, 4096, 4096)
+    wt = w.t().contiguous()
+    y = pkg.matmul(x.to(dev), wt.to(dev), b_transposed=True)
+    ref = oracle.matmul_f16(x.numpy(), wt.numpy(), b_transposed=True)
+    fp16_ok(oracle, y.cpu().numpy(), ref)
+
+
+# ------------------------------------------------------------------ GEMV ----
+
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (1, 11008, 4096),
+                                   (1, 4096, 11008), (2, 520, 1000),
+                                   (4, 4096, 4096), (3, 8, 7), (1, 1024, 1024)])
+def test_gemv_f16(pkg, oracle, dev, m, n, k):
+    g = torch.Generator().manual_seed(m * 7 + n + k)
+    x = (torch.randn(m, k, generator=g) * 0.02).half()
+    w = (torch.randn(k, n, generator=g) * 0.02).half()
+    assert pkg.plan(pkg.make_desc(0, 0, 0, m, n, k, 0)).family == pkg.FAMILY_GEMV
+    buf, y = canary_out((m, n), torch.float16, dev, 3.0)
+    pkg.matmul(x.to(dev), w.to(dev), y)
+    ref = oracle.matmul_f16(x.numpy(), w.numpy())
+    check_canary(buf, m, n, 3.0)
+    fp16_ok(oracle, y.cpu().numpy(), ref)
+    # f32 output and accumulate through the same kernel
+    init = torch.randn(m, n, generator=g)
+    y32 = init.to(dev).clone()
+    pkg.matmul(x.to(dev), w.to(dev), y32, accumulate=True,
+               out_dtype=torch.float32)
+    ref32 = oracle.matmul_f16(x.numpy(), w.numpy(), init.numpy(), out_f32=True)
+    fp16_ok(oracle, y32.cpu().numpy(), ref32)
+
+
+def test_gemv_repeated_calls_rearm_counters(pkg, oracle, dev):
+    g = torch.Generator().manual_seed(11)
+    for n, k in ((4096, 4096), (2048, 8192), (4096, 4096), (512, 300)):
+        x = torch.randn(1, k, generator=g).half()
+        w = (torch.randn(k, n, generator=g) * 0.05).half()
+        y = pkg.matmul(x.to(dev), w.to(dev))
+        fp16_ok(oracle, y.cpu().numpy(), oracle.matmul_f16(x.numpy(), w.numpy()))
+
+
+def test_gemv_caller_workspace(pkg, oracle, dev):
+    lib = pkg.library()
+    m, n, k = 1, 4096, 4096
+    need = lib.iree_mi355x_matmul_workspace_bytes(m, n, k, 0)
+    assert need > 0
+    ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(m, k, generator=g).half().to(dev)
+    w = (torch.randn(k, n, generator=g) * 0.02).half().to(dev)
+    y = torch.empty(m, n, dtype=torch.float16, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    st = lib.iree_mi355x_matmul_f16(x.data_ptr(), w.data_ptr(), y.data_ptr(),
+                                    m, n, k, k, n, n, 0, ws.data_ptr(), 16, s)
+    assert st == pkg.WORKSPACE_TOO_SMALL
+    for _ in range(2):
+        st = lib.iree_mi355x_matmul_f16(x.data_ptr(), w.data_ptr(),
+                                        y.data_ptr(), m, n, k, k, n, n, 0,
+                                        ws.data_ptr(), need, s)
+        assert st == pkg.OK
+        ref = oracle.matmul_f16(x.cpu().numpy(), w.cpu().numpy())
+        fp16_ok(oracle, y.cpu().numpy(), ref)
+
+
+# ------------------------------------------------------------- int8 matmul --
+
+def test_matmul_i8_golden(pkg, dev):
+    d = np.load(os.path.join(GOLDEN, "matmul_i8.npz"))
+    c = pkg.matmul(torch.from_numpy(d["a"]).to(dev),
+                   torch.from_numpy(d["bt"]).to(dev), b_transposed=True)
+    assert np.array_equal(c.cpu().numpy(), d["expected"])
+
+
+@pytest.mark.parametrize("shape", [(256, 256, 128), (512, 512, 512),
+                                   (256, 1024, 384)])
+def test_matmul_i8_tn_configs(pkg, oracle, dev, shape):
+    m, n, k = shape
+    g = torch.Generator().manual_seed(m + 2 * n + k)
+    a = torch.randint(-128, 128, (m, k), generator=g).to(torch.int8)
+    bt = torch.randint(-128, 128, (n, k), generator=g).to(torch.int8)
+    ref = oracle.matmul_i8(a.numpy(), bt.numpy(), b_transposed=True)
+    ran = 0
+    for cfg in pkg.tn_configs():
+        if cfg.a_elem != pkg.ELEM_I8:
+            continue
+        if m % cfg.tile_m or n % cfg.tile_n or k % cfg.tile_k:
+            continue
+        c = torch.empty(m, n, dtype=torch.int32, device=dev)
+        pkg.matmul_tn_config(cfg.index, a.to(dev), bt.to(dev), c)
+        assert np.array_equal(c.cpu().numpy(), ref), cfg.name
+        ran += 1
+    assert ran > 0
+
+
+@pytest.mark.parametrize("m,n,k,bt", [(17, 19, 23, False), (65, 64, 64, True),
+                                      (100, 130, 257, False), (1, 4096, 4096, False),
+                                      (33, 70, 129, True)])
+def test_matmul_i8_general(pkg, oracle, dev, m, n, k, bt):
+    g = torch.Generator().manual_seed(m + n + k)
+    a = torch.randint(-128, 128, (m, k), generator=g).to(torch.int8)
+    b = torch.randint(-128, 128, (n, k) if bt else (k, n), generator=g).to(torch.int8)
+    init = torch.randint(-10 ** 6, 10 ** 6, (m, n), generator=g, dtype=torch.int32)
+    buf, c = canary_out((m, n), torch.int32, dev, 12345)
+    c.copy_(init.to(dev))
+    pkg.matmul(a.to(dev), b.to(dev), c, b_transposed=bt, accumulate=True)
+    ref = oracle.matmul_i8(a.numpy(), b.numpy(), init.numpy(), b_transposed=bt)
+    assert np.array_equal(c.cpu().numpy(), ref)
+    check_canary(buf, m, n, 12345)
+
+
+def test_c2_matmul_i8_4096_bit_exact(pkg, oracle, inputs, dev):
+    a, bt = inputs.c2_matmul_i8()
+    c = pkg.matmul(a.to(dev), bt.to(dev), b_transposed=True)
+    got = c.cpu().numpy()
+    # size-independent check first: row sums = A . (sum of B rows), in int64
+    row_sums = a.numpy().astype(np.int64) @ bt.numpy().astype(np.int64).sum(0)
+    assert np.array_equal(got.astype(np.int64).sum(1), row_sums)
+    ref = oracle.matmul_i8(a.numpy(), bt.numpy(), b_transposed=True)
+    assert np.array_equal(got, ref)
+
+
+# ------------------------------------------------------------------ W8A16 ---
+
+@pytest.mark.parametrize("m", [1, 4])
+def test_c5_w8a16_gemv(pkg, oracle, inputs, dev, m):
+    x, w, s = inputs.c5_w8a16(m)
+    y = pkg.quantized_matmul(x.to(dev), w.to(dev), s.to(dev))
+    ref = oracle.w8a16(x.numpy(), w.numpy(), s.numpy())
+    fp16_ok(oracle, y.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("m,transposed", [(512, False), (37, True), (5, False)])
+def test_w8a16_general(pkg, oracle, inputs, dev, m, transposed):
+    x, w, s = inputs.c5_w8a16(m, n=1100 if m != 512 else 11008, k=4096)
+    if transposed:
+        w = w.t().contiguous()
+    y = pkg.quantized_matmul(x.to(dev), w.to(dev), s.to(dev),
+                             w_transposed=transposed)
+    rows = min(m, 128)
+    ref = oracle.w8a16(x[:rows].numpy(), w.numpy(), s.numpy(),
+                       w_transposed=transposed)
+    fp16_ok(oracle, y[:rows].cpu().numpy(), ref)
+
+
+# -------------------------------------------------------------- attention ---
+
+@pytest.mark.parametrize("name", ["b1h2s128d64_causal", "b1h2s128d64",
+                                  "b1h1s160d128_causal"])
+def test_attention_golden(pkg, oracle, dev, name):
+    d = np.load(os.path.join(GOLDEN, f"attention_{name}.npz"))
+    q, k, v = (torch.from_numpy(d[x]).to(dev) for x in ("q", "k", "v"))
+    o = pkg.attention(q, k, v, causal=bool(d["causal"]))
+    got = o.cpu().numpy()
+    atol, rtol, rel_l2 = d["tol"]
+    rel, _, close = oracle.compare_arrays(d["expected"], got, atol, rtol)
+    assert close and rel <= rel_l2
+    fp16_ok(oracle, got, d["expected"])
+
+
+@pytest.mark.parametrize("shape,causal", [((1, 4, 512, 128), True),
+                                          ((2, 3, 200, 64), False),
+                                          ((1, 2, 333, 128), True),
+                                          ((4, 1, 1024, 128), False)])
+def test_attention_vs_oracle(pkg, oracle, dev, shape, causal):
+    g = torch.Generator().manual_seed(sum(shape))
+    q, k, v = (torch.randn(shape, generator=g).half() for _ in range(3))
+    o = pkg.attention(q.to(dev), k.to(dev), v.to(dev), causal=causal)
+    ref = oracle.attention_f16(q.numpy(), k.numpy(), v.numpy(), causal=causal)
+    fp16_ok(oracle, o.cpu().numpy(), ref)
+
+
+def test_c4_attention_full(pkg, oracle, inputs, dev):
+    q, k, v = inputs.c4_attention_f16()
+    o = pkg.attention(q.to(dev), k.to(dev), v.to(dev), causal=True)
+    got = o.cpu().numpy()
+    # query 0 attends only key 0
+    assert np.array_equal(got[:, :, 0], v.numpy()[:, :, 0])
+    ref = oracle.attention_f16(q.numpy(), k.numpy(), v.numpy(), causal=True)
+    fp16_ok(oracle, got, ref)
+
+
+# ------------------------------------------------------ executable library --
+
+def test_dispatch_through_export_table(pkg, oracle, dev):
+    g = torch.Generator().manual_seed(21)
+    m, n, k = 256, 512, 128
+    a = torch.randint(-128, 128, (m, k), generator=g).to(torch.int8).to(dev)
+    bt = torch.randint(-128, 128, (n, k), generator=g).to(torch.int8).to(dev)
+    c = torch.zeros(m, n, dtype=torch.int32, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    st = pkg.call_export(
+        "matmul_i8", pkg.matmul_constants(m, n, k, k, k, n, pkg.B_TRANSPOSED),
+        [a.data_ptr(), bt.data_ptr(), c.data_ptr()],
+        [a.numel(), bt.numel(), c.numel() * 4], s)
+    assert st == pkg.OK, pkg.last_error()
+    ref = oracle.matmul_i8(a.cpu().numpy(), bt.cpu().numpy(), b_transposed=True)
+    assert np.array_equal(c.cpu().numpy(), ref)
+    q, kk, v = (torch.randn(1, 2, 128, 64, generator=g).half().to(dev)
+                for _ in range(3))
+    o = torch.empty_like(q)
+    nbytes = q.numel() * 2
+    st = pkg.call_export("attention_f16",
+                         pkg.attention_constants(1, 2, 128, 128, 64, 0.125, 1),
+                         [q.data_ptr(), kk.data_ptr(), v.data_ptr(), o.data_ptr()],
+                         [nbytes] * 4, s)
+    assert st == pkg.OK, pkg.last_error()
+    ref = oracle.attention_f16(q.cpu().numpy(), kk.cpu().numpy(),
+                               v.cpu().numpy(), scale=0.125, causal=True)
+    fp16_ok(oracle, o.cpu().numpy(), ref)

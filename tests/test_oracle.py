@@ -1,0 +1,260 @@
+"""The CPU oracle pinned against golden vectors, closed forms and independent
+implementations (no GPU). A check here must fail for a plausible mistake in
+the oracle: a dropped term, a wrong sign or index, a transposed operand."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from conftest import GOLDEN
+
+
+# ------------------------------------------------------------------ f16 ----
+
+def test_f16_to_f32_exhaustive(oracle):
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    h = bits.view(np.float16)
+    got = oracle.f16_to_f32(h)
+    want = h.astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_matches_numpy_rne(oracle):
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.standard_normal(200000).astype(np.float32) * 100,
+        rng.standard_normal(100000).astype(np.float32) * 1e-5,   # subnormals
+        (np.arange(65536, dtype=np.uint32).astype(np.uint16)
+         .view(np.float16).astype(np.float32)),                 # exact halves
+        # ties: midpoints between adjacent halves round to even
+        ((np.arange(1, 30000, dtype=np.uint32).astype(np.uint16).view(np.float16)
+          .astype(np.float64) + np.arange(2, 30001, dtype=np.uint32)
+          .astype(np.uint16).view(np.float16).astype(np.float64)) / 2)
+        .astype(np.float32),
+        np.array([65504, 65519.9, 65520, 1e9, -1e9, np.inf, -np.inf, 0.0, -0.0,
+                  2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26], np.float32),
+    ])
+    got = oracle.f32_to_f16(x)
+    want = x.astype(np.float16)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
+# -------------------------------------------------------------- matmul i8 --
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (17, 19, 23), (64, 65, 63),
+                                   (5, 300, 257)])
+@pytest.mark.parametrize("bt", [False, True])
+def test_matmul_i8_vs_int64(oracle, m, n, k, bt):
+    rng = np.random.default_rng(m * 1000 + n + k)
+    a = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-128, 128, (n, k) if bt else (k, n), dtype=np.int8)
+    want = a.astype(np.int64) @ (b.T if bt else b).astype(np.int64)
+    got = oracle.matmul_i8(a, b, b_transposed=bt)
+    assert np.array_equal(got, want.astype(np.int32))
+    init = rng.integers(-1000, 1000, (m, n), dtype=np.int32)
+    got = oracle.matmul_i8(a, b, init, b_transposed=bt)
+    assert np.array_equal(got, (want + init).astype(np.int32))
+
+
+def test_matmul_i8_extreme_values_no_overflow(oracle):
+    # |sum| <= 4096 * 128 * 128 = 2^26 < 2^31: the worst case is exact.
+    k = 4096
+    a = np.full((2, k), -128, np.int8)
+    b = np.full((k, 3), -128, np.int8)
+    assert (oracle.matmul_i8(a, b) == 128 * 128 * k).all()
+    b[:, 1] = 127
+    assert (oracle.matmul_i8(a, b)[:, 1] == -128 * 127 * k).all()
+
+
+def test_matmul_i8_golden(oracle):
+    d = np.load(os.path.join(GOLDEN, "matmul_i8.npz"))
+    got = oracle.matmul_i8(d["a"], d["bt"], b_transposed=True)
+    assert np.array_equal(got, d["expected"])
+
+
+# ------------------------------------------------------------- matmul f16 --
+
+@pytest.mark.parametrize("name", ["small_prime_17x19x23", "ragged_m_65x64x64",
+                                  "ragged_n_64x65x64", "ragged_k_64x64x65",
+                                  "square_32x32x32"])
+def test_matmul_f16_golden_micro_models(oracle, name):
+    d = np.load(os.path.join(GOLDEN, f"matmul_{name}.npz"))
+    atol, rtol, rel_l2 = d["tol"]
+    got = oracle.matmul_f16(d["a"], d["b"], out_f32=True)
+    rel, _, close = oracle.compare_arrays(d["expected"], got, atol, rtol)
+    assert close and rel <= rel_l2
+    # f32 accumulation of exact f16 products: far inside the model tolerance
+    assert oracle.fp16_parity(got, d["expected"]) < 1e-5
+
+
+def test_matmul_f16_exact_small_integers(oracle):
+    # products and partial sums are small integers: exact in f32, order-free
+    rng = np.random.default_rng(1)
+    a = rng.integers(-3, 4, (33, 70)).astype(np.float16)
+    b = rng.integers(-3, 4, (70, 45)).astype(np.float16)
+    want = a.astype(np.int64) @ b.astype(np.int64)
+    got = oracle.matmul_f16(a, b, out_f32=True)
+    assert np.array_equal(got, want.astype(np.float32))
+    got_t = oracle.matmul_f16(a, np.ascontiguousarray(b.T), b_transposed=True,
+                              out_f32=True)
+    assert np.array_equal(got_t, want.astype(np.float32))
+    got16 = oracle.matmul_f16(a, b)
+    assert np.array_equal(got16, want.astype(np.float16))
+
+
+def test_matmul_f16_identity_and_accumulate(oracle):
+    rng = np.random.default_rng(2)
+    a = rng.standard_normal((40, 24)).astype(np.float16)
+    eye = np.eye(24, dtype=np.float16)
+    assert np.array_equal(oracle.matmul_f16(a, eye), a)
+    init = rng.standard_normal((40, 24)).astype(np.float32)
+    got = oracle.matmul_f16(a, eye, init, out_f32=True)
+    assert np.array_equal(got, init + a.astype(np.float32))
+
+
+def test_matmul_f16_rounds_once_rne(oracle):
+    # 1 + 2^-11 is a tie between 1 and 1+2^-10 in f16: RNE gives 1.0
+    a = np.array([[1.0, 2.0 ** -11]], np.float16)
+    b = np.array([[1.0], [1.0]], np.float16)
+    assert oracle.matmul_f16(a, b)[0, 0] == np.float16(1.0)
+    a = np.array([[1.0 + 2.0 ** -10, 2.0 ** -11]], np.float16)
+    assert oracle.matmul_f16(a, b)[0, 0] == np.float16(1.0 + 2.0 ** -9)
+
+
+def test_matmul_f16_sensitive_to_transpose(oracle):
+    # a transposed-operand bug cannot pass the comparisons above
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal((16, 16)).astype(np.float16)
+    b = rng.standard_normal((16, 16)).astype(np.float16)
+    good = oracle.matmul_f16(a, b, out_f32=True)
+    wrong = oracle.matmul_f16(a, b, b_transposed=True, out_f32=True)
+    assert oracle.fp16_parity(wrong, good) > 0.1
+
+
+# ------------------------------------------------------------------ w8a16 --
+
+def test_w8a16_exact_power_of_two_scales(oracle):
+    rng = np.random.default_rng(4)
+    x = rng.integers(-4, 5, (3, 64)).astype(np.float16)
+    w = rng.integers(-128, 128, (64, 48), dtype=np.int8)
+    s = (2.0 ** -rng.integers(3, 8, 48)).astype(np.float16)
+    want = (x.astype(np.int64) @ w.astype(np.int64)) * s.astype(np.float64)
+    got = oracle.w8a16(x, w, s)
+    assert np.array_equal(got, want.astype(np.float16))
+    got_t = oracle.w8a16(x, np.ascontiguousarray(w.T), s, w_transposed=True)
+    assert np.array_equal(got_t, got)
+
+
+def test_w8a16_matches_per_element_dequant(oracle, inputs):
+    x, w, s = (t.numpy() for t in inputs.c5_w8a16(4, n=512, k=1024))
+    got = oracle.w8a16(x, w, s)
+    deq = (w.astype(np.float64) * s.astype(np.float64)).astype(np.float16)
+    want = x.astype(np.float64) @ deq.astype(np.float64)
+    assert oracle.fp16_parity(got, want) < 2e-3
+
+
+# -------------------------------------------------------------- attention --
+
+@pytest.mark.parametrize("name", ["b1h2s128d64_causal", "b1h2s128d64",
+                                  "b1h1s160d128_causal"])
+def test_attention_golden_sdpa(oracle, name):
+    d = np.load(os.path.join(GOLDEN, f"attention_{name}.npz"))
+    got = oracle.attention_f16(d["q"], d["k"], d["v"], causal=bool(d["causal"]))
+    atol, rtol, rel_l2 = d["tol"]
+    rel, _, close = oracle.compare_arrays(d["expected"], got, atol, rtol)
+    assert close and rel <= rel_l2
+    assert oracle.fp16_parity(got, d["expected"]) < 1e-3
+
+
+def test_attention_causal_invariants(oracle):
+    rng = np.random.default_rng(5)
+    q, k, v = (rng.standard_normal((1, 2, 50, 64)).astype(np.float16)
+               for _ in range(3))
+    o = oracle.attention_f16(q, k, v, causal=True)
+    # query 0 sees only key 0: output is V[0] exactly
+    assert np.array_equal(o[:, :, 0], v[:, :, 0])
+    # q = 0: uniform weights, row i is the mean of V[0..i]
+    o0 = oracle.attention_f16(np.zeros_like(q), k, v, causal=True)
+    csum = np.cumsum(v.astype(np.float64), axis=2)
+    mean = csum / np.arange(1, 51)[None, None, :, None]
+    assert np.abs(o0.astype(np.float64) - mean).max() < 2e-3
+    # future keys/values do not change earlier rows
+    k2, v2 = k.copy(), v.copy()
+    k2[:, :, 30:] = 7
+    v2[:, :, 30:] = -7
+    o2 = oracle.attention_f16(q, k2, v2, causal=True)
+    assert np.array_equal(o2[:, :, :30], o[:, :, :30])
+
+
+def test_attention_vs_torch_sdpa_nonsquare(oracle):
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn(1, 3, 40, 64, generator=g).half()
+    k = torch.randn(1, 3, 72, 64, generator=g).half()
+    v = torch.randn(1, 3, 72, 64, generator=g).half()
+    want = F.scaled_dot_product_attention(q.float(), k.float(), v.float())
+    got = oracle.attention_f16(q.numpy(), k.numpy(), v.numpy(), causal=False)
+    assert oracle.fp16_parity(got, want.numpy()) < 1e-3
+
+
+# --------------------------------------------------------------- planner ---
+
+def test_select_hmx_tile_sizes_lit_goldens(oracle):
+    with open(os.path.join(GOLDEN, "tile_search.json")) as f:
+        spec = json.load(f)
+    for case in spec["cases"]:
+        got = oracle.select_hmx_tile_sizes(
+            case["m"], case["n"], case["k"], elem_bytes=case["elem_bytes"],
+            b_transposed=case["b_transposed"],
+            budget_bytes=spec["budget_flag_bytes"],
+            double_buffering=spec["double_buffering"])
+        assert got == case["expected"], (case, got)
+
+
+def test_select_hmx_tile_sizes_budget_matters(oracle):
+    # without the halve-then-double budget plumbing, the first golden would
+    # pick N=64 (a 4 MiB budget admits it): the plumbing is pinned
+    got = oracle.select_hmx_tile_sizes(52, 896, 7680, elem_bytes=(2, 2, 4),
+                                       b_transposed=True,
+                                       budget_bytes=4 * 1024 * 1024)
+    assert got == [52, 64, 7680]
+
+
+def brute_force_tiling_factor(bound, preferred, multiple_of):
+    if preferred <= 0:
+        return 0
+    step = max(1, multiple_of)
+    if bound <= 0 or bound % step or preferred < step:
+        return min(bound, preferred)
+    best = 0
+    for d in range(1, bound // step + 1):
+        if (bound // step) % d == 0 and d * step <= preferred:
+            best = max(best, d * step)
+    return best
+
+
+def test_choose_static_tiling_factor_brute_force(oracle):
+    for bound in list(range(-2, 130)) + [4096, 11008, 7680]:
+        for preferred in (-1, 0, 1, 3, 8, 13, 32, 64, 200):
+            for mult in (0, 1, 2, 8, 32):
+                want = brute_force_tiling_factor(bound, preferred, mult)
+                got = oracle.choose_static_tiling_factor(bound, preferred, mult)
+                assert got == want, (bound, preferred, mult)
+    assert oracle.choose_static_tiling_factor(oracle.DYNAMIC, 8, 1) == 8
+
+
+def test_hmx_pack_reference_cases(oracle):
+    d = np.load(os.path.join(GOLDEN, "hmx_pack.npz"))
+    got = oracle.hmx_pack_f16(d["full_src"], 1, 1, stride=32)
+    assert np.array_equal(got.view(np.uint16), d["full_packed"].view(np.uint16))
+    src = d["ragged_src"]
+    out = np.empty(9 * 1024, np.float16)
+    lib = oracle._load()
+    lib.oracle_hmx_pack_f16(out.ctypes.data, np.ascontiguousarray(src).ctypes.data,
+                            41, 35, 37, 3, 3)
+    assert np.array_equal(out.view(np.uint16), d["ragged_packed"].view(np.uint16))
+    assert not (out == 99).any()
