@@ -36,22 +36,57 @@ def parse():
     p.add_argument("--suite", action="store_true")
     p.add_argument("--tune", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-graph", action="store_true",
+                   help="time eager launches instead of one captured graph")
+    p.add_argument("--only", choices=["i8", "f16", "f16nn", "gemv", "attn",
+                                      "w8a16", "w8a16_gemm"],
+                   help="run one workload (for rocprof passes) and exit")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="with --only: first copy 256 MiB device-to-device "
+                        "once, the known-size reference for FETCH_SIZE / "
+                        "WRITE_SIZE counter scaling")
     return p.parse_args()
 
 
+USE_GRAPH = True
+
+
 def timed(fn, steps, warmup):
-    """Average ms per call of fn() over `steps` calls, HIP events on the
-    current stream (the stream every op is enqueued on)."""
+    """Average ms per step of fn() over exactly `steps` steps.
+
+    `warmup` eager steps first (they also size the library workspace, so the
+    timed steps allocate nothing). The `steps` launches are then captured into
+    one HIP graph (no memset nodes: the kernels re-arm their own counters) and
+    replayed once untimed and once between HIP events recorded on the capture
+    stream, with a device synchronize on both sides. Without the graph a
+    5-microsecond GEMV would measure the Python launch path, not the kernel.
+    """
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    if not USE_GRAPH:
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            fn()
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / steps
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for _ in range(steps):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
-        fn()
-    stop.record()
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        graph.replay()
+        stop.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / steps
 
@@ -86,6 +121,10 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
+    global USE_GRAPH
+    USE_GRAPH = not args.no_graph
+    if args.only:
+        return only(pkg, inputs, dev, args)
     if args.tune:
         return tune(pkg, inputs, dev, args)
     if args.suite:
@@ -242,6 +281,53 @@ def suite(pkg, inputs, dev, args):
              n * k + 2 * n + 2 * m * k + 2 * m * n, "hbm" if m == 1 else "mfma",
              {"rotating_copies": copies})
         del ws
+
+
+def only(pkg, inputs, dev, args):
+    """One workload, for profiler passes: prints ms per step."""
+    import torch
+    w = args.only
+    if args.calibrate_copy:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    if w == "i8":
+        a, bt = (t.to(dev) for t in inputs.c2_matmul_i8())
+        c = torch.empty(4096, 4096, dtype=torch.int32, device=dev)
+        fn = lambda: pkg.matmul(a, bt, c, b_transposed=True)  # noqa: E731
+    elif w in ("f16", "f16nn"):
+        x, wt = inputs.c3_linear_f16(4096, 4096, 4096)
+        x = x.to(dev)
+        bt = w == "f16"
+        b = (wt.t().contiguous() if bt else wt).to(dev)
+        c = torch.empty(4096, 4096, dtype=torch.float16, device=dev)
+        fn = lambda: pkg.matmul(x, b, c, b_transposed=bt)  # noqa: E731
+    elif w == "gemv":
+        copies = ROTATE_BYTES // (4096 * 4096 * 2) + 1
+        ws = [(torch.randn(4096, 4096, device=dev) * 0.02).half()
+              for _ in range(copies)]
+        x = torch.randn(1, 4096, device=dev).half()
+        y = torch.empty(1, 4096, dtype=torch.float16, device=dev)
+        it = [0]
+
+        def fn():
+            pkg.matmul(x, ws[it[0] % copies], y)
+            it[0] += 1
+    elif w == "attn":
+        q, k, v = (t.to(dev) for t in inputs.c4_attention_f16())
+        o = torch.empty_like(q)
+        fn = lambda: pkg.attention(q, k, v, o, causal=True)  # noqa: E731
+    else:
+        m = 1 if w == "w8a16" else 512
+        x, wq, s = (t.to(dev) for t in inputs.c5_w8a16(m))
+        y = torch.empty(m, wq.shape[1], dtype=torch.float16, device=dev)
+        fn = lambda: pkg.quantized_matmul(x, wq, s, y)  # noqa: E731
+    ms = timed(fn, args.steps, args.warmup)
+    print(json.dumps({"only": w, "ms_per_step": round(ms, 5),
+                      "steps": args.steps}), flush=True)
 
 
 def tune(pkg, inputs, dev, args):

@@ -110,6 +110,32 @@ __device__ __forceinline__ i32x4 lds_read_16(const IHP_LDS char *p) {
   return *(const IHP_LDS i32x4 *)p;
 }
 
+// ds_read_b128 issued as inline asm: the compiler inserts no wait for it, so
+// the caller must wait with lgkm_wait<N>() and tie the result registers with
+// lgkm_tie() before using them. LDS reads return in issue order, so after
+// issuing R more reads, lgkmcnt(R) guarantees this one has landed.
+template <int OFF>
+__device__ __forceinline__ i32x4 lds_read_16_async(const IHP_LDS char *p) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset range");
+  i32x4 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2"
+               : "=v"(v)
+               : "v"((unsigned)(uintptr_t)p), "i"(OFF));
+  return v;
+}
+
+template <int N>
+__device__ __forceinline__ void lgkm_wait() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N));
+}
+
+// Orders every later use of `v` after the preceding lgkm_wait (both are
+// volatile asm, which keep their order).
+__device__ __forceinline__ void lgkm_tie(i32x4 &v) {
+  asm volatile("" : "+v"(v));
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own
 // L2). Renumber them so that consecutive logical tile ids share an XCD, then
 // walk tiles in GROUP_M-row bands so an XCD's tiles reuse the same A row

@@ -16,10 +16,21 @@
 //    the whole K loop (the reference reads its accumulator out as f16,
 //    HexagonConvertMatmulToHmx.cpp:592-596; this keeps full precision);
 //  * the unpack (add into the DPS init, UK/hmx.c:328-357) is the epilogue.
+#include <type_traits>
+
 #include "device_common.h"
 #include "kernels_internal.h"
 
 namespace ihp {
+
+// Compile-time loop: f(std::integral_constant<int, I>()) for I in [0, N).
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>());
+    static_for<N, I + 1>(f);
+  }
+}
 
 // ----------------------------------------------------------------------------
 // Fast path: A [M,K] and B [N,K], both K-contiguous ("TN"), every extent a
@@ -28,9 +39,13 @@ namespace ihp {
 
 template <int CH>
 __device__ __forceinline__ int chunk_swizzle(int row) {
-  // 16-byte chunk permutation of a staged row of CH chunks. Rows are grouped
-  // so that 8 consecutive rows cover all 32 banks of one 128-byte bank line.
-  return (row / (8 / CH)) % CH;
+  // 16-byte chunk permutation of a staged row of CH chunks. gfx950 LDS has 64
+  // four-byte banks (a 256-byte bank line) and serves a ds_read_b128 16 lanes
+  // at a time; the 16 lanes of a fragment read 16 consecutive rows at one
+  // logical chunk. Rows sharing a bank line keep their offset within it, and
+  // the chunk index is XORed with the bank-line number, so the 16 reads hit
+  // 16 distinct 16-byte bank groups.
+  return (row / (16 / CH)) % CH;
 }
 
 template <typename T, typename OutT, int BM, int BN, int BKB, int WM, int WN,
@@ -54,7 +69,10 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_tn_lds_kernel(
   constexpr int STAGE_BYTES = (BM + BN) * BKB;
   constexpr int KSTEPS = BKB / 32;
   static_assert(BM % ROWS_PER_PASS == 0 && BN % ROWS_PER_PASS == 0, "tile");
-  static_assert(FM >= 1 && FN >= 1 && CH >= 2 && CH <= 8, "tile");
+  static_assert(FM >= 1 && FN >= 1 && (CH == 4 || CH == 8), "tile");
+  // The swizzle repeats every 16 rows. Block-wide copy passes start on that
+  // period, so a lane's swizzle depends only on its row within the pass.
+  static_assert(ROWS_PER_PASS % 16 == 0 && (16 / CH) * CH == 16, "swz");
   static_assert(KSTEPS % 2 == 0, "fragment double buffer parity");
   static_assert(STAGES >= 2 && (STAGES - 2) * LOADS_PER_STAGE < 64,
                 "vmcnt range");
@@ -73,7 +91,8 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_tn_lds_kernel(
   // chunk it fetches is the logical chunk that belongs in that slot. The
   // address is a wave-uniform base plus a 32-bit lane offset.
   const int ld_row = lane / CH;
-  const int ld_chunk = (lane % CH) ^ chunk_swizzle<CH>(ld_row);
+  const int ld_chunk =
+      (lane % CH) ^ chunk_swizzle<CH>(wave * ROWS_PER_WAVE + ld_row);
   const int64_t lda_b = lda * (int64_t)sizeof(T);
   const int64_t ldb_b = ldb * (int64_t)sizeof(T);
   const uint32_t a_lane =
@@ -110,14 +129,26 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_tn_lds_kernel(
   const int a_rd = (wm * WTM + rd_row) * BKB;
   const int b_rd = A_BYTES + (wn * WTN + rd_row) * BKB;
 
+  // Issue the FM + FN fragment reads of (slot, ks); they complete in order.
   auto read_frags = [&](int slot, int ks, i32x4 *af, i32x4 *bf) {
-    const IHP_LDS char *st = lds + slot * STAGE_BYTES;
+    const IHP_LDS char *pa = lds + slot * STAGE_BYTES + a_rd + koff[ks];
+    const IHP_LDS char *pb = lds + slot * STAGE_BYTES + b_rd + koff[ks];
+    static_for<FM>([&](auto i) {
+      af[i] = lds_read_16_async<decltype(i)::value * 32 * BKB>(pa);
+    });
+    static_for<FN>([&](auto j) {
+      bf[j] = lds_read_16_async<decltype(j)::value * 32 * BKB>(pb);
+    });
+  };
+  // Wait until at most N reads are outstanding, then pin the fragments.
+  auto frags_ready = [&](auto n, i32x4 *af, i32x4 *bf) {
+    lgkm_wait<decltype(n)::value>();
 #pragma unroll
     for (int i = 0; i < FM; ++i)
-      af[i] = lds_read_16(st + a_rd + i * 32 * BKB + koff[ks]);
+      lgkm_tie(af[i]);
 #pragma unroll
     for (int j = 0; j < FN; ++j)
-      bf[j] = lds_read_16(st + b_rd + j * 32 * BKB + koff[ks]);
+      lgkm_tie(bf[j]);
   };
 
   Acc acc[FM][FN];
@@ -144,6 +175,9 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_tn_lds_kernel(
   i32x4 af[2][FM], bf[2][FN];
   read_frags(0, 0, af[0], bf[0]);
 
+  // Per K step: issue the next step's fragment reads, wait only for this
+  // step's (issued one step earlier), then this step's MFMAs, which run
+  // while the new reads are in flight.
   for (int kt = 0; kt < nk; ++kt) {
     const int slot = kt % STAGES;
 #pragma unroll
@@ -151,19 +185,23 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_tn_lds_kernel(
       const int cur = ks & 1, nxt = cur ^ 1;
       if (ks + 1 < KSTEPS) {
         read_frags(slot, ks + 1, af[nxt], bf[nxt]);
+        frags_ready(std::integral_constant<int, FM + FN>(), af[cur], bf[cur]);
       } else if (kt + 1 < nk) {
-        // Stage handoff: stage kt+1 must have landed for every wave, and
-        // every wave must be done reading stage kt before its slot is
-        // refilled with stage kt+STAGES.
+        // Stage handoff: this step's fragments are in registers (all LDS
+        // reads done), stage kt+1 must have landed for every wave, and every
+        // wave must be done reading stage kt before its slot is refilled
+        // with stage kt+STAGES.
+        frags_ready(std::integral_constant<int, 0>(), af[cur], bf[cur]);
         if (kt + STAGES - 1 < nk)
           wait_vmcnt<(STAGES - 2) * LOADS_PER_STAGE>();
         else
           wait_vmcnt<0>();
-        wait_lgkmcnt0();
         block_barrier();
         if (kt + STAGES < nk)
           load_stage(kt + STAGES, slot);
         read_frags((kt + 1) % STAGES, 0, af[nxt], bf[nxt]);
+      } else {
+        frags_ready(std::integral_constant<int, 0>(), af[cur], bf[cur]);
       }
 #pragma unroll
       for (int i = 0; i < FM; ++i)
@@ -304,16 +342,25 @@ static hipError_t launch_tn(const MatmulArgs &a) {
 // name or by its LDS-budget ranking; the autotuner times them.
 // Names: <types>_tn_<BM>x<BN>x<BK in elements>_w<wave grid>_s<LDS stages>.
 static const TnConfig kTnConfigs[] = {
+    IHP_TN_CONFIG("i8_tn_256x256x128_w2x4_s2", int8_t, int32_t, 256, 256, 128, 2, 4, 2),
+    IHP_TN_CONFIG("i8_tn_256x256x64_w2x4_s4", int8_t, int32_t, 256, 256, 64, 2, 4, 4),
+    IHP_TN_CONFIG("i8_tn_256x256x64_w4x2_s5", int8_t, int32_t, 256, 256, 64, 4, 2, 5),
     IHP_TN_CONFIG("i8_tn_256x256x128_w2x2_s2", int8_t, int32_t, 256, 256, 128, 2, 2, 2),
-    IHP_TN_CONFIG("i8_tn_256x256x64_w2x2_s3", int8_t, int32_t, 256, 256, 64, 2, 2, 3),
-    IHP_TN_CONFIG("i8_tn_256x128x128_w2x2_s2", int8_t, int32_t, 256, 128, 128, 2, 2, 2),
-    IHP_TN_CONFIG("i8_tn_128x128x128_w2x2_s3", int8_t, int32_t, 128, 128, 128, 2, 2, 3),
+    IHP_TN_CONFIG("i8_tn_256x256x64_w2x2_s5", int8_t, int32_t, 256, 256, 64, 2, 2, 5),
+    IHP_TN_CONFIG("i8_tn_256x128x128_w2x4_s2", int8_t, int32_t, 256, 128, 128, 2, 4, 2),
+    IHP_TN_CONFIG("i8_tn_256x128x64_w2x2_s5", int8_t, int32_t, 256, 128, 64, 2, 2, 5),
+    IHP_TN_CONFIG("i8_tn_128x128x128_w2x2_s4", int8_t, int32_t, 128, 128, 128, 2, 2, 4),
+    IHP_TN_CONFIG("f16_tn_256x256x64_w2x4_s2", f16, f16, 256, 256, 128, 2, 4, 2),
+    IHP_TN_CONFIG("f16_tn_256x256x32_w2x4_s4", f16, f16, 256, 256, 64, 2, 4, 4),
+    IHP_TN_CONFIG("f16_tn_256x256x32_w4x2_s5", f16, f16, 256, 256, 64, 4, 2, 5),
     IHP_TN_CONFIG("f16_tn_256x256x64_w2x2_s2", f16, f16, 256, 256, 128, 2, 2, 2),
-    IHP_TN_CONFIG("f16_tn_256x256x32_w2x2_s3", f16, f16, 256, 256, 64, 2, 2, 3),
-    IHP_TN_CONFIG("f16_tn_256x128x64_w2x2_s2", f16, f16, 256, 128, 128, 2, 2, 2),
-    IHP_TN_CONFIG("f16_tn_128x128x64_w2x2_s3", f16, f16, 128, 128, 128, 2, 2, 3),
-    IHP_TN_CONFIG("f16f32_tn_256x256x64_w2x2_s2", f16, float, 256, 256, 128, 2, 2, 2),
-    IHP_TN_CONFIG("f16f32_tn_128x128x64_w2x2_s3", f16, float, 128, 128, 128, 2, 2, 3),
+    IHP_TN_CONFIG("f16_tn_256x256x32_w2x2_s5", f16, f16, 256, 256, 64, 2, 2, 5),
+    IHP_TN_CONFIG("f16_tn_256x128x64_w2x4_s2", f16, f16, 256, 128, 128, 2, 4, 2),
+    IHP_TN_CONFIG("f16_tn_256x128x32_w2x2_s5", f16, f16, 256, 128, 64, 2, 2, 5),
+    IHP_TN_CONFIG("f16_tn_128x128x64_w2x2_s4", f16, f16, 128, 128, 128, 2, 2, 4),
+    IHP_TN_CONFIG("f16f32_tn_256x256x64_w2x4_s2", f16, float, 256, 256, 128, 2, 4, 2),
+    IHP_TN_CONFIG("f16f32_tn_256x256x32_w2x4_s4", f16, float, 256, 256, 64, 2, 4, 4),
+    IHP_TN_CONFIG("f16f32_tn_128x128x64_w2x2_s4", f16, float, 128, 128, 128, 2, 2, 4),
 };
 
 const TnConfig *tn_configs(int *count) {

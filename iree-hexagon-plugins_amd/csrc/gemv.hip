@@ -105,7 +105,32 @@ __global__ __launch_bounds__(kThreads) void gemv_splitk_kernel(
 
   const char *wrow = (const char *)(W + n0);
   const int64_t ldw_b = ldw * (int64_t)sizeof(WT);
-  for (int64_t kb = k0 + tk; kb < k1; kb += kTK * kUnroll) {
+  // Full groups of kUnroll rows: every load in range, no per-load branch.
+  int64_t kb = k0 + tk;
+  if (col_ok) {
+    for (; kb + (int64_t)(kUnroll - 1) * kTK < k1; kb += kTK * kUnroll) {
+      i32x4 v[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u)
+        v[u] = __builtin_nontemporal_load(
+            (const i32x4 *)(wrow + (kb + (int64_t)u * kTK) * ldw_b));
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int64_t k = kb + (int64_t)u * kTK;
+        float w[CPT];
+        Tr::widen(v[u], w);
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+          const float xv = xs[r * kMaxKChunk + (k - k0)];
+#pragma unroll
+          for (int c = 0; c < CPT; ++c)
+            acc[r][c] += xv * w[c];
+        }
+      }
+    }
+  }
+  // Tail (K not a multiple of the group).
+  for (; kb < k1; kb += kTK * kUnroll) {
     i32x4 v[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -158,23 +183,29 @@ __global__ __launch_bounds__(kThreads) void gemv_splitk_kernel(
       const float sc = scale ? (float)scale[n] : 1.0f;
       store_y(Y + r * ldy + n, s * sc, accumulate);
     } else {
-      partials[((int64_t)split * MR + r) * N + n] = s;
+      // Agent-scope atomic store: written through past this XCD's L2, so a
+      // workgroup on another XCD reads it with an agent-scope atomic load.
+      __hip_atomic_store(&partials[((int64_t)split * MR + r) * N + n], s,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   if (direct)
     return;
 
-  // Publish the partial, then count arrivals for this column block.
-  __threadfence();
+  // Every partial store of this workgroup is acknowledged before its arrival
+  // is counted: vmcnt(0) per thread, then the barrier. Only the partials and
+  // the counter are shared between workgroups, and both are accessed with
+  // agent-scope atomics, so no L2 write-back / invalidate fence is needed.
+  wait_vmcnt<0>();
   __syncthreads();
   if (tid == 0) {
-    const unsigned prev = atomicAdd(&counters[blockIdx.x], 1u);
+    const unsigned prev = __hip_atomic_fetch_add(
+        &counters[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last_flag = prev == (unsigned)(splits - 1);
   }
   __syncthreads();
   if (!last_flag)
     return;
-  __threadfence();
   for (int i = tid; i < MR * BNC; i += kThreads) {
     const int r = i / BNC, col = i % BNC;
     const int64_t n = n_base + col;
@@ -182,12 +213,14 @@ __global__ __launch_bounds__(kThreads) void gemv_splitk_kernel(
       continue;
     float s = 0.0f;
     for (int sp = 0; sp < splits; ++sp)
-      s += __builtin_nontemporal_load(&partials[((int64_t)sp * MR + r) * N + n]);
+      s += __hip_atomic_load(&partials[((int64_t)sp * MR + r) * N + n],
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const float sc = scale ? (float)scale[n] : 1.0f;
     store_y(Y + r * ldy + n, s * sc, accumulate);
   }
-  if (tid == 0)
-    counters[blockIdx.x] = 0u;  // re-arm for the next call on this workspace
+  if (tid == 0)  // re-arm for the next call on this workspace
+    __hip_atomic_store(&counters[blockIdx.x], 0u, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
 }
 
 static int round_up(int64_t v, int64_t a) { return (int)((v + a - 1) / a * a); }

@@ -150,11 +150,11 @@ const iree_mi355x_executable_dispatch_attrs_t kAttrs[] = {
          IREE_MI355X_DISPATCH_FLAG_USES_MFMA |
          IREE_MI355X_DISPATCH_FLAG_USES_LDS_DMA |
          IREE_MI355X_DISPATCH_FLAG_USES_WORKSPACE,
-     131072, 256},
+     163840, 512},
     {IREE_MI355X_DISPATCH_FLAG_RESOURCES_VALID |
          IREE_MI355X_DISPATCH_FLAG_USES_MFMA |
          IREE_MI355X_DISPATCH_FLAG_USES_LDS_DMA,
-     131072, 256},
+     163840, 512},
     {IREE_MI355X_DISPATCH_FLAG_RESOURCES_VALID |
          IREE_MI355X_DISPATCH_FLAG_USES_MFMA |
          IREE_MI355X_DISPATCH_FLAG_USES_WORKSPACE,

@@ -28,7 +28,16 @@ struct TunedEntry {
   uint32_t flags;
   const char *config;
 };
+// Measured on MI355X with random inputs (bench.py --tune): the 4-wave
+// 256x256 tile wins for int8 (the 8-wave one draws more power for the same
+// work), the 8-wave one for f16.
 const TunedEntry kTuned[] = {
+    {IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_I32, 4096, 4096, 4096,
+     IREE_MI355X_MATMUL_B_TRANSPOSED, "i8_tn_256x256x128_w2x2_s2"},
+    {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 4096, 4096, 4096,
+     IREE_MI355X_MATMUL_B_TRANSPOSED, "f16_tn_256x256x64_w2x4_s2"},
+    {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F32, 4096, 4096, 4096,
+     IREE_MI355X_MATMUL_B_TRANSPOSED, "f16f32_tn_256x256x64_w2x4_s2"},
     {0, 0, 0, 0, 0, 0, nullptr},  // sentinel
 };
 

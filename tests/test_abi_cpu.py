@@ -46,7 +46,7 @@ def test_executable_library_table(pkg):
         attrs = lib.exports.attrs[i]
         assert attrs.flags & 1  # RESOURCES_VALID
         assert 0 < attrs.lds_bytes <= 160 * 1024
-        assert attrs.threads == 256
+        assert attrs.threads in (256, 512)
     # any other version: NULL, like the reference's exact-version rule
     assert pkg.executable_library(0x48580001) is None
     assert pkg.executable_library(pkg.EXECUTABLE_LIBRARY_VERSION + 1) is None
@@ -55,25 +55,33 @@ def test_executable_library_table(pkg):
 F16, I8, I32, F32 = 0, 1, 2, 3
 
 
-@pytest.mark.parametrize("case,family,config", [
-    ((I8, I8, I32, 4096, 4096, 4096, 1), 1, "i8_tn_256x256x128_w2x2_s2"),
-    ((F16, F16, F16, 4096, 4096, 4096, 1), 1, "f16_tn_256x256x64_w2x2_s2"),
-    ((F16, F16, F32, 4096, 4096, 4096, 1), 1, "f16f32_tn_256x256x64_w2x2_s2"),
-    ((F16, F16, F16, 2048, 4096, 4096, 1), 1, "f16_tn_256x128x64_w2x2_s2"),
-    ((F16, F16, F16, 128, 512, 256, 0), 2, "general_64x64"),
-    ((F16, F16, F16, 17, 19, 23, 1), 2, "general_64x64"),
-    ((F16, F16, F16, 1, 4096, 4096, 0), 3, "gemv_f16_r1"),
-    ((F16, F16, F16, 4, 11008, 4096, 0), 3, "gemv_f16_r4"),
-    ((F16, F16, F16, 5, 4096, 4096, 0), 2, "general_64x64"),
-    ((I8, I8, I32, 1, 4096, 4096, 0), 2, "general_64x64"),
+@pytest.mark.parametrize("case,family,tile", [
+    ((I8, I8, I32, 4096, 4096, 4096, 1), 1, (256, 256)),
+    ((F16, F16, F16, 4096, 4096, 4096, 1), 1, (256, 256)),
+    ((F16, F16, F32, 4096, 4096, 4096, 1), 1, (256, 256)),
+    ((F16, F16, F16, 2048, 4096, 4096, 1), 1, (256, 128)),
+    ((F16, F16, F16, 128, 512, 256, 0), 2, (64, 64)),
+    ((F16, F16, F16, 17, 19, 23, 1), 2, (64, 64)),
+    ((F16, F16, F16, 1, 4096, 4096, 0), 3, (1, 256)),
+    ((F16, F16, F16, 4, 11008, 4096, 0), 3, (4, 256)),
+    ((F16, F16, F16, 5, 4096, 4096, 0), 2, (64, 64)),
+    ((I8, I8, I32, 1, 4096, 4096, 0), 2, (64, 64)),
 ])
-def test_planner_classification(pkg, case, family, config):
+def test_planner_classification(pkg, case, family, tile):
     a, b, c, m, n, k, flags = case
     d = pkg.make_desc(a, b, c, m, n, k, flags)
     assert pkg.classify(d) == family
     p = pkg.plan(d)
     assert p.family == family
-    assert p.config_name.decode() == config
+    assert (p.tile_m, p.tile_n) == tile
+    name = p.config_name.decode()
+    prefix = {1: ("i8_tn_" if a == I8 else ("f16f32_tn_" if c == F32 else "f16_tn_")),
+              2: "general_", 3: "gemv_"}[family]
+    assert name.startswith(prefix), name
+    if family == 1:
+        # the chosen config really has this macro-tile and fits the LDS budget
+        cfg = [x for x in pkg.tn_configs() if x.name == name][0]
+        assert (cfg.tile_m, cfg.tile_n) == tile and cfg.lds_bytes <= 160 * 1024
 
 
 def test_planner_w8a16_and_unsupported_types(pkg):
@@ -96,9 +104,9 @@ def test_planner_lds_budget_and_alignment(pkg):
     assert pkg.classify(d) == pkg.FAMILY_GENERAL
     d = pkg.make_desc(I8, I8, I32, 4096, 4096, 4096, 1, aligned=False)
     assert pkg.classify(d) == pkg.FAMILY_GENERAL
-    d = pkg.make_desc(I8, I8, I32, 4096, 4096, 4096, 1, lds_budget_bytes=100 * 1024)
+    d = pkg.make_desc(I8, I8, I32, 4096, 4096, 4096, 1, lds_budget_bytes=130 * 1024)
     p = pkg.plan(d)
-    assert p.lds_bytes <= 100 * 1024 and p.family == pkg.FAMILY_MFMA_TN
+    assert p.lds_bytes <= 130 * 1024 and p.family == pkg.FAMILY_MFMA_TN
 
 
 def test_planner_ranking_prefers_least_traffic(pkg):
@@ -116,7 +124,7 @@ def test_tn_config_table(pkg):
     for c in cfgs:
         assert c.lds_bytes <= 160 * 1024
         assert c.tile_m % 32 == 0 and c.tile_n % 32 == 0
-        assert c.threads == 256
+        assert c.threads in (256, 512)
 
 
 def test_workspace_query(pkg):
