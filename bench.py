@@ -338,15 +338,22 @@ def tune(pkg, inputs, dev, args):
     b8 = torch.randint(-128, 128, (n, k), generator=g).to(torch.int8).to(dev)
     a16 = torch.randn(m, k, generator=g).half().to(dev)
     b16 = torch.randn(n, k, generator=g).half().to(dev)
-    for cfg in pkg.tn_configs():
+    b16n = torch.randn(k, n, generator=g).half().to(dev)
+    w8 = torch.randint(-128, 128, (k, n), generator=g).to(torch.int8).to(dev)
+    s8 = (torch.rand(n, generator=g) * 0.019 + 0.001).half().to(dev)
+    for cfg in pkg.mfma_configs():
+        sc = None
         if cfg.a_elem == pkg.ELEM_I8:
             a, b = a8, b8
             c = torch.empty(m, n, dtype=torch.int32, device=dev)
         else:
-            a, b = a16, b16
+            a = a16
+            b = {pkg.B_FORM_TN: b16, pkg.B_FORM_NN: b16n,
+                 pkg.B_FORM_W8A16: w8}[cfg.b_form]
+            sc = s8 if cfg.b_form == pkg.B_FORM_W8A16 else None
             c = torch.empty(m, n, dtype=torch.float32 if cfg.c_elem == pkg.ELEM_F32
                             else torch.float16, device=dev)
-        ms = timed(lambda: pkg.matmul_tn_config(cfg.index, a, b, c),
+        ms = timed(lambda: pkg.matmul_mfma_config(cfg.index, a, b, c, scale=sc),
                    args.steps, args.warmup)
         tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
         peak = PEAK_I8_TOPS if cfg.a_elem == pkg.ELEM_I8 else PEAK_F16_TFLOPS

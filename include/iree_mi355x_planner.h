@@ -35,7 +35,7 @@ typedef enum iree_mi355x_elem_e {
 
 typedef enum iree_mi355x_family_e {
   IREE_MI355X_FAMILY_NONE = 0,     // not a dispatch this library takes
-  IREE_MI355X_FAMILY_MFMA_TN = 1,  // LDS-DMA MFMA macro-tile kernel
+  IREE_MI355X_FAMILY_MFMA = 1,     // LDS-DMA MFMA macro-tile kernel
   IREE_MI355X_FAMILY_GENERAL = 2,  // bounds-checked MFMA kernel, any shape
   IREE_MI355X_FAMILY_GEMV = 3,     // HBM-streaming skinny kernel (M <= 4)
 } iree_mi355x_family_t;
@@ -53,7 +53,7 @@ typedef struct iree_mi355x_matmul_desc_t {
 
 typedef struct iree_mi355x_matmul_plan_t {
   int32_t family;        // iree_mi355x_family_t
-  int32_t config_index;  // MFMA_TN: index into the compiled config table
+  int32_t config_index;  // MFMA: index into the compiled config table
   char config_name[64];
   int64_t tile_m, tile_n, tile_k;  // workgroup macro-tile (the VTCM tile)
   int64_t lds_bytes;               // LDS per workgroup
@@ -81,21 +81,32 @@ int32_t iree_mi355x_classify_matmul(const iree_mi355x_matmul_desc_t *desc);
 int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *desc,
                             iree_mi355x_matmul_plan_t *plan);
 
-// The compiled MFMA_TN configurations (for the autotuner and the library
-// export table): name, macro-tile and LDS bytes of entry `index`.
-int iree_mi355x_tn_config_count(void);
-int iree_mi355x_tn_config_info(int index, const char **name, int32_t *a_elem,
-                               int32_t *c_elem, int64_t *tile_m,
-                               int64_t *tile_n, int64_t *tile_k,
-                               int64_t *lds_bytes, int32_t *threads);
+// B operand forms of the MFMA family.
+typedef enum iree_mi355x_b_form_e {
+  IREE_MI355X_B_FORM_TN = 0,     // B [N,K], element type of A
+  IREE_MI355X_B_FORM_NN = 1,     // B [K,N] f16
+  IREE_MI355X_B_FORM_W8A16 = 2,  // B [K,N] int8 + per-column f16 scale
+} iree_mi355x_b_form_t;
 
-// Launch one compiled MFMA_TN configuration by index on an eligible shape
-// (autotuner entry). Same argument meaning as iree_mi355x_matmul_f16/_i8;
-// returns IREE_MI355X_UNSUPPORTED if the shape does not tile exactly.
-int iree_mi355x_matmul_tn_config(int index, const void *a, const void *b,
-                                 void *c, int64_t m, int64_t n, int64_t k,
-                                 int64_t lda, int64_t ldb, int64_t ldc,
-                                 uint32_t flags, void *stream);
+// The compiled MFMA configurations (for the autotuner and the library export
+// table): name, operand forms, macro-tile and resources of entry `index`.
+int iree_mi355x_mfma_config_count(void);
+int iree_mi355x_mfma_config_info(int index, const char **name,
+                                 int32_t *b_form, int32_t *a_elem,
+                                 int32_t *c_elem, int64_t *tile_m,
+                                 int64_t *tile_n, int64_t *tile_k,
+                                 int64_t *lds_bytes, int32_t *threads);
+
+// Launch one compiled MFMA configuration by index on an eligible shape
+// (autotuner entry). Arguments as iree_mi355x_matmul_f16 / _i8 /
+// _w8a16_matmul (scale is read only by the W8A16 form); flags must match the
+// configuration's B form. Returns IREE_MI355X_UNSUPPORTED if the shape does
+// not tile exactly.
+int iree_mi355x_matmul_mfma_config(int index, const void *a, const void *b,
+                                   const void *scale, void *c, int64_t m,
+                                   int64_t n, int64_t k, int64_t lda,
+                                   int64_t ldb, int64_t ldc, uint32_t flags,
+                                   void *stream);
 
 #ifdef __cplusplus
 }  // extern "C"

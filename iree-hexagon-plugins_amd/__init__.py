@@ -41,8 +41,9 @@ CAUSAL = 0x1
 
 # Element kinds (iree_mi355x_elem_t) and kernel families.
 ELEM_F16, ELEM_I8, ELEM_I32, ELEM_F32 = 0, 1, 2, 3
-FAMILY_NONE, FAMILY_MFMA_TN, FAMILY_GENERAL, FAMILY_GEMV = 0, 1, 2, 3
-FAMILY_NAMES = {FAMILY_NONE: "none", FAMILY_MFMA_TN: "mfma_tn",
+FAMILY_NONE, FAMILY_MFMA, FAMILY_GENERAL, FAMILY_GEMV = 0, 1, 2, 3
+B_FORM_TN, B_FORM_NN, B_FORM_W8A16 = 0, 1, 2
+FAMILY_NAMES = {FAMILY_NONE: "none", FAMILY_MFMA: "mfma",
                 FAMILY_GENERAL: "general", FAMILY_GEMV: "gemv"}
 
 EXECUTABLE_LIBRARY_VERSION = 0x4D490001
@@ -54,8 +55,8 @@ EXPORTED_SYMBOLS = (
     "iree_mi355x_matmul_workspace_bytes", "iree_mi355x_last_error",
     "iree_mi355x_version", "iree_mi355x_device_count",
     "iree_mi355x_matmul_desc_init", "iree_mi355x_classify_matmul",
-    "iree_mi355x_plan_matmul", "iree_mi355x_tn_config_count",
-    "iree_mi355x_tn_config_info", "iree_mi355x_matmul_tn_config",
+    "iree_mi355x_plan_matmul", "iree_mi355x_mfma_config_count",
+    "iree_mi355x_mfma_config_info", "iree_mi355x_matmul_mfma_config",
     "iree_mi355x_executable_library_query",
 )
 
@@ -170,14 +171,15 @@ def library():
     lib.iree_mi355x_classify_matmul.argtypes = [ctypes.POINTER(MatmulDesc)]
     lib.iree_mi355x_plan_matmul.argtypes = [ctypes.POINTER(MatmulDesc),
                                             ctypes.POINTER(MatmulPlan)]
-    lib.iree_mi355x_tn_config_info.argtypes = [
+    lib.iree_mi355x_mfma_config_info.argtypes = [
         ctypes.c_int, ctypes.POINTER(ctypes.c_char_p),
+        ctypes.POINTER(ctypes.c_int32),
         ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
         ctypes.POINTER(i64), ctypes.POINTER(i64), ctypes.POINTER(i64),
         ctypes.POINTER(i64), ctypes.POINTER(ctypes.c_int32)]
-    lib.iree_mi355x_matmul_tn_config.argtypes = [ctypes.c_int, p, p, p, i64,
-                                                 i64, i64, i64, i64, i64, u32,
-                                                 p]
+    lib.iree_mi355x_matmul_mfma_config.argtypes = [ctypes.c_int, p, p, p, p,
+                                                   i64, i64, i64, i64, i64,
+                                                   i64, u32, p]
     lib.iree_mi355x_executable_library_query.restype = ctypes.c_void_p
     lib.iree_mi355x_executable_library_query.argtypes = [u32, p]
     _lib = lib
@@ -219,9 +221,10 @@ def plan(desc: MatmulDesc) -> MatmulPlan:
 
 
 @dataclass
-class TnConfig:
+class MfmaConfig:
     index: int
     name: str
+    b_form: int
     a_elem: int
     c_elem: int
     tile_m: int
@@ -231,19 +234,20 @@ class TnConfig:
     threads: int
 
 
-def tn_configs() -> list[TnConfig]:
+def mfma_configs() -> list[MfmaConfig]:
     lib = library()
     out = []
-    for i in range(lib.iree_mi355x_tn_config_count()):
+    for i in range(lib.iree_mi355x_mfma_config_count()):
         name = ctypes.c_char_p()
-        ae, ce, th = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+        bf, ae, ce, th = (ctypes.c_int32() for _ in range(4))
         tm, tn, tk, lds = (ctypes.c_int64() for _ in range(4))
-        _check(lib.iree_mi355x_tn_config_info(
-            i, ctypes.byref(name), ctypes.byref(ae), ctypes.byref(ce),
-            ctypes.byref(tm), ctypes.byref(tn), ctypes.byref(tk),
-            ctypes.byref(lds), ctypes.byref(th)))
-        out.append(TnConfig(i, name.value.decode(), ae.value, ce.value,
-                            tm.value, tn.value, tk.value, lds.value, th.value))
+        _check(lib.iree_mi355x_mfma_config_info(
+            i, ctypes.byref(name), ctypes.byref(bf), ctypes.byref(ae),
+            ctypes.byref(ce), ctypes.byref(tm), ctypes.byref(tn),
+            ctypes.byref(tk), ctypes.byref(lds), ctypes.byref(th)))
+        out.append(MfmaConfig(i, name.value.decode(), bf.value, ae.value,
+                              ce.value, tm.value, tn.value, tk.value,
+                              lds.value, th.value))
     return out
 
 
@@ -388,15 +392,22 @@ def attention(q, k, v, o=None, *, causal=True, scale=None, stream=None):
     return o
 
 
-def matmul_tn_config(index, a, b, c, *, stream=None):
-    """Run one compiled MFMA_TN configuration (autotuner entry point)."""
-    m, k = a.shape
-    n = b.shape[0]
-    flags = B_TRANSPOSED
+def matmul_mfma_config(index, a, b, c, *, scale=None, stream=None):
+    """Run one compiled MFMA configuration (autotuner entry point).
+
+    The configuration's B form decides how `b` is read: TN takes B [N, K],
+    NN takes B [K, N] f16, W8A16 takes B [K, N] int8 plus `scale`."""
     import torch
+    cfg = mfma_configs()[index]
+    m, k = a.shape
+    if cfg.b_form == B_FORM_TN:
+        n, flags = b.shape[0], B_TRANSPOSED
+    else:
+        n, flags = b.shape[1], 0
     if c.dtype == torch.float32 and a.dtype == torch.float16:
         flags |= OUT_F32
-    _check(library().iree_mi355x_matmul_tn_config(
-        index, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, a.stride(0),
-        b.stride(0), c.stride(0), flags, _stream_ptr(stream)))
+    _check(library().iree_mi355x_matmul_mfma_config(
+        index, a.data_ptr(), b.data_ptr(),
+        scale.data_ptr() if scale is not None else None, c.data_ptr(), m, n,
+        k, a.stride(0), b.stride(0), c.stride(0), flags, _stream_ptr(stream)))
     return c

@@ -184,9 +184,9 @@ int iree_mi355x_matmul_f16(const void *a, const void *b, void *c, int64_t m,
       return launch_status(launch_gemv(args, 2, nullptr, out_f32, ws),
                            "gemv_f16");
     }
-    case IREE_MI355X_FAMILY_MFMA_TN: {
+    case IREE_MI355X_FAMILY_MFMA: {
       int count = 0;
-      const TnConfig *cfgs = tn_configs(&count);
+      const FastConfig *cfgs = fast_configs(&count);
       return launch_status(cfgs[plan.config_index].launch(args),
                            cfgs[plan.config_index].name);
     }
@@ -219,9 +219,9 @@ int iree_mi355x_matmul_i8(const int8_t *a, const int8_t *b, int32_t *c,
   iree_mi355x_matmul_plan_t plan;
   if (iree_mi355x_plan_matmul(&desc, &plan) != IREE_MI355X_OK)
     return fail(IREE_MI355X_UNSUPPORTED, "matmul_i8: no plan");
-  if (plan.family == IREE_MI355X_FAMILY_MFMA_TN) {
+  if (plan.family == IREE_MI355X_FAMILY_MFMA) {
     int count = 0;
-    const TnConfig *cfgs = tn_configs(&count);
+    const FastConfig *cfgs = fast_configs(&count);
     return launch_status(cfgs[plan.config_index].launch(args),
                          cfgs[plan.config_index].name);
   }
@@ -243,7 +243,8 @@ int iree_mi355x_w8a16_matmul(const void *x, const int8_t *w, const void *scale,
   if (!aligned(scale, 2))
     return fail(IREE_MI355X_MISALIGNED, "w8a16_matmul: scale misaligned");
   MatmulArgs args{x, w, y, m, n, k, ldx, ldw, ldy,
-                  (flags & IREE_MI355X_MATMUL_B_TRANSPOSED) ? 1 : 0, 0, stream};
+                  (flags & IREE_MI355X_MATMUL_B_TRANSPOSED) ? 1 : 0, 0, stream,
+                  scale};
   iree_mi355x_matmul_desc_t desc;
   iree_mi355x_matmul_desc_init(&desc, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_I8,
                                IREE_MI355X_ELEM_F16, m, n, k, flags);
@@ -265,6 +266,12 @@ int iree_mi355x_w8a16_matmul(const void *x, const int8_t *w, const void *scale,
         return st;
     }
     return launch_status(launch_gemv(args, 1, scale, 0, ws), "gemv_w8a16");
+  }
+  if (plan.family == IREE_MI355X_FAMILY_MFMA) {
+    int count = 0;
+    const FastConfig *cfgs = fast_configs(&count);
+    return launch_status(cfgs[plan.config_index].launch(args),
+                         cfgs[plan.config_index].name);
   }
   return launch_status(launch_general(args, kGeneralW8A16, scale),
                        "gemm_general_w8a16");

@@ -33,49 +33,123 @@ __device__ __forceinline__ void static_for(F &&f) {
 }
 
 // ----------------------------------------------------------------------------
-// Fast path: A [M,K] and B [N,K], both K-contiguous ("TN"), every extent a
-// multiple of the macro-tile, 16-byte aligned rows.
+// Fast path: A [M,K] K-contiguous, every extent a multiple of the macro-tile,
+// 16-byte aligned rows. Three B forms (BMODE):
+//   kBTN   B [N,K] of the A type (K-contiguous, "column-major B")
+//   kBNN16 B [K,N] f16 (N-contiguous, row-major weights)
+//   kBW8   B [K,N] int8 with a per-column f16 scale (W8A16), dequantized to
+//          f16 in registers after the LDS read, scale applied in the epilogue
 // ----------------------------------------------------------------------------
 
 template <int CH>
 __device__ __forceinline__ int chunk_swizzle(int row) {
-  // 16-byte chunk permutation of a staged row of CH chunks. gfx950 LDS has 64
-  // four-byte banks (a 256-byte bank line) and serves a ds_read_b128 16 lanes
-  // at a time; the 16 lanes of a fragment read 16 consecutive rows at one
-  // logical chunk. Rows sharing a bank line keep their offset within it, and
-  // the chunk index is XORed with the bank-line number, so the 16 reads hit
-  // 16 distinct 16-byte bank groups.
+  // 16-byte chunk permutation of a staged K-contiguous row of CH chunks.
+  // gfx950 LDS has 64 four-byte banks (a 256-byte bank line) and serves a
+  // ds_read_b128 16 lanes at a time; the 16 lanes of a fragment read 16
+  // consecutive rows at one logical chunk. Rows sharing a bank line keep
+  // their offset within it, and the chunk index is XORed with the bank-line
+  // number, so the 16 reads hit 16 distinct 16-byte bank groups.
   return (row / (16 / CH)) % CH;
 }
 
+// Chunk swizzle of a staged N-contiguous B row (row = k). A transposed LDS
+// read (ds_read_b64_tr_b16 / _b8) makes each 16-lane block read 4 (f16) or 8
+// (int8) consecutive k rows at one 32- or 16-byte column window; XORing the
+// chunk index with a multiple of the row index spreads the rows of two
+// neighbouring blocks over all 64 banks.
+template <int BMODE>
+__device__ __forceinline__ int nn_swizzle(int k) {
+  return BMODE == kBNN16 ? 4 * (k & 3) : 2 * (k & 7);
+}
+
+// 8 int8 weights (two dwords) -> 8 f16, exact: each byte b becomes the f16
+// with exponent 2^10 and mantissa (b ^ 0x80), i.e. 1024 + (b + 128), and
+// subtracting 1152 leaves b. Two v_perm_b32 and one packed f16 subtract per
+// four weights.
+__device__ __forceinline__ i32x4 i8x8_to_f16x8(i32x2 q) {
+  i32x4 out;
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    const unsigned y = (unsigned)q[d] ^ 0x80808080u;
+    const unsigned lo = __builtin_amdgcn_perm(0x64646464u, y, 0x05010400u);
+    const unsigned hi = __builtin_amdgcn_perm(0x64646464u, y, 0x07030602u);
+    const f16x2 bias = {(f16)1152.0f, (f16)1152.0f};
+    out[2 * d] = __builtin_bit_cast(int, __builtin_bit_cast(f16x2, lo) - bias);
+    out[2 * d + 1] =
+        __builtin_bit_cast(int, __builtin_bit_cast(f16x2, hi) - bias);
+  }
+  return out;
+}
+
+template <int OFF>
+__device__ __forceinline__ i32x2 lds_read_tr16_async(const IHP_LDS char *p) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset range");
+  i32x2 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
+               : "=v"(v)
+               : "v"((unsigned)(uintptr_t)p), "i"(OFF));
+  return v;
+}
+
+template <int OFF>
+__device__ __forceinline__ i32x2 lds_read_tr8_async(const IHP_LDS char *p) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset range");
+  i32x2 v;
+  asm volatile("ds_read_b64_tr_b8 %0, %1 offset:%2"
+               : "=v"(v)
+               : "v"((unsigned)(uintptr_t)p), "i"(OFF));
+  return v;
+}
+
+__device__ __forceinline__ void lgkm_tie2(i32x2 &v) {
+  asm volatile("" : "+v"(v));
+}
+
 template <typename T, typename OutT, int BM, int BN, int BKB, int WM, int WN,
-          int STAGES>
-__global__ __launch_bounds__(64 * WM *WN, 1) void gemm_tn_lds_kernel(
-    const T *__restrict__ A, const T *__restrict__ B, OutT *__restrict__ C,
-    int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
-    int accumulate) {
+          int STAGES, int BMODE>
+__global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
+    const T *__restrict__ A, const void *__restrict__ Bv, OutT *__restrict__ C,
+    const f16 *__restrict__ scale, int M, int N, int K, int64_t lda,
+    int64_t ldb, int64_t ldc, int accumulate) {
   typedef Mfma32<T> MF;
   typedef typename MF::Acc Acc;
+  constexpr bool kNN = BMODE != kBTN;
+  constexpr int TBB = BMODE == kBW8 ? 1 : (int)sizeof(T);  // B element bytes
   constexpr int NT = 64 * WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int FM = WTM / 32, FN = WTN / 32;
-  constexpr int CH = BKB / 16;
+  constexpr int KE = BKB / (int)sizeof(T);  // K elements per stage
+  constexpr int CH = BKB / 16;              // chunks per staged A (TN B) row
   constexpr int ROWS_PER_WAVE = 64 / CH;
   constexpr int ROWS_PER_PASS = NT / CH;
   constexpr int A_PASSES = BM / ROWS_PER_PASS;
-  constexpr int B_PASSES = BN / ROWS_PER_PASS;
+  // B staging: TN rows are N (BKB bytes each); NN rows are K (BN*TBB bytes).
+  constexpr int BROW = kNN ? BN * TBB : BKB;
+  constexpr int BCH = BROW / 16;
+  constexpr int B_ROWS = kNN ? KE : BN;
+  constexpr int B_RPW = 64 / BCH;    // B rows per wave copy instruction
+  constexpr int B_RPP = NT / BCH;    // B rows per block-wide pass
+  constexpr int B_PASSES = B_ROWS / B_RPP;
   constexpr int LOADS_PER_STAGE = A_PASSES + B_PASSES;
   constexpr int A_BYTES = BM * BKB;
-  constexpr int STAGE_BYTES = (BM + BN) * BKB;
+  constexpr int STAGE_BYTES = A_BYTES + B_ROWS * BROW;
   constexpr int KSTEPS = BKB / 32;
-  static_assert(BM % ROWS_PER_PASS == 0 && BN % ROWS_PER_PASS == 0, "tile");
+  // LDS reads per K step: FM A fragments, FN B fragments (two transposed
+  // reads each for f16 NN).
+  constexpr int B_READS = BMODE == kBNN16 ? 2 * FN : FN;
+  constexpr int RD = FM + B_READS;
+  static_assert(BM % ROWS_PER_PASS == 0 && B_ROWS % B_RPP == 0, "tile");
+  static_assert(B_RPP * BCH == NT && B_RPW * BCH == 64, "B copy shape");
   static_assert(FM >= 1 && FN >= 1 && (CH == 4 || CH == 8), "tile");
-  // The swizzle repeats every 16 rows. Block-wide copy passes start on that
-  // period, so a lane's swizzle depends only on its row within the pass.
-  static_assert(ROWS_PER_PASS % 16 == 0 && (16 / CH) * CH == 16, "swz");
   static_assert(KSTEPS % 2 == 0, "fragment double buffer parity");
+  // The A swizzle repeats every 16 rows; block-wide copy passes start on
+  // that period, so a lane's swizzle depends only on its row in the pass.
+  static_assert(ROWS_PER_PASS % 16 == 0 && (16 / CH) * CH == 16, "swz");
+  static_assert(!kNN || (BCH >= 16 && B_RPP % 8 == 0 && B_RPW <= 8), "nn");
   static_assert(STAGES >= 2 && (STAGES - 2) * LOADS_PER_STAGE < 64,
                 "vmcnt range");
+  static_assert(RD < 16, "lgkmcnt range");
+  static_assert(STAGES * STAGE_BYTES <= 160 * 1024, "LDS budget");
 
   __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE_BYTES];
 
@@ -94,32 +168,52 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_tn_lds_kernel(
   const int ld_chunk =
       (lane % CH) ^ chunk_swizzle<CH>(wave * ROWS_PER_WAVE + ld_row);
   const int64_t lda_b = lda * (int64_t)sizeof(T);
-  const int64_t ldb_b = ldb * (int64_t)sizeof(T);
+  const int64_t ldb_b = ldb * (int64_t)TBB;
   const uint32_t a_lane =
       (uint32_t)((wave * ROWS_PER_WAVE + ld_row) * lda_b + ld_chunk * 16);
-  const uint32_t b_lane =
-      (uint32_t)((wave * ROWS_PER_WAVE + ld_row) * ldb_b + ld_chunk * 16);
   const char *a_base = (const char *)A + m0 * lda_b;
-  const char *b_base = (const char *)B + n0 * ldb_b;
+  uint32_t b_lane;
+  const char *b_base;
+  if constexpr (kNN) {
+    const int krow = wave * B_RPW + lane / BCH;
+    const int chunk = (lane % BCH) ^ nn_swizzle<BMODE>(krow);
+    b_lane = (uint32_t)(krow * ldb_b + chunk * 16);
+    b_base = (const char *)Bv + n0 * TBB;
+  } else {
+    b_lane = (uint32_t)((wave * ROWS_PER_WAVE + ld_row) * ldb_b +
+                        ld_chunk * 16);
+    b_base = (const char *)Bv + n0 * ldb_b;
+  }
   IHP_LDS char *lds = (IHP_LDS char *)smem;
 
   auto load_stage = [&](int kt, int slot) {
-    const int64_t kb = (int64_t)kt * BKB;
-    IHP_LDS char *dst = lds + slot * STAGE_BYTES + wave * ROWS_PER_WAVE * BKB;
+    IHP_LDS char *dst = lds + slot * STAGE_BYTES;
+    const int64_t ka = (int64_t)kt * BKB;
 #pragma unroll
     for (int p = 0; p < A_PASSES; ++p)
-      global_to_lds_16(a_base + kb + (int64_t)p * ROWS_PER_PASS * lda_b +
+      global_to_lds_16(a_base + ka + (int64_t)p * ROWS_PER_PASS * lda_b +
                            a_lane,
-                       dst + p * ROWS_PER_PASS * BKB);
+                       dst + wave * ROWS_PER_WAVE * BKB +
+                           p * ROWS_PER_PASS * BKB);
+    if constexpr (kNN) {
+      const int64_t kb = (int64_t)kt * KE * ldb_b;
 #pragma unroll
-    for (int p = 0; p < B_PASSES; ++p)
-      global_to_lds_16(b_base + kb + (int64_t)p * ROWS_PER_PASS * ldb_b +
-                           b_lane,
-                       dst + A_BYTES + p * ROWS_PER_PASS * BKB);
+      for (int p = 0; p < B_PASSES; ++p)
+        global_to_lds_16(b_base + kb + (int64_t)p * B_RPP * ldb_b + b_lane,
+                         dst + A_BYTES + wave * B_RPW * BROW +
+                             p * B_RPP * BROW);
+    } else {
+#pragma unroll
+      for (int p = 0; p < B_PASSES; ++p)
+        global_to_lds_16(b_base + ka + (int64_t)p * ROWS_PER_PASS * ldb_b +
+                             b_lane,
+                         dst + A_BYTES + wave * ROWS_PER_WAVE * BKB +
+                             p * ROWS_PER_PASS * BKB);
+    }
   };
 
-  // Read side: lane reads row (lane % 32) of each 32-row fragment, logical
-  // chunk 2*ks + lane/32 of the staged row.
+  // Read side, A (and TN B): lane reads row (lane % 32) of each 32-row
+  // fragment, logical chunk 2*ks + lane/32 of the staged row.
   const int rd_row = lane & 31;
   const int rd_sw = chunk_swizzle<CH>(rd_row) ^ (lane >> 5);
   int koff[KSTEPS];
@@ -128,27 +222,88 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_tn_lds_kernel(
     koff[ks] = ((2 * ks) ^ rd_sw) * 16;
   const int a_rd = (wm * WTM + rd_row) * BKB;
   const int b_rd = A_BYTES + (wn * WTN + rd_row) * BKB;
+  // Read side, NN B: per-lane byte offset of fragment j within a stage for
+  // K step 0 (a K step adds 16 rows; the swizzle repeats every 4 or 8).
+  int b_nn[FN];
+  if constexpr (kNN) {
+    const int blk = lane >> 4, jj = lane & 15;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      if constexpr (BMODE == kBNN16) {
+        // block reads k rows 8*(blk/2) + jj/4 (+4), columns 16*(blk%2) +
+        // 4*(jj%4) .. +3 of the fragment
+        const int k = 8 * (blk >> 1) + (jj >> 2);
+        const int byte = 2 * (wn * WTN + j * 32 + 16 * (blk & 1) + 4 * (jj & 3));
+        b_nn[j] = A_BYTES + k * BROW +
+                  (((byte >> 4) ^ nn_swizzle<BMODE>(k)) << 4) + (byte & 15);
+      } else {
+        // block reads k rows 8*(blk/2) + jj/2, columns 16*(blk%2) +
+        // 8*(jj%2) .. +7 of the fragment (bytes)
+        const int k = 8 * (blk >> 1) + (jj >> 1);
+        const int byte = wn * WTN + j * 32 + 16 * (blk & 1) + 8 * (jj & 1);
+        b_nn[j] = A_BYTES + k * BROW +
+                  (((byte >> 4) ^ nn_swizzle<BMODE>(k)) << 4) + (byte & 15);
+      }
+    }
+  }
 
-  // Issue the FM + FN fragment reads of (slot, ks); they complete in order.
-  auto read_frags = [&](int slot, int ks, i32x4 *af, i32x4 *bf) {
-    const IHP_LDS char *pa = lds + slot * STAGE_BYTES + a_rd + koff[ks];
-    const IHP_LDS char *pb = lds + slot * STAGE_BYTES + b_rd + koff[ks];
-    static_for<FM>([&](auto i) {
-      af[i] = lds_read_16_async<decltype(i)::value * 32 * BKB>(pa);
-    });
-    static_for<FN>([&](auto j) {
-      bf[j] = lds_read_16_async<decltype(j)::value * 32 * BKB>(pb);
-    });
+  // Raw fragment registers: A (and TN B) 16 bytes; NN B two or one 8-byte
+  // transposed reads.
+  struct Frags {
+    i32x4 a[FM];
+    i32x4 b[FN];
+    i32x2 t[BMODE == kBNN16 ? 2 * FN : FN];
   };
-  // Wait until at most N reads are outstanding, then pin the fragments.
-  auto frags_ready = [&](auto n, i32x4 *af, i32x4 *bf) {
+  auto read_frags = [&](int slot, int ks, Frags &f) {
+    const IHP_LDS char *st = lds + slot * STAGE_BYTES;
+    const IHP_LDS char *pa = st + a_rd + koff[ks];
+    static_for<FM>([&](auto i) {
+      f.a[i] = lds_read_16_async<decltype(i)::value * 32 * BKB>(pa);
+    });
+    if constexpr (BMODE == kBTN) {
+      const IHP_LDS char *pb = st + b_rd + koff[ks];
+      static_for<FN>([&](auto j) {
+        f.b[j] = lds_read_16_async<decltype(j)::value * 32 * BKB>(pb);
+      });
+    } else {
+      const IHP_LDS char *pb = st + ks * 16 * BROW;
+      static_for<FN>([&](auto j) {
+        constexpr int J = decltype(j)::value;
+        if constexpr (BMODE == kBNN16) {
+          f.t[2 * J] = lds_read_tr16_async<0>(pb + b_nn[J]);
+          f.t[2 * J + 1] = lds_read_tr16_async<4 * BROW>(pb + b_nn[J]);
+        } else {
+          f.t[J] = lds_read_tr8_async<0>(pb + b_nn[J]);
+        }
+      });
+    }
+  };
+  // Wait until at most N reads are outstanding, pin the fragments, and
+  // assemble NN B operands from the transposed reads.
+  auto frags_ready = [&](auto n, Frags &f) {
     lgkm_wait<decltype(n)::value>();
 #pragma unroll
     for (int i = 0; i < FM; ++i)
-      lgkm_tie(af[i]);
+      lgkm_tie(f.a[i]);
+    if constexpr (BMODE == kBTN) {
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
-      lgkm_tie(bf[j]);
+      for (int j = 0; j < FN; ++j)
+        lgkm_tie(f.b[j]);
+    } else if constexpr (BMODE == kBNN16) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        lgkm_tie2(f.t[2 * j]);
+        lgkm_tie2(f.t[2 * j + 1]);
+        f.b[j] = i32x4{f.t[2 * j][0], f.t[2 * j][1], f.t[2 * j + 1][0],
+                       f.t[2 * j + 1][1]};
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        lgkm_tie2(f.t[j]);
+        f.b[j] = i8x8_to_f16x8(f.t[j]);
+      }
+    }
   };
 
   Acc acc[FM][FN];
@@ -172,8 +327,8 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_tn_lds_kernel(
     wait_vmcnt<0>();
   block_barrier();
 
-  i32x4 af[2][FM], bf[2][FN];
-  read_frags(0, 0, af[0], bf[0]);
+  Frags fr[2];
+  read_frags(0, 0, fr[0]);
 
   // Per K step: issue the next step's fragment reads, wait only for this
   // step's (issued one step earlier), then this step's MFMAs, which run
@@ -184,14 +339,14 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_tn_lds_kernel(
     for (int ks = 0; ks < KSTEPS; ++ks) {
       const int cur = ks & 1, nxt = cur ^ 1;
       if (ks + 1 < KSTEPS) {
-        read_frags(slot, ks + 1, af[nxt], bf[nxt]);
-        frags_ready(std::integral_constant<int, FM + FN>(), af[cur], bf[cur]);
+        read_frags(slot, ks + 1, fr[nxt]);
+        frags_ready(std::integral_constant<int, RD>(), fr[cur]);
       } else if (kt + 1 < nk) {
         // Stage handoff: this step's fragments are in registers (all LDS
         // reads done), stage kt+1 must have landed for every wave, and every
         // wave must be done reading stage kt before its slot is refilled
         // with stage kt+STAGES.
-        frags_ready(std::integral_constant<int, 0>(), af[cur], bf[cur]);
+        frags_ready(std::integral_constant<int, 0>(), fr[cur]);
         if (kt + STAGES - 1 < nk)
           wait_vmcnt<(STAGES - 2) * LOADS_PER_STAGE>();
         else
@@ -199,19 +354,20 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_tn_lds_kernel(
         block_barrier();
         if (kt + STAGES < nk)
           load_stage(kt + STAGES, slot);
-        read_frags((kt + 1) % STAGES, 0, af[nxt], bf[nxt]);
+        read_frags((kt + 1) % STAGES, 0, fr[nxt]);
       } else {
-        frags_ready(std::integral_constant<int, 0>(), af[cur], bf[cur]);
+        frags_ready(std::integral_constant<int, 0>(), fr[cur]);
       }
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          acc[i][j] = MF::mma(af[cur][i], bf[cur][j], acc[i][j]);
+          acc[i][j] = MF::mma(fr[cur].a[i], fr[cur].b[j], acc[i][j]);
     }
   }
 
-  // Epilogue: C_out = [C_init +] acc, one rounding for f16 outputs.
+  // Epilogue: C_out = [C_init +] acc (W8A16: acc * scale[n]), one rounding
+  // for f16 outputs.
   const int col_l = lane & 31;
   const int row_l = 4 * (lane >> 5);
 #pragma unroll
@@ -220,10 +376,18 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_tn_lds_kernel(
                  col_l;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
+      float sc = 1.0f;
+      if constexpr (BMODE == kBW8)
+        sc = (float)scale[n0 + wn * WTN + j * 32 + col_l];
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        store_out(crow + (8 * (r >> 2) + (r & 3)) * ldc + j * 32,
-                  acc[i][j][r], accumulate);
+      for (int r = 0; r < 16; ++r) {
+        if constexpr (BMODE == kBW8)
+          store_out(crow + (8 * (r >> 2) + (r & 3)) * ldc + j * 32,
+                    (float)acc[i][j][r] * sc, 0);
+        else
+          store_out(crow + (8 * (r >> 2) + (r & 3)) * ldc + j * 32,
+                    acc[i][j][r], accumulate);
+      }
     }
   }
 }
@@ -322,50 +486,63 @@ __global__ __launch_bounds__(256) void gemm_general_kernel(
 // ----------------------------------------------------------------------------
 
 template <typename T, typename OutT, int BM, int BN, int BKB, int WM, int WN,
-          int STAGES>
-static hipError_t launch_tn(const MatmulArgs &a) {
+          int STAGES, int BMODE>
+static hipError_t launch_fast(const MatmulArgs &a) {
   const int tiles = (int)((a.m / BM) * (a.n / BN));
   hipLaunchKernelGGL(
-      (gemm_tn_lds_kernel<T, OutT, BM, BN, BKB, WM, WN, STAGES>), dim3(tiles),
-      dim3(64 * WM * WN), 0, (hipStream_t)a.stream, (const T *)a.a,
-      (const T *)a.b, (OutT *)a.c, (int)a.m, (int)a.n, (int)a.k, a.lda, a.ldb,
-      a.ldc, a.accumulate);
+      (gemm_lds_kernel<T, OutT, BM, BN, BKB, WM, WN, STAGES, BMODE>),
+      dim3(tiles), dim3(64 * WM * WN), 0, (hipStream_t)a.stream,
+      (const T *)a.a, a.b, (OutT *)a.c, (const f16 *)a.scale, (int)a.m,
+      (int)a.n, (int)a.k, a.lda, a.ldb, a.ldc, a.accumulate);
   return hipGetLastError();
 }
 
-#define IHP_TN_CONFIG(NAME, T, OUT, BM, BN, BKB, WM, WN, ST)                   \
-  {NAME, sizeof(T) == 1 ? kElemI8 : kElemF16, sizeof(OUT) == 4, BM, BN,       \
-   BKB / (int)sizeof(T), 64 * WM * WN, ST, (BM + BN) * BKB * ST,              \
-   &launch_tn<T, OUT, BM, BN, BKB, WM, WN, ST>}
+#define IHP_FAST_CONFIG(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST)           \
+  {NAME,                                                                      \
+   MODE,                                                                      \
+   sizeof(T) == 1 ? kElemI8 : kElemF16,                                       \
+   sizeof(OUT) == 4 && sizeof(T) == 2,                                        \
+   BM,                                                                        \
+   BN,                                                                        \
+   BKB / (int)sizeof(T),                                                      \
+   64 * WM * WN,                                                              \
+   ST,                                                                        \
+   ST * (BM * BKB + (MODE == kBTN ? BN * BKB                                  \
+                                  : (BKB / (int)sizeof(T)) * BN *             \
+                                        (MODE == kBW8 ? 1 : (int)sizeof(T)))),\
+   &launch_fast<T, OUT, BM, BN, BKB, WM, WN, ST, MODE>}
 
 // Every compiled fast-path configuration. The planner picks among these by
-// name or by its LDS-budget ranking; the autotuner times them.
-// Names: <types>_tn_<BM>x<BN>x<BK in elements>_w<wave grid>_s<LDS stages>.
-static const TnConfig kTnConfigs[] = {
-    IHP_TN_CONFIG("i8_tn_256x256x128_w2x4_s2", int8_t, int32_t, 256, 256, 128, 2, 4, 2),
-    IHP_TN_CONFIG("i8_tn_256x256x64_w2x4_s4", int8_t, int32_t, 256, 256, 64, 2, 4, 4),
-    IHP_TN_CONFIG("i8_tn_256x256x64_w4x2_s5", int8_t, int32_t, 256, 256, 64, 4, 2, 5),
-    IHP_TN_CONFIG("i8_tn_256x256x128_w2x2_s2", int8_t, int32_t, 256, 256, 128, 2, 2, 2),
-    IHP_TN_CONFIG("i8_tn_256x256x64_w2x2_s5", int8_t, int32_t, 256, 256, 64, 2, 2, 5),
-    IHP_TN_CONFIG("i8_tn_256x128x128_w2x4_s2", int8_t, int32_t, 256, 128, 128, 2, 4, 2),
-    IHP_TN_CONFIG("i8_tn_256x128x64_w2x2_s5", int8_t, int32_t, 256, 128, 64, 2, 2, 5),
-    IHP_TN_CONFIG("i8_tn_128x128x128_w2x2_s4", int8_t, int32_t, 128, 128, 128, 2, 2, 4),
-    IHP_TN_CONFIG("f16_tn_256x256x64_w2x4_s2", f16, f16, 256, 256, 128, 2, 4, 2),
-    IHP_TN_CONFIG("f16_tn_256x256x32_w2x4_s4", f16, f16, 256, 256, 64, 2, 4, 4),
-    IHP_TN_CONFIG("f16_tn_256x256x32_w4x2_s5", f16, f16, 256, 256, 64, 4, 2, 5),
-    IHP_TN_CONFIG("f16_tn_256x256x64_w2x2_s2", f16, f16, 256, 256, 128, 2, 2, 2),
-    IHP_TN_CONFIG("f16_tn_256x256x32_w2x2_s5", f16, f16, 256, 256, 64, 2, 2, 5),
-    IHP_TN_CONFIG("f16_tn_256x128x64_w2x4_s2", f16, f16, 256, 128, 128, 2, 4, 2),
-    IHP_TN_CONFIG("f16_tn_256x128x32_w2x2_s5", f16, f16, 256, 128, 64, 2, 2, 5),
-    IHP_TN_CONFIG("f16_tn_128x128x64_w2x2_s4", f16, f16, 128, 128, 128, 2, 2, 4),
-    IHP_TN_CONFIG("f16f32_tn_256x256x64_w2x4_s2", f16, float, 256, 256, 128, 2, 4, 2),
-    IHP_TN_CONFIG("f16f32_tn_256x256x32_w2x4_s4", f16, float, 256, 256, 64, 2, 4, 4),
-    IHP_TN_CONFIG("f16f32_tn_128x128x64_w2x2_s4", f16, float, 128, 128, 128, 2, 2, 4),
+// its LDS-budget ranking or a measured table entry; bench.py --tune times
+// them. Names: <types>_<b form>_<BM>x<BN>x<BK in elements>_w<wave grid>_s<LDS
+// stages>.
+static const FastConfig kFastConfigs[] = {
+    IHP_FAST_CONFIG("i8_tn_256x256x128_w2x2_s2", kBTN, int8_t, int32_t, 256, 256, 128, 2, 2, 2),
+    IHP_FAST_CONFIG("i8_tn_256x256x128_w2x4_s2", kBTN, int8_t, int32_t, 256, 256, 128, 2, 4, 2),
+    IHP_FAST_CONFIG("i8_tn_256x256x64_w2x4_s4", kBTN, int8_t, int32_t, 256, 256, 64, 2, 4, 4),
+    IHP_FAST_CONFIG("i8_tn_256x128x128_w2x4_s2", kBTN, int8_t, int32_t, 256, 128, 128, 2, 4, 2),
+    IHP_FAST_CONFIG("i8_tn_128x128x128_w2x2_s4", kBTN, int8_t, int32_t, 128, 128, 128, 2, 2, 4),
+    IHP_FAST_CONFIG("f16_tn_256x256x64_w2x4_s2", kBTN, f16, f16, 256, 256, 128, 2, 4, 2),
+    IHP_FAST_CONFIG("f16_tn_256x256x64_w2x2_s2", kBTN, f16, f16, 256, 256, 128, 2, 2, 2),
+    IHP_FAST_CONFIG("f16_tn_256x256x32_w2x4_s4", kBTN, f16, f16, 256, 256, 64, 2, 4, 4),
+    IHP_FAST_CONFIG("f16_tn_256x128x64_w2x4_s2", kBTN, f16, f16, 256, 128, 128, 2, 4, 2),
+    IHP_FAST_CONFIG("f16_tn_128x128x64_w2x2_s4", kBTN, f16, f16, 128, 128, 128, 2, 2, 4),
+    IHP_FAST_CONFIG("f16f32_tn_256x256x64_w2x4_s2", kBTN, f16, float, 256, 256, 128, 2, 4, 2),
+    IHP_FAST_CONFIG("f16f32_tn_128x128x64_w2x2_s4", kBTN, f16, float, 128, 128, 128, 2, 2, 4),
+    IHP_FAST_CONFIG("f16_nn_256x256x64_w2x4_s2", kBNN16, f16, f16, 256, 256, 128, 2, 4, 2),
+    IHP_FAST_CONFIG("f16_nn_256x256x64_w2x2_s2", kBNN16, f16, f16, 256, 256, 128, 2, 2, 2),
+    IHP_FAST_CONFIG("f16_nn_256x128x64_w2x4_s2", kBNN16, f16, f16, 256, 128, 128, 2, 4, 2),
+    IHP_FAST_CONFIG("f16_nn_128x128x64_w2x2_s4", kBNN16, f16, f16, 128, 128, 128, 2, 2, 4),
+    IHP_FAST_CONFIG("f16f32_nn_256x256x64_w2x4_s2", kBNN16, f16, float, 256, 256, 128, 2, 4, 2),
+    IHP_FAST_CONFIG("f16f32_nn_128x128x64_w2x2_s4", kBNN16, f16, float, 128, 128, 128, 2, 2, 4),
+    IHP_FAST_CONFIG("w8a16_nn_256x256x64_w2x4_s3", kBW8, f16, f16, 256, 256, 128, 2, 4, 3),
+    IHP_FAST_CONFIG("w8a16_nn_128x256x64_w2x4_s4", kBW8, f16, f16, 128, 256, 128, 2, 4, 4),
+    IHP_FAST_CONFIG("w8a16_nn_128x256x64_w2x2_s4", kBW8, f16, f16, 128, 256, 128, 2, 2, 4),
 };
 
-const TnConfig *tn_configs(int *count) {
-  *count = (int)(sizeof(kTnConfigs) / sizeof(kTnConfigs[0]));
-  return kTnConfigs;
+const FastConfig *fast_configs(int *count) {
+  *count = (int)(sizeof(kFastConfigs) / sizeof(kFastConfigs[0]));
+  return kFastConfigs;
 }
 
 template <typename TA, typename TB, typename OutT, bool kScale>

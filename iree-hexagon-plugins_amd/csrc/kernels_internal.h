@@ -11,6 +11,13 @@ namespace ihp {
 
 enum ElemKind { kElemF16 = 0, kElemI8 = 1 };
 
+// B operand forms of the fast (LDS-DMA MFMA) kernel.
+enum BMode {
+  kBTN = 0,    // B [N,K], same type as A
+  kBNN16 = 1,  // B [K,N] f16
+  kBW8 = 2,    // B [K,N] int8 with per-column f16 scale (W8A16)
+};
+
 // One matmul launch: C[M,N] = [C +] A[M,K] . B (B [K,N] or [N,K]).
 struct MatmulArgs {
   const void *a;
@@ -21,24 +28,26 @@ struct MatmulArgs {
   int b_transposed;
   int accumulate;
   void *stream;
+  const void *scale;  // W8A16 per-column scale (else NULL)
 };
 
-typedef hipError_t (*TnLaunchFn)(const MatmulArgs &);
+typedef hipError_t (*FastLaunchFn)(const MatmulArgs &);
 
-// A compiled fast-path (TN, LDS-DMA) GEMM configuration.
-struct TnConfig {
+// A compiled fast-path (LDS-DMA MFMA) GEMM configuration.
+struct FastConfig {
   const char *name;
-  int elem;      // ElemKind of A and B
+  int b_mode;    // BMode
+  int elem;      // ElemKind of A (and of B unless kBW8)
   int out_f32;   // f16 path: f32 output (i8 path: always i32)
   int bm, bn;    // macro-tile
   int bk;        // K elements per LDS stage
   int threads;   // workgroup size
   int stages;    // LDS ring depth
   int lds_bytes; // static LDS per workgroup
-  TnLaunchFn launch;
+  FastLaunchFn launch;
 };
 
-const TnConfig *tn_configs(int *count);
+const FastConfig *fast_configs(int *count);
 
 enum GeneralKind {
   kGeneralF16F16 = 0,

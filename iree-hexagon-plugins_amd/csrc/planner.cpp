@@ -80,17 +80,35 @@ bool gemv_eligible(const iree_mi355x_matmul_desc_t &d) {
   return true;
 }
 
-// TN (both operands K-contiguous) candidates that tile the shape exactly.
-bool tn_fits(const iree_mi355x_matmul_desc_t &d, const TnConfig &c) {
-  if (!(d.flags & IREE_MI355X_MATMUL_B_TRANSPOSED) || !d.a_aligned16 ||
-      !d.b_aligned16 || d.has_scale)
+// The B form a dispatch needs, or -1 if no fast kernel computes it.
+int wanted_b_mode(const iree_mi355x_matmul_desc_t &d) {
+  const bool bt = d.flags & IREE_MI355X_MATMUL_B_TRANSPOSED;
+  if (d.has_scale)
+    return (!bt && d.a_elem == IREE_MI355X_ELEM_F16 &&
+            d.b_elem == IREE_MI355X_ELEM_I8 &&
+            d.c_elem == IREE_MI355X_ELEM_F16 &&
+            !(d.flags & IREE_MI355X_MATMUL_ACCUMULATE))
+               ? kBW8
+               : -1;
+  if (d.a_elem != d.b_elem)
+    return -1;
+  if (bt)
+    return kBTN;
+  return d.a_elem == IREE_MI355X_ELEM_F16 ? kBNN16 : -1;
+}
+
+// Fast-kernel candidates that tile the shape exactly.
+bool fast_fits(const iree_mi355x_matmul_desc_t &d, const FastConfig &c) {
+  if (!d.a_aligned16 || !d.b_aligned16 || d.k <= 0)
+    return false;
+  if (c.b_mode != wanted_b_mode(d))
     return false;
   const int want_elem = d.a_elem == IREE_MI355X_ELEM_I8 ? kElemI8 : kElemF16;
-  if (c.elem != want_elem || d.a_elem != d.b_elem)
+  if (c.elem != want_elem)
     return false;
   if (want_elem == kElemF16 && c.out_f32 != (d.c_elem == IREE_MI355X_ELEM_F32))
     return false;
-  return d.m % c.bm == 0 && d.n % c.bn == 0 && d.k % c.bk == 0 && d.k > 0;
+  return d.m % c.bm == 0 && d.n % c.bn == 0 && d.k % c.bk == 0;
 }
 
 }  // namespace
@@ -124,10 +142,10 @@ int32_t iree_mi355x_classify_matmul(const iree_mi355x_matmul_desc_t *d) {
   if (gemv_eligible(*d))
     return IREE_MI355X_FAMILY_GEMV;
   int count = 0;
-  const TnConfig *cfgs = tn_configs(&count);
+  const FastConfig *cfgs = fast_configs(&count);
   for (int i = 0; i < count; ++i)
-    if (tn_fits(*d, cfgs[i]) && cfgs[i].lds_bytes <= d->lds_budget_bytes)
-      return IREE_MI355X_FAMILY_MFMA_TN;
+    if (fast_fits(*d, cfgs[i]) && cfgs[i].lds_bytes <= d->lds_budget_bytes)
+      return IREE_MI355X_FAMILY_MFMA;
   return IREE_MI355X_FAMILY_GENERAL;
 }
 
@@ -161,9 +179,9 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
     return IREE_MI355X_OK;
   }
 
-  if (family == IREE_MI355X_FAMILY_MFMA_TN) {
+  if (family == IREE_MI355X_FAMILY_MFMA) {
     int count = 0;
-    const TnConfig *cfgs = tn_configs(&count);
+    const FastConfig *cfgs = fast_configs(&count);
     int best = -1;
     // A measured entry wins when it fits.
     for (const TunedEntry &t : kTuned) {
@@ -171,7 +189,7 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
           t.n != d->n || t.k != d->k || t.flags != d->flags)
         continue;
       for (int i = 0; i < count; ++i)
-        if (strcmp(cfgs[i].name, t.config) == 0 && tn_fits(*d, cfgs[i]) &&
+        if (strcmp(cfgs[i].name, t.config) == 0 && fast_fits(*d, cfgs[i]) &&
             cfgs[i].lds_bytes <= budget) {
           best = i;
           plan->from_tuned_table = 1;
@@ -179,16 +197,16 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
     }
     // Otherwise rank: (over budget, per-CU critical work, traffic, tiles, -N).
     std::tuple<int, int64_t, int64_t, int64_t, int64_t> best_rank;
-    const int64_t eb = elem_bytes(d->a_elem);
+    const int64_t ab = elem_bytes(d->a_elem), bb = elem_bytes(d->b_elem);
     if (best < 0) {
       for (int i = 0; i < count; ++i) {
-        const TnConfig &c = cfgs[i];
-        if (!tn_fits(*d, c) || c.lds_bytes > budget)
+        const FastConfig &c = cfgs[i];
+        if (!fast_fits(*d, c) || c.lds_bytes > budget)
           continue;
         const int64_t tiles = (d->m / c.bm) * (d->n / c.bn);
         const int64_t critical = ((tiles + cus - 1) / cus) * c.bm * c.bn;
-        const int64_t traffic =
-            eb * (d->m * d->k * (d->n / c.bn) + d->n * d->k * (d->m / c.bm));
+        const int64_t traffic = ab * d->m * d->k * (d->n / c.bn) +
+                                bb * d->n * d->k * (d->m / c.bm);
         auto rank = std::make_tuple(0, critical, traffic, tiles,
                                     -(int64_t)c.bn);
         if (best < 0 || rank < best_rank) {
@@ -199,7 +217,7 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
     }
     if (best < 0)
       return IREE_MI355X_UNSUPPORTED;
-    const TnConfig &c = cfgs[best];
+    const FastConfig &c = cfgs[best];
     plan->config_index = best;
     snprintf(plan->config_name, sizeof(plan->config_name), "%s", c.name);
     plan->tile_m = c.bm;
@@ -208,8 +226,8 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
     plan->lds_bytes = c.lds_bytes;
     plan->workgroups = (d->m / c.bm) * (d->n / c.bn);
     plan->threads = c.threads;
-    plan->traffic_bytes =
-        eb * (d->m * d->k * (d->n / c.bn) + d->n * d->k * (d->m / c.bm));
+    plan->traffic_bytes = ab * d->m * d->k * (d->n / c.bn) +
+                          bb * d->n * d->k * (d->m / c.bm);
     return IREE_MI355X_OK;
   }
 
@@ -230,23 +248,26 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
   return IREE_MI355X_OK;
 }
 
-int iree_mi355x_tn_config_count(void) {
+int iree_mi355x_mfma_config_count(void) {
   int count = 0;
-  tn_configs(&count);
+  fast_configs(&count);
   return count;
 }
 
-int iree_mi355x_tn_config_info(int index, const char **name, int32_t *a_elem,
-                               int32_t *c_elem, int64_t *tile_m,
-                               int64_t *tile_n, int64_t *tile_k,
-                               int64_t *lds_bytes, int32_t *threads) {
+int iree_mi355x_mfma_config_info(int index, const char **name,
+                                 int32_t *b_form, int32_t *a_elem,
+                                 int32_t *c_elem, int64_t *tile_m,
+                                 int64_t *tile_n, int64_t *tile_k,
+                                 int64_t *lds_bytes, int32_t *threads) {
   int count = 0;
-  const TnConfig *cfgs = tn_configs(&count);
+  const FastConfig *cfgs = fast_configs(&count);
   if (index < 0 || index >= count)
     return IREE_MI355X_INVALID_ARGUMENT;
-  const TnConfig &c = cfgs[index];
+  const FastConfig &c = cfgs[index];
   if (name)
     *name = c.name;
+  if (b_form)
+    *b_form = c.b_mode;
   if (a_elem)
     *a_elem = c.elem == kElemI8 ? IREE_MI355X_ELEM_I8 : IREE_MI355X_ELEM_F16;
   if (c_elem)
@@ -266,38 +287,45 @@ int iree_mi355x_tn_config_info(int index, const char **name, int32_t *a_elem,
   return IREE_MI355X_OK;
 }
 
-int iree_mi355x_matmul_tn_config(int index, const void *a, const void *b,
-                                 void *c, int64_t m, int64_t n, int64_t k,
-                                 int64_t lda, int64_t ldb, int64_t ldc,
-                                 uint32_t flags, void *stream) {
+int iree_mi355x_matmul_mfma_config(int index, const void *a, const void *b,
+                                   const void *scale, void *c, int64_t m,
+                                   int64_t n, int64_t k, int64_t lda,
+                                   int64_t ldb, int64_t ldc, uint32_t flags,
+                                   void *stream) {
   int count = 0;
-  const TnConfig *cfgs = tn_configs(&count);
+  const FastConfig *cfgs = fast_configs(&count);
   if (index < 0 || index >= count)
-    return fail(IREE_MI355X_INVALID_ARGUMENT, "tn_config: bad index %d", index);
-  const TnConfig &cfg = cfgs[index];
-  iree_mi355x_matmul_desc_t d;
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "mfma_config: bad index %d",
+                index);
+  const FastConfig &cfg = cfgs[index];
   const int32_t ae = cfg.elem == kElemI8 ? IREE_MI355X_ELEM_I8
                                          : IREE_MI355X_ELEM_F16;
+  const int32_t be = cfg.b_mode == kBW8 ? IREE_MI355X_ELEM_I8 : ae;
   const int32_t ce = cfg.elem == kElemI8
                          ? IREE_MI355X_ELEM_I32
                          : (cfg.out_f32 ? IREE_MI355X_ELEM_F32
                                         : IREE_MI355X_ELEM_F16);
-  iree_mi355x_matmul_desc_init(&d, ae, ae, ce, m, n, k, flags);
-  const int64_t eb = elem_bytes(ae);
-  d.a_aligned16 = a && ((uintptr_t)a % 16 == 0) && (lda * eb) % 16 == 0;
-  d.b_aligned16 = b && ((uintptr_t)b % 16 == 0) && (ldb * eb) % 16 == 0;
+  iree_mi355x_matmul_desc_t d;
+  iree_mi355x_matmul_desc_init(&d, ae, be, ce, m, n, k, flags);
+  d.has_scale = cfg.b_mode == kBW8;
+  const int64_t aeb = elem_bytes(ae), beb = elem_bytes(be);
+  d.a_aligned16 = a && ((uintptr_t)a % 16 == 0) && (lda * aeb) % 16 == 0;
+  d.b_aligned16 = b && ((uintptr_t)b % 16 == 0) && (ldb * beb) % 16 == 0;
+  const bool bt = flags & IREE_MI355X_MATMUL_B_TRANSPOSED;
   if (flags & ~(IREE_MI355X_MATMUL_B_TRANSPOSED | IREE_MI355X_MATMUL_ACCUMULATE |
                 IREE_MI355X_MATMUL_OUT_F32))
-    return fail(IREE_MI355X_INVALID_ARGUMENT, "tn_config: unknown flags");
-  if (!c || (uintptr_t)c % elem_bytes(ce) != 0 || lda < k || ldb < k ||
-      ldc < n || m >= ((int64_t)1 << 31) || n >= ((int64_t)1 << 31) ||
-      k >= ((int64_t)1 << 31))
-    return fail(IREE_MI355X_INVALID_ARGUMENT, "tn_config: bad arguments");
-  if (!tn_fits(d, cfg))
-    return fail(IREE_MI355X_UNSUPPORTED, "tn_config %s: shape does not tile",
-                cfg.name);
-  MatmulArgs args{a, b, c, m, n, k, lda, ldb, ldc, 1,
-                  (flags & IREE_MI355X_MATMUL_ACCUMULATE) ? 1 : 0, stream};
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "mfma_config: unknown flags");
+  if (!c || (uintptr_t)c % elem_bytes(ce) != 0 || lda < k ||
+      ldb < (bt ? k : n) || ldc < n || m >= ((int64_t)1 << 31) ||
+      n >= ((int64_t)1 << 31) || k >= ((int64_t)1 << 31) ||
+      (d.has_scale && (!scale || (uintptr_t)scale % 2 != 0)))
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "mfma_config: bad arguments");
+  if (!fast_fits(d, cfg))
+    return fail(IREE_MI355X_UNSUPPORTED,
+                "mfma_config %s: shape or layout does not fit", cfg.name);
+  MatmulArgs args{a, b, c, m, n, k, lda, ldb, ldc, bt ? 1 : 0,
+                  (flags & IREE_MI355X_MATMUL_ACCUMULATE) ? 1 : 0, stream,
+                  scale};
   hipError_t e = cfg.launch(args);
   if (e != hipSuccess)
     return fail(IREE_MI355X_LAUNCH_FAILED, "%s: %s", cfg.name,

@@ -60,7 +60,9 @@ F16, I8, I32, F32 = 0, 1, 2, 3
     ((F16, F16, F16, 4096, 4096, 4096, 1), 1, (256, 256)),
     ((F16, F16, F32, 4096, 4096, 4096, 1), 1, (256, 256)),
     ((F16, F16, F16, 2048, 4096, 4096, 1), 1, (256, 128)),
-    ((F16, F16, F16, 128, 512, 256, 0), 2, (64, 64)),
+    ((F16, F16, F16, 128, 512, 256, 0), 1, (128, 128)),
+    ((F16, F16, F16, 2048, 4096, 4096, 0), 1, (256, 128)),
+    ((F16, F16, F16, 100, 512, 256, 0), 2, (64, 64)),
     ((F16, F16, F16, 17, 19, 23, 1), 2, (64, 64)),
     ((F16, F16, F16, 1, 4096, 4096, 0), 3, (1, 256)),
     ((F16, F16, F16, 4, 11008, 4096, 0), 3, (4, 256)),
@@ -75,12 +77,13 @@ def test_planner_classification(pkg, case, family, tile):
     assert p.family == family
     assert (p.tile_m, p.tile_n) == tile
     name = p.config_name.decode()
-    prefix = {1: ("i8_tn_" if a == I8 else ("f16f32_tn_" if c == F32 else "f16_tn_")),
+    form = "tn" if flags & 1 else "nn"
+    prefix = {1: ("i8_" if a == I8 else ("f16f32_" if c == F32 else "f16_")) + form + "_",
               2: "general_", 3: "gemv_"}[family]
     assert name.startswith(prefix), name
     if family == 1:
         # the chosen config really has this macro-tile and fits the LDS budget
-        cfg = [x for x in pkg.tn_configs() if x.name == name][0]
+        cfg = [x for x in pkg.mfma_configs() if x.name == name][0]
         assert (cfg.tile_m, cfg.tile_n) == tile and cfg.lds_bytes <= 160 * 1024
 
 
@@ -90,6 +93,10 @@ def test_planner_w8a16_and_unsupported_types(pkg):
     assert p.family == pkg.FAMILY_GEMV and p.tile_n == 512
     assert p.workspace_bytes > 0 and p.splits > 1
     d = pkg.make_desc(F16, I8, F16, 512, 11008, 4096, 0, has_scale=True)
+    p = pkg.plan(d)
+    assert p.family == pkg.FAMILY_MFMA and p.config_name.startswith(b"w8a16_nn_")
+    d = pkg.make_desc(F16, I8, F16, 512, 11008, 4096, pkg.B_TRANSPOSED,
+                      has_scale=True)
     assert pkg.classify(d) == pkg.FAMILY_GENERAL
     for bad in ((F32, F32, F32), (I8, F16, F16), (F16, F16, I32), (I8, I8, F16)):
         d = pkg.make_desc(*bad, 64, 64, 64, 0)
@@ -106,7 +113,7 @@ def test_planner_lds_budget_and_alignment(pkg):
     assert pkg.classify(d) == pkg.FAMILY_GENERAL
     d = pkg.make_desc(I8, I8, I32, 4096, 4096, 4096, 1, lds_budget_bytes=130 * 1024)
     p = pkg.plan(d)
-    assert p.lds_bytes <= 130 * 1024 and p.family == pkg.FAMILY_MFMA_TN
+    assert p.lds_bytes <= 130 * 1024 and p.family == pkg.FAMILY_MFMA
 
 
 def test_planner_ranking_prefers_least_traffic(pkg):
@@ -118,8 +125,8 @@ def test_planner_ranking_prefers_least_traffic(pkg):
     assert p.workgroups == 256
 
 
-def test_tn_config_table(pkg):
-    cfgs = pkg.tn_configs()
+def test_mfma_config_table(pkg):
+    cfgs = pkg.mfma_configs()
     assert len(cfgs) >= 8
     for c in cfgs:
         assert c.lds_bytes <= 160 * 1024

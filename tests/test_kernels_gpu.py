@@ -82,16 +82,63 @@ def test_matmul_f16_tn_configs(pkg, oracle, dev, shape):
     ref32 = oracle.matmul_f16(a.numpy(), bt.numpy(), b_transposed=True,
                               out_f32=True)
     ran = 0
-    for cfg in pkg.tn_configs():
-        if cfg.a_elem != pkg.ELEM_F16:
+    for cfg in pkg.mfma_configs():
+        if cfg.a_elem != pkg.ELEM_F16 or cfg.b_form != pkg.B_FORM_TN:
             continue
         if m % cfg.tile_m or n % cfg.tile_n or k % cfg.tile_k:
             continue
         out32 = cfg.c_elem == pkg.ELEM_F32
         c = torch.empty(m, n, dtype=torch.float32 if out32 else torch.float16,
                         device=dev)
-        pkg.matmul_tn_config(cfg.index, a.to(dev), bt.to(dev), c)
+        pkg.matmul_mfma_config(cfg.index, a.to(dev), bt.to(dev), c)
         fp16_ok(oracle, c.cpu().numpy(), ref32 if out32 else ref16)
+        ran += 1
+    assert ran > 0
+
+
+@pytest.mark.parametrize("shape", [(256, 256, 64), (512, 512, 256),
+                                   (256, 768, 192)])
+def test_matmul_f16_nn_configs(pkg, oracle, dev, shape):
+    m, n, k = shape
+    g = torch.Generator().manual_seed(7 * m + n + k)
+    a = torch.randn(m, k, generator=g).half()
+    b = torch.randn(k, n, generator=g).half()
+    ref16 = oracle.matmul_f16(a.numpy(), b.numpy())
+    ref32 = oracle.matmul_f16(a.numpy(), b.numpy(), out_f32=True)
+    ran = 0
+    for cfg in pkg.mfma_configs():
+        if cfg.b_form != pkg.B_FORM_NN:
+            continue
+        if m % cfg.tile_m or n % cfg.tile_n or k % cfg.tile_k:
+            continue
+        out32 = cfg.c_elem == pkg.ELEM_F32
+        c = torch.empty(m, n, dtype=torch.float32 if out32 else torch.float16,
+                        device=dev)
+        pkg.matmul_mfma_config(cfg.index, a.to(dev), b.to(dev), c)
+        fp16_ok(oracle, c.cpu().numpy(), ref32 if out32 else ref16)
+        ran += 1
+    assert ran > 0
+
+
+@pytest.mark.parametrize("shape", [(128, 256, 64), (256, 512, 256),
+                                   (128, 768, 384)])
+def test_w8a16_mfma_configs(pkg, oracle, dev, shape):
+    m, n, k = shape
+    g = torch.Generator().manual_seed(5 * m + n + k)
+    x = torch.randn(m, k, generator=g).half()
+    w = torch.randint(-128, 128, (k, n), generator=g).to(torch.int8)
+    s = (torch.rand(n, generator=g) * 0.019 + 0.001).half()
+    ref = oracle.w8a16(x.numpy(), w.numpy(), s.numpy())
+    ran = 0
+    for cfg in pkg.mfma_configs():
+        if cfg.b_form != pkg.B_FORM_W8A16:
+            continue
+        if m % cfg.tile_m or n % cfg.tile_n or k % cfg.tile_k:
+            continue
+        y = torch.empty(m, n, dtype=torch.float16, device=dev)
+        pkg.matmul_mfma_config(cfg.index, x.to(dev), w.to(dev), y,
+                               scale=s.to(dev))
+        fp16_ok(oracle, y.cpu().numpy(), ref)
         ran += 1
     assert ran > 0
 
@@ -208,13 +255,13 @@ def test_matmul_i8_tn_configs(pkg, oracle, dev, shape):
     bt = torch.randint(-128, 128, (n, k), generator=g).to(torch.int8)
     ref = oracle.matmul_i8(a.numpy(), bt.numpy(), b_transposed=True)
     ran = 0
-    for cfg in pkg.tn_configs():
+    for cfg in pkg.mfma_configs():
         if cfg.a_elem != pkg.ELEM_I8:
             continue
         if m % cfg.tile_m or n % cfg.tile_n or k % cfg.tile_k:
             continue
         c = torch.empty(m, n, dtype=torch.int32, device=dev)
-        pkg.matmul_tn_config(cfg.index, a.to(dev), bt.to(dev), c)
+        pkg.matmul_mfma_config(cfg.index, a.to(dev), bt.to(dev), c)
         assert np.array_equal(c.cpu().numpy(), ref), cfg.name
         ran += 1
     assert ran > 0
