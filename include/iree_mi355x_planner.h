@@ -59,7 +59,8 @@ typedef struct iree_mi355x_matmul_plan_t {
   int64_t lds_bytes;               // LDS per workgroup
   int64_t workgroups;
   int32_t threads;                 // threads per workgroup
-  int32_t splits;                  // GEMV K splits
+  int32_t splits;                  // K splits (GEMV, split-K MFMA)
+  int32_t k_split;                 // K elements per split (split-K MFMA)
   int64_t workspace_bytes;
   int64_t traffic_bytes;           // modeled global->LDS bytes of the plan
   int32_t from_tuned_table;        // 1 if a measured entry chose it

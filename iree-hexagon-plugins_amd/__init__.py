@@ -83,6 +83,7 @@ class MatmulPlan(ctypes.Structure):
                 ("tile_n", ctypes.c_int64), ("tile_k", ctypes.c_int64),
                 ("lds_bytes", ctypes.c_int64), ("workgroups", ctypes.c_int64),
                 ("threads", ctypes.c_int32), ("splits", ctypes.c_int32),
+                ("k_split", ctypes.c_int32),
                 ("workspace_bytes", ctypes.c_int64),
                 ("traffic_bytes", ctypes.c_int64),
                 ("from_tuned_table", ctypes.c_int32)]

@@ -51,7 +51,7 @@ struct DeviceWorkspace {
 static std::mutex g_ws_mutex;
 static std::vector<DeviceWorkspace> g_ws;
 
-static int library_workspace(size_t need, void **out) {
+int library_workspace(size_t need, void **out) {
   *out = nullptr;
   if (need == 0)
     return IREE_MI355X_OK;
@@ -86,6 +86,32 @@ static int launch_status(hipError_t e, const char *what) {
   if (e != hipSuccess)
     return fail(IREE_MI355X_LAUNCH_FAILED, "%s: %s", what, hipGetErrorString(e));
   return ok();
+}
+
+// Launch the planned MFMA configuration, with its split-K workspace (the
+// caller's if given and large enough, else the library's).
+static int launch_mfma(MatmulArgs &args, const iree_mi355x_matmul_plan_t &plan,
+                       void *workspace, size_t workspace_bytes,
+                       const char *who) {
+  int count = 0;
+  const FastConfig *cfgs = fast_configs(&count);
+  args.splits = plan.splits > 1 ? plan.splits : 1;
+  args.k_split = plan.k_split;
+  args.workspace = nullptr;
+  if (plan.workspace_bytes > 0) {
+    if (workspace && workspace_bytes < (size_t)plan.workspace_bytes)
+      return fail(IREE_MI355X_WORKSPACE_TOO_SMALL, "%s: workspace %zu < %lld",
+                  who, workspace_bytes, (long long)plan.workspace_bytes);
+    args.workspace = workspace;
+    if (!args.workspace) {
+      const int st = library_workspace((size_t)plan.workspace_bytes,
+                                       &args.workspace);
+      if (st != IREE_MI355X_OK)
+        return st;
+    }
+  }
+  return launch_status(cfgs[plan.config_index].launch(args),
+                       cfgs[plan.config_index].name);
 }
 
 // Shared shape / stride checks for the three matmul entry points.
@@ -135,12 +161,28 @@ int iree_mi355x_device_count(void) {
 
 size_t iree_mi355x_matmul_workspace_bytes(int64_t m, int64_t n, int64_t k,
                                           uint32_t flags) {
-  if (m <= 0 || n <= 0 || k <= 0 || m > kGemvMaxRows ||
-      (flags & IREE_MI355X_MATMUL_B_TRANSPOSED))
+  if (m <= 0 || n <= 0 || k <= 0)
     return 0;
-  size_t f16b = gemv_workspace_bytes(m, n, k, 2);
-  size_t i8b = gemv_workspace_bytes(m, n, k, 1);
-  return f16b > i8b ? f16b : i8b;
+  // The largest workspace any f16 or W8A16 plan of this shape uses (plans
+  // assume 16-byte aligned operands, the case that can pick split-K).
+  size_t most = 0;
+  const int32_t forms[3][3] = {
+      {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16},
+      {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F32},
+      {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_F16}};
+  for (int f = 0; f < 3; ++f) {
+    iree_mi355x_matmul_desc_t d;
+    iree_mi355x_matmul_desc_init(&d, forms[f][0], forms[f][1], forms[f][2], m,
+                                 n, k, flags & ~IREE_MI355X_MATMUL_OUT_F32);
+    d.has_scale = f == 2;
+    if (f == 1)
+      d.flags |= IREE_MI355X_MATMUL_OUT_F32;
+    iree_mi355x_matmul_plan_t p;
+    if (iree_mi355x_plan_matmul(&d, &p) == IREE_MI355X_OK &&
+        (size_t)p.workspace_bytes > most)
+      most = (size_t)p.workspace_bytes;
+  }
+  return most;
 }
 
 int iree_mi355x_matmul_f16(const void *a, const void *b, void *c, int64_t m,
@@ -184,12 +226,8 @@ int iree_mi355x_matmul_f16(const void *a, const void *b, void *c, int64_t m,
       return launch_status(launch_gemv(args, 2, nullptr, out_f32, ws),
                            "gemv_f16");
     }
-    case IREE_MI355X_FAMILY_MFMA: {
-      int count = 0;
-      const FastConfig *cfgs = fast_configs(&count);
-      return launch_status(cfgs[plan.config_index].launch(args),
-                           cfgs[plan.config_index].name);
-    }
+    case IREE_MI355X_FAMILY_MFMA:
+      return launch_mfma(args, plan, workspace, workspace_bytes, "matmul_f16");
     default:
       return launch_status(
           launch_general(args, out_f32 ? kGeneralF16F32 : kGeneralF16F16,
@@ -219,12 +257,8 @@ int iree_mi355x_matmul_i8(const int8_t *a, const int8_t *b, int32_t *c,
   iree_mi355x_matmul_plan_t plan;
   if (iree_mi355x_plan_matmul(&desc, &plan) != IREE_MI355X_OK)
     return fail(IREE_MI355X_UNSUPPORTED, "matmul_i8: no plan");
-  if (plan.family == IREE_MI355X_FAMILY_MFMA) {
-    int count = 0;
-    const FastConfig *cfgs = fast_configs(&count);
-    return launch_status(cfgs[plan.config_index].launch(args),
-                         cfgs[plan.config_index].name);
-  }
+  if (plan.family == IREE_MI355X_FAMILY_MFMA)
+    return launch_mfma(args, plan, nullptr, 0, "matmul_i8");
   return launch_status(launch_general(args, kGeneralI8I32, nullptr),
                        "gemm_general_i8");
 }
@@ -267,12 +301,8 @@ int iree_mi355x_w8a16_matmul(const void *x, const int8_t *w, const void *scale,
     }
     return launch_status(launch_gemv(args, 1, scale, 0, ws), "gemv_w8a16");
   }
-  if (plan.family == IREE_MI355X_FAMILY_MFMA) {
-    int count = 0;
-    const FastConfig *cfgs = fast_configs(&count);
-    return launch_status(cfgs[plan.config_index].launch(args),
-                         cfgs[plan.config_index].name);
-  }
+  if (plan.family == IREE_MI355X_FAMILY_MFMA)
+    return launch_mfma(args, plan, workspace, workspace_bytes, "w8a16_matmul");
   return launch_status(launch_general(args, kGeneralW8A16, scale),
                        "gemm_general_w8a16");
 }

@@ -136,6 +136,61 @@ __device__ __forceinline__ void lgkm_tie(i32x4 &v) {
   asm volatile("" : "+v"(v));
 }
 
+// Device-scope (sc1) 32-bit store / load for data one workgroup publishes and
+// another, possibly on another XCD, reads within the same kernel: the store
+// is written through past this XCD's L2 and the load bypasses it. They are
+// the instructions the compiler emits for agent-scope relaxed atomics, issued
+// as asm so they are not each followed by a wait: callers drain stores with
+// wait_vmcnt<0>() and collect loads with partial_sum().
+__device__ __forceinline__ void store_device(float *p, float v) {
+  asm volatile("global_store_dword %0, %1, off sc1" ::"v"(p), "v"(v)
+               : "memory");
+}
+__device__ __forceinline__ void store_device(int *p, int v) {
+  asm volatile("global_store_dword %0, %1, off sc1" ::"v"(p), "v"(v)
+               : "memory");
+}
+template <typename P>
+__device__ __forceinline__ P load_device(const P *p) {
+  static_assert(sizeof(P) == 4, "32-bit");
+  P v;
+  asm volatile("global_load_dword %0, %1, off sc1" : "=v"(v) : "v"(p)
+               : "memory");
+  return v;
+}
+template <typename P>
+__device__ __forceinline__ void vm_tie(P &v) {
+  asm volatile("" : "+v"(v));
+}
+
+// sum_{s < splits} base[s * stride], added in s order, with up to 8 loads in
+// flight per wait.
+template <typename P>
+__device__ __forceinline__ P partial_sum(const P *base, int64_t stride,
+                                         int splits) {
+  P sum = 0;
+  int s = 0;
+  for (; s + 8 <= splits; s += 8) {
+    P v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      v[u] = load_device(base + (int64_t)(s + u) * stride);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      vm_tie(v[u]);
+      sum += v[u];
+    }
+  }
+  for (; s < splits; ++s) {
+    P v = load_device(base + (int64_t)s * stride);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    vm_tie(v);
+    sum += v;
+  }
+  return sum;
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own
 // L2). Renumber them so that consecutive logical tile ids share an XCD, then
 // walk tiles in GROUP_M-row bands so an XCD's tiles reuse the same A row

@@ -105,12 +105,19 @@ __device__ __forceinline__ void lgkm_tie2(i32x2 &v) {
   asm volatile("" : "+v"(v));
 }
 
+// SPLIT: the K extent is split over gridDim.y (k_split elements each); every
+// workgroup publishes an f32 (i32) partial tile and the last one to arrive at
+// a tile sums the partials in split order and writes C. M need not be a
+// multiple of BM: A rows past M are clamped to row M-1 on the copy side (rows
+// of C depend only on their own row of A) and never stored.
 template <typename T, typename OutT, int BM, int BN, int BKB, int WM, int WN,
-          int STAGES, int BMODE>
+          int STAGES, int BMODE, bool SPLIT>
 __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     const T *__restrict__ A, const void *__restrict__ Bv, OutT *__restrict__ C,
     const f16 *__restrict__ scale, int M, int N, int K, int64_t lda,
-    int64_t ldb, int64_t ldc, int accumulate) {
+    int64_t ldb, int64_t ldc, int accumulate, int k_split,
+    typename Mfma32<T>::AccScalar *__restrict__ partials,
+    unsigned *__restrict__ counters) {
   typedef Mfma32<T> MF;
   typedef typename MF::Acc Acc;
   constexpr bool kNN = BMODE != kBTN;
@@ -157,9 +164,14 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
+  const int tiles_m = SPLIT ? (M + BM - 1) / BM : M / BM;
   int tm, tn;
-  xcd_tile_order(blockIdx.x, gridDim.x, M / BM, N / BN, 4, &tm, &tn);
+  xcd_tile_order(blockIdx.x, gridDim.x, tiles_m, N / BN, 4, &tm, &tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  // This workgroup's K range (the whole K unless split).
+  const int64_t k_begin = SPLIT ? (int64_t)blockIdx.y * k_split : 0;
+  const int64_t k_len = SPLIT ? (K - k_begin < k_split ? K - k_begin : k_split)
+                              : K;
 
   // Copy side: lane -> (row in the wave's slab, physical chunk); the global
   // chunk it fetches is the logical chunk that belongs in that slot. The
@@ -169,20 +181,28 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
       (lane % CH) ^ chunk_swizzle<CH>(wave * ROWS_PER_WAVE + ld_row);
   const int64_t lda_b = lda * (int64_t)sizeof(T);
   const int64_t ldb_b = ldb * (int64_t)TBB;
-  const uint32_t a_lane =
-      (uint32_t)((wave * ROWS_PER_WAVE + ld_row) * lda_b + ld_chunk * 16);
-  const char *a_base = (const char *)A + m0 * lda_b;
+  // A row of each copy pass, clamped to the last row of A (split mode).
+  uint32_t a_lane[A_PASSES];
+#pragma unroll
+  for (int p = 0; p < A_PASSES; ++p) {
+    int64_t row = m0 + p * ROWS_PER_PASS + wave * ROWS_PER_WAVE + ld_row;
+    if (SPLIT && row > M - 1)
+      row = M - 1;
+    a_lane[p] = (uint32_t)((row - m0) * lda_b + ld_chunk * 16);
+  }
+  const char *a_base =
+      (const char *)A + m0 * lda_b + k_begin * (int64_t)sizeof(T);
   uint32_t b_lane;
   const char *b_base;
   if constexpr (kNN) {
     const int krow = wave * B_RPW + lane / BCH;
     const int chunk = (lane % BCH) ^ nn_swizzle<BMODE>(krow);
     b_lane = (uint32_t)(krow * ldb_b + chunk * 16);
-    b_base = (const char *)Bv + n0 * TBB;
+    b_base = (const char *)Bv + n0 * TBB + k_begin * ldb_b;
   } else {
     b_lane = (uint32_t)((wave * ROWS_PER_WAVE + ld_row) * ldb_b +
                         ld_chunk * 16);
-    b_base = (const char *)Bv + n0 * ldb_b;
+    b_base = (const char *)Bv + n0 * ldb_b + k_begin * (int64_t)sizeof(T);
   }
   IHP_LDS char *lds = (IHP_LDS char *)smem;
 
@@ -191,8 +211,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     const int64_t ka = (int64_t)kt * BKB;
 #pragma unroll
     for (int p = 0; p < A_PASSES; ++p)
-      global_to_lds_16(a_base + ka + (int64_t)p * ROWS_PER_PASS * lda_b +
-                           a_lane,
+      global_to_lds_16(a_base + ka + a_lane[p],
                        dst + wave * ROWS_PER_WAVE * BKB +
                            p * ROWS_PER_PASS * BKB);
     if constexpr (kNN) {
@@ -315,7 +334,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
       for (int r = 0; r < 16; ++r)
         acc[i][j][r] = 0;
 
-  const int nk = (int)(((int64_t)K * sizeof(T)) / BKB);
+  const int nk = (int)((k_len * (int64_t)sizeof(T)) / BKB);
   // Prologue: fill every slot of the ring, wait for stage 0.
 #pragma unroll
   for (int s = 0; s < STAGES; ++s)
@@ -370,25 +389,77 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   // for f16 outputs.
   const int col_l = lane & 31;
   const int row_l = 4 * (lane >> 5);
+  if constexpr (!SPLIT) {
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    OutT *crow = C + (m0 + wm * WTM + i * 32 + row_l) * ldc + n0 + wn * WTN +
-                 col_l;
+    for (int i = 0; i < FM; ++i) {
+      OutT *crow = C + (m0 + wm * WTM + i * 32 + row_l) * ldc + n0 +
+                   wn * WTN + col_l;
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      float sc = 1.0f;
-      if constexpr (BMODE == kBW8)
-        sc = (float)scale[n0 + wn * WTN + j * 32 + col_l];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
+      for (int j = 0; j < FN; ++j) {
+        float sc = 1.0f;
         if constexpr (BMODE == kBW8)
-          store_out(crow + (8 * (r >> 2) + (r & 3)) * ldc + j * 32,
-                    (float)acc[i][j][r] * sc, 0);
-        else
-          store_out(crow + (8 * (r >> 2) + (r & 3)) * ldc + j * 32,
-                    acc[i][j][r], accumulate);
+          sc = (float)scale[n0 + wn * WTN + j * 32 + col_l];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          if constexpr (BMODE == kBW8)
+            store_out(crow + (8 * (r >> 2) + (r & 3)) * ldc + j * 32,
+                      (float)acc[i][j][r] * sc, 0);
+          else
+            store_out(crow + (8 * (r >> 2) + (r & 3)) * ldc + j * 32,
+                      acc[i][j][r], accumulate);
+        }
       }
     }
+  } else {
+    typedef typename MF::AccScalar P;
+    // Publish this split's partial tile (rows < M only) with device-scope
+    // stores; the last workgroup of the tile reads them with device-scope
+    // loads. Only partials and the counter are shared, so no L2 write-back /
+    // invalidate fence is needed, only the stores drained before arriving.
+    P *part = partials + (int64_t)blockIdx.y * M * N;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int64_t col = n0 + wn * WTN + j * 32 + col_l;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row =
+              m0 + wm * WTM + i * 32 + row_l + 8 * (r >> 2) + (r & 3);
+          if (row < M)
+            store_device(part + row * N + col, (P)acc[i][j][r]);
+        }
+      }
+    }
+    // The LDS ring is idle once every wave passed the barrier below; its
+    // first word carries the arrival result to the workgroup.
+    unsigned *last_split = (unsigned *)smem;
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (tid == 0) {
+      const unsigned prev =
+          __hip_atomic_fetch_add(&counters[blockIdx.x], 1u, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+      *last_split = prev == gridDim.y - 1;
+    }
+    __syncthreads();
+    if (!*last_split)
+      return;
+    const int splits = (int)gridDim.y;
+    for (int idx = tid; idx < BM * BN; idx += NT) {
+      const int64_t row = m0 + idx / BN, col = n0 + idx % BN;
+      if (row >= M)
+        continue;
+      const P sum =
+          partial_sum(partials + row * N + col, (int64_t)M * N, splits);
+      if constexpr (BMODE == kBW8)
+        store_out(C + row * ldc + col, (float)sum * (float)scale[col], 0);
+      else
+        store_out(C + row * ldc + col, sum, accumulate);
+    }
+    if (tid == 0)  // re-arm for the next call on this workspace
+      __hip_atomic_store(&counters[blockIdx.x], 0u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -486,20 +557,32 @@ __global__ __launch_bounds__(256) void gemm_general_kernel(
 // ----------------------------------------------------------------------------
 
 template <typename T, typename OutT, int BM, int BN, int BKB, int WM, int WN,
-          int STAGES, int BMODE>
+          int STAGES, int BMODE, bool SPLIT>
 static hipError_t launch_fast(const MatmulArgs &a) {
-  const int tiles = (int)((a.m / BM) * (a.n / BN));
+  typedef typename Mfma32<T>::AccScalar P;
+  const int64_t tiles_m = SPLIT ? (a.m + BM - 1) / BM : a.m / BM;
+  const int tiles = (int)(tiles_m * (a.n / BN));
+  const int splits = SPLIT ? a.splits : 1;
+  const int k_split = SPLIT ? a.k_split : (int)a.k;
+  unsigned *counters = SPLIT ? (unsigned *)a.workspace : nullptr;
+  P *partials = SPLIT ? (P *)((char *)a.workspace +
+                              split_counter_bytes(tiles))
+                      : nullptr;
   hipLaunchKernelGGL(
-      (gemm_lds_kernel<T, OutT, BM, BN, BKB, WM, WN, STAGES, BMODE>),
-      dim3(tiles), dim3(64 * WM * WN), 0, (hipStream_t)a.stream,
+      (gemm_lds_kernel<T, OutT, BM, BN, BKB, WM, WN, STAGES, BMODE, SPLIT>),
+      dim3(tiles, splits), dim3(64 * WM * WN), 0, (hipStream_t)a.stream,
       (const T *)a.a, a.b, (OutT *)a.c, (const f16 *)a.scale, (int)a.m,
-      (int)a.n, (int)a.k, a.lda, a.ldb, a.ldc, a.accumulate);
+      (int)a.n, (int)a.k, a.lda, a.ldb, a.ldc, a.accumulate, k_split,
+      partials, counters);
   return hipGetLastError();
 }
 
 #define IHP_FAST_CONFIG(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST)           \
+  IHP_FAST_CONFIG_S(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, false)
+#define IHP_FAST_CONFIG_S(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, SPLIT)  \
   {NAME,                                                                      \
    MODE,                                                                      \
+   SPLIT,                                                                     \
    sizeof(T) == 1 ? kElemI8 : kElemF16,                                       \
    sizeof(OUT) == 4 && sizeof(T) == 2,                                        \
    BM,                                                                        \
@@ -510,7 +593,7 @@ static hipError_t launch_fast(const MatmulArgs &a) {
    ST * (BM * BKB + (MODE == kBTN ? BN * BKB                                  \
                                   : (BKB / (int)sizeof(T)) * BN *             \
                                         (MODE == kBW8 ? 1 : (int)sizeof(T)))),\
-   &launch_fast<T, OUT, BM, BN, BKB, WM, WN, ST, MODE>}
+   &launch_fast<T, OUT, BM, BN, BKB, WM, WN, ST, MODE, SPLIT>}
 
 // Every compiled fast-path configuration. The planner picks among these by
 // its LDS-budget ranking or a measured table entry; bench.py --tune times
@@ -538,6 +621,15 @@ static const FastConfig kFastConfigs[] = {
     IHP_FAST_CONFIG("w8a16_nn_256x256x64_w2x4_s3", kBW8, f16, f16, 256, 256, 128, 2, 4, 3),
     IHP_FAST_CONFIG("w8a16_nn_128x256x64_w2x4_s4", kBW8, f16, f16, 128, 256, 128, 2, 4, 4),
     IHP_FAST_CONFIG("w8a16_nn_128x256x64_w2x2_s4", kBW8, f16, f16, 128, 256, 128, 2, 2, 4),
+    // split-K skinny tiles (M < tile rows allowed; partials in workspace)
+    IHP_FAST_CONFIG_S("f16_nn_32x256x64_w1x4_s4_sk", kBNN16, f16, f16, 32, 256, 128, 1, 4, 4, true),
+    IHP_FAST_CONFIG_S("f16_nn_64x256x64_w1x4_s4_sk", kBNN16, f16, f16, 64, 256, 128, 1, 4, 4, true),
+    IHP_FAST_CONFIG_S("f16_nn_128x128x64_w2x2_s4_sk", kBNN16, f16, f16, 128, 128, 128, 2, 2, 4, true),
+    IHP_FAST_CONFIG_S("f16f32_nn_32x256x64_w1x4_s4_sk", kBNN16, f16, float, 32, 256, 128, 1, 4, 4, true),
+    IHP_FAST_CONFIG_S("f16_tn_32x256x64_w1x4_s4_sk", kBTN, f16, f16, 32, 256, 128, 1, 4, 4, true),
+    IHP_FAST_CONFIG_S("f16_tn_128x128x64_w2x2_s4_sk", kBTN, f16, f16, 128, 128, 128, 2, 2, 4, true),
+    IHP_FAST_CONFIG_S("w8a16_nn_32x256x64_w1x4_s4_sk", kBW8, f16, f16, 32, 256, 128, 1, 4, 4, true),
+    IHP_FAST_CONFIG_S("w8a16_nn_128x256x64_w2x4_s4_sk", kBW8, f16, f16, 128, 256, 128, 2, 4, 4, true),
 };
 
 const FastConfig *fast_configs(int *count) {

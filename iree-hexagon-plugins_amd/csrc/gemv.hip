@@ -183,10 +183,9 @@ __global__ __launch_bounds__(kThreads) void gemv_splitk_kernel(
       const float sc = scale ? (float)scale[n] : 1.0f;
       store_y(Y + r * ldy + n, s * sc, accumulate);
     } else {
-      // Agent-scope atomic store: written through past this XCD's L2, so a
-      // workgroup on another XCD reads it with an agent-scope atomic load.
-      __hip_atomic_store(&partials[((int64_t)split * MR + r) * N + n], s,
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // Device-scope store: written through past this XCD's L2, so a
+      // workgroup on another XCD reads it with a device-scope load.
+      store_device(&partials[((int64_t)split * MR + r) * N + n], s);
     }
   }
   if (direct)
@@ -194,8 +193,8 @@ __global__ __launch_bounds__(kThreads) void gemv_splitk_kernel(
 
   // Every partial store of this workgroup is acknowledged before its arrival
   // is counted: vmcnt(0) per thread, then the barrier. Only the partials and
-  // the counter are shared between workgroups, and both are accessed with
-  // agent-scope atomics, so no L2 write-back / invalidate fence is needed.
+  // the counter are shared between workgroups, and both are accessed at
+  // device scope, so no L2 write-back / invalidate fence is needed.
   wait_vmcnt<0>();
   __syncthreads();
   if (tid == 0) {
@@ -211,10 +210,8 @@ __global__ __launch_bounds__(kThreads) void gemv_splitk_kernel(
     const int64_t n = n_base + col;
     if (n >= N)
       continue;
-    float s = 0.0f;
-    for (int sp = 0; sp < splits; ++sp)
-      s += __hip_atomic_load(&partials[((int64_t)sp * MR + r) * N + n],
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float s = partial_sum(&partials[(int64_t)r * N + n],
+                                (int64_t)MR * N, splits);
     const float sc = scale ? (float)scale[n] : 1.0f;
     store_y(Y + r * ldy + n, s * sc, accumulate);
   }

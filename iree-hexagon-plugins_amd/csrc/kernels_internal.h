@@ -29,7 +29,17 @@ struct MatmulArgs {
   int accumulate;
   void *stream;
   const void *scale;  // W8A16 per-column scale (else NULL)
+  // split-K configurations: split count, K elements per split, workspace
+  // ([counters, one per tile][partials, splits x M x N accumulators])
+  int splits;
+  int k_split;
+  void *workspace;
 };
+
+// Bytes of the split-K counter block at the start of the workspace.
+inline size_t split_counter_bytes(int64_t tiles) {
+  return (size_t)((tiles * 4 + 255) / 256 * 256);
+}
 
 typedef hipError_t (*FastLaunchFn)(const MatmulArgs &);
 
@@ -37,6 +47,7 @@ typedef hipError_t (*FastLaunchFn)(const MatmulArgs &);
 struct FastConfig {
   const char *name;
   int b_mode;    // BMode
+  int split_k;   // K split over grid.y, M may be ragged (skinny shapes)
   int elem;      // ElemKind of A (and of B unless kBW8)
   int out_f32;   // f16 path: f32 output (i8 path: always i32)
   int bm, bn;    // macro-tile

@@ -14,6 +14,7 @@
 namespace ihp {
 
 int fail(int status, const char *fmt, ...);
+int library_workspace(size_t need, void **out);
 
 namespace {
 
@@ -97,9 +98,10 @@ int wanted_b_mode(const iree_mi355x_matmul_desc_t &d) {
   return d.a_elem == IREE_MI355X_ELEM_F16 ? kBNN16 : -1;
 }
 
-// Fast-kernel candidates that tile the shape exactly.
+// Fast-kernel candidates for the shape: N and K tile exactly; M tiles
+// exactly unless the configuration splits K (its A copy clamps rows to M-1).
 bool fast_fits(const iree_mi355x_matmul_desc_t &d, const FastConfig &c) {
-  if (!d.a_aligned16 || !d.b_aligned16 || d.k <= 0)
+  if (!d.a_aligned16 || !d.b_aligned16 || d.k <= 0 || d.m <= 0)
     return false;
   if (c.b_mode != wanted_b_mode(d))
     return false;
@@ -108,7 +110,99 @@ bool fast_fits(const iree_mi355x_matmul_desc_t &d, const FastConfig &c) {
     return false;
   if (want_elem == kElemF16 && c.out_f32 != (d.c_elem == IREE_MI355X_ELEM_F32))
     return false;
-  return d.m % c.bm == 0 && d.n % c.bn == 0 && d.k % c.bk == 0;
+  if (d.n % c.bn != 0 || d.k % c.bk != 0)
+    return false;
+  return c.split_k ? true : d.m % c.bm == 0;
+}
+
+// One ranked candidate: a configuration plus its K split.
+struct Candidate {
+  int index = -1;
+  int splits = 1;
+  int k_split = 0;
+  int64_t tiles = 0;
+  int64_t critical = 0;  // per-CU critical-path MACs
+  int64_t traffic = 0;   // modeled global->LDS bytes (operands + partials)
+  int64_t workspace = 0;
+  int64_t est_ns = 0;    // modeled time, the ranking key
+};
+
+// MI355X rates the cost model uses (measured on the box where noted):
+// dense MFMA per CU at 2.4 GHz; the LDS-DMA operand feed of all CUs (about
+// 16 TB/s measured with the copy-only variant of the MFMA kernel); HBM at
+// about three quarters of its 8 TB/s peak.
+constexpr double kMacsPerCuNsF16 = 2048.0 * 2.4;  // 4096 flop/clk
+constexpr double kMacsPerCuNsI8 = 4096.0 * 2.4;   // 8192 op/clk
+constexpr double kFeedBytesPerNs = 16000.0;
+constexpr double kHbmBytesPerNs = 6000.0;
+// Fixed latencies: each round of workgroups (one per CU) pays the pipeline
+// fill and the epilogue; a split-K tile also pays the partial publish, the
+// arrival count and the last arriver's reduction.
+constexpr double kRoundNs = 1500.0;
+constexpr double kSplitNs = 2000.0;
+// A split covers at least this many K stages, so its copy pipeline overlaps.
+constexpr int64_t kMinStagesPerSplit = 2;
+
+// `explicit_config`: the caller named this configuration, so a split
+// configuration runs even where one split is all the shape needs.
+bool evaluate(const iree_mi355x_matmul_desc_t &d, const FastConfig &c,
+              int index, int64_t cus, Candidate *out,
+              bool explicit_config = false) {
+  if (!fast_fits(d, c))
+    return false;
+  const int64_t tiles_m = (d.m + c.bm - 1) / c.bm;
+  const int64_t tiles = tiles_m * (d.n / c.bn);
+  int splits = 1;
+  int64_t k_split = d.k;
+  if (c.split_k) {
+    // Enough workgroups to cover every CU; each split a multiple of BK.
+    int64_t want = (cus + tiles - 1) / tiles;
+    const int64_t max_splits =
+        explicit_config ? d.k / c.bk : d.k / (kMinStagesPerSplit * c.bk);
+    if (want > max_splits)
+      want = max_splits;
+    if (want < 1)
+      want = 1;
+    k_split = ((d.k + want - 1) / want + c.bk - 1) / c.bk * c.bk;
+    splits = (int)((d.k + k_split - 1) / k_split);
+    if (splits < 2 && !explicit_config)
+      return false;  // an unsplit configuration covers this shape better
+  }
+  const int64_t ab = elem_bytes(d.a_elem), bb = elem_bytes(d.b_elem);
+  const int64_t acc_bytes = 4;
+  Candidate r;
+  r.index = index;
+  r.splits = splits;
+  r.k_split = (int)k_split;
+  r.tiles = tiles;
+  r.critical = ((tiles * splits + cus - 1) / cus) * c.bm * c.bn * k_split;
+  r.traffic = ab * d.m * d.k * (d.n / c.bn) + bb * d.n * d.k * tiles_m;
+  int64_t partial_bytes = 0;
+  if (c.split_k) {
+    r.workspace = (int64_t)split_counter_bytes(tiles) +
+                  (int64_t)splits * d.m * d.n * acc_bytes;
+    partial_bytes = 2 * (int64_t)splits * d.m * d.n * acc_bytes;
+    r.traffic += partial_bytes;
+  }
+  // time = the slowest of MFMA work on the busiest CU, the operand feed, and
+  // HBM (each operand and C once, plus split partials written and read)
+  const double macs_per_ns =
+      d.a_elem == IREE_MI355X_ELEM_I8 ? kMacsPerCuNsI8 : kMacsPerCuNsF16;
+  const double t_mfma = (double)r.critical / macs_per_ns;
+  const double t_feed = (double)r.traffic / kFeedBytesPerNs;
+  const double hbm = (double)(ab * d.m * d.k + bb * d.n * d.k +
+                              elem_bytes(d.c_elem) * d.m * d.n +
+                              partial_bytes);
+  const double t_hbm = hbm / kHbmBytesPerNs;
+  double t = t_mfma > t_feed ? t_mfma : t_feed;
+  if (t_hbm > t)
+    t = t_hbm;
+  t += (double)((tiles * splits + cus - 1) / cus) * kRoundNs;
+  if (c.split_k)
+    t += kSplitNs;
+  r.est_ns = (int64_t)t;
+  *out = r;
+  return true;
 }
 
 }  // namespace
@@ -143,9 +237,13 @@ int32_t iree_mi355x_classify_matmul(const iree_mi355x_matmul_desc_t *d) {
     return IREE_MI355X_FAMILY_GEMV;
   int count = 0;
   const FastConfig *cfgs = fast_configs(&count);
-  for (int i = 0; i < count; ++i)
-    if (fast_fits(*d, cfgs[i]) && cfgs[i].lds_bytes <= d->lds_budget_bytes)
+  const int64_t cus = d->num_cus > 0 ? d->num_cus : kDefaultCus;
+  for (int i = 0; i < count; ++i) {
+    Candidate c;
+    if (cfgs[i].lds_bytes <= d->lds_budget_bytes &&
+        evaluate(*d, cfgs[i], i, cus, &c))
       return IREE_MI355X_FAMILY_MFMA;
+  }
   return IREE_MI355X_FAMILY_GENERAL;
 }
 
@@ -182,52 +280,52 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
   if (family == IREE_MI355X_FAMILY_MFMA) {
     int count = 0;
     const FastConfig *cfgs = fast_configs(&count);
-    int best = -1;
+    Candidate best;
     // A measured entry wins when it fits.
     for (const TunedEntry &t : kTuned) {
-      if (!t.config || t.a_elem != d->a_elem || t.c_elem != d->c_elem || t.m != d->m ||
-          t.n != d->n || t.k != d->k || t.flags != d->flags)
+      if (!t.config || t.a_elem != d->a_elem || t.c_elem != d->c_elem ||
+          t.m != d->m || t.n != d->n || t.k != d->k || t.flags != d->flags)
         continue;
-      for (int i = 0; i < count; ++i)
-        if (strcmp(cfgs[i].name, t.config) == 0 && fast_fits(*d, cfgs[i]) &&
-            cfgs[i].lds_bytes <= budget) {
-          best = i;
+      for (int i = 0; i < count; ++i) {
+        Candidate c;
+        if (strcmp(cfgs[i].name, t.config) == 0 &&
+            cfgs[i].lds_bytes <= budget && evaluate(*d, cfgs[i], i, cus, &c)) {
+          best = c;
           plan->from_tuned_table = 1;
         }
+      }
     }
-    // Otherwise rank: (over budget, per-CU critical work, traffic, tiles, -N).
-    std::tuple<int, int64_t, int64_t, int64_t, int64_t> best_rank;
-    const int64_t ab = elem_bytes(d->a_elem), bb = elem_bytes(d->b_elem);
-    if (best < 0) {
+    // Otherwise rank: (modeled time, traffic, tiles, -N) over the
+    // configurations within the LDS budget.
+    if (best.index < 0) {
+      std::tuple<int64_t, int64_t, int64_t, int64_t> best_rank;
       for (int i = 0; i < count; ++i) {
-        const FastConfig &c = cfgs[i];
-        if (!fast_fits(*d, c) || c.lds_bytes > budget)
+        Candidate c;
+        if (cfgs[i].lds_bytes > budget || !evaluate(*d, cfgs[i], i, cus, &c))
           continue;
-        const int64_t tiles = (d->m / c.bm) * (d->n / c.bn);
-        const int64_t critical = ((tiles + cus - 1) / cus) * c.bm * c.bn;
-        const int64_t traffic = ab * d->m * d->k * (d->n / c.bn) +
-                                bb * d->n * d->k * (d->m / c.bm);
-        auto rank = std::make_tuple(0, critical, traffic, tiles,
-                                    -(int64_t)c.bn);
-        if (best < 0 || rank < best_rank) {
-          best = i;
+        auto rank = std::make_tuple(c.est_ns, c.traffic, c.tiles,
+                                    -(int64_t)cfgs[i].bn);
+        if (best.index < 0 || rank < best_rank) {
+          best = c;
           best_rank = rank;
         }
       }
     }
-    if (best < 0)
+    if (best.index < 0)
       return IREE_MI355X_UNSUPPORTED;
-    const FastConfig &c = cfgs[best];
-    plan->config_index = best;
+    const FastConfig &c = cfgs[best.index];
+    plan->config_index = best.index;
     snprintf(plan->config_name, sizeof(plan->config_name), "%s", c.name);
     plan->tile_m = c.bm;
     plan->tile_n = c.bn;
     plan->tile_k = c.bk;
     plan->lds_bytes = c.lds_bytes;
-    plan->workgroups = (d->m / c.bm) * (d->n / c.bn);
+    plan->workgroups = best.tiles * best.splits;
     plan->threads = c.threads;
-    plan->traffic_bytes = ab * d->m * d->k * (d->n / c.bn) +
-                          bb * d->n * d->k * (d->m / c.bm);
+    plan->splits = best.splits;
+    plan->k_split = best.k_split;
+    plan->workspace_bytes = best.workspace;
+    plan->traffic_bytes = best.traffic;
     return IREE_MI355X_OK;
   }
 
@@ -320,12 +418,19 @@ int iree_mi355x_matmul_mfma_config(int index, const void *a, const void *b,
       n >= ((int64_t)1 << 31) || k >= ((int64_t)1 << 31) ||
       (d.has_scale && (!scale || (uintptr_t)scale % 2 != 0)))
     return fail(IREE_MI355X_INVALID_ARGUMENT, "mfma_config: bad arguments");
-  if (!fast_fits(d, cfg))
+  Candidate cand;
+  if (!evaluate(d, cfg, index, kDefaultCus, &cand, true))
     return fail(IREE_MI355X_UNSUPPORTED,
                 "mfma_config %s: shape or layout does not fit", cfg.name);
+  void *ws = nullptr;
+  if (cand.workspace > 0) {
+    int st = library_workspace((size_t)cand.workspace, &ws);
+    if (st != IREE_MI355X_OK)
+      return st;
+  }
   MatmulArgs args{a, b, c, m, n, k, lda, ldb, ldc, bt ? 1 : 0,
                   (flags & IREE_MI355X_MATMUL_ACCUMULATE) ? 1 : 0, stream,
-                  scale};
+                  scale, cand.splits, cand.k_split, ws};
   hipError_t e = cfg.launch(args);
   if (e != hipSuccess)
     return fail(IREE_MI355X_LAUNCH_FAILED, "%s: %s", cfg.name,

@@ -62,11 +62,13 @@ F16, I8, I32, F32 = 0, 1, 2, 3
     ((F16, F16, F16, 2048, 4096, 4096, 1), 1, (256, 128)),
     ((F16, F16, F16, 128, 512, 256, 0), 1, (128, 128)),
     ((F16, F16, F16, 2048, 4096, 4096, 0), 1, (256, 128)),
-    ((F16, F16, F16, 100, 512, 256, 0), 2, (64, 64)),
+    ((F16, F16, F16, 100, 512, 256, 0), 1, None),
+    ((F16, F16, F16, 100, 500, 256, 0), 2, (64, 64)),
     ((F16, F16, F16, 17, 19, 23, 1), 2, (64, 64)),
     ((F16, F16, F16, 1, 4096, 4096, 0), 3, (1, 256)),
     ((F16, F16, F16, 4, 11008, 4096, 0), 3, (4, 256)),
-    ((F16, F16, F16, 5, 4096, 4096, 0), 2, (64, 64)),
+    ((F16, F16, F16, 5, 4096, 4096, 0), 1, None),
+    ((F16, F16, F16, 5, 4090, 4096, 0), 2, (64, 64)),
     ((I8, I8, I32, 1, 4096, 4096, 0), 2, (64, 64)),
 ])
 def test_planner_classification(pkg, case, family, tile):
@@ -75,7 +77,10 @@ def test_planner_classification(pkg, case, family, tile):
     assert pkg.classify(d) == family
     p = pkg.plan(d)
     assert p.family == family
-    assert (p.tile_m, p.tile_n) == tile
+    if tile is None:  # ragged M: a split-K configuration, tile by cost model
+        assert p.config_name.decode().endswith("_sk") and p.splits >= 2
+    else:
+        assert (p.tile_m, p.tile_n) == tile
     name = p.config_name.decode()
     form = "tn" if flags & 1 else "nn"
     prefix = {1: ("i8_" if a == I8 else ("f16f32_" if c == F32 else "f16_")) + form + "_",
@@ -84,7 +89,8 @@ def test_planner_classification(pkg, case, family, tile):
     if family == 1:
         # the chosen config really has this macro-tile and fits the LDS budget
         cfg = [x for x in pkg.mfma_configs() if x.name == name][0]
-        assert (cfg.tile_m, cfg.tile_n) == tile and cfg.lds_bytes <= 160 * 1024
+        assert (cfg.tile_m, cfg.tile_n) == (p.tile_m, p.tile_n)
+        assert cfg.lds_bytes <= 160 * 1024
 
 
 def test_planner_w8a16_and_unsupported_types(pkg):
@@ -136,9 +142,24 @@ def test_mfma_config_table(pkg):
 
 def test_workspace_query(pkg):
     lib = pkg.library()
+    # GEMV (M <= 4, B [K,N]) and split-K shapes use one; full tiles do not
     assert lib.iree_mi355x_matmul_workspace_bytes(1, 4096, 4096, 0) > 0
-    assert lib.iree_mi355x_matmul_workspace_bytes(1, 4096, 4096, 1) == 0
+    assert lib.iree_mi355x_matmul_workspace_bytes(16, 4096, 4096, 0) > 0
     assert lib.iree_mi355x_matmul_workspace_bytes(2048, 4096, 4096, 0) == 0
+    assert lib.iree_mi355x_matmul_workspace_bytes(4096, 4096, 4096, 1) == 0
+
+
+def test_planner_split_k_for_skinny_shapes(pkg):
+    # M = 16 cannot fill 256 CUs with output tiles: K is split and the
+    # plan carries the split count and a workspace for the partials
+    p = pkg.plan(pkg.make_desc(F16, F16, F16, 16, 4096, 4096, 0))
+    assert p.family == pkg.FAMILY_MFMA and p.splits > 1
+    assert p.config_name.endswith(b"_sk")
+    assert p.splits * p.k_split >= 4096 and p.k_split % p.tile_k == 0
+    assert p.workgroups >= 128 and p.workspace_bytes >= p.splits * 16 * 4096 * 4
+    # large M: enough tiles, no split
+    p = pkg.plan(pkg.make_desc(F16, F16, F16, 2048, 4096, 4096, 0))
+    assert p.splits == 1 and p.workspace_bytes == 0
 
 
 # Argument validation: every call below fails on the host, so no GPU is needed.

@@ -143,6 +143,52 @@ def test_w8a16_mfma_configs(pkg, oracle, dev, shape):
     assert ran > 0
 
 
+@pytest.mark.parametrize("m,n,k,form", [
+    (16, 4096, 4096, "nn"), (5, 512, 256, "nn"), (100, 512, 768, "nn"),
+    (128, 4096, 4096, "nn"), (37, 1024, 1024, "tn"), (64, 4096, 4096, "tn"),
+    (16, 11008, 4096, "w8"), (37, 1024, 2048, "w8")])
+def test_split_k_skinny(pkg, oracle, dev, m, n, k, form):
+    """Split-K MFMA plans (ragged M, partials reduced in-kernel by the last
+    workgroup of each tile); two calls in a row re-use the re-armed
+    counters of the library workspace."""
+    g = torch.Generator().manual_seed(m * 31 + n + k)
+    x = (torch.randn(m, k, generator=g) * 0.5).half()
+    if form == "w8":
+        w = torch.randint(-128, 128, (k, n), generator=g).to(torch.int8)
+        s = (torch.rand(n, generator=g) * 0.019 + 0.001).half()
+        p = pkg.plan(pkg.make_desc(0, 1, 0, m, n, k, 0, has_scale=True))
+        ref = oracle.w8a16(x.numpy(), w.numpy(), s.numpy())
+    else:
+        w = (torch.randn(n, k, generator=g) if form == "tn" else
+             torch.randn(k, n, generator=g)).half()
+        flags = pkg.B_TRANSPOSED if form == "tn" else 0
+        p = pkg.plan(pkg.make_desc(0, 0, 0, m, n, k, flags))
+        ref = oracle.matmul_f16(x.numpy(), w.numpy(), b_transposed=form == "tn")
+    assert p.family == pkg.FAMILY_MFMA and p.splits > 1, p.config_name
+    for _ in range(2):
+        buf, y = canary_out((m, n), torch.float16, dev, 5.0)
+        if form == "w8":
+            pkg.quantized_matmul(x.to(dev), w.to(dev), s.to(dev), y)
+        else:
+            pkg.matmul(x.to(dev), w.to(dev), y, b_transposed=form == "tn")
+        fp16_ok(oracle, y.cpu().numpy(), ref)
+        check_canary(buf, m, n, 5.0)
+
+
+def test_split_k_accumulate_f32(pkg, oracle, dev):
+    g = torch.Generator().manual_seed(77)
+    m, n, k = 24, 2048, 4096
+    x = torch.randn(m, k, generator=g).half()
+    w = torch.randn(k, n, generator=g).half()
+    init = torch.randn(m, n, generator=g)
+    p = pkg.plan(pkg.make_desc(0, 0, 3, m, n, k, pkg.ACCUMULATE | pkg.OUT_F32))
+    assert p.splits > 1
+    y = init.to(dev).clone()
+    pkg.matmul(x.to(dev), w.to(dev), y, accumulate=True, out_dtype=torch.float32)
+    ref = oracle.matmul_f16(x.numpy(), w.numpy(), init.numpy(), out_f32=True)
+    fp16_ok(oracle, y.cpu().numpy(), ref)
+
+
 def test_matmul_f16_accumulate(pkg, oracle, dev):
     g = torch.Generator().manual_seed(3)
     for m, n, k, bt in ((512, 512, 256, True), (100, 70, 90, False)):
