@@ -70,7 +70,8 @@ typedef enum iree_mi355x_status_e {
 //   a: [M, K] row-major, lda >= K
 //   b: [K, N] row-major (ldb >= N) or [N, K] with B_TRANSPOSED (ldb >= K)
 //   c: [M, N] row-major, ldc >= N; f16, or f32 with OUT_F32
-// M == 1..16 dispatches to the HBM-streaming GEMV kernel.
+// M <= 4 with row-major B dispatches to the HBM-streaming GEMV kernel; a
+// ragged M or a skinny M the macro-tiles leave idle splits K over the CUs.
 // Replaces iree_hexagon_hmx_pack_f16 / pack_transposed_f16 / mma_f16 /
 // acc_read_f16 / unpack_acc_f16_to_{f16,f32} (UK/api.h:28-67) as sequenced
 // by HexagonExpandHmxMatmul.cpp:286-331.

@@ -10,12 +10,14 @@
 //    (CG/Strategy/Planning/VTCMPlanning.cpp:156-329) with the 2 MiB VTCM
 //    budget (CG/Pipelines/TranslationPipeline.cpp:28-34) replaced by the
 //    160 KiB LDS of one gfx950 CU, and the candidates by the compiled MFMA
-//    macro-tiles. The ranking keeps the reference's order (in budget, least
-//    global traffic, fewest tiles, larger N) with one key added first: the
-//    per-CU critical-path work ceil(tiles / CUs) * BM * BN, since 256 CUs run
-//    the tiles in parallel where the DSP ran them in sequence
-//    (RT/dsp/command_buffer.c:670-719). A measured table (autotuner) is
-//    consulted before the ranking.
+//    macro-tiles. The ranking keeps the reference's tie-breaks (in budget,
+//    least global traffic, fewest tiles, larger N) behind one key added
+//    first: a modeled time, the slowest of MFMA work on the busiest CU, the
+//    LDS-DMA operand feed and HBM traffic, plus fixed latencies per round of
+//    workgroups and per K split, since 256 CUs run the tiles in parallel
+//    where the DSP ran them in sequence (RT/dsp/command_buffer.c:670-719).
+//    Split-K candidates divide K so that the tiles times splits cover the
+//    CUs. A measured table (autotuner) is consulted before the ranking.
 #ifndef IREE_MI355X_PLANNER_H_
 #define IREE_MI355X_PLANNER_H_
 

@@ -209,6 +209,25 @@ def test_matmul_f16_accumulate(pkg, oracle, dev):
         fp16_ok(oracle, c16.cpu().numpy(), ref16)
 
 
+# The shapes of the reference's micro/hmx models (IT/models/micro/hmx/*):
+# ragged-large, skinny, tall, wide, deep-K and the rhs-transposed square.
+@pytest.mark.parametrize("m,n,k,bt", [(1537, 1539, 257, False),
+                                      (1, 1024, 1024, False),
+                                      (4096, 32, 256, False),
+                                      (32, 4096, 256, False),
+                                      (32, 32, 4096, False),
+                                      (1024, 1024, 1024, True)])
+def test_matmul_f16_reference_micro_shapes(pkg, oracle, dev, m, n, k, bt):
+    g = torch.Generator().manual_seed(m * 7 + n * 3 + k)
+    a = (torch.rand(m, k, generator=g) * 2 - 1).half()
+    b = (torch.rand(*((n, k) if bt else (k, n)), generator=g) * 2 - 1).half()
+    buf, c = canary_out((m, n), torch.float16, dev, 3.0)
+    pkg.matmul(a.to(dev), b.to(dev), c, b_transposed=bt)
+    check_canary(buf, m, n, 3.0)
+    ref = oracle.matmul_f16(a.numpy(), b.numpy(), b_transposed=bt)
+    fp16_ok(oracle, c.cpu().numpy(), ref)
+
+
 @pytest.mark.parametrize("m,n,k", [(2048, 4096, 4096), (128, 11008, 4096),
                                    (16, 4096, 11008)])
 def test_c3_linear_sweep(pkg, oracle, inputs, dev, m, n, k):
