@@ -163,30 +163,25 @@ __device__ __forceinline__ void vm_tie(P &v) {
   asm volatile("" : "+v"(v));
 }
 
-// sum_{s < splits} base[s * stride], added in s order, with up to 8 loads in
-// flight per wait.
-template <typename P>
+// sum_{s < splits} base[s * stride], added in s order, with up to B loads in
+// flight per wait (a short last batch adds exact zeros, which leave the sum
+// unchanged).
+template <typename P, int B = 8>
 __device__ __forceinline__ P partial_sum(const P *base, int64_t stride,
                                          int splits) {
   P sum = 0;
-  int s = 0;
-  for (; s + 8 <= splits; s += 8) {
-    P v[8];
+  for (int s = 0; s < splits; s += B) {
+    P v[B];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      v[u] = load_device(base + (int64_t)(s + u) * stride);
+    for (int u = 0; u < B; ++u)
+      v[u] = s + u < splits ? load_device(base + (int64_t)(s + u) * stride)
+                            : (P)0;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < B; ++u) {
       vm_tie(v[u]);
       sum += v[u];
     }
-  }
-  for (; s < splits; ++s) {
-    P v = load_device(base + (int64_t)s * stride);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    vm_tie(v);
-    sum += v;
   }
   return sum;
 }

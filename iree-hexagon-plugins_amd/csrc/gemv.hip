@@ -7,11 +7,12 @@
 // VTCM plan keeps K whole (CG/Strategy/Planning/VTCMPlanning.cpp:156-260).
 // With M = 1 the work is reading W once, so on MI355X it is a bandwidth
 // kernel, not an MFMA kernel:
-//  * each thread streams 16-byte row segments of W (8 f16 or 16 int8
-//    weights), several loads in flight, and accumulates in f32;
-//  * K is split over a 2-D grid (column block x K split) so the whole chip
-//    streams at once; each workgroup reduces its 8 K-lanes through LDS and
-//    writes an f32 partial;
+//  * each lane streams one 16-byte column segment of W (8 f16 or 16 int8
+//    weights) down a run of rows, 16 loads in flight, and accumulates in
+//    f32; x is read through the scalar cache, nothing is staged first;
+//  * K is split over a 2-D grid (column block x K split) sized to about one
+//    workgroup per CU; each workgroup sums its 8 waves through LDS and writes
+//    an f32 partial;
 //  * the last workgroup to finish a column block (device-scope arrival
 //    counter) sums the partials, applies the per-column scale (W8A16), adds
 //    the DPS init if asked, rounds once and re-arms the counter, so the
@@ -23,12 +24,11 @@ namespace ihp {
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kTN = 32;                 // threads across columns
-constexpr int kTK = kThreads / kTN;     // K lanes per workgroup
-constexpr int kUnroll = 8;              // 16-byte loads in flight per thread
-constexpr int kKChunkAlign = kTK * kUnroll;
-constexpr int kMaxKChunk = 1024;        // rows of W per workgroup (x in LDS)
+constexpr int kThreads = kGemvThreads;  // 8 waves
+constexpr int kWaves = kThreads / 64;
+constexpr int kBatch = 8;        // 16-byte loads per batch; two batches in flight
+constexpr int kSumBatch = 32;    // partial loads in flight in the final sum
+constexpr int kMaxRowsPerWave = 64;
 
 template <typename WT>
 struct WTraits;
@@ -65,36 +65,36 @@ __device__ __forceinline__ void store_y(f16 *p, float v, int acc) {
 
 }  // namespace
 
+// Grid: (column blocks, K splits). A workgroup owns 64 * kCols columns
+// (512 f16 / 1024 int8: one 16-byte segment per lane of a row) and k_chunk
+// rows, which its 8 waves split into contiguous runs of rows_per_wave. Each
+// lane streams its column segment down its wave's rows, two batches of
+// kBatch loads in flight, and accumulates in f32; x[r][k] is wave-uniform and
+// comes through the scalar cache.
 template <typename WT, int MR, typename OutT>
-__global__ __launch_bounds__(kThreads) void gemv_splitk_kernel(
+__global__ __launch_bounds__(kThreads, 1) void gemv_splitk_kernel(
     const f16 *__restrict__ X, const WT *__restrict__ W,
     const f16 *__restrict__ scale, OutT *__restrict__ Y, int N, int K,
-    int64_t ldx, int64_t ldw, int64_t ldy, int k_chunk, int accumulate,
-    float *__restrict__ partials, unsigned *__restrict__ counters) {
+    int64_t ldx, int64_t ldw, int64_t ldy, int k_chunk, int rows_per_wave,
+    int accumulate, float *__restrict__ partials,
+    unsigned *__restrict__ counters) {
   typedef WTraits<WT> Tr;
   constexpr int CPT = Tr::kCols;
-  constexpr int BNC = kTN * CPT;
-  __shared__ float xs[MR * kMaxKChunk];
-  __shared__ float red[4][MR][BNC];
+  constexpr int BNC = 64 * CPT;
+  __shared__ float red[kWaves][MR][BNC];
   __shared__ unsigned last_flag;
 
   const int tid = threadIdx.x;
-  const int tn = tid % kTN, tk = tid / kTN;
-  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int split = blockIdx.y, splits = gridDim.y;
-  const int64_t k0 = (int64_t)split * k_chunk;
-  const int64_t k1 = k0 + k_chunk < K ? k0 + k_chunk : K;
   const int64_t n_base = (int64_t)blockIdx.x * BNC;
-  const int64_t n0 = n_base + tn * CPT;
+  const int64_t n0 = n_base + lane * CPT;
   const bool col_ok = n0 < N;  // N is a multiple of CPT
-
-  // Stage this split's slice of x (MR rows) into LDS as f32.
-  for (int64_t i = tid; i < (int64_t)MR * (k1 - k0); i += kThreads) {
-    const int r = (int)(i / (k1 - k0));
-    const int64_t kk = i - r * (k1 - k0);
-    xs[r * kMaxKChunk + kk] = (float)X[r * ldx + k0 + kk];
-  }
-  __syncthreads();
+  const int64_t kc0 = (int64_t)split * k_chunk;
+  const int64_t kc1 = kc0 + k_chunk < K ? kc0 + k_chunk : K;
+  const int64_t kw0 = kc0 + (int64_t)wave * rows_per_wave;
+  const int64_t kw1 = kw0 + rows_per_wave < kc1 ? kw0 + rows_per_wave : kc1;
 
   float acc[MR][CPT];
 #pragma unroll
@@ -103,82 +103,84 @@ __global__ __launch_bounds__(kThreads) void gemv_splitk_kernel(
     for (int c = 0; c < CPT; ++c)
       acc[r][c] = 0.0f;
 
-  const char *wrow = (const char *)(W + n0);
+  // x[r][kw0 + lane] for this wave's rows (at most 64), loaded before any
+  // weight so that the in-order return of vector loads lets the weights stay
+  // in flight while it is read; row u of the run is then lane u's value,
+  // broadcast with readlane.
+  int xl[MR];  // raw f16 bits, widened when broadcast
+  const unsigned short *xbits = (const unsigned short *)X;
+#pragma unroll
+  for (int r = 0; r < MR; ++r)
+    xl[r] = kw0 + lane < kw1 ? (int)xbits[r * ldx + kw0 + lane] : 0;
+
+  // Lanes past N read column 0 instead (never stored), so every load of a
+  // batch is unpredicated and only the wave-uniform row bound branches.
+  const char *wcol = (const char *)(W + (col_ok ? n0 : 0));
   const int64_t ldw_b = ldw * (int64_t)sizeof(WT);
-  // Full groups of kUnroll rows: every load in range, no per-load branch.
-  int64_t kb = k0 + tk;
-  if (col_ok) {
-    for (; kb + (int64_t)(kUnroll - 1) * kTK < k1; kb += kTK * kUnroll) {
-      i32x4 v[kUnroll];
+  // Rows past the run re-read its last row (their products are skipped), so
+  // a batch is 8 unconditional loads the wait counter can track exactly.
+  auto load_batch = [&](int64_t kb, i32x4 *v) {
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u)
-        v[u] = __builtin_nontemporal_load(
-            (const i32x4 *)(wrow + (kb + (int64_t)u * kTK) * ldw_b));
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t k = kb + u < kw1 ? kb + u : kw1 - 1;
+      v[u] = __builtin_nontemporal_load((const i32x4 *)(wcol + k * ldw_b));
+    }
+  };
+  auto consume = [&](int64_t kb, const i32x4 *v) {
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int64_t k = kb + (int64_t)u * kTK;
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t k = kb + u;
+      if (k < kw1) {  // wave-uniform
         float w[CPT];
         Tr::widen(v[u], w);
+        const int idx = (int)(k - kw0);
 #pragma unroll
         for (int r = 0; r < MR; ++r) {
-          const float xv = xs[r * kMaxKChunk + (k - k0)];
+          const float xv = (float)__builtin_bit_cast(
+              f16, (unsigned short)__builtin_amdgcn_readlane(xl[r], idx));
 #pragma unroll
           for (int c = 0; c < CPT; ++c)
             acc[r][c] += xv * w[c];
         }
       }
     }
-  }
-  // Tail (K not a multiple of the group).
-  for (; kb < k1; kb += kTK * kUnroll) {
-    i32x4 v[kUnroll];
+  };
+  if (kw0 < kw1) {
+    i32x4 cur[kBatch], nxt[kBatch];
+    int64_t kb = kw0;
+    load_batch(kb, cur);
+    while (true) {
+      const bool more = kb + kBatch < kw1;
+      if (more)
+        load_batch(kb + kBatch, nxt);
+      consume(kb, cur);
+      if (!more)
+        break;
+      kb += kBatch;
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t k = kb + (int64_t)u * kTK;
-      v[u] = (col_ok && k < k1)
-                 ? __builtin_nontemporal_load((const i32x4 *)(wrow + k * ldw_b))
-                 : i32x4{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t k = kb + (int64_t)u * kTK;
-      if (k < k1) {
-        float w[CPT];
-        Tr::widen(v[u], w);
-#pragma unroll
-        for (int r = 0; r < MR; ++r) {
-          const float xv = xs[r * kMaxKChunk + (k - k0)];
-#pragma unroll
-          for (int c = 0; c < CPT; ++c)
-            acc[r][c] += xv * w[c];
-        }
-      }
+      for (int u = 0; u < kBatch; ++u)
+        cur[u] = nxt[u];
     }
   }
 
-  // Reduce the two K lanes of each wave, then the four waves through LDS.
+  // Sum the 8 waves' row runs through LDS, in wave order.
 #pragma unroll
   for (int r = 0; r < MR; ++r)
 #pragma unroll
     for (int c = 0; c < CPT; ++c)
-      acc[r][c] += __shfl_xor(acc[r][c], 32);
-  if ((tid & 63) < 32) {
-#pragma unroll
-    for (int r = 0; r < MR; ++r)
-#pragma unroll
-      for (int c = 0; c < CPT; ++c)
-        red[wave][r][tn * CPT + c] = acc[r][c];
-  }
+      red[wave][r][lane * CPT + c] = acc[r][c];
   __syncthreads();
 
   const bool direct = splits == 1;
   for (int i = tid; i < MR * BNC; i += kThreads) {
     const int r = i / BNC, col = i % BNC;
-    const float s = red[0][r][col] + red[1][r][col] + red[2][r][col] +
-                    red[3][r][col];
     const int64_t n = n_base + col;
     if (n >= N)
       continue;
+    float s = red[0][r][col];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w)
+      s += red[w][r][col];
     if (direct) {
       const float sc = scale ? (float)scale[n] : 1.0f;
       store_y(Y + r * ldy + n, s * sc, accumulate);
@@ -210,8 +212,8 @@ __global__ __launch_bounds__(kThreads) void gemv_splitk_kernel(
     const int64_t n = n_base + col;
     if (n >= N)
       continue;
-    const float s = partial_sum(&partials[(int64_t)r * N + n],
-                                (int64_t)MR * N, splits);
+    const float s = partial_sum<float, kSumBatch>(
+        &partials[(int64_t)r * N + n], (int64_t)MR * N, splits);
     const float sc = scale ? (float)scale[n] : 1.0f;
     store_y(Y + r * ldy + n, s * sc, accumulate);
   }
@@ -220,25 +222,30 @@ __global__ __launch_bounds__(kThreads) void gemv_splitk_kernel(
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
-static int round_up(int64_t v, int64_t a) { return (int)((v + a - 1) / a * a); }
-
 GemvPlan gemv_plan(int64_t m, int64_t n, int64_t k, int w_bytes) {
   (void)m;
   const int cpt = w_bytes == 2 ? 8 : 16;
   GemvPlan p;
-  p.cols_per_wg = kTN * cpt;
+  p.cols_per_wg = 64 * cpt;
   const int64_t col_blocks = (n + p.cols_per_wg - 1) / p.cols_per_wg;
-  // Aim for about three workgroups per CU over 256 CUs.
-  int64_t want = (768 + col_blocks - 1) / col_blocks;
+  // About one workgroup per CU (256): measured over 128..1024 workgroups on
+  // the C3 / C5 shapes, fewer and longer K runs shorten the split-K tail (the
+  // partial publish, arrival count and final sum are three memory round
+  // trips) but leave CUs idle, more add tail latency. Split K so that
+  // col_blocks x splits is about that, each wave's run of rows a multiple of
+  // the load batch.
+  int64_t want = (kGemvTargetWgs + col_blocks / 2) / col_blocks;
   if (want < 1)
     want = 1;
-  int chunk = round_up((k + want - 1) / want, kKChunkAlign);
-  if (chunk > kMaxKChunk)
-    chunk = kMaxKChunk;
-  if (chunk < kKChunkAlign)
-    chunk = kKChunkAlign;
-  p.k_chunk = chunk;
-  p.splits = k > 0 ? (int)((k + chunk - 1) / chunk) : 1;
+  int64_t rpw = (k + want * kWaves - 1) / (want * kWaves);
+  rpw = (rpw + kBatch - 1) / kBatch * kBatch;
+  if (rpw < kBatch)
+    rpw = kBatch;
+  if (rpw > kMaxRowsPerWave)  // x of a run is one value per lane
+    rpw = kMaxRowsPerWave;
+  p.rows_per_wave = (int)rpw;
+  p.k_chunk = (int)(rpw * kWaves);
+  p.splits = k > 0 ? (int)((k + p.k_chunk - 1) / p.k_chunk) : 1;
   p.col_blocks = col_blocks;
   return p;
 }
@@ -271,7 +278,7 @@ static hipError_t launch_gemv_t(const MatmulArgs &a, const void *scale,
                      0, (hipStream_t)a.stream, (const f16 *)a.a,
                      (const WT *)a.b, (const f16 *)scale, (OutT *)a.c,
                      (int)a.n, (int)a.k, a.lda, a.ldb, a.ldc, p.k_chunk,
-                     a.accumulate, partials, counters);
+                     p.rows_per_wave, a.accumulate, partials, counters);
   return hipGetLastError();
 }
 

@@ -72,10 +72,13 @@ hipError_t launch_general(const MatmulArgs &a, GeneralKind kind,
 // Skinny (M <= kGemvMaxRows) matmul with B [K,N] row-major: split-K streaming
 // kernel with an in-kernel last-arriver reduction over `splits` partials.
 constexpr int kGemvMaxRows = 4;
+constexpr int kGemvThreads = 512;
+constexpr int kGemvTargetWgs = 256;
 struct GemvPlan {
   int splits;          // K split count (grid y)
   int cols_per_wg;     // output columns per workgroup
   int k_chunk;         // rows of W per workgroup
+  int rows_per_wave;   // contiguous rows each of the 8 waves streams
   int64_t col_blocks;  // grid x
 };
 GemvPlan gemv_plan(int64_t m, int64_t n, int64_t k, int w_bytes);

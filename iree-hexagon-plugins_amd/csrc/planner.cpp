@@ -270,7 +270,7 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
     plan->tile_n = g.cols_per_wg;
     plan->tile_k = g.k_chunk;
     plan->workgroups = g.col_blocks * g.splits;
-    plan->threads = 256;
+    plan->threads = kGemvThreads;
     plan->splits = g.splits;
     plan->workspace_bytes = (int64_t)gemv_workspace_bytes(d->m, d->n, d->k, wb);
     plan->traffic_bytes = d->n * d->k * wb + d->m * d->k * 2;
