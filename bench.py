@@ -31,8 +31,12 @@ ROTATE_BYTES = 600 << 20   # > 2 x 256 MiB Infinity Cache
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=10)
+    # The defaults time the GPU at its sustained clock: on random operands
+    # the shader clock settles over the first ~30 ms of MFMA load (measured
+    # 1.5 -> 2.0 GHz), so 1000 warmup dispatches (~70 ms) precede the
+    # 500 timed ones (~35 ms) of the headline workload.
+    p.add_argument("--steps", type=int, default=500)
+    p.add_argument("--warmup", type=int, default=1000)
     p.add_argument("--suite", action="store_true")
     p.add_argument("--tune", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")

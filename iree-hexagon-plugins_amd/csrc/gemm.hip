@@ -206,30 +206,38 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   }
   IHP_LDS char *lds = (IHP_LDS char *)smem;
 
-  auto load_stage = [&](int kt, int slot) {
+  // Copy pass p of stage kt into `slot` (A passes first, then B passes).
+  auto load_pass = [&](int kt, int slot, int p) {
     IHP_LDS char *dst = lds + slot * STAGE_BYTES;
     const int64_t ka = (int64_t)kt * BKB;
-#pragma unroll
-    for (int p = 0; p < A_PASSES; ++p)
+    if (p < A_PASSES) {
       global_to_lds_16(a_base + ka + a_lane[p],
                        dst + wave * ROWS_PER_WAVE * BKB +
                            p * ROWS_PER_PASS * BKB);
-    if constexpr (kNN) {
-      const int64_t kb = (int64_t)kt * KE * ldb_b;
-#pragma unroll
-      for (int p = 0; p < B_PASSES; ++p)
-        global_to_lds_16(b_base + kb + (int64_t)p * B_RPP * ldb_b + b_lane,
-                         dst + A_BYTES + wave * B_RPW * BROW +
-                             p * B_RPP * BROW);
     } else {
-#pragma unroll
-      for (int p = 0; p < B_PASSES; ++p)
-        global_to_lds_16(b_base + ka + (int64_t)p * ROWS_PER_PASS * ldb_b +
+      const int q = p - A_PASSES;
+      if constexpr (kNN) {
+        const int64_t kb = (int64_t)kt * KE * ldb_b;
+        global_to_lds_16(b_base + kb + (int64_t)q * B_RPP * ldb_b + b_lane,
+                         dst + A_BYTES + wave * B_RPW * BROW +
+                             q * B_RPP * BROW);
+      } else {
+        global_to_lds_16(b_base + ka + (int64_t)q * ROWS_PER_PASS * ldb_b +
                              b_lane,
                          dst + A_BYTES + wave * ROWS_PER_WAVE * BKB +
-                             p * ROWS_PER_PASS * BKB);
+                             q * ROWS_PER_PASS * BKB);
+      }
     }
   };
+  // Passes [LO, HI) of stage kt.
+  auto load_passes = [&](auto lo, auto hi, int kt, int slot) {
+    static_for<decltype(hi)::value - decltype(lo)::value>([&](auto i) {
+      load_pass(kt, slot, decltype(lo)::value + decltype(i)::value);
+    });
+  };
+  using First = std::integral_constant<int, 0>;
+  using Half = std::integral_constant<int, LOADS_PER_STAGE / 2>;
+  using All = std::integral_constant<int, LOADS_PER_STAGE>;
 
   // Read side, A (and TN B): lane reads row (lane % 32) of each 32-row
   // fragment, logical chunk 2*ks + lane/32 of the staged row.
@@ -339,7 +347,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
 #pragma unroll
   for (int s = 0; s < STAGES; ++s)
     if (s < nk)
-      load_stage(s, s);
+      load_passes(First(), All(), s, s);
   if (STAGES - 1 < nk)
     wait_vmcnt<(STAGES - 1) * LOADS_PER_STAGE>();
   else
@@ -351,12 +359,19 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
 
   // Per K step: issue the next step's fragment reads, wait only for this
   // step's (issued one step earlier), then this step's MFMAs, which run
-  // while the new reads are in flight.
+  // while the new reads are in flight. The copies of stage kt+STAGES are
+  // issued in two halves, at the stage handoff and after the next stage's
+  // first K step, so the waves of a SIMD do not all stall on copy issue at
+  // once while their MFMAs wait (measured 3-4 % on the int8 4096^3 case).
   for (int kt = 0; kt < nk; ++kt) {
     const int slot = kt % STAGES;
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
       const int cur = ks & 1, nxt = cur ^ 1;
+      // Second half of stage kt-1+STAGES, into the slot stage kt-1 used:
+      // every wave finished reading it before the previous handoff barrier.
+      if (ks == 1 && kt >= 1 && kt - 1 + STAGES < nk)
+        load_passes(Half(), All(), kt - 1 + STAGES, (kt - 1) % STAGES);
       if (ks + 1 < KSTEPS) {
         read_frags(slot, ks + 1, fr[nxt]);
         frags_ready(std::integral_constant<int, RD>(), fr[cur]);
@@ -364,7 +379,9 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
         // Stage handoff: this step's fragments are in registers (all LDS
         // reads done), stage kt+1 must have landed for every wave, and every
         // wave must be done reading stage kt before its slot is refilled
-        // with stage kt+STAGES.
+        // with stage kt+STAGES. By now this wave has issued every copy up to
+        // stage kt+STAGES-1, so stage kt+1 has landed once at most
+        // STAGES-2 stages of copies remain in flight.
         frags_ready(std::integral_constant<int, 0>(), fr[cur]);
         if (kt + STAGES - 1 < nk)
           wait_vmcnt<(STAGES - 2) * LOADS_PER_STAGE>();
@@ -372,7 +389,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
           wait_vmcnt<0>();
         block_barrier();
         if (kt + STAGES < nk)
-          load_stage(kt + STAGES, slot);
+          load_passes(First(), Half(), kt + STAGES, slot);
         read_frags((kt + 1) % STAGES, 0, fr[nxt]);
       } else {
         frags_ready(std::integral_constant<int, 0>(), fr[cur]);
