@@ -462,17 +462,51 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     __syncthreads();
     if (!*last_split)
       return;
+    // The tile's valid rows, G elements per thread at a time, each summed
+    // over the splits in split order: G x SB device-scope loads in flight
+    // per wait instead of one element's splits.
     const int splits = (int)gridDim.y;
-    for (int idx = tid; idx < BM * BN; idx += NT) {
-      const int64_t row = m0 + idx / BN, col = n0 + idx % BN;
-      if (row >= M)
-        continue;
-      const P sum =
-          partial_sum(partials + row * N + col, (int64_t)M * N, splits);
-      if constexpr (BMODE == kBW8)
-        store_out(C + row * ldc + col, (float)sum * (float)scale[col], 0);
-      else
-        store_out(C + row * ldc + col, sum, accumulate);
+    const int rows_valid = (int)(M - m0 < BM ? M - m0 : BM);
+    const int count = rows_valid * BN;
+    constexpr int G = 8, SB = 8;
+    for (int base = 0; base < count; base += NT * G) {
+      P sum[G];
+#pragma unroll
+      for (int e = 0; e < G; ++e)
+        sum[e] = 0;
+      for (int s0 = 0; s0 < splits; s0 += SB) {
+        P v[G][SB];
+#pragma unroll
+        for (int e = 0; e < G; ++e) {
+          const int idx = base + e * NT + tid;
+          const int64_t row = m0 + idx / BN, col = n0 + idx % BN;
+          const P *src = partials + ((int64_t)s0 * M + row) * N + col;
+#pragma unroll
+          for (int u = 0; u < SB; ++u)
+            v[e][u] = idx < count && s0 + u < splits
+                          ? load_device(src + (int64_t)u * M * N)
+                          : (P)0;
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int e = 0; e < G; ++e)
+#pragma unroll
+          for (int u = 0; u < SB; ++u) {
+            vm_tie(v[e][u]);
+            sum[e] += v[e][u];
+          }
+      }
+#pragma unroll
+      for (int e = 0; e < G; ++e) {
+        const int idx = base + e * NT + tid;
+        if (idx >= count)
+          continue;
+        const int64_t row = m0 + idx / BN, col = n0 + idx % BN;
+        if constexpr (BMODE == kBW8)
+          store_out(C + row * ldc + col, (float)sum[e] * (float)scale[col], 0);
+        else
+          store_out(C + row * ldc + col, sum[e], accumulate);
+      }
     }
     if (tid == 0)  // re-arm for the next call on this workspace
       __hip_atomic_store(&counters[blockIdx.x], 0u, __ATOMIC_RELAXED,
@@ -639,11 +673,13 @@ static const FastConfig kFastConfigs[] = {
     IHP_FAST_CONFIG("w8a16_nn_128x256x64_w2x4_s4", kBW8, f16, f16, 128, 256, 128, 2, 4, 4),
     IHP_FAST_CONFIG("w8a16_nn_128x256x64_w2x2_s4", kBW8, f16, f16, 128, 256, 128, 2, 2, 4),
     // split-K skinny tiles (M < tile rows allowed; partials in workspace)
-    IHP_FAST_CONFIG_S("f16_nn_32x256x64_w1x4_s4_sk", kBNN16, f16, f16, 32, 256, 128, 1, 4, 4, true),
-    IHP_FAST_CONFIG_S("f16_nn_64x256x64_w1x4_s4_sk", kBNN16, f16, f16, 64, 256, 128, 1, 4, 4, true),
+    // (measured on M = 16..128 with N, K in {4096, 11008}: 32x128 beats
+    // 32x256 / 64x256 at every point, 64x128 is best for some M = 64..128)
+    IHP_FAST_CONFIG_S("f16_nn_32x128x64_w1x4_s4_sk", kBNN16, f16, f16, 32, 128, 128, 1, 4, 4, true),
+    IHP_FAST_CONFIG_S("f16_nn_64x128x64_w2x2_s4_sk", kBNN16, f16, f16, 64, 128, 128, 2, 2, 4, true),
     IHP_FAST_CONFIG_S("f16_nn_128x128x64_w2x2_s4_sk", kBNN16, f16, f16, 128, 128, 128, 2, 2, 4, true),
-    IHP_FAST_CONFIG_S("f16f32_nn_32x256x64_w1x4_s4_sk", kBNN16, f16, float, 32, 256, 128, 1, 4, 4, true),
-    IHP_FAST_CONFIG_S("f16_tn_32x256x64_w1x4_s4_sk", kBTN, f16, f16, 32, 256, 128, 1, 4, 4, true),
+    IHP_FAST_CONFIG_S("f16f32_nn_32x128x64_w1x4_s4_sk", kBNN16, f16, float, 32, 128, 128, 1, 4, 4, true),
+    IHP_FAST_CONFIG_S("f16_tn_32x128x64_w1x4_s4_sk", kBTN, f16, f16, 32, 128, 128, 1, 4, 4, true),
     IHP_FAST_CONFIG_S("f16_tn_128x128x64_w2x2_s4_sk", kBTN, f16, f16, 128, 128, 128, 2, 2, 4, true),
     IHP_FAST_CONFIG_S("w8a16_nn_32x256x64_w1x4_s4_sk", kBW8, f16, f16, 32, 256, 128, 1, 4, 4, true),
     IHP_FAST_CONFIG_S("w8a16_nn_128x256x64_w2x4_s4_sk", kBW8, f16, f16, 128, 256, 128, 2, 4, 4, true),

@@ -250,12 +250,12 @@ GemvPlan gemv_plan(int64_t m, int64_t n, int64_t k, int w_bytes) {
   return p;
 }
 
-// Workspace layout: [arrival counters, one per column block][f32 partials
-// (splits x rows x N)]. The counters sit at offset 0 for every shape, so one
-// zero-filled workspace serves any sequence of calls; each call leaves the
-// counters it used at zero again.
+// Workspace layout: [the fixed counter region, one counter per column block]
+// [f32 partials (splits x rows x N)]. Each call leaves the counters it used at
+// zero again.
 static size_t counter_bytes(int64_t col_blocks) {
-  return (size_t)((col_blocks * 4 + 255) / 256 * 256);
+  (void)col_blocks;
+  return kWorkspaceCounterBytes;
 }
 
 size_t gemv_workspace_bytes(int64_t m, int64_t n, int64_t k, int w_bytes) {

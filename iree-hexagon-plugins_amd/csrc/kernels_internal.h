@@ -30,15 +30,21 @@ struct MatmulArgs {
   void *stream;
   const void *scale;  // W8A16 per-column scale (else NULL)
   // split-K configurations: split count, K elements per split, workspace
-  // ([counters, one per tile][partials, splits x M x N accumulators])
+  // ([counter region][partials, splits x M x N accumulators])
   int splits;
   int k_split;
   void *workspace;
 };
 
-// Bytes of the split-K counter block at the start of the workspace.
+// Every workspace starts with one fixed counter region: one u32 arrival
+// counter per tile (split-K GEMM) or column block (GEMV), left at zero by
+// every call. Its size does not depend on the shape, so no call's partials
+// can overlap another call's counters on a shared workspace.
+constexpr size_t kWorkspaceCounterBytes = 64 * 1024;
+constexpr int64_t kMaxWorkspaceCounters = kWorkspaceCounterBytes / 4;
 inline size_t split_counter_bytes(int64_t tiles) {
-  return (size_t)((tiles * 4 + 255) / 256 * 256);
+  (void)tiles;
+  return kWorkspaceCounterBytes;
 }
 
 typedef hipError_t (*FastLaunchFn)(const MatmulArgs &);

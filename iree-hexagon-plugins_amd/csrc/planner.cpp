@@ -75,6 +75,9 @@ bool gemv_eligible(const iree_mi355x_matmul_desc_t &d) {
   const int cols = 16 / elem_bytes(d.b_elem);
   if (d.n % cols != 0)
     return false;
+  // one arrival counter per column block of 64 lanes x `cols` columns
+  if ((d.n + 64 * cols - 1) / (64 * cols) > kMaxWorkspaceCounters)
+    return false;
   // int8 weights only in the W8A16 form; f16 with f16 or f32 output.
   if (d.b_elem == IREE_MI355X_ELEM_I8)
     return d.has_scale;
@@ -140,6 +143,8 @@ constexpr double kHbmBytesPerNs = 6000.0;
 // arrival count and the last arriver's reduction.
 constexpr double kRoundNs = 1500.0;
 constexpr double kSplitNs = 2000.0;
+constexpr double kRoundTripNs = 700.0;  // one dependent device-scope access
+constexpr double kStageNs = 500.0;      // per K stage of one workgroup
 // A split covers at least this many K stages, so its copy pipeline overlaps.
 constexpr int64_t kMinStagesPerSplit = 2;
 
@@ -152,6 +157,8 @@ bool evaluate(const iree_mi355x_matmul_desc_t &d, const FastConfig &c,
     return false;
   const int64_t tiles_m = (d.m + c.bm - 1) / c.bm;
   const int64_t tiles = tiles_m * (d.n / c.bn);
+  if (c.split_k && tiles > kMaxWorkspaceCounters)
+    return false;  // one arrival counter per tile
   int splits = 1;
   int64_t k_split = d.k;
   if (c.split_k) {
@@ -176,7 +183,10 @@ bool evaluate(const iree_mi355x_matmul_desc_t &d, const FastConfig &c,
   r.k_split = (int)k_split;
   r.tiles = tiles;
   r.critical = ((tiles * splits + cus - 1) / cus) * c.bm * c.bn * k_split;
-  r.traffic = ab * d.m * d.k * (d.n / c.bn) + bb * d.n * d.k * tiles_m;
+  // A rows past M (split configurations) are still copied, as clamped
+  // duplicates of row M-1.
+  r.traffic = ab * (tiles_m * c.bm) * d.k * (d.n / c.bn) +
+              bb * d.n * d.k * tiles_m;
   int64_t partial_bytes = 0;
   if (c.split_k) {
     r.workspace = (int64_t)split_counter_bytes(tiles) +
@@ -197,9 +207,20 @@ bool evaluate(const iree_mi355x_matmul_desc_t &d, const FastConfig &c,
   double t = t_mfma > t_feed ? t_mfma : t_feed;
   if (t_hbm > t)
     t = t_hbm;
-  t += (double)((tiles * splits + cus - 1) / cus) * kRoundNs;
-  if (c.split_k)
-    t += kSplitNs;
+  // A workgroup's K loop is a chain of stages, each at least a copy latency
+  // apart once the ring's lookahead is spent.
+  const int64_t rounds = (tiles * splits + cus - 1) / cus;
+  const double t_chain = (double)rounds * (double)(k_split / c.bk) * kStageNs;
+  if (t_chain > t)
+    t = t_chain;
+  t += (double)rounds * kRoundNs;
+  if (c.split_k) {
+    // the last arriver sums G=8 elements x 8 splits per memory round trip
+    const int64_t rows = d.m < c.bm ? d.m : c.bm;
+    const int64_t per_thread = (rows * c.bn + c.threads - 1) / c.threads;
+    t += kSplitNs + (double)((per_thread + 7) / 8) *
+                        (double)((splits + 7) / 8) * kRoundTripNs;
+  }
   r.est_ns = (int64_t)t;
   *out = r;
   return true;

@@ -175,6 +175,26 @@ def test_split_k_skinny(pkg, oracle, dev, m, n, k, form):
         check_canary(buf, m, n, 5.0)
 
 
+def test_workspace_shared_across_kernels(pkg, oracle, dev):
+    """GEMV and split-K GEMM calls of different shapes, interleaved on the
+    library's one workspace: no call's partials may land on another call's
+    arrival counters (regression: a GEMV's partials once overwrote the
+    counters of split-K tiles past the 64th)."""
+    g = torch.Generator().manual_seed(11)
+    cases = [(1, 11008, 2048), (64, 8448, 2048), (3, 4096, 1024),
+             (96, 8448, 1024), (1, 4096, 1024), (64, 11008, 2048),
+             (2, 11008, 2048), (64, 8448, 2048)]
+    for m, n, k in cases:
+        p = pkg.plan(pkg.make_desc(0, 0, 0, m, n, k, 0))
+        assert p.splits > 1 and (p.family == pkg.FAMILY_GEMV or
+                                 p.workgroups // p.splits > 64), (m, n, k)
+        x = (torch.randn(m, k, generator=g) * 0.5).half()
+        w = torch.randn(k, n, generator=g).half()
+        y = pkg.matmul(x.to(dev), w.to(dev))
+        ref = oracle.matmul_f16(x.numpy(), w.numpy())
+        fp16_ok(oracle, y.cpu().numpy(), ref)
+
+
 def test_split_k_accumulate_f32(pkg, oracle, dev):
     g = torch.Generator().manual_seed(77)
     m, n, k = 24, 2048, 4096
