@@ -14,9 +14,12 @@
 //  * online softmax in f32 (exp2 with the scale folded in), running max and
 //    sum per row, output rescaled in registers;
 //  * O^T += V^T P^T on MFMA with P taken straight from the score registers
-//    (rounded to f16) and V^T staged in LDS;
+//    (rounded to f16) and V^T read transposed from key-major LDS
+//    (ds_read_b64_tr_b16);
+//  * K and V blocks stream HBM -> LDS (global_load_lds) one block ahead of
+//    the block being computed;
 //  * causal blocks above the diagonal are skipped, the diagonal blocks are
-//    masked, and query blocks are scheduled heaviest first.
+//    masked, and heavy query blocks are interleaved with light ones.
 #include "device_common.h"
 #include "kernels_internal.h"
 
@@ -25,28 +28,67 @@ namespace ihp {
 namespace {
 constexpr int kBQ = 128;   // query rows per workgroup
 constexpr int kBKV = 64;   // keys per block
-constexpr int kVtPad = 4;  // halves of padding per V^T row (bank spread)
+constexpr int kThreads = 256;
+
+// Transposed 8-byte LDS read (ds_read_b64_tr_b16): within each 16-lane
+// block, lane i receives element i%4 of the 8-byte loads of lanes
+// 4r + i/4, r = 0..3.
+__device__ __forceinline__ i32x2 lds_read_tr16(const IHP_LDS char *p) {
+  i32x2 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v)
+               : "v"((unsigned)(uintptr_t)p));
+  return v;
+}
+__device__ __forceinline__ void tie2(i32x2 &v) { asm volatile("" : "+v"(v)); }
 }  // namespace
 
+// K and V blocks are copied HBM -> LDS with global_load_lds into a two-slot
+// ring (block kb+1 streams in while block kb is computed). Both are stored
+// key-major as in HBM, 16-byte chunks XOR-swizzled on the copy side:
+//  * K rows are read by ds_read_b128, 16 lanes = 16 consecutive keys at one
+//    chunk: chunk ^ (key & 15) for 256-byte rows (D = 128),
+//    chunk ^ ((key >> 1) & 7) for 128-byte rows (D = 64);
+//  * V is read transposed (V^T operand) by ds_read_b64_tr_b16, 32 lanes =
+//    4 consecutive keys x 32 d: chunk ^ 4 * (key & 3) (D = 128),
+//    chunk ^ 4 * ((key >> 1) & 1) (D = 64).
 template <int D>
-__global__ __launch_bounds__(256, 2) void attention_fwd_kernel(
+__device__ __forceinline__ int k_swizzle(int key) {
+  return D == 128 ? (key & 15) : ((key >> 1) & 7);
+}
+template <int D>
+__device__ __forceinline__ int v_swizzle(int key) {
+  return D == 128 ? 4 * (key & 3) : 4 * ((key >> 1) & 1);
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
     const f16 *__restrict__ Q, const f16 *__restrict__ K,
     const f16 *__restrict__ V, f16 *__restrict__ O, int heads, int seq_q,
     int seq_kv, float scale_log2, int causal) {
-  constexpr int DS = D / 16;         // 16-wide d steps of S^T = K Q^T
-  constexpr int DT = D / 32;         // 32-row d tiles of O^T
-  constexpr int KROW = D * 2;        // bytes per staged K row
-  constexpr int KCH = KROW / 16;     // 16-byte chunks per K row
-  constexpr int VT_ROW = kBKV + kVtPad;  // halves per V^T row
-  __shared__ __attribute__((aligned(16))) char Ks[kBKV * KROW];
-  __shared__ __attribute__((aligned(16))) f16 Vt[D * VT_ROW];
+  constexpr int DS = D / 16;       // 16-wide d steps of S^T = K Q^T
+  constexpr int DT = D / 32;       // 32-row d tiles of O^T
+  constexpr int ROW = D * 2;       // bytes per staged K / V row
+  constexpr int CH = ROW / 16;     // 16-byte chunks per row
+  constexpr int BLK = kBKV * ROW;  // bytes of one staged K (or V) block
+  constexpr int ROWS_PER_INSN = 64 / CH;             // rows per wave copy
+  constexpr int PASSES = kBKV / (4 * ROWS_PER_INSN);  // per wave, per tensor
+  static_assert(PASSES * 4 * ROWS_PER_INSN == kBKV, "copy shape");
+  __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * BLK];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
   const int q_blocks = (seq_q + kBQ - 1) / kBQ;
   // Heaviest (last) query blocks first under a causal mask.
-  const int qb = q_blocks - 1 - (int)(blockIdx.x / (unsigned)(gridDim.x / q_blocks));
-  const int plane = (int)(blockIdx.x % (unsigned)(gridDim.x / q_blocks));
+  // Under a causal mask query block qb costs qb + 1 units. The first half
+  // of the grid takes the heavy blocks (heaviest first), the second half the
+  // light ones (lightest first), so the two workgroups that share a CU sum to
+  // about the same work.
+  const int planes = (int)(gridDim.x / (unsigned)q_blocks);
+  const int idx = (int)(blockIdx.x / (unsigned)planes);
+  const int half = (q_blocks + 1) / 2;
+  const int qb = idx < half ? q_blocks - 1 - idx : idx - half;
+  const int plane = (int)(blockIdx.x % (unsigned)planes);
   const int64_t q_off = (int64_t)plane * seq_q * D;
   const int64_t kv_off = (int64_t)plane * seq_kv * D;
   const int q0 = qb * kBQ + wave * 32;  // this wave's first query row
@@ -63,6 +105,44 @@ __global__ __launch_bounds__(256, 2) void attention_fwd_kernel(
       qf[s] = i32x4{0, 0, 0, 0};
   }
 
+  int kv_end = seq_kv;
+  if (causal) {
+    const int last_q = qb * kBQ + kBQ - 1;
+    kv_end = last_q + 1 < seq_kv ? last_q + 1 : seq_kv;
+  }
+  const int n_blocks = (kv_end + kBKV - 1) / kBKV;
+
+  // Copy side: a wave instruction moves ROWS_PER_INSN rows of CH chunks;
+  // lane -> (row, physical chunk), fetching the logical chunk that belongs
+  // there. Keys past seq_kv are clamped to the last key (masked later).
+  const int c_row = lane / CH, c_phys = lane % CH;
+  IHP_LDS char *lds = (IHP_LDS char *)smem;
+  auto copy_block = [&](int kb, int slot) {
+    const int kv0 = kb * kBKV;
+    IHP_LDS char *kd = lds + slot * 2 * BLK;
+    IHP_LDS char *vd = kd + BLK;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int row = (p * 4 + wave) * ROWS_PER_INSN + c_row;
+      int key = kv0 + row;
+      key = key < seq_kv ? key : seq_kv - 1;
+      const f16 *kr = K + kv_off + (int64_t)key * D;
+      const f16 *vr = V + kv_off + (int64_t)key * D;
+      global_to_lds_16(kr + 8 * (c_phys ^ k_swizzle<D>(row)),
+                       kd + (p * 4 + wave) * ROWS_PER_INSN * ROW);
+      global_to_lds_16(vr + 8 * (c_phys ^ v_swizzle<D>(row)),
+                       vd + (p * 4 + wave) * ROWS_PER_INSN * ROW);
+    }
+  };
+
+  // V^T read side: for key step (t, h) lane group g needs keys
+  // kstart = 32t + 16h + 4g .. +3 and kstart + 8 .. +11 (the order the S^T
+  // registers hold them in). Load lane j = lane % 16 of block b = lane / 16
+  // reads row kstart + j/4, d = 32 dt + 16 (b % 2) + 4 (j % 4) .. +3.
+  const int vj = lane & 15, vb = lane >> 4;
+  const int v_row_in = vj >> 2;                       // + kstart
+  const int v_dbyte = 2 * (16 * (vb & 1) + 4 * (vj & 3));  // + 64 dt
+
   f32x16 o[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t)
@@ -71,31 +151,19 @@ __global__ __launch_bounds__(256, 2) void attention_fwd_kernel(
       o[t][r] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
 
-  int kv_end = seq_kv;
-  if (causal) {
-    const int last_q = qb * kBQ + kBQ - 1;
-    kv_end = last_q + 1 < seq_kv ? last_q + 1 : seq_kv;
-  }
-  const int n_blocks = (kv_end + kBKV - 1) / kBKV;
-
+  if (n_blocks > 0)
+    copy_block(0, 0);
   for (int kb = 0; kb < n_blocks; ++kb) {
     const int kv0 = kb * kBKV;
-    __syncthreads();  // previous block's K / V^T reads are done
-    // Stage K [64][D] (16-byte chunks XOR-swizzled by row) and V^T [D][64].
-    for (int it = tid; it < kBKV * KCH; it += 256) {
-      const int key = it / KCH, c = it % KCH;
-      i32x4 kv = i32x4{0, 0, 0, 0}, vv = i32x4{0, 0, 0, 0};
-      if (kv0 + key < seq_kv) {
-        kv = *(const i32x4 *)(K + kv_off + (int64_t)(kv0 + key) * D + 8 * c);
-        vv = *(const i32x4 *)(V + kv_off + (int64_t)(kv0 + key) * D + 8 * c);
-      }
-      *(i32x4 *)(Ks + key * KROW + ((c ^ (key & 7)) * 16)) = kv;
-      f16x8 vh = __builtin_bit_cast(f16x8, vv);
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        Vt[(8 * c + e) * VT_ROW + key] = vh[e];
-    }
-    __syncthreads();
+    const int slot = kb & 1;
+    // Block kb has landed for every wave, and every wave is done with block
+    // kb-1, whose slot now receives block kb+1 while kb is computed.
+    wait_vmcnt<0>();
+    block_barrier();
+    if (kb + 1 < n_blocks)
+      copy_block(kb + 1, slot ^ 1);
+    const IHP_LDS char *ks = lds + slot * 2 * BLK;
+    const IHP_LDS char *vs = ks + BLK;
 
     // S^T tiles: keys 32t..32t+31 x this wave's 32 queries.
     f32x16 st[2];
@@ -108,51 +176,70 @@ __global__ __launch_bounds__(256, 2) void attention_fwd_kernel(
 #pragma unroll
       for (int s = 0; s < DS; ++s) {
         const int c = 2 * s + g;
-        i32x4 kf = *(const i32x4 *)(Ks + key * KROW + ((c ^ (key & 7)) * 16));
+        const i32x4 kf =
+            *(const IHP_LDS i32x4 *)(ks + key * ROW + ((c ^ k_swizzle<D>(key)) * 16));
         st[t] = Mfma32<f16>::mma(kf, qf[s], st[t]);
       }
     }
 
-    // Mask (causal diagonal, sequence tail), then the online softmax update.
-    const bool need_mask = (causal && kv0 + kBKV - 1 > q0) || kv0 + kBKV > seq_kv;
-    float mx = -INFINITY;
+    // Mask (causal diagonal, sequence tail), then the online softmax update
+    // in the log2 domain: p = 2^(s * scale_log2 - m). Off the diagonal the
+    // row max is taken on the raw scores (scale_log2 > 0 keeps the order) and
+    // the scale is fused into the exponent's FMA.
+    const bool need_mask =
+        (causal && kv0 + kBKV - 1 > q0) || kv0 + kBKV > seq_kv;
+    float mx;
+    float sc = scale_log2;  // multiplier applied inside the exponent
+    if (need_mask || scale_log2 <= 0.0f) {
+      mx = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < 2; ++t) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float s = st[t][r] * scale_log2;
-        if (need_mask) {
+        for (int r = 0; r < 16; ++r) {
+          float s = st[t][r] * scale_log2;
           const int key = kv0 + 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
           if (key >= seq_kv || (causal && key > my_q))
             s = -INFINITY;
+          st[t][r] = s;
+          mx = fmaxf(mx, s);
         }
-        st[t][r] = s;
-        mx = fmaxf(mx, s);
       }
+      sc = 1.0f;
+    } else {
+      mx = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          mx = fmaxf(mx, st[t][r]);
+      mx *= scale_log2;
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float m_new = fmaxf(m_run, mx);
     // A row with every key masked so far keeps m = -inf; exp2 of a finite
     // offset from it must not produce nan.
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = exp2f(m_run - m_use);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
     float psum = 0.0f;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = exp2f(st[t][r] - m_use);
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(st[t][r], sc, -m_use));
         st[t][r] = p;
         psum += p;
       }
     psum += __shfl_xor(psum, 32);
     l_run = l_run * alpha + psum;
     m_run = m_new;
+    // rescale the running output only when some row's max moved
+    if (!__all(alpha == 1.0f)) {
 #pragma unroll
-    for (int t = 0; t < DT; ++t)
+      for (int t = 0; t < DT; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        o[t][r] *= alpha;
+        for (int r = 0; r < 16; ++r)
+          o[t][r] *= alpha;
+    }
 
     // O^T[d][q] += V^T[d][key] P^T[key][q], 16 keys per MFMA.
 #pragma unroll
@@ -164,13 +251,22 @@ __global__ __launch_bounds__(256, 2) void attention_fwd_kernel(
         for (int e = 0; e < 8; ++e)
           pf[e] = (f16)st[t][8 * h + e];
         const i32x4 pb = __builtin_bit_cast(i32x4, pf);
-        const int kbase = 32 * t + 16 * h + 4 * g;
+        const int kstart = 32 * t + 16 * h + 4 * g;
+        const int r0 = kstart + v_row_in, r1 = r0 + 8;
+        // all 2 x DT transposed reads of this key step under one wait
+        i32x2 lo[DT], hi[DT];
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          const f16 *vrow = Vt + (32 * dt + l32) * VT_ROW + kbase;
-          const i32x2 lo = *(const i32x2 *)(vrow);
-          const i32x2 hi = *(const i32x2 *)(vrow + 8);
-          const i32x4 vf = i32x4{lo[0], lo[1], hi[0], hi[1]};
+          const int b0 = 64 * dt + v_dbyte, c0 = b0 >> 4, w0 = b0 & 15;
+          lo[dt] = lds_read_tr16(vs + r0 * ROW + ((c0 ^ v_swizzle<D>(r0)) << 4) + w0);
+          hi[dt] = lds_read_tr16(vs + r1 * ROW + ((c0 ^ v_swizzle<D>(r1)) << 4) + w0);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          tie2(lo[dt]);
+          tie2(hi[dt]);
+          const i32x4 vf = i32x4{lo[dt][0], lo[dt][1], hi[dt][0], hi[dt][1]};
           o[dt] = Mfma32<f16>::mma(vf, pb, o[dt]);
         }
       }
@@ -203,12 +299,12 @@ hipError_t launch_attention(const void *q, const void *k, const void *v,
   dim3 grid((unsigned)(q_blocks * planes));
   const float scale_log2 = scale * 1.4426950408889634f;  // log2(e)
   if (head_dim == 128)
-    hipLaunchKernelGGL((attention_fwd_kernel<128>), grid, dim3(256), 0,
+    hipLaunchKernelGGL((attention_fwd_kernel<128>), grid, dim3(kThreads), 0,
                        (hipStream_t)stream, (const f16 *)q, (const f16 *)k,
                        (const f16 *)v, (f16 *)o, (int)heads, (int)seq_q,
                        (int)seq_kv, scale_log2, causal);
   else if (head_dim == 64)
-    hipLaunchKernelGGL((attention_fwd_kernel<64>), grid, dim3(256), 0,
+    hipLaunchKernelGGL((attention_fwd_kernel<64>), grid, dim3(kThreads), 0,
                        (hipStream_t)stream, (const f16 *)q, (const f16 *)k,
                        (const f16 *)v, (f16 *)o, (int)heads, (int)seq_q,
                        (int)seq_kv, scale_log2, causal);
