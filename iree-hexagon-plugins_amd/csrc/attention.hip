@@ -20,6 +20,8 @@
 //    the block being computed;
 //  * causal blocks above the diagonal are skipped, the diagonal blocks are
 //    masked, and heavy query blocks are interleaved with light ones.
+#include <type_traits>
+
 #include "device_common.h"
 #include "kernels_internal.h"
 
@@ -29,6 +31,14 @@ namespace {
 constexpr int kBQ = 128;   // query rows per workgroup
 constexpr int kBKV = 64;   // keys per block
 constexpr int kThreads = 256;
+
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>());
+    static_for<N, I + 1>(f);
+  }
+}
 
 // Transposed 8-byte LDS read (ds_read_b64_tr_b16): within each 16-lane
 // block, lane i receives element i%4 of the 8-byte loads of lanes
@@ -40,6 +50,42 @@ __device__ __forceinline__ i32x2 lds_read_tr16(const IHP_LDS char *p) {
   return v;
 }
 __device__ __forceinline__ void tie2(i32x2 &v) { asm volatile("" : "+v"(v)); }
+
+// ds_read_b64_tr_b16 with an immediate byte offset; the caller waits with
+// lgkm_wait<N>() and ties the result before use.
+template <int OFF>
+__device__ __forceinline__ i32x2 lds_read_tr16_at(const IHP_LDS char *p) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset range");
+  i32x2 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
+               : "=v"(v)
+               : "v"((unsigned)(uintptr_t)p), "i"(OFF));
+  return v;
+}
+
+// x[l % 32] op x[l % 32 + 32] in every lane l (the two lane halves hold
+// different keys of the same query row). v_permlane32_swap_b32 exchanges
+// lanes 32..63 of its first operand with lanes 0..31 of its second: with
+// both set to x, one then holds x[0..31] twice and the other x[32..63]
+// twice. Issued as asm with both operands tied: the compiler's builtin for
+// it maps both results to one register. s_nop 1 covers the VALU-write ->
+// permlane-read wait states the compiler inserts before it.
+__device__ __forceinline__ void half_swap(float x, float &lo, float &hi) {
+  lo = x;
+  hi = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1"
+               : "+v"(lo), "+v"(hi));
+}
+__device__ __forceinline__ float pair_max(float x) {
+  float a, b;
+  half_swap(x, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  float a, b;
+  half_swap(x, a, b);
+  return a + b;
+}
 }  // namespace
 
 // K and V blocks are copied HBM -> LDS with global_load_lds into a two-slot
@@ -139,9 +185,18 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
   // kstart = 32t + 16h + 4g .. +3 and kstart + 8 .. +11 (the order the S^T
   // registers hold them in). Load lane j = lane % 16 of block b = lane / 16
   // reads row kstart + j/4, d = 32 dt + 16 (b % 2) + 4 (j % 4) .. +3.
+  // The swizzle of rows kstart + j/4 (+ 8) depends only on j/4, so each d
+  // tile's read address is one per-lane offset; key step (t, h) and the +8
+  // row half are immediate offsets.
   const int vj = lane & 15, vb = lane >> 4;
-  const int v_row_in = vj >> 2;                       // + kstart
-  const int v_dbyte = 2 * (16 * (vb & 1) + 4 * (vj & 3));  // + 64 dt
+  const int v_row_in = vj >> 2;
+  int v_off[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    const int b0 = 64 * dt + 2 * (16 * (vb & 1) + 4 * (vj & 3));
+    v_off[dt] = (4 * g + v_row_in) * ROW +
+                (((b0 >> 4) ^ v_swizzle<D>(v_row_in)) << 4) + (b0 & 15);
+  }
 
   f32x16 o[DT];
 #pragma unroll
@@ -214,7 +269,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
           mx = fmaxf(mx, st[t][r]);
       mx *= scale_log2;
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = pair_max(mx);
     const float m_new = fmaxf(m_run, mx);
     // A row with every key masked so far keeps m = -inf; exp2 of a finite
     // offset from it must not produce nan.
@@ -229,7 +284,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
         st[t][r] = p;
         psum += p;
       }
-    psum += __shfl_xor(psum, 32);
+    psum = pair_sum(psum);
     l_run = l_run * alpha + psum;
     m_run = m_new;
     // rescale the running output only when some row's max moved
@@ -241,36 +296,42 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
           o[t][r] *= alpha;
     }
 
-    // O^T[d][q] += V^T[d][key] P^T[key][q], 16 keys per MFMA.
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        f16x8 pf;
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          pf[e] = (f16)st[t][8 * h + e];
-        const i32x4 pb = __builtin_bit_cast(i32x4, pf);
-        const int kstart = 32 * t + 16 * h + 4 * g;
-        const int r0 = kstart + v_row_in, r1 = r0 + 8;
-        // all 2 x DT transposed reads of this key step under one wait
-        i32x2 lo[DT], hi[DT];
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const int b0 = 64 * dt + v_dbyte, c0 = b0 >> 4, w0 = b0 & 15;
-          lo[dt] = lds_read_tr16(vs + r0 * ROW + ((c0 ^ v_swizzle<D>(r0)) << 4) + w0);
-          hi[dt] = lds_read_tr16(vs + r1 * ROW + ((c0 ^ v_swizzle<D>(r1)) << 4) + w0);
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          tie2(lo[dt]);
-          tie2(hi[dt]);
-          const i32x4 vf = i32x4{lo[dt][0], lo[dt][1], hi[dt][0], hi[dt][1]};
-          o[dt] = Mfma32<f16>::mma(vf, pb, o[dt]);
-        }
+    // O^T[d][q] += V^T[d][key] P^T[key][q], 16 keys per MFMA; the V^T
+    // reads of key step i+1 are in flight during the MFMAs of step i.
+    i32x2 vr[2][DT][2];
+    auto read_v = [&](auto step, i32x2 (&dst)[DT][2]) {
+      constexpr int ST = decltype(step)::value;  // (t, h) = (ST / 2, ST % 2)
+      constexpr int KOFF = 16 * ST * ROW;
+      static_for<DT>([&](auto dt) {
+        constexpr int DTI = decltype(dt)::value;
+        dst[DTI][0] = lds_read_tr16_at<KOFF>(vs + v_off[DTI]);
+        dst[DTI][1] = lds_read_tr16_at<KOFF + 8 * ROW>(vs + v_off[DTI]);
+      });
+    };
+    read_v(std::integral_constant<int, 0>(), vr[0]);
+    static_for<4>([&](auto step) {
+      constexpr int ST = decltype(step)::value;
+      constexpr int CUR = ST & 1;
+      if constexpr (ST + 1 < 4) {
+        read_v(std::integral_constant<int, ST + 1>(), vr[CUR ^ 1]);
+        lgkm_wait<2 * DT>();
+      } else {
+        lgkm_wait<0>();
       }
-    }
+      f16x8 pf;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        pf[e] = (f16)st[ST >> 1][8 * (ST & 1) + e];
+      const i32x4 pb = __builtin_bit_cast(i32x4, pf);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        tie2(vr[CUR][dt][0]);
+        tie2(vr[CUR][dt][1]);
+        const i32x4 vf = i32x4{vr[CUR][dt][0][0], vr[CUR][dt][0][1],
+                               vr[CUR][dt][1][0], vr[CUR][dt][1][1]};
+        o[dt] = Mfma32<f16>::mma(vf, pb, o[dt]);
+      }
+    });
   }
 
   if (my_q >= seq_q)
