@@ -109,6 +109,11 @@ iree_mi355x_executable_library_query(
 //  "w8a16_matmul" same constants   bindings: x w scale y
 //  "attention_f16" constants: batch heads seq_q seq_kv head_dim
 //                 scale_bits(f32) flags   bindings: q k v o
+//  "batch_matmul_f16" constants: the matmul_f16 ones, then batch_lo batch_hi
+//                 stride_a_lo/hi stride_b_lo/hi stride_c_lo/hi activation
+//                 epilogue_bindings (bit 0 bias, bit 1 multiplier)
+//                 ld_multiplier_lo/hi batch_stride_multiplier_lo/hi
+//                 bindings: a b c [bias] [multiplier]
 
 #ifdef __cplusplus
 }  // extern "C"

@@ -80,6 +80,52 @@ int iree_mi355x_matmul_f16(const void *a, const void *b, void *c, int64_t m,
                            int64_t ldc, uint32_t flags, void *workspace,
                            size_t workspace_bytes, void *stream);
 
+// Activations of the fused epilogue.
+#define IREE_MI355X_ACT_NONE 0u
+#define IREE_MI355X_ACT_RELU 1u
+// 0.5 v (1 + tanh(0.7978845608 (v + 0.044715 v^3))), the GELU form of the
+// reference's epilogue-fusion test (plugins/compiler/hexagon/test/codegen/
+// pipelines/hexagon_hmx_epilogue_keeps_config.mlir).
+#define IREE_MI355X_ACT_GELU_TANH 2u
+#define IREE_MI355X_ACT_SILU 3u  // v / (1 + e^-v)
+
+// Elementwise epilogue fused into a matmul's store, computed in f32 on the
+// f32 accumulator and rounded once:
+//   out[m][n] = [C_init[m][n] +] multiplier[m][n] * act(acc[m][n] + bias[n])
+// (the linalg.generic consumers the reference fuses after a matmul: bias add,
+// activation, gating multiply, e.g. a GeGLU gate). Every member is optional:
+// a NULL pointer drops its term.
+typedef struct iree_mi355x_epilogue_t {
+  const void *bias;        // f16 [N], shared by every row and batch
+  const void *multiplier;  // f16 [M, N] per batch, row pitch ld_multiplier
+  int64_t ld_multiplier;
+  int64_t batch_stride_multiplier;  // elements between batches (0 = shared)
+  uint32_t activation;              // IREE_MI355X_ACT_*
+} iree_mi355x_epilogue_t;
+
+// Strided batched f16 matmul with an optional fused epilogue
+// (linalg.batch_matmul, e.g. LIT/integration/hmx_batched_matmul.mlir and the
+// micro model batch-matmul-4x1024x1024x128): for b in [0, batch),
+//   C + b*stride_c = epilogue(A + b*stride_a . B + b*stride_b)
+// with the layouts and flags of iree_mi355x_matmul_f16. Strides are in
+// elements; stride_a or stride_b 0 shares one operand across the batch
+// (broadcast weights), stride_c must separate the outputs. batch <= 65535.
+// iree_mi355x_matmul_f16 is this call with batch 1 and no epilogue.
+int iree_mi355x_batch_matmul_f16(const void *a, const void *b, void *c,
+                                 int64_t batch, int64_t m, int64_t n,
+                                 int64_t k, int64_t lda, int64_t ldb,
+                                 int64_t ldc, int64_t stride_a,
+                                 int64_t stride_b, int64_t stride_c,
+                                 uint32_t flags,
+                                 const iree_mi355x_epilogue_t *epilogue,
+                                 void *workspace, size_t workspace_bytes,
+                                 void *stream);
+
+// Workspace a batch_matmul_f16 call of this shape needs (0 if none).
+size_t iree_mi355x_batch_matmul_workspace_bytes(int64_t batch, int64_t m,
+                                                int64_t n, int64_t k,
+                                                uint32_t flags);
+
 // i8 x i8 -> i32 matmul, exact (linalg.matmul i8,i8->i32 or
 // linalg.quantized_matmul with zero points 0). Same layouts and flags as
 // iree_mi355x_matmul_f16 except OUT_F32. The reference has no accelerator

@@ -51,6 +51,7 @@ typedef struct iree_mi355x_matmul_desc_t {
   int32_t has_scale;         // per-column f16 scale (W8A16)
   int64_t lds_budget_bytes;  // per-workgroup LDS budget (default 160 KiB)
   int32_t num_cus;           // CUs the tiles spread over (default 256)
+  int64_t batch;             // matrices per dispatch (default 1)
 } iree_mi355x_matmul_desc_t;
 
 typedef struct iree_mi355x_matmul_plan_t {
@@ -69,7 +70,7 @@ typedef struct iree_mi355x_matmul_plan_t {
 } iree_mi355x_matmul_plan_t;
 
 // Fills defaults: both operands assumed 16-byte aligned, no scale, 160 KiB
-// LDS, 256 CUs.
+// LDS, 256 CUs, batch 1.
 void iree_mi355x_matmul_desc_init(iree_mi355x_matmul_desc_t *desc,
                                   int32_t a_elem, int32_t b_elem,
                                   int32_t c_elem, int64_t m, int64_t n,

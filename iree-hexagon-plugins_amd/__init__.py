@@ -57,8 +57,23 @@ EXPORTED_SYMBOLS = (
     "iree_mi355x_matmul_desc_init", "iree_mi355x_classify_matmul",
     "iree_mi355x_plan_matmul", "iree_mi355x_mfma_config_count",
     "iree_mi355x_mfma_config_info", "iree_mi355x_matmul_mfma_config",
-    "iree_mi355x_executable_library_query",
+    "iree_mi355x_executable_library_query", "iree_mi355x_batch_matmul_f16",
+    "iree_mi355x_batch_matmul_workspace_bytes",
 )
+
+# Activations of the fused matmul epilogue (include/iree_mi355x_kernels.h).
+ACT_NONE, ACT_RELU, ACT_GELU_TANH, ACT_SILU = 0, 1, 2, 3
+_ACT_NAMES = {None: ACT_NONE, "none": ACT_NONE, "relu": ACT_RELU,
+              "gelu_tanh": ACT_GELU_TANH, "gelu": ACT_GELU_TANH,
+              "silu": ACT_SILU}
+
+
+class Epilogue(ctypes.Structure):
+    """iree_mi355x_epilogue_t."""
+    _fields_ = [("bias", ctypes.c_void_p), ("multiplier", ctypes.c_void_p),
+                ("ld_multiplier", ctypes.c_int64),
+                ("batch_stride_multiplier", ctypes.c_int64),
+                ("activation", ctypes.c_uint32)]
 
 
 class MI355XError(RuntimeError):
@@ -74,7 +89,7 @@ class MatmulDesc(ctypes.Structure):
                 ("flags", ctypes.c_uint32), ("a_aligned16", ctypes.c_int32),
                 ("b_aligned16", ctypes.c_int32), ("has_scale", ctypes.c_int32),
                 ("lds_budget_bytes", ctypes.c_int64),
-                ("num_cus", ctypes.c_int32)]
+                ("num_cus", ctypes.c_int32), ("batch", ctypes.c_int64)]
 
 
 class MatmulPlan(ctypes.Structure):
@@ -163,6 +178,12 @@ def library():
                                               i64, ctypes.c_float, u32, p]
     lib.iree_mi355x_matmul_workspace_bytes.restype = sz
     lib.iree_mi355x_matmul_workspace_bytes.argtypes = [i64, i64, i64, u32]
+    lib.iree_mi355x_batch_matmul_f16.argtypes = [
+        p, p, p, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, u32,
+        ctypes.POINTER(Epilogue), p, sz, p]
+    lib.iree_mi355x_batch_matmul_workspace_bytes.restype = sz
+    lib.iree_mi355x_batch_matmul_workspace_bytes.argtypes = [i64, i64, i64,
+                                                             i64, u32]
     lib.iree_mi355x_last_error.restype = ctypes.c_char_p
     lib.iree_mi355x_version.restype = ctypes.c_char_p
     lib.iree_mi355x_matmul_desc_init.restype = None
@@ -199,10 +220,11 @@ def _check(status: int) -> None:
 # ------------------------------------------------------------------ planner --
 
 def make_desc(a_elem, b_elem, c_elem, m, n, k, flags=0, *, has_scale=False,
-              aligned=True, lds_budget_bytes=None) -> MatmulDesc:
+              aligned=True, lds_budget_bytes=None, batch=1) -> MatmulDesc:
     d = MatmulDesc()
     library().iree_mi355x_matmul_desc_init(ctypes.byref(d), a_elem, b_elem,
                                            c_elem, m, n, k, flags)
+    d.batch = batch
     d.has_scale = int(has_scale)
     d.a_aligned16 = d.b_aligned16 = int(aligned)
     if lds_budget_bytes is not None:
@@ -288,6 +310,19 @@ def matmul_constants(m, n, k, lda, ldb, ldc, flags):
     return words + [flags]
 
 
+def batch_matmul_constants(m, n, k, lda, ldb, ldc, flags, batch, stride_a,
+                           stride_b, stride_c, activation=ACT_NONE,
+                           has_bias=False, has_multiplier=False,
+                           ld_multiplier=0, batch_stride_multiplier=0):
+    words = matmul_constants(m, n, k, lda, ldb, ldc, flags)
+    for v in (batch, stride_a, stride_b, stride_c):
+        words += [v & 0xFFFFFFFF, (v >> 32) & 0xFFFFFFFF]
+    words += [activation, (1 if has_bias else 0) | (2 if has_multiplier else 0)]
+    for v in (ld_multiplier, batch_stride_multiplier):
+        words += [v & 0xFFFFFFFF, (v >> 32) & 0xFFFFFFFF]
+    return words
+
+
 def attention_constants(batch, heads, seq_q, seq_kv, head_dim, scale, flags):
     scale_bits = struct.unpack("<I", struct.pack("<f", scale))[0]
     return [batch, heads, seq_q, seq_kv, head_dim, scale_bits, flags]
@@ -301,14 +336,15 @@ def _stream_ptr(stream=None):
     return s.cuda_stream
 
 
-def _require(t, dtype, name):
+def _require(t, dtype, name, dims=(2,)):
     import torch
     if not isinstance(t, torch.Tensor) or not t.is_cuda:
         raise TypeError(f"{name} must be a device tensor")
     if t.dtype != dtype:
         raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
-    if t.dim() != 2 or t.stride(1) != 1:
-        raise ValueError(f"{name} must be 2-D with unit column stride")
+    if t.dim() not in dims or t.stride(-1) != 1:
+        raise ValueError(f"{name} must be {'/'.join(map(str, dims))}-D with "
+                         "unit column stride")
 
 
 def matmul(a, b, c=None, *, b_transposed=False, accumulate=False,
@@ -353,6 +389,91 @@ def matmul(a, b, c=None, *, b_transposed=False, accumulate=False,
                                           b.stride(0), c.stride(0), flags,
                                           None, 0, s))
     return c
+
+
+def _epilogue(bias, activation, multiplier, m, n, batch):
+    import torch
+    act = _ACT_NAMES[activation] if not isinstance(activation, int) else activation
+    if bias is None and multiplier is None and act == ACT_NONE:
+        return None
+    e = Epilogue()
+    e.activation = act
+    if bias is not None:
+        _require(bias, torch.float16, "bias", (1,))
+        if bias.numel() != n or not bias.is_contiguous():
+            raise ValueError("bias must be a contiguous f16 vector of N")
+        e.bias = bias.data_ptr()
+    if multiplier is not None:
+        _require(multiplier, torch.float16, "multiplier", (2, 3))
+        if multiplier.shape[-2:] != (m, n) or multiplier.stride(-1) != 1:
+            raise ValueError("multiplier must be [.., M, N] with unit column stride")
+        e.multiplier = multiplier.data_ptr()
+        e.ld_multiplier = multiplier.stride(-2)
+        e.batch_stride_multiplier = (multiplier.stride(0)
+                                     if multiplier.dim() == 3 else 0)
+        if multiplier.dim() == 3 and multiplier.shape[0] != batch:
+            raise ValueError("multiplier batch differs")
+    return e
+
+
+def batch_matmul(a, b, c=None, *, b_transposed=False, accumulate=False,
+                 out_dtype=None, bias=None, activation=None, multiplier=None,
+                 stream=None):
+    """linalg.batch_matmul (f16, f32 accumulation) with a fused epilogue:
+    C[z] = [C[z] +] multiplier[z] * act(A[z] . B[z] + bias).
+
+    a: [Z, M, K] (or [M, K] shared); b: [Z, K, N] / [Z, N, K] with
+    ``b_transposed`` (or 2-D, shared by the batch); bias [N]; multiplier
+    [Z, M, N] or [M, N]; activation None / "relu" / "gelu_tanh" / "silu".
+    Every matrix needs a unit column stride; batch strides may be 0.
+    """
+    import torch
+    lib = library()
+    _require(a, torch.float16, "a", (2, 3))
+    _require(b, torch.float16, "b", (2, 3))
+    out_dtype = out_dtype or torch.float16
+    a3 = a if a.dim() == 3 else a.unsqueeze(0)
+    b3 = b if b.dim() == 3 else b.unsqueeze(0)
+    batch = max(a3.shape[0], b3.shape[0])
+    if a.dim() == 2 and b.dim() == 2:
+        batch = 1
+    m, k = a3.shape[1], a3.shape[2]
+    n = b3.shape[1] if b_transposed else b3.shape[2]
+    if (b3.shape[2] if b_transposed else b3.shape[1]) != k:
+        raise ValueError("contraction extents differ")
+    for t, name in ((a3, "a"), (b3, "b")):
+        if t.shape[0] not in (1, batch) or t.stride(-1) != 1:
+            raise ValueError(f"{name}: batch extent or column stride unsupported")
+    sa = 0 if a.dim() == 2 or a3.shape[0] == 1 else a3.stride(0)
+    sb = 0 if b.dim() == 2 or b3.shape[0] == 1 else b3.stride(0)
+    if c is None:
+        if accumulate:
+            raise ValueError("accumulate needs an init tensor c")
+        c = torch.empty((batch, m, n) if (a.dim() == 3 or b.dim() == 3) else (m, n),
+                        dtype=out_dtype, device=a.device)
+    else:
+        _require(c, out_dtype, "c", (2, 3))
+    c3 = c if c.dim() == 3 else c.unsqueeze(0)
+    sc = c3.stride(0) if batch > 1 else m * n
+    flags = ((B_TRANSPOSED if b_transposed else 0) |
+             (ACCUMULATE if accumulate else 0) |
+             (OUT_F32 if out_dtype == torch.float32 else 0))
+    e = _epilogue(bias, activation, multiplier, m, n, batch)
+    _check(lib.iree_mi355x_batch_matmul_f16(
+        a3.data_ptr(), b3.data_ptr(), c3.data_ptr(), batch, m, n, k,
+        a3.stride(1), b3.stride(1), c3.stride(1), sa, sb, sc, flags,
+        ctypes.byref(e) if e is not None else None, None, 0,
+        _stream_ptr(stream)))
+    return c
+
+
+def linear(x, w, bias=None, *, activation=None, multiplier=None,
+           w_transposed=False, out=None, stream=None):
+    """y = multiplier * act(x . W + bias) for x [M, K], W [K, N] (or [N, K]
+    with ``w_transposed``): one dispatch, epilogue fused into the store."""
+    return batch_matmul(x, w, out, b_transposed=w_transposed, bias=bias,
+                        activation=activation, multiplier=multiplier,
+                        stream=stream)
 
 
 def quantized_matmul(x, w, scale, y=None, *, w_transposed=False, stream=None):

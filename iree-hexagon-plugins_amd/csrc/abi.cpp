@@ -185,6 +185,59 @@ size_t iree_mi355x_matmul_workspace_bytes(int64_t m, int64_t n, int64_t k,
   return most;
 }
 
+}  // extern "C"
+
+namespace ihp {
+
+// f16 matmul of `args` (batch and epilogue included): plan, workspace,
+// launch. Shapes and pointers are validated by the caller.
+static int matmul_f16_run(const char *who, MatmulArgs &args, uint32_t flags,
+                          void *workspace, size_t workspace_bytes) {
+  const bool out_f32 = flags & IREE_MI355X_MATMUL_OUT_F32;
+  iree_mi355x_matmul_desc_t desc;
+  iree_mi355x_matmul_desc_init(&desc, IREE_MI355X_ELEM_F16,
+                               IREE_MI355X_ELEM_F16,
+                               out_f32 ? IREE_MI355X_ELEM_F32
+                                       : IREE_MI355X_ELEM_F16,
+                               args.m, args.n, args.k, flags);
+  desc.a_aligned16 = aligned(args.a, 16) && (args.lda * 2) % 16 == 0 &&
+                     (args.sa * 2) % 16 == 0;
+  desc.b_aligned16 = aligned(args.b, 16) && (args.ldb * 2) % 16 == 0 &&
+                     (args.sb * 2) % 16 == 0;
+  desc.batch = args.batch;
+  iree_mi355x_matmul_plan_t plan;
+  if (iree_mi355x_plan_matmul(&desc, &plan) != IREE_MI355X_OK)
+    return fail(IREE_MI355X_UNSUPPORTED, "%s: no plan", who);
+  int st;
+  switch (plan.family) {
+    case IREE_MI355X_FAMILY_GEMV: {
+      void *ws = workspace;
+      if (plan.workspace_bytes > 0) {
+        if (ws && workspace_bytes < (size_t)plan.workspace_bytes)
+          return fail(IREE_MI355X_WORKSPACE_TOO_SMALL,
+                      "%s: workspace %zu < %zu", who, workspace_bytes,
+                      (size_t)plan.workspace_bytes);
+        if (!ws && (st = library_workspace(plan.workspace_bytes, &ws)) !=
+                       IREE_MI355X_OK)
+          return st;
+      }
+      return launch_status(launch_gemv(args, 2, nullptr, out_f32, ws),
+                           "gemv_f16");
+    }
+    case IREE_MI355X_FAMILY_MFMA:
+      return launch_mfma(args, plan, workspace, workspace_bytes, who);
+    default:
+      return launch_status(
+          launch_general(args, out_f32 ? kGeneralF16F32 : kGeneralF16F16,
+                         nullptr),
+          "gemm_general_f16");
+  }
+}
+
+}  // namespace ihp
+
+extern "C" {
+
 int iree_mi355x_matmul_f16(const void *a, const void *b, void *c, int64_t m,
                            int64_t n, int64_t k, int64_t lda, int64_t ldb,
                            int64_t ldc, uint32_t flags, void *workspace,
@@ -200,40 +253,82 @@ int iree_mi355x_matmul_f16(const void *a, const void *b, void *c, int64_t m,
   MatmulArgs args{a, b, c, m, n, k, lda, ldb, ldc,
                   (flags & IREE_MI355X_MATMUL_B_TRANSPOSED) ? 1 : 0,
                   (flags & IREE_MI355X_MATMUL_ACCUMULATE) ? 1 : 0, stream};
-  iree_mi355x_matmul_desc_t desc;
-  iree_mi355x_matmul_desc_init(&desc, IREE_MI355X_ELEM_F16,
-                               IREE_MI355X_ELEM_F16,
-                               out_f32 ? IREE_MI355X_ELEM_F32
-                                       : IREE_MI355X_ELEM_F16,
-                               m, n, k, flags);
-  desc.a_aligned16 = aligned(a, 16) && (lda * 2) % 16 == 0;
-  desc.b_aligned16 = aligned(b, 16) && (ldb * 2) % 16 == 0;
-  iree_mi355x_matmul_plan_t plan;
-  if (iree_mi355x_plan_matmul(&desc, &plan) != IREE_MI355X_OK)
-    return fail(IREE_MI355X_UNSUPPORTED, "matmul_f16: no plan");
-  switch (plan.family) {
-    case IREE_MI355X_FAMILY_GEMV: {
-      void *ws = workspace;
-      if (plan.workspace_bytes > 0) {
-        if (ws && workspace_bytes < plan.workspace_bytes)
-          return fail(IREE_MI355X_WORKSPACE_TOO_SMALL,
-                      "matmul_f16: workspace %zu < %zu", workspace_bytes,
-                      (size_t)plan.workspace_bytes);
-        if (!ws && (st = library_workspace(plan.workspace_bytes, &ws)) !=
-                       IREE_MI355X_OK)
-          return st;
-      }
-      return launch_status(launch_gemv(args, 2, nullptr, out_f32, ws),
-                           "gemv_f16");
-    }
-    case IREE_MI355X_FAMILY_MFMA:
-      return launch_mfma(args, plan, workspace, workspace_bytes, "matmul_f16");
-    default:
-      return launch_status(
-          launch_general(args, out_f32 ? kGeneralF16F32 : kGeneralF16F16,
-                         nullptr),
-          "gemm_general_f16");
+  return matmul_f16_run("matmul_f16", args, flags, workspace,
+                        workspace_bytes);
+}
+
+int iree_mi355x_batch_matmul_f16(const void *a, const void *b, void *c,
+                                 int64_t batch, int64_t m, int64_t n,
+                                 int64_t k, int64_t lda, int64_t ldb,
+                                 int64_t ldc, int64_t stride_a,
+                                 int64_t stride_b, int64_t stride_c,
+                                 uint32_t flags,
+                                 const iree_mi355x_epilogue_t *epilogue,
+                                 void *workspace, size_t workspace_bytes,
+                                 void *stream) {
+  const char *who = "batch_matmul_f16";
+  const bool out_f32 = flags & IREE_MI355X_MATMUL_OUT_F32;
+  if (batch < 0 || stride_a < 0 || stride_b < 0 || stride_c < 0)
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: negative batch or stride",
+                who);
+  if (batch > 65535)
+    return fail(IREE_MI355X_UNSUPPORTED, "%s: batch %lld > 65535", who,
+                (long long)batch);
+  int st = check_matmul(who, a, b, c, m, n, k, lda, ldb, ldc, flags,
+                        IREE_MI355X_MATMUL_B_TRANSPOSED |
+                            IREE_MI355X_MATMUL_ACCUMULATE |
+                            IREE_MI355X_MATMUL_OUT_F32,
+                        2, 2, out_f32 ? 4 : 2);
+  if (st != IREE_MI355X_OK || m == 0 || n == 0 || batch == 0)
+    return st == IREE_MI355X_OK ? ok() : st;
+  if (batch > 1 && stride_c < (m - 1) * ldc + n)
+    return fail(IREE_MI355X_INVALID_ARGUMENT,
+                "%s: stride_c %lld overlaps the outputs of consecutive "
+                "batches", who, (long long)stride_c);
+  MatmulArgs args{a, b, c, m, n, k, lda, ldb, ldc,
+                  (flags & IREE_MI355X_MATMUL_B_TRANSPOSED) ? 1 : 0,
+                  (flags & IREE_MI355X_MATMUL_ACCUMULATE) ? 1 : 0, stream};
+  args.batch = batch;
+  args.sa = stride_a;
+  args.sb = stride_b;
+  args.sc = stride_c;
+  if (epilogue) {
+    if (epilogue->activation > IREE_MI355X_ACT_SILU)
+      return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: unknown activation %u",
+                  who, epilogue->activation);
+    if ((epilogue->bias && !aligned(epilogue->bias, 2)) ||
+        (epilogue->multiplier && !aligned(epilogue->multiplier, 2)))
+      return fail(IREE_MI355X_MISALIGNED, "%s: epilogue operand misaligned",
+                  who);
+    if (epilogue->multiplier && (epilogue->ld_multiplier < n ||
+                                 epilogue->batch_stride_multiplier < 0))
+      return fail(IREE_MI355X_INVALID_ARGUMENT,
+                  "%s: multiplier pitch smaller than the row", who);
+    args.bias = epilogue->bias;
+    args.mul = epilogue->multiplier;
+    args.ld_mul = epilogue->ld_multiplier;
+    args.s_mul = epilogue->batch_stride_multiplier;
+    args.act = (int)epilogue->activation;
   }
+  return matmul_f16_run(who, args, flags, workspace, workspace_bytes);
+}
+
+size_t iree_mi355x_batch_matmul_workspace_bytes(int64_t batch, int64_t m,
+                                                int64_t n, int64_t k,
+                                                uint32_t flags) {
+  if (batch <= 0 || m <= 0 || n <= 0 || k <= 0)
+    return 0;
+  iree_mi355x_matmul_desc_t d;
+  iree_mi355x_matmul_desc_init(
+      &d, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16,
+      (flags & IREE_MI355X_MATMUL_OUT_F32) ? IREE_MI355X_ELEM_F32
+                                           : IREE_MI355X_ELEM_F16,
+      m, n, k, flags);
+  d.batch = batch;
+  iree_mi355x_matmul_plan_t p;
+  if (iree_mi355x_plan_matmul(&d, &p) != IREE_MI355X_OK)
+    return 0;
+  return (size_t)p.workspace_bytes;
 }
 
 int iree_mi355x_matmul_i8(const int8_t *a, const int8_t *b, int32_t *c,

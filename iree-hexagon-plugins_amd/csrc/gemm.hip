@@ -117,7 +117,8 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     const f16 *__restrict__ scale, int M, int N, int K, int64_t lda,
     int64_t ldb, int64_t ldc, int accumulate, int k_split,
     typename Mfma32<T>::AccScalar *__restrict__ partials,
-    unsigned *__restrict__ counters) {
+    unsigned *__restrict__ counters, int64_t sa, int64_t sb, int64_t sc,
+    Epi epi, int64_t s_mul) {
   typedef Mfma32<T> MF;
   typedef typename MF::Acc Acc;
   constexpr bool kNN = BMODE != kBTN;
@@ -159,6 +160,24 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   static_assert(STAGES * STAGE_BYTES <= 160 * 1024, "LDS budget");
 
   __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE_BYTES];
+
+  // Batch z: this workgroup's matrices, partials and counters. No branch on
+  // a kernel argument here: each one would serialize another round of
+  // kernel-argument loads ahead of the first copy. (s_mul is 0 without a
+  // multiplier; one split has no partials, so zs only keeps those pointers
+  // unmoved.)
+  {
+    const int64_t z = blockIdx.z;
+    A += z * sa;
+    Bv = (const char *)Bv + z * sb * TBB;
+    C += z * sc;
+    epi.mul += z * s_mul;
+    if constexpr (SPLIT) {
+      const int64_t zs = gridDim.y > 1 ? z : 0;
+      partials += zs * (int64_t)gridDim.y * M * N;
+      counters += zs * gridDim.x;
+    }
+  }
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -406,7 +425,47 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   // for f16 outputs.
   const int col_l = lane & 31;
   const int row_l = 4 * (lane >> 5);
-  if constexpr (!SPLIT) {
+  constexpr bool kIntOut = std::is_same<OutT, int32_t>::value;
+  if constexpr (!kIntOut) {
+    if ((!SPLIT || gridDim.y == 1) && !epi_plain(epi)) {
+      // Fused epilogue: each 32-row fragment band of a wave goes through
+      // LDS (the idle stage ring) column-major with a 33-float pitch, then
+      // one rolled loop applies scale / bias / activation / multiplier and
+      // stores whole rows, so the epilogue is instanced once per band
+      // instead of once per accumulator register.
+      constexpr int PITCH = 33;
+      static_assert(WM * WN * WTN * PITCH * 4 <= STAGES * STAGE_BYTES,
+                    "epilogue staging");
+      float *stage = (float *)smem + wave * WTN * PITCH;
+      const int64_t row0 = m0 + wm * WTM, col0 = n0 + wn * WTN;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        __syncthreads();  // LDS ring (or the previous band) fully read
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            stage[(j * 32 + col_l) * PITCH + row_l + 8 * (r >> 2) +
+                  (r & 3)] = (float)acc[i][j][r];
+        __syncthreads();
+        for (int t = lane; t < 32 * WTN; t += 64) {
+          const int rr = t / WTN, cc = t % WTN;
+          const int64_t row = row0 + i * 32 + rr, col = col0 + cc;
+          if (SPLIT && row >= M)
+            continue;
+          float v = stage[cc * PITCH + rr];
+          if constexpr (BMODE == kBW8)
+            v *= (float)scale[col];
+          store_out(C + row * ldc + col, epi_apply(v, row, col, epi),
+                    accumulate);
+        }
+      }
+      return;
+    }
+  }
+  // One split (a ragged-M shape whose tiles alone cover the CUs): store
+  // directly, rows past M masked, no partials.
+  if (!SPLIT || gridDim.y == 1) {
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       OutT *crow = C + (m0 + wm * WTM + i * 32 + row_l) * ldc + n0 +
@@ -418,12 +477,19 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
           sc = (float)scale[n0 + wn * WTN + j * 32 + col_l];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          if constexpr (BMODE == kBW8)
-            store_out(crow + (8 * (r >> 2) + (r & 3)) * ldc + j * 32,
-                      (float)acc[i][j][r] * sc, 0);
-          else
-            store_out(crow + (8 * (r >> 2) + (r & 3)) * ldc + j * 32,
-                      acc[i][j][r], accumulate);
+          OutT *dst = crow + (8 * (r >> 2) + (r & 3)) * ldc + j * 32;
+          const int64_t row =
+              m0 + wm * WTM + i * 32 + row_l + 8 * (r >> 2) + (r & 3);
+          if (SPLIT && row >= M)
+            continue;
+          if constexpr (kIntOut) {
+            store_out(dst, acc[i][j][r], accumulate);
+          } else {
+            float v = (float)acc[i][j][r];
+            if constexpr (BMODE == kBW8)
+              v *= sc;
+            store_out(dst, v, accumulate);
+          }
         }
       }
     }
@@ -469,45 +535,59 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     const int rows_valid = (int)(M - m0 < BM ? M - m0 : BM);
     const int count = rows_valid * BN;
     constexpr int G = 8, SB = 8;
-    for (int base = 0; base < count; base += NT * G) {
-      P sum[G];
+    // The epilogue choice is made once, outside the loop: a per-element
+    // test of the epilogue fields costs the plain reduction ~10%.
+    auto reduce = [&](auto with_epi) {
+      for (int base = 0; base < count; base += NT * G) {
+        P sum[G];
 #pragma unroll
-      for (int e = 0; e < G; ++e)
-        sum[e] = 0;
-      for (int s0 = 0; s0 < splits; s0 += SB) {
-        P v[G][SB];
+        for (int e = 0; e < G; ++e)
+          sum[e] = 0;
+        for (int s0 = 0; s0 < splits; s0 += SB) {
+          P v[G][SB];
+#pragma unroll
+          for (int e = 0; e < G; ++e) {
+            const int idx = base + e * NT + tid;
+            const int64_t row = m0 + idx / BN, col = n0 + idx % BN;
+            const P *src = partials + ((int64_t)s0 * M + row) * N + col;
+#pragma unroll
+            for (int u = 0; u < SB; ++u)
+              v[e][u] = idx < count && s0 + u < splits
+                            ? load_device(src + (int64_t)u * M * N)
+                            : (P)0;
+          }
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+          for (int e = 0; e < G; ++e)
+#pragma unroll
+            for (int u = 0; u < SB; ++u) {
+              vm_tie(v[e][u]);
+              sum[e] += v[e][u];
+            }
+        }
 #pragma unroll
         for (int e = 0; e < G; ++e) {
           const int idx = base + e * NT + tid;
+          if (idx >= count)
+            continue;
           const int64_t row = m0 + idx / BN, col = n0 + idx % BN;
-          const P *src = partials + ((int64_t)s0 * M + row) * N + col;
-#pragma unroll
-          for (int u = 0; u < SB; ++u)
-            v[e][u] = idx < count && s0 + u < splits
-                          ? load_device(src + (int64_t)u * M * N)
-                          : (P)0;
-        }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#pragma unroll
-        for (int e = 0; e < G; ++e)
-#pragma unroll
-          for (int u = 0; u < SB; ++u) {
-            vm_tie(v[e][u]);
-            sum[e] += v[e][u];
+          if constexpr (kIntOut) {
+            store_out(C + row * ldc + col, sum[e], accumulate);
+          } else {
+            float v = (float)sum[e];
+            if constexpr (BMODE == kBW8)
+              v *= (float)scale[col];
+            if constexpr (decltype(with_epi)::value)
+              v = epi_apply(v, row, col, epi);
+            store_out(C + row * ldc + col, v, accumulate);
           }
+        }
       }
-#pragma unroll
-      for (int e = 0; e < G; ++e) {
-        const int idx = base + e * NT + tid;
-        if (idx >= count)
-          continue;
-        const int64_t row = m0 + idx / BN, col = n0 + idx % BN;
-        if constexpr (BMODE == kBW8)
-          store_out(C + row * ldc + col, (float)sum[e] * (float)scale[col], 0);
-        else
-          store_out(C + row * ldc + col, sum[e], accumulate);
-      }
-    }
+    };
+    if (kIntOut || epi_plain(epi))
+      reduce(std::false_type());
+    else
+      reduce(std::true_type());
     if (tid == 0)  // re-arm for the next call on this workspace
       __hip_atomic_store(&counters[blockIdx.x], 0u, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
@@ -525,7 +605,15 @@ template <typename TA, typename TB, typename OutT, bool kScale>
 __global__ __launch_bounds__(256) void gemm_general_kernel(
     const TA *__restrict__ A, const TB *__restrict__ B, OutT *__restrict__ C,
     const f16 *__restrict__ scale, int M, int N, int K, int64_t lda,
-    int64_t ldb, int64_t ldc, int b_transposed, int accumulate) {
+    int64_t ldb, int64_t ldc, int b_transposed, int accumulate, int64_t sa,
+    int64_t sb, int64_t sc, Epi epi, int64_t s_mul) {
+  {
+    const int64_t z = blockIdx.z;
+    A += z * sa;
+    B += z * sb;
+    C += z * sc;
+    epi.mul += z * s_mul;  // s_mul is 0 without a multiplier
+  }
   // MFMA input type: f16 unless both operands are int8.
   typedef typename MfmaInput<TA, TB>::type TM;
   typedef Mfma32<TM> MF;
@@ -595,10 +683,15 @@ __global__ __launch_bounds__(256) void gemm_general_kernel(
   for (int r = 0; r < 16; ++r) {
     const int64_t row = m0 + wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
     if (row < M) {
-      if (kScale)
-        store_out(C + row * ldc + col, (float)acc[r] * s, accumulate);
-      else
+      if constexpr (std::is_same<OutT, int32_t>::value) {
         store_out(C + row * ldc + col, acc[r], accumulate);
+      } else {
+        float v = (float)acc[r];
+        if (kScale)
+          v *= s;
+        store_out(C + row * ldc + col, epi_apply(v, row, col, epi),
+                  accumulate);
+      }
     }
   }
 }
@@ -621,10 +714,11 @@ static hipError_t launch_fast(const MatmulArgs &a) {
                       : nullptr;
   hipLaunchKernelGGL(
       (gemm_lds_kernel<T, OutT, BM, BN, BKB, WM, WN, STAGES, BMODE, SPLIT>),
-      dim3(tiles, splits), dim3(64 * WM * WN), 0, (hipStream_t)a.stream,
-      (const T *)a.a, a.b, (OutT *)a.c, (const f16 *)a.scale, (int)a.m,
-      (int)a.n, (int)a.k, a.lda, a.ldb, a.ldc, a.accumulate, k_split,
-      partials, counters);
+      dim3(tiles, splits, (unsigned)a.batch), dim3(64 * WM * WN), 0,
+      (hipStream_t)a.stream, (const T *)a.a, a.b, (OutT *)a.c,
+      (const f16 *)a.scale, (int)a.m, (int)a.n, (int)a.k, a.lda, a.ldb, a.ldc,
+      a.accumulate, k_split, partials, counters, a.sa, a.sb, a.sc, make_epi(a),
+      epi_batch_stride(a));
   return hipGetLastError();
 }
 
@@ -692,12 +786,14 @@ const FastConfig *fast_configs(int *count) {
 
 template <typename TA, typename TB, typename OutT, bool kScale>
 static hipError_t launch_general_t(const MatmulArgs &a, const void *scale) {
-  dim3 grid((unsigned)((a.n + 63) / 64), (unsigned)((a.m + 63) / 64));
+  dim3 grid((unsigned)((a.n + 63) / 64), (unsigned)((a.m + 63) / 64),
+            (unsigned)a.batch);
   hipLaunchKernelGGL((gemm_general_kernel<TA, TB, OutT, kScale>), grid,
                      dim3(256), 0, (hipStream_t)a.stream, (const TA *)a.a,
                      (const TB *)a.b, (OutT *)a.c, (const f16 *)scale,
                      (int)a.m, (int)a.n, (int)a.k, a.lda, a.ldb, a.ldc,
-                     a.b_transposed, a.accumulate);
+                     a.b_transposed, a.accumulate, a.sa, a.sb, a.sc,
+                     make_epi(a), epi_batch_stride(a));
   return hipGetLastError();
 }
 

@@ -17,6 +17,8 @@
 //    counter) sums the partials, applies the per-column scale (W8A16), adds
 //    the DPS init if asked, rounds once and re-arms the counter, so the
 //    whole matmul is one launch.
+#include <type_traits>
+
 #include "device_common.h"
 #include "kernels_internal.h"
 
@@ -77,13 +79,24 @@ __global__ __launch_bounds__(kThreads, 1) void gemv_splitk_kernel(
     const f16 *__restrict__ scale, OutT *__restrict__ Y, int N, int K,
     int64_t ldx, int64_t ldw, int64_t ldy, int k_chunk, int rows_per_wave,
     int accumulate, float *__restrict__ partials,
-    unsigned *__restrict__ counters) {
+    unsigned *__restrict__ counters, int64_t sx, int64_t sw, int64_t sy,
+    Epi epi, int64_t s_mul) {
   typedef WTraits<WT> Tr;
   constexpr int CPT = Tr::kCols;
   constexpr int BNC = 64 * CPT;
   __shared__ float red[kWaves][MR][BNC];
   __shared__ unsigned last_flag;
 
+  // Batch z: this workgroup's x, W, y, partials and counters.
+  {
+    const int64_t z = blockIdx.z;
+    X += z * sx;
+    W += z * sw;
+    Y += z * sy;
+    epi.mul += z * s_mul;  // s_mul is 0 without a multiplier
+    partials += z * (int64_t)gridDim.y * MR * N;
+    counters += z * gridDim.x;
+  }
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -171,25 +184,40 @@ __global__ __launch_bounds__(kThreads, 1) void gemv_splitk_kernel(
       red[wave][r][lane * CPT + c] = acc[r][c];
   __syncthreads();
 
+  // Output of one element: scale, fused epilogue (chosen once per
+  // workgroup, outside the loops: testing the epilogue fields per element
+  // slows the plain store), one rounding.
+  auto finish = [&](auto with_epi, float s, int r, int64_t n) {
+    float v = s * (scale ? (float)scale[n] : 1.0f);
+    if constexpr (decltype(with_epi)::value)
+      v = epi_apply(v, r, n, epi);
+    store_y(Y + r * ldy + n, v, accumulate);
+  };
+  const bool plain = epi_plain(epi);
   const bool direct = splits == 1;
-  for (int i = tid; i < MR * BNC; i += kThreads) {
-    const int r = i / BNC, col = i % BNC;
-    const int64_t n = n_base + col;
-    if (n >= N)
-      continue;
-    float s = red[0][r][col];
+  auto first = [&](auto with_epi) {
+    for (int i = tid; i < MR * BNC; i += kThreads) {
+      const int r = i / BNC, col = i % BNC;
+      const int64_t n = n_base + col;
+      if (n >= N)
+        continue;
+      float s = red[0][r][col];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w)
-      s += red[w][r][col];
-    if (direct) {
-      const float sc = scale ? (float)scale[n] : 1.0f;
-      store_y(Y + r * ldy + n, s * sc, accumulate);
-    } else {
-      // Device-scope store: written through past this XCD's L2, so a
-      // workgroup on another XCD reads it with a device-scope load.
-      store_device(&partials[((int64_t)split * MR + r) * N + n], s);
+      for (int w = 1; w < kWaves; ++w)
+        s += red[w][r][col];
+      if (direct) {
+        finish(with_epi, s, r, n);
+      } else {
+        // Device-scope store: written through past this XCD's L2, so a
+        // workgroup on another XCD reads it with a device-scope load.
+        store_device(&partials[((int64_t)split * MR + r) * N + n], s);
+      }
     }
-  }
+  };
+  if (plain)
+    first(std::false_type());
+  else
+    first(std::true_type());
   if (direct)
     return;
 
@@ -207,22 +235,28 @@ __global__ __launch_bounds__(kThreads, 1) void gemv_splitk_kernel(
   __syncthreads();
   if (!last_flag)
     return;
-  for (int i = tid; i < MR * BNC; i += kThreads) {
-    const int r = i / BNC, col = i % BNC;
-    const int64_t n = n_base + col;
-    if (n >= N)
-      continue;
-    const float s = partial_sum<float, kSumBatch>(
-        &partials[(int64_t)r * N + n], (int64_t)MR * N, splits);
-    const float sc = scale ? (float)scale[n] : 1.0f;
-    store_y(Y + r * ldy + n, s * sc, accumulate);
-  }
+  auto last = [&](auto with_epi) {
+    for (int i = tid; i < MR * BNC; i += kThreads) {
+      const int r = i / BNC, col = i % BNC;
+      const int64_t n = n_base + col;
+      if (n >= N)
+        continue;
+      const float s = partial_sum<float, kSumBatch>(
+          &partials[(int64_t)r * N + n], (int64_t)MR * N, splits);
+      finish(with_epi, s, r, n);
+    }
+  };
+  if (plain)
+    last(std::false_type());
+  else
+    last(std::true_type());
   if (tid == 0)  // re-arm for the next call on this workspace
     __hip_atomic_store(&counters[blockIdx.x], 0u, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
-GemvPlan gemv_plan(int64_t m, int64_t n, int64_t k, int w_bytes) {
+GemvPlan gemv_plan(int64_t m, int64_t n, int64_t k, int w_bytes,
+                   int64_t batch) {
   (void)m;
   const int cpt = w_bytes == 2 ? 8 : 16;
   GemvPlan p;
@@ -234,7 +268,8 @@ GemvPlan gemv_plan(int64_t m, int64_t n, int64_t k, int w_bytes) {
   // trips) but leave CUs idle, more add tail latency. Split K so that
   // col_blocks x splits is about that, each wave's run of rows a multiple of
   // the load batch.
-  int64_t want = (kGemvTargetWgs + col_blocks / 2) / col_blocks;
+  const int64_t per_batch = (kGemvTargetWgs + batch - 1) / batch;
+  int64_t want = (per_batch + col_blocks / 2) / col_blocks;
   if (want < 1)
     want = 1;
   int64_t rpw = (k + want * kWaves - 1) / (want * kWaves);
@@ -258,12 +293,13 @@ static size_t counter_bytes(int64_t col_blocks) {
   return kWorkspaceCounterBytes;
 }
 
-size_t gemv_workspace_bytes(int64_t m, int64_t n, int64_t k, int w_bytes) {
-  GemvPlan p = gemv_plan(m, n, k, w_bytes);
+size_t gemv_workspace_bytes(int64_t m, int64_t n, int64_t k, int w_bytes,
+                            int64_t batch) {
+  GemvPlan p = gemv_plan(m, n, k, w_bytes, batch);
   if (p.splits <= 1)
     return 0;
   return counter_bytes(p.col_blocks) +
-         (size_t)p.splits * kGemvMaxRows * (size_t)n * 4;
+         (size_t)batch * p.splits * kGemvMaxRows * (size_t)n * 4;
 }
 
 template <typename WT, int MR, typename OutT>
@@ -273,12 +309,13 @@ static hipError_t launch_gemv_t(const MatmulArgs &a, const void *scale,
   float *partials =
       workspace ? (float *)((char *)workspace + counter_bytes(p.col_blocks))
                 : nullptr;
-  dim3 grid((unsigned)p.col_blocks, (unsigned)p.splits);
+  dim3 grid((unsigned)p.col_blocks, (unsigned)p.splits, (unsigned)a.batch);
   hipLaunchKernelGGL((gemv_splitk_kernel<WT, MR, OutT>), grid, dim3(kThreads),
                      0, (hipStream_t)a.stream, (const f16 *)a.a,
                      (const WT *)a.b, (const f16 *)scale, (OutT *)a.c,
                      (int)a.n, (int)a.k, a.lda, a.ldb, a.ldc, p.k_chunk,
-                     p.rows_per_wave, a.accumulate, partials, counters);
+                     p.rows_per_wave, a.accumulate, partials, counters, a.sa,
+                     a.sb, a.sc, make_epi(a), epi_batch_stride(a));
   return hipGetLastError();
 }
 
@@ -300,7 +337,7 @@ static hipError_t launch_gemv_rows(const MatmulArgs &a, const void *scale,
 
 hipError_t launch_gemv(const MatmulArgs &a, int w_bytes, const void *scale,
                        int out_f32, void *workspace) {
-  const GemvPlan p = gemv_plan(a.m, a.n, a.k, w_bytes);
+  const GemvPlan p = gemv_plan(a.m, a.n, a.k, w_bytes, a.batch);
   if (w_bytes == 2)
     return out_f32 ? launch_gemv_rows<f16, float>(a, nullptr, workspace, p)
                    : launch_gemv_rows<f16, f16>(a, nullptr, workspace, p);

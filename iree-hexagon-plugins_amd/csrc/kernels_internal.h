@@ -30,11 +30,41 @@ struct MatmulArgs {
   void *stream;
   const void *scale;  // W8A16 per-column scale (else NULL)
   // split-K configurations: split count, K elements per split, workspace
-  // ([counter region][partials, splits x M x N accumulators])
+  // ([counter region][partials, batch x splits x M x N accumulators])
   int splits;
   int k_split;
   void *workspace;
+  // Batch (grid z): element strides between consecutive matrices of A, B, C
+  // (0 = one matrix shared by every batch).
+  int64_t batch = 1;
+  int64_t sa = 0, sb = 0, sc = 0;
+  // Fused epilogue (f16 / f32 outputs): out = [C +] mul * act(acc + bias).
+  const void *bias = nullptr;  // f16 [N]
+  const void *mul = nullptr;   // f16 [M, N] per batch, row pitch ld_mul
+  int64_t ld_mul = 0, s_mul = 0;
+  int act = 0;                 // kActNone / kActRelu / kActGeluTanh / kActSilu
 };
+
+enum Activation { kActNone = 0, kActRelu = 1, kActGeluTanh = 2, kActSilu = 3 };
+
+// Device-side view of the fused epilogue; `mul` already points at this
+// batch's matrix.
+struct Epi {
+  const _Float16 *bias;
+  const _Float16 *mul;
+  int64_t ld_mul;
+  int act;
+};
+inline Epi make_epi(const MatmulArgs &a) {
+  return Epi{(const _Float16 *)a.bias, (const _Float16 *)a.mul, a.ld_mul,
+             a.act};
+}
+// Batch stride of the multiplier as the kernels take it: 0 without a
+// multiplier, so a kernel offsets `mul` by z * stride with no branch and a
+// null multiplier stays null.
+inline int64_t epi_batch_stride(const MatmulArgs &a) {
+  return a.mul ? a.s_mul : 0;
+}
 
 // Every workspace starts with one fixed counter region: one u32 arrival
 // counter per tile (split-K GEMM) or column block (GEMV), left at zero by
@@ -87,8 +117,10 @@ struct GemvPlan {
   int rows_per_wave;   // contiguous rows each of the 8 waves streams
   int64_t col_blocks;  // grid x
 };
-GemvPlan gemv_plan(int64_t m, int64_t n, int64_t k, int w_bytes);
-size_t gemv_workspace_bytes(int64_t m, int64_t n, int64_t k, int w_bytes);
+GemvPlan gemv_plan(int64_t m, int64_t n, int64_t k, int w_bytes,
+                   int64_t batch = 1);
+size_t gemv_workspace_bytes(int64_t m, int64_t n, int64_t k, int w_bytes,
+                            int64_t batch = 1);
 // w_bytes = 2: f16 weights (scale == NULL); 1: int8 weights with f16 scale.
 hipError_t launch_gemv(const MatmulArgs &a, int w_bytes, const void *scale,
                        int out_f32, void *workspace);
@@ -112,6 +144,44 @@ template <>
 struct MfmaInput<int8_t, int8_t> {
   typedef int8_t type;
 };
+
+// out = mul[row][col] * act(v + bias[col]), in f32 (the accumulator is not
+// rounded first). GELU is the tanh form the reference's epilogue fusion test
+// computes (plugins/compiler/hexagon/test/codegen/pipelines/
+// hexagon_hmx_epilogue_keeps_config.mlir: 0.5 h (1 + tanh(0.7978 (h + 0.0447
+// h^3)))); SiLU is v / (1 + e^-v).
+//
+// Both smooth activations are v * sigmoid(a): SiLU with a = v, and GELU with
+// a = 2u, since 0.5 (1 + tanh(u)) = 1 / (1 + e^-2u). The sigmoid is one
+// hardware exp2 and one reciprocal (each within ~1 ulp of f32), so the
+// epilogue stays a few instructions; e^-a overflowing to +inf gives 0, and
+// underflowing to 0 gives 1, the limits of the function.
+__device__ __forceinline__ float sigmoid_fast(float a) {
+  const float e = __builtin_amdgcn_exp2f(-a * 1.4426950408889634f);
+  return __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+__device__ __forceinline__ float epi_apply(float v, int64_t row, int64_t col,
+                                           const Epi &e) {
+  if (e.bias)
+    v += (float)e.bias[col];
+  if (e.act == kActRelu) {
+    v = v > 0.0f ? v : 0.0f;
+  } else if (e.act != kActNone) {
+    const float a =
+        e.act == kActGeluTanh
+            ? 1.5957691216057308f * (v + 0.044715f * v * v * v)
+            : v;
+    v *= sigmoid_fast(a);
+  }
+  if (e.mul)
+    v *= (float)e.mul[row * e.ld_mul + col];
+  return v;
+}
+
+__device__ __forceinline__ bool epi_plain(const Epi &e) {
+  return !e.bias && !e.mul && e.act == kActNone;
+}
 
 __device__ __forceinline__ void store_out(float *p, float v, int acc) {
   *p = acc ? *p + v : v;

@@ -138,39 +138,102 @@ int dispatch_attention(const iree_mi355x_executable_environment_t *,
                                    s->stream);
 }
 
+// "batch_matmul_f16": the matmul_f16 constants, then batch, stride_a,
+// stride_b, stride_c (lo/hi pairs), activation, epilogue bindings (bit 0:
+// bias, bit 1: multiplier), ld_multiplier, batch_stride_multiplier (lo/hi).
+// Bindings: a b c [bias] [multiplier].
+int dispatch_batch_matmul(const iree_mi355x_executable_environment_t *,
+                          const iree_mi355x_executable_dispatch_state_t *s) {
+  const char *who = "batch_matmul_f16";
+  MatmulConsts c;
+  int st = decode_matmul(s, 3, &c);
+  if (st)
+    return st;
+  if (s->constant_count < 27)
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: constants missing", who);
+  const uint32_t *k = s->constants;
+  const int64_t batch = u64(k, 13), sa = u64(k, 15), sb = u64(k, 17),
+                sc = u64(k, 19);
+  const uint32_t act = k[21], epi_bindings = k[22];
+  const int64_t ld_mul = u64(k, 23), s_mul = u64(k, 25);
+  const bool has_bias = epi_bindings & 1u, has_mul = epi_bindings & 2u;
+  const uint32_t need = 3 + (has_bias ? 1 : 0) + (has_mul ? 1 : 0);
+  if (s->binding_count < need || batch < 0 || sa < 0 || sb < 0 || sc < 0 ||
+      s_mul < 0)
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: bindings or strides", who);
+  const bool bt = c.flags & IREE_MI355X_MATMUL_B_TRANSPOSED;
+  const int64_t cb = (c.flags & IREE_MI355X_MATMUL_OUT_F32) ? 4 : 2;
+  const int64_t last = batch > 0 ? batch - 1 : 0;
+  auto batched = [&](int64_t stride, int64_t one, int64_t elem) {
+    return one > 0 ? last * stride * elem + one : 0;
+  };
+  if ((st = check_binding(s, 0, batched(sa, span(c.m, c.k, c.lda, 2), 2),
+                          who)) ||
+      (st = check_binding(
+           s, 1,
+           batched(sb, bt ? span(c.n, c.k, c.ldb, 2) : span(c.k, c.n, c.ldb, 2),
+                   2),
+           who)) ||
+      (st = check_binding(s, 2, batched(sc, span(c.m, c.n, c.ldc, cb), cb),
+                          who)))
+    return st;
+  iree_mi355x_epilogue_t epi = {};
+  epi.activation = act;
+  uint32_t next = 3;
+  if (has_bias) {
+    if ((st = check_binding(s, next, c.n * 2, who)))
+      return st;
+    epi.bias = s->binding_ptrs[next++];
+  }
+  if (has_mul) {
+    if ((st = check_binding(s, next,
+                            batched(s_mul, span(c.m, c.n, ld_mul, 2), 2), who)))
+      return st;
+    epi.multiplier = s->binding_ptrs[next++];
+    epi.ld_multiplier = ld_mul;
+    epi.batch_stride_multiplier = s_mul;
+  }
+  return iree_mi355x_batch_matmul_f16(
+      s->binding_ptrs[0], s->binding_ptrs[1], s->binding_ptrs[2], batch, c.m,
+      c.n, c.k, c.lda, c.ldb, c.ldc, sa, sb, sc, c.flags, &epi, nullptr, 0,
+      s->stream);
+}
+
 const iree_mi355x_executable_library_header_t kHeader = {
     IREE_MI355X_EXECUTABLE_LIBRARY_VERSION_LATEST, "iree_mi355x_gfx950"};
 
 const iree_mi355x_executable_dispatch_fn_t kPtrs[] = {
     dispatch_matmul_f16, dispatch_matmul_i8, dispatch_w8a16,
-    dispatch_attention};
+    dispatch_attention, dispatch_batch_matmul};
 
+// Largest static LDS and workgroup of any kernel an export can launch: the
+// f16 MFMA ring (up to 160 KiB, 512 threads), the GEMV (512 threads), the
+// W8A16 256x256 ring (3 x 48 KiB), the attention K/V ring (2 x 32 KiB).
+constexpr uint64_t kF16Flags = IREE_MI355X_DISPATCH_FLAG_RESOURCES_VALID |
+                               IREE_MI355X_DISPATCH_FLAG_USES_MFMA |
+                               IREE_MI355X_DISPATCH_FLAG_USES_LDS_DMA |
+                               IREE_MI355X_DISPATCH_FLAG_USES_WORKSPACE;
 const iree_mi355x_executable_dispatch_attrs_t kAttrs[] = {
-    {IREE_MI355X_DISPATCH_FLAG_RESOURCES_VALID |
-         IREE_MI355X_DISPATCH_FLAG_USES_MFMA |
-         IREE_MI355X_DISPATCH_FLAG_USES_LDS_DMA |
-         IREE_MI355X_DISPATCH_FLAG_USES_WORKSPACE,
-     163840, 512},
+    {kF16Flags, 163840, 512},
     {IREE_MI355X_DISPATCH_FLAG_RESOURCES_VALID |
          IREE_MI355X_DISPATCH_FLAG_USES_MFMA |
          IREE_MI355X_DISPATCH_FLAG_USES_LDS_DMA,
      163840, 512},
+    {kF16Flags, 147456, 512},
     {IREE_MI355X_DISPATCH_FLAG_RESOURCES_VALID |
          IREE_MI355X_DISPATCH_FLAG_USES_MFMA |
-         IREE_MI355X_DISPATCH_FLAG_USES_WORKSPACE,
-     49152 + 4, 256},
-    {IREE_MI355X_DISPATCH_FLAG_RESOURCES_VALID |
-         IREE_MI355X_DISPATCH_FLAG_USES_MFMA,
-     16384 + 128 * 68 * 2, 256},
+         IREE_MI355X_DISPATCH_FLAG_USES_LDS_DMA,
+     65536, 256},
+    {kF16Flags, 163840, 512},
 };
 
 const char *const kNames[] = {"matmul_f16", "matmul_i8", "w8a16_matmul",
-                              "attention_f16"};
+                              "attention_f16", "batch_matmul_f16"};
 
 const iree_mi355x_executable_library_t kLibrary = {
     &kHeader,
     {0, nullptr},
-    {4, kPtrs, kAttrs, kNames},
+    {5, kPtrs, kAttrs, kNames},
 };
 
 }  // namespace

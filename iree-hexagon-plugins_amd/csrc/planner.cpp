@@ -75,8 +75,10 @@ bool gemv_eligible(const iree_mi355x_matmul_desc_t &d) {
   const int cols = 16 / elem_bytes(d.b_elem);
   if (d.n % cols != 0)
     return false;
-  // one arrival counter per column block of 64 lanes x `cols` columns
-  if ((d.n + 64 * cols - 1) / (64 * cols) > kMaxWorkspaceCounters)
+  // one arrival counter per column block of 64 lanes x `cols` columns, per
+  // batch
+  const int64_t batch = d.batch > 0 ? d.batch : 1;
+  if ((d.n + 64 * cols - 1) / (64 * cols) * batch > kMaxWorkspaceCounters)
     return false;
   // int8 weights only in the W8A16 form; f16 with f16 or f32 output.
   if (d.b_elem == IREE_MI355X_ELEM_I8)
@@ -155,15 +157,16 @@ bool evaluate(const iree_mi355x_matmul_desc_t &d, const FastConfig &c,
               bool explicit_config = false) {
   if (!fast_fits(d, c))
     return false;
+  const int64_t batch = d.batch > 0 ? d.batch : 1;
   const int64_t tiles_m = (d.m + c.bm - 1) / c.bm;
   const int64_t tiles = tiles_m * (d.n / c.bn);
-  if (c.split_k && tiles > kMaxWorkspaceCounters)
-    return false;  // one arrival counter per tile
+  if (c.split_k && tiles * batch > kMaxWorkspaceCounters)
+    return false;  // one arrival counter per tile of every batch
   int splits = 1;
   int64_t k_split = d.k;
   if (c.split_k) {
     // Enough workgroups to cover every CU; each split a multiple of BK.
-    int64_t want = (cus + tiles - 1) / tiles;
+    int64_t want = (cus + tiles * batch - 1) / (tiles * batch);
     const int64_t max_splits =
         explicit_config ? d.k / c.bk : d.k / (kMinStagesPerSplit * c.bk);
     if (want > max_splits)
@@ -172,8 +175,10 @@ bool evaluate(const iree_mi355x_matmul_desc_t &d, const FastConfig &c,
       want = 1;
     k_split = ((d.k + want - 1) / want + c.bk - 1) / c.bk * c.bk;
     splits = (int)((d.k + k_split - 1) / k_split);
-    if (splits < 2 && !explicit_config)
-      return false;  // an unsplit configuration covers this shape better
+    // One split stores directly (rows past M masked): worth it only where
+    // M is ragged, else an unsplit configuration covers the shape better.
+    if (splits < 2 && !explicit_config && d.m % c.bm == 0)
+      return false;
   }
   const int64_t ab = elem_bytes(d.a_elem), bb = elem_bytes(d.b_elem);
   const int64_t acc_bytes = 4;
@@ -182,16 +187,17 @@ bool evaluate(const iree_mi355x_matmul_desc_t &d, const FastConfig &c,
   r.splits = splits;
   r.k_split = (int)k_split;
   r.tiles = tiles;
-  r.critical = ((tiles * splits + cus - 1) / cus) * c.bm * c.bn * k_split;
+  r.critical =
+      ((tiles * splits * batch + cus - 1) / cus) * c.bm * c.bn * k_split;
   // A rows past M (split configurations) are still copied, as clamped
   // duplicates of row M-1.
-  r.traffic = ab * (tiles_m * c.bm) * d.k * (d.n / c.bn) +
-              bb * d.n * d.k * tiles_m;
+  r.traffic = batch * (ab * (tiles_m * c.bm) * d.k * (d.n / c.bn) +
+                       bb * d.n * d.k * tiles_m);
   int64_t partial_bytes = 0;
-  if (c.split_k) {
+  if (c.split_k && splits > 1) {
     r.workspace = (int64_t)split_counter_bytes(tiles) +
-                  (int64_t)splits * d.m * d.n * acc_bytes;
-    partial_bytes = 2 * (int64_t)splits * d.m * d.n * acc_bytes;
+                  batch * splits * d.m * d.n * acc_bytes;
+    partial_bytes = 2 * batch * splits * d.m * d.n * acc_bytes;
     r.traffic += partial_bytes;
   }
   // time = the slowest of MFMA work on the busiest CU, the operand feed, and
@@ -200,8 +206,8 @@ bool evaluate(const iree_mi355x_matmul_desc_t &d, const FastConfig &c,
       d.a_elem == IREE_MI355X_ELEM_I8 ? kMacsPerCuNsI8 : kMacsPerCuNsF16;
   const double t_mfma = (double)r.critical / macs_per_ns;
   const double t_feed = (double)r.traffic / kFeedBytesPerNs;
-  const double hbm = (double)(ab * d.m * d.k + bb * d.n * d.k +
-                              elem_bytes(d.c_elem) * d.m * d.n +
+  const double hbm = (double)(batch * (ab * d.m * d.k + bb * d.n * d.k +
+                                       elem_bytes(d.c_elem) * d.m * d.n) +
                               partial_bytes);
   const double t_hbm = hbm / kHbmBytesPerNs;
   double t = t_mfma > t_feed ? t_mfma : t_feed;
@@ -209,12 +215,12 @@ bool evaluate(const iree_mi355x_matmul_desc_t &d, const FastConfig &c,
     t = t_hbm;
   // A workgroup's K loop is a chain of stages, each at least a copy latency
   // apart once the ring's lookahead is spent.
-  const int64_t rounds = (tiles * splits + cus - 1) / cus;
+  const int64_t rounds = (tiles * splits * batch + cus - 1) / cus;
   const double t_chain = (double)rounds * (double)(k_split / c.bk) * kStageNs;
   if (t_chain > t)
     t = t_chain;
   t += (double)rounds * kRoundNs;
-  if (c.split_k) {
+  if (c.split_k && splits > 1) {
     // the last arriver sums G=8 elements x 8 splits per memory round trip
     const int64_t rows = d.m < c.bm ? d.m : c.bm;
     const int64_t per_thread = (rows * c.bn + c.threads - 1) / c.threads;
@@ -249,6 +255,7 @@ void iree_mi355x_matmul_desc_init(iree_mi355x_matmul_desc_t *desc,
   desc->b_aligned16 = 1;
   desc->lds_budget_bytes = kDefaultLdsBudget;
   desc->num_cus = kDefaultCus;
+  desc->batch = 1;
 }
 
 int32_t iree_mi355x_classify_matmul(const iree_mi355x_matmul_desc_t *d) {
@@ -284,17 +291,19 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
 
   if (family == IREE_MI355X_FAMILY_GEMV) {
     const int wb = elem_bytes(d->b_elem);
-    GemvPlan g = gemv_plan(d->m, d->n, d->k, wb);
+    const int64_t batch = d->batch > 0 ? d->batch : 1;
+    GemvPlan g = gemv_plan(d->m, d->n, d->k, wb, batch);
     snprintf(plan->config_name, sizeof(plan->config_name), "gemv_%s_r%lld",
              wb == 1 ? "w8a16" : "f16", (long long)d->m);
     plan->tile_m = d->m;
     plan->tile_n = g.cols_per_wg;
     plan->tile_k = g.k_chunk;
-    plan->workgroups = g.col_blocks * g.splits;
+    plan->workgroups = g.col_blocks * g.splits * batch;
     plan->threads = kGemvThreads;
     plan->splits = g.splits;
-    plan->workspace_bytes = (int64_t)gemv_workspace_bytes(d->m, d->n, d->k, wb);
-    plan->traffic_bytes = d->n * d->k * wb + d->m * d->k * 2;
+    plan->workspace_bytes =
+        (int64_t)gemv_workspace_bytes(d->m, d->n, d->k, wb, batch);
+    plan->traffic_bytes = batch * (d->n * d->k * wb + d->m * d->k * 2);
     return IREE_MI355X_OK;
   }
 
@@ -341,7 +350,7 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
     plan->tile_n = c.bn;
     plan->tile_k = c.bk;
     plan->lds_bytes = c.lds_bytes;
-    plan->workgroups = best.tiles * best.splits;
+    plan->workgroups = best.tiles * best.splits * (d->batch > 0 ? d->batch : 1);
     plan->threads = c.threads;
     plan->splits = best.splits;
     plan->k_split = best.k_split;

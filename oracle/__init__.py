@@ -49,6 +49,13 @@ def _load():
                                       ctypes.c_uint32, ctypes.c_int]
     lib.oracle_matmul_i8.argtypes = [p, p, p, i64, i64, i64, i64, i64, i64,
                                      ctypes.c_uint32, ctypes.c_int]
+    lib.oracle_batch_matmul_f16.argtypes = [
+        p, p, p, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64,
+        ctypes.c_uint32, p, p, i64, i64, ctypes.c_uint32, ctypes.c_int]
+    lib.oracle_activation.argtypes = [ctypes.c_float, ctypes.c_uint32]
+    lib.oracle_activation.restype = ctypes.c_float
+    lib.oracle_geglu_f16_ops.argtypes = [ctypes.c_float, ctypes.c_uint16]
+    lib.oracle_geglu_f16_ops.restype = ctypes.c_uint16
     lib.oracle_w8a16.argtypes = [p, p, p, p, i64, i64, i64, i64, i64, i64,
                                  ctypes.c_uint32, ctypes.c_int]
     lib.oracle_attention_f16.argtypes = [p, p, p, p, i64, i64, i64, i64, i64,
@@ -60,6 +67,7 @@ def _load():
                                                  ctypes.c_int, i64, i64, p]
     lib.oracle_hmx_pack_f16.argtypes = [p, p] + [ctypes.c_uint32] * 5
     for name in ("oracle_matmul_f16", "oracle_matmul_i8", "oracle_w8a16",
+                 "oracle_batch_matmul_f16",
                  "oracle_attention_f16", "oracle_select_hmx_tile_sizes"):
         getattr(lib, name).restype = ctypes.c_int
     _lib = lib
@@ -109,6 +117,60 @@ def matmul_f16(a, b, c_init=None, *, b_transposed=False, out_f32=False,
     assert rc == 0, rc
     return c
 
+
+
+ACT_NONE, ACT_RELU, ACT_GELU_TANH, ACT_SILU = 0, 1, 2, 3
+
+
+def batch_matmul_f16(a, b, c_init=None, *, b_transposed=False, out_f32=False,
+                     bias=None, activation=ACT_NONE, multiplier=None,
+                     threads=None) -> np.ndarray:
+    """Per batch z: out = [C_init +] multiplier * act(A_z.B_z + bias).
+
+    a: [Z, M, K] f16; b: [Z, K, N] (or [Z, N, K] transposed) f16, or 2-D to
+    share one B across the batch; bias [N] f16; multiplier [Z, M, N] or
+    [M, N] f16. f32 accumulation and epilogue, one rounding."""
+    a = np.ascontiguousarray(a, np.float16)
+    b = np.ascontiguousarray(b, np.float16)
+    z, m, k = a.shape
+    shared_b = b.ndim == 2
+    n = (b.shape[-2] if b_transposed else b.shape[-1])
+    ldb = b.shape[-1]
+    sb = 0 if shared_b else b.shape[1] * b.shape[2]
+    flags = (B_TRANSPOSED if b_transposed else 0) | (OUT_F32 if out_f32 else 0)
+    dt = np.float32 if out_f32 else np.float16
+    if c_init is not None:
+        c = np.ascontiguousarray(c_init, dt).copy()
+        flags |= ACCUMULATE
+    else:
+        c = np.zeros((z, m, n), dt)
+    bias_a = None if bias is None else np.ascontiguousarray(bias, np.float16)
+    mul_a, s_mul = None, 0
+    if multiplier is not None:
+        mul_a = np.ascontiguousarray(multiplier, np.float16)
+        s_mul = 0 if mul_a.ndim == 2 else m * n
+    rc = _load().oracle_batch_matmul_f16(
+        _ptr(a), _ptr(b), _ptr(c), z, m, n, k, k, ldb, n, m * k, sb, m * n,
+        flags, None if bias_a is None else _ptr(bias_a),
+        None if mul_a is None else _ptr(mul_a), n, s_mul, activation,
+        threads or default_threads())
+    assert rc == 0, rc
+    return c
+
+
+def activation(v: float, act: int) -> float:
+    """The oracle's f32 activation of one value."""
+    return float(_load().oracle_activation(v, act))
+
+
+def geglu_f16_ops(acc, up) -> np.ndarray:
+    """The reference IR's GeGLU epilogue with every op rounded to f16."""
+    acc = np.asarray(acc, np.float32).ravel()
+    up = np.asarray(up, np.float16).ravel()
+    lib = _load()
+    out = np.array([lib.oracle_geglu_f16_ops(float(x), int(u.view(np.uint16)))
+                    for x, u in zip(acc, up)], np.uint16)
+    return out.view(np.float16)
 
 def matmul_i8(a, b, c_init=None, *, b_transposed=False, threads=None):
     """C = [C_init +] A.B, int8 inputs, exact int32 accumulation/output."""

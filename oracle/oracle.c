@@ -133,6 +133,92 @@ int oracle_matmul_f16(const uint16_t *a, const uint16_t *b, void *c,
   return 0;
 }
 
+/* ------------------------------------------- fused epilogue / batches ---- */
+
+/* act(v) in f32 (double for the transcendental). GELU is the tanh form of the
+ * reference's epilogue fusion test (LIT/codegen/pipelines/
+ * hexagon_hmx_epilogue_keeps_config.mlir); SiLU is v / (1 + e^-v). */
+float oracle_activation(float v, uint32_t act) {
+  switch (act) {
+    case ORACLE_ACT_RELU:
+      return v > 0.0f ? v : 0.0f;
+    case ORACLE_ACT_GELU_TANH: {
+      const double x = v;
+      return (float)(0.5 * x *
+                     (1.0 + tanh(0.7978845608028654 * (x + 0.044715 * x * x * x))));
+    }
+    case ORACLE_ACT_SILU:
+      return (float)((double)v / (1.0 + exp(-(double)v)));
+    default:
+      return v;
+  }
+}
+
+int oracle_batch_matmul_f16(const uint16_t *a, const uint16_t *b, void *c,
+                            int64_t batch, int64_t m, int64_t n, int64_t k,
+                            int64_t lda, int64_t ldb, int64_t ldc, int64_t sa,
+                            int64_t sb, int64_t sc, uint32_t flags,
+                            const uint16_t *bias, const uint16_t *mul,
+                            int64_t ld_mul, int64_t s_mul, uint32_t act,
+                            int threads) {
+  if (bad_dims(m, n, k) || batch < 0)
+    return 1;
+  const int out_f32 = (flags & ORACLE_OUT_F32) != 0;
+  const int accumulate = (flags & ORACLE_ACCUMULATE) != 0;
+  float *acc = (float *)malloc(sizeof(float) * (size_t)(m * n + 1));
+  if (!acc)
+    return 2;
+  for (int64_t z = 0; z < batch; ++z) {
+    /* f32 sums of this batch: the plain matmul into an f32 scratch */
+    int rc = oracle_matmul_f16(a + z * sa, b + z * sb, acc, m, n, k, lda, ldb,
+                               n, (flags & ORACLE_B_TRANSPOSED) | ORACLE_OUT_F32,
+                               threads);
+    if (rc) {
+      free(acc);
+      return rc;
+    }
+    for (int64_t i = 0; i < m; ++i)
+      for (int64_t j = 0; j < n; ++j) {
+        float v = acc[i * n + j];
+        if (bias)
+          v += oracle_f16_to_f32(bias[j]);
+        v = oracle_activation(v, act);
+        if (mul)
+          v *= oracle_f16_to_f32(mul[z * s_mul + i * ld_mul + j]);
+        if (out_f32) {
+          float *cp = (float *)c + z * sc + i * ldc + j;
+          *cp = accumulate ? *cp + v : v;
+        } else {
+          uint16_t *cp = (uint16_t *)c + z * sc + i * ldc + j;
+          *cp = oracle_f32_to_f16(accumulate ? oracle_f16_to_f32(*cp) + v : v);
+        }
+      }
+  }
+  free(acc);
+  return 0;
+}
+
+/* The reference's GeGLU epilogue exactly as its IR states it
+ * (LIT/codegen/pipelines/hexagon_hmx_epilogue_keeps_config.mlir:82-101):
+ * h = f16(acc), then every op in f16 (each result rounded to f16):
+ * g = h * 0.5 * (1 + tanh(k0 * (h + k1 * h^3))) with the f16 constants
+ * k0 = 0.797852, k1 = 0.044708, out = g * up. */
+uint16_t oracle_geglu_f16_ops(float acc, uint16_t up) {
+#define R16(x) oracle_f16_to_f32(oracle_f32_to_f16((float)(x)))
+  const float k0 = R16(7.978520e-01f), k1 = R16(4.470830e-02f);
+  const float h = R16(acc);
+  const float h3 = R16(R16(h * h) * h);
+  const float t0 = R16(h3 * k1);
+  const float t1 = R16(h + t0);
+  const float t2 = R16(t1 * k0);
+  const float t3 = R16(tanh((double)t2));
+  const float t4 = R16(t3 + 1.0f);
+  const float t5 = R16(t4 * 0.5f);
+  const float g = R16(h * t5);
+  return oracle_f32_to_f16(g * oracle_f16_to_f32(up));
+#undef R16
+}
+
 /* ---------------------------------------------------------- matmul i8 ---- */
 
 int oracle_matmul_i8(const int8_t *a, const int8_t *b, int32_t *c, int64_t m,

@@ -21,6 +21,13 @@
  *   select_hmx_tile_sizes reference lit goldens
  *   choose_static_tiling  brute-force divisor search
  *   hmx_pack              reference closed form on the UK test cases
+ *   batch_matmul_f16      per-batch equality with matmul_f16; bias / ReLU /
+ *                         GELU / SiLU against numpy closed forms; epilogue
+ *                         order (bias before act, multiplier after)
+ *   activation            ReLU / SiLU exact points, GELU-tanh identities
+ *                         (odd part, limits, the value at 1)
+ *   geglu_f16_ops         hand-computed values at h = 1, -2, 0 and large |h|,
+ *                         and within 2e-3 of the f32 epilogue
  *
  * Parity unpinned (no check in this container can fix it):
  *   matmul_f16 / w8a16 / attention summation order: IREE llvm-cpu
@@ -57,6 +64,33 @@ void oracle_f32_to_f16_array(const float *src, uint16_t *dst, int64_t n);
 int oracle_matmul_f16(const uint16_t *a, const uint16_t *b, void *c,
                       int64_t m, int64_t n, int64_t k, int64_t lda,
                       int64_t ldb, int64_t ldc, uint32_t flags, int threads);
+
+/* Activations of the fused epilogue (same values as the product ABI). */
+#define ORACLE_ACT_NONE 0u
+#define ORACLE_ACT_RELU 1u
+#define ORACLE_ACT_GELU_TANH 2u
+#define ORACLE_ACT_SILU 3u
+float oracle_activation(float v, uint32_t act);
+
+/* linalg.batch_matmul f16 with f32 accumulation and the fused elementwise
+ * epilogue the reference fuses after a matmul (bias add, activation, gating
+ * multiply; LIT/codegen/pipelines/hexagon_hmx_epilogue_keeps_config.mlir):
+ * for each batch z, out = [C_init +] mul * act(A_z.B_z + bias), computed in
+ * f32 from the f32 sum and rounded once. bias [N] and mul [M,N] (pitch
+ * ld_mul, batch stride s_mul) may be NULL. Strides are in elements. */
+int oracle_batch_matmul_f16(const uint16_t *a, const uint16_t *b, void *c,
+                            int64_t batch, int64_t m, int64_t n, int64_t k,
+                            int64_t lda, int64_t ldb, int64_t ldc, int64_t sa,
+                            int64_t sb, int64_t sc, uint32_t flags,
+                            const uint16_t *bias, const uint16_t *mul,
+                            int64_t ld_mul, int64_t s_mul, uint32_t act,
+                            int threads);
+
+/* One element of the reference's GeGLU epilogue with every op rounded to f16,
+ * as its IR computes it (LIT/codegen/pipelines/
+ * hexagon_hmx_epilogue_keeps_config.mlir:82-101); math.fpowi h^3 is taken as
+ * two f16 multiplies. */
+uint16_t oracle_geglu_f16_ops(float acc, uint16_t up);
 
 /* i8 x i8 -> i32 exact integer matmul (linalg.matmul / quantized_matmul with
  * zero points 0). */

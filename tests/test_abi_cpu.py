@@ -41,7 +41,7 @@ def test_executable_library_table(pkg):
     assert lib.header.contents.version == pkg.EXECUTABLE_LIBRARY_VERSION
     assert lib.imports.count == 0
     assert pkg.export_names() == ["matmul_f16", "matmul_i8", "w8a16_matmul",
-                                  "attention_f16"]
+                                  "attention_f16", "batch_matmul_f16"]
     for i in range(lib.exports.count):
         attrs = lib.exports.attrs[i]
         assert attrs.flags & 1  # RESOURCES_VALID
@@ -231,3 +231,69 @@ def test_dispatch_rejects_short_bindings(pkg):
     q = 1 * 2 * 128 * 64 * 2
     assert pkg.call_export("attention_f16", att, [FAKE] * 4,
                            [q, q, q - 2, q]) == pkg.INVALID_ARGUMENT
+
+
+def test_batch_dispatch_rejects_short_bindings(pkg):
+    """batch_matmul_f16 export: every binding, the batched spans included,
+    is checked before anything launches."""
+    z, m, n, k = 3, 64, 32, 16
+    consts = pkg.batch_matmul_constants(m, n, k, k, n, n, 0, z, m * k, k * n,
+                                        m * n, pkg.ACT_RELU, True, True, n, m * n)
+    full = [z * m * k * 2, z * k * n * 2, z * m * n * 2, n * 2, z * m * n * 2]
+    for i in range(5):
+        short = list(full)
+        short[i] -= 2
+        assert pkg.call_export("batch_matmul_f16", consts, [FAKE] * 5,
+                               short) == pkg.INVALID_ARGUMENT, i
+    # fewer bindings than the epilogue bits announce
+    assert pkg.call_export("batch_matmul_f16", consts, [FAKE] * 4,
+                           full[:4]) == pkg.INVALID_ARGUMENT
+    # too few constants
+    assert pkg.call_export("batch_matmul_f16", consts[:20], [FAKE] * 5,
+                           full) == pkg.INVALID_ARGUMENT
+
+
+def test_batch_matmul_argument_checks(pkg):
+    lib = pkg.library()
+    f = lib.iree_mi355x_batch_matmul_f16
+    # negative batch, batch over the grid limit, outputs that overlap
+    assert f(FAKE, FAKE, FAKE, -1, 8, 8, 8, 8, 8, 8, 64, 64, 64, 0, None,
+             None, 0, None) == pkg.INVALID_ARGUMENT
+    assert f(FAKE, FAKE, FAKE, 70000, 8, 8, 8, 8, 8, 8, 64, 64, 64, 0, None,
+             None, 0, None) == pkg.UNSUPPORTED
+    assert f(FAKE, FAKE, FAKE, 2, 8, 8, 8, 8, 8, 8, 64, 64, 32, 0, None,
+             None, 0, None) == pkg.INVALID_ARGUMENT
+    e = pkg.Epilogue()
+    e.activation = 7
+    assert f(FAKE, FAKE, FAKE, 2, 8, 8, 8, 8, 8, 8, 64, 64, 64, 0,
+             ctypes.byref(e), None, 0, None) == pkg.INVALID_ARGUMENT
+    e.activation = pkg.ACT_GELU_TANH
+    e.multiplier = FAKE + 1
+    assert f(FAKE, FAKE, FAKE, 2, 8, 8, 8, 8, 8, 8, 64, 64, 64, 0,
+             ctypes.byref(e), None, 0, None) == pkg.MISALIGNED
+    e.multiplier = FAKE
+    e.ld_multiplier = 4
+    assert f(FAKE, FAKE, FAKE, 2, 8, 8, 8, 8, 8, 8, 64, 64, 64, 0,
+             ctypes.byref(e), None, 0, None) == pkg.INVALID_ARGUMENT
+    # batch 0 is a no-op
+    assert f(FAKE, FAKE, FAKE, 0, 8, 8, 8, 8, 8, 8, 64, 64, 64, 0, None,
+             None, 0, None) == pkg.OK
+
+
+def test_batch_planner_and_workspace(pkg):
+    # batch spreads work over the CUs: fewer K splits than batch 1
+    d1 = pkg.make_desc(0, 0, 0, 16, 4096, 4096, 0)
+    d8 = pkg.make_desc(0, 0, 0, 16, 4096, 4096, 0, batch=8)
+    p1, p8 = pkg.plan(d1), pkg.plan(d8)
+    assert p8.family == pkg.FAMILY_MFMA and p8.splits < p1.splits
+    assert p8.workgroups >= p1.workgroups
+    # one split per tile stores directly: no workspace
+    d32 = pkg.make_desc(0, 0, 0, 16, 4096, 4096, 0, batch=32)
+    p32 = pkg.plan(d32)
+    assert p32.family == pkg.FAMILY_MFMA and p32.splits == 1
+    assert p32.workspace_bytes == 0
+    lib = pkg.library()
+    w1 = lib.iree_mi355x_batch_matmul_workspace_bytes(1, 1, 4096, 4096, 0)
+    w4 = lib.iree_mi355x_batch_matmul_workspace_bytes(4, 1, 4096, 4096, 0)
+    assert w1 == pkg.plan(pkg.make_desc(0, 0, 0, 1, 4096, 4096, 0)).workspace_bytes
+    assert w4 > 64 * 1024 and w1 > 64 * 1024

@@ -4,6 +4,7 @@ Bars: int8 -> i32 bit-exact; f16 max|y - y_cpu| / max|y_cpu| <= 2e-3 (the
 BASELINE fp16 rule), plus the reference's allclose + relative-L2 recipe with
 each micro model's tolerances (IT/stages/checking.py:46-132).
 """
+import ctypes
 import os
 
 import numpy as np
@@ -467,3 +468,135 @@ def test_dispatch_through_export_table(pkg, oracle, dev):
     ref = oracle.attention_f16(q.cpu().numpy(), kk.cpu().numpy(),
                                v.cpu().numpy(), scale=0.125, causal=True)
     fp16_ok(oracle, o.cpu().numpy(), ref)
+    # batched matmul with a SiLU-gated epilogue through the export table
+    z, m, n, k = 3, 64, 256, 128
+    a = (torch.randn(z, m, k, generator=g) * 0.5).half()
+    b = torch.randn(z, k, n, generator=g).half()
+    bias = torch.randn(n, generator=g).half()
+    mul = torch.randn(z, m, n, generator=g).half()
+    a_d, b_d, bias_d, mul_d = (t.to(dev) for t in (a, b, bias, mul))
+    y = torch.empty(z, m, n, dtype=torch.float16, device=dev)
+    st = pkg.call_export(
+        "batch_matmul_f16",
+        pkg.batch_matmul_constants(m, n, k, k, n, n, 0, z, m * k, k * n, m * n,
+                                   pkg.ACT_SILU, True, True, n, m * n),
+        [a_d.data_ptr(), b_d.data_ptr(), y.data_ptr(), bias_d.data_ptr(),
+         mul_d.data_ptr()],
+        [a.numel() * 2, b.numel() * 2, y.numel() * 2, n * 2, mul.numel() * 2], s)
+    assert st == pkg.OK, pkg.last_error()
+    ref = oracle.batch_matmul_f16(a.numpy(), b.numpy(), bias=bias.numpy(),
+                                  activation=3, multiplier=mul.numpy())
+    fp16_ok(oracle, y.cpu().numpy(), ref)
+    # a multiplier binding one byte short is rejected before launch
+    st = pkg.call_export(
+        "batch_matmul_f16",
+        pkg.batch_matmul_constants(m, n, k, k, n, n, 0, z, m * k, k * n, m * n,
+                                   pkg.ACT_SILU, True, True, n, m * n),
+        [a_d.data_ptr(), b_d.data_ptr(), y.data_ptr(), bias_d.data_ptr(),
+         mul_d.data_ptr()],
+        [a.numel() * 2, b.numel() * 2, y.numel() * 2, n * 2, mul.numel() * 2 - 1], s)
+    assert st == pkg.INVALID_ARGUMENT
+
+
+# --------------------------------------------- batch matmul + epilogue ----
+
+def test_batch_matmul_reference_micro_model(pkg, oracle, dev):
+    """IT/models/micro/hmx/batch-matmul-4x1024x1024x128-f16: a [4,1024,128],
+    b [4,128,1024] normal seeds 0/1, f32 result, the model's tolerances."""
+    a = torch.randn(4, 1024, 128, generator=torch.Generator().manual_seed(0)).half()
+    b = torch.randn(4, 128, 1024, generator=torch.Generator().manual_seed(1)).half()
+    c = pkg.batch_matmul(a.to(dev), b.to(dev), out_dtype=torch.float32)
+    ref = oracle.batch_matmul_f16(a.numpy(), b.numpy(), out_f32=True)
+    got = c.cpu().numpy()
+    rel, _, close = oracle.compare_arrays(ref, got, 1.5e-1, 5.0e-3)
+    assert close and rel <= 0.05
+    fp16_ok(oracle, got, ref)
+
+
+@pytest.mark.parametrize("z,m,n,k,bt,shared_b", [
+    (3, 1, 4096, 1024, False, True),     # GEMV, shared weights
+    (2, 4, 2048, 512, False, False),     # GEMV, 4 rows
+    (4, 16, 2048, 1024, False, True),    # split-K skinny
+    (2, 100, 512, 768, False, False),    # split-K ragged M
+    (2, 256, 512, 256, True, False),     # macro-tile TN
+    (3, 256, 256, 512, False, True),     # macro-tile NN, shared B
+    (2, 17, 19, 23, True, False),        # general kernel
+    (16, 16, 2048, 512, False, True),    # ragged M, one split per tile
+])
+@pytest.mark.parametrize("act", [None, "relu", "gelu_tanh", "silu"])
+def test_batch_matmul_epilogue_paths(pkg, oracle, dev, z, m, n, k, bt, shared_b, act):
+    g = torch.Generator().manual_seed(z * 1000 + m * 7 + n + k)
+    a = (torch.randn(z, m, k, generator=g) * 0.5).half()
+    bshape = (n, k) if bt else (k, n)
+    b = (torch.randn(*bshape, generator=g) if shared_b else
+         torch.randn(z, *bshape, generator=g)).half()
+    bias = torch.randn(n, generator=g).half()
+    mul = torch.randn(z, m, n, generator=g).half()
+    y = pkg.batch_matmul(a.to(dev), b.to(dev), b_transposed=bt, bias=bias.to(dev),
+                         activation=act, multiplier=mul.to(dev))
+    ref = oracle.batch_matmul_f16(a.numpy(), b.numpy(), b_transposed=bt,
+                                  bias=bias.numpy(),
+                                  activation=pkg._ACT_NAMES[act],
+                                  multiplier=mul.numpy())
+    fp16_ok(oracle, y.cpu().numpy(), ref)
+
+
+def test_batch_matmul_accumulate_f32_and_strided_batches(pkg, oracle, dev):
+    """Accumulate into an f32 init, with A and C views whose batch stride is
+    larger than a matrix (every batch still separate)."""
+    g = torch.Generator().manual_seed(41)
+    z, m, n, k = 3, 64, 256, 128
+    abig = (torch.randn(z, m + 8, k, generator=g) * 0.5).half()
+    a = abig[:, :m, :]
+    b = torch.randn(z, k, n, generator=g).half()
+    init = torch.randn(z, m, n, generator=g)
+    cbig = torch.zeros(z, m + 4, n)
+    cbig[:, :m, :] = init
+    c_d = cbig.to(dev)
+    pkg.batch_matmul(abig.to(dev)[:, :m, :], b.to(dev),
+                     c_d[:, :m, :], accumulate=True, out_dtype=torch.float32,
+                     bias=torch.ones(n, dtype=torch.float16, device=dev),
+                     activation="relu")
+    ref = oracle.batch_matmul_f16(a.contiguous().numpy(), b.numpy(),
+                                  init.numpy(), out_f32=True,
+                                  bias=np.ones(n, np.float16), activation=1)
+    fp16_ok(oracle, c_d[:, :m, :].cpu().numpy(), ref)
+    assert bool((c_d[:, m:, :] == 0).all().item()), "write outside the batches"
+
+
+def test_geglu_epilogue_reference_shape(pkg, oracle, dev):
+    """The reference's fused-epilogue test dispatch
+    (hexagon_hmx_epilogue_keeps_config.mlir): x [1,256] . W^T, W [2048,256],
+    tanh-GELU, gated by up [1,2048]. Checked against the f32 oracle and the
+    reference IR's f16-per-op form."""
+    g = torch.Generator().manual_seed(3)
+    x = (torch.randn(1, 256, generator=g)).half()
+    w = (torch.randn(2048, 256, generator=g) * 0.1).half()
+    up = torch.randn(1, 2048, generator=g).half()
+    y = pkg.linear(x.to(dev), w.to(dev), activation="gelu_tanh",
+                   multiplier=up.to(dev), w_transposed=True)
+    got = y.cpu().numpy()
+    ref32 = oracle.batch_matmul_f16(x.numpy()[None], w.numpy(), b_transposed=True,
+                                    activation=2, multiplier=up.numpy())[0]
+    fp16_ok(oracle, got, ref32)
+    acc = oracle.matmul_f16(x.numpy(), w.numpy(), b_transposed=True, out_f32=True)
+    ref16 = oracle.geglu_f16_ops(acc, up.numpy()).reshape(1, 2048)
+    fp16_ok(oracle, got, ref16.astype(np.float32))
+
+
+def test_batch_matmul_argument_errors(pkg, dev):
+    a = torch.zeros(2, 8, 8, dtype=torch.float16, device=dev)
+    b = torch.zeros(2, 8, 8, dtype=torch.float16, device=dev)
+    lib = pkg.library()
+    c = torch.zeros(2, 8, 8, dtype=torch.float16, device=dev)
+    # stride_c 0 with two batches would write both into one matrix
+    st = lib.iree_mi355x_batch_matmul_f16(a.data_ptr(), b.data_ptr(), c.data_ptr(),
+                                          2, 8, 8, 8, 8, 8, 8, 64, 64, 0, 0,
+                                          None, None, 0, None)
+    assert st == 1
+    e = pkg.Epilogue()
+    e.activation = 9
+    st = lib.iree_mi355x_batch_matmul_f16(a.data_ptr(), b.data_ptr(), c.data_ptr(),
+                                          2, 8, 8, 8, 8, 8, 8, 64, 64, 64, 0,
+                                          ctypes.byref(e), None, 0, None)
+    assert st == 1

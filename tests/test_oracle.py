@@ -258,3 +258,79 @@ def test_hmx_pack_reference_cases(oracle):
                             41, 35, 37, 3, 3)
     assert np.array_equal(out.view(np.uint16), d["ragged_packed"].view(np.uint16))
     assert not (out == 99).any()
+
+
+# ------------------------------------------------ batch matmul / epilogue ----
+
+def test_batch_matmul_equals_per_batch_matmul(oracle):
+    g = np.random.default_rng(5)
+    a = g.standard_normal((3, 17, 23)).astype(np.float16)
+    b = g.standard_normal((3, 23, 19)).astype(np.float16)
+    got = oracle.batch_matmul_f16(a, b, out_f32=True)
+    for z in range(3):
+        ref = oracle.matmul_f16(a[z], b[z], out_f32=True)
+        assert np.array_equal(got[z], ref)
+    # a 2-D B is shared by every batch; transposed B gives the same sums
+    bt = np.ascontiguousarray(b[0].T)
+    shared = oracle.batch_matmul_f16(a, bt, b_transposed=True, out_f32=True)
+    for z in range(3):
+        assert np.array_equal(shared[z], oracle.matmul_f16(a[z], b[0], out_f32=True))
+
+
+@pytest.mark.parametrize("act", [0, 1, 2, 3])
+def test_batch_matmul_epilogue_closed_forms(oracle, act):
+    """out = mul * act(acc + bias) against numpy closed forms (f64)."""
+    g = np.random.default_rng(6 + act)
+    a = g.standard_normal((2, 9, 16)).astype(np.float16)
+    b = g.standard_normal((2, 16, 12)).astype(np.float16)
+    bias = g.standard_normal(12).astype(np.float16)
+    mul = g.standard_normal((2, 9, 12)).astype(np.float16)
+    got = oracle.batch_matmul_f16(a, b, out_f32=True, bias=bias, activation=act,
+                                  multiplier=mul)
+    x = np.einsum("zmk,zkn->zmn", a.astype(np.float64), b.astype(np.float64))
+    x = x + bias.astype(np.float64)
+    if act == 1:
+        x = np.maximum(x, 0.0)
+    elif act == 2:
+        x = 0.5 * x * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (x + 0.044715 * x ** 3)))
+    elif act == 3:
+        x = x / (1.0 + np.exp(-x))
+    x = x * mul.astype(np.float64)
+    assert np.abs(got - x).max() <= 1e-4 * max(1.0, np.abs(x).max())
+    # order matters: the bias is added before the activation
+    if act == 1:
+        wrong = np.maximum(x / mul.astype(np.float64) - bias.astype(np.float64),
+                           0.0) + bias.astype(np.float64)
+        assert np.abs(got - wrong * mul.astype(np.float64)).max() > 1e-2
+
+
+def test_activation_points(oracle):
+    assert oracle.activation(3.5, 1) == 3.5 and oracle.activation(-3.5, 1) == 0.0
+    assert oracle.activation(0.0, 2) == 0.0 and oracle.activation(0.0, 3) == 0.0
+    # GELU(x) - GELU(-x) = x (odd part), limits, the value at 1
+    for x in (0.3, 1.7, 4.0):
+        assert abs(oracle.activation(x, 2) - oracle.activation(-x, 2) - x) < 1e-6
+    assert abs(oracle.activation(10.0, 2) - 10.0) < 1e-6
+    assert abs(oracle.activation(-10.0, 2)) < 1e-6
+    assert abs(oracle.activation(1.0, 2) - 0.8411919906) < 1e-6
+    # SiLU(x) = x sigmoid(x); SiLU(x) - SiLU(-x) = x
+    assert abs(oracle.activation(2.0, 3) - 2.0 / (1.0 + np.exp(-2.0))) < 1e-6
+    assert abs(oracle.activation(1.3, 3) - oracle.activation(-1.3, 3) - 1.3) < 1e-6
+
+
+def test_geglu_f16_ops_reference_form(oracle):
+    """The reference IR's GeGLU epilogue (every op in f16) at hand-computed
+    points, and its distance from the f32 epilogue the kernels compute."""
+    got = oracle.geglu_f16_ops([1.0, -2.0, 0.0, 8.0, -8.0], [1.0, 1.0, 1.0, 2.0, 1.0])
+    assert abs(float(got[0]) - 0.8412) < 2e-3
+    assert abs(float(got[1]) + 0.0455) < 2e-4
+    assert float(got[2]) == 0.0
+    assert float(got[3]) == 16.0
+    assert abs(float(got[4])) < 1e-6
+    g = np.random.default_rng(7)
+    acc = (g.standard_normal(4096) * 2.0).astype(np.float32)
+    up = g.standard_normal(4096).astype(np.float16)
+    f16_ops = oracle.geglu_f16_ops(acc, up).astype(np.float32)
+    f32 = np.array([oracle.activation(float(v), 2) for v in acc], np.float32)
+    f32 = f32 * up.astype(np.float32)
+    assert np.abs(f16_ops - f32).max() / np.abs(f32).max() <= 2e-3
