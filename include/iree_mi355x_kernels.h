@@ -60,6 +60,11 @@ typedef enum iree_mi355x_status_e {
 #define IREE_MI355X_MATMUL_ACCUMULATE 0x2u
 // f16 matmul only: write f32 C instead of f16.
 #define IREE_MI355X_MATMUL_OUT_F32 0x4u
+// f16 matmul only: A is stored [K, M] (indexing map (d2, d0), a transposed
+// LHS), lda >= M. Combines with B_TRANSPOSED
+// (test/codegen/transforms/convert_matmul_to_hmx.mlir:87-115 packs such an A
+// along its second dimension).
+#define IREE_MI355X_MATMUL_A_TRANSPOSED 0x8u
 
 // Attention flags.
 #define IREE_MI355X_ATTENTION_CAUSAL 0x1u

@@ -101,6 +101,10 @@ int iree_mi355x_mfma_config_info(int index, const char **name,
                                  int64_t *tile_n, int64_t *tile_k,
                                  int64_t *lds_bytes, int32_t *threads);
 
+// The layout flags (IREE_MI355X_MATMUL_B_TRANSPOSED, _A_TRANSPOSED) a
+// configuration's operands must carry, or -1 for a bad index.
+int32_t iree_mi355x_mfma_config_layout_flags(int index);
+
 // Launch one compiled MFMA configuration by index on an eligible shape
 // (autotuner entry). Arguments as iree_mi355x_matmul_f16 / _i8 /
 // _w8a16_matmul (scale is read only by the W8A16 form); flags must match the

@@ -37,6 +37,7 @@ STATUS_NAMES = {
 B_TRANSPOSED = 0x1
 ACCUMULATE = 0x2
 OUT_F32 = 0x4
+A_TRANSPOSED = 0x8
 CAUSAL = 0x1
 
 # Element kinds (iree_mi355x_elem_t) and kernel families.
@@ -59,6 +60,7 @@ EXPORTED_SYMBOLS = (
     "iree_mi355x_mfma_config_info", "iree_mi355x_matmul_mfma_config",
     "iree_mi355x_executable_library_query", "iree_mi355x_batch_matmul_f16",
     "iree_mi355x_batch_matmul_workspace_bytes",
+    "iree_mi355x_mfma_config_layout_flags",
 )
 
 # Activations of the fused matmul epilogue (include/iree_mi355x_kernels.h).
@@ -199,6 +201,8 @@ def library():
         ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
         ctypes.POINTER(i64), ctypes.POINTER(i64), ctypes.POINTER(i64),
         ctypes.POINTER(i64), ctypes.POINTER(ctypes.c_int32)]
+    lib.iree_mi355x_mfma_config_layout_flags.restype = ctypes.c_int32
+    lib.iree_mi355x_mfma_config_layout_flags.argtypes = [ctypes.c_int]
     lib.iree_mi355x_matmul_mfma_config.argtypes = [ctypes.c_int, p, p, p, p,
                                                    i64, i64, i64, i64, i64,
                                                    i64, u32, p]
@@ -255,6 +259,11 @@ class MfmaConfig:
     tile_k: int
     lds_bytes: int
     threads: int
+    layout_flags: int = 0  # B_TRANSPOSED / A_TRANSPOSED the operands carry
+
+    @property
+    def a_transposed(self) -> bool:
+        return bool(self.layout_flags & A_TRANSPOSED)
 
 
 def mfma_configs() -> list[MfmaConfig]:
@@ -270,7 +279,8 @@ def mfma_configs() -> list[MfmaConfig]:
             ctypes.byref(tk), ctypes.byref(lds), ctypes.byref(th)))
         out.append(MfmaConfig(i, name.value.decode(), bf.value, ae.value,
                               ce.value, tm.value, tn.value, tk.value,
-                              lds.value, th.value))
+                              lds.value, th.value,
+                              lib.iree_mi355x_mfma_config_layout_flags(i)))
     return out
 
 
@@ -336,24 +346,30 @@ def _stream_ptr(stream=None):
     return s.cuda_stream
 
 
+def _unit_col(t) -> bool:
+    """Elements of a row are adjacent (a one-element row has any stride)."""
+    return t.shape[-1] == 1 or t.stride(-1) == 1
+
+
 def _require(t, dtype, name, dims=(2,)):
     import torch
     if not isinstance(t, torch.Tensor) or not t.is_cuda:
         raise TypeError(f"{name} must be a device tensor")
     if t.dtype != dtype:
         raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
-    if t.dim() not in dims or t.stride(-1) != 1:
+    if t.dim() not in dims or not _unit_col(t):
         raise ValueError(f"{name} must be {'/'.join(map(str, dims))}-D with "
                          "unit column stride")
 
 
 def matmul(a, b, c=None, *, b_transposed=False, accumulate=False,
-           out_dtype=None, stream=None):
+           out_dtype=None, a_transposed=False, stream=None):
     """linalg.matmul dispatch: C = [C +] A . B on the MI355X kernels.
 
     f16 inputs accumulate in f32 and write f16 (or f32 with
     out_dtype=torch.float32); int8 inputs accumulate exactly into int32.
-    ``b_transposed``: B is stored [N, K].
+    ``b_transposed``: B is stored [N, K]. ``a_transposed`` (f16 only): A is
+    stored [K, M].
     """
     import torch
     lib = library()
@@ -365,7 +381,7 @@ def matmul(a, b, c=None, *, b_transposed=False, accumulate=False,
         _require(a, torch.float16, "a")
         _require(b, torch.float16, "b")
         out_dtype = out_dtype or torch.float16
-    m, k = a.shape
+    k, m = a.shape if a_transposed else a.shape[::-1]
     n = b.shape[0] if b_transposed else b.shape[1]
     if (b.shape[1] if b_transposed else b.shape[0]) != k:
         raise ValueError("contraction extents differ")
@@ -375,7 +391,9 @@ def matmul(a, b, c=None, *, b_transposed=False, accumulate=False,
         c = torch.empty((m, n), dtype=out_dtype, device=a.device)
     else:
         _require(c, out_dtype, "c")
-    flags = (B_TRANSPOSED if b_transposed else 0) | (ACCUMULATE if accumulate else 0)
+    flags = ((B_TRANSPOSED if b_transposed else 0) |
+             (ACCUMULATE if accumulate else 0) |
+             (A_TRANSPOSED if a_transposed else 0))
     s = _stream_ptr(stream)
     if a.dtype == torch.int8:
         _check(lib.iree_mi355x_matmul_i8(a.data_ptr(), b.data_ptr(),
@@ -405,7 +423,7 @@ def _epilogue(bias, activation, multiplier, m, n, batch):
         e.bias = bias.data_ptr()
     if multiplier is not None:
         _require(multiplier, torch.float16, "multiplier", (2, 3))
-        if multiplier.shape[-2:] != (m, n) or multiplier.stride(-1) != 1:
+        if multiplier.shape[-2:] != (m, n) or not _unit_col(multiplier):
             raise ValueError("multiplier must be [.., M, N] with unit column stride")
         e.multiplier = multiplier.data_ptr()
         e.ld_multiplier = multiplier.stride(-2)
@@ -418,12 +436,13 @@ def _epilogue(bias, activation, multiplier, m, n, batch):
 
 def batch_matmul(a, b, c=None, *, b_transposed=False, accumulate=False,
                  out_dtype=None, bias=None, activation=None, multiplier=None,
-                 stream=None):
+                 a_transposed=False, stream=None):
     """linalg.batch_matmul (f16, f32 accumulation) with a fused epilogue:
     C[z] = [C[z] +] multiplier[z] * act(A[z] . B[z] + bias).
 
-    a: [Z, M, K] (or [M, K] shared); b: [Z, K, N] / [Z, N, K] with
-    ``b_transposed`` (or 2-D, shared by the batch); bias [N]; multiplier
+    a: [Z, M, K] (or [M, K] shared; [Z, K, M] / [K, M] with
+    ``a_transposed``); b: [Z, K, N] / [Z, N, K] with ``b_transposed`` (or
+    2-D, shared by the batch); bias [N]; multiplier
     [Z, M, N] or [M, N]; activation None / "relu" / "gelu_tanh" / "silu".
     Every matrix needs a unit column stride; batch strides may be 0.
     """
@@ -437,12 +456,12 @@ def batch_matmul(a, b, c=None, *, b_transposed=False, accumulate=False,
     batch = max(a3.shape[0], b3.shape[0])
     if a.dim() == 2 and b.dim() == 2:
         batch = 1
-    m, k = a3.shape[1], a3.shape[2]
+    k, m = (a3.shape[1], a3.shape[2]) if a_transposed else (a3.shape[2], a3.shape[1])
     n = b3.shape[1] if b_transposed else b3.shape[2]
     if (b3.shape[2] if b_transposed else b3.shape[1]) != k:
         raise ValueError("contraction extents differ")
     for t, name in ((a3, "a"), (b3, "b")):
-        if t.shape[0] not in (1, batch) or t.stride(-1) != 1:
+        if t.shape[0] not in (1, batch) or not _unit_col(t):
             raise ValueError(f"{name}: batch extent or column stride unsupported")
     sa = 0 if a.dim() == 2 or a3.shape[0] == 1 else a3.stride(0)
     sb = 0 if b.dim() == 2 or b3.shape[0] == 1 else b3.stride(0)
@@ -457,7 +476,8 @@ def batch_matmul(a, b, c=None, *, b_transposed=False, accumulate=False,
     sc = c3.stride(0) if batch > 1 else m * n
     flags = ((B_TRANSPOSED if b_transposed else 0) |
              (ACCUMULATE if accumulate else 0) |
-             (OUT_F32 if out_dtype == torch.float32 else 0))
+             (OUT_F32 if out_dtype == torch.float32 else 0) |
+             (A_TRANSPOSED if a_transposed else 0))
     e = _epilogue(bias, activation, multiplier, m, n, batch)
     _check(lib.iree_mi355x_batch_matmul_f16(
         a3.data_ptr(), b3.data_ptr(), c3.data_ptr(), batch, m, n, k,
@@ -518,14 +538,23 @@ def matmul_mfma_config(index, a, b, c, *, scale=None, stream=None):
     """Run one compiled MFMA configuration (autotuner entry point).
 
     The configuration's B form decides how `b` is read: TN takes B [N, K],
-    NN takes B [K, N] f16, W8A16 takes B [K, N] int8 plus `scale`."""
+    NN takes B [K, N] f16, W8A16 takes B [K, N] int8 plus `scale`; a
+    transposed-A configuration takes A [K, M]."""
     import torch
     cfg = mfma_configs()[index]
-    m, k = a.shape
+    k, m = a.shape if cfg.a_transposed else a.shape[::-1]
     if cfg.b_form == B_FORM_TN:
         n, flags = b.shape[0], B_TRANSPOSED
     else:
         n, flags = b.shape[1], 0
+    if cfg.a_transposed:
+        flags |= A_TRANSPOSED
+    # The C-ABI sees only pointers: the extents it is given must be the
+    # tensors' own, or the kernel would stream past a buffer.
+    if (b.shape[1] if cfg.b_form == B_FORM_TN else b.shape[0]) != k:
+        raise ValueError(f"{cfg.name}: b does not contract over K = {k}")
+    if tuple(c.shape) != (m, n):
+        raise ValueError(f"{cfg.name}: c must be [{m}, {n}]")
     if c.dtype == torch.float32 and a.dtype == torch.float16:
         flags |= OUT_F32
     _check(library().iree_mi355x_matmul_mfma_config(

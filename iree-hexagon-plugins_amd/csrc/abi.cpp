@@ -130,9 +130,11 @@ static int check_matmul(const char *who, const void *a, const void *b,
   if (m == 0 || n == 0)
     return IREE_MI355X_OK;
   const bool bt = flags & IREE_MI355X_MATMUL_B_TRANSPOSED;
+  const bool at = flags & IREE_MI355X_MATMUL_A_TRANSPOSED;
   if (!c || (k > 0 && (!a || !b)))
     return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: null pointer", who);
-  if (lda < k || ldb < (bt ? k : n) || ldc < n || lda < 0 || ldb < 0)
+  if (lda < (at ? m : k) || ldb < (bt ? k : n) || ldc < n || lda < 0 ||
+      ldb < 0)
     return fail(IREE_MI355X_INVALID_ARGUMENT,
                 "%s: leading dimension smaller than the row", who);
   if ((a && !aligned(a, a_elem)) || (b && !aligned(b, b_elem)) ||
@@ -194,16 +196,22 @@ namespace ihp {
 static int matmul_f16_run(const char *who, MatmulArgs &args, uint32_t flags,
                           void *workspace, size_t workspace_bytes) {
   const bool out_f32 = flags & IREE_MI355X_MATMUL_OUT_F32;
+  args.a_transposed = (flags & IREE_MI355X_MATMUL_A_TRANSPOSED) ? 1 : 0;
+  if (args.a_transposed && args.m == 1 && args.lda == 1) {
+    // One row of a [K,1] A with unit pitch is the contiguous row [1,K]: the
+    // same matmul without the transpose (so M = 1 decode streams as GEMV).
+    args.a_transposed = 0;
+    args.lda = args.k;
+    flags &= ~IREE_MI355X_MATMUL_A_TRANSPOSED;
+  }
   iree_mi355x_matmul_desc_t desc;
   iree_mi355x_matmul_desc_init(&desc, IREE_MI355X_ELEM_F16,
                                IREE_MI355X_ELEM_F16,
                                out_f32 ? IREE_MI355X_ELEM_F32
                                        : IREE_MI355X_ELEM_F16,
                                args.m, args.n, args.k, flags);
-  desc.a_aligned16 = aligned(args.a, 16) && (args.lda * 2) % 16 == 0 &&
-                     (args.sa * 2) % 16 == 0;
-  desc.b_aligned16 = aligned(args.b, 16) && (args.ldb * 2) % 16 == 0 &&
-                     (args.sb * 2) % 16 == 0;
+  desc.a_aligned16 = fast_operand(args.a, args.lda * 2, args.sa * 2);
+  desc.b_aligned16 = fast_operand(args.b, args.ldb * 2, args.sb * 2);
   desc.batch = args.batch;
   iree_mi355x_matmul_plan_t plan;
   if (iree_mi355x_plan_matmul(&desc, &plan) != IREE_MI355X_OK)
@@ -246,7 +254,8 @@ int iree_mi355x_matmul_f16(const void *a, const void *b, void *c, int64_t m,
   int st = check_matmul("matmul_f16", a, b, c, m, n, k, lda, ldb, ldc, flags,
                         IREE_MI355X_MATMUL_B_TRANSPOSED |
                             IREE_MI355X_MATMUL_ACCUMULATE |
-                            IREE_MI355X_MATMUL_OUT_F32,
+                            IREE_MI355X_MATMUL_OUT_F32 |
+                            IREE_MI355X_MATMUL_A_TRANSPOSED,
                         2, 2, out_f32 ? 4 : 2);
   if (st != IREE_MI355X_OK || m == 0 || n == 0)
     return st == IREE_MI355X_OK ? ok() : st;
@@ -277,7 +286,8 @@ int iree_mi355x_batch_matmul_f16(const void *a, const void *b, void *c,
   int st = check_matmul(who, a, b, c, m, n, k, lda, ldb, ldc, flags,
                         IREE_MI355X_MATMUL_B_TRANSPOSED |
                             IREE_MI355X_MATMUL_ACCUMULATE |
-                            IREE_MI355X_MATMUL_OUT_F32,
+                            IREE_MI355X_MATMUL_OUT_F32 |
+                            IREE_MI355X_MATMUL_A_TRANSPOSED,
                         2, 2, out_f32 ? 4 : 2);
   if (st != IREE_MI355X_OK || m == 0 || n == 0 || batch == 0)
     return st == IREE_MI355X_OK ? ok() : st;
@@ -347,8 +357,8 @@ int iree_mi355x_matmul_i8(const int8_t *a, const int8_t *b, int32_t *c,
   iree_mi355x_matmul_desc_t desc;
   iree_mi355x_matmul_desc_init(&desc, IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_I8,
                                IREE_MI355X_ELEM_I32, m, n, k, flags);
-  desc.a_aligned16 = aligned(a, 16) && lda % 16 == 0;
-  desc.b_aligned16 = aligned(b, 16) && ldb % 16 == 0;
+  desc.a_aligned16 = fast_operand(a, lda);
+  desc.b_aligned16 = fast_operand(b, ldb);
   iree_mi355x_matmul_plan_t plan;
   if (iree_mi355x_plan_matmul(&desc, &plan) != IREE_MI355X_OK)
     return fail(IREE_MI355X_UNSUPPORTED, "matmul_i8: no plan");
@@ -377,8 +387,8 @@ int iree_mi355x_w8a16_matmul(const void *x, const int8_t *w, const void *scale,
   iree_mi355x_matmul_desc_t desc;
   iree_mi355x_matmul_desc_init(&desc, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_I8,
                                IREE_MI355X_ELEM_F16, m, n, k, flags);
-  desc.a_aligned16 = aligned(x, 16) && (ldx * 2) % 16 == 0;
-  desc.b_aligned16 = aligned(w, 16) && ldw % 16 == 0;
+  desc.a_aligned16 = fast_operand(x, ldx * 2);
+  desc.b_aligned16 = fast_operand(w, ldw);
   desc.has_scale = 1;
   iree_mi355x_matmul_plan_t plan;
   if (iree_mi355x_plan_matmul(&desc, &plan) != IREE_MI355X_OK)

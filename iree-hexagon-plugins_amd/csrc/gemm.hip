@@ -105,13 +105,18 @@ __device__ __forceinline__ void lgkm_tie2(i32x2 &v) {
   asm volatile("" : "+v"(v));
 }
 
+// AT: A is stored [K,M] (M-contiguous, the (d2, d0) indexing map of a
+// transposed LHS). Its K rows are staged like row-major f16 B and read with
+// the same transposed LDS reads: the A and B operands of the 32x32x16 MFMA
+// share one lane layout (lane % 32 = row / column, 8 * (lane / 32) = k run).
+//
 // SPLIT: the K extent is split over gridDim.y (k_split elements each); every
 // workgroup publishes an f32 (i32) partial tile and the last one to arrive at
 // a tile sums the partials in split order and writes C. M need not be a
 // multiple of BM: A rows past M are clamped to row M-1 on the copy side (rows
 // of C depend only on their own row of A) and never stored.
 template <typename T, typename OutT, int BM, int BN, int BKB, int WM, int WN,
-          int STAGES, int BMODE, bool SPLIT>
+          int STAGES, int BMODE, bool SPLIT, bool AT>
 __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     const T *__restrict__ A, const void *__restrict__ Bv, OutT *__restrict__ C,
     const f16 *__restrict__ scale, int M, int N, int K, int64_t lda,
@@ -130,7 +135,14 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   constexpr int CH = BKB / 16;              // chunks per staged A (TN B) row
   constexpr int ROWS_PER_WAVE = 64 / CH;
   constexpr int ROWS_PER_PASS = NT / CH;
-  constexpr int A_PASSES = BM / ROWS_PER_PASS;
+  // A staging: K-contiguous rows are M (BKB bytes each); AT rows are K
+  // (BM * 2 bytes each).
+  constexpr int AROW = AT ? BM * 2 : BKB;
+  constexpr int ACH = AROW / 16;
+  constexpr int A_ROWS = AT ? KE : BM;
+  constexpr int A_RPW = AT ? 64 / ACH : ROWS_PER_WAVE;  // rows per wave copy
+  constexpr int A_RPP = AT ? NT / ACH : ROWS_PER_PASS;  // rows per pass
+  constexpr int A_PASSES = A_ROWS / A_RPP;
   // B staging: TN rows are N (BKB bytes each); NN rows are K (BN*TBB bytes).
   constexpr int BROW = kNN ? BN * TBB : BKB;
   constexpr int BCH = BROW / 16;
@@ -145,8 +157,12 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   // LDS reads per K step: FM A fragments, FN B fragments (two transposed
   // reads each for f16 NN).
   constexpr int B_READS = BMODE == kBNN16 ? 2 * FN : FN;
-  constexpr int RD = FM + B_READS;
-  static_assert(BM % ROWS_PER_PASS == 0 && B_ROWS % B_RPP == 0, "tile");
+  constexpr int A_READS = AT ? 2 * FM : FM;
+  constexpr int RD = A_READS + B_READS;
+  static_assert(A_ROWS % A_RPP == 0 && B_ROWS % B_RPP == 0, "tile");
+  static_assert(!AT || (sizeof(T) == 2 && !SPLIT && ACH >= 16 &&
+                        A_RPP % 8 == 0 && A_RPW <= 8),
+                "transposed A: f16, exact M tiling, BM >= 128");
   static_assert(B_RPP * BCH == NT && B_RPW * BCH == 64, "B copy shape");
   static_assert(FM >= 1 && FN >= 1 && (CH == 4 || CH == 8), "tile");
   static_assert(KSTEPS % 2 == 0, "fragment double buffer parity");
@@ -202,6 +218,14 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   const int64_t ldb_b = ldb * (int64_t)TBB;
   // A row of each copy pass, clamped to the last row of A (split mode).
   uint32_t a_lane[A_PASSES];
+  if constexpr (AT) {
+    // Same copy shape as row-major B: lane -> (k row, swizzled chunk).
+    const int krow = wave * A_RPW + lane / ACH;
+    const int chunk = (lane % ACH) ^ nn_swizzle<kBNN16>(krow);
+#pragma unroll
+    for (int p = 0; p < A_PASSES; ++p)
+      a_lane[p] = (uint32_t)((p * A_RPP + krow) * lda_b + chunk * 16);
+  } else {
 #pragma unroll
   for (int p = 0; p < A_PASSES; ++p) {
     int64_t row = m0 + p * ROWS_PER_PASS + wave * ROWS_PER_WAVE + ld_row;
@@ -209,8 +233,10 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
       row = M - 1;
     a_lane[p] = (uint32_t)((row - m0) * lda_b + ld_chunk * 16);
   }
+  }
   const char *a_base =
-      (const char *)A + m0 * lda_b + k_begin * (int64_t)sizeof(T);
+      AT ? (const char *)A + m0 * (int64_t)sizeof(T) + k_begin * lda_b
+         : (const char *)A + m0 * lda_b + k_begin * (int64_t)sizeof(T);
   uint32_t b_lane;
   const char *b_base;
   if constexpr (kNN) {
@@ -230,9 +256,13 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     IHP_LDS char *dst = lds + slot * STAGE_BYTES;
     const int64_t ka = (int64_t)kt * BKB;
     if (p < A_PASSES) {
-      global_to_lds_16(a_base + ka + a_lane[p],
-                       dst + wave * ROWS_PER_WAVE * BKB +
-                           p * ROWS_PER_PASS * BKB);
+      if constexpr (AT)
+        global_to_lds_16(a_base + (int64_t)kt * KE * lda_b + a_lane[p],
+                         dst + wave * A_RPW * AROW + p * A_RPP * AROW);
+      else
+        global_to_lds_16(a_base + ka + a_lane[p],
+                         dst + wave * ROWS_PER_WAVE * BKB +
+                             p * ROWS_PER_PASS * BKB);
     } else {
       const int q = p - A_PASSES;
       if constexpr (kNN) {
@@ -268,6 +298,18 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     koff[ks] = ((2 * ks) ^ rd_sw) * 16;
   const int a_rd = (wm * WTM + rd_row) * BKB;
   const int b_rd = A_BYTES + (wn * WTN + rd_row) * BKB;
+  // Read side, transposed A: the row-major B offsets below with M for N.
+  int a_nn[FM];
+  if constexpr (AT) {
+    const int blk = lane >> 4, jj = lane & 15;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int k = 8 * (blk >> 1) + (jj >> 2);
+      const int byte = 2 * (wm * WTM + i * 32 + 16 * (blk & 1) + 4 * (jj & 3));
+      a_nn[i] = k * AROW +
+                (((byte >> 4) ^ nn_swizzle<kBNN16>(k)) << 4) + (byte & 15);
+    }
+  }
   // Read side, NN B: per-lane byte offset of fragment j within a stage for
   // K step 0 (a K step adds 16 rows; the swizzle repeats every 4 or 8).
   int b_nn[FN];
@@ -299,13 +341,23 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     i32x4 a[FM];
     i32x4 b[FN];
     i32x2 t[BMODE == kBNN16 ? 2 * FN : FN];
+    i32x2 ta[AT ? 2 * FM : 1];
   };
   auto read_frags = [&](int slot, int ks, Frags &f) {
     const IHP_LDS char *st = lds + slot * STAGE_BYTES;
-    const IHP_LDS char *pa = st + a_rd + koff[ks];
-    static_for<FM>([&](auto i) {
-      f.a[i] = lds_read_16_async<decltype(i)::value * 32 * BKB>(pa);
-    });
+    if constexpr (AT) {
+      const IHP_LDS char *pa = st + ks * 16 * AROW;
+      static_for<FM>([&](auto i) {
+        constexpr int I = decltype(i)::value;
+        f.ta[2 * I] = lds_read_tr16_async<0>(pa + a_nn[I]);
+        f.ta[2 * I + 1] = lds_read_tr16_async<4 * AROW>(pa + a_nn[I]);
+      });
+    } else {
+      const IHP_LDS char *pa = st + a_rd + koff[ks];
+      static_for<FM>([&](auto i) {
+        f.a[i] = lds_read_16_async<decltype(i)::value * 32 * BKB>(pa);
+      });
+    }
     if constexpr (BMODE == kBTN) {
       const IHP_LDS char *pb = st + b_rd + koff[ks];
       static_for<FN>([&](auto j) {
@@ -328,9 +380,19 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   // assemble NN B operands from the transposed reads.
   auto frags_ready = [&](auto n, Frags &f) {
     lgkm_wait<decltype(n)::value>();
+    if constexpr (AT) {
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
-      lgkm_tie(f.a[i]);
+      for (int i = 0; i < FM; ++i) {
+        lgkm_tie2(f.ta[2 * i]);
+        lgkm_tie2(f.ta[2 * i + 1]);
+        f.a[i] = i32x4{f.ta[2 * i][0], f.ta[2 * i][1], f.ta[2 * i + 1][0],
+                       f.ta[2 * i + 1][1]};
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        lgkm_tie(f.a[i]);
+    }
     if constexpr (BMODE == kBTN) {
 #pragma unroll
       for (int j = 0; j < FN; ++j)
@@ -595,7 +657,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
 }
 
 // ----------------------------------------------------------------------------
-// General path: any extents, strides and B layout; bounds-checked element
+// General path: any extents, strides, A and B layout; bounds-checked element
 // loads staged through registers into LDS (B converted to the MFMA input type
 // on the way, which is where W8A16 dequantizes), 64x64 tiles, 4 waves of
 // 32x32 fragments, optional per-column scale in the epilogue.
@@ -606,7 +668,7 @@ __global__ __launch_bounds__(256) void gemm_general_kernel(
     const TA *__restrict__ A, const TB *__restrict__ B, OutT *__restrict__ C,
     const f16 *__restrict__ scale, int M, int N, int K, int64_t lda,
     int64_t ldb, int64_t ldc, int b_transposed, int accumulate, int64_t sa,
-    int64_t sb, int64_t sc, Epi epi, int64_t s_mul) {
+    int64_t sb, int64_t sc, Epi epi, int64_t s_mul, int a_transposed) {
   {
     const int64_t z = blockIdx.z;
     A += z * sa;
@@ -634,13 +696,23 @@ __global__ __launch_bounds__(256) void gemm_general_kernel(
   const int ld_r = tid / 4, ld_c = (tid % 4) * EPT;
 
   for (int k0 = 0; k0 < K; k0 += KE) {
-    {  // A rows
+    if (!a_transposed) {  // A rows are M
       TM *dst = (TM *)(As + ld_r * ROWB) + ld_c;
       const int64_t m = m0 + ld_r;
 #pragma unroll
       for (int e = 0; e < EPT; ++e) {
         const int k = k0 + ld_c + e;
         dst[e] = (m < M && k < K) ? (TM)A[m * lda + k] : (TM)0;
+      }
+    } else {  // A [K,M]: m fastest across threads, staged transposed
+      const int mm = tid & 63, kq = tid >> 6;
+      constexpr int KPT = KE / 4;
+      TM *dst = (TM *)(As + mm * ROWB) + kq * KPT;
+      const int64_t m = m0 + mm;
+#pragma unroll
+      for (int e = 0; e < KPT; ++e) {
+        const int k = k0 + kq * KPT + e;
+        dst[e] = (m < M && k < K) ? (TM)A[(int64_t)k * lda + m] : (TM)0;
       }
     }
     if (b_transposed) {  // B rows are N
@@ -701,7 +773,7 @@ __global__ __launch_bounds__(256) void gemm_general_kernel(
 // ----------------------------------------------------------------------------
 
 template <typename T, typename OutT, int BM, int BN, int BKB, int WM, int WN,
-          int STAGES, int BMODE, bool SPLIT>
+          int STAGES, int BMODE, bool SPLIT, bool AT>
 static hipError_t launch_fast(const MatmulArgs &a) {
   typedef typename Mfma32<T>::AccScalar P;
   const int64_t tiles_m = SPLIT ? (a.m + BM - 1) / BM : a.m / BM;
@@ -713,7 +785,8 @@ static hipError_t launch_fast(const MatmulArgs &a) {
                               split_counter_bytes(tiles))
                       : nullptr;
   hipLaunchKernelGGL(
-      (gemm_lds_kernel<T, OutT, BM, BN, BKB, WM, WN, STAGES, BMODE, SPLIT>),
+      (gemm_lds_kernel<T, OutT, BM, BN, BKB, WM, WN, STAGES, BMODE, SPLIT,
+                       AT>),
       dim3(tiles, splits, (unsigned)a.batch), dim3(64 * WM * WN), 0,
       (hipStream_t)a.stream, (const T *)a.a, a.b, (OutT *)a.c,
       (const f16 *)a.scale, (int)a.m, (int)a.n, (int)a.k, a.lda, a.ldb, a.ldc,
@@ -723,11 +796,17 @@ static hipError_t launch_fast(const MatmulArgs &a) {
 }
 
 #define IHP_FAST_CONFIG(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST)           \
-  IHP_FAST_CONFIG_S(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, false)
+  IHP_FAST_CONFIG_X(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, false, false)
 #define IHP_FAST_CONFIG_S(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, SPLIT)  \
+  IHP_FAST_CONFIG_X(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, SPLIT, false)
+#define IHP_FAST_CONFIG_AT(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST)        \
+  IHP_FAST_CONFIG_X(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, false, true)
+#define IHP_FAST_CONFIG_X(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, SPLIT,  \
+                          AT)                                                 \
   {NAME,                                                                      \
    MODE,                                                                      \
    SPLIT,                                                                     \
+   AT,                                                                        \
    sizeof(T) == 1 ? kElemI8 : kElemF16,                                       \
    sizeof(OUT) == 4 && sizeof(T) == 2,                                        \
    BM,                                                                        \
@@ -738,7 +817,7 @@ static hipError_t launch_fast(const MatmulArgs &a) {
    ST * (BM * BKB + (MODE == kBTN ? BN * BKB                                  \
                                   : (BKB / (int)sizeof(T)) * BN *             \
                                         (MODE == kBW8 ? 1 : (int)sizeof(T)))),\
-   &launch_fast<T, OUT, BM, BN, BKB, WM, WN, ST, MODE, SPLIT>}
+   &launch_fast<T, OUT, BM, BN, BKB, WM, WN, ST, MODE, SPLIT, AT>}
 
 // Every compiled fast-path configuration. The planner picks among these by
 // its LDS-budget ranking or a measured table entry; bench.py --tune times
@@ -777,6 +856,14 @@ static const FastConfig kFastConfigs[] = {
     IHP_FAST_CONFIG_S("f16_tn_128x128x64_w2x2_s4_sk", kBTN, f16, f16, 128, 128, 128, 2, 2, 4, true),
     IHP_FAST_CONFIG_S("w8a16_nn_32x256x64_w1x4_s4_sk", kBW8, f16, f16, 32, 256, 128, 1, 4, 4, true),
     IHP_FAST_CONFIG_S("w8a16_nn_128x256x64_w2x4_s4_sk", kBW8, f16, f16, 128, 256, 128, 2, 4, 4, true),
+    // transposed A ([K,M], M-contiguous), either B form
+    IHP_FAST_CONFIG_AT("f16at_nn_256x256x64_w2x4_s2", kBNN16, f16, f16, 256, 256, 128, 2, 4, 2),
+    IHP_FAST_CONFIG_AT("f16at_nn_256x128x64_w2x4_s2", kBNN16, f16, f16, 256, 128, 128, 2, 4, 2),
+    IHP_FAST_CONFIG_AT("f16at_nn_128x128x64_w2x2_s4", kBNN16, f16, f16, 128, 128, 128, 2, 2, 4),
+    IHP_FAST_CONFIG_AT("f16at_tn_256x256x64_w2x4_s2", kBTN, f16, f16, 256, 256, 128, 2, 4, 2),
+    IHP_FAST_CONFIG_AT("f16at_tn_128x128x64_w2x2_s4", kBTN, f16, f16, 128, 128, 128, 2, 2, 4),
+    IHP_FAST_CONFIG_AT("f16f32at_nn_128x128x64_w2x2_s4", kBNN16, f16, float, 128, 128, 128, 2, 2, 4),
+    IHP_FAST_CONFIG_AT("f16f32at_tn_128x128x64_w2x2_s4", kBTN, f16, float, 128, 128, 128, 2, 2, 4),
 };
 
 const FastConfig *fast_configs(int *count) {
@@ -793,7 +880,7 @@ static hipError_t launch_general_t(const MatmulArgs &a, const void *scale) {
                      (const TB *)a.b, (OutT *)a.c, (const f16 *)scale,
                      (int)a.m, (int)a.n, (int)a.k, a.lda, a.ldb, a.ldc,
                      a.b_transposed, a.accumulate, a.sa, a.sb, a.sc,
-                     make_epi(a), epi_batch_stride(a));
+                     make_epi(a), epi_batch_stride(a), a.a_transposed);
   return hipGetLastError();
 }
 

@@ -43,6 +43,7 @@ struct MatmulArgs {
   const void *mul = nullptr;   // f16 [M, N] per batch, row pitch ld_mul
   int64_t ld_mul = 0, s_mul = 0;
   int act = 0;                 // kActNone / kActRelu / kActGeluTanh / kActSilu
+  int a_transposed = 0;        // A stored [K,M] (lda >= M)
 };
 
 enum Activation { kActNone = 0, kActRelu = 1, kActGeluTanh = 2, kActSilu = 3 };
@@ -77,6 +78,17 @@ inline size_t split_counter_bytes(int64_t tiles) {
   return kWorkspaceCounterBytes;
 }
 
+// An operand the fast (LDS-DMA) kernels can stream: 16-byte aligned base,
+// row pitch and batch stride, and a row pitch below 8 MiB, so that a
+// macro-tile's lane offsets (at most 256 rows of pitch) fit the 32-bit
+// offsets of the copy side. Any other operand takes the general kernel.
+constexpr int64_t kMaxFastPitchBytes = (int64_t)1 << 23;
+inline bool fast_operand(const void *p, int64_t ld_bytes,
+                         int64_t batch_stride_bytes = 0) {
+  return (uintptr_t)p % 16 == 0 && ld_bytes % 16 == 0 &&
+         ld_bytes < kMaxFastPitchBytes && batch_stride_bytes % 16 == 0;
+}
+
 typedef hipError_t (*FastLaunchFn)(const MatmulArgs &);
 
 // A compiled fast-path (LDS-DMA MFMA) GEMM configuration.
@@ -84,6 +96,7 @@ struct FastConfig {
   const char *name;
   int b_mode;    // BMode
   int split_k;   // K split over grid.y, M may be ragged (skinny shapes)
+  int a_trans;   // A stored [K,M] (f16 only, exact tiling)
   int elem;      // ElemKind of A (and of B unless kBW8)
   int out_f32;   // f16 path: f32 output (i8 path: always i32)
   int bm, bn;    // macro-tile

@@ -61,8 +61,11 @@ int check_matmul_bindings(const iree_mi355x_executable_dispatch_state_t *s,
                           const MatmulConsts &c, int64_t ab, int64_t bb,
                           int64_t cb, int c_index, const char *who) {
   const bool bt = c.flags & IREE_MI355X_MATMUL_B_TRANSPOSED;
+  const bool at = c.flags & IREE_MI355X_MATMUL_A_TRANSPOSED;
   int st;
-  if ((st = check_binding(s, 0, span(c.m, c.k, c.lda, ab), who)) ||
+  if ((st = check_binding(
+           s, 0, at ? span(c.k, c.m, c.lda, ab) : span(c.m, c.k, c.lda, ab),
+           who)) ||
       (st = check_binding(
            s, 1, bt ? span(c.n, c.k, c.ldb, bb) : span(c.k, c.n, c.ldb, bb),
            who)) ||
@@ -162,13 +165,17 @@ int dispatch_batch_matmul(const iree_mi355x_executable_environment_t *,
       s_mul < 0)
     return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: bindings or strides", who);
   const bool bt = c.flags & IREE_MI355X_MATMUL_B_TRANSPOSED;
+  const bool at = c.flags & IREE_MI355X_MATMUL_A_TRANSPOSED;
   const int64_t cb = (c.flags & IREE_MI355X_MATMUL_OUT_F32) ? 4 : 2;
   const int64_t last = batch > 0 ? batch - 1 : 0;
   auto batched = [&](int64_t stride, int64_t one, int64_t elem) {
     return one > 0 ? last * stride * elem + one : 0;
   };
-  if ((st = check_binding(s, 0, batched(sa, span(c.m, c.k, c.lda, 2), 2),
-                          who)) ||
+  if ((st = check_binding(
+           s, 0,
+           batched(sa, at ? span(c.k, c.m, c.lda, 2) : span(c.m, c.k, c.lda, 2),
+                   2),
+           who)) ||
       (st = check_binding(
            s, 1,
            batched(sb, bt ? span(c.n, c.k, c.ldb, 2) : span(c.k, c.n, c.ldb, 2),

@@ -70,7 +70,9 @@ bool types_supported(const iree_mi355x_matmul_desc_t &d) {
 
 bool gemv_eligible(const iree_mi355x_matmul_desc_t &d) {
   if (d.m < 1 || d.m > kGemvMaxRows || d.k < 1 ||
-      (d.flags & IREE_MI355X_MATMUL_B_TRANSPOSED) || !d.b_aligned16)
+      (d.flags & (IREE_MI355X_MATMUL_B_TRANSPOSED |
+                  IREE_MI355X_MATMUL_A_TRANSPOSED)) ||
+      !d.b_aligned16)
     return false;
   const int cols = 16 / elem_bytes(d.b_elem);
   if (d.n % cols != 0)
@@ -109,6 +111,8 @@ bool fast_fits(const iree_mi355x_matmul_desc_t &d, const FastConfig &c) {
   if (!d.a_aligned16 || !d.b_aligned16 || d.k <= 0 || d.m <= 0)
     return false;
   if (c.b_mode != wanted_b_mode(d))
+    return false;
+  if (c.a_trans != ((d.flags & IREE_MI355X_MATMUL_A_TRANSPOSED) ? 1 : 0))
     return false;
   const int want_elem = d.a_elem == IREE_MI355X_ELEM_I8 ? kElemI8 : kElemF16;
   if (c.elem != want_elem)
@@ -415,6 +419,18 @@ int iree_mi355x_mfma_config_info(int index, const char **name,
   return IREE_MI355X_OK;
 }
 
+int32_t iree_mi355x_mfma_config_layout_flags(int index) {
+  int count = 0;
+  const FastConfig *cfgs = fast_configs(&count);
+  if (index < 0 || index >= count)
+    return -1;
+  return (int32_t)((cfgs[index].b_mode == kBTN
+                        ? IREE_MI355X_MATMUL_B_TRANSPOSED
+                        : 0u) |
+                   (cfgs[index].a_trans ? IREE_MI355X_MATMUL_A_TRANSPOSED
+                                        : 0u));
+}
+
 int iree_mi355x_matmul_mfma_config(int index, const void *a, const void *b,
                                    const void *scale, void *c, int64_t m,
                                    int64_t n, int64_t k, int64_t lda,
@@ -437,13 +453,14 @@ int iree_mi355x_matmul_mfma_config(int index, const void *a, const void *b,
   iree_mi355x_matmul_desc_init(&d, ae, be, ce, m, n, k, flags);
   d.has_scale = cfg.b_mode == kBW8;
   const int64_t aeb = elem_bytes(ae), beb = elem_bytes(be);
-  d.a_aligned16 = a && ((uintptr_t)a % 16 == 0) && (lda * aeb) % 16 == 0;
-  d.b_aligned16 = b && ((uintptr_t)b % 16 == 0) && (ldb * beb) % 16 == 0;
+  d.a_aligned16 = a && fast_operand(a, lda * aeb);
+  d.b_aligned16 = b && fast_operand(b, ldb * beb);
   const bool bt = flags & IREE_MI355X_MATMUL_B_TRANSPOSED;
+  const bool at = flags & IREE_MI355X_MATMUL_A_TRANSPOSED;
   if (flags & ~(IREE_MI355X_MATMUL_B_TRANSPOSED | IREE_MI355X_MATMUL_ACCUMULATE |
-                IREE_MI355X_MATMUL_OUT_F32))
+                IREE_MI355X_MATMUL_OUT_F32 | IREE_MI355X_MATMUL_A_TRANSPOSED))
     return fail(IREE_MI355X_INVALID_ARGUMENT, "mfma_config: unknown flags");
-  if (!c || (uintptr_t)c % elem_bytes(ce) != 0 || lda < k ||
+  if (!c || (uintptr_t)c % elem_bytes(ce) != 0 || lda < (at ? m : k) ||
       ldb < (bt ? k : n) || ldc < n || m >= ((int64_t)1 << 31) ||
       n >= ((int64_t)1 << 31) || k >= ((int64_t)1 << 31) ||
       (d.has_scale && (!scale || (uintptr_t)scale % 2 != 0)))
@@ -461,6 +478,7 @@ int iree_mi355x_matmul_mfma_config(int index, const void *a, const void *b,
   MatmulArgs args{a, b, c, m, n, k, lda, ldb, ldc, bt ? 1 : 0,
                   (flags & IREE_MI355X_MATMUL_ACCUMULATE) ? 1 : 0, stream,
                   scale, cand.splits, cand.k_split, ws};
+  args.a_transposed = at ? 1 : 0;
   hipError_t e = cfg.launch(args);
   if (e != hipSuccess)
     return fail(IREE_MI355X_LAUNCH_FAILED, "%s: %s", cfg.name,

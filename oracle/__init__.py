@@ -23,6 +23,7 @@ _lib = None
 B_TRANSPOSED = 1
 ACCUMULATE = 2
 OUT_F32 = 4
+A_TRANSPOSED = 8
 
 
 def build() -> None:
@@ -97,22 +98,26 @@ def f32_to_f16(x: np.ndarray) -> np.ndarray:
 
 
 def matmul_f16(a, b, c_init=None, *, b_transposed=False, out_f32=False,
-               threads=None) -> np.ndarray:
-    """C = [C_init +] A.B with f16 inputs, f32 accumulation, f16/f32 output."""
+               a_transposed=False, threads=None) -> np.ndarray:
+    """C = [C_init +] A.B with f16 inputs, f32 accumulation, f16/f32 output.
+    a is [M, K], or [K, M] with ``a_transposed``; b is [K, N], or [N, K] with
+    ``b_transposed``."""
     a = np.ascontiguousarray(a, np.float16)
     b = np.ascontiguousarray(b, np.float16)
-    m, k = a.shape
+    k, m = a.shape if a_transposed else a.shape[::-1]
     n = b.shape[0] if b_transposed else b.shape[1]
     assert (b.shape[1] if b_transposed else b.shape[0]) == k
     dt = np.float32 if out_f32 else np.float16
-    flags = (B_TRANSPOSED if b_transposed else 0) | (OUT_F32 if out_f32 else 0)
+    flags = ((B_TRANSPOSED if b_transposed else 0) |
+             (OUT_F32 if out_f32 else 0) |
+             (A_TRANSPOSED if a_transposed else 0))
     if c_init is not None:
         c = np.array(c_init, dtype=dt, copy=True, order="C")
         flags |= ACCUMULATE
     else:
         c = np.empty((m, n), dt)
-    rc = _load().oracle_matmul_f16(_ptr(a), _ptr(b), _ptr(c), m, n, k, k,
-                                   b.shape[1], n, flags,
+    rc = _load().oracle_matmul_f16(_ptr(a), _ptr(b), _ptr(c), m, n, k,
+                                   a.shape[1], b.shape[1], n, flags,
                                    threads or default_threads())
     assert rc == 0, rc
     return c

@@ -99,8 +99,11 @@ int oracle_matmul_f16(const uint16_t *a, const uint16_t *b, void *c,
   if (bad_dims(m, n, k))
     return 1;
   const int transposed = (flags & ORACLE_B_TRANSPOSED) != 0;
+  const int a_t = (flags & ORACLE_A_TRANSPOSED) != 0;
   const int accumulate = (flags & ORACLE_ACCUMULATE) != 0;
   const int out_f32 = (flags & ORACLE_OUT_F32) != 0;
+  /* A [K,M] (transposed LHS): element (m, k) at k * lda + m. */
+  const int64_t a_rs = a_t ? 1 : lda, a_ks = a_t ? lda : 1;
   float *bf = widen_b_f16(b, n, k, ldb, transposed);
   if (!bf)
     return 2;
@@ -110,7 +113,7 @@ int oracle_matmul_f16(const uint16_t *a, const uint16_t *b, void *c,
   for (int64_t mm = 0; mm < m; ++mm) {
     float *acc = (float *)calloc((size_t)n + 1, sizeof(float));
     for (int64_t kk = 0; kk < k; ++kk) {
-      const float av = oracle_f16_to_f32(a[mm * lda + kk]);
+      const float av = oracle_f16_to_f32(a[mm * a_rs + kk * a_ks]);
       const float *brow = bf + kk * n;
       for (int64_t nn = 0; nn < n; ++nn) {
         float prod = av * brow[nn];
@@ -170,9 +173,10 @@ int oracle_batch_matmul_f16(const uint16_t *a, const uint16_t *b, void *c,
     return 2;
   for (int64_t z = 0; z < batch; ++z) {
     /* f32 sums of this batch: the plain matmul into an f32 scratch */
-    int rc = oracle_matmul_f16(a + z * sa, b + z * sb, acc, m, n, k, lda, ldb,
-                               n, (flags & ORACLE_B_TRANSPOSED) | ORACLE_OUT_F32,
-                               threads);
+    int rc = oracle_matmul_f16(
+        a + z * sa, b + z * sb, acc, m, n, k, lda, ldb, n,
+        (flags & (ORACLE_B_TRANSPOSED | ORACLE_A_TRANSPOSED)) | ORACLE_OUT_F32,
+        threads);
     if (rc) {
       free(acc);
       return rc;

@@ -14,7 +14,9 @@
  *   half conversions      exhaustive vs numpy float16
  *   matmul_i8             brute force int64 numpy, closed-form overflow bound
  *   matmul_f16            torch.matmul(a.float(), b.float()) (the reference
- *                         micro model), exact small-integer cases, identity
+ *                         micro model), exact small-integer cases, identity;
+ *                         A / B transposed = the plain form of the
+ *                         transposed copies, bit for bit
  *   w8a16                 per-element-dequant form, exact power-of-two cases
  *   attention             torch F.scaled_dot_product_attention (the reference
  *                         micro attention model) in f32, causal invariants
@@ -57,10 +59,13 @@ void oracle_f32_to_f16_array(const float *src, uint16_t *dst, int64_t n);
 #define ORACLE_B_TRANSPOSED 1u /* B stored [N,K] (indexing map (d1,d2)) */
 #define ORACLE_ACCUMULATE 2u   /* C_out = C_init + A.B (DPS init is read) */
 #define ORACLE_OUT_F32 4u      /* f32 output, else f16 */
+#define ORACLE_A_TRANSPOSED 8u /* A stored [K,M] (indexing map (d2,d0)) */
 
 /* linalg.matmul f16 x f16 with f32 accumulation (arith.extf on the inputs),
  * C_out = C_init + sum_k A[m,k]*B[k,n], summed in k order in f32.
- * examples/matmul/matmul.mlir:1-14, UK/hmx.c:328-357 (add into init). */
+ * examples/matmul/matmul.mlir:1-14, UK/hmx.c:328-357 (add into init); the
+ * transposed-operand maps of LIT/codegen/transforms/
+ * convert_matmul_to_hmx.mlir:60-115 via ORACLE_A/B_TRANSPOSED. */
 int oracle_matmul_f16(const uint16_t *a, const uint16_t *b, void *c,
                       int64_t m, int64_t n, int64_t k, int64_t lda,
                       int64_t ldb, int64_t ldc, uint32_t flags, int threads);

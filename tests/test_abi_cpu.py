@@ -297,3 +297,76 @@ def test_batch_planner_and_workspace(pkg):
     w4 = lib.iree_mi355x_batch_matmul_workspace_bytes(4, 1, 4096, 4096, 0)
     assert w1 == pkg.plan(pkg.make_desc(0, 0, 0, 1, 4096, 4096, 0)).workspace_bytes
     assert w4 > 64 * 1024 and w1 > 64 * 1024
+
+
+# ------------------------------------------------------ transposed A ----
+
+def test_transposed_a_planning(pkg):
+    """A stored [K, M]: exact tiles take a transposed-A MFMA configuration of
+    the same B form; ragged, skinny or misaligned shapes take the general
+    kernel (never the GEMV, which streams A by rows)."""
+    AT, BT = pkg.A_TRANSPOSED, pkg.B_TRANSPOSED
+    for flags, form in ((AT, pkg.B_FORM_NN), (AT | BT, pkg.B_FORM_TN)):
+        p = pkg.plan(pkg.make_desc(F16, F16, F16, 4096, 4096, 4096, flags))
+        assert p.family == pkg.FAMILY_MFMA
+        cfg = pkg.mfma_configs()[p.config_index]
+        assert cfg.a_transposed and cfg.b_form == form
+        assert pkg.plan(pkg.make_desc(F16, F16, F16, 64, 128, 96,
+                                      flags)).family == pkg.FAMILY_GENERAL
+        assert pkg.plan(pkg.make_desc(F16, F16, F16, 2, 4096, 4096,
+                                      flags)).family == pkg.FAMILY_GENERAL
+    # f32 output has transposed-A tiles too
+    p = pkg.plan(pkg.make_desc(F16, F16, pkg.ELEM_F32, 512, 512, 512, AT))
+    assert p.family == pkg.FAMILY_MFMA
+    assert pkg.mfma_configs()[p.config_index].a_transposed
+    # a plain-A dispatch never takes a transposed-A configuration
+    for m, n, k in ((4096, 4096, 4096), (512, 512, 512), (256, 256, 128)):
+        for flags in (0, BT):
+            p = pkg.plan(pkg.make_desc(F16, F16, F16, m, n, k, flags))
+            assert not pkg.mfma_configs()[p.config_index].a_transposed
+
+
+def test_config_layout_flags(pkg):
+    lib = pkg.library()
+    cfgs = pkg.mfma_configs()
+    assert any(c.a_transposed for c in cfgs)
+    for c in cfgs:
+        lf = lib.iree_mi355x_mfma_config_layout_flags(c.index)
+        assert bool(lf & pkg.B_TRANSPOSED) == (c.b_form == pkg.B_FORM_TN)
+        assert bool(lf & pkg.A_TRANSPOSED) == ("at_" in c.name)
+        if c.a_transposed:
+            assert c.a_elem == F16 and c.tile_m >= 128
+    assert lib.iree_mi355x_mfma_config_layout_flags(len(cfgs)) == -1
+    assert lib.iree_mi355x_mfma_config_layout_flags(-1) == -1
+
+
+def test_transposed_a_argument_checks(pkg):
+    lib = pkg.library()
+    AT = pkg.A_TRANSPOSED
+    # A [K, M] needs lda >= M (here M = 64 > lda = 32), not lda >= K
+    assert call_f16(lib, flags=AT, lda=32) == pkg.INVALID_ARGUMENT
+    # integer and W8A16 entry points take no transposed A
+    assert lib.iree_mi355x_matmul_i8(FAKE, FAKE, FAKE, 8, 8, 8, 8, 8, 8, AT,
+                                     None) == pkg.INVALID_ARGUMENT
+    assert lib.iree_mi355x_w8a16_matmul(FAKE, FAKE, FAKE, FAKE, 1, 64, 64, 64,
+                                        64, 64, AT, None, 0,
+                                        None) == pkg.INVALID_ARGUMENT
+    # a configuration and the layout flags must agree
+    at_cfg = [c for c in pkg.mfma_configs()
+              if c.a_transposed and c.b_form == pkg.B_FORM_NN][0]
+    f = lib.iree_mi355x_matmul_mfma_config
+    assert f(at_cfg.index, FAKE, FAKE, None, FAKE, 256, 256, 256, 256, 256,
+             256, 0, None) == pkg.UNSUPPORTED
+
+
+def test_fast_path_pitch_limit(pkg):
+    """A row pitch of 8 MiB or more would overflow the 32-bit lane offsets of
+    the fast kernels' copy side: such operands are not fast-path eligible."""
+    lib = pkg.library()
+    cfg = [c for c in pkg.mfma_configs() if c.name == "f16_nn_128x128x64_w2x2_s4"][0]
+    f = lib.iree_mi355x_matmul_mfma_config
+    big = (1 << 22)  # f16 elements: an 8 MiB row
+    assert f(cfg.index, FAKE, FAKE, None, FAKE, 128, 128, 64, big, 128, 128, 0,
+             None) == pkg.UNSUPPORTED
+    assert f(cfg.index, FAKE, FAKE, None, FAKE, 128, 128, 64, 128, big, 128, 0,
+             None) == pkg.UNSUPPORTED

@@ -84,7 +84,8 @@ def test_matmul_f16_tn_configs(pkg, oracle, dev, shape):
                               out_f32=True)
     ran = 0
     for cfg in pkg.mfma_configs():
-        if cfg.a_elem != pkg.ELEM_F16 or cfg.b_form != pkg.B_FORM_TN:
+        if (cfg.a_elem != pkg.ELEM_F16 or cfg.b_form != pkg.B_FORM_TN
+                or cfg.a_transposed):
             continue
         if m % cfg.tile_m or n % cfg.tile_n or k % cfg.tile_k:
             continue
@@ -108,7 +109,7 @@ def test_matmul_f16_nn_configs(pkg, oracle, dev, shape):
     ref32 = oracle.matmul_f16(a.numpy(), b.numpy(), out_f32=True)
     ran = 0
     for cfg in pkg.mfma_configs():
-        if cfg.b_form != pkg.B_FORM_NN:
+        if cfg.b_form != pkg.B_FORM_NN or cfg.a_transposed:
             continue
         if m % cfg.tile_m or n % cfg.tile_n or k % cfg.tile_k:
             continue
@@ -600,3 +601,89 @@ def test_batch_matmul_argument_errors(pkg, dev):
                                           2, 8, 8, 8, 8, 8, 8, 64, 64, 64, 0,
                                           ctypes.byref(e), None, 0, None)
     assert st == 1
+
+
+# ------------------------------------------------------------ transposed A --
+
+@pytest.mark.parametrize("shape", [(256, 256, 128), (512, 512, 256),
+                                   (256, 768, 192)])
+def test_transposed_a_configs(pkg, oracle, dev, shape):
+    """Every transposed-A macro-tile (A stored [K, M]) with both B forms."""
+    m, n, k = shape
+    g = torch.Generator().manual_seed(3 * m + n + k)
+    a = torch.randn(m, k, generator=g).half()
+    b = torch.randn(k, n, generator=g).half()
+    at, bt = a.t().contiguous(), b.t().contiguous()
+    ref16 = oracle.matmul_f16(a.numpy(), b.numpy())
+    ref32 = oracle.matmul_f16(a.numpy(), b.numpy(), out_f32=True)
+    ran = 0
+    for cfg in pkg.mfma_configs():
+        if not cfg.a_transposed:
+            continue
+        if m % cfg.tile_m or n % cfg.tile_n or k % cfg.tile_k:
+            continue
+        out32 = cfg.c_elem == pkg.ELEM_F32
+        c = torch.empty(m, n, dtype=torch.float32 if out32 else torch.float16,
+                        device=dev)
+        bb = bt if cfg.b_form == pkg.B_FORM_TN else b
+        pkg.matmul_mfma_config(cfg.index, at.to(dev), bb.to(dev), c)
+        fp16_ok(oracle, c.cpu().numpy(), ref32 if out32 else ref16)
+        ran += 1
+    assert ran > 0
+
+
+@pytest.mark.parametrize("m,n,k,bt", [
+    (64, 128, 96, True),      # convert_matmul_to_hmx.mlir:87-115 (both transposed)
+    (512, 1024, 256, False),  # transposed-A macro-tile, B [K, N]
+    (1024, 512, 384, True),   # transposed-A macro-tile, B [N, K]
+    (100, 200, 300, False),   # ragged: general kernel
+    (3, 512, 256, False),     # skinny: general kernel
+    (1, 4096, 4096, False),   # one row of unit pitch: streamed as a GEMV
+])
+@pytest.mark.parametrize("out32", [False, True])
+def test_matmul_transposed_a(pkg, oracle, dev, m, n, k, bt, out32):
+    g = torch.Generator().manual_seed(m + 3 * n + 7 * k + out32)
+    a = (torch.randn(m, k, generator=g) * 0.5).half()
+    b = torch.randn(n, k, generator=g).half() if bt else torch.randn(
+        k, n, generator=g).half()
+    at = a.t().contiguous()
+    ref = oracle.matmul_f16(at.numpy(), b.numpy(), a_transposed=True,
+                            b_transposed=bt, out_f32=out32)
+    dt = torch.float32 if out32 else torch.float16
+    buf, c = canary_out((m, n), dt, dev, -7.0)
+    pkg.matmul(at.to(dev), b.to(dev), c, a_transposed=True, b_transposed=bt,
+               out_dtype=dt)
+    fp16_ok(oracle, c.cpu().numpy(), ref)
+    check_canary(buf, m, n, -7.0)
+
+
+def test_matmul_transposed_a_accumulate_and_pitch(pkg, oracle, dev):
+    """Accumulate into the init, with A [K, M] a view of a wider buffer
+    (lda > M) on the fast path."""
+    g = torch.Generator().manual_seed(77)
+    m, n, k = 256, 512, 192
+    abig = (torch.randn(k, m + 64, generator=g) * 0.5).half()
+    at = abig[:, :m]
+    b = torch.randn(k, n, generator=g).half()
+    init = torch.randn(m, n, generator=g).half()
+    c = init.to(dev)
+    pkg.matmul(abig.to(dev)[:, :m], b.to(dev), c, a_transposed=True,
+               accumulate=True)
+    ref = oracle.matmul_f16(at.contiguous().numpy(), b.numpy(), init.numpy(),
+                            a_transposed=True)
+    fp16_ok(oracle, c.cpu().numpy(), ref)
+
+
+def test_batch_matmul_transposed_a_epilogue(pkg, oracle, dev):
+    """Batch of A [Z, K, M] with a shared B, bias and GELU in the store."""
+    g = torch.Generator().manual_seed(78)
+    z, m, n, k = 3, 256, 512, 128
+    a = (torch.randn(z, m, k, generator=g) * 0.5).half()
+    b = torch.randn(k, n, generator=g).half()
+    bias = torch.randn(n, generator=g).half()
+    y = pkg.batch_matmul(a.transpose(1, 2).contiguous().to(dev), b.to(dev),
+                         a_transposed=True, bias=bias.to(dev),
+                         activation="gelu_tanh")
+    ref = oracle.batch_matmul_f16(a.numpy(), b.numpy(), bias=bias.numpy(),
+                                  activation=pkg.ACT_GELU_TANH)
+    fp16_ok(oracle, y.cpu().numpy(), ref)

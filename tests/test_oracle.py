@@ -136,6 +136,39 @@ def test_matmul_f16_sensitive_to_transpose(oracle):
     assert oracle.fp16_parity(wrong, good) > 0.1
 
 
+def test_matmul_f16_a_transposed_exact(oracle):
+    """A stored [K, M] (LIT/codegen/transforms/convert_matmul_to_hmx.mlir:
+    87-115, the both-transposed case at its 64x128x96 shape and ragged
+    ones): small-integer operands make every sum exact, so the result must
+    equal the int64 product of the logical A and B bit for bit."""
+    rng = np.random.default_rng(4)
+    for m, n, k in [(64, 128, 96), (33, 45, 70), (1, 8, 5), (7, 1, 13)]:
+        a = rng.integers(-3, 4, (m, k)).astype(np.float16)
+        b = rng.integers(-3, 4, (k, n)).astype(np.float16)
+        want = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
+        at = np.ascontiguousarray(a.T)
+        bt = np.ascontiguousarray(b.T)
+        got = oracle.matmul_f16(at, b, a_transposed=True, out_f32=True)
+        assert got.shape == (m, n) and np.array_equal(got, want)
+        got = oracle.matmul_f16(at, bt, a_transposed=True, b_transposed=True,
+                                out_f32=True)
+        assert np.array_equal(got, want)
+
+
+def test_matmul_f16_a_transposed_random_and_sensitive(oracle):
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal((48, 80)).astype(np.float16)
+    b = rng.standard_normal((80, 32)).astype(np.float16)
+    ref = oracle.matmul_f16(a, b, out_f32=True)
+    got = oracle.matmul_f16(np.ascontiguousarray(a.T), b, a_transposed=True,
+                            out_f32=True)
+    assert np.array_equal(got, ref)          # same sums in the same k order
+    sq = rng.standard_normal((40, 40)).astype(np.float16)
+    wrong = oracle.matmul_f16(sq, b[:40], a_transposed=True, out_f32=True)
+    good = oracle.matmul_f16(sq, b[:40], out_f32=True)
+    assert oracle.fp16_parity(wrong, good) > 0.1
+
+
 # ------------------------------------------------------------------ w8a16 --
 
 def test_w8a16_exact_power_of_two_scales(oracle):
