@@ -44,6 +44,17 @@ typedef struct iree_mi355x_executable_environment_t {
 
 // Per-dispatch state. `constants` are the push constants (u32), whose layout
 // each export documents below; 64-bit extents are passed as lo/hi pairs.
+//
+// `workspace` is the split-K / GEMV scratch of this dispatch (NULL: the
+// library's per-device one, which dispatches on different streams must not
+// share); its counter region must be zero before first use, and the kernels
+// leave it zero. Dispatches that may run concurrently need disjoint ones.
+//
+// `workspace_query`, when non-NULL, turns the call into a validation: every
+// check and the plan run, nothing is allocated or enqueued, and the bytes of
+// workspace the dispatch needs are written there. A runtime validates a whole
+// command buffer this way before enqueuing any of it (where the reference's
+// DSP scheduler sizes VTCM partitions, RT/dsp/command_buffer.c:807-913).
 typedef struct iree_mi355x_executable_dispatch_state_t {
   uint32_t constant_count;
   const uint32_t *constants;
@@ -51,6 +62,9 @@ typedef struct iree_mi355x_executable_dispatch_state_t {
   void *const *binding_ptrs;       // device pointers
   const size_t *binding_lengths;   // bytes, 1:1 with binding_ptrs
   void *stream;                    // hipStream_t
+  void *workspace;
+  size_t workspace_bytes;
+  size_t *workspace_query;
 } iree_mi355x_executable_dispatch_state_t;
 
 // Returns 0 on success. Unlike the reference (where non-zero means device

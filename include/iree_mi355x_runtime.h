@@ -1,0 +1,134 @@
+// Runtime caller of the MI355X dispatch library: command buffers that record
+// dispatches of an executable library, fills, copies and barriers, and submit
+// them onto HIP streams, running the dispatches between two barriers
+// concurrently on up to N streams.
+//
+// Replaces the Hexagon HAL command buffer and its DSP-side scheduler:
+//  * recording (RT/command_buffer.c:586-665 serializes each dispatch with its
+//    constants and buffer references; binding-table slots are resolved at
+//    submission) is kept on the host, constants copied at record time;
+//  * execution (RT/dsp/command_buffer.c:807-913: up to
+//    --hexagon_max_concurrent_dispatches dispatches in flight between
+//    barriers, RT/registration/driver_module.c:20-23, each in its own VTCM
+//    partition) becomes up to `max_concurrent` lane streams: the commands of
+//    one barrier segment go round-robin over the lanes, a barrier joins every
+//    lane (events) and the end joins them back into the caller's stream;
+//  * the VTCM partition of a dispatch becomes a split-K / GEMV workspace
+//    slice per lane, sized by validating every dispatch of the command buffer
+//    (its workspace query) before any of it is enqueued.
+//
+// Every enqueue goes through the executable library's export functions on the
+// caller's stream or a lane stream; nothing here allocates device memory
+// except the runtime's own lane workspace (when the caller passes none) and
+// the lane streams and events, created on first use and kept for the process.
+// A submission with max_concurrent = 1 enqueues in order on the caller's
+// stream only, so it can be captured into a HIP graph; a submission with more
+// lanes into a capturing stream is refused (UNSUPPORTED).
+#ifndef IREE_MI355X_RUNTIME_H_
+#define IREE_MI355X_RUNTIME_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "iree_mi355x_executable_library.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// A buffer reference: a direct device pointer, or a slot of the binding table
+// given at submission (the reference's binding-table slots, resolved by the
+// DSP at execution, RT/dsp/command_buffer.c:600-633).
+#define IREE_MI355X_BINDING_DIRECT 0xFFFFFFFFu
+#define IREE_MI355X_WHOLE_BUFFER UINT64_MAX
+
+typedef struct iree_mi355x_buffer_ref_t {
+  uint32_t binding_slot;  // binding-table slot, or IREE_MI355X_BINDING_DIRECT
+  void *buffer;           // the device pointer when direct
+  uint64_t offset;        // bytes into the slot or buffer
+  uint64_t length;        // bytes; IREE_MI355X_WHOLE_BUFFER: rest of the slot
+} iree_mi355x_buffer_ref_t;
+
+typedef struct iree_mi355x_binding_t {
+  void *buffer;     // device pointer
+  uint64_t length;  // bytes
+} iree_mi355x_binding_t;
+
+typedef struct iree_mi355x_command_buffer_t iree_mi355x_command_buffer_t;
+
+// Lanes used when a submission asks for 0 ("as many as the device runs"):
+// the hardware queues HIP gives one process by default.
+#define IREE_MI355X_DEFAULT_CONCURRENCY 4u
+#define IREE_MI355X_MAX_CONCURRENCY 8u
+
+// New, empty command buffer recording against `library` (NULL: this
+// library's own table, iree_mi355x_executable_library_query).
+int iree_mi355x_command_buffer_create(
+    const iree_mi355x_executable_library_t *library,
+    iree_mi355x_command_buffer_t **out_command_buffer);
+
+void iree_mi355x_command_buffer_release(
+    iree_mi355x_command_buffer_t *command_buffer);
+
+// Record a dispatch of export `ordinal` with its push constants (copied) and
+// bindings (as the export documents them).
+int iree_mi355x_command_buffer_dispatch(
+    iree_mi355x_command_buffer_t *command_buffer, uint32_t ordinal,
+    const uint32_t *constants, uint32_t constant_count,
+    const iree_mi355x_buffer_ref_t *bindings, uint32_t binding_count);
+
+// Fill `target` with a 1-, 2- or 4-byte pattern; offset and length must be
+// multiples of the pattern length. Runs as a kernel, not a memset, so a
+// captured graph holds no memset node.
+int iree_mi355x_command_buffer_fill(
+    iree_mi355x_command_buffer_t *command_buffer,
+    iree_mi355x_buffer_ref_t target, const void *pattern,
+    uint32_t pattern_length);
+
+// Copy `length` bytes from `source` to `target` (device to device; the ranges
+// must not overlap).
+int iree_mi355x_command_buffer_copy(
+    iree_mi355x_command_buffer_t *command_buffer,
+    iree_mi355x_buffer_ref_t source, iree_mi355x_buffer_ref_t target,
+    uint64_t length);
+
+// Every command recorded before completes before any recorded after starts
+// (the reference's execution barrier, RT/dsp/command_buffer.c:915-933).
+int iree_mi355x_command_buffer_barrier(
+    iree_mi355x_command_buffer_t *command_buffer);
+
+// Ends recording; a command buffer is submitted only after this.
+int iree_mi355x_command_buffer_end(
+    iree_mi355x_command_buffer_t *command_buffer);
+
+// Bytes of workspace a submission with this binding table and concurrency
+// needs (one slice per lane, each the largest any dispatch asks for), after
+// validating every command; 0 on error (see iree_mi355x_last_error).
+size_t iree_mi355x_command_buffer_workspace_bytes(
+    const iree_mi355x_command_buffer_t *command_buffer,
+    const iree_mi355x_binding_t *binding_table, uint32_t binding_count,
+    uint32_t max_concurrent);
+
+// Submit on `stream` (hipStream_t; NULL = the null stream): resolves the
+// binding table, validates every command (a failing one enqueues nothing),
+// then enqueues. max_concurrent: 0 = IREE_MI355X_DEFAULT_CONCURRENCY, 1 = in
+// order on `stream` alone, at most IREE_MI355X_MAX_CONCURRENCY. `workspace`
+// (zero-filled before its first use; the kernels leave it zero) holds the
+// lane slices; NULL lets the runtime use its own, which submissions on
+// different streams must not use at the same time. Work is stream-ordered
+// after `stream`'s prior work, and `stream`'s later work is ordered after it.
+int iree_mi355x_command_buffer_submit(
+    const iree_mi355x_command_buffer_t *command_buffer,
+    const iree_mi355x_binding_t *binding_table, uint32_t binding_count,
+    uint32_t max_concurrent, void *workspace, size_t workspace_bytes,
+    void *stream);
+
+// Recorded commands (for inspection and tests).
+uint32_t iree_mi355x_command_buffer_count(
+    const iree_mi355x_command_buffer_t *command_buffer);
+
+#ifdef __cplusplus
+}  // extern "C"
+#endif
+
+#endif  // IREE_MI355X_RUNTIME_H_

@@ -61,6 +61,12 @@ EXPORTED_SYMBOLS = (
     "iree_mi355x_executable_library_query", "iree_mi355x_batch_matmul_f16",
     "iree_mi355x_batch_matmul_workspace_bytes",
     "iree_mi355x_mfma_config_layout_flags",
+    "iree_mi355x_command_buffer_create", "iree_mi355x_command_buffer_release",
+    "iree_mi355x_command_buffer_dispatch", "iree_mi355x_command_buffer_fill",
+    "iree_mi355x_command_buffer_copy", "iree_mi355x_command_buffer_barrier",
+    "iree_mi355x_command_buffer_end",
+    "iree_mi355x_command_buffer_workspace_bytes",
+    "iree_mi355x_command_buffer_submit", "iree_mi355x_command_buffer_count",
 )
 
 # Activations of the fused matmul epilogue (include/iree_mi355x_kernels.h).
@@ -112,7 +118,10 @@ class DispatchState(ctypes.Structure):
                 ("binding_count", ctypes.c_uint32),
                 ("binding_ptrs", ctypes.POINTER(ctypes.c_void_p)),
                 ("binding_lengths", ctypes.POINTER(ctypes.c_size_t)),
-                ("stream", ctypes.c_void_p)]
+                ("stream", ctypes.c_void_p),
+                ("workspace", ctypes.c_void_p),
+                ("workspace_bytes", ctypes.c_size_t),
+                ("workspace_query", ctypes.POINTER(ctypes.c_size_t))]
 
 
 DISPATCH_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p,
@@ -143,6 +152,24 @@ class LibraryHeader(ctypes.Structure):
 class Library(ctypes.Structure):
     _fields_ = [("header", ctypes.POINTER(LibraryHeader)),
                 ("imports", ImportTable), ("exports", ExportTable)]
+
+
+# Runtime (include/iree_mi355x_runtime.h).
+BINDING_DIRECT = 0xFFFFFFFF
+WHOLE_BUFFER = (1 << 64) - 1
+DEFAULT_CONCURRENCY = 4
+MAX_CONCURRENCY = 8
+
+
+class BufferRef(ctypes.Structure):
+    """iree_mi355x_buffer_ref_t: a binding-table slot or a direct pointer."""
+    _fields_ = [("binding_slot", ctypes.c_uint32), ("buffer", ctypes.c_void_p),
+                ("offset", ctypes.c_uint64), ("length", ctypes.c_uint64)]
+
+
+class Binding(ctypes.Structure):
+    """iree_mi355x_binding_t: one binding-table entry."""
+    _fields_ = [("buffer", ctypes.c_void_p), ("length", ctypes.c_uint64)]
 
 
 _lib = None
@@ -206,6 +233,24 @@ def library():
     lib.iree_mi355x_matmul_mfma_config.argtypes = [ctypes.c_int, p, p, p, p,
                                                    i64, i64, i64, i64, i64,
                                                    i64, u32, p]
+    cbp = ctypes.c_void_p
+    lib.iree_mi355x_command_buffer_create.argtypes = [p, ctypes.POINTER(cbp)]
+    lib.iree_mi355x_command_buffer_release.argtypes = [cbp]
+    lib.iree_mi355x_command_buffer_release.restype = None
+    lib.iree_mi355x_command_buffer_dispatch.argtypes = [
+        cbp, u32, ctypes.POINTER(u32), u32, ctypes.POINTER(BufferRef), u32]
+    lib.iree_mi355x_command_buffer_fill.argtypes = [cbp, BufferRef, p, u32]
+    lib.iree_mi355x_command_buffer_copy.argtypes = [cbp, BufferRef, BufferRef,
+                                                    ctypes.c_uint64]
+    lib.iree_mi355x_command_buffer_barrier.argtypes = [cbp]
+    lib.iree_mi355x_command_buffer_end.argtypes = [cbp]
+    lib.iree_mi355x_command_buffer_count.argtypes = [cbp]
+    lib.iree_mi355x_command_buffer_count.restype = u32
+    lib.iree_mi355x_command_buffer_workspace_bytes.argtypes = [
+        cbp, ctypes.POINTER(Binding), u32, u32]
+    lib.iree_mi355x_command_buffer_workspace_bytes.restype = sz
+    lib.iree_mi355x_command_buffer_submit.argtypes = [
+        cbp, ctypes.POINTER(Binding), u32, u32, p, sz, p]
     lib.iree_mi355x_executable_library_query.restype = ctypes.c_void_p
     lib.iree_mi355x_executable_library_query.argtypes = [u32, p]
     _lib = lib
@@ -299,8 +344,10 @@ def export_names() -> list[str]:
     return [lib.exports.names[i].decode() for i in range(lib.exports.count)]
 
 
-def call_export(name: str, constants, bindings, binding_lengths, stream=None):
-    """Invoke an export's dispatch function; returns the status code."""
+def call_export(name: str, constants, bindings, binding_lengths, stream=None,
+                workspace=None, workspace_bytes=0, query=False):
+    """Invoke an export's dispatch function; returns the status code, or with
+    ``query`` (validate only, nothing enqueued) (status, workspace bytes)."""
     lib = executable_library()
     names = export_names()
     idx = names.index(name)
@@ -308,9 +355,12 @@ def call_export(name: str, constants, bindings, binding_lengths, stream=None):
     consts = (ctypes.c_uint32 * len(constants))(*constants)
     ptrs = (ctypes.c_void_p * len(bindings))(*bindings)
     lens = (ctypes.c_size_t * len(binding_lengths))(*binding_lengths)
+    need = ctypes.c_size_t(0)
     state = DispatchState(len(constants), consts, len(bindings), ptrs, lens,
-                          stream)
-    return fn(None, ctypes.byref(state))
+                          stream, workspace, workspace_bytes,
+                          ctypes.pointer(need) if query else None)
+    st = fn(None, ctypes.byref(state))
+    return (st, need.value) if query else st
 
 
 def matmul_constants(m, n, k, lda, ldb, ldc, flags):
@@ -341,6 +391,10 @@ def attention_constants(batch, heads, seq_q, seq_kv, head_dim, scale, flags):
 # --------------------------------------------------------------- operators --
 
 def _stream_ptr(stream=None):
+    """hipStream_t of a torch stream (None: the current one); an int is taken
+    as the raw handle (0: the null stream)."""
+    if isinstance(stream, int):
+        return stream
     import torch
     s = stream if stream is not None else torch.cuda.current_stream()
     return s.cuda_stream
@@ -562,3 +616,92 @@ def matmul_mfma_config(index, a, b, c, *, scale=None, stream=None):
         scale.data_ptr() if scale is not None else None, c.data_ptr(), m, n,
         k, a.stride(0), b.stride(0), c.stride(0), flags, _stream_ptr(stream)))
     return c
+
+
+# ----------------------------------------------------------------- runtime --
+
+def slot(index: int, offset: int = 0, length: int = WHOLE_BUFFER) -> BufferRef:
+    """Reference to binding-table slot `index` (bytes [offset, +length))."""
+    return BufferRef(index, None, offset, length)
+
+
+def direct(t, offset: int = 0, length: int | None = None) -> BufferRef:
+    """Reference to a device tensor (or (pointer, bytes)) directly."""
+    ptr, nbytes = _ptr_len(t)
+    return BufferRef(BINDING_DIRECT, ptr, offset,
+                     nbytes - offset if length is None else length)
+
+
+def _ptr_len(t):
+    if isinstance(t, tuple):
+        return t
+    return t.data_ptr(), t.numel() * t.element_size()
+
+
+def binding_table(entries):
+    """A binding table from device tensors or (pointer, bytes) pairs."""
+    arr = (Binding * max(1, len(entries)))()
+    for i, e in enumerate(entries):
+        arr[i] = Binding(*_ptr_len(e))
+    return arr, len(entries)
+
+
+class CommandBuffer:
+    """Recorded dispatches, fills, copies and barriers of an executable
+    library, submitted onto HIP streams with the dispatches of each barrier
+    segment spread over up to `max_concurrent` streams."""
+
+    def __init__(self):
+        lib = library()
+        self._lib = lib
+        h = ctypes.c_void_p()
+        _check(lib.iree_mi355x_command_buffer_create(None, ctypes.byref(h)))
+        self._h = h
+        self._names = export_names()
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            self._lib.iree_mi355x_command_buffer_release(h)
+            self._h = None
+
+    def __len__(self):
+        return self._lib.iree_mi355x_command_buffer_count(self._h)
+
+    def dispatch(self, export, constants, bindings):
+        ordinal = self._names.index(export) if isinstance(export, str) else export
+        consts = (ctypes.c_uint32 * max(1, len(constants)))(*constants)
+        refs = (BufferRef * max(1, len(bindings)))(*bindings)
+        _check(self._lib.iree_mi355x_command_buffer_dispatch(
+            self._h, ordinal, consts, len(constants), refs, len(bindings)))
+        return self
+
+    def fill(self, target: BufferRef, pattern: bytes):
+        buf = ctypes.create_string_buffer(bytes(pattern), len(pattern))
+        _check(self._lib.iree_mi355x_command_buffer_fill(
+            self._h, target, buf, len(pattern)))
+        return self
+
+    def copy(self, source: BufferRef, target: BufferRef, length: int):
+        _check(self._lib.iree_mi355x_command_buffer_copy(
+            self._h, source, target, length))
+        return self
+
+    def barrier(self):
+        _check(self._lib.iree_mi355x_command_buffer_barrier(self._h))
+        return self
+
+    def end(self):
+        _check(self._lib.iree_mi355x_command_buffer_end(self._h))
+        return self
+
+    def workspace_bytes(self, table=(), max_concurrent=0) -> int:
+        arr, n = binding_table(list(table))
+        return self._lib.iree_mi355x_command_buffer_workspace_bytes(
+            self._h, arr, n, max_concurrent)
+
+    def submit(self, table=(), max_concurrent=0, workspace=None, stream=None):
+        arr, n = binding_table(list(table))
+        ws, wsb = (None, 0) if workspace is None else _ptr_len(workspace)
+        _check(self._lib.iree_mi355x_command_buffer_submit(
+            self._h, arr, n, max_concurrent, ws, wsb, _stream_ptr(stream)))

@@ -36,6 +36,20 @@ static int ok() {
   return IREE_MI355X_OK;
 }
 
+// Validate-only calls (an executable-library dispatch whose state carries a
+// workspace query): every check and the plan run, nothing is allocated or
+// launched, and the workspace the launch would need is written to the sink.
+static thread_local size_t *g_dry_run = nullptr;
+
+void set_dry_run(size_t *sink) { g_dry_run = sink; }
+
+static bool dry_run(int64_t workspace_needed) {
+  if (!g_dry_run)
+    return false;
+  *g_dry_run = workspace_needed > 0 ? (size_t)workspace_needed : 0;
+  return true;
+}
+
 static bool aligned(const void *p, size_t a) {
   return ((uintptr_t)p % a) == 0;
 }
@@ -216,6 +230,8 @@ static int matmul_f16_run(const char *who, MatmulArgs &args, uint32_t flags,
   iree_mi355x_matmul_plan_t plan;
   if (iree_mi355x_plan_matmul(&desc, &plan) != IREE_MI355X_OK)
     return fail(IREE_MI355X_UNSUPPORTED, "%s: no plan", who);
+  if (dry_run(plan.workspace_bytes))
+    return ok();
   int st;
   switch (plan.family) {
     case IREE_MI355X_FAMILY_GEMV: {
@@ -362,6 +378,8 @@ int iree_mi355x_matmul_i8(const int8_t *a, const int8_t *b, int32_t *c,
   iree_mi355x_matmul_plan_t plan;
   if (iree_mi355x_plan_matmul(&desc, &plan) != IREE_MI355X_OK)
     return fail(IREE_MI355X_UNSUPPORTED, "matmul_i8: no plan");
+  if (dry_run(plan.workspace_bytes))
+    return ok();
   if (plan.family == IREE_MI355X_FAMILY_MFMA)
     return launch_mfma(args, plan, nullptr, 0, "matmul_i8");
   return launch_status(launch_general(args, kGeneralI8I32, nullptr),
@@ -393,6 +411,8 @@ int iree_mi355x_w8a16_matmul(const void *x, const int8_t *w, const void *scale,
   iree_mi355x_matmul_plan_t plan;
   if (iree_mi355x_plan_matmul(&desc, &plan) != IREE_MI355X_OK)
     return fail(IREE_MI355X_UNSUPPORTED, "w8a16_matmul: no plan");
+  if (dry_run(plan.workspace_bytes))
+    return ok();
   if (plan.family == IREE_MI355X_FAMILY_GEMV) {
     void *ws = workspace;
     if (plan.workspace_bytes > 0) {
@@ -440,6 +460,8 @@ int iree_mi355x_attention_f16(const void *q, const void *k, const void *v,
       seq_kv >= kMaxExtent || batch * heads * (seq_q > seq_kv ? seq_q : seq_kv) *
                                       head_dim >= ((int64_t)1 << 62))
     return fail(IREE_MI355X_UNSUPPORTED, "attention_f16: problem too large");
+  if (dry_run(0))
+    return ok();
   return launch_status(
       launch_attention(q, k, v, o, batch, heads, seq_q, seq_kv, head_dim, scale,
                        (flags & IREE_MI355X_ATTENTION_CAUSAL) ? 1 : 0, stream),

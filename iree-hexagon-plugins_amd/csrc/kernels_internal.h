@@ -89,6 +89,11 @@ inline bool fast_operand(const void *p, int64_t ld_bytes,
          ld_bytes < kMaxFastPitchBytes && batch_stride_bytes % 16 == 0;
 }
 
+// While set, the C-ABI entry points on this thread validate and plan only:
+// no allocation, no launch; the workspace the call needs is written to
+// *sink. nullptr ends it.
+void set_dry_run(size_t *sink);
+
 typedef hipError_t (*FastLaunchFn)(const MatmulArgs &);
 
 // A compiled fast-path (LDS-DMA MFMA) GEMM configuration.

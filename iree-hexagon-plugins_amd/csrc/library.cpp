@@ -9,11 +9,13 @@
 
 namespace ihp {
 int fail(int status, const char *fmt, ...);
+void set_dry_run(size_t *sink);
 }
 
 namespace {
 
 using ihp::fail;
+using ihp::set_dry_run;
 
 int64_t u64(const uint32_t *c, int i) {
   return (int64_t)((uint64_t)c[i] | ((uint64_t)c[i + 1] << 32));
@@ -74,8 +76,18 @@ int check_matmul_bindings(const iree_mi355x_executable_dispatch_state_t *s,
   return IREE_MI355X_OK;
 }
 
+// A dispatch whose state asks for a workspace query only validates and plans
+// (see the dispatch-state declaration); the scope ends that mode on return.
+struct DryRunScope {
+  explicit DryRunScope(const iree_mi355x_executable_dispatch_state_t *s) {
+    set_dry_run(s ? s->workspace_query : nullptr);
+  }
+  ~DryRunScope() { set_dry_run(nullptr); }
+};
+
 int dispatch_matmul_f16(const iree_mi355x_executable_environment_t *,
                         const iree_mi355x_executable_dispatch_state_t *s) {
+  DryRunScope dry(s);
   MatmulConsts c;
   int st = decode_matmul(s, 3, &c);
   if (st)
@@ -85,11 +97,13 @@ int dispatch_matmul_f16(const iree_mi355x_executable_environment_t *,
     return st;
   return iree_mi355x_matmul_f16(s->binding_ptrs[0], s->binding_ptrs[1],
                                 s->binding_ptrs[2], c.m, c.n, c.k, c.lda,
-                                c.ldb, c.ldc, c.flags, nullptr, 0, s->stream);
+                                c.ldb, c.ldc, c.flags, s->workspace,
+                                s->workspace_bytes, s->stream);
 }
 
 int dispatch_matmul_i8(const iree_mi355x_executable_environment_t *,
                        const iree_mi355x_executable_dispatch_state_t *s) {
+  DryRunScope dry(s);
   MatmulConsts c;
   int st = decode_matmul(s, 3, &c);
   if (st)
@@ -104,6 +118,7 @@ int dispatch_matmul_i8(const iree_mi355x_executable_environment_t *,
 
 int dispatch_w8a16(const iree_mi355x_executable_environment_t *,
                    const iree_mi355x_executable_dispatch_state_t *s) {
+  DryRunScope dry(s);
   MatmulConsts c;
   int st = decode_matmul(s, 4, &c);
   if (st)
@@ -114,11 +129,12 @@ int dispatch_w8a16(const iree_mi355x_executable_environment_t *,
   return iree_mi355x_w8a16_matmul(
       s->binding_ptrs[0], (const int8_t *)s->binding_ptrs[1],
       s->binding_ptrs[2], s->binding_ptrs[3], c.m, c.n, c.k, c.lda, c.ldb,
-      c.ldc, c.flags, nullptr, 0, s->stream);
+      c.ldc, c.flags, s->workspace, s->workspace_bytes, s->stream);
 }
 
 int dispatch_attention(const iree_mi355x_executable_environment_t *,
                        const iree_mi355x_executable_dispatch_state_t *s) {
+  DryRunScope dry(s);
   if (!s || s->constant_count < 7 || !s->constants || s->binding_count < 4 ||
       !s->binding_ptrs || !s->binding_lengths)
     return fail(IREE_MI355X_INVALID_ARGUMENT,
@@ -147,6 +163,7 @@ int dispatch_attention(const iree_mi355x_executable_environment_t *,
 // Bindings: a b c [bias] [multiplier].
 int dispatch_batch_matmul(const iree_mi355x_executable_environment_t *,
                           const iree_mi355x_executable_dispatch_state_t *s) {
+  DryRunScope dry(s);
   const char *who = "batch_matmul_f16";
   MatmulConsts c;
   int st = decode_matmul(s, 3, &c);
@@ -202,8 +219,8 @@ int dispatch_batch_matmul(const iree_mi355x_executable_environment_t *,
   }
   return iree_mi355x_batch_matmul_f16(
       s->binding_ptrs[0], s->binding_ptrs[1], s->binding_ptrs[2], batch, c.m,
-      c.n, c.k, c.lda, c.ldb, c.ldc, sa, sb, sc, c.flags, &epi, nullptr, 0,
-      s->stream);
+      c.n, c.k, c.lda, c.ldb, c.ldc, sa, sb, sc, c.flags, &epi, s->workspace,
+      s->workspace_bytes, s->stream);
 }
 
 const iree_mi355x_executable_library_header_t kHeader = {
