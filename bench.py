@@ -313,6 +313,66 @@ def suite(pkg, inputs, dev, args):
              {"rotating_copies": copies})
         del ws
 
+    runtime_suite(pkg, inputs, dev, emit, steps)
+
+
+def timed_queued(fn, steps, warmup):
+    """Average ms per step of fn() for work that cannot be graph-captured
+    (concurrent lane streams): `warmup` steps, then `steps` steps enqueued
+    behind a spin kernel long enough that the host has queued them all before
+    the GPU starts, timed between events on the current stream."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(SPIN_CYCLES * 16)
+    start.record()
+    for _ in range(steps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def runtime_suite(pkg, inputs, dev, emit, steps):
+    """The runtime's concurrency (the reference's max concurrent dispatches):
+    one command buffer of 8 independent dispatches, submitted with 1, 2, 4
+    and 8 lanes, for C1-size f16 matmuls (4 workgroups each), C3 M=16 skinny
+    ones (split-K over every CU, one workspace slice per lane) and long int8
+    matmuls of 2 workgroups each (K = 8192, no split-K for int8)."""
+    import torch
+    cases = (("C1 f16 128x512x256", "matmul_f16", (128, 512, 256)),
+             ("C3 f16 M=16 N=4096 K=4096", "matmul_f16", (16, 4096, 4096)),
+             ("i8 256x512x8192", "matmul_i8", (256, 512, 8192)))
+    for label, export, (m, n, k) in cases:
+        g = torch.Generator().manual_seed(1)
+        i8 = export == "matmul_i8"
+        if i8:
+            xs = [torch.randint(-128, 128, (m, k), generator=g).to(torch.int8).to(dev)
+                  for _ in range(8)]
+            w = torch.randint(-128, 128, (n, k), generator=g).to(torch.int8).to(dev)
+            ys = [torch.empty(m, n, dtype=torch.int32, device=dev) for _ in range(8)]
+            consts = pkg.matmul_constants(m, n, k, k, k, n, pkg.B_TRANSPOSED)
+        else:
+            xs = [torch.randn(m, k, generator=g).half().to(dev) for _ in range(8)]
+            w = torch.randn(k, n, generator=g).half().to(dev)
+            ys = [torch.empty(m, n, dtype=torch.float16, device=dev) for _ in range(8)]
+            consts = pkg.matmul_constants(m, n, k, k, n, n, 0)
+        cb = pkg.CommandBuffer()
+        for i in range(8):
+            cb.dispatch(export, consts, [pkg.slot(i), pkg.slot(8), pkg.slot(9 + i)])
+        cb.end()
+        table = xs + [w] + ys
+        for lanes in (1, 2, 4, 8):
+            steps_q = max(20, min(steps, 100))
+            ms = timed_queued(lambda: cb.submit(table, max_concurrent=lanes),
+                              steps_q, 20)
+            emit(f"runtime 8 x {label}, {lanes} lane{'s' if lanes > 1 else ''}",
+                 ms, 8 * 2 * m * n * k, 8 * 2 * (m * k + k * n + m * n),
+                 "latency", {"dispatches": 8, "lanes": lanes})
+
 
 def only(pkg, inputs, dev, args):
     """One workload, for profiler passes: prints ms per step."""

@@ -56,9 +56,13 @@ typedef struct iree_mi355x_binding_t {
 
 typedef struct iree_mi355x_command_buffer_t iree_mi355x_command_buffer_t;
 
-// Lanes used when a submission asks for 0 ("as many as the device runs"):
-// the hardware queues HIP gives one process by default.
-#define IREE_MI355X_DEFAULT_CONCURRENCY 4u
+// Lanes used when a submission asks for 0: one (in order). Lane 0 is the
+// caller's stream; every further lane is a stream on another hardware queue,
+// and a fork / join across hardware queues costs ~35-40 us of GPU time per
+// submission on MI355X. The planner already spreads a dispatch over every CU
+// (split-K for skinny shapes), so lanes pay only for long dispatches that
+// leave most CUs idle, and are requested explicitly.
+#define IREE_MI355X_DEFAULT_CONCURRENCY 1u
 #define IREE_MI355X_MAX_CONCURRENCY 8u
 
 // New, empty command buffer recording against `library` (NULL: this

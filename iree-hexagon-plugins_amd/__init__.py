@@ -157,7 +157,7 @@ class Library(ctypes.Structure):
 # Runtime (include/iree_mi355x_runtime.h).
 BINDING_DIRECT = 0xFFFFFFFF
 WHOLE_BUFFER = (1 << 64) - 1
-DEFAULT_CONCURRENCY = 4
+DEFAULT_CONCURRENCY = 1
 MAX_CONCURRENCY = 8
 
 

@@ -288,12 +288,14 @@ DeviceLanes *device_lanes(int dev) {
   return g_devices[dev];
 }
 
+// Lane 0 is the caller's stream; lanes 1.. are the device's lane streams
+// streams[0..lanes-2]. Every lane has an event.
 int ensure_lanes(DeviceLanes *d, uint32_t lanes) {
   if (!d->fork &&
       hipEventCreateWithFlags(&d->fork, hipEventDisableTiming) != hipSuccess)
     return fail(IREE_MI355X_LAUNCH_FAILED, "submit: hipEventCreate failed");
   for (uint32_t l = 0; l < lanes; ++l) {
-    if (!d->streams[l] &&
+    if (l + 1 < lanes && !d->streams[l] &&
         hipStreamCreateWithFlags(&d->streams[l], hipStreamNonBlocking) !=
             hipSuccess)
       return fail(IREE_MI355X_LAUNCH_FAILED, "submit: hipStreamCreate failed");
@@ -596,14 +598,19 @@ int iree_mi355x_command_buffer_submit(
     roctxRangePop();
     return st;
   }
-  // Fork: every lane's first command of a segment waits for the events of
-  // the previous barrier (initially the caller's prior work); a lane does
-  // not wait for its own event, which stream order already covers.
+  // Lane 0 is the caller's stream itself, lanes 1.. the device's lane
+  // streams. Fork: every lane's first command of a segment waits for the
+  // events of the previous barrier (initially the caller's prior work); a
+  // lane does not wait for its own event, which stream order already covers.
+  hipStream_t lane_stream[IREE_MI355X_MAX_CONCURRENCY];
+  lane_stream[0] = caller;
+  for (uint32_t l = 1; l < lanes; ++l)
+    lane_stream[l] = d->streams[l - 1];
   struct Prior {
     hipEvent_t event;
-    int lane;  // -1: the caller's stream
+    uint32_t lane;
   };
-  std::vector<Prior> prior = {{d->fork, -1}};
+  std::vector<Prior> prior = {{d->fork, 0}};
   bool used_ever[IREE_MI355X_MAX_CONCURRENCY] = {};
   st = hip_ok(hipEventRecord(d->fork, caller), "fork record");
   uint32_t i = 0;
@@ -617,13 +624,13 @@ int iree_mi355x_command_buffer_submit(
       if (!used[l]) {
         used[l] = used_ever[l] = true;
         for (const Prior &e : prior)
-          if (e.lane != (int)l &&
-              (st = hip_ok(hipStreamWaitEvent(d->streams[l], e.event, 0),
+          if (e.lane != l &&
+              (st = hip_ok(hipStreamWaitEvent(lane_stream[l], e.event, 0),
                            "lane wait")))
             break;
       }
       if (!st)
-        st = enqueue(cb, j, ready[j], d->streams[l],
+        st = enqueue(cb, j, ready[j], lane_stream[l],
                      slice ? ws + (size_t)l * slice : nullptr, slice);
     }
     if (end > i && !st) {
@@ -631,20 +638,20 @@ int iree_mi355x_command_buffer_submit(
       prior.clear();
       for (uint32_t l = 0; l < lanes && !st; ++l)
         if (used[l]) {
-          st = hip_ok(hipEventRecord(d->lane_done[l], d->streams[l]),
+          st = hip_ok(hipEventRecord(d->lane_done[l], lane_stream[l]),
                       "lane record");
-          prior.push_back({d->lane_done[l], (int)l});
+          prior.push_back({d->lane_done[l], l});
         }
     }
     i = end + 1;  // past the barrier
   }
-  // Join: the caller's stream waits for every lane this submission used
-  // (each lane's last event covers its work).
-  for (uint32_t l = 0; l < lanes; ++l) {
+  // Join: the caller's stream (lane 0) waits for every other lane this
+  // submission used (each lane's last event covers its work).
+  for (uint32_t l = 1; l < lanes; ++l) {
     if (!used_ever[l])
       continue;
     const int rs =
-        hip_ok(hipEventRecord(d->lane_done[l], d->streams[l]), "join record");
+        hip_ok(hipEventRecord(d->lane_done[l], lane_stream[l]), "join record");
     const int ws2 = rs ? rs
                        : hip_ok(hipStreamWaitEvent(caller, d->lane_done[l], 0),
                                 "join wait");

@@ -115,7 +115,7 @@ def test_workspace_sizing(pkg):
     table = skinny_table(4)
     assert cb.workspace_bytes(table, 1) == slice_
     assert cb.workspace_bytes(table, 2) == 2 * slice_
-    assert cb.workspace_bytes(table, 0) == 4 * slice_     # default 4 lanes
+    assert cb.workspace_bytes(table, 0) == slice_         # default: in order
     assert cb.workspace_bytes(table, 8) == 4 * slice_     # 4 dispatches only
     # too small a caller workspace is refused before anything is enqueued
     with pytest.raises(pkg.MI355XError) as e:
