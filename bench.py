@@ -40,6 +40,9 @@ def parse():
     p.add_argument("--suite", action="store_true")
     p.add_argument("--tune", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--resources", action="store_true",
+                   help="print every compiled kernel's registers, LDS, "
+                        "scratch and occupancy (one JSON line each)")
     p.add_argument("--no-graph", action="store_true",
                    help="time eager launches instead of one captured graph")
     p.add_argument("--only", choices=["i8", "f16", "f16nn", "gemv", "attn",
@@ -158,6 +161,10 @@ def main():
         return tune(pkg, inputs, dev, args)
     if args.suite:
         return suite(pkg, inputs, dev, args)
+    if args.resources:
+        for rec in pkg.kernel_resources():
+            print(json.dumps(rec), flush=True)
+        return
 
     # ---- headline: C2 int8 4096^3 ----
     m = n = k = 4096

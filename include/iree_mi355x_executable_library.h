@@ -116,6 +116,30 @@ iree_mi355x_executable_library_query(
     iree_mi355x_executable_library_version_t max_version,
     const iree_mi355x_executable_environment_t *environment);
 
+// Resources of one compiled kernel: the measured side of the export
+// attributes above, which must cover every kernel an export may launch (the
+// reference annotates each export with the VTCM, HVX threads and HMX use of
+// its dispatch, CG/Transforms/HexagonAnnotateDispatchResources.cpp).
+typedef struct iree_mi355x_kernel_resources_t {
+  const char *name;           // MFMA configuration or kernel name
+  uint32_t exports;           // bit i: export ordinal i may launch it
+  int32_t threads;            // workgroup size it is launched with
+  int32_t vgprs;              // registers per lane (hipFuncGetAttributes)
+  int32_t lds_bytes;          // static LDS per workgroup
+  int32_t scratch_bytes;      // private memory per lane (register spills)
+  int32_t max_threads;        // the kernel's launch bound
+  int32_t workgroups_per_cu;  // resident workgroups per CU at `threads`
+} iree_mi355x_kernel_resources_t;
+
+// Number of compiled kernels (MFMA configurations, general, GEMV, attention
+// and runtime kernels).
+int iree_mi355x_kernel_count(void);
+
+// Fills name, exports and threads always; the other fields load the kernel
+// and need a device (IREE_MI355X_NO_DEVICE without one).
+int iree_mi355x_kernel_resources(int index,
+                                 iree_mi355x_kernel_resources_t *out);
+
 // Export push-constant layouts (u32 words):
 //  "matmul_f16"   constants: m_lo m_hi n_lo n_hi k_lo k_hi lda_lo lda_hi
 //                 ldb_lo ldb_hi ldc_lo ldc_hi flags   bindings: a b c

@@ -67,6 +67,7 @@ EXPORTED_SYMBOLS = (
     "iree_mi355x_command_buffer_end",
     "iree_mi355x_command_buffer_workspace_bytes",
     "iree_mi355x_command_buffer_submit", "iree_mi355x_command_buffer_count",
+    "iree_mi355x_kernel_count", "iree_mi355x_kernel_resources",
 )
 
 # Activations of the fused matmul epilogue (include/iree_mi355x_kernels.h).
@@ -152,6 +153,15 @@ class LibraryHeader(ctypes.Structure):
 class Library(ctypes.Structure):
     _fields_ = [("header", ctypes.POINTER(LibraryHeader)),
                 ("imports", ImportTable), ("exports", ExportTable)]
+
+
+class KernelResources(ctypes.Structure):
+    """iree_mi355x_kernel_resources_t."""
+    _fields_ = [("name", ctypes.c_char_p), ("exports", ctypes.c_uint32),
+                ("threads", ctypes.c_int32), ("vgprs", ctypes.c_int32),
+                ("lds_bytes", ctypes.c_int32), ("scratch_bytes", ctypes.c_int32),
+                ("max_threads", ctypes.c_int32),
+                ("workgroups_per_cu", ctypes.c_int32)]
 
 
 # Runtime (include/iree_mi355x_runtime.h).
@@ -251,6 +261,8 @@ def library():
     lib.iree_mi355x_command_buffer_workspace_bytes.restype = sz
     lib.iree_mi355x_command_buffer_submit.argtypes = [
         cbp, ctypes.POINTER(Binding), u32, u32, p, sz, p]
+    lib.iree_mi355x_kernel_resources.argtypes = [ctypes.c_int,
+                                                 ctypes.POINTER(KernelResources)]
     lib.iree_mi355x_executable_library_query.restype = ctypes.c_void_p
     lib.iree_mi355x_executable_library_query.argtypes = [u32, p]
     _lib = lib
@@ -705,3 +717,26 @@ class CommandBuffer:
         ws, wsb = (None, 0) if workspace is None else _ptr_len(workspace)
         _check(self._lib.iree_mi355x_command_buffer_submit(
             self._h, arr, n, max_concurrent, ws, wsb, _stream_ptr(stream)))
+
+
+def kernel_resources(device: bool = True) -> list[dict]:
+    """Every compiled kernel: name, the exports that may launch it (a list
+    of export names) and its launch threads; with ``device``, also the VGPRs,
+    static LDS, scratch per lane, launch bound and resident workgroups per
+    CU that the loaded code object reports."""
+    lib = library()
+    names = export_names()
+    out = []
+    for i in range(lib.iree_mi355x_kernel_count()):
+        r = KernelResources()
+        st = lib.iree_mi355x_kernel_resources(i, ctypes.byref(r))
+        if st != OK and (device or st != NO_DEVICE):
+            _check(st)
+        rec = {"name": r.name.decode(), "threads": r.threads,
+               "exports": [n for b, n in enumerate(names) if r.exports >> b & 1]}
+        if st == OK:
+            rec.update(vgprs=r.vgprs, lds_bytes=r.lds_bytes,
+                       scratch_bytes=r.scratch_bytes, max_threads=r.max_threads,
+                       workgroups_per_cu=r.workgroups_per_cu)
+        out.append(rec)
+    return out

@@ -375,3 +375,16 @@ hipError_t launch_attention(const void *q, const void *k, const void *v,
 }
 
 }  // namespace ihp
+
+namespace ihp {
+
+const KernelEntry *attention_kernels(int *count) {
+  static const KernelEntry all[] = {
+      {"attention_fwd_d128", (const void *)&attention_fwd_kernel<128>, kThreads, kExportAttention},
+      {"attention_fwd_d64", (const void *)&attention_fwd_kernel<64>, kThreads, kExportAttention},
+  };
+  *count = (int)(sizeof(all) / sizeof(all[0]));
+  return all;
+}
+
+}  // namespace ihp

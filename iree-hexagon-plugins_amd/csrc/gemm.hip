@@ -17,6 +17,7 @@
 //    HexagonConvertMatmulToHmx.cpp:592-596; this keeps full precision);
 //  * the unpack (add into the DPS init, UK/hmx.c:328-357) is the epilogue.
 #include <type_traits>
+#include <vector>
 
 #include "device_common.h"
 #include "kernels_internal.h"
@@ -807,6 +808,8 @@ static hipError_t launch_fast(const MatmulArgs &a) {
    MODE,                                                                      \
    SPLIT,                                                                     \
    AT,                                                                        \
+   (const void *)&gemm_lds_kernel<T, OUT, BM, BN, BKB, WM, WN, ST, MODE,      \
+                                  SPLIT, AT>,                                 \
    sizeof(T) == 1 ? kElemI8 : kElemF16,                                       \
    sizeof(OUT) == 4 && sizeof(T) == 2,                                        \
    BM,                                                                        \
@@ -869,6 +872,29 @@ static const FastConfig kFastConfigs[] = {
 const FastConfig *fast_configs(int *count) {
   *count = (int)(sizeof(kFastConfigs) / sizeof(kFastConfigs[0]));
   return kFastConfigs;
+}
+
+// Every GEMM kernel: the macro-tile configurations, then the general kernel's
+// four instances.
+const KernelEntry *gemm_kernels(int *count) {
+  static const std::vector<KernelEntry> all = [] {
+    std::vector<KernelEntry> v;
+    for (const FastConfig &c : kFastConfigs) {
+      const uint32_t ex = c.elem == kElemI8 ? kExportMatmulI8
+                          : c.b_mode == kBW8
+                              ? kExportW8A16
+                              : kExportMatmulF16 | kExportBatchMatmulF16;
+      v.push_back({c.name, c.kernel, c.threads, ex});
+    }
+    const uint32_t f16x = kExportMatmulF16 | kExportBatchMatmulF16;
+    v.push_back({"general_f16", (const void *)&gemm_general_kernel<f16, f16, f16, false>, 256, f16x});
+    v.push_back({"general_f16f32", (const void *)&gemm_general_kernel<f16, f16, float, false>, 256, f16x});
+    v.push_back({"general_i8", (const void *)&gemm_general_kernel<int8_t, int8_t, int32_t, false>, 256, kExportMatmulI8});
+    v.push_back({"general_w8a16", (const void *)&gemm_general_kernel<f16, int8_t, f16, true>, 256, kExportW8A16});
+    return v;
+  }();
+  *count = (int)all.size();
+  return all.data();
 }
 
 template <typename TA, typename TB, typename OutT, bool kScale>

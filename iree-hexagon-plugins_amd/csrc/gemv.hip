@@ -345,3 +345,28 @@ hipError_t launch_gemv(const MatmulArgs &a, int w_bytes, const void *scale,
 }
 
 }  // namespace ihp
+
+namespace ihp {
+
+// Every GEMV kernel: rows 1..4 for f16 weights (f16 / f32 out) and W8A16.
+const KernelEntry *gemv_kernels(int *count) {
+  const uint32_t f16x = kExportMatmulF16 | kExportBatchMatmulF16;
+  static const KernelEntry all[] = {
+      {"gemv_f16_r1", (const void *)&gemv_splitk_kernel<f16, 1, f16>, kThreads, f16x},
+      {"gemv_f16_r2", (const void *)&gemv_splitk_kernel<f16, 2, f16>, kThreads, f16x},
+      {"gemv_f16_r3", (const void *)&gemv_splitk_kernel<f16, 3, f16>, kThreads, f16x},
+      {"gemv_f16_r4", (const void *)&gemv_splitk_kernel<f16, 4, f16>, kThreads, f16x},
+      {"gemv_f16f32_r1", (const void *)&gemv_splitk_kernel<f16, 1, float>, kThreads, f16x},
+      {"gemv_f16f32_r2", (const void *)&gemv_splitk_kernel<f16, 2, float>, kThreads, f16x},
+      {"gemv_f16f32_r3", (const void *)&gemv_splitk_kernel<f16, 3, float>, kThreads, f16x},
+      {"gemv_f16f32_r4", (const void *)&gemv_splitk_kernel<f16, 4, float>, kThreads, f16x},
+      {"gemv_w8a16_r1", (const void *)&gemv_splitk_kernel<int8_t, 1, f16>, kThreads, kExportW8A16},
+      {"gemv_w8a16_r2", (const void *)&gemv_splitk_kernel<int8_t, 2, f16>, kThreads, kExportW8A16},
+      {"gemv_w8a16_r3", (const void *)&gemv_splitk_kernel<int8_t, 3, f16>, kThreads, kExportW8A16},
+      {"gemv_w8a16_r4", (const void *)&gemv_splitk_kernel<int8_t, 4, f16>, kThreads, kExportW8A16},
+  };
+  *count = (int)(sizeof(all) / sizeof(all[0]));
+  return all;
+}
+
+}  // namespace ihp

@@ -96,12 +96,32 @@ void set_dry_run(size_t *sink);
 
 typedef hipError_t (*FastLaunchFn)(const MatmulArgs &);
 
+// One compiled kernel: its name, entry (for hipFuncGetAttributes), the
+// workgroup size it is launched with, and the executable-library exports
+// that may launch it (bit i = export ordinal i; 0 = runtime-internal).
+struct KernelEntry {
+  const char *name;
+  const void *fn;
+  int threads;
+  uint32_t exports;
+};
+constexpr uint32_t kExportMatmulF16 = 1u << 0;
+constexpr uint32_t kExportMatmulI8 = 1u << 1;
+constexpr uint32_t kExportW8A16 = 1u << 2;
+constexpr uint32_t kExportAttention = 1u << 3;
+constexpr uint32_t kExportBatchMatmulF16 = 1u << 4;
+const KernelEntry *gemm_kernels(int *count);
+const KernelEntry *gemv_kernels(int *count);
+const KernelEntry *attention_kernels(int *count);
+const KernelEntry *runtime_kernels(int *count);
+
 // A compiled fast-path (LDS-DMA MFMA) GEMM configuration.
 struct FastConfig {
   const char *name;
   int b_mode;    // BMode
   int split_k;   // K split over grid.y, M may be ragged (skinny shapes)
   int a_trans;   // A stored [K,M] (f16 only, exact tiling)
+  const void *kernel;  // the instantiated kernel (resource queries)
   int elem;      // ElemKind of A (and of B unless kBW8)
   int out_f32;   // f16 path: f32 output (i8 path: always i32)
   int bm, bn;    // macro-tile

@@ -2,14 +2,16 @@
 // export per matched dispatch kind, each decoding its push constants and
 // bindings, checking that every binding covers what the kernel will touch,
 // and calling the flat entry point on the dispatch's stream.
+#include <hip/hip_runtime.h>
+
 #include <cstring>
 
 #include "../../include/iree_mi355x_executable_library.h"
 #include "../../include/iree_mi355x_kernels.h"
+#include "kernels_internal.h"
 
 namespace ihp {
 int fail(int status, const char *fmt, ...);
-void set_dry_run(size_t *sink);
 }
 
 namespace {
@@ -230,25 +232,27 @@ const iree_mi355x_executable_dispatch_fn_t kPtrs[] = {
     dispatch_matmul_f16, dispatch_matmul_i8, dispatch_w8a16,
     dispatch_attention, dispatch_batch_matmul};
 
-// Largest static LDS and workgroup of any kernel an export can launch: the
-// f16 MFMA ring (up to 160 KiB, 512 threads), the GEMV (512 threads), the
-// W8A16 256x256 ring (3 x 48 KiB), the attention K/V ring (2 x 32 KiB).
+// Largest static LDS and workgroup of any kernel an export can launch (the
+// GPU tests compare them with what the loaded kernels report): the f16 and
+// int8 MFMA rings (128 KiB: 2 x 64 KiB or 4 x 32 KiB, 512 threads), the
+// W8A16 256x256 ring (3 x 48 KiB), the GEMV (512 threads, its 8-wave
+// reduction buffer at most 128 KiB), the attention K/V ring (2 x 32 KiB).
 constexpr uint64_t kF16Flags = IREE_MI355X_DISPATCH_FLAG_RESOURCES_VALID |
                                IREE_MI355X_DISPATCH_FLAG_USES_MFMA |
                                IREE_MI355X_DISPATCH_FLAG_USES_LDS_DMA |
                                IREE_MI355X_DISPATCH_FLAG_USES_WORKSPACE;
 const iree_mi355x_executable_dispatch_attrs_t kAttrs[] = {
-    {kF16Flags, 163840, 512},
+    {kF16Flags, 131072, 512},
     {IREE_MI355X_DISPATCH_FLAG_RESOURCES_VALID |
          IREE_MI355X_DISPATCH_FLAG_USES_MFMA |
          IREE_MI355X_DISPATCH_FLAG_USES_LDS_DMA,
-     163840, 512},
+     131072, 512},
     {kF16Flags, 147456, 512},
     {IREE_MI355X_DISPATCH_FLAG_RESOURCES_VALID |
          IREE_MI355X_DISPATCH_FLAG_USES_MFMA |
          IREE_MI355X_DISPATCH_FLAG_USES_LDS_DMA,
      65536, 256},
-    {kF16Flags, 163840, 512},
+    {kF16Flags, 131072, 512},
 };
 
 const char *const kNames[] = {"matmul_f16", "matmul_i8", "w8a16_matmul",
@@ -272,4 +276,71 @@ iree_mi355x_executable_library_query(
   // The library struct begins with its header pointer.
   return const_cast<const iree_mi355x_executable_library_header_t **>(
       &kLibrary.header);
+}
+
+// ---------------------------------------------------------------- resources
+
+namespace {
+
+// The kernel lists of every translation unit, in one index space.
+const ihp::KernelEntry *kernel_at(int index) {
+  const ihp::KernelEntry *(*lists[])(int *) = {
+      ihp::gemm_kernels, ihp::gemv_kernels, ihp::attention_kernels,
+      ihp::runtime_kernels};
+  for (auto list : lists) {
+    int n = 0;
+    const ihp::KernelEntry *e = list(&n);
+    if (index < n)
+      return e + index;
+    index -= n;
+  }
+  return nullptr;
+}
+
+}  // namespace
+
+extern "C" int iree_mi355x_kernel_count(void) {
+  int total = 0, n = 0;
+  ihp::gemm_kernels(&n);
+  total += n;
+  ihp::gemv_kernels(&n);
+  total += n;
+  ihp::attention_kernels(&n);
+  total += n;
+  ihp::runtime_kernels(&n);
+  return total + n;
+}
+
+extern "C" int iree_mi355x_kernel_resources(
+    int index, iree_mi355x_kernel_resources_t *out) {
+  if (!out || index < 0)
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "kernel_resources: bad argument");
+  const ihp::KernelEntry *e = kernel_at(index);
+  if (!e)
+    return fail(IREE_MI355X_INVALID_ARGUMENT,
+                "kernel_resources: index %d of %d", index,
+                iree_mi355x_kernel_count());
+  memset(out, 0, sizeof(*out));
+  out->name = e->name;
+  out->exports = e->exports;
+  out->threads = e->threads;
+  int devices = 0;
+  if (hipGetDeviceCount(&devices) != hipSuccess || devices == 0)
+    return fail(IREE_MI355X_NO_DEVICE,
+                "kernel_resources: no device to load %s from", e->name);
+  hipFuncAttributes attr;
+  if (hipFuncGetAttributes(&attr, e->fn) != hipSuccess)
+    return fail(IREE_MI355X_LAUNCH_FAILED,
+                "kernel_resources: hipFuncGetAttributes(%s) failed", e->name);
+  int resident = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, e->fn,
+                                                   e->threads, 0) != hipSuccess)
+    return fail(IREE_MI355X_LAUNCH_FAILED,
+                "kernel_resources: occupancy of %s failed", e->name);
+  out->vgprs = attr.numRegs;
+  out->lds_bytes = (int32_t)attr.sharedSizeBytes;
+  out->scratch_bytes = (int32_t)attr.localSizeBytes;
+  out->max_threads = attr.maxThreadsPerBlock;
+  out->workgroups_per_cu = resident;
+  return IREE_MI355X_OK;
 }

@@ -63,6 +63,14 @@ __global__ __launch_bounds__(256) void fill_kernel(unsigned char *dst,
     body[j] = v;
 }
 
+const KernelEntry *runtime_kernels(int *count) {
+  static const KernelEntry all[] = {
+      {"runtime_fill", (const void *)&fill_kernel, 256, 0u},
+  };
+  *count = 1;
+  return all;
+}
+
 namespace {
 
 struct Ref {

@@ -370,3 +370,42 @@ def test_fast_path_pitch_limit(pkg):
              None) == pkg.UNSUPPORTED
     assert f(cfg.index, FAKE, FAKE, None, FAKE, 128, 128, 64, 128, big, 128, 0,
              None) == pkg.UNSUPPORTED
+
+
+# ------------------------------------------------------ kernel resources ----
+
+def test_kernel_registry_without_device(pkg):
+    """Every compiled kernel is listed with the exports that may launch it;
+    every export has kernels, and every MFMA configuration is one of them."""
+    ks = pkg.kernel_resources(device=False)
+    names = [k["name"] for k in ks]
+    assert len(names) == len(set(names)) == pkg.library().iree_mi355x_kernel_count()
+    for cfg in pkg.mfma_configs():
+        assert cfg.name in names
+    for export in pkg.export_names():
+        assert any(export in k["exports"] for k in ks), export
+    by = {k["name"]: k for k in ks}
+    assert by["general_i8"]["exports"] == ["matmul_i8"]
+    assert set(by["gemv_f16_r1"]["exports"]) == {"matmul_f16", "batch_matmul_f16"}
+    assert by["gemv_w8a16_r4"]["exports"] == ["w8a16_matmul"]
+    assert by["runtime_fill"]["exports"] == []
+    assert all(k["threads"] in (256, 512) for k in ks)
+    assert "vgprs" not in by["general_i8"]       # needs a device
+    lib = pkg.library()
+    r = pkg.KernelResources()
+    assert lib.iree_mi355x_kernel_resources(len(ks), ctypes.byref(r)) == \
+        pkg.INVALID_ARGUMENT
+
+
+def test_export_attributes_cover_mfma_configs(pkg):
+    """Every export's static LDS / thread attributes cover the MFMA
+    configurations it may launch (the GPU tests check equality against all
+    of its kernels as loaded)."""
+    lib = pkg.executable_library()
+    names = pkg.export_names()
+    by_name = {k["name"]: k for k in pkg.kernel_resources(device=False)}
+    for cfg in pkg.mfma_configs():
+        for export in by_name[cfg.name]["exports"]:
+            attrs = lib.exports.attrs[names.index(export)]
+            assert attrs.lds_bytes >= cfg.lds_bytes, (export, cfg.name)
+            assert attrs.threads >= cfg.threads, (export, cfg.name)

@@ -687,3 +687,27 @@ def test_batch_matmul_transposed_a_epilogue(pkg, oracle, dev):
     ref = oracle.batch_matmul_f16(a.numpy(), b.numpy(), bias=bias.numpy(),
                                   activation=pkg.ACT_GELU_TANH)
     fp16_ok(oracle, y.cpu().numpy(), ref)
+
+
+# ------------------------------------------------------ kernel resources ----
+
+def test_export_attributes_cover_their_kernels(pkg):
+    """The executable library's static per-export attributes (largest LDS
+    and workgroup of any kernel the export may launch) equal what the loaded
+    kernels report; every kernel fits the CU's LDS and is resident at its
+    launch size; the configuration table's LDS formula matches the compiler."""
+    ks = pkg.kernel_resources()
+    lib = pkg.executable_library()
+    names = pkg.export_names()
+    for i, export in enumerate(names):
+        mine = [k for k in ks if export in k["exports"]]
+        attrs = lib.exports.attrs[i]
+        assert attrs.lds_bytes == max(k["lds_bytes"] for k in mine), export
+        assert attrs.threads == max(k["threads"] for k in mine), export
+    cfg_lds = {c.name: c.lds_bytes for c in pkg.mfma_configs()}
+    for k in ks:
+        assert k["lds_bytes"] <= 160 * 1024, k
+        assert k["workgroups_per_cu"] >= 1, k
+        assert k["max_threads"] >= k["threads"], k
+        if k["name"] in cfg_lds:
+            assert k["lds_bytes"] == cfg_lds[k["name"]], k
