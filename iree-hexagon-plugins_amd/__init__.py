@@ -68,6 +68,9 @@ EXPORTED_SYMBOLS = (
     "iree_mi355x_command_buffer_workspace_bytes",
     "iree_mi355x_command_buffer_submit", "iree_mi355x_command_buffer_count",
     "iree_mi355x_kernel_count", "iree_mi355x_kernel_resources",
+    "iree_mi355x_executable_serialize", "iree_mi355x_executable_verify",
+    "iree_mi355x_executable_load", "iree_mi355x_loaded_executable_library",
+    "iree_mi355x_loaded_executable_release",
 )
 
 # Activations of the fused matmul epilogue (include/iree_mi355x_kernels.h).
@@ -263,6 +266,14 @@ def library():
         cbp, ctypes.POINTER(Binding), u32, u32, p, sz, p]
     lib.iree_mi355x_kernel_resources.argtypes = [ctypes.c_int,
                                                  ctypes.POINTER(KernelResources)]
+    lib.iree_mi355x_executable_serialize.restype = sz
+    lib.iree_mi355x_executable_serialize.argtypes = [ctypes.c_char_p, p, sz]
+    lib.iree_mi355x_executable_verify.argtypes = [p, sz]
+    lib.iree_mi355x_executable_load.argtypes = [p, sz, ctypes.POINTER(p)]
+    lib.iree_mi355x_loaded_executable_library.restype = p
+    lib.iree_mi355x_loaded_executable_library.argtypes = [p]
+    lib.iree_mi355x_loaded_executable_release.restype = None
+    lib.iree_mi355x_loaded_executable_release.argtypes = [p]
     lib.iree_mi355x_executable_library_query.restype = ctypes.c_void_p
     lib.iree_mi355x_executable_library_query.argtypes = [u32, p]
     _lib = lib
@@ -660,16 +671,20 @@ def binding_table(entries):
 
 class CommandBuffer:
     """Recorded dispatches, fills, copies and barriers of an executable
-    library, submitted onto HIP streams with the dispatches of each barrier
-    segment spread over up to `max_concurrent` streams."""
+    library (this library's own, or a `LoadedExecutable`'s), submitted onto
+    HIP streams with the dispatches of each barrier segment spread over up to
+    `max_concurrent` streams."""
 
-    def __init__(self):
+    def __init__(self, executable=None):
         lib = library()
         self._lib = lib
+        self._exe = executable          # keeps a loaded library alive
+        table = executable.table_ptr if executable is not None else None
         h = ctypes.c_void_p()
-        _check(lib.iree_mi355x_command_buffer_create(None, ctypes.byref(h)))
+        _check(lib.iree_mi355x_command_buffer_create(table, ctypes.byref(h)))
         self._h = h
-        self._names = export_names()
+        self._names = (executable.export_names() if executable is not None
+                       else export_names())
 
     def __del__(self):
         h = getattr(self, "_h", None)
@@ -740,3 +755,48 @@ def kernel_resources(device: bool = True) -> list[dict]:
                        workgroups_per_cu=r.workgroups_per_cu)
         out.append(rec)
     return out
+
+
+# ------------------------------------------------------------- executables --
+
+def serialize_executable(library_path: str | None = None) -> bytes:
+    """The versioned container of an ELF dispatch library (default: this
+    one) with its export table and checksum."""
+    lib = library()
+    path = library_path.encode() if library_path else None
+    need = lib.iree_mi355x_executable_serialize(path, None, 0)
+    if need == 0:
+        raise MI355XError(INVALID_ARGUMENT, last_error())
+    buf = ctypes.create_string_buffer(need)
+    got = lib.iree_mi355x_executable_serialize(path, buf, need)
+    if got != need:
+        raise MI355XError(INVALID_ARGUMENT, last_error())
+    return buf.raw
+
+
+def verify_executable(data: bytes) -> int:
+    """Status of the container's header / version / arch / checksum check."""
+    return library().iree_mi355x_executable_verify(data, len(data))
+
+
+class LoadedExecutable:
+    """A container loaded into this process (its ELF dlopened privately)."""
+
+    def __init__(self, data: bytes):
+        lib = library()
+        self._lib = lib
+        h = ctypes.c_void_p()
+        _check(lib.iree_mi355x_executable_load(data, len(data), ctypes.byref(h)))
+        self._h = h
+        self.table_ptr = lib.iree_mi355x_loaded_executable_library(h)
+
+    def export_names(self) -> list[str]:
+        table = ctypes.cast(self.table_ptr, ctypes.POINTER(Library)).contents
+        return [table.exports.names[i].decode()
+                for i in range(table.exports.count)]
+
+    def release(self):
+        """Unload (every dispatch of it must have completed)."""
+        if self._h is not None and self._h.value:
+            self._lib.iree_mi355x_loaded_executable_release(self._h)
+        self._h = None

@@ -184,3 +184,32 @@ def test_captured_in_order_submission_replays(pkg, oracle, dev):
         torch.cuda.synchronize()
         graph.replay()
         p.check(oracle)
+
+
+def test_loaded_executable_dispatches(pkg, oracle, dev):
+    """A serialized executable loaded into a private copy of the library:
+    its exports run a macro-tile and a split-K matmul through a command
+    buffer, matching the oracle."""
+    exe = pkg.LoadedExecutable(pkg.serialize_executable())
+    try:
+        g = torch.Generator().manual_seed(41)
+        cases = [(256, 512, 128), (16, 4096, 2048)]
+        ts, refs = [], []
+        cb = pkg.CommandBuffer(executable=exe)
+        for i, (m, n, k) in enumerate(cases):
+            a = (torch.randn(m, k, generator=g) * 0.5).half()
+            b = torch.randn(k, n, generator=g).half()
+            refs.append(oracle.matmul_f16(a.numpy(), b.numpy()))
+            c = torch.full((m, n), 3.0, dtype=torch.float16, device=dev)
+            ts += [a.to(dev), b.to(dev), c]
+            cb.dispatch("matmul_f16", consts(pkg, m, n, k),
+                        [pkg.slot(3 * i), pkg.slot(3 * i + 1), pkg.slot(3 * i + 2)])
+        cb.end()
+        cb.submit(ts, max_concurrent=1)
+        torch.cuda.synchronize()
+        for i, ref in enumerate(refs):
+            assert oracle.fp16_parity(ts[3 * i + 2].cpu().numpy(), ref) <= FP16_BOUND
+        del cb
+    finally:
+        torch.cuda.synchronize()
+        exe.release()
