@@ -46,7 +46,7 @@ def parse():
     p.add_argument("--no-graph", action="store_true",
                    help="time eager launches instead of one captured graph")
     p.add_argument("--only", choices=["i8", "f16", "f16nn", "gemv", "attn",
-                                      "w8a16", "w8a16_gemm"],
+                                      "w8a16", "w8a16_gemm", "runtime"],
                    help="run one workload (for rocprof passes) and exit")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="with --only: first copy 256 MiB device-to-device "
@@ -418,6 +418,35 @@ def only(pkg, inputs, dev, args):
         q, k, v = (t.to(dev) for t in inputs.c4_attention_f16())
         o = torch.empty_like(q)
         fn = lambda: pkg.attention(q, k, v, o, causal=True)  # noqa: E731
+    elif w == "runtime":
+        # One command buffer: fill, barrier, 4 C1 matmuls and 4 M=16 split-K
+        # matmuls on 2 lanes, barrier, copy; submitted eagerly (lanes are not
+        # graph-captured), each command a roctx range.
+        g = torch.Generator().manual_seed(2)
+        shapes = [(128, 512, 256)] * 4 + [(16, 4096, 4096)] * 4
+        table, cb = [], pkg.CommandBuffer()
+        out0 = None
+        for i, (m, n, k) in enumerate(shapes):
+            a = torch.randn(m, k, generator=g).half().to(dev)
+            b = torch.randn(k, n, generator=g).half().to(dev)
+            c = torch.empty(m, n, dtype=torch.float16, device=dev)
+            out0 = c if out0 is None else out0
+            table += [a, b, c]
+        copy_dst = torch.empty_like(out0)
+        table.append(copy_dst)
+        cb.fill(pkg.slot(2), b"\x00\x00")
+        cb.barrier()
+        for i, (m, n, k) in enumerate(shapes):
+            cb.dispatch("matmul_f16", pkg.matmul_constants(m, n, k, k, n, n, 0),
+                        [pkg.slot(3 * i), pkg.slot(3 * i + 1), pkg.slot(3 * i + 2)])
+        cb.barrier()
+        cb.copy(pkg.slot(2), pkg.slot(3 * len(shapes)), out0.numel() * 2)
+        cb.end()
+        fn = lambda: cb.submit(table, max_concurrent=2)  # noqa: E731
+        ms = timed_queued(fn, args.steps, args.warmup)
+        print(json.dumps({"only": w, "ms_per_step": round(ms, 5),
+                          "steps": args.steps}), flush=True)
+        return
     else:
         m = 1 if w == "w8a16" else 512
         x, wq, s = (t.to(dev) for t in inputs.c5_w8a16(m))
