@@ -116,6 +116,14 @@ int iree_mi355x_matmul_mfma_config(int index, const void *a, const void *b,
                                    int64_t ldb, int64_t ldc, uint32_t flags,
                                    void *stream);
 
+// As iree_mi355x_matmul_mfma_config, with the K split count of a split-K
+// configuration forced (0: the planner's; clamped to one K stage per split),
+// so the autotuner can time every split.
+int iree_mi355x_matmul_mfma_config_split(
+    int index, int32_t splits, const void *a, const void *b, const void *scale,
+    void *c, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb,
+    int64_t ldc, uint32_t flags, void *stream);
+
 #ifdef __cplusplus
 }  // extern "C"
 #endif

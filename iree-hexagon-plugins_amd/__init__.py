@@ -61,6 +61,7 @@ EXPORTED_SYMBOLS = (
     "iree_mi355x_executable_library_query", "iree_mi355x_batch_matmul_f16",
     "iree_mi355x_batch_matmul_workspace_bytes",
     "iree_mi355x_mfma_config_layout_flags",
+    "iree_mi355x_matmul_mfma_config_split",
     "iree_mi355x_command_buffer_create", "iree_mi355x_command_buffer_release",
     "iree_mi355x_command_buffer_dispatch", "iree_mi355x_command_buffer_fill",
     "iree_mi355x_command_buffer_copy", "iree_mi355x_command_buffer_barrier",
@@ -243,6 +244,9 @@ def library():
         ctypes.POINTER(i64), ctypes.POINTER(ctypes.c_int32)]
     lib.iree_mi355x_mfma_config_layout_flags.restype = ctypes.c_int32
     lib.iree_mi355x_mfma_config_layout_flags.argtypes = [ctypes.c_int]
+    lib.iree_mi355x_matmul_mfma_config_split.argtypes = [
+        ctypes.c_int, ctypes.c_int32, p, p, p, p, i64, i64, i64, i64, i64, i64,
+        u32, p]
     lib.iree_mi355x_matmul_mfma_config.argtypes = [ctypes.c_int, p, p, p, p,
                                                    i64, i64, i64, i64, i64,
                                                    i64, u32, p]
@@ -611,7 +615,7 @@ def attention(q, k, v, o=None, *, causal=True, scale=None, stream=None):
     return o
 
 
-def matmul_mfma_config(index, a, b, c, *, scale=None, stream=None):
+def matmul_mfma_config(index, a, b, c, *, scale=None, splits=0, stream=None):
     """Run one compiled MFMA configuration (autotuner entry point).
 
     The configuration's B form decides how `b` is read: TN takes B [N, K],
@@ -634,8 +638,8 @@ def matmul_mfma_config(index, a, b, c, *, scale=None, stream=None):
         raise ValueError(f"{cfg.name}: c must be [{m}, {n}]")
     if c.dtype == torch.float32 and a.dtype == torch.float16:
         flags |= OUT_F32
-    _check(library().iree_mi355x_matmul_mfma_config(
-        index, a.data_ptr(), b.data_ptr(),
+    _check(library().iree_mi355x_matmul_mfma_config_split(
+        index, splits, a.data_ptr(), b.data_ptr(),
         scale.data_ptr() if scale is not None else None, c.data_ptr(), m, n,
         k, a.stride(0), b.stride(0), c.stride(0), flags, _stream_ptr(stream)))
     return c

@@ -597,10 +597,16 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     const int splits = (int)gridDim.y;
     const int rows_valid = (int)(M - m0 < BM ? M - m0 : BM);
     const int count = rows_valid * BN;
-    constexpr int G = 8, SB = 8;
-    // The epilogue choice is made once, outside the loop: a per-element
-    // test of the epilogue fields costs the plain reduction ~10%.
-    auto reduce = [&](auto with_epi) {
+    // L device-scope loads in flight per wait (64, or 32 where 512 threads
+    // leave 256 registers a lane): SB split slots for each of G = L / SB
+    // elements, SB the smallest of 2, 4, 8 that covers the splits (more
+    // splits loop in steps of 8). Each element is summed in split order
+    // whatever SB is. The epilogue choice is made once, outside the loop: a
+    // per-element test of the epilogue fields costs the plain reduction ~10%.
+    constexpr int L = NT > 256 ? 32 : 64;
+    auto reduce = [&](auto with_epi, auto sb) {
+      constexpr int SB = decltype(sb)::value;
+      constexpr int G = L / SB;
       for (int base = 0; base < count; base += NT * G) {
         P sum[G];
 #pragma unroll
@@ -647,10 +653,18 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
         }
       }
     };
+    auto reduce_sb = [&](auto with_epi) {
+      if (splits <= 2)
+        reduce(with_epi, std::integral_constant<int, 2>());
+      else if (splits <= 4)
+        reduce(with_epi, std::integral_constant<int, 4>());
+      else
+        reduce(with_epi, std::integral_constant<int, 8>());
+    };
     if (kIntOut || epi_plain(epi))
-      reduce(std::false_type());
+      reduce_sb(std::false_type());
     else
-      reduce(std::true_type());
+      reduce_sb(std::true_type());
     if (tid == 0)  // re-arm for the next call on this workspace
       __hip_atomic_store(&counters[blockIdx.x], 0u, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);

@@ -24,22 +24,32 @@ constexpr int32_t kDefaultCus = 256;
 // Measured choices (bench.py --tune writes the candidates' timings; the
 // winners are recorded here). Keyed by element types, exact shape and flags.
 struct TunedEntry {
-  int32_t a_elem, c_elem;
+  int32_t a_elem, b_elem, c_elem;
   int64_t m, n, k;
   uint32_t flags;
   const char *config;
+  int32_t splits;  // K splits of a split-K configuration (0: the model's)
 };
 // Measured on MI355X with random inputs (bench.py --tune): the 4-wave
 // 256x256 tile wins for int8 (the 8-wave one draws more power for the same
 // work), the 8-wave one for f16.
 const TunedEntry kTuned[] = {
-    {IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_I32, 4096, 4096, 4096,
-     IREE_MI355X_MATMUL_B_TRANSPOSED, "i8_tn_256x256x128_w2x2_s2"},
-    {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 4096, 4096, 4096,
-     IREE_MI355X_MATMUL_B_TRANSPOSED, "f16_tn_256x256x64_w2x4_s2"},
-    {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F32, 4096, 4096, 4096,
-     IREE_MI355X_MATMUL_B_TRANSPOSED, "f16f32_tn_256x256x64_w2x4_s2"},
-    {0, 0, 0, 0, 0, 0, nullptr},  // sentinel
+    {IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_I32, 4096, 4096,
+     4096,
+     IREE_MI355X_MATMUL_B_TRANSPOSED, "i8_tn_256x256x128_w2x2_s2", 0},
+    {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 4096,
+     4096, 4096, IREE_MI355X_MATMUL_B_TRANSPOSED, "f16_tn_256x256x64_w2x4_s2",
+     0},
+    {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F32, 4096,
+     4096, 4096, IREE_MI355X_MATMUL_B_TRANSPOSED,
+     "f16f32_tn_256x256x64_w2x4_s2", 0},
+    // Skinny shapes where the model's pick measured slower than a sweep of
+    // every tile and split count (random inputs, rotating weights).
+    {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 16,
+     4096, 11008, 0, "f16_nn_32x128x64_w1x4_s4_sk", 8},
+    {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_F16, 128,
+     11008, 4096, 0, "w8a16_nn_32x256x64_w1x4_s4_sk", 1},
+    {0, 0, 0, 0, 0, 0, 0, nullptr, 0},  // sentinel
 };
 
 int elem_bytes(int32_t e) {
@@ -158,7 +168,7 @@ constexpr int64_t kMinStagesPerSplit = 2;
 // configuration runs even where one split is all the shape needs.
 bool evaluate(const iree_mi355x_matmul_desc_t &d, const FastConfig &c,
               int index, int64_t cus, Candidate *out,
-              bool explicit_config = false) {
+              bool explicit_config = false, int forced_splits = 0) {
   if (!fast_fits(d, c))
     return false;
   const int64_t batch = d.batch > 0 ? d.batch : 1;
@@ -173,6 +183,8 @@ bool evaluate(const iree_mi355x_matmul_desc_t &d, const FastConfig &c,
     int64_t want = (cus + tiles * batch - 1) / (tiles * batch);
     const int64_t max_splits =
         explicit_config ? d.k / c.bk : d.k / (kMinStagesPerSplit * c.bk);
+    if (forced_splits > 0)
+      want = forced_splits;
     if (want > max_splits)
       want = max_splits;
     if (want < 1)
@@ -225,11 +237,15 @@ bool evaluate(const iree_mi355x_matmul_desc_t &d, const FastConfig &c,
     t = t_chain;
   t += (double)rounds * kRoundNs;
   if (c.split_k && splits > 1) {
-    // the last arriver sums G=8 elements x 8 splits per memory round trip
+    // the last arriver keeps L loads in flight per round trip: SB split
+    // slots (2, 4 or 8) for each of L / SB elements
     const int64_t rows = d.m < c.bm ? d.m : c.bm;
     const int64_t per_thread = (rows * c.bn + c.threads - 1) / c.threads;
-    t += kSplitNs + (double)((per_thread + 7) / 8) *
-                        (double)((splits + 7) / 8) * kRoundTripNs;
+    const int64_t loads = c.threads > 256 ? 32 : 64;
+    const int64_t sb = splits <= 2 ? 2 : splits <= 4 ? 4 : 8;
+    const int64_t g = loads / sb;
+    t += kSplitNs + (double)((per_thread + g - 1) / g) *
+                        (double)((splits + sb - 1) / sb) * kRoundTripNs;
   }
   r.est_ns = (int64_t)t;
   *out = r;
@@ -317,31 +333,42 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
     Candidate best;
     // A measured entry wins when it fits.
     for (const TunedEntry &t : kTuned) {
-      if (!t.config || t.a_elem != d->a_elem || t.c_elem != d->c_elem ||
+      if (!t.config || t.a_elem != d->a_elem || t.b_elem != d->b_elem ||
+          t.c_elem != d->c_elem ||
           t.m != d->m || t.n != d->n || t.k != d->k || t.flags != d->flags)
         continue;
       for (int i = 0; i < count; ++i) {
         Candidate c;
         if (strcmp(cfgs[i].name, t.config) == 0 &&
-            cfgs[i].lds_bytes <= budget && evaluate(*d, cfgs[i], i, cus, &c)) {
+            cfgs[i].lds_bytes <= budget &&
+            evaluate(*d, cfgs[i], i, cus, &c, t.splits > 0, t.splits)) {
           best = c;
           plan->from_tuned_table = 1;
         }
       }
     }
     // Otherwise rank: (modeled time, traffic, tiles, -N) over the
-    // configurations within the LDS budget.
+    // configurations within the LDS budget, each split-K configuration at
+    // the split count that just covers the CUs and at a range of others
+    // (more splits spread the work, fewer shorten the reduction).
     if (best.index < 0) {
       std::tuple<int64_t, int64_t, int64_t, int64_t> best_rank;
+      static const int kSplitChoices[] = {0, 2, 3, 4, 5, 6, 8, 10, 12, 16};
       for (int i = 0; i < count; ++i) {
-        Candidate c;
-        if (cfgs[i].lds_bytes > budget || !evaluate(*d, cfgs[i], i, cus, &c))
+        if (cfgs[i].lds_bytes > budget)
           continue;
-        auto rank = std::make_tuple(c.est_ns, c.traffic, c.tiles,
-                                    -(int64_t)cfgs[i].bn);
-        if (best.index < 0 || rank < best_rank) {
-          best = c;
-          best_rank = rank;
+        for (int forced : kSplitChoices) {
+          if (forced && !cfgs[i].split_k)
+            break;
+          Candidate c;
+          if (!evaluate(*d, cfgs[i], i, cus, &c, false, forced))
+            continue;
+          auto rank = std::make_tuple(c.est_ns, c.traffic, c.tiles,
+                                      -(int64_t)cfgs[i].bn);
+          if (best.index < 0 || rank < best_rank) {
+            best = c;
+            best_rank = rank;
+          }
         }
       }
     }
@@ -431,11 +458,10 @@ int32_t iree_mi355x_mfma_config_layout_flags(int index) {
                                         : 0u));
 }
 
-int iree_mi355x_matmul_mfma_config(int index, const void *a, const void *b,
-                                   const void *scale, void *c, int64_t m,
-                                   int64_t n, int64_t k, int64_t lda,
-                                   int64_t ldb, int64_t ldc, uint32_t flags,
-                                   void *stream) {
+int iree_mi355x_matmul_mfma_config_split(
+    int index, int32_t splits, const void *a, const void *b, const void *scale,
+    void *c, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb,
+    int64_t ldc, uint32_t flags, void *stream) {
   int count = 0;
   const FastConfig *cfgs = fast_configs(&count);
   if (index < 0 || index >= count)
@@ -466,7 +492,10 @@ int iree_mi355x_matmul_mfma_config(int index, const void *a, const void *b,
       (d.has_scale && (!scale || (uintptr_t)scale % 2 != 0)))
     return fail(IREE_MI355X_INVALID_ARGUMENT, "mfma_config: bad arguments");
   Candidate cand;
-  if (!evaluate(d, cfg, index, kDefaultCus, &cand, true))
+  if (splits < 0 || (splits > 1 && !cfg.split_k))
+    return fail(IREE_MI355X_INVALID_ARGUMENT,
+                "mfma_config %s: %d splits", cfg.name, splits);
+  if (!evaluate(d, cfg, index, kDefaultCus, &cand, true, splits))
     return fail(IREE_MI355X_UNSUPPORTED,
                 "mfma_config %s: shape or layout does not fit", cfg.name);
   void *ws = nullptr;
@@ -484,6 +513,15 @@ int iree_mi355x_matmul_mfma_config(int index, const void *a, const void *b,
     return fail(IREE_MI355X_LAUNCH_FAILED, "%s: %s", cfg.name,
                 hipGetErrorString(e));
   return IREE_MI355X_OK;
+}
+
+int iree_mi355x_matmul_mfma_config(int index, const void *a, const void *b,
+                                   const void *scale, void *c, int64_t m,
+                                   int64_t n, int64_t k, int64_t lda,
+                                   int64_t ldb, int64_t ldc, uint32_t flags,
+                                   void *stream) {
+  return iree_mi355x_matmul_mfma_config_split(index, 0, a, b, scale, c, m, n,
+                                              k, lda, ldb, ldc, flags, stream);
 }
 
 }  // extern "C"
