@@ -39,6 +39,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=1000)
     p.add_argument("--suite", action="store_true")
     p.add_argument("--tune", action="store_true")
+    p.add_argument("--tune-skinny", action="store_true",
+                   help="with --tune: sweep tiles x split counts on the "
+                        "skinny C3 / C5 shapes")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--resources", action="store_true",
                    help="print every compiled kernel's registers, LDS, "
@@ -457,8 +460,60 @@ def only(pkg, inputs, dev, args):
                       "steps": args.steps}), flush=True)
 
 
+def tune_skinny(pkg, dev, args):
+    """Every eligible tile at every split count (1..16) on the skinny C3 /
+    C5 shapes, with rotating weights: the sweep the planner's skinny tuned
+    entries and its split enumeration were checked against."""
+    import torch
+    shapes = [("f16", 16, 4096, 4096), ("f16", 16, 11008, 4096),
+              ("f16", 16, 4096, 11008), ("f16", 128, 4096, 4096),
+              ("f16", 128, 11008, 4096), ("f16", 128, 4096, 11008),
+              ("w8a16", 512, 11008, 4096), ("w8a16", 128, 11008, 4096)]
+    cfgs = pkg.mfma_configs()
+    for kind, m, n, k in shapes:
+        g = torch.Generator().manual_seed(m + n + k)
+        x = (torch.randn(m, k, generator=g) * 0.5).half().to(dev)
+        if kind == "f16":
+            w0 = (torch.randn(k, n, generator=g) * 0.02).half().to(dev)
+            sc, form = None, pkg.B_FORM_NN
+            desc = pkg.make_desc(pkg.ELEM_F16, pkg.ELEM_F16, pkg.ELEM_F16, m, n, k)
+        else:
+            w0 = torch.randint(-128, 128, (k, n), generator=g).to(torch.int8).to(dev)
+            sc = (torch.rand(n, generator=g) * 0.019 + 0.001).half().to(dev)
+            form = pkg.B_FORM_W8A16
+            desc = pkg.make_desc(pkg.ELEM_F16, pkg.ELEM_I8, pkg.ELEM_F16, m, n,
+                                 k, has_scale=True)
+        copies = max(1, min(24, ROTATE_BYTES // (w0.numel() * w0.element_size()) + 1))
+        ws = [w0] + [w0.clone() for _ in range(copies - 1)]
+        y = torch.empty(m, n, dtype=torch.float16, device=dev)
+        plan = pkg.plan(desc)
+        for c in cfgs:
+            if (c.b_form != form or c.a_transposed or c.c_elem != pkg.ELEM_F16
+                    or n % c.tile_n or k % c.tile_k):
+                continue
+            split = "_sk" in c.name
+            if not split and m % c.tile_m:
+                continue
+            for sp in ((1, 2, 3, 4, 6, 8, 12, 16) if split else (0,)):
+                if split and k // sp < c.tile_k:
+                    continue
+                it = [0]
+
+                def fn():
+                    pkg.matmul_mfma_config(c.index, x, ws[it[0] % copies], y,
+                                           scale=sc, splits=sp)
+                    it[0] += 1
+                ms = timed(fn, args.steps, args.warmup)
+                print(json.dumps({"shape": [kind, m, n, k], "config": c.name,
+                                  "splits": sp, "us": round(ms * 1000, 2),
+                                  "planned": c.index == plan.config_index and
+                                  (sp == plan.splits or not split)}), flush=True)
+
+
 def tune(pkg, inputs, dev, args):
     import torch
+    if args.tune_skinny:
+        return tune_skinny(pkg, dev, args)
     m = n = k = 4096
     g = torch.Generator().manual_seed(0)
     a8 = torch.randint(-128, 128, (m, k), generator=g).to(torch.int8).to(dev)
