@@ -460,6 +460,11 @@ int iree_mi355x_attention_f16(const void *q, const void *k, const void *v,
       seq_kv >= kMaxExtent || batch * heads * (seq_q > seq_kv ? seq_q : seq_kv) *
                                       head_dim >= ((int64_t)1 << 62))
     return fail(IREE_MI355X_UNSUPPORTED, "attention_f16: problem too large");
+  // The Q / K / V copies address a plane with a 32-bit byte offset.
+  if ((seq_q > seq_kv ? seq_q : seq_kv) * head_dim * 2 > (int64_t)UINT32_MAX)
+    return fail(IREE_MI355X_UNSUPPORTED,
+                "attention_f16: seq %lld x head_dim exceeds 4 GiB per head",
+                (long long)(seq_q > seq_kv ? seq_q : seq_kv));
   if (dry_run(0))
     return ok();
   return launch_status(

@@ -6,8 +6,10 @@
 // iree_linalg_ext.attention, decomposed into an online-softmax loop over KV
 // tiles (CG/Pipelines/LoweringPipelines.cpp:561-595). This kernel is that
 // online-softmax loop on MFMA:
-//  * a workgroup owns a 128-row query block of one (batch, head); each of its
-//    4 waves owns 32 query rows held in registers for the whole loop;
+//  * a workgroup owns a 128-row query block of one (batch, head) and fills a
+//    CU: two groups of 4 waves take alternate 64-key blocks, each wave
+//    owning 32 query rows held in registers for the whole loop, and merge
+//    their partial (O, max, sum) through LDS at the end;
 //  * per 64-key block: S^T = K Q^T on v_mfma_f32_32x32x16_f16, laid out so a
 //    lane holds all scores of one query row (the row max and row sum need one
 //    cross-lane exchange, lane ^ 32);
@@ -16,10 +18,11 @@
 //  * O^T += V^T P^T on MFMA with P taken straight from the score registers
 //    (rounded to f16) and V^T read transposed from key-major LDS
 //    (ds_read_b64_tr_b16);
-//  * K and V blocks stream HBM -> LDS (global_load_lds) one block ahead of
-//    the block being computed;
+//  * K and V blocks stream HBM -> LDS (global_load_lds) into per-group
+//    rings; S^T of the next block is computed on MFMA under the softmax of
+//    the current one;
 //  * causal blocks above the diagonal are skipped, the diagonal blocks are
-//    masked, and heavy query blocks are interleaved with light ones.
+//    masked, and the grid runs the heaviest query blocks first.
 #include <type_traits>
 
 #include "device_common.h"
@@ -30,7 +33,9 @@ namespace ihp {
 namespace {
 constexpr int kBQ = 128;   // query rows per workgroup
 constexpr int kBKV = 64;   // keys per block
-constexpr int kThreads = 256;
+constexpr int kGroups = 2;  // wave groups, each taking every other key block
+constexpr int kThreads = 256 * kGroups;
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 template <int N, int I = 0, typename F>
 __device__ __forceinline__ void static_for(F &&f) {
@@ -40,18 +45,11 @@ __device__ __forceinline__ void static_for(F &&f) {
   }
 }
 
-// Transposed 8-byte LDS read (ds_read_b64_tr_b16): within each 16-lane
-// block, lane i receives element i%4 of the 8-byte loads of lanes
-// 4r + i/4, r = 0..3.
-__device__ __forceinline__ i32x2 lds_read_tr16(const IHP_LDS char *p) {
-  i32x2 v;
-  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v)
-               : "v"((unsigned)(uintptr_t)p));
-  return v;
-}
 __device__ __forceinline__ void tie2(i32x2 &v) { asm volatile("" : "+v"(v)); }
 
-// ds_read_b64_tr_b16 with an immediate byte offset; the caller waits with
+// Transposed 8-byte LDS read (ds_read_b64_tr_b16) with an immediate byte
+// offset: within each 16-lane block, lane i receives element i%4 of the
+// 8-byte loads of lanes 4r + i/4, r = 0..3. The caller waits with
 // lgkm_wait<N>() and ties the result before use.
 template <int OFF>
 __device__ __forceinline__ i32x2 lds_read_tr16_at(const IHP_LDS char *p) {
@@ -107,7 +105,7 @@ __device__ __forceinline__ int v_swizzle(int key) {
 }
 
 template <int D>
-__global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
+__global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
     const f16 *__restrict__ Q, const f16 *__restrict__ K,
     const f16 *__restrict__ V, f16 *__restrict__ O, int heads, int seq_q,
     int seq_kv, float scale_log2, int causal) {
@@ -119,65 +117,115 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
   constexpr int ROWS_PER_INSN = 64 / CH;             // rows per wave copy
   constexpr int PASSES = kBKV / (4 * ROWS_PER_INSN);  // per wave, per tensor
   static_assert(PASSES * 4 * ROWS_PER_INSN == kBKV, "copy shape");
-  __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * BLK];
+  // Per wave group: K ring (slots 0, 1) then V ring (slots 0, 1). After both
+  // groups' rings: the (max, sum) pairs of the merge, one per (wave, lane).
+  // Slot 1 of the rings also stages, between key loops, the query block's
+  // rows (Q in the V slots, rows 0-63 in group 0's, 64-127 in group 1's),
+  // the merge's O hand-over, and the block's output rows (the K slots).
+  constexpr int RING = 4 * BLK;
+  constexpr int XML = 4 * 64 * 8;
+  __shared__ __attribute__((aligned(1024))) char smem[kGroups * RING + XML];
+  // The merge hands one wave's O (DT tiles of 16 floats per lane) through
+  // one ring slot.
+  static_assert(DT * 4 * 64 * 16 == BLK, "one wave's O fills one ring slot");
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // Group grp (waves 4 grp .. 4 grp + 3) takes key blocks grp, grp + 2, ...
+  // of the same 128 query rows; wave wq of each group owns rows 32 wq ..
+  const int grp = wave >> 2, wq = wave & 3;
   const int g = lane >> 5, l32 = lane & 31;
   const int q_blocks = (seq_q + kBQ - 1) / kBQ;
-  // Heaviest (last) query blocks first under a causal mask.
-  // Under a causal mask query block qb costs qb + 1 units. The first half
-  // of the grid takes the heavy blocks (heaviest first), the second half the
-  // light ones (lightest first), so the two workgroups that share a CU sum to
-  // about the same work.
-  const int planes = (int)(gridDim.x / (unsigned)q_blocks);
-  const int idx = (int)(blockIdx.x / (unsigned)planes);
-  const int half = (q_blocks + 1) / 2;
-  const int qb = idx < half ? q_blocks - 1 - idx : idx - half;
+  // A workgroup fills a CU (its LDS) and takes query blocks
+  // q_blocks - 1 - pair and pair of one plane, in that order (one block when
+  // they coincide). Under a causal mask block qb costs qb + 1 units, so every
+  // pair costs q_blocks + 1. Consecutive workgroups take consecutive planes:
+  // with a multiple of 8 planes a plane's pairs share an XCD (and its L2).
+  const int pairs = (q_blocks + 1) >> 1;
+  const int planes = (int)(gridDim.x / (unsigned)pairs);
+  const int pair = (int)(blockIdx.x / (unsigned)planes);
   const int plane = (int)(blockIdx.x % (unsigned)planes);
+  const int n_items = q_blocks - 1 - pair == pair ? 1 : 2;
   const int64_t q_off = (int64_t)plane * seq_q * D;
   const int64_t kv_off = (int64_t)plane * seq_kv * D;
-  const int q0 = qb * kBQ + wave * 32;  // this wave's first query row
-  const int my_q = q0 + l32;
 
-  // Q fragments (B operand of S^T = K Q^T): lane holds query my_q, d chunk
+  // Per query block: this wave's first row, this group's
+  // key blocks (local block i is key block 2 i + grp) and the steps of the
+  // longer group (group 0), which both groups' barriers follow.
+  int q0 = 0, n_mine = 0, n_steps = 0;
+  auto setup = [&](int item) {
+    const int qb = item == 0 ? q_blocks - 1 - pair : pair;
+    q0 = qb * kBQ + wq * 32;
+    const int kv_end = causal ? min(qb * kBQ + kBQ, seq_kv) : seq_kv;
+    const int n_blocks = (kv_end + kBKV - 1) / kBKV;
+    n_mine = (n_blocks - grp + 1) >> 1;
+    n_steps = (n_blocks + 1) >> 1;
+  };
+
+  // Q fragments (B operand of S^T = K Q^T): lane holds query q0 + l32, d chunk
   // 16*s + 8*g .. +7 for every step s.
   i32x4 qf[DS];
-#pragma unroll
-  for (int s = 0; s < DS; ++s) {
-    if (my_q < seq_q)
-      qf[s] = *(const i32x4 *)(Q + q_off + (int64_t)my_q * D + 16 * s + 8 * g);
-    else
-      qf[s] = i32x4{0, 0, 0, 0};
-  }
-
-  int kv_end = seq_kv;
-  if (causal) {
-    const int last_q = qb * kBQ + kBQ - 1;
-    kv_end = last_q + 1 < seq_kv ? last_q + 1 : seq_kv;
-  }
-  const int n_blocks = (kv_end + kBKV - 1) / kBKV;
+  // Row r (0..127) of a query block staged in LDS: rows 0-63 in group 0's
+  // slot `slot`, 64-127 in group 1's, chunks swizzled as K rows are.
+  auto staged_row = [&](int r, int slot) {
+    return (IHP_LDS char *)smem + (r >> 6) * RING + slot * BLK + (r & 63) * ROW;
+  };
 
   // Copy side: a wave instruction moves ROWS_PER_INSN rows of CH chunks;
   // lane -> (row, physical chunk), fetching the logical chunk that belongs
-  // there. Keys past seq_kv are clamped to the last key (masked later).
+  // there. Keys past seq_kv are clamped to the last key (masked later). A
+  // block copy is PASSES instructions per wave.
   const int c_row = lane / CH, c_phys = lane % CH;
-  IHP_LDS char *lds = (IHP_LDS char *)smem;
-  auto copy_block = [&](int kb, int slot) {
+  IHP_LDS char *lds = (IHP_LDS char *)smem + grp * RING;
+  auto copy_block = [&](const f16 *src, int kb, IHP_LDS char *dst,
+                        auto is_v) {
     const int kv0 = kb * kBKV;
-    IHP_LDS char *kd = lds + slot * 2 * BLK;
-    IHP_LDS char *vd = kd + BLK;
+    // Opaque copies: the per-pass addresses are recomputed at each copy
+    // instead of being hoisted into live registers.
+    int lane_row = c_row, lane_chunk = c_phys;
+    asm volatile("" : "+v"(lane_row), "+v"(lane_chunk));
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
-      const int row = (p * 4 + wave) * ROWS_PER_INSN + c_row;
+      const int row = (p * 4 + wq) * ROWS_PER_INSN + lane_row;
       int key = kv0 + row;
       key = key < seq_kv ? key : seq_kv - 1;
-      const f16 *kr = K + kv_off + (int64_t)key * D;
-      const f16 *vr = V + kv_off + (int64_t)key * D;
-      global_to_lds_16(kr + 8 * (c_phys ^ k_swizzle<D>(row)),
-                       kd + (p * 4 + wave) * ROWS_PER_INSN * ROW);
-      global_to_lds_16(vr + 8 * (c_phys ^ v_swizzle<D>(row)),
-                       vd + (p * 4 + wave) * ROWS_PER_INSN * ROW);
+      const int sw = decltype(is_v)::value ? v_swizzle<D>(row)
+                                           : k_swizzle<D>(row);
+      // Uniform plane base + 32-bit lane offset: one VGPR per address.
+      const uint32_t off = (uint32_t)key * ROW + 16u * (lane_chunk ^ sw);
+      global_to_lds_16((const char *)(src + kv_off) + off,
+                       dst + (p * 4 + wq) * ROWS_PER_INSN * ROW);
+    }
+  };
+  auto copy_k = [&](int i) {
+    copy_block(K, 2 * i + grp, lds + (i & 1) * BLK, std::false_type());
+  };
+  // The query block's rows into the V slots 1 (all 8 waves, PASSES
+  // instructions each); rows past seq_q are clamped to the last row (their
+  // outputs are not stored).
+  auto copy_q = [&]() {
+    int lane_row = c_row, lane_chunk = c_phys;
+    asm volatile("" : "+v"(lane_row), "+v"(lane_chunk));
+    const int qrow0 = q0 - wq * 32;  // the block's first row
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int r0 = (p * 8 + wave) * ROWS_PER_INSN;
+      const int r = r0 + lane_row;
+      const int row = min(qrow0 + r, seq_q - 1);
+      const uint32_t off =
+          (uint32_t)row * ROW + 16u * (lane_chunk ^ k_swizzle<D>(r));
+      global_to_lds_16((const char *)(Q + q_off) + off, staged_row(r0, 3));
+    }
+  };
+  auto copy_v = [&](int i) {
+    copy_block(V, 2 * i + grp, lds + (2 + (i & 1)) * BLK, std::true_type());
+  };
+  // A query block's first key blocks (slots 0); K(1) goes out separately,
+  // last, and the block's first barrier does not wait for it.
+  auto copy_first = [&]() {
+    if (n_mine > 0) {
+      copy_k(0);
+      copy_v(0);
     }
   };
 
@@ -198,156 +246,299 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(
                 (((b0 >> 4) ^ v_swizzle<D>(v_row_in)) << 4) + (b0 & 15);
   }
 
-  f32x16 o[DT];
+  // K read side: step s reads chunk c = 2s + g of key l32 (+32 for the
+  // second key tile, which has the same swizzle). With w = k_swizzle(key),
+  // c ^ w = 2 (s ^ w/2) + (g ^ w%2), so every step's address is one base
+  // XOR 32 s (the key * ROW part has no bits below ROW).
+  // S^T tiles of local block i: keys 32t..32t+31 x this wave's 32 queries.
+  auto scores = [&](int i, f32x16 (&st)[2]) {
+    const IHP_LDS char *ks = lds + (i & 1) * BLK;
+    // Recomputed from an opaque copy of the lane id at each call, instead
+    // of keeping the base (or DS per-step addresses) live across the loop.
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int kl = ln & 31, kg = ln >> 5;
+    const int k_sw = k_swizzle<D>(kl);
+    const int kaddr = kl * ROW + 16 * (kg ^ (k_sw & 1)) + 32 * (k_sw >> 1);
 #pragma unroll
-  for (int t = 0; t < DT; ++t)
-#pragma unroll
-    for (int r = 0; r < 16; ++r)
-      o[t][r] = 0.0f;
-  float m_run = -INFINITY, l_run = 0.0f;
-
-  if (n_blocks > 0)
-    copy_block(0, 0);
-  for (int kb = 0; kb < n_blocks; ++kb) {
-    const int kv0 = kb * kBKV;
-    const int slot = kb & 1;
-    // Block kb has landed for every wave, and every wave is done with block
-    // kb-1, whose slot now receives block kb+1 while kb is computed.
-    wait_vmcnt<0>();
-    block_barrier();
-    if (kb + 1 < n_blocks)
-      copy_block(kb + 1, slot ^ 1);
-    const IHP_LDS char *ks = lds + slot * 2 * BLK;
-    const IHP_LDS char *vs = ks + BLK;
-
-    // S^T tiles: keys 32t..32t+31 x this wave's 32 queries.
-    f32x16 st[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        st[t][r] = 0.0f;
-      const int key = 32 * t + l32;
-#pragma unroll
-      for (int s = 0; s < DS; ++s) {
-        const int c = 2 * s + g;
-        const i32x4 kf =
-            *(const IHP_LDS i32x4 *)(ks + key * ROW + ((c ^ k_swizzle<D>(key)) * 16));
-        st[t] = Mfma32<f16>::mma(kf, qf[s], st[t]);
-      }
-    }
-
-    // Mask (causal diagonal, sequence tail), then the online softmax update
-    // in the log2 domain: p = 2^(s * scale_log2 - m). Off the diagonal the
-    // row max is taken on the raw scores (scale_log2 > 0 keeps the order) and
-    // the scale is fused into the exponent's FMA.
-    const bool need_mask =
-        (causal && kv0 + kBKV - 1 > q0) || kv0 + kBKV > seq_kv;
-    float mx;
-    float sc = scale_log2;  // multiplier applied inside the exponent
-    if (need_mask || scale_log2 <= 0.0f) {
-      mx = -INFINITY;
+    for (int s = 0; s < DS; ++s)
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
+        const i32x4 kf = *(const IHP_LDS i32x4 *)(ks + (kaddr ^ (32 * s)) +
+                                                  32 * t * ROW);
+        // The first step accumulates onto an inline zero.
+        st[t] = Mfma32<f16>::mma(kf, qf[s], s == 0 ? f32x16{} : st[t]);
+      }
+  };
+  // Mask (causal diagonal, sequence tail) and row max of local block i, in
+  // the log2 domain. Off the diagonal the max is taken on the raw scores
+  // (scale_log2 > 0 keeps the order) and the scale goes into the exponent's
+  // FMA (*sc); masked blocks are scaled in place (*sc = 1).
+  auto mask_max = [&](int i, f32x16 (&st)[2], float &mx, float &sc) {
+    const int kv0 = (2 * i + grp) * kBKV;
+    const bool need_mask =
+        (causal && kv0 + kBKV - 1 > q0) || kv0 + kBKV > seq_kv;
+    mx = -INFINITY;
+    if (need_mask || scale_log2 <= 0.0f) {
+      // Element (t, r) holds key kv0 + 4 g + c, c = 32 t + 8 (r / 4) + r % 4;
+      // keys at or past min(seq_kv, q0 + l32 + 1) (causal) are masked, i.e.
+      // c >= thr: one compare against a constant and one select each.
+      // (Lane terms recomputed from an opaque lane id: not kept live.)
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int row = q0 + (ln & 31);
+      const int lim = causal ? min(seq_kv, row + 1) : seq_kv;
+      const int thr = lim - kv0 - 4 * (ln >> 5);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          float s = st[t][r] * scale_log2;
-          const int key = kv0 + 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
-          if (key >= seq_kv || (causal && key > my_q))
-            s = -INFINITY;
+          const int c = 32 * t + 8 * (r >> 2) + (r & 3);
+          const float s = c >= thr ? -INFINITY : st[t][r] * scale_log2;
           st[t][r] = s;
           mx = fmaxf(mx, s);
         }
-      }
       sc = 1.0f;
     } else {
-      mx = -INFINITY;
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
           mx = fmaxf(mx, st[t][r]);
       mx *= scale_log2;
+      sc = scale_log2;
     }
     mx = pair_max(mx);
-    const float m_new = fmaxf(m_run, mx);
-    // A row with every key masked so far keeps m = -inf; exp2 of a finite
-    // offset from it must not produce nan.
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    float psum = 0.0f;
+  };
+
+  // Group 0's O^T tile of this wave, normalised to f16, into the staged
+  // output rows (the K slots 1): 4 d of row 32 wq + l32 per register
+  // quarter, 16-byte chunk 4 dt + rq swizzled as K rows are, half g.
+  auto stage_o = [&](const f32x16 (&acc)[DT], float inv) {
+    const int r = wq * 32 + l32;
+    IHP_LDS char *dst = staged_row(r, 1);
+    const int sw = k_swizzle<D>(r);
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(st[t][r], sc, -m_use));
-        st[t][r] = p;
-        psum += p;
+      for (int rq = 0; rq < 4; ++rq) {
+        f16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[e] = (f16)(acc[dt][4 * rq + e] * inv);
+        *(IHP_LDS f16x4 *)(dst + 16 * ((4 * dt + rq) ^ sw) + 8 * g) = v;
       }
-    psum = pair_sum(psum);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-    // rescale the running output only when some row's max moved
-    if (!__all(alpha == 1.0f)) {
+  };
+  // The staged rows to HBM, 16 bytes per lane (all 8 waves, PASSES
+  // instructions each); rows past seq_q are not written.
+  auto store_rows = [&](int qrow0) {
 #pragma unroll
-      for (int t = 0; t < DT; ++t)
+    for (int p = 0; p < PASSES; ++p) {
+      const int r = (p * 8 + wave) * ROWS_PER_INSN + c_row;
+      const i32x4 v = *(const IHP_LDS i32x4 *)(
+          staged_row(r, 1) + 16 * (c_phys ^ k_swizzle<D>(r)));
+      if (qrow0 + r < seq_q)
+        *(i32x4 *)(O + q_off + (int64_t)(qrow0 + r) * D + 8 * c_phys) = v;
+    }
+  };
+
+  f32x16 o[DT];
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  setup(0);
+  copy_q();
+  copy_first();
+  if (n_mine > 1)
+    copy_k(1);
+  for (int item = 0;;) {
+    // Q, K(0), V(0) of this block (and the previous block's output
+    // stores) have completed in every wave. K(1), when issued, is each
+    // wave's newest memory operation and may stay in flight.
+    if (n_mine > 1)
+      wait_vmcnt<PASSES>();
+    else
+      wait_vmcnt<0>();
+    block_barrier();
+    {
+      // This wave's 32 query rows, read like K rows (conflict-free). The V
+      // slots 1 are overwritten only after step 0's barrier, which every
+      // wave reaches after consuming qf in S(0).
+      const IHP_LDS char *qs = staged_row(wq * 32, 3);
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int kl = ln & 31, kg = ln >> 5;
+      const int k_sw = k_swizzle<D>(kl);
+      const int qaddr = kl * ROW + 16 * (kg ^ (k_sw & 1)) + 32 * (k_sw >> 1);
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          o[t][r] *= alpha;
+      for (int s = 0; s < DS; ++s)
+        qf[s] = *(const IHP_LDS i32x4 *)(qs + (qaddr ^ (32 * s)));
+    }
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        o[t][r] = 0.0f;
+    m_run = -INFINITY;
+    l_run = 0.0f;
+
+    // Pipeline over this group's key blocks: iteration j computes S(j+1) on
+    // MFMA while the VALU turns the first half of block j's scores into
+    // probabilities, then O += V(j) P(j) on MFMA while the VALU finishes
+    // block j's probabilities and masks S(j+1). K and V have rings of their
+    // own, one block apart: at the top of iteration j (after the barrier) K
+    // slot j%2 (read by S(j)) and V slot (j+1)%2 (read by PV(j-1)) are free
+    // and receive K(j+2), V(j+1). The last iteration computes a discarded S
+    // from a stale, in-bounds slot. Every wave passes n_steps barriers here.
+    if (n_mine > 0) {
+      f32x16 sa[2], sb[2];
+      float mx_a, sc_a, mx_b, sc_b;
+      scores(0, sa);
+      mask_max(0, sa, mx_a, sc_a);
+
+      auto step = [&](int j, f32x16 (&cur)[2], float mx_cur, float sc_cur,
+                      f32x16 (&nxt)[2], float &mx_nxt, float &sc_nxt) {
+        wait_vmcnt<0>();
+        block_barrier();
+        if (j + 2 < n_mine)
+          copy_k(j + 2);
+        if (j + 1 < n_mine)
+          copy_v(j + 1);
+        // Phase A: running max, output rescale when it moved, S(j+1) on
+        // MFMA with the first 32 keys' probabilities on the VALU.
+        const float m_new = fmaxf(m_run, mx_cur);
+        // A row with every key masked so far keeps m = -inf; exp2 of a
+        // finite offset from it must not produce nan.
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        m_run = m_new;
+        if (!__all(alpha == 1.0f)) {
+#pragma unroll
+          for (int t = 0; t < DT; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              o[t][r] *= alpha;
+        }
+        scores(j + 1, nxt);
+        float psum = 0.0f;
+        // P fragment of key step st (keys 16 st .. 16 st + 15 of block j).
+        auto probs = [&](int st) {
+          f16x8 pf;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(
+                cur[st >> 1][8 * (st & 1) + e], sc_cur, -m_use));
+            psum += p;
+            pf[e] = (f16)p;
+          }
+          return __builtin_bit_cast(i32x4, pf);
+        };
+        i32x4 pb0 = probs(0), pb1 = probs(1);
+        // Phase B: O^T[d][q] += V^T[d][key] P^T[key][q], 16 keys per MFMA,
+        // with the other 32 keys' probabilities and the mask / max of S(j+1)
+        // on the VALU.
+        const IHP_LDS char *vs = lds + (2 + (j & 1)) * BLK;
+        static_for<4>([&](auto step_c) {
+          constexpr int ST = decltype(step_c)::value;
+          constexpr int KOFF = 16 * ST * ROW;
+          i32x2 vr[DT][2];
+          static_for<DT>([&](auto dt) {
+            constexpr int DTI = decltype(dt)::value;
+            vr[DTI][0] = lds_read_tr16_at<KOFF>(vs + v_off[DTI]);
+            vr[DTI][1] = lds_read_tr16_at<KOFF + 8 * ROW>(vs + v_off[DTI]);
+          });
+          const i32x4 pcur = ST == 0 ? pb0 : ST == 1 ? pb1 : probs(ST);
+          lgkm_wait<0>();
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) {
+            tie2(vr[dt][0]);
+            tie2(vr[dt][1]);
+            const i32x4 vf = i32x4{vr[dt][0][0], vr[dt][0][1], vr[dt][1][0],
+                                   vr[dt][1][1]};
+            o[dt] = Mfma32<f16>::mma(vf, pcur, o[dt]);
+          }
+        });
+        l_run = l_run * alpha + pair_sum(psum);
+        mask_max(j + 1, nxt, mx_nxt, sc_nxt);
+      };
+
+      int j = 0;
+      while (true) {
+        step(j, sa, mx_a, sc_a, sb, mx_b, sc_b);
+        if (++j == n_mine)
+          break;
+        step(j, sb, mx_b, sc_b, sa, mx_a, sc_a);
+        if (++j == n_mine)
+          break;
+      }
+    }
+    // Group 1 has one block fewer when the block count is odd: it meets
+    // group 0's last barrier here.
+    if (n_mine < n_steps)
+      block_barrier();
+    // Every ring slot is free once all waves pass this barrier.
+    block_barrier();
+    const int qrow0 = q0 - wq * 32;  // this block's first row
+    const bool more = item + 1 < n_items;
+    // The next block's first key blocks stream into slots 0 during the
+    // merge, which uses slots 1.
+    if (more) {
+      setup(item + 1);
+      copy_first();
     }
 
-    // O^T[d][q] += V^T[d][key] P^T[key][q], 16 keys per MFMA; the V^T
-    // reads of key step i+1 are in flight during the MFMAs of step i.
-    i32x2 vr[2][DT][2];
-    auto read_v = [&](auto step, i32x2 (&dst)[DT][2]) {
-      constexpr int ST = decltype(step)::value;  // (t, h) = (ST / 2, ST % 2)
-      constexpr int KOFF = 16 * ST * ROW;
-      static_for<DT>([&](auto dt) {
-        constexpr int DTI = decltype(dt)::value;
-        dst[DTI][0] = lds_read_tr16_at<KOFF>(vs + v_off[DTI]);
-        dst[DTI][1] = lds_read_tr16_at<KOFF + 8 * ROW>(vs + v_off[DTI]);
-      });
-    };
-    read_v(std::integral_constant<int, 0>(), vr[0]);
-    static_for<4>([&](auto step) {
-      constexpr int ST = decltype(step)::value;
-      constexpr int CUR = ST & 1;
-      if constexpr (ST + 1 < 4) {
-        read_v(std::integral_constant<int, ST + 1>(), vr[CUR ^ 1]);
-        lgkm_wait<2 * DT>();
-      } else {
-        lgkm_wait<0>();
-      }
-      f16x8 pf;
+    // Merge: group 1 hands (O, m, l) to group 0. Wave wq's O goes through
+    // ring slot 1 (K, then V) of group wq / 2: float4 k of tile dt at
+    // (dt 4 + k) 64 + lane; (m, l) after the rings at wq 64 + lane.
+    IHP_LDS f32x4 *xo = (IHP_LDS f32x4 *)(smem + (wq >> 1) * RING +
+                                          (1 + 2 * (wq & 1)) * BLK);
+    IHP_LDS f32x2 *xml = (IHP_LDS f32x2 *)(smem + kGroups * RING);
+    if (grp == 1) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        pf[e] = (f16)st[ST >> 1][8 * (ST & 1) + e];
-      const i32x4 pb = __builtin_bit_cast(i32x4, pf);
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        tie2(vr[CUR][dt][0]);
-        tie2(vr[CUR][dt][1]);
-        const i32x4 vf = i32x4{vr[CUR][dt][0][0], vr[CUR][dt][0][1],
-                               vr[CUR][dt][1][0], vr[CUR][dt][1][1]};
-        o[dt] = Mfma32<f16>::mma(vf, pb, o[dt]);
-      }
-    });
-  }
-
-  if (my_q >= seq_q)
-    return;
-  const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-  f16 *orow = O + q_off + (int64_t)my_q * D;
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-    for (int rq = 0; rq < 4; ++rq) {
-      f16x4 v;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        v[e] = (f16)(o[dt][4 * rq + e] * inv);
-      *(f16x4 *)(orow + 32 * dt + 8 * rq + 4 * g) = v;
+        for (int k = 0; k < 4; ++k)
+          xo[(dt * 4 + k) * 64 + lane] =
+              f32x4{o[dt][4 * k], o[dt][4 * k + 1], o[dt][4 * k + 2],
+                    o[dt][4 * k + 3]};
+      xml[wq * 64 + lane] = f32x2{m_run, l_run};
+      wait_lgkmcnt0();
     }
+    block_barrier();
+    if (grp == 0) {
+      const f32x2 ml = xml[wq * 64 + lane];
+      const float m = fmaxf(m_run, ml[0]);
+      const float m_use = m == -INFINITY ? 0.0f : m;
+      const float a0 = __builtin_amdgcn_exp2f(m_run - m_use);
+      const float a1 = __builtin_amdgcn_exp2f(ml[0] - m_use);
+      l_run = l_run * a0 + ml[1] * a1;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const f32x4 x = xo[(dt * 4 + k) * 64 + lane];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            o[dt][4 * k + e] = o[dt][4 * k + e] * a0 + x[e] * a1;
+        }
+    }
+    // The slots 1 are free again: the next block's rows stream into the V
+    // slots, this block's output rows are staged in the K slots.
+    block_barrier();
+    if (more)
+      copy_q();
+    if (grp == 0)
+      stage_o(o, l_run > 0.0f ? 1.0f / l_run : 0.0f);
+    wait_lgkmcnt0();
+    block_barrier();
+    store_rows(qrow0);
+    if (!more)
+      return;
+    // The staged rows have been read: K(1) of the next block may land.
+    wait_lgkmcnt0();
+    block_barrier();
+    if (n_mine > 1)
+      copy_k(1);
+    ++item;
   }
 }
 
@@ -357,7 +548,8 @@ hipError_t launch_attention(const void *q, const void *k, const void *v,
                             float scale, int causal, void *stream) {
   const int64_t q_blocks = (seq_q + kBQ - 1) / kBQ;
   const int64_t planes = batch * heads;
-  dim3 grid((unsigned)(q_blocks * planes));
+  // One workgroup per pair of query blocks (q_blocks - 1 - k, k).
+  dim3 grid((unsigned)((q_blocks + 1) / 2 * planes));
   const float scale_log2 = scale * 1.4426950408889634f;  // log2(e)
   if (head_dim == 128)
     hipLaunchKernelGGL((attention_fwd_kernel<128>), grid, dim3(kThreads), 0,

@@ -236,7 +236,9 @@ const iree_mi355x_executable_dispatch_fn_t kPtrs[] = {
 // GPU tests compare them with what the loaded kernels report): the f16 and
 // int8 MFMA rings (128 KiB: 2 x 64 KiB or 4 x 32 KiB, 512 threads), the
 // W8A16 256x256 ring (3 x 48 KiB), the GEMV (512 threads, its 8-wave
-// reduction buffer at most 128 KiB), the attention K/V ring (2 x 32 KiB).
+// reduction buffer at most 128 KiB), the attention K/V rings (two wave
+// groups x 4 x 16 KiB) and the merge's (max, sum) exchange (2 KiB), 512
+// threads.
 constexpr uint64_t kF16Flags = IREE_MI355X_DISPATCH_FLAG_RESOURCES_VALID |
                                IREE_MI355X_DISPATCH_FLAG_USES_MFMA |
                                IREE_MI355X_DISPATCH_FLAG_USES_LDS_DMA |
@@ -251,7 +253,7 @@ const iree_mi355x_executable_dispatch_attrs_t kAttrs[] = {
     {IREE_MI355X_DISPATCH_FLAG_RESOURCES_VALID |
          IREE_MI355X_DISPATCH_FLAG_USES_MFMA |
          IREE_MI355X_DISPATCH_FLAG_USES_LDS_DMA,
-     65536, 256},
+     133120, 512},
     {kF16Flags, 131072, 512},
 };
 

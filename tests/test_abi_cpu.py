@@ -211,6 +211,13 @@ def test_attention_argument_errors(pkg):
                None) == pkg.INVALID_ARGUMENT
     assert att(FAKE, FAKE, FAKE, FAKE, 0, 1, 128, 128, 128, 0.1, 1,
                None) == pkg.OK
+    # one head's K / V past 4 GiB (32-bit copy offsets)
+    assert att(FAKE, FAKE, FAKE, FAKE, 1, 1, 128, 1 << 24, 128, 0.1, 0,
+               None) == pkg.UNSUPPORTED
+    assert "4 GiB" in pkg.last_error()
+    assert att(FAKE, FAKE, FAKE, FAKE, 1, 1, 1 << 24, 128, 128, 0.1, 0,
+               None) == pkg.UNSUPPORTED
+    assert "4 GiB" in pkg.last_error()
 
 
 def test_dispatch_rejects_short_bindings(pkg):
