@@ -36,6 +36,9 @@ constexpr int kBKV = 64;   // keys per block
 constexpr int kGroups = 2;  // wave groups, each taking every other key block
 constexpr int kThreads = 256 * kGroups;
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+// Lazy running max: tolerated growth of a row's max (log2 units) before the
+// reference max moves and the output is rescaled.
+constexpr float kLazyMax = 8.0f;
 
 template <int N, int I = 0, typename F>
 __device__ __forceinline__ void static_for(F &&f) {
@@ -403,21 +406,26 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
           copy_k(j + 2);
         if (j + 1 < n_mine)
           copy_v(j + 1);
-        // Phase A: running max, output rescale when it moved, S(j+1) on
-        // MFMA with the first 32 keys' probabilities on the VALU.
-        const float m_new = fmaxf(m_run, mx_cur);
-        // A row with every key masked so far keeps m = -inf; exp2 of a
-        // finite offset from it must not produce nan.
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-        m_run = m_new;
-        if (!__all(alpha == 1.0f)) {
+        // Phase A: reference max and output rescale, S(j+1) on MFMA with
+        // the first 32 keys' probabilities on the VALU. The reference max
+        // m_run moves only when some row's block max exceeds it by more
+        // than kLazyMax (log2 units), so probabilities stay at most
+        // 2^kLazyMax (exact in f16) and most blocks skip the rescale.
+        float alpha = 1.0f;
+        if (!__all(mx_cur <= m_run + kLazyMax)) {
+          const float m_new = fmaxf(m_run, mx_cur);
+          // A row with every key masked so far keeps m = -inf; exp2 of a
+          // finite offset from it must not produce nan.
+          alpha = __builtin_amdgcn_exp2f(
+              m_run - (m_new == -INFINITY ? 0.0f : m_new));
+          m_run = m_new;
 #pragma unroll
           for (int t = 0; t < DT; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r)
               o[t][r] *= alpha;
         }
+        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
         scores(j + 1, nxt);
         float psum = 0.0f;
         // P fragment of key step st (keys 16 st .. 16 st + 15 of block j).
