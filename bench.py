@@ -494,8 +494,9 @@ def tune_skinny(pkg, dev, args):
             split = "_sk" in c.name
             if not split and m % c.tile_m:
                 continue
-            for sp in ((1, 2, 3, 4, 6, 8, 12, 16) if split else (0,)):
-                if split and k // sp < c.tile_k:
+            for sp in ((1, 2, 3, 4, 6, 8, 12, 16, pkg.SPLITS_STREAM_K)
+                       if split else (0,)):
+                if split and sp > 0 and k // sp < c.tile_k:
                     continue
                 it = [0]
 
@@ -507,7 +508,10 @@ def tune_skinny(pkg, dev, args):
                 print(json.dumps({"shape": [kind, m, n, k], "config": c.name,
                                   "splits": sp, "us": round(ms * 1000, 2),
                                   "planned": c.index == plan.config_index and
-                                  (sp == plan.splits or not split)}), flush=True)
+                                  (not split or
+                                   (sp == pkg.SPLITS_STREAM_K
+                                    if plan.stream_k_steps > 0
+                                    else sp == plan.splits))}), flush=True)
 
 
 def tune(pkg, inputs, dev, args):

@@ -67,6 +67,10 @@ typedef struct iree_mi355x_matmul_plan_t {
   int64_t workspace_bytes;
   int64_t traffic_bytes;           // modeled global->LDS bytes of the plan
   int32_t from_tuned_table;        // 1 if a measured entry chose it
+  // Stream-K (split-K configuration, batch 1): K stages per workgroup; the
+  // workgroups take equal runs of the (tile, K stage) pairs and `splits`
+  // is the most runs one tile spans. 0: one tile (split) per workgroup.
+  int32_t stream_k_steps;
 } iree_mi355x_matmul_plan_t;
 
 // Fills defaults: both operands assumed 16-byte aligned, no scale, 160 KiB
@@ -117,8 +121,10 @@ int iree_mi355x_matmul_mfma_config(int index, const void *a, const void *b,
                                    void *stream);
 
 // As iree_mi355x_matmul_mfma_config, with the K split count of a split-K
-// configuration forced (0: the planner's; clamped to one K stage per split),
-// so the autotuner can time every split.
+// configuration forced (0: the planner's; clamped to one K stage per split;
+// IREE_MI355X_SPLITS_STREAM_K: stream-K runs, batch 1), so the autotuner can
+// time every split.
+#define IREE_MI355X_SPLITS_STREAM_K (-1)
 int iree_mi355x_matmul_mfma_config_split(
     int index, int32_t splits, const void *a, const void *b, const void *scale,
     void *c, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb,

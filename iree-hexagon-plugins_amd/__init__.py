@@ -38,6 +38,7 @@ B_TRANSPOSED = 0x1
 ACCUMULATE = 0x2
 OUT_F32 = 0x4
 A_TRANSPOSED = 0x8
+SPLITS_STREAM_K = -1  # matmul_mfma_config: stream-K runs of (tile, K stage)
 CAUSAL = 0x1
 
 # Element kinds (iree_mi355x_elem_t) and kernel families.
@@ -114,7 +115,8 @@ class MatmulPlan(ctypes.Structure):
                 ("k_split", ctypes.c_int32),
                 ("workspace_bytes", ctypes.c_int64),
                 ("traffic_bytes", ctypes.c_int64),
-                ("from_tuned_table", ctypes.c_int32)]
+                ("from_tuned_table", ctypes.c_int32),
+                ("stream_k_steps", ctypes.c_int32)]
 
 
 class DispatchState(ctypes.Structure):
@@ -620,7 +622,9 @@ def matmul_mfma_config(index, a, b, c, *, scale=None, splits=0, stream=None):
 
     The configuration's B form decides how `b` is read: TN takes B [N, K],
     NN takes B [K, N] f16, W8A16 takes B [K, N] int8 plus `scale`; a
-    transposed-A configuration takes A [K, M]."""
+    transposed-A configuration takes A [K, M]. `splits` forces a split-K
+    configuration's K split count (0: the planner's; SPLITS_STREAM_K:
+    stream-K runs)."""
     import torch
     cfg = mfma_configs()[index]
     k, m = a.shape if cfg.a_transposed else a.shape[::-1]

@@ -111,6 +111,8 @@ static int launch_mfma(MatmulArgs &args, const iree_mi355x_matmul_plan_t &plan,
   const FastConfig *cfgs = fast_configs(&count);
   args.splits = plan.splits > 1 ? plan.splits : 1;
   args.k_split = plan.k_split;
+  args.sk_steps = plan.stream_k_steps;
+  args.sk_workgroups = plan.stream_k_steps > 0 ? (int)plan.workgroups : 0;
   args.workspace = nullptr;
   if (plan.workspace_bytes > 0) {
     if (workspace && workspace_bytes < (size_t)plan.workspace_bytes)

@@ -113,7 +113,10 @@ __device__ __forceinline__ void lgkm_tie2(i32x2 &v) {
 //
 // SPLIT: the K extent is split over gridDim.y (k_split elements each); every
 // workgroup publishes an f32 (i32) partial tile and the last one to arrive at
-// a tile sums the partials in split order and writes C. M need not be a
+// a tile sums the partials in split order and writes C. With sk_steps > 0
+// (stream-K) the workgroups instead take equal runs of the (tile, K stage)
+// pairs, so tile counts that leave CUs idle still fill the chip; a tile
+// split over several runs is reduced the same way. M need not be a
 // multiple of BM: A rows past M are clamped to row M-1 on the copy side (rows
 // of C depend only on their own row of A) and never stored.
 template <typename T, typename OutT, int BM, int BN, int BKB, int WM, int WN,
@@ -121,7 +124,7 @@ template <typename T, typename OutT, int BM, int BN, int BKB, int WM, int WN,
 __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     const T *__restrict__ A, const void *__restrict__ Bv, OutT *__restrict__ C,
     const f16 *__restrict__ scale, int M, int N, int K, int64_t lda,
-    int64_t ldb, int64_t ldc, int accumulate, int k_split,
+    int64_t ldb, int64_t ldc, int accumulate, int k_split, int sk_steps,
     typename Mfma32<T>::AccScalar *__restrict__ partials,
     unsigned *__restrict__ counters, int64_t sa, int64_t sb, int64_t sc,
     Epi epi, int64_t s_mul) {
@@ -201,13 +204,14 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   const int wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int tiles_m = SPLIT ? (M + BM - 1) / BM : M / BM;
+
+  // One tile's K range [k_begin, k_begin + k_len): partial `part` of the
+  // tile's `parts` (a single part stores C directly).
+  auto tile_body = [&](int tile, int tiles, int64_t k_begin, int64_t k_len,
+                       int part, int parts) __attribute__((always_inline)) {
   int tm, tn;
-  xcd_tile_order(blockIdx.x, gridDim.x, tiles_m, N / BN, 4, &tm, &tn);
+  xcd_tile_order(tile, tiles, tiles_m, N / BN, 4, &tm, &tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  // This workgroup's K range (the whole K unless split).
-  const int64_t k_begin = SPLIT ? (int64_t)blockIdx.y * k_split : 0;
-  const int64_t k_len = SPLIT ? (K - k_begin < k_split ? K - k_begin : k_split)
-                              : K;
 
   // Copy side: lane -> (row in the wave's slab, physical chunk); the global
   // chunk it fetches is the logical chunk that belongs in that slot. The
@@ -490,7 +494,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   const int row_l = 4 * (lane >> 5);
   constexpr bool kIntOut = std::is_same<OutT, int32_t>::value;
   if constexpr (!kIntOut) {
-    if ((!SPLIT || gridDim.y == 1) && !epi_plain(epi)) {
+    if ((!SPLIT || parts == 1) && !epi_plain(epi)) {
       // Fused epilogue: each 32-row fragment band of a wave goes through
       // LDS (the idle stage ring) column-major with a 33-float pitch, then
       // one rolled loop applies scale / bias / activation / multiplier and
@@ -528,7 +532,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   }
   // One split (a ragged-M shape whose tiles alone cover the CUs): store
   // directly, rows past M masked, no partials.
-  if (!SPLIT || gridDim.y == 1) {
+  if (!SPLIT || parts == 1) {
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       OutT *crow = C + (m0 + wm * WTM + i * 32 + row_l) * ldc + n0 +
@@ -562,7 +566,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     // stores; the last workgroup of the tile reads them with device-scope
     // loads. Only partials and the counter are shared, so no L2 write-back /
     // invalidate fence is needed, only the stores drained before arriving.
-    P *part = partials + (int64_t)blockIdx.y * M * N;
+    P *part_out = partials + (int64_t)part * M * N;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -573,7 +577,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
           const int64_t row =
               m0 + wm * WTM + i * 32 + row_l + 8 * (r >> 2) + (r & 3);
           if (row < M)
-            store_device(part + row * N + col, (P)acc[i][j][r]);
+            store_device(part_out + row * N + col, (P)acc[i][j][r]);
         }
       }
     }
@@ -584,9 +588,9 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     __syncthreads();
     if (tid == 0) {
       const unsigned prev =
-          __hip_atomic_fetch_add(&counters[blockIdx.x], 1u, __ATOMIC_RELAXED,
+          __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_AGENT);
-      *last_split = prev == gridDim.y - 1;
+      *last_split = prev == (unsigned)parts - 1;
     }
     __syncthreads();
     if (!*last_split)
@@ -594,7 +598,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     // The tile's valid rows, G elements per thread at a time, each summed
     // over the splits in split order: G x SB device-scope loads in flight
     // per wait instead of one element's splits.
-    const int splits = (int)gridDim.y;
+    const int splits = parts;
     const int rows_valid = (int)(M - m0 < BM ? M - m0 : BM);
     const int count = rows_valid * BN;
     // L device-scope loads in flight per wait (64, or 32 where 512 threads
@@ -666,8 +670,49 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     else
       reduce_sb(std::true_type());
     if (tid == 0)  // re-arm for the next call on this workspace
-      __hip_atomic_store(&counters[blockIdx.x], 0u, __ATOMIC_RELAXED,
+      __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
+  }
+  };
+
+  const int tiles = tiles_m * (N / BN);
+  if (!SPLIT || sk_steps == 0) {
+    // One tile per workgroup; split-K: K split `blockIdx.y` of gridDim.y.
+    const int64_t k_begin = SPLIT ? (int64_t)blockIdx.y * k_split : 0;
+    const int64_t k_len =
+        SPLIT ? (K - k_begin < k_split ? K - k_begin : k_split) : K;
+    tile_body((int)blockIdx.x, (int)gridDim.x, k_begin, k_len,
+              SPLIT ? (int)blockIdx.y : 0, SPLIT ? (int)gridDim.y : 1);
+    return;
+  }
+  if constexpr (SPLIT) {
+    // Stream-K: the (tile, K stage) pairs in tile order are cut into runs of
+    // sk_steps stages, one run per workgroup. The runs of one XCD's
+    // workgroups are consecutive (workgroups go to XCDs round-robin), so a
+    // tile's contributors mostly share an L2. A run covers the end of one
+    // tile, whole tiles, and the start of another; a tile covered by c runs
+    // gets partials 0 .. c-1 in K order, summed in that order by the last
+    // to arrive.
+    const int ksteps = (int)(K / KE);
+    const int nwg = (int)gridDim.x, w = (int)blockIdx.x;
+    const int run = nwg % 8 == 0 ? (w % 8) * (nwg / 8) + w / 8 : w;
+    const int64_t total = (int64_t)tiles * ksteps;
+    int64_t g = (int64_t)run * sk_steps;
+    const int64_t g_end = g + sk_steps < total ? g + sk_steps : total;
+    while (g < g_end) {
+      const int tile = (int)(g / ksteps);
+      const int64_t t0 = (int64_t)tile * ksteps;
+      const int a = (int)(g - t0);
+      const int b = g_end - t0 < ksteps ? (int)(g_end - t0) : ksteps;
+      const int c0 = (int)(t0 / sk_steps);
+      const int c1 = (int)((t0 + ksteps - 1) / sk_steps);
+      // tile order without the XCD remap (the runs already follow the XCDs)
+      tile_body(tile, 1, (int64_t)a * KE, (int64_t)(b - a) * KE, run - c0,
+                c1 - c0 + 1);
+      g = t0 + b;
+      if (g < g_end)
+        __syncthreads();  // the next tile's copies reuse the LDS ring
+    }
   }
 }
 
@@ -799,14 +844,16 @@ static hipError_t launch_fast(const MatmulArgs &a) {
   P *partials = SPLIT ? (P *)((char *)a.workspace +
                               split_counter_bytes(tiles))
                       : nullptr;
+  const bool stream_k = SPLIT && a.sk_steps > 0;
+  const dim3 grid = stream_k ? dim3((unsigned)a.sk_workgroups, 1, 1)
+                             : dim3(tiles, splits, (unsigned)a.batch);
   hipLaunchKernelGGL(
       (gemm_lds_kernel<T, OutT, BM, BN, BKB, WM, WN, STAGES, BMODE, SPLIT,
                        AT>),
-      dim3(tiles, splits, (unsigned)a.batch), dim3(64 * WM * WN), 0,
-      (hipStream_t)a.stream, (const T *)a.a, a.b, (OutT *)a.c,
-      (const f16 *)a.scale, (int)a.m, (int)a.n, (int)a.k, a.lda, a.ldb, a.ldc,
-      a.accumulate, k_split, partials, counters, a.sa, a.sb, a.sc, make_epi(a),
-      epi_batch_stride(a));
+      grid, dim3(64 * WM * WN), 0, (hipStream_t)a.stream, (const T *)a.a, a.b,
+      (OutT *)a.c, (const f16 *)a.scale, (int)a.m, (int)a.n, (int)a.k, a.lda,
+      a.ldb, a.ldc, a.accumulate, k_split, stream_k ? a.sk_steps : 0,
+      partials, counters, a.sa, a.sb, a.sc, make_epi(a), epi_batch_stride(a));
   return hipGetLastError();
 }
 

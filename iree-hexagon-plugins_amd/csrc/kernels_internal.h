@@ -34,6 +34,11 @@ struct MatmulArgs {
   int splits;
   int k_split;
   void *workspace;
+  // Stream-K (split configurations, batch 1): K stages per workgroup run and
+  // the workgroup count; `splits` is then the most runs any tile spans (the
+  // partial layers). 0 = one tile (split) per workgroup.
+  int sk_steps = 0;
+  int sk_workgroups = 0;
   // Batch (grid z): element strides between consecutive matrices of A, B, C
   // (0 = one matrix shared by every batch).
   int64_t batch = 1;

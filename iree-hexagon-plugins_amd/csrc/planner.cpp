@@ -137,8 +137,10 @@ bool fast_fits(const iree_mi355x_matmul_desc_t &d, const FastConfig &c) {
 // One ranked candidate: a configuration plus its K split.
 struct Candidate {
   int index = -1;
-  int splits = 1;
+  int splits = 1;       // stream-K: the most runs one tile spans
   int k_split = 0;
+  int sk_steps = 0;     // stream-K: K stages per workgroup run (0: off)
+  int64_t sk_wgs = 0;   // stream-K: workgroups
   int64_t tiles = 0;
   int64_t critical = 0;  // per-CU critical-path MACs
   int64_t traffic = 0;   // modeled global->LDS bytes (operands + partials)
@@ -164,8 +166,86 @@ constexpr double kStageNs = 500.0;      // per K stage of one workgroup
 // A split covers at least this many K stages, so its copy pipeline overlaps.
 constexpr int64_t kMinStagesPerSplit = 2;
 
+// Stream-K's forced split value: equal runs of (tile, K stage) pairs.
+constexpr int kStreamK = -1;
+
+// Stream-K: one workgroup per CU, each taking an equal run of the (tile, K
+// stage) pairs in tile order (at least kMinStagesPerSplit stages). Priced
+// like split-K: the busiest CU's MACs, the operand feed and HBM (plus the
+// partial tiles of tiles split across runs), one pipeline fill per tile a
+// run touches, and the last arriver's reduction of the most runs a tile
+// spans.
+bool evaluate_stream_k(const iree_mi355x_matmul_desc_t &d, const FastConfig &c,
+                       int index, int64_t cus, int64_t tiles, int64_t tiles_m,
+                       Candidate *out) {
+  const int64_t ks = d.k / c.bk;
+  const int64_t total = tiles * ks;
+  int64_t run = (total + cus - 1) / cus;
+  if (run < kMinStagesPerSplit)
+    run = kMinStagesPerSplit;
+  if (run >= ((int64_t)1 << 31) / 2)
+    return false;
+  const int64_t wgs = (total + run - 1) / run;
+  int layers = 1;
+  int64_t split_parts = 0;  // partial tiles published
+  for (int64_t t = 0; t < tiles; ++t) {
+    const int64_t c0 = t * ks / run, c1 = (t * ks + ks - 1) / run;
+    const int n = (int)(c1 - c0 + 1);
+    if (n > layers)
+      layers = n;
+    if (n > 1)
+      split_parts += n;
+  }
+  const int64_t segs = (run + ks - 1) / ks + 1;  // most tiles one run touches
+  const int64_t ab = elem_bytes(d.a_elem), bb = elem_bytes(d.b_elem);
+  Candidate r;
+  r.index = index;
+  r.splits = layers;
+  r.k_split = 0;
+  r.sk_steps = (int)run;
+  r.sk_wgs = wgs;
+  r.tiles = tiles;
+  r.critical = run * c.bm * c.bn * c.bk;
+  r.traffic = ab * (tiles_m * c.bm) * d.k * (d.n / c.bn) +
+              bb * d.n * d.k * tiles_m;
+  const int64_t partial_bytes = 2 * split_parts * c.bm * c.bn * 4;
+  r.traffic += partial_bytes;
+  r.workspace = layers > 1 ? (int64_t)split_counter_bytes(tiles) +
+                                 layers * d.m * d.n * 4
+                           : 0;
+  const double macs_per_ns =
+      d.a_elem == IREE_MI355X_ELEM_I8 ? kMacsPerCuNsI8 : kMacsPerCuNsF16;
+  double t = (double)r.critical / macs_per_ns;
+  const double t_feed = (double)r.traffic / kFeedBytesPerNs;
+  const double t_hbm =
+      (double)(ab * d.m * d.k + bb * d.n * d.k +
+               elem_bytes(d.c_elem) * d.m * d.n + partial_bytes) /
+      kHbmBytesPerNs;
+  const double t_chain = (double)run * kStageNs;
+  if (t_feed > t)
+    t = t_feed;
+  if (t_hbm > t)
+    t = t_hbm;
+  if (t_chain > t)
+    t = t_chain;
+  t += (double)segs * kRoundNs;
+  if (layers > 1) {
+    const int64_t rows = d.m < c.bm ? d.m : c.bm;
+    const int64_t per_thread = (rows * c.bn + c.threads - 1) / c.threads;
+    const int64_t loads = c.threads > 256 ? 32 : 64;
+    const int64_t sb = layers <= 2 ? 2 : layers <= 4 ? 4 : 8;
+    const int64_t g = loads / sb;
+    t += kSplitNs + (double)((per_thread + g - 1) / g) *
+                        (double)((layers + sb - 1) / sb) * kRoundTripNs;
+  }
+  r.est_ns = (int64_t)t;
+  *out = r;
+  return true;
+}
+
 // `explicit_config`: the caller named this configuration, so a split
 // configuration runs even where one split is all the shape needs.
+// `forced_splits` kStreamK asks for stream-K instead of a split count.
 bool evaluate(const iree_mi355x_matmul_desc_t &d, const FastConfig &c,
               int index, int64_t cus, Candidate *out,
               bool explicit_config = false, int forced_splits = 0) {
@@ -178,6 +258,11 @@ bool evaluate(const iree_mi355x_matmul_desc_t &d, const FastConfig &c,
     return false;  // one arrival counter per tile of every batch
   int splits = 1;
   int64_t k_split = d.k;
+  if (forced_splits == kStreamK) {
+    if (!c.split_k || batch != 1)
+      return false;
+    return evaluate_stream_k(d, c, index, cus, tiles, tiles_m, out);
+  }
   if (c.split_k) {
     // Enough workgroups to cover every CU; each split a multiple of BK.
     int64_t want = (cus + tiles * batch - 1) / (tiles * batch);
@@ -341,7 +426,7 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
         Candidate c;
         if (strcmp(cfgs[i].name, t.config) == 0 &&
             cfgs[i].lds_bytes <= budget &&
-            evaluate(*d, cfgs[i], i, cus, &c, t.splits > 0, t.splits)) {
+            evaluate(*d, cfgs[i], i, cus, &c, t.splits != 0, t.splits)) {
           best = c;
           plan->from_tuned_table = 1;
         }
@@ -353,7 +438,8 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
     // (more splits spread the work, fewer shorten the reduction).
     if (best.index < 0) {
       std::tuple<int64_t, int64_t, int64_t, int64_t> best_rank;
-      static const int kSplitChoices[] = {0, 2, 3, 4, 5, 6, 8, 10, 12, 16};
+      static const int kSplitChoices[] = {0,  2,  3,  4,  5, 6,
+                                          8, 10, 12, 16, kStreamK};
       for (int i = 0; i < count; ++i) {
         if (cfgs[i].lds_bytes > budget)
           continue;
@@ -381,10 +467,14 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
     plan->tile_n = c.bn;
     plan->tile_k = c.bk;
     plan->lds_bytes = c.lds_bytes;
-    plan->workgroups = best.tiles * best.splits * (d->batch > 0 ? d->batch : 1);
+    plan->workgroups =
+        best.sk_steps > 0
+            ? best.sk_wgs
+            : best.tiles * best.splits * (d->batch > 0 ? d->batch : 1);
     plan->threads = c.threads;
     plan->splits = best.splits;
     plan->k_split = best.k_split;
+    plan->stream_k_steps = best.sk_steps;
     plan->workspace_bytes = best.workspace;
     plan->traffic_bytes = best.traffic;
     return IREE_MI355X_OK;
@@ -492,7 +582,8 @@ int iree_mi355x_matmul_mfma_config_split(
       (d.has_scale && (!scale || (uintptr_t)scale % 2 != 0)))
     return fail(IREE_MI355X_INVALID_ARGUMENT, "mfma_config: bad arguments");
   Candidate cand;
-  if (splits < 0 || (splits > 1 && !cfg.split_k))
+  if (splits < kStreamK || ((splits > 1 || splits == kStreamK) &&
+                            !cfg.split_k))
     return fail(IREE_MI355X_INVALID_ARGUMENT,
                 "mfma_config %s: %d splits", cfg.name, splits);
   if (!evaluate(d, cfg, index, kDefaultCus, &cand, true, splits))
@@ -508,6 +599,8 @@ int iree_mi355x_matmul_mfma_config_split(
                   (flags & IREE_MI355X_MATMUL_ACCUMULATE) ? 1 : 0, stream,
                   scale, cand.splits, cand.k_split, ws};
   args.a_transposed = at ? 1 : 0;
+  args.sk_steps = cand.sk_steps;
+  args.sk_workgroups = (int)cand.sk_wgs;
   hipError_t e = cfg.launch(args);
   if (e != hipSuccess)
     return fail(IREE_MI355X_LAUNCH_FAILED, "%s: %s", cfg.name,

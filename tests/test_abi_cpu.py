@@ -162,6 +162,33 @@ def test_planner_split_k_for_skinny_shapes(pkg):
     assert p.splits == 1 and p.workspace_bytes == 0
 
 
+def test_planner_stream_k(pkg):
+    # 192 x 11008 on 128x128 tiles: 172 tiles for 256 CUs. Stream-K runs
+    # (equal runs of (tile, K stage) pairs) measured fastest here.
+    m, n, k = 192, 11008, 4096
+    p = pkg.plan(pkg.make_desc(F16, F16, F16, m, n, k, 0))
+    assert p.stream_k_steps > 0 and p.config_name.endswith(b"_sk")
+    ks = k // p.tile_k
+    tiles = -(-m // p.tile_m) * (n // p.tile_n)
+    run = p.stream_k_steps
+    assert p.workgroups == -(-tiles * ks // run) <= 256
+    layers = max((t * ks + ks - 1) // run - t * ks // run + 1
+                 for t in range(tiles))
+    assert p.splits == layers > 1
+    assert p.workspace_bytes == 65536 + layers * m * n * 4
+    lib = pkg.library()
+    assert lib.iree_mi355x_matmul_workspace_bytes(m, n, k, 0) >= \
+        p.workspace_bytes
+    # C5 W8A16 M=512 measured faster on whole 128x256 tiles than in runs
+    p = pkg.plan(pkg.make_desc(F16, I8, F16, 512, 11008, 4096, 0,
+                               has_scale=True))
+    assert p.stream_k_steps == 0
+    # batch > 1 never runs stream-K
+    d = pkg.make_desc(F16, F16, F16, m, n, k, 0)
+    d.batch = 2
+    assert pkg.plan(d).stream_k_steps == 0
+
+
 # Argument validation: every call below fails on the host, so no GPU is needed.
 FAKE = 0x10000  # 64 KiB aligned, never dereferenced
 

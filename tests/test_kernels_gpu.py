@@ -177,6 +177,45 @@ def test_split_k_skinny(pkg, oracle, dev, m, n, k, form):
         check_canary(buf, m, n, 5.0)
 
 
+@pytest.mark.parametrize("cfg_name,m,n,k,form", [
+    # C5 W8A16 M=512: 172 tiles of 64 K stages in runs of 43 (3 layers)
+    ("w8a16_nn_128x256x64_w2x4_s4_sk", 512, 11008, 4096, "w8"),
+    ("w8a16_nn_32x256x64_w1x4_s4_sk", 37, 2048, 2048, "w8"),  # ragged M
+    ("f16_nn_64x128x64_w2x2_s4_sk", 200, 384, 1088, "nn"),    # 17 stages
+    ("f16_nn_128x128x64_w2x2_s4_sk", 256, 4096, 4096, "nn"),
+    ("f16_tn_128x128x64_w2x2_s4_sk", 128, 1024, 8192, "tn"),  # 32 runs a tile
+    ("f16f32_nn_32x128x64_w1x4_s4_sk", 64, 1024, 1024, "f32"),
+    ("f16_nn_64x128x64_w2x2_s4_sk", 1024, 2048, 4096, "nn"),  # one run a tile
+])
+def test_stream_k(pkg, oracle, dev, cfg_name, m, n, k, form):
+    """Stream-K (each workgroup an equal run of the (tile, K stage) pairs;
+    a tile spanning several runs is summed in K order by the last to
+    arrive) against the oracle, two calls in a row (re-armed counters),
+    with nothing written outside the output view."""
+    cfg = next(c for c in pkg.mfma_configs() if c.name == cfg_name)
+    g = torch.Generator().manual_seed(m * 7 + n + k)
+    x = (torch.randn(m, k, generator=g) * 0.5).half()
+    scale = None
+    if form == "w8":
+        w = torch.randint(-128, 128, (k, n), generator=g).to(torch.int8)
+        scale = (torch.rand(n, generator=g) * 0.019 + 0.001).half()
+        ref = oracle.w8a16(x.numpy(), w.numpy(), scale.numpy())
+        scale = scale.to(dev)
+    else:
+        w = (torch.randn(n, k, generator=g) if form == "tn" else
+             torch.randn(k, n, generator=g)).half()
+        ref = oracle.matmul_f16(x.numpy(), w.numpy(), b_transposed=form == "tn",
+                                out_f32=form == "f32")
+    out_dtype = torch.float32 if form == "f32" else torch.float16
+    xd, wd = x.to(dev), w.to(dev)
+    for _ in range(2):
+        buf, y = canary_out((m, n), out_dtype, dev, 5.0)
+        pkg.matmul_mfma_config(cfg.index, xd, wd, y, scale=scale,
+                               splits=pkg.SPLITS_STREAM_K)
+        fp16_ok(oracle, y.cpu().numpy(), ref)
+        check_canary(buf, m, n, 5.0)
+
+
 def test_workspace_shared_across_kernels(pkg, oracle, dev):
     """GEMV and split-K GEMM calls of different shapes, interleaved on the
     library's one workspace: no call's partials may land on another call's
@@ -540,6 +579,27 @@ def test_batch_matmul_epilogue_paths(pkg, oracle, dev, z, m, n, k, bt, shared_b,
                                   activation=pkg._ACT_NAMES[act],
                                   multiplier=mul.numpy())
     fp16_ok(oracle, y.cpu().numpy(), ref)
+
+
+def test_stream_k_planned_with_epilogue(pkg, oracle, dev):
+    """A shape the planner gives to stream-K, through the batch_matmul entry
+    point (one batch) with bias, GELU and multiplier: the fused epilogue runs
+    in the direct stores of whole tiles and in the last arriver's reduction
+    of split ones."""
+    m, n, k = 192, 11008, 4096
+    assert pkg.plan(pkg.make_desc(0, 0, 0, m, n, k, 0)).stream_k_steps > 0
+    g = torch.Generator().manual_seed(192)
+    a = (torch.randn(1, m, k, generator=g) * 0.5).half()
+    b = (torch.randn(k, n, generator=g) * 0.05).half()
+    bias = torch.randn(n, generator=g).half()
+    mul = torch.randn(1, m, n, generator=g).half()
+    for _ in range(2):
+        y = pkg.batch_matmul(a.to(dev), b.to(dev), bias=bias.to(dev),
+                             activation="gelu_tanh", multiplier=mul.to(dev))
+        ref = oracle.batch_matmul_f16(a.numpy(), b.numpy(), bias=bias.numpy(),
+                                      activation=pkg._ACT_NAMES["gelu_tanh"],
+                                      multiplier=mul.numpy())
+        fp16_ok(oracle, y.cpu().numpy(), ref)
 
 
 def test_batch_matmul_accumulate_f32_and_strided_batches(pkg, oracle, dev):
