@@ -461,14 +461,18 @@ def only(pkg, inputs, dev, args):
 
 
 def tune_skinny(pkg, dev, args):
-    """Every eligible tile at every split count (1..16) on the skinny C3 /
-    C5 shapes, with rotating weights: the sweep the planner's skinny tuned
-    entries and its split enumeration were checked against."""
+    """Every eligible tile at every split count (1..16) and in stream-K runs
+    on the skinny C3 / C5 shapes and two tile counts stream-K is planned
+    for, with rotating weights: the sweep the planner's skinny tuned
+    entries, its split enumeration and its stream-K choice were checked
+    against."""
     import torch
     shapes = [("f16", 16, 4096, 4096), ("f16", 16, 11008, 4096),
               ("f16", 16, 4096, 11008), ("f16", 128, 4096, 4096),
               ("f16", 128, 11008, 4096), ("f16", 128, 4096, 11008),
-              ("w8a16", 512, 11008, 4096), ("w8a16", 128, 11008, 4096)]
+              ("w8a16", 512, 11008, 4096), ("w8a16", 128, 11008, 4096),
+              # tile counts stream-K is planned for
+              ("f16", 192, 11008, 4096), ("w8a16", 192, 11008, 11008)]
     cfgs = pkg.mfma_configs()
     for kind, m, n, k in shapes:
         g = torch.Generator().manual_seed(m + n + k)

@@ -49,6 +49,11 @@ const TunedEntry kTuned[] = {
      4096, 11008, 0, "f16_nn_32x128x64_w1x4_s4_sk", 8},
     {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_F16, 128,
      11008, 4096, 0, "w8a16_nn_32x256x64_w1x4_s4_sk", 1},
+    {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 128,
+     11008, 4096, 0, "f16_nn_64x128x64_w2x2_s4_sk", 1},
+    // Stream-K (splits -1) where it measured fastest.
+    {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_F16, 192,
+     11008, 11008, 0, "w8a16_nn_128x256x64_w2x4_s4_sk", -1},
     {0, 0, 0, 0, 0, 0, 0, nullptr, 0},  // sentinel
 };
 
@@ -438,8 +443,10 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
     // (more splits spread the work, fewer shorten the reduction).
     if (best.index < 0) {
       std::tuple<int64_t, int64_t, int64_t, int64_t> best_rank;
-      static const int kSplitChoices[] = {0,  2,  3,  4,  5, 6,
-                                          8, 10, 12, 16, kStreamK};
+      // Stream-K is not ranked: measured against the split counts it won
+      // only where K is long (the partial tiles it publishes cost more
+      // than the model prices); measured entries above select it.
+      static const int kSplitChoices[] = {0, 1, 2, 3, 4, 5, 6, 8, 10, 12, 16};
       for (int i = 0; i < count; ++i) {
         if (cfgs[i].lds_bytes > budget)
           continue;

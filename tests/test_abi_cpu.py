@@ -77,8 +77,9 @@ def test_planner_classification(pkg, case, family, tile):
     assert pkg.classify(d) == family
     p = pkg.plan(d)
     assert p.family == family
-    if tile is None:  # ragged M: a split-K configuration, tile by cost model
-        assert p.config_name.decode().endswith("_sk") and p.splits >= 2
+    if tile is None:  # ragged M: a split-K configuration (rows past M
+        # masked), tile and split count by cost model
+        assert p.config_name.decode().endswith("_sk") and p.splits >= 1
     else:
         assert (p.tile_m, p.tile_n) == tile
     name = p.config_name.decode()
@@ -163,11 +164,13 @@ def test_planner_split_k_for_skinny_shapes(pkg):
 
 
 def test_planner_stream_k(pkg):
-    # 192 x 11008 on 128x128 tiles: 172 tiles for 256 CUs. Stream-K runs
-    # (equal runs of (tile, K stage) pairs) measured fastest here.
-    m, n, k = 192, 11008, 4096
-    p = pkg.plan(pkg.make_desc(F16, F16, F16, m, n, k, 0))
-    assert p.stream_k_steps > 0 and p.config_name.endswith(b"_sk")
+    # W8A16 192 x 11008 x 11008 on 128x256 tiles: 86 tiles for 256 CUs.
+    # Stream-K runs (equal runs of (tile, K stage) pairs) measured fastest
+    # here; the measured entry selects them.
+    m, n, k = 192, 11008, 11008
+    p = pkg.plan(pkg.make_desc(F16, I8, F16, m, n, k, 0, has_scale=True))
+    assert p.stream_k_steps > 0 and p.from_tuned_table
+    assert p.config_name.endswith(b"_sk")
     ks = k // p.tile_k
     tiles = -(-m // p.tile_m) * (n // p.tile_n)
     run = p.stream_k_steps
@@ -176,15 +179,14 @@ def test_planner_stream_k(pkg):
                  for t in range(tiles))
     assert p.splits == layers > 1
     assert p.workspace_bytes == 65536 + layers * m * n * 4
-    lib = pkg.library()
-    assert lib.iree_mi355x_matmul_workspace_bytes(m, n, k, 0) >= \
-        p.workspace_bytes
-    # C5 W8A16 M=512 measured faster on whole 128x256 tiles than in runs
-    p = pkg.plan(pkg.make_desc(F16, I8, F16, 512, 11008, 4096, 0,
-                               has_scale=True))
-    assert p.stream_k_steps == 0
+    # Not ranked by the model (it won only where K is long): the C5 and C3
+    # skinny shapes keep their split counts.
+    for d in (pkg.make_desc(F16, I8, F16, 512, 11008, 4096, 0, has_scale=True),
+              pkg.make_desc(F16, F16, F16, 192, 11008, 4096, 0),
+              pkg.make_desc(F16, F16, F16, 16, 4096, 4096, 0)):
+        assert pkg.plan(d).stream_k_steps == 0
     # batch > 1 never runs stream-K
-    d = pkg.make_desc(F16, F16, F16, m, n, k, 0)
+    d = pkg.make_desc(F16, I8, F16, m, n, k, 0, has_scale=True)
     d.batch = 2
     assert pkg.plan(d).stream_k_steps == 0
 

@@ -146,7 +146,7 @@ def test_w8a16_mfma_configs(pkg, oracle, dev, shape):
 
 
 @pytest.mark.parametrize("m,n,k,form", [
-    (16, 4096, 4096, "nn"), (5, 512, 256, "nn"), (100, 512, 768, "nn"),
+    (16, 4096, 4096, "nn"), (5, 512, 1024, "nn"), (100, 512, 768, "nn"),
     (128, 4096, 4096, "nn"), (37, 1024, 1024, "tn"), (64, 4096, 4096, "tn"),
     (16, 11008, 4096, "w8"), (37, 1024, 2048, "w8")])
 def test_split_k_skinny(pkg, oracle, dev, m, n, k, form):
@@ -223,7 +223,7 @@ def test_workspace_shared_across_kernels(pkg, oracle, dev):
     counters of split-K tiles past the 64th)."""
     g = torch.Generator().manual_seed(11)
     cases = [(1, 11008, 2048), (64, 8448, 2048), (3, 4096, 1024),
-             (96, 8448, 1024), (1, 4096, 1024), (64, 11008, 2048),
+             (96, 8448, 2048), (1, 4096, 1024), (64, 11008, 2048),
              (2, 11008, 2048), (64, 8448, 2048)]
     for m, n, k in cases:
         p = pkg.plan(pkg.make_desc(0, 0, 0, m, n, k, 0))
@@ -581,25 +581,23 @@ def test_batch_matmul_epilogue_paths(pkg, oracle, dev, z, m, n, k, bt, shared_b,
     fp16_ok(oracle, y.cpu().numpy(), ref)
 
 
-def test_stream_k_planned_with_epilogue(pkg, oracle, dev):
-    """A shape the planner gives to stream-K, through the batch_matmul entry
-    point (one batch) with bias, GELU and multiplier: the fused epilogue runs
-    in the direct stores of whole tiles and in the last arriver's reduction
-    of split ones."""
-    m, n, k = 192, 11008, 4096
-    assert pkg.plan(pkg.make_desc(0, 0, 0, m, n, k, 0)).stream_k_steps > 0
+def test_stream_k_planned(pkg, oracle, dev):
+    """A shape the planner runs in stream-K (a measured entry), through the
+    quantized_matmul entry point, twice in a row (re-armed counters)."""
+    m, n, k = 192, 11008, 11008
+    assert pkg.plan(pkg.make_desc(0, 1, 0, m, n, k, 0,
+                                  has_scale=True)).stream_k_steps > 0
     g = torch.Generator().manual_seed(192)
-    a = (torch.randn(1, m, k, generator=g) * 0.5).half()
-    b = (torch.randn(k, n, generator=g) * 0.05).half()
-    bias = torch.randn(n, generator=g).half()
-    mul = torch.randn(1, m, n, generator=g).half()
+    x = (torch.randn(m, k, generator=g) * 0.5).half()
+    w = torch.randint(-128, 128, (k, n), generator=g).to(torch.int8)
+    s = (torch.rand(n, generator=g) * 0.019 + 0.001).half()
+    ref = oracle.w8a16(x.numpy(), w.numpy(), s.numpy())
+    xd, wd, sd = x.to(dev), w.to(dev), s.to(dev)
     for _ in range(2):
-        y = pkg.batch_matmul(a.to(dev), b.to(dev), bias=bias.to(dev),
-                             activation="gelu_tanh", multiplier=mul.to(dev))
-        ref = oracle.batch_matmul_f16(a.numpy(), b.numpy(), bias=bias.numpy(),
-                                      activation=pkg._ACT_NAMES["gelu_tanh"],
-                                      multiplier=mul.numpy())
+        buf, y = canary_out((m, n), torch.float16, dev, 5.0)
+        pkg.quantized_matmul(xd, wd, sd, y)
         fp16_ok(oracle, y.cpu().numpy(), ref)
+        check_canary(buf, m, n, 5.0)
 
 
 def test_batch_matmul_accumulate_f32_and_strided_batches(pkg, oracle, dev):
