@@ -173,7 +173,7 @@ int iree_mi355x_attention_f16(const void *q, const void *k, const void *v,
 // (CG/Conversion/HexagonRuntimeLinking.h:35-38). Passing workspace == NULL
 // makes the library use its own per-device workspace (allocated once, grown on
 // demand); a caller workspace must be zero-filled before its first use and is
-// left zero-filled in its counter region (its first 64 KiB) after every call,
+// left zero-filled in its counter region (its first 256 KiB) after every call,
 // so one workspace serves any sequence of calls of any shapes.
 size_t iree_mi355x_matmul_workspace_bytes(int64_t m, int64_t n, int64_t k,
                                           uint32_t flags);

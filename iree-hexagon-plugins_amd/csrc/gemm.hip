@@ -195,7 +195,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     if constexpr (SPLIT) {
       const int64_t zs = gridDim.y > 1 ? z : 0;
       partials += zs * (int64_t)gridDim.y * M * N;
-      counters += zs * gridDim.x;
+      counters += zs * gridDim.x * kCounterStride;
     }
   }
 
@@ -588,7 +588,8 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     __syncthreads();
     if (tid == 0) {
       const unsigned prev =
-          __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED,
+          __hip_atomic_fetch_add(&counters[tile * kCounterStride], 1u,
+                                 __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_AGENT);
       *last_split = prev == (unsigned)parts - 1;
     }
@@ -670,7 +671,8 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     else
       reduce_sb(std::true_type());
     if (tid == 0)  // re-arm for the next call on this workspace
-      __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED,
+      __hip_atomic_store(&counters[tile * kCounterStride], 0u,
+                         __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
   }
   };

@@ -95,7 +95,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemv_splitk_kernel(
     Y += z * sy;
     epi.mul += z * s_mul;  // s_mul is 0 without a multiplier
     partials += z * (int64_t)gridDim.y * MR * N;
-    counters += z * gridDim.x;
+    counters += z * gridDim.x * kCounterStride;
   }
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -229,7 +229,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemv_splitk_kernel(
   __syncthreads();
   if (tid == 0) {
     const unsigned prev = __hip_atomic_fetch_add(
-        &counters[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        &counters[blockIdx.x * kCounterStride], 1u, __ATOMIC_RELAXED,
+        __HIP_MEMORY_SCOPE_AGENT);
     last_flag = prev == (unsigned)(splits - 1);
   }
   __syncthreads();
@@ -251,7 +252,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemv_splitk_kernel(
   else
     last(std::true_type());
   if (tid == 0)  // re-arm for the next call on this workspace
-    __hip_atomic_store(&counters[blockIdx.x], 0u, __ATOMIC_RELAXED,
+    __hip_atomic_store(&counters[blockIdx.x * kCounterStride], 0u,
+                       __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 

@@ -74,10 +74,15 @@ inline int64_t epi_batch_stride(const MatmulArgs &a) {
 
 // Every workspace starts with one fixed counter region: one u32 arrival
 // counter per tile (split-K GEMM) or column block (GEMV), left at zero by
-// every call. Its size does not depend on the shape, so no call's partials
-// can overlap another call's counters on a shared workspace.
-constexpr size_t kWorkspaceCounterBytes = 64 * 1024;
-constexpr int64_t kMaxWorkspaceCounters = kWorkspaceCounterBytes / 4;
+// every call. Each counter has a 128-byte line of its own (kCounterStride
+// u32 apart): counters sharing a line serialized the arrivals of all their
+// workgroups (up to 2 us for the last of 256 GEMV workgroups). The region's
+// size does not depend on the shape, so no call's partials can overlap
+// another call's counters on a shared workspace.
+constexpr int kCounterStride = 32;
+constexpr size_t kWorkspaceCounterBytes = 256 * 1024;
+constexpr int64_t kMaxWorkspaceCounters =
+    kWorkspaceCounterBytes / (4 * kCounterStride);
 inline size_t split_counter_bytes(int64_t tiles) {
   (void)tiles;
   return kWorkspaceCounterBytes;

@@ -178,7 +178,7 @@ def test_planner_stream_k(pkg):
     layers = max((t * ks + ks - 1) // run - t * ks // run + 1
                  for t in range(tiles))
     assert p.splits == layers > 1
-    assert p.workspace_bytes == 65536 + layers * m * n * 4
+    assert p.workspace_bytes == 256 * 1024 + layers * m * n * 4
     # Not ranked by the model (it won only where K is long): the C5 and C3
     # skinny shapes keep their split counts.
     for d in (pkg.make_desc(F16, I8, F16, 512, 11008, 4096, 0, has_scale=True),
