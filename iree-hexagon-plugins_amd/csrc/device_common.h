@@ -84,6 +84,26 @@ __device__ __forceinline__ void global_to_lds_16(const void *gptr,
   __builtin_amdgcn_global_load_lds(gptr, lds_wave_base, 16, 0, 0);
 }
 
+// The same copy from a wave-uniform 64-bit base (SGPRs) plus a 32-bit
+// per-lane offset, with the LDS address in M0 set from an SGPR: the
+// global_load_lds saddr form. The address then costs no vector instruction;
+// the builtin above makes the compiler build a 64-bit per-lane address and
+// move the LDS address out of a VGPR (v_readfirstlane) for every copy.
+// Issued as asm, so it is not counted by the compiler's own waits: callers
+// wait with wait_vmcnt<N>().
+__device__ __forceinline__ void global_to_lds_16s(const char *sbase,
+                                                  uint32_t voff,
+                                                  IHP_LDS void *lds_wave_base) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)lds_wave_base;
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(voff), "s"(sbase), "s"(m0)
+      : "memory", "m0");
+}
+
 // s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] | vmcnt[5:4] << 14, other
 // counters left at their maximum so they are not waited on).
 template <int N>

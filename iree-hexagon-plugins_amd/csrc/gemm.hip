@@ -201,7 +201,8 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // Wave-uniform (SGPR): the copies' LDS addresses derive from it.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const int tiles_m = SPLIT ? (M + BM - 1) / BM : M / BM;
 
@@ -262,24 +263,24 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     const int64_t ka = (int64_t)kt * BKB;
     if (p < A_PASSES) {
       if constexpr (AT)
-        global_to_lds_16(a_base + (int64_t)kt * KE * lda_b + a_lane[p],
-                         dst + wave * A_RPW * AROW + p * A_RPP * AROW);
+        global_to_lds_16s(a_base + (int64_t)kt * KE * lda_b, a_lane[p],
+                          dst + wave * A_RPW * AROW + p * A_RPP * AROW);
       else
-        global_to_lds_16(a_base + ka + a_lane[p],
-                         dst + wave * ROWS_PER_WAVE * BKB +
-                             p * ROWS_PER_PASS * BKB);
+        global_to_lds_16s(a_base + ka, a_lane[p],
+                          dst + wave * ROWS_PER_WAVE * BKB +
+                              p * ROWS_PER_PASS * BKB);
     } else {
       const int q = p - A_PASSES;
       if constexpr (kNN) {
         const int64_t kb = (int64_t)kt * KE * ldb_b;
-        global_to_lds_16(b_base + kb + (int64_t)q * B_RPP * ldb_b + b_lane,
-                         dst + A_BYTES + wave * B_RPW * BROW +
-                             q * B_RPP * BROW);
+        global_to_lds_16s(b_base + kb + (int64_t)q * B_RPP * ldb_b, b_lane,
+                          dst + A_BYTES + wave * B_RPW * BROW +
+                              q * B_RPP * BROW);
       } else {
-        global_to_lds_16(b_base + ka + (int64_t)q * ROWS_PER_PASS * ldb_b +
-                             b_lane,
-                         dst + A_BYTES + wave * ROWS_PER_WAVE * BKB +
-                             q * ROWS_PER_PASS * BKB);
+        global_to_lds_16s(b_base + ka + (int64_t)q * ROWS_PER_PASS * ldb_b,
+                          b_lane,
+                          dst + A_BYTES + wave * ROWS_PER_WAVE * BKB +
+                              q * ROWS_PER_PASS * BKB);
       }
     }
   };
