@@ -543,8 +543,14 @@ def tune(pkg, inputs, dev, args):
             sc = s8 if cfg.b_form == pkg.B_FORM_W8A16 else None
             c = torch.empty(m, n, dtype=torch.float32 if cfg.c_elem == pkg.ELEM_F32
                             else torch.float16, device=dev)
-        ms = timed(lambda: pkg.matmul_mfma_config(cfg.index, a, b, c, scale=sc),
-                   args.steps, args.warmup)
+        try:
+            ms = timed(lambda: pkg.matmul_mfma_config(cfg.index, a, b, c,
+                                                      scale=sc),
+                       args.steps, args.warmup)
+        except pkg.MI355XError as ex:  # a skinny split-K tile: not 4096^3
+            print(json.dumps({"config": cfg.name, "skipped": str(ex)}),
+                  flush=True)
+            continue
         tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
         peak = PEAK_I8_TOPS if cfg.a_elem == pkg.ELEM_I8 else PEAK_F16_TFLOPS
         print(json.dumps({"config": cfg.name, "ms": round(ms, 4),

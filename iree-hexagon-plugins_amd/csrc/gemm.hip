@@ -430,13 +430,20 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
         acc[i][j][r] = 0;
 
   const int nk = (int)((k_len * (int64_t)sizeof(T)) / BKB);
-  // Prologue: fill every slot of the ring, wait for stage 0.
+  // Prologue: stages 0..STAGES-2 whole and the first half of stage
+  // STAGES-1 (its second half is issued during stage 0, as every later
+  // stage's is during the stage STAGES-1 before it), then wait for stage 0.
 #pragma unroll
-  for (int s = 0; s < STAGES; ++s)
-    if (s < nk)
-      load_passes(First(), All(), s, s);
+  for (int s = 0; s < STAGES; ++s) {
+    if (s < nk) {
+      if (s < STAGES - 1)
+        load_passes(First(), All(), s, s);
+      else
+        load_passes(First(), Half(), s, s);
+    }
+  }
   if (STAGES - 1 < nk)
-    wait_vmcnt<(STAGES - 1) * LOADS_PER_STAGE>();
+    wait_vmcnt<(STAGES - 2) * LOADS_PER_STAGE + Half::value>();
   else
     wait_vmcnt<0>();
   block_barrier();
@@ -444,38 +451,45 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   Frags fr[2];
   read_frags(0, 0, fr[0]);
 
-  // Per K step: issue the next step's fragment reads, wait only for this
-  // step's (issued one step earlier), then this step's MFMAs, which run
-  // while the new reads are in flight. The copies of stage kt+STAGES are
-  // issued in two halves, at the stage handoff and after the next stage's
-  // first K step, so the waves of a SIMD do not all stall on copy issue at
-  // once while their MFMAs wait (measured 3-4 % on the int8 4096^3 case).
-  for (int kt = 0; kt < nk; ++kt) {
+  // One stage. Per K step: issue the next step's fragment reads, wait only
+  // for this step's (issued one step earlier), then this step's MFMAs, which
+  // run while the new reads are in flight. The copies of stage kt+STAGES are
+  // issued in two halves, at the stage handoff (FIRST) and after the next
+  // stage's first K step (SECOND), so the waves of a SIMD do not all stall
+  // on copy issue at once while their MFMAs wait (measured 3-4 % on the
+  // int8 4096^3 case). The flags are compile-time constants, so each phase
+  // of the K loop below is free of branches: with them the loop-carried
+  // fragment registers had to be copied at every stage.
+  auto stage = [&](int kt, auto second, auto first, auto handoff,
+                   auto exact) __attribute__((always_inline)) {
     const int slot = kt % STAGES;
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
       const int cur = ks & 1, nxt = cur ^ 1;
       // Second half of stage kt-1+STAGES, into the slot stage kt-1 used:
       // every wave finished reading it before the previous handoff barrier.
-      if (ks == 1 && kt >= 1 && kt - 1 + STAGES < nk)
-        load_passes(Half(), All(), kt - 1 + STAGES, (kt - 1) % STAGES);
+      if constexpr (decltype(second)::value) {
+        if (ks == 1)
+          load_passes(Half(), All(), kt - 1 + STAGES,
+                      (kt - 1 + STAGES) % STAGES);
+      }
       if (ks + 1 < KSTEPS) {
         read_frags(slot, ks + 1, fr[nxt]);
         frags_ready(std::integral_constant<int, RD>(), fr[cur]);
-      } else if (kt + 1 < nk) {
+      } else if constexpr (decltype(handoff)::value) {
         // Stage handoff: this step's fragments are in registers (all LDS
         // reads done), stage kt+1 must have landed for every wave, and every
         // wave must be done reading stage kt before its slot is refilled
-        // with stage kt+STAGES. By now this wave has issued every copy up to
-        // stage kt+STAGES-1, so stage kt+1 has landed once at most
-        // STAGES-2 stages of copies remain in flight.
+        // with stage kt+STAGES. With EXACT this wave has issued every copy
+        // up to stage kt+STAGES-1, so stage kt+1 has landed once at most
+        // STAGES-2 stages of copies remain in flight; otherwise wait for all.
         frags_ready(std::integral_constant<int, 0>(), fr[cur]);
-        if (kt + STAGES - 1 < nk)
+        if constexpr (decltype(exact)::value)
           wait_vmcnt<(STAGES - 2) * LOADS_PER_STAGE>();
         else
           wait_vmcnt<0>();
         block_barrier();
-        if (kt + STAGES < nk)
+        if constexpr (decltype(first)::value)
           load_passes(First(), Half(), kt + STAGES, slot);
         read_frags((kt + 1) % STAGES, 0, fr[nxt]);
       } else {
@@ -487,7 +501,23 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
         for (int j = 0; j < FN; ++j)
           acc[i][j] = MF::mma(fr[cur].a[i], fr[cur].b[j], acc[i][j]);
     }
+  };
+  using Yes = std::true_type;
+  using No = std::false_type;
+  // Phases: both halves of a later stage to issue (kt < nk-STAGES); the
+  // second half of the last stage only (kt == nk-STAGES); no copies; the
+  // last stage, without a handoff.
+  int kt = 0;
+  for (; kt < nk - STAGES; ++kt)
+    stage(kt, Yes(), Yes(), Yes(), Yes());
+  if (kt == nk - STAGES) {
+    stage(kt, Yes(), No(), Yes(), Yes());
+    ++kt;
   }
+  for (; kt < nk - 1; ++kt)
+    stage(kt, No(), No(), Yes(), No());
+  if (kt < nk)
+    stage(kt, No(), No(), No(), No());
 
   // Epilogue: C_out = [C_init +] acc (W8A16: acc * scale[n]), one rounding
   // for f16 outputs.
