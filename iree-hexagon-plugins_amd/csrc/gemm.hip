@@ -291,7 +291,6 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     });
   };
   using First = std::integral_constant<int, 0>;
-  using Half = std::integral_constant<int, LOADS_PER_STAGE / 2>;
   using All = std::integral_constant<int, LOADS_PER_STAGE>;
 
   // Read side, A (and TN B): lane reads row (lane % 32) of each 32-row
@@ -430,20 +429,13 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
         acc[i][j][r] = 0;
 
   const int nk = (int)((k_len * (int64_t)sizeof(T)) / BKB);
-  // Prologue: stages 0..STAGES-2 whole and the first half of stage
-  // STAGES-1 (its second half is issued during stage 0, as every later
-  // stage's is during the stage STAGES-1 before it), then wait for stage 0.
+  // Prologue: fill every slot of the ring, wait for stage 0.
 #pragma unroll
-  for (int s = 0; s < STAGES; ++s) {
-    if (s < nk) {
-      if (s < STAGES - 1)
-        load_passes(First(), All(), s, s);
-      else
-        load_passes(First(), Half(), s, s);
-    }
-  }
+  for (int s = 0; s < STAGES; ++s)
+    if (s < nk)
+      load_passes(First(), All(), s, s);
   if (STAGES - 1 < nk)
-    wait_vmcnt<(STAGES - 2) * LOADS_PER_STAGE + Half::value>();
+    wait_vmcnt<(STAGES - 1) * LOADS_PER_STAGE>();
   else
     wait_vmcnt<0>();
   block_barrier();
@@ -454,25 +446,17 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   // One stage. Per K step: issue the next step's fragment reads, wait only
   // for this step's (issued one step earlier), then this step's MFMAs, which
   // run while the new reads are in flight. The copies of stage kt+STAGES are
-  // issued in two halves, at the stage handoff (FIRST) and after the next
-  // stage's first K step (SECOND), so the waves of a SIMD do not all stall
-  // on copy issue at once while their MFMAs wait (measured 3-4 % on the
-  // int8 4096^3 case). The flags are compile-time constants, so each phase
-  // of the K loop below is free of branches: with them the loop-carried
-  // fragment registers had to be copied at every stage.
-  auto stage = [&](int kt, auto second, auto first, auto handoff,
-                   auto exact) __attribute__((always_inline)) {
+  // issued whole at the handoff (COPY): their addresses cost no vector
+  // instructions, and issuing them in two halves, the second after the next
+  // stage's first K step, measured ~1 % slower. The flags are compile-time
+  // constants, so each phase of the K loop below is free of branches: with
+  // them the loop-carried fragment registers had to be copied at every stage.
+  auto stage = [&](int kt, auto copy, auto handoff, auto exact)
+      __attribute__((always_inline)) {
     const int slot = kt % STAGES;
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
       const int cur = ks & 1, nxt = cur ^ 1;
-      // Second half of stage kt-1+STAGES, into the slot stage kt-1 used:
-      // every wave finished reading it before the previous handoff barrier.
-      if constexpr (decltype(second)::value) {
-        if (ks == 1)
-          load_passes(Half(), All(), kt - 1 + STAGES,
-                      (kt - 1 + STAGES) % STAGES);
-      }
       if (ks + 1 < KSTEPS) {
         read_frags(slot, ks + 1, fr[nxt]);
         frags_ready(std::integral_constant<int, RD>(), fr[cur]);
@@ -489,8 +473,8 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
         else
           wait_vmcnt<0>();
         block_barrier();
-        if constexpr (decltype(first)::value)
-          load_passes(First(), Half(), kt + STAGES, slot);
+        if constexpr (decltype(copy)::value)
+          load_passes(First(), All(), kt + STAGES, slot);
         read_frags((kt + 1) % STAGES, 0, fr[nxt]);
       } else {
         frags_ready(std::integral_constant<int, 0>(), fr[cur]);
@@ -504,20 +488,20 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   };
   using Yes = std::true_type;
   using No = std::false_type;
-  // Phases: both halves of a later stage to issue (kt < nk-STAGES); the
-  // second half of the last stage only (kt == nk-STAGES); no copies; the
-  // last stage, without a handoff.
+  // Phases: a later stage to copy (kt < nk-STAGES); the first stage with
+  // every copy issued (kt == nk-STAGES, still an exact wait); the rest with
+  // a handoff; the last stage, without one.
   int kt = 0;
   for (; kt < nk - STAGES; ++kt)
-    stage(kt, Yes(), Yes(), Yes(), Yes());
+    stage(kt, Yes(), Yes(), Yes());
   if (kt == nk - STAGES) {
-    stage(kt, Yes(), No(), Yes(), Yes());
+    stage(kt, No(), Yes(), Yes());
     ++kt;
   }
   for (; kt < nk - 1; ++kt)
-    stage(kt, No(), No(), Yes(), No());
+    stage(kt, No(), Yes(), No());
   if (kt < nk)
-    stage(kt, No(), No(), No(), No());
+    stage(kt, No(), No(), No());
 
   // Epilogue: C_out = [C_init +] acc (W8A16: acc * scale[n]), one rounding
   // for f16 outputs.
