@@ -124,7 +124,7 @@ template <typename T, typename OutT, int BM, int BN, int BKB, int WM, int WN,
 __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     const T *__restrict__ A, const void *__restrict__ Bv, OutT *__restrict__ C,
     const f16 *__restrict__ scale, int M, int N, int K, int64_t lda,
-    int64_t ldb, int64_t ldc, int accumulate, int k_split, int sk_steps,
+    int64_t ldb, int64_t ldc, int store_mode, int k_split, int sk_steps,
     typename Mfma32<T>::AccScalar *__restrict__ partials,
     unsigned *__restrict__ counters, int64_t sa, int64_t sb, int64_t sc,
     Epi epi, int64_t s_mul) {
@@ -539,7 +539,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
           if constexpr (BMODE == kBW8)
             v *= (float)scale[col];
           store_out(C + row * ldc + col, epi_apply(v, row, col, epi),
-                    accumulate);
+                    store_mode);
         }
       }
       return;
@@ -548,6 +548,23 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   // One split (a ragged-M shape whose tiles alone cover the CUs): store
   // directly, rows past M masked, no partials.
   if (!SPLIT || parts == 1) {
+    if constexpr (kIntOut && !SPLIT) {
+      // Large i32 outputs: written through past the L2, tested once here.
+      if (store_mode == kStoreThrough) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          OutT *crow = C + (m0 + wm * WTM + i * 32 + row_l) * ldc + n0 +
+                       wn * WTN + col_l;
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              store_through(crow + (8 * (r >> 2) + (r & 3)) * ldc + j * 32,
+                            acc[i][j][r]);
+        }
+        return;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       OutT *crow = C + (m0 + wm * WTM + i * 32 + row_l) * ldc + n0 +
@@ -565,12 +582,12 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
           if (SPLIT && row >= M)
             continue;
           if constexpr (kIntOut) {
-            store_out(dst, acc[i][j][r], accumulate);
+            store_out(dst, acc[i][j][r], store_mode);
           } else {
             float v = (float)acc[i][j][r];
             if constexpr (BMODE == kBW8)
               v *= sc;
-            store_out(dst, v, accumulate);
+            store_out(dst, v, store_mode);
           }
         }
       }
@@ -661,14 +678,14 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
             continue;
           const int64_t row = m0 + idx / BN, col = n0 + idx % BN;
           if constexpr (kIntOut) {
-            store_out(C + row * ldc + col, sum[e], accumulate);
+            store_out(C + row * ldc + col, sum[e], store_mode);
           } else {
             float v = (float)sum[e];
             if constexpr (BMODE == kBW8)
               v *= (float)scale[col];
             if constexpr (decltype(with_epi)::value)
               v = epi_apply(v, row, col, epi);
-            store_out(C + row * ldc + col, v, accumulate);
+            store_out(C + row * ldc + col, v, store_mode);
           }
         }
       }
@@ -864,12 +881,18 @@ static hipError_t launch_fast(const MatmulArgs &a) {
   const bool stream_k = SPLIT && a.sk_steps > 0;
   const dim3 grid = stream_k ? dim3((unsigned)a.sk_workgroups, 1, 1)
                              : dim3(tiles, splits, (unsigned)a.batch);
+  const int store_mode =
+      a.accumulate ? kStoreAccumulate
+      : !SPLIT && std::is_same<OutT, int32_t>::value &&
+              a.m * a.n * a.batch * (int64_t)sizeof(OutT) >= kStoreThroughBytes
+          ? kStoreThrough
+          : kStorePlain;
   hipLaunchKernelGGL(
       (gemm_lds_kernel<T, OutT, BM, BN, BKB, WM, WN, STAGES, BMODE, SPLIT,
                        AT>),
       grid, dim3(64 * WM * WN), 0, (hipStream_t)a.stream, (const T *)a.a, a.b,
       (OutT *)a.c, (const f16 *)a.scale, (int)a.m, (int)a.n, (int)a.k, a.lda,
-      a.ldb, a.ldc, a.accumulate, k_split, stream_k ? a.sk_steps : 0,
+      a.ldb, a.ldc, store_mode, k_split, stream_k ? a.sk_steps : 0,
       partials, counters, a.sa, a.sb, a.sc, make_epi(a), epi_batch_stride(a));
   return hipGetLastError();
 }

@@ -231,6 +231,26 @@ __device__ __forceinline__ bool epi_plain(const Epi &e) {
   return !e.bias && !e.mul && e.act == kActNone;
 }
 
+// Output store modes (the MFMA kernel's `store_mode` argument): plain store,
+// C += result, or (i32 outputs of unsplit tiles only) a store written through
+// past this XCD's L2 (sc1). The kernel does not read its output again, and
+// written through it leaves no dirty lines for the L2 write-back at the end
+// of the kernel: measured 0.7-2.5 % on the int8 4096^3 matmul, whose 64 MiB
+// i32 output otherwise sat dirty in the L2s. The launcher chooses it for i32
+// outputs of at least kStoreThroughBytes; the kernel tests it once, outside
+// its store loop (a per-element three-way test slowed the f16 kernels ~5 %).
+constexpr int kStorePlain = 0;
+constexpr int kStoreAccumulate = 1;
+constexpr int kStoreThrough = 2;
+constexpr int64_t kStoreThroughBytes = 8 << 20;
+
+// Issued as asm: no wait follows a store.
+__device__ __forceinline__ void store_through(int32_t *p, int32_t v) {
+  asm volatile("global_store_dword %0, %1, off sc1" ::"v"(p), "v"(v)
+               : "memory");
+}
+
+// Plain or accumulating store (`acc`: kStorePlain or kStoreAccumulate).
 __device__ __forceinline__ void store_out(float *p, float v, int acc) {
   *p = acc ? *p + v : v;
 }
