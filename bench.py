@@ -88,19 +88,23 @@ def timed(fn, steps, warmup):
     5-microsecond GEMV would measure the Python launch path, not the kernel.
     """
     import torch
-    for _ in range(warmup):
-        fn()
+    stream = capture_stream()
+    # Warm up on the stream the graph is captured on: the library keeps one
+    # workspace per stream and never allocates under capture.
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            fn()
     torch.cuda.synchronize()
     if not USE_GRAPH:
         start = torch.cuda.Event(enable_timing=True)
         stop = torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(steps):
-            fn()
-        stop.record()
+        with torch.cuda.stream(stream):
+            start.record(stream)
+            for _ in range(steps):
+                fn()
+            stop.record(stream)
         torch.cuda.synchronize()
         return start.elapsed_time(stop) / steps
-    stream = torch.cuda.Stream()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
         for _ in range(steps):
@@ -119,6 +123,18 @@ def timed(fn, steps, warmup):
         stop.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / steps
+
+
+_CAPTURE_STREAM = None
+
+
+def capture_stream():
+    """The one side stream every timed workload runs and is captured on."""
+    import torch
+    global _CAPTURE_STREAM
+    if _CAPTURE_STREAM is None:
+        _CAPTURE_STREAM = torch.cuda.Stream()
+    return _CAPTURE_STREAM
 
 
 def rotating(make, count):

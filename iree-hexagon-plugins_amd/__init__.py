@@ -435,14 +435,36 @@ def _unit_col(t) -> bool:
 
 
 def _require(t, dtype, name, dims=(2,)):
+    """Type, rank and layout of one operand (the device is checked last, by
+    _on_device, so that every shape error is reported first)."""
     import torch
-    if not isinstance(t, torch.Tensor) or not t.is_cuda:
-        raise TypeError(f"{name} must be a device tensor")
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
     if t.dtype != dtype:
         raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
     if t.dim() not in dims or not _unit_col(t):
         raise ValueError(f"{name} must be {'/'.join(map(str, dims))}-D with "
                          "unit column stride")
+
+
+def _shape(t, expected, name):
+    if tuple(t.shape) != tuple(expected):
+        raise ValueError(f"{name} must be {list(expected)}, got {list(t.shape)}")
+
+
+def _on_device(*named):
+    """Every operand is a device tensor on the same GPU: the C-ABI sees only
+    pointers, and a host or foreign-device pointer would fault the kernel."""
+    device = None
+    for t, name in named:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise TypeError(f"{name} must be a device tensor")
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise ValueError(f"{name} is on {t.device}, expected {device}")
 
 
 def matmul(a, b, c=None, *, b_transposed=False, accumulate=False,
@@ -452,18 +474,23 @@ def matmul(a, b, c=None, *, b_transposed=False, accumulate=False,
     f16 inputs accumulate in f32 and write f16 (or f32 with
     out_dtype=torch.float32); int8 inputs accumulate exactly into int32.
     ``b_transposed``: B is stored [N, K]. ``a_transposed`` (f16 only): A is
-    stored [K, M].
+    stored [K, M]. ``c`` (required with ``accumulate``) must be [M, N].
     """
     import torch
-    lib = library()
     if a.dtype == torch.int8:
+        if a_transposed:
+            raise ValueError("a_transposed is an f16 layout")
         _require(a, torch.int8, "a")
         _require(b, torch.int8, "b")
+        if out_dtype not in (None, torch.int32):
+            raise TypeError("int8 matmul writes int32")
         out_dtype = torch.int32
     else:
         _require(a, torch.float16, "a")
         _require(b, torch.float16, "b")
         out_dtype = out_dtype or torch.float16
+        if out_dtype not in (torch.float16, torch.float32):
+            raise TypeError("f16 matmul writes float16 or float32")
     k, m = a.shape if a_transposed else a.shape[::-1]
     n = b.shape[0] if b_transposed else b.shape[1]
     if (b.shape[1] if b_transposed else b.shape[0]) != k:
@@ -471,9 +498,13 @@ def matmul(a, b, c=None, *, b_transposed=False, accumulate=False,
     if c is None:
         if accumulate:
             raise ValueError("accumulate needs an init tensor c")
-        c = torch.empty((m, n), dtype=out_dtype, device=a.device)
     else:
         _require(c, out_dtype, "c")
+        _shape(c, (m, n), "c")
+    _on_device((a, "a"), (b, "b"), (c, "c"))
+    lib = library()
+    if c is None:
+        c = torch.empty((m, n), dtype=out_dtype, device=a.device)
     flags = ((B_TRANSPOSED if b_transposed else 0) |
              (ACCUMULATE if accumulate else 0) |
              (A_TRANSPOSED if a_transposed else 0))
@@ -494,7 +525,14 @@ def matmul(a, b, c=None, *, b_transposed=False, accumulate=False,
 
 def _epilogue(bias, activation, multiplier, m, n, batch):
     import torch
-    act = _ACT_NAMES[activation] if not isinstance(activation, int) else activation
+    if isinstance(activation, int):
+        if activation not in _ACT_NAMES.values():
+            raise ValueError(f"unknown activation {activation}")
+        act = activation
+    else:
+        if activation not in _ACT_NAMES:
+            raise ValueError(f"unknown activation {activation!r}")
+        act = _ACT_NAMES[activation]
     if bias is None and multiplier is None and act == ACT_NONE:
         return None
     e = Epilogue()
@@ -506,14 +544,15 @@ def _epilogue(bias, activation, multiplier, m, n, batch):
         e.bias = bias.data_ptr()
     if multiplier is not None:
         _require(multiplier, torch.float16, "multiplier", (2, 3))
-        if multiplier.shape[-2:] != (m, n) or not _unit_col(multiplier):
-            raise ValueError("multiplier must be [.., M, N] with unit column stride")
+        if tuple(multiplier.shape[-2:]) != (m, n):
+            raise ValueError(f"multiplier must be [.., {m}, {n}]")
+        if multiplier.dim() == 3 and multiplier.shape[0] != batch:
+            raise ValueError("multiplier batch differs")
         e.multiplier = multiplier.data_ptr()
         e.ld_multiplier = multiplier.stride(-2)
         e.batch_stride_multiplier = (multiplier.stride(0)
-                                     if multiplier.dim() == 3 else 0)
-        if multiplier.dim() == 3 and multiplier.shape[0] != batch:
-            raise ValueError("multiplier batch differs")
+                                     if multiplier.dim() == 3 and batch > 1
+                                     else 0)
     return e
 
 
@@ -527,41 +566,48 @@ def batch_matmul(a, b, c=None, *, b_transposed=False, accumulate=False,
     ``a_transposed``); b: [Z, K, N] / [Z, N, K] with ``b_transposed`` (or
     2-D, shared by the batch); bias [N]; multiplier
     [Z, M, N] or [M, N]; activation None / "relu" / "gelu_tanh" / "silu".
+    c is [Z, M, N] when either operand is 3-D, else [M, N].
     Every matrix needs a unit column stride; batch strides may be 0.
     """
     import torch
-    lib = library()
     _require(a, torch.float16, "a", (2, 3))
     _require(b, torch.float16, "b", (2, 3))
     out_dtype = out_dtype or torch.float16
+    if out_dtype not in (torch.float16, torch.float32):
+        raise TypeError("batch_matmul writes float16 or float32")
     a3 = a if a.dim() == 3 else a.unsqueeze(0)
     b3 = b if b.dim() == 3 else b.unsqueeze(0)
+    batched = a.dim() == 3 or b.dim() == 3
     batch = max(a3.shape[0], b3.shape[0])
-    if a.dim() == 2 and b.dim() == 2:
-        batch = 1
     k, m = (a3.shape[1], a3.shape[2]) if a_transposed else (a3.shape[2], a3.shape[1])
     n = b3.shape[1] if b_transposed else b3.shape[2]
     if (b3.shape[2] if b_transposed else b3.shape[1]) != k:
         raise ValueError("contraction extents differ")
     for t, name in ((a3, "a"), (b3, "b")):
-        if t.shape[0] not in (1, batch) or not _unit_col(t):
-            raise ValueError(f"{name}: batch extent or column stride unsupported")
-    sa = 0 if a.dim() == 2 or a3.shape[0] == 1 else a3.stride(0)
-    sb = 0 if b.dim() == 2 or b3.shape[0] == 1 else b3.stride(0)
+        if t.shape[0] not in (1, batch):
+            raise ValueError(f"{name}: batch extent {t.shape[0]} is neither 1 "
+                             f"nor {batch}")
+    sa = 0 if a3.shape[0] == 1 else a3.stride(0)
+    sb = 0 if b3.shape[0] == 1 else b3.stride(0)
+    out_shape = (batch, m, n) if batched else (m, n)
     if c is None:
         if accumulate:
             raise ValueError("accumulate needs an init tensor c")
-        c = torch.empty((batch, m, n) if (a.dim() == 3 or b.dim() == 3) else (m, n),
-                        dtype=out_dtype, device=a.device)
     else:
-        _require(c, out_dtype, "c", (2, 3))
+        _require(c, out_dtype, "c", (3,) if batched else (2,))
+        _shape(c, out_shape, "c")
+    e = _epilogue(bias, activation, multiplier, m, n, batch)
+    _on_device((a, "a"), (b, "b"), (c, "c"), (bias, "bias"),
+               (multiplier, "multiplier"))
+    lib = library()
+    if c is None:
+        c = torch.empty(out_shape, dtype=out_dtype, device=a.device)
     c3 = c if c.dim() == 3 else c.unsqueeze(0)
     sc = c3.stride(0) if batch > 1 else m * n
     flags = ((B_TRANSPOSED if b_transposed else 0) |
              (ACCUMULATE if accumulate else 0) |
              (OUT_F32 if out_dtype == torch.float32 else 0) |
              (A_TRANSPOSED if a_transposed else 0))
-    e = _epilogue(bias, activation, multiplier, m, n, batch)
     _check(lib.iree_mi355x_batch_matmul_f16(
         a3.data_ptr(), b3.data_ptr(), c3.data_ptr(), batch, m, n, k,
         a3.stride(1), b3.stride(1), c3.stride(1), sa, sb, sc, flags,
@@ -580,15 +626,24 @@ def linear(x, w, bias=None, *, activation=None, multiplier=None,
 
 
 def quantized_matmul(x, w, scale, y=None, *, w_transposed=False, stream=None):
-    """W8A16 linear: y = f16((x . w_int8) * scale[n]), zero point 0."""
+    """W8A16 linear: y = f16((x . w_int8) * scale[n]), zero point 0.
+    x [M, K] f16, w [K, N] int8 (or [N, K] with ``w_transposed``), scale [N]
+    f16, y [M, N] f16."""
     import torch
-    lib = library()
     _require(x, torch.float16, "x")
     _require(w, torch.int8, "w")
     m, k = x.shape
     n = w.shape[0] if w_transposed else w.shape[1]
-    if scale.dtype != torch.float16 or scale.numel() != n or not scale.is_contiguous():
+    if (w.shape[1] if w_transposed else w.shape[0]) != k:
+        raise ValueError("w does not contract over K")
+    _require(scale, torch.float16, "scale", (1,))
+    if scale.numel() != n or not scale.is_contiguous():
         raise ValueError("scale must be a contiguous f16 vector of N")
+    if y is not None:
+        _require(y, torch.float16, "y")
+        _shape(y, (m, n), "y")
+    _on_device((x, "x"), (w, "w"), (scale, "scale"), (y, "y"))
+    lib = library()
     if y is None:
         y = torch.empty((m, n), dtype=torch.float16, device=x.device)
     _check(lib.iree_mi355x_w8a16_matmul(
@@ -599,14 +654,23 @@ def quantized_matmul(x, w, scale, y=None, *, w_transposed=False, stream=None):
 
 
 def attention(q, k, v, o=None, *, causal=True, scale=None, stream=None):
-    """Fused attention forward on [B, H, S, D] f16 tensors (contiguous)."""
+    """Fused attention forward on contiguous f16 tensors: q, o [B, H, Sq, D];
+    k, v [B, H, Skv, D]."""
     import torch
-    lib = library()
-    for t, nm in ((q, "q"), (k, "k"), (v, "v")):
-        if t.dtype != torch.float16 or not t.is_cuda or not t.is_contiguous() or t.dim() != 4:
-            raise TypeError(f"{nm} must be a contiguous [B,H,S,D] f16 device tensor")
+    for t, nm in ((q, "q"), (k, "k"), (v, "v"), (o, "o")):
+        if t is None:
+            continue
+        if (not isinstance(t, torch.Tensor) or t.dtype != torch.float16
+                or not t.is_contiguous() or t.dim() != 4):
+            raise TypeError(f"{nm} must be a contiguous 4-D f16 tensor")
     b, h, sq, d = q.shape
     skv = k.shape[2]
+    _shape(k, (b, h, skv, d), "k")
+    _shape(v, (b, h, skv, d), "v")
+    if o is not None:
+        _shape(o, (b, h, sq, d), "o")
+    _on_device((q, "q"), (k, "k"), (v, "v"), (o, "o"))
+    lib = library()
     if scale is None:
         scale = d ** -0.5
     if o is None:
@@ -627,6 +691,13 @@ def matmul_mfma_config(index, a, b, c, *, scale=None, splits=0, stream=None):
     stream-K runs)."""
     import torch
     cfg = mfma_configs()[index]
+    a_dtype = torch.int8 if cfg.a_elem == ELEM_I8 else torch.float16
+    b_dtype = torch.int8 if cfg.b_form == B_FORM_W8A16 else a_dtype
+    c_dtype = {ELEM_I32: torch.int32, ELEM_F32: torch.float32}.get(
+        cfg.c_elem, torch.float16)
+    _require(a, a_dtype, "a")
+    _require(b, b_dtype, "b")
+    _require(c, c_dtype, "c")
     k, m = a.shape if cfg.a_transposed else a.shape[::-1]
     if cfg.b_form == B_FORM_TN:
         n, flags = b.shape[0], B_TRANSPOSED
@@ -638,8 +709,14 @@ def matmul_mfma_config(index, a, b, c, *, scale=None, splits=0, stream=None):
     # tensors' own, or the kernel would stream past a buffer.
     if (b.shape[1] if cfg.b_form == B_FORM_TN else b.shape[0]) != k:
         raise ValueError(f"{cfg.name}: b does not contract over K = {k}")
-    if tuple(c.shape) != (m, n):
-        raise ValueError(f"{cfg.name}: c must be [{m}, {n}]")
+    _shape(c, (m, n), "c")
+    if cfg.b_form == B_FORM_W8A16:
+        if scale is None:
+            raise ValueError(f"{cfg.name}: needs a scale")
+        _require(scale, torch.float16, "scale", (1,))
+        if scale.numel() != n or not scale.is_contiguous():
+            raise ValueError("scale must be a contiguous f16 vector of N")
+    _on_device((a, "a"), (b, "b"), (c, "c"), (scale, "scale"))
     if c.dtype == torch.float32 and a.dtype == torch.float16:
         flags |= OUT_F32
     _check(library().iree_mi355x_matmul_mfma_config_split(

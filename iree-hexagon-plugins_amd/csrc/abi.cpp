@@ -8,6 +8,8 @@
 // launch and reports an iree_mi355x_status_t; nothing is launched on error.
 #include <hip/hip_runtime.h>
 
+#include <dlfcn.h>
+
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -56,43 +58,95 @@ static bool aligned(const void *p, size_t a) {
 
 static const int64_t kMaxExtent = (int64_t)1 << 31;
 
-// Library-owned workspace, one per device, zero-filled when (re)allocated.
-// Calls that share it must be ordered (same stream or synchronized).
-struct DeviceWorkspace {
-  void *ptr = nullptr;
-  size_t bytes = 0;
+// The library's own workspace, for calls made with workspace == NULL: one
+// buffer per (device, stream), so calls on different streams never share
+// arrival counters or partials. A buffer is allocated outside stream capture
+// only, its counter region zero-filled in stream order; it grows
+// geometrically and is never freed: a graph captured earlier, or a launch
+// another thread is still queueing, may hold a smaller one, and freeing it
+// would turn that launch into a use of freed memory. Streams are told apart
+// by hipStreamGetId (where the runtime has it) as well as their handle, so a
+// new stream that reuses a destroyed one's handle gets a buffer of its own.
+struct StreamWorkspace {
+  int device;
+  uintptr_t handle;
+  unsigned long long id;
+  void *ptr;
+  size_t bytes;
 };
 static std::mutex g_ws_mutex;
-static std::vector<DeviceWorkspace> g_ws;
+static std::vector<StreamWorkspace> g_ws;
 
-int library_workspace(size_t need, void **out) {
+// hipStreamGetId, looked up at run time: the HIP runtime this process runs
+// on (torch's, when loaded from Python) may predate it, and then streams are
+// told apart by their handle alone.
+typedef hipError_t (*StreamIdFn)(hipStream_t, unsigned long long *);
+static StreamIdFn stream_id_fn() {
+  static const StreamIdFn fn =
+      (StreamIdFn)dlsym(RTLD_DEFAULT, "hipStreamGetId");
+  return fn;
+}
+
+int library_workspace(size_t need, void *stream, void **out) {
   *out = nullptr;
   if (need == 0)
     return IREE_MI355X_OK;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess)
     return fail(IREE_MI355X_NO_DEVICE, "hipGetDevice failed");
-  std::lock_guard<std::mutex> lock(g_ws_mutex);
-  if ((int)g_ws.size() <= dev)
-    g_ws.resize(dev + 1);
-  DeviceWorkspace &ws = g_ws[dev];
-  if (ws.bytes < need) {
-    size_t grow = need < ((size_t)64 << 20) ? ((size_t)64 << 20) : need;
-    if (ws.ptr) {
-      // Work queued on any stream may still use the old buffer.
-      if (hipDeviceSynchronize() != hipSuccess || hipFree(ws.ptr) != hipSuccess)
-        return fail(IREE_MI355X_LAUNCH_FAILED, "workspace release failed");
-      ws.ptr = nullptr;
-      ws.bytes = 0;
-    }
-    if (hipMalloc(&ws.ptr, grow) != hipSuccess)
-      return fail(IREE_MI355X_LAUNCH_FAILED, "workspace hipMalloc(%zu) failed",
-                  grow);
-    if (hipMemset(ws.ptr, 0, grow) != hipSuccess)
-      return fail(IREE_MI355X_LAUNCH_FAILED, "workspace hipMemset failed");
-    ws.bytes = grow;
+  unsigned long long id = 0;
+  if (stream_id_fn() &&
+      stream_id_fn()((hipStream_t)stream, &id) != hipSuccess) {
+    (void)hipGetLastError();
+    id = 0;
   }
-  *out = ws.ptr;
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  StreamWorkspace *ws = nullptr;
+  for (StreamWorkspace &w : g_ws)
+    if (w.device == dev && w.handle == (uintptr_t)stream && w.id == id)
+      ws = &w;
+  if (ws && ws->bytes >= need) {
+    *out = ws->ptr;
+    return IREE_MI355X_OK;
+  }
+  const size_t have = ws ? ws->bytes : 0;
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing((hipStream_t)stream, &capture) != hipSuccess) {
+    (void)hipGetLastError();
+    capture = hipStreamCaptureStatusActive;  // unknown: do not allocate
+  }
+  if (capture != hipStreamCaptureStatusNone)
+    return fail(IREE_MI355X_WORKSPACE_TOO_SMALL,
+                "the stream is capturing and its library workspace holds "
+                "%zu < %zu bytes: pass a workspace sized by the workspace "
+                "query, or make one call on this stream before capture",
+                have, need);
+  size_t grow = (size_t)64 << 20;
+  if (grow < 2 * have)
+    grow = 2 * have;
+  if (grow < need)
+    grow = need;
+  void *p = nullptr;
+  if (hipMalloc(&p, grow) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(IREE_MI355X_LAUNCH_FAILED, "workspace hipMalloc(%zu) failed",
+                grow);
+  }
+  // Only the arrival counters must start at zero; partials are written
+  // before they are read. Stream order puts the fill before the kernel.
+  if (hipMemsetAsync(p, 0, kWorkspaceCounterBytes, (hipStream_t)stream) !=
+      hipSuccess) {
+    (void)hipGetLastError();
+    (void)hipFree(p);
+    return fail(IREE_MI355X_LAUNCH_FAILED, "workspace fill failed");
+  }
+  if (ws) {
+    ws->ptr = p;  // the old buffer is retired, not freed
+    ws->bytes = grow;
+  } else {
+    g_ws.push_back({dev, (uintptr_t)stream, id, p, grow});
+  }
+  *out = p;
   return IREE_MI355X_OK;
 }
 
@@ -121,7 +175,7 @@ static int launch_mfma(MatmulArgs &args, const iree_mi355x_matmul_plan_t &plan,
     args.workspace = workspace;
     if (!args.workspace) {
       const int st = library_workspace((size_t)plan.workspace_bytes,
-                                       &args.workspace);
+                                       args.stream, &args.workspace);
       if (st != IREE_MI355X_OK)
         return st;
     }
@@ -160,6 +214,15 @@ static int check_matmul(const char *who, const void *a, const void *b,
   return IREE_MI355X_OK;
 }
 
+// One row of a transposed A ([K, 1] with unit pitch) is the contiguous row
+// [1, K]: the same matmul without the transpose, which lets M = 1 decode
+// stream as a GEMV. Returns the flags the call runs with.
+uint32_t m1_row_layout(int64_t m, int64_t lda, uint32_t flags) {
+  if ((flags & IREE_MI355X_MATMUL_A_TRANSPOSED) && m == 1 && lda == 1)
+    return flags & ~IREE_MI355X_MATMUL_A_TRANSPOSED;
+  return flags;
+}
+
 }  // namespace ihp
 
 using namespace ihp;
@@ -182,23 +245,31 @@ size_t iree_mi355x_matmul_workspace_bytes(int64_t m, int64_t n, int64_t k,
   if (m <= 0 || n <= 0 || k <= 0)
     return 0;
   // The largest workspace any f16 or W8A16 plan of this shape uses (plans
-  // assume 16-byte aligned operands, the case that can pick split-K).
+  // assume 16-byte aligned operands, the case that can pick split-K), over
+  // both layouts a call may take: one row of a transposed A with unit pitch
+  // runs as the untransposed row (see m1_row_layout).
   size_t most = 0;
   const int32_t forms[3][3] = {
       {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16},
       {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F32},
       {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_F16}};
-  for (int f = 0; f < 3; ++f) {
-    iree_mi355x_matmul_desc_t d;
-    iree_mi355x_matmul_desc_init(&d, forms[f][0], forms[f][1], forms[f][2], m,
-                                 n, k, flags & ~IREE_MI355X_MATMUL_OUT_F32);
-    d.has_scale = f == 2;
-    if (f == 1)
-      d.flags |= IREE_MI355X_MATMUL_OUT_F32;
-    iree_mi355x_matmul_plan_t p;
-    if (iree_mi355x_plan_matmul(&d, &p) == IREE_MI355X_OK &&
-        (size_t)p.workspace_bytes > most)
-      most = (size_t)p.workspace_bytes;
+  for (int layout = 0; layout < 2; ++layout) {
+    const uint32_t lf =
+        layout == 0 ? flags : m1_row_layout(m, 1, flags);
+    if (layout == 1 && lf == flags)
+      break;
+    for (int f = 0; f < 3; ++f) {
+      iree_mi355x_matmul_desc_t d;
+      iree_mi355x_matmul_desc_init(&d, forms[f][0], forms[f][1], forms[f][2],
+                                   m, n, k, lf & ~IREE_MI355X_MATMUL_OUT_F32);
+      d.has_scale = f == 2;
+      if (f == 1)
+        d.flags |= IREE_MI355X_MATMUL_OUT_F32;
+      iree_mi355x_matmul_plan_t p;
+      if (iree_mi355x_plan_matmul(&d, &p) == IREE_MI355X_OK &&
+          (size_t)p.workspace_bytes > most)
+        most = (size_t)p.workspace_bytes;
+    }
   }
   return most;
 }
@@ -212,14 +283,12 @@ namespace ihp {
 static int matmul_f16_run(const char *who, MatmulArgs &args, uint32_t flags,
                           void *workspace, size_t workspace_bytes) {
   const bool out_f32 = flags & IREE_MI355X_MATMUL_OUT_F32;
-  args.a_transposed = (flags & IREE_MI355X_MATMUL_A_TRANSPOSED) ? 1 : 0;
-  if (args.a_transposed && args.m == 1 && args.lda == 1) {
-    // One row of a [K,1] A with unit pitch is the contiguous row [1,K]: the
-    // same matmul without the transpose (so M = 1 decode streams as GEMV).
-    args.a_transposed = 0;
+  const uint32_t run_flags = m1_row_layout(args.m, args.lda, flags);
+  if (run_flags != flags) {
     args.lda = args.k;
-    flags &= ~IREE_MI355X_MATMUL_A_TRANSPOSED;
+    flags = run_flags;
   }
+  args.a_transposed = (flags & IREE_MI355X_MATMUL_A_TRANSPOSED) ? 1 : 0;
   iree_mi355x_matmul_desc_t desc;
   iree_mi355x_matmul_desc_init(&desc, IREE_MI355X_ELEM_F16,
                                IREE_MI355X_ELEM_F16,
@@ -243,8 +312,8 @@ static int matmul_f16_run(const char *who, MatmulArgs &args, uint32_t flags,
           return fail(IREE_MI355X_WORKSPACE_TOO_SMALL,
                       "%s: workspace %zu < %zu", who, workspace_bytes,
                       (size_t)plan.workspace_bytes);
-        if (!ws && (st = library_workspace(plan.workspace_bytes, &ws)) !=
-                       IREE_MI355X_OK)
+        if (!ws && (st = library_workspace(plan.workspace_bytes, args.stream,
+                                           &ws)) != IREE_MI355X_OK)
           return st;
       }
       return launch_status(launch_gemv(args, 2, nullptr, out_f32, ws),
@@ -346,17 +415,24 @@ size_t iree_mi355x_batch_matmul_workspace_bytes(int64_t batch, int64_t m,
                                                 uint32_t flags) {
   if (batch <= 0 || m <= 0 || n <= 0 || k <= 0)
     return 0;
-  iree_mi355x_matmul_desc_t d;
-  iree_mi355x_matmul_desc_init(
-      &d, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16,
-      (flags & IREE_MI355X_MATMUL_OUT_F32) ? IREE_MI355X_ELEM_F32
-                                           : IREE_MI355X_ELEM_F16,
-      m, n, k, flags);
-  d.batch = batch;
-  iree_mi355x_matmul_plan_t p;
-  if (iree_mi355x_plan_matmul(&d, &p) != IREE_MI355X_OK)
-    return 0;
-  return (size_t)p.workspace_bytes;
+  size_t most = 0;
+  for (int layout = 0; layout < 2; ++layout) {
+    const uint32_t lf = layout == 0 ? flags : m1_row_layout(m, 1, flags);
+    if (layout == 1 && lf == flags)
+      break;
+    iree_mi355x_matmul_desc_t d;
+    iree_mi355x_matmul_desc_init(
+        &d, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16,
+        (lf & IREE_MI355X_MATMUL_OUT_F32) ? IREE_MI355X_ELEM_F32
+                                          : IREE_MI355X_ELEM_F16,
+        m, n, k, lf);
+    d.batch = batch;
+    iree_mi355x_matmul_plan_t p;
+    if (iree_mi355x_plan_matmul(&d, &p) == IREE_MI355X_OK &&
+        (size_t)p.workspace_bytes > most)
+      most = (size_t)p.workspace_bytes;
+  }
+  return most;
 }
 
 int iree_mi355x_matmul_i8(const int8_t *a, const int8_t *b, int32_t *c,
@@ -422,8 +498,8 @@ int iree_mi355x_w8a16_matmul(const void *x, const int8_t *w, const void *scale,
         return fail(IREE_MI355X_WORKSPACE_TOO_SMALL,
                     "w8a16_matmul: workspace %zu < %zu", workspace_bytes,
                     (size_t)plan.workspace_bytes);
-      if (!ws && (st = library_workspace(plan.workspace_bytes, &ws)) !=
-                     IREE_MI355X_OK)
+      if (!ws && (st = library_workspace(plan.workspace_bytes, stream,
+                                         &ws)) != IREE_MI355X_OK)
         return st;
     }
     return launch_status(launch_gemv(args, 1, scale, 0, ws), "gemv_w8a16");

@@ -23,11 +23,29 @@ int64_t u64(const uint32_t *c, int i) {
   return (int64_t)((uint64_t)c[i] | ((uint64_t)c[i + 1] << 32));
 }
 
-// Bytes a row-major [rows, cols] operand with leading dimension ld occupies.
+// Checked int64 arithmetic for binding sizes computed from caller constants:
+// any overflow, or a negative operand, yields -1, which check_binding
+// rejects. These checks run before the entry points' own extent checks, so
+// they must not wrap to a small size that a short binding would pass.
+int64_t mul_checked(int64_t a, int64_t b) {
+  int64_t r;
+  if (a < 0 || b < 0 || __builtin_mul_overflow(a, b, &r))
+    return -1;
+  return r;
+}
+int64_t add_checked(int64_t a, int64_t b) {
+  int64_t r;
+  if (a < 0 || b < 0 || __builtin_add_overflow(a, b, &r))
+    return -1;
+  return r;
+}
+
+// Bytes a row-major [rows, cols] operand with leading dimension ld occupies
+// (-1 if that does not fit in int64 or ld is negative).
 int64_t span(int64_t rows, int64_t cols, int64_t ld, int64_t elem) {
   if (rows <= 0 || cols <= 0)
     return 0;
-  return ((rows - 1) * ld + cols) * elem;
+  return mul_checked(add_checked(mul_checked(rows - 1, ld), cols), elem);
 }
 
 struct MatmulConsts {
@@ -126,7 +144,8 @@ int dispatch_w8a16(const iree_mi355x_executable_environment_t *,
   if (st)
     return st;
   if ((st = check_matmul_bindings(s, c, 2, 1, 2, 3, "w8a16_matmul")) ||
-      (st = check_binding(s, 2, c.n > 0 ? c.n * 2 : 0, "w8a16_matmul")))
+      (st = check_binding(s, 2, c.n > 0 ? mul_checked(c.n, 2) : 0,
+                          "w8a16_matmul")))
     return st;
   return iree_mi355x_w8a16_matmul(
       s->binding_ptrs[0], (const int8_t *)s->binding_ptrs[1],
@@ -145,8 +164,10 @@ int dispatch_attention(const iree_mi355x_executable_environment_t *,
   const int64_t batch = c[0], heads = c[1], sq = c[2], skv = c[3], d = c[4];
   float scale;
   memcpy(&scale, &c[5], 4);
-  const int64_t q_bytes = batch * heads * sq * d * 2;
-  const int64_t kv_bytes = batch * heads * skv * d * 2;
+  const int64_t planes = mul_checked(batch, heads);
+  const int64_t q_bytes = mul_checked(mul_checked(mul_checked(planes, sq), d), 2);
+  const int64_t kv_bytes =
+      mul_checked(mul_checked(mul_checked(planes, skv), d), 2);
   int st;
   if ((st = check_binding(s, 0, q_bytes, "attention_f16")) ||
       (st = check_binding(s, 1, kv_bytes, "attention_f16")) ||
@@ -188,7 +209,9 @@ int dispatch_batch_matmul(const iree_mi355x_executable_environment_t *,
   const int64_t cb = (c.flags & IREE_MI355X_MATMUL_OUT_F32) ? 4 : 2;
   const int64_t last = batch > 0 ? batch - 1 : 0;
   auto batched = [&](int64_t stride, int64_t one, int64_t elem) {
-    return one > 0 ? last * stride * elem + one : 0;
+    if (one <= 0)
+      return one;  // 0: nothing read; -1: overflow
+    return add_checked(mul_checked(mul_checked(last, stride), elem), one);
   };
   if ((st = check_binding(
            s, 0,
@@ -207,7 +230,7 @@ int dispatch_batch_matmul(const iree_mi355x_executable_environment_t *,
   epi.activation = act;
   uint32_t next = 3;
   if (has_bias) {
-    if ((st = check_binding(s, next, c.n * 2, who)))
+    if ((st = check_binding(s, next, mul_checked(c.n, 2), who)))
       return st;
     epi.bias = s->binding_ptrs[next++];
   }

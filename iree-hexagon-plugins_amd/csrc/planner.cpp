@@ -14,7 +14,7 @@
 namespace ihp {
 
 int fail(int status, const char *fmt, ...);
-int library_workspace(size_t need, void **out);
+int library_workspace(size_t need, void *stream, void **out);
 
 namespace {
 
@@ -598,7 +598,7 @@ int iree_mi355x_matmul_mfma_config_split(
                 "mfma_config %s: shape or layout does not fit", cfg.name);
   void *ws = nullptr;
   if (cand.workspace > 0) {
-    int st = library_workspace((size_t)cand.workspace, &ws);
+    int st = library_workspace((size_t)cand.workspace, stream, &ws);
     if (st != IREE_MI355X_OK)
       return st;
   }

@@ -77,17 +77,175 @@ static int bad_dims(int64_t m, int64_t n, int64_t k) {
   return m < 0 || n < 0 || k < 0;
 }
 
-/* B as f32 in [K][N] order (transposing a [N][K] operand), so every matmul
- * below runs the same row-update loop and sums each output in k order. */
-static float *widen_b_f16(const uint16_t *b, int64_t n, int64_t k, int64_t ldb,
-                          int transposed) {
-  float *out = (float *)malloc(sizeof(float) * (size_t)(n * k + 1));
+/* ------------------------------------------------ blocked k-order core ----
+ * Every matmul below computes acc[i][j] = sum_k A[i][k] * B[k][j] with each
+ * product rounded to f32 and added to the running sum in ascending k (integer
+ * forms: exact products, sums modulo 2^32). Blocking over rows, columns and k
+ * changes only which sums are in flight at once, never the operations of one
+ * sum: a k block resumes the stored f32 (u32) partial exactly where the
+ * previous block left it. B is packed into panels of NR columns, [panel][k][NR]
+ * (columns past N zero), A into f32 rows [i][k]. */
+#define OR_MR 6    /* rows per register block */
+#define OR_NR 16   /* columns per panel (two 8-lane vectors) */
+#define OR_KC 256  /* k per block */
+#define OR_MC 48   /* rows per task */
+#define OR_NC 256  /* columns per task */
+typedef float or_v8f __attribute__((vector_size(32)));
+typedef uint32_t or_v8u __attribute__((vector_size(32)));
+
+static int64_t or_panels(int64_t n) { return (n + OR_NR - 1) / OR_NR; }
+
+/* One register block: rows [0, rows) of `a` (row pitch lda, rows past `rows`
+ * repeat the last, discarded on store) times one panel over k in [k0, k1),
+ * resuming and storing the partial sums held in `ct` (row pitch OR_NC). */
+static void or_block_f32(const float *a, int64_t lda, int rows,
+                         const float *panel, int64_t k0, int64_t k1,
+                         float *ct) {
+  const float *ar[OR_MR];
+  or_v8f c[OR_MR][2];
+  for (int r = 0; r < OR_MR; ++r) {
+    ar[r] = a + (r < rows ? r : rows - 1) * lda;
+    memcpy(&c[r][0], ct + r * OR_NC, 32);
+    memcpy(&c[r][1], ct + r * OR_NC + 8, 32);
+  }
+  for (int64_t kk = k0; kk < k1; ++kk) {
+    or_v8f b0, b1;
+    memcpy(&b0, panel + kk * OR_NR, 32);
+    memcpy(&b1, panel + kk * OR_NR + 8, 32);
+    for (int r = 0; r < OR_MR; ++r) {
+      const or_v8f av = (or_v8f){0} + ar[r][kk];
+      const or_v8f p0 = av * b0, p1 = av * b1;
+      c[r][0] = c[r][0] + p0;
+      c[r][1] = c[r][1] + p1;
+    }
+  }
+  for (int r = 0; r < rows; ++r) {
+    memcpy(ct + r * OR_NC, &c[r][0], 32);
+    memcpy(ct + r * OR_NC + 8, &c[r][1], 32);
+  }
+}
+
+static void or_block_u32(const uint32_t *a, int64_t lda, int rows,
+                         const uint32_t *panel, int64_t k0, int64_t k1,
+                         uint32_t *ct) {
+  const uint32_t *ar[OR_MR];
+  or_v8u c[OR_MR][2];
+  for (int r = 0; r < OR_MR; ++r) {
+    ar[r] = a + (r < rows ? r : rows - 1) * lda;
+    memcpy(&c[r][0], ct + r * OR_NC, 32);
+    memcpy(&c[r][1], ct + r * OR_NC + 8, 32);
+  }
+  for (int64_t kk = k0; kk < k1; ++kk) {
+    or_v8u b0, b1;
+    memcpy(&b0, panel + kk * OR_NR, 32);
+    memcpy(&b1, panel + kk * OR_NR + 8, 32);
+    for (int r = 0; r < OR_MR; ++r) {
+      const or_v8u av = (or_v8u){0} + ar[r][kk];
+      c[r][0] = c[r][0] + av * b0;
+      c[r][1] = c[r][1] + av * b1;
+    }
+  }
+  for (int r = 0; r < rows; ++r) {
+    memcpy(ct + r * OR_NC, &c[r][0], 32);
+    memcpy(ct + r * OR_NC + 8, &c[r][1], 32);
+  }
+}
+
+/* acc [m][n] (pitch n) = A [m][k] . B-panels, 4-byte elements; `u32` picks
+ * the integer form. Tasks are (48-row, 256-column) output tiles. */
+static void or_gemm(const void *a, const void *bp, void *acc, int64_t m,
+                    int64_t n, int64_t k, int u32, int threads) {
+  const int64_t tm = (m + OR_MC - 1) / OR_MC, tn = (n + OR_NC - 1) / OR_NC;
+  if (threads < 1)
+    threads = 1;
+#pragma omp parallel for num_threads(threads) schedule(dynamic, 1)
+  for (int64_t task = 0; task < tm * tn; ++task) {
+    const int64_t i0 = (task / tn) * OR_MC, j0 = (task % tn) * OR_NC;
+    const int64_t rows = m - i0 < OR_MC ? m - i0 : OR_MC;
+    const int64_t cols = n - j0 < OR_NC ? n - j0 : OR_NC;
+    uint32_t tile[OR_MC * OR_NC];
+    memset(tile, 0, sizeof(tile));
+    for (int64_t k0 = 0; k0 < k; k0 += OR_KC) {
+      const int64_t k1 = k - k0 < OR_KC ? k : k0 + OR_KC;
+      for (int64_t jp = 0; jp < cols; jp += OR_NR) {
+        const int64_t panel = (j0 + jp) / OR_NR;
+        for (int64_t ib = 0; ib < rows; ib += OR_MR) {
+          const int r = (int)(rows - ib < OR_MR ? rows - ib : OR_MR);
+          if (u32)
+            or_block_u32((const uint32_t *)a + (i0 + ib) * k, k, r,
+                         (const uint32_t *)bp + panel * k * OR_NR, k0, k1,
+                         tile + ib * OR_NC + jp);
+          else
+            or_block_f32((const float *)a + (i0 + ib) * k, k, r,
+                         (const float *)bp + panel * k * OR_NR, k0, k1,
+                         (float *)tile + ib * OR_NC + jp);
+        }
+      }
+    }
+    for (int64_t i = 0; i < rows; ++i)
+      memcpy((uint32_t *)acc + (i0 + i) * n + j0, tile + i * OR_NC,
+             (size_t)cols * 4);
+  }
+}
+
+/* Element (i, j) of a 2-D operand stored row-major with pitch ld, or
+ * transposed (element (i, j) at j * ld + i). */
+#define OR_AT(p, i, j, ld, t) ((t) ? (p)[(j) * (ld) + (i)] : (p)[(i) * (ld) + (j)])
+
+/* B [K][N] (or [N][K] when transposed) of f16 / int8 as f32 / u32 panels. */
+static void *or_pack_b(const void *b, int64_t n, int64_t k, int64_t ldb,
+                       int transposed, int kind /* 0 f16, 1 i8->f32, 2 i8->u32 */,
+                       int threads) {
+  const int64_t np = or_panels(n);
+  uint32_t *out = (uint32_t *)calloc((size_t)(np * k * OR_NR + 1), 4);
   if (!out)
     return NULL;
-  for (int64_t kk = 0; kk < k; ++kk)
-    for (int64_t nn = 0; nn < n; ++nn)
-      out[kk * n + nn] = oracle_f16_to_f32(transposed ? b[nn * ldb + kk]
-                                                      : b[kk * ldb + nn]);
+  if (threads < 1)
+    threads = 1;
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t p = 0; p < np; ++p)
+    for (int64_t kk = 0; kk < k; ++kk)
+      for (int64_t c = 0; c < OR_NR && p * OR_NR + c < n; ++c) {
+        const int64_t j = p * OR_NR + c;
+        uint32_t *dst = out + (p * k + kk) * OR_NR + c;
+        if (kind == 0) {
+          const float f = oracle_f16_to_f32(
+              OR_AT((const uint16_t *)b, kk, j, ldb, transposed));
+          memcpy(dst, &f, 4);
+        } else {
+          const int8_t v = OR_AT((const int8_t *)b, kk, j, ldb, transposed);
+          if (kind == 1) {
+            const float f = (float)v;
+            memcpy(dst, &f, 4);
+          } else {
+            *dst = (uint32_t)(int32_t)v;
+          }
+        }
+      }
+  return out;
+}
+
+/* A [M][K] (or [K][M] when transposed) as f32 / u32 rows [i][k]. */
+static void *or_pack_a(const void *a, int64_t m, int64_t k, int64_t lda,
+                       int transposed, int kind /* 0 f16, 2 i8->u32 */,
+                       int threads) {
+  uint32_t *out = (uint32_t *)malloc((size_t)(m * k + 1) * 4);
+  if (!out)
+    return NULL;
+  if (threads < 1)
+    threads = 1;
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t i = 0; i < m; ++i)
+    for (int64_t kk = 0; kk < k; ++kk) {
+      uint32_t *dst = out + i * k + kk;
+      if (kind == 0) {
+        const float f =
+            oracle_f16_to_f32(OR_AT((const uint16_t *)a, i, kk, lda, transposed));
+        memcpy(dst, &f, 4);
+      } else {
+        *dst = (uint32_t)(int32_t)OR_AT((const int8_t *)a, i, kk, lda, transposed);
+      }
+    }
   return out;
 }
 
@@ -102,37 +260,30 @@ int oracle_matmul_f16(const uint16_t *a, const uint16_t *b, void *c,
   const int a_t = (flags & ORACLE_A_TRANSPOSED) != 0;
   const int accumulate = (flags & ORACLE_ACCUMULATE) != 0;
   const int out_f32 = (flags & ORACLE_OUT_F32) != 0;
-  /* A [K,M] (transposed LHS): element (m, k) at k * lda + m. */
-  const int64_t a_rs = a_t ? 1 : lda, a_ks = a_t ? lda : 1;
-  float *bf = widen_b_f16(b, n, k, ldb, transposed);
-  if (!bf)
+  float *af = (float *)or_pack_a(a, m, k, lda, a_t, 0, threads);
+  float *bf = (float *)or_pack_b(b, n, k, ldb, transposed, 0, threads);
+  float *acc = (float *)malloc(sizeof(float) * (size_t)(m * n + 1));
+  if (!af || !bf || !acc) {
+    free(af);
+    free(bf);
+    free(acc);
     return 2;
-  if (threads < 1)
-    threads = 1;
-#pragma omp parallel for num_threads(threads) schedule(static)
-  for (int64_t mm = 0; mm < m; ++mm) {
-    float *acc = (float *)calloc((size_t)n + 1, sizeof(float));
-    for (int64_t kk = 0; kk < k; ++kk) {
-      const float av = oracle_f16_to_f32(a[mm * a_rs + kk * a_ks]);
-      const float *brow = bf + kk * n;
-      for (int64_t nn = 0; nn < n; ++nn) {
-        float prod = av * brow[nn];
-        acc[nn] = acc[nn] + prod;
-      }
-    }
+  }
+  or_gemm(af, bf, acc, m, n, k, 0, threads);
+  for (int64_t mm = 0; mm < m; ++mm)
     for (int64_t nn = 0; nn < n; ++nn) {
+      const float s = acc[mm * n + nn];
       if (out_f32) {
         float *cp = (float *)c + mm * ldc + nn;
-        *cp = accumulate ? *cp + acc[nn] : acc[nn];
+        *cp = accumulate ? *cp + s : s;
       } else {
         uint16_t *cp = (uint16_t *)c + mm * ldc + nn;
-        float init = accumulate ? oracle_f16_to_f32(*cp) : 0.0f;
-        *cp = oracle_f32_to_f16(accumulate ? init + acc[nn] : acc[nn]);
+        *cp = oracle_f32_to_f16(accumulate ? oracle_f16_to_f32(*cp) + s : s);
       }
     }
-    free(acc);
-  }
+  free(af);
   free(bf);
+  free(acc);
   return 0;
 }
 
@@ -232,31 +383,25 @@ int oracle_matmul_i8(const int8_t *a, const int8_t *b, int32_t *c, int64_t m,
     return 1;
   const int transposed = (flags & ORACLE_B_TRANSPOSED) != 0;
   const int accumulate = (flags & ORACLE_ACCUMULATE) != 0;
-  int32_t *bi = (int32_t *)malloc(sizeof(int32_t) * (size_t)(n * k + 1));
-  if (!bi)
+  uint32_t *ai = (uint32_t *)or_pack_a(a, m, k, lda, 0, 2, threads);
+  uint32_t *bi = (uint32_t *)or_pack_b(b, n, k, ldb, transposed, 2, threads);
+  uint32_t *acc = (uint32_t *)malloc(sizeof(uint32_t) * (size_t)(m * n + 1));
+  if (!ai || !bi || !acc) {
+    free(ai);
+    free(bi);
+    free(acc);
     return 2;
-  for (int64_t kk = 0; kk < k; ++kk)
-    for (int64_t nn = 0; nn < n; ++nn)
-      bi[kk * n + nn] = transposed ? b[nn * ldb + kk] : b[kk * ldb + nn];
-  if (threads < 1)
-    threads = 1;
-#pragma omp parallel for num_threads(threads) schedule(static)
-  for (int64_t mm = 0; mm < m; ++mm) {
-    int32_t *acc = (int32_t *)calloc((size_t)n + 1, sizeof(int32_t));
-    for (int64_t kk = 0; kk < k; ++kk) {
-      const int32_t av = a[mm * lda + kk];
-      const int32_t *brow = bi + kk * n;
-      for (int64_t nn = 0; nn < n; ++nn)
-        acc[nn] += av * brow[nn];
-    }
+  }
+  or_gemm(ai, bi, acc, m, n, k, 1, threads);
+  for (int64_t mm = 0; mm < m; ++mm)
     for (int64_t nn = 0; nn < n; ++nn) {
       int32_t *cp = c + mm * ldc + nn;
       /* wrap like two's-complement i32 hardware adds */
-      *cp = accumulate ? (int32_t)((uint32_t)*cp + (uint32_t)acc[nn]) : acc[nn];
+      *cp = (int32_t)((accumulate ? (uint32_t)*cp : 0u) + acc[mm * n + nn]);
     }
-    free(acc);
-  }
+  free(ai);
   free(bi);
+  free(acc);
   return 0;
 }
 
@@ -268,31 +413,23 @@ int oracle_w8a16(const uint16_t *x, const int8_t *w, const uint16_t *scale,
   if (bad_dims(m, n, k))
     return 1;
   const int transposed = (flags & ORACLE_B_TRANSPOSED) != 0;
-  float *wf = (float *)malloc(sizeof(float) * (size_t)(n * k + 1));
-  if (!wf)
+  float *xf = (float *)or_pack_a(x, m, k, ldx, 0, 0, threads);
+  float *wf = (float *)or_pack_b(w, n, k, ldw, transposed, 1, threads);
+  float *acc = (float *)malloc(sizeof(float) * (size_t)(m * n + 1));
+  if (!xf || !wf || !acc) {
+    free(xf);
+    free(wf);
+    free(acc);
     return 2;
-  for (int64_t kk = 0; kk < k; ++kk)
-    for (int64_t nn = 0; nn < n; ++nn)
-      wf[kk * n + nn] = (float)(transposed ? w[nn * ldw + kk] : w[kk * ldw + nn]);
-  if (threads < 1)
-    threads = 1;
-#pragma omp parallel for num_threads(threads) schedule(static)
-  for (int64_t mm = 0; mm < m; ++mm) {
-    float *acc = (float *)calloc((size_t)n + 1, sizeof(float));
-    for (int64_t kk = 0; kk < k; ++kk) {
-      const float xv = oracle_f16_to_f32(x[mm * ldx + kk]);
-      const float *wrow = wf + kk * n;
-      for (int64_t nn = 0; nn < n; ++nn) {
-        float prod = xv * wrow[nn];
-        acc[nn] = acc[nn] + prod;
-      }
-    }
+  }
+  or_gemm(xf, wf, acc, m, n, k, 0, threads);
+  for (int64_t mm = 0; mm < m; ++mm)
     for (int64_t nn = 0; nn < n; ++nn)
       y[mm * ldy + nn] =
-          oracle_f32_to_f16(acc[nn] * oracle_f16_to_f32(scale[nn]));
-    free(acc);
-  }
+          oracle_f32_to_f16(acc[mm * n + nn] * oracle_f16_to_f32(scale[nn]));
+  free(xf);
   free(wf);
+  free(acc);
   return 0;
 }
 

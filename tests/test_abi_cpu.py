@@ -445,3 +445,55 @@ def test_export_attributes_cover_mfma_configs(pkg):
             attrs = lib.exports.attrs[names.index(export)]
             assert attrs.lds_bytes >= cfg.lds_bytes, (export, cfg.name)
             assert attrs.threads >= cfg.threads, (export, cfg.name)
+
+
+def test_dispatch_binding_spans_do_not_wrap(pkg):
+    """Binding sizes computed from caller constants are overflow-checked: an
+    ld or extent whose byte span wraps int64 is rejected before any launch
+    instead of wrapping to a small size a short binding would pass."""
+    big = 1 << 62
+    # (M - 1) * lda overflows: 3 * 2^62
+    consts = pkg.matmul_constants(4, 64, 64, big, 64, 64, 0)
+    assert pkg.call_export("matmul_f16", consts, [FAKE] * 3,
+                           [4096] * 3) == pkg.INVALID_ARGUMENT
+    assert "binding 0" in pkg.last_error()
+    # wraps to exactly 2^64 + small: (rows-1)*ld + cols = 2^63 - 1 + 1
+    consts = pkg.matmul_constants(2, 1, 1, (1 << 63) - 1, 1, 1, 0)
+    assert pkg.call_export("matmul_f16", consts, [FAKE] * 3,
+                           [64] * 3) == pkg.INVALID_ARGUMENT
+    # attention: batch * heads * seq * d * 2 past 2^64 from 32-bit constants
+    att = pkg.attention_constants(0xFFFFFFFF, 0xFFFFFFFF, 0xFFFF, 0xFFFF, 128,
+                                  0.125, 0)
+    assert pkg.call_export("attention_f16", att, [FAKE] * 4,
+                           [1 << 20] * 4) == pkg.INVALID_ARGUMENT
+    # batch strides: (batch - 1) * stride * 2 overflows
+    z, m, n, k = 3, 8, 8, 8
+    consts = pkg.batch_matmul_constants(m, n, k, k, n, n, 0, z, 1 << 62, 0,
+                                        m * n)
+    assert pkg.call_export("batch_matmul_f16", consts, [FAKE] * 3,
+                           [1 << 20] * 3) == pkg.INVALID_ARGUMENT
+
+
+def test_workspace_query_matches_dispatch_dry_run(pkg):
+    """The workspace query is an upper bound of what the call needs, the
+    M = 1 transposed-A row (planned as a GEMV) included; the dispatch
+    dry run reports what the call would use."""
+    lib = pkg.library()
+    cases = [(1, 4096, 4096, pkg.A_TRANSPOSED, 1),
+             (1, 4096, 4096, 0, 4096),
+             (16, 4096, 11008, 0, 11008),
+             (128, 11008, 4096, 0, 4096),
+             (2048, 4096, 4096, 0, 4096)]
+    for m, n, k, flags, lda in cases:
+        q = lib.iree_mi355x_matmul_workspace_bytes(m, n, k, flags)
+        consts = pkg.matmul_constants(m, n, k, lda, n, n, flags)
+        a_bytes = (k * lda if flags & pkg.A_TRANSPOSED else m * lda) * 2
+        st, need = pkg.call_export("matmul_f16", consts, [FAKE] * 3,
+                                   [a_bytes, k * n * 2, m * n * 2],
+                                   query=True)
+        assert st == pkg.OK, pkg.last_error()
+        assert need <= q, (m, n, k, flags, need, q)
+        if flags & pkg.A_TRANSPOSED:
+            assert need > 0  # runs as the GEMV, which needs a workspace
+        qb = lib.iree_mi355x_batch_matmul_workspace_bytes(1, m, n, k, flags)
+        assert need <= qb

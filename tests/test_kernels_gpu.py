@@ -289,14 +289,23 @@ def test_matmul_f16_reference_micro_shapes(pkg, oracle, dev, m, n, k, bt):
     fp16_ok(oracle, c.cpu().numpy(), ref)
 
 
-@pytest.mark.parametrize("m,n,k", [(2048, 4096, 4096), (128, 11008, 4096),
-                                   (16, 4096, 11008)])
+# Every BASELINE C3 point: M in {1, 16, 128, 2048} x (N, K) in
+# {(4096, 4096), (11008, 4096), (4096, 11008)}, each on the kernel the planner
+# picks for it, compared over the whole output.
+C3_POINTS = [(m, n, k) for m in (1, 16, 128, 2048)
+             for n, k in ((4096, 4096), (11008, 4096), (4096, 11008))]
+
+
+@pytest.mark.parametrize("m,n,k", C3_POINTS)
 def test_c3_linear_sweep(pkg, oracle, inputs, dev, m, n, k):
     x, w = inputs.c3_linear_f16(m, n, k)
+    print(f"c3 sweep m={m} n={n} k={k} plan="
+          f"{pkg.plan(pkg.make_desc(0, 0, 0, m, n, k, 0)).config_name.decode()}",
+          flush=True)
     y = pkg.matmul(x.to(dev), w.to(dev))
-    rows = min(m, 256)  # oracle on a row slice keeps the test short
-    ref = oracle.matmul_f16(x[:rows].numpy(), w.numpy())
-    fp16_ok(oracle, y[:rows].cpu().numpy(), ref)
+    ref = oracle.matmul_f16(x.numpy(), w.numpy(),
+                            threads=oracle.default_threads())
+    fp16_ok(oracle, y.cpu().numpy(), ref)
 
 
 def test_c3_linear_transposed_weights_full(pkg, oracle, inputs, dev):
@@ -437,10 +446,9 @@ def test_w8a16_general(pkg, oracle, inputs, dev, m, transposed):
         w = w.t().contiguous()
     y = pkg.quantized_matmul(x.to(dev), w.to(dev), s.to(dev),
                              w_transposed=transposed)
-    rows = min(m, 128)
-    ref = oracle.w8a16(x[:rows].numpy(), w.numpy(), s.numpy(),
-                       w_transposed=transposed)
-    fp16_ok(oracle, y[:rows].cpu().numpy(), ref)
+    ref = oracle.w8a16(x.numpy(), w.numpy(), s.numpy(),
+                       w_transposed=transposed, threads=oracle.default_threads())
+    fp16_ok(oracle, y.cpu().numpy(), ref)
 
 
 # -------------------------------------------------------------- attention ---
@@ -769,3 +777,72 @@ def test_export_attributes_cover_their_kernels(pkg):
         assert k["max_threads"] >= k["threads"], k
         if k["name"] in cfg_lds:
             assert k["lds_bytes"] == cfg_lds[k["name"]], k
+
+
+# ----------------------------------------------- library workspace, streams --
+
+def test_split_k_on_two_streams_library_workspace(pkg, oracle, dev):
+    """workspace == NULL on two streams at once: each stream has its own
+    library workspace, so the two split-K reductions (and two GEMVs) cannot
+    share arrival counters or partials."""
+    g = torch.Generator().manual_seed(21)
+    cases = [(16, 4096, 4096), (1, 4096, 4096)]
+    for m, n, k in cases:
+        assert pkg.plan(pkg.make_desc(0, 0, 0, m, n, k, 0)).workspace_bytes > 0
+        xs = [(torch.randn(m, k, generator=g) * 0.5).half() for _ in range(2)]
+        ws = [(torch.randn(k, n, generator=g) * 0.02).half() for _ in range(2)]
+        xd = [x.to(dev) for x in xs]
+        wd = [w.to(dev) for w in ws]
+        streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+        torch.cuda.synchronize()
+        outs = [[], []]
+        for rep in range(8):  # interleaved on both streams
+            for i, s in enumerate(streams):
+                with torch.cuda.stream(s):
+                    outs[i].append(pkg.matmul(xd[i], wd[i]))
+        torch.cuda.synchronize()
+        for i in range(2):
+            ref = oracle.matmul_f16(xs[i].numpy(), ws[i].numpy())
+            for y in outs[i]:
+                fp16_ok(oracle, y.cpu().numpy(), ref)
+
+
+def test_library_workspace_under_capture(pkg, oracle, dev):
+    """A capturing stream never allocates: with no library workspace yet the
+    call is refused (WORKSPACE_TOO_SMALL, nothing captured); after one eager
+    call on that stream the workspace exists and the captured split-K
+    matmul replays correctly, with eager work between replays."""
+    m, n, k = 16, 4096, 4096
+    g = torch.Generator().manual_seed(22)
+    x = (torch.randn(m, k, generator=g) * 0.5).half()
+    w = (torch.randn(k, n, generator=g) * 0.02).half()
+    xd, wd = x.to(dev), w.to(dev)
+    y = torch.empty(m, n, dtype=torch.float16, device=dev)
+    ref = oracle.matmul_f16(x.numpy(), w.numpy())
+    s = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with pytest.raises(pkg.MI355XError) as err:
+        with torch.cuda.graph(graph, stream=s):
+            y.zero_()  # the graph is not empty when the matmul is refused
+            pkg.matmul(xd, wd, y)
+    assert err.value.status == pkg.WORKSPACE_TOO_SMALL
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        pkg.matmul(xd, wd, y)  # sizes this stream's workspace
+    torch.cuda.synchronize()
+    fp16_ok(oracle, y.cpu().numpy(), ref)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        pkg.matmul(xd, wd, y)
+    x2 = (torch.randn(m, k, generator=g) * 0.5).half()
+    ref2 = oracle.matmul_f16(x2.numpy(), w.numpy())
+    x2d = x2.to(dev)
+    for rep in range(4):
+        y.fill_(7.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        fp16_ok(oracle, y.cpu().numpy(), ref)
+        with torch.cuda.stream(s):  # eager split-K on the same workspace
+            y2 = pkg.matmul(x2d, wd)
+        torch.cuda.synchronize()
+        fp16_ok(oracle, y2.cpu().numpy(), ref2)
