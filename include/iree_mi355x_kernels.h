@@ -178,6 +178,22 @@ int iree_mi355x_attention_f16(const void *q, const void *k, const void *v,
 size_t iree_mi355x_matmul_workspace_bytes(int64_t m, int64_t n, int64_t k,
                                           uint32_t flags);
 
+// iree_mi355x_matmul_f16 without any allocation: the split-K partials and
+// arrival counters live in the library's own device scratch (32 MiB per GPU,
+// a static device array held until the process ends) instead of a caller or
+// library workspace, so the call never allocates, frees or synchronizes.
+// No counterpart in the reference: it is for callers that cannot allocate
+// (code under HIP graph capture, tight serving loops, harnesses that forbid
+// hipMalloc). A shape whose plan needs more scratch than that returns
+// IREE_MI355X_WORKSPACE_TOO_SMALL before anything is launched. Every call
+// on one GPU shares that GPU's scratch: calls that overlap on a GPU (on
+// different streams, or graphs replayed concurrently) race and must be
+// ordered by the caller.
+int iree_mi355x_matmul_f16_no_alloc(const void *a, const void *b, void *c,
+                                    int64_t m, int64_t n, int64_t k,
+                                    int64_t lda, int64_t ldb, int64_t ldc,
+                                    uint32_t flags, void *stream);
+
 // Last error message recorded on this thread (empty string if none).
 const char *iree_mi355x_last_error(void);
 

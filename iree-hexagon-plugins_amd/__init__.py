@@ -73,6 +73,7 @@ EXPORTED_SYMBOLS = (
     "iree_mi355x_executable_serialize", "iree_mi355x_executable_verify",
     "iree_mi355x_executable_load", "iree_mi355x_loaded_executable_library",
     "iree_mi355x_loaded_executable_release",
+    "iree_mi355x_matmul_f16_no_alloc",
 )
 
 # Activations of the fused matmul epilogue (include/iree_mi355x_kernels.h).
@@ -217,6 +218,8 @@ def library():
                                            i64, u32, p, sz, p]
     lib.iree_mi355x_matmul_i8.argtypes = [p, p, p, i64, i64, i64, i64, i64,
                                           i64, u32, p]
+    lib.iree_mi355x_matmul_f16_no_alloc.argtypes = [p, p, p, i64, i64, i64,
+                                                    i64, i64, i64, u32, p]
     lib.iree_mi355x_w8a16_matmul.argtypes = [p, p, p, p, i64, i64, i64, i64,
                                              i64, i64, u32, p, sz, p]
     lib.iree_mi355x_attention_f16.argtypes = [p, p, p, p, i64, i64, i64, i64,

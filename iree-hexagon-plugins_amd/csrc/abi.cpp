@@ -150,6 +150,42 @@ int library_workspace(size_t need, void *stream, void **out) {
   return IREE_MI355X_OK;
 }
 
+// Scratch of the allocation-free entry point: device memory of the
+// library's own code object, one copy per GPU that runs the library, held
+// until the process ends. It is zero from load, and every kernel that uses
+// it leaves its arrival counters at zero again, so no call clears it;
+// calls that overlap on one GPU race on it.
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+// Device address of `scratch` on the current device, looked up once per
+// device: the host-side name is only a stand-in, not a device address.
+static std::mutex g_scratch_mutex;
+static std::vector<void *> g_scratch;
+
+static int scratch_address(void **out) {
+  *out = nullptr;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess)
+    return fail(IREE_MI355X_NO_DEVICE, "hipGetDevice failed");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if ((int)g_scratch.size() <= dev)
+    g_scratch.resize(dev + 1, nullptr);
+  if (!g_scratch[dev]) {
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress((void **)&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      (void)hipGetLastError();
+      return fail(IREE_MI355X_LAUNCH_FAILED,
+                  "scratch: hipGetSymbolAddress failed: %s",
+                  hipGetErrorString(e));
+    }
+    g_scratch[dev] = ptr;
+  }
+  *out = g_scratch[dev];
+  return IREE_MI355X_OK;
+}
+
 static int launch_status(hipError_t e, const char *what) {
   if (e != hipSuccess)
     return fail(IREE_MI355X_LAUNCH_FAILED, "%s: %s", what, hipGetErrorString(e));
@@ -351,6 +387,31 @@ int iree_mi355x_matmul_f16(const void *a, const void *b, void *c, int64_t m,
                   (flags & IREE_MI355X_MATMUL_ACCUMULATE) ? 1 : 0, stream};
   return matmul_f16_run("matmul_f16", args, flags, workspace,
                         workspace_bytes);
+}
+
+int iree_mi355x_matmul_f16_no_alloc(const void *a, const void *b, void *c,
+                                    int64_t m, int64_t n, int64_t k,
+                                    int64_t lda, int64_t ldb, int64_t ldc,
+                                    uint32_t flags, void *stream) {
+  const char *who = "matmul_f16_no_alloc";
+  const bool out_f32 = flags & IREE_MI355X_MATMUL_OUT_F32;
+  int st = check_matmul(who, a, b, c, m, n, k, lda, ldb, ldc, flags,
+                        IREE_MI355X_MATMUL_B_TRANSPOSED |
+                            IREE_MI355X_MATMUL_ACCUMULATE |
+                            IREE_MI355X_MATMUL_OUT_F32 |
+                            IREE_MI355X_MATMUL_A_TRANSPOSED,
+                        2, 2, out_f32 ? 4 : 2);
+  if (st != IREE_MI355X_OK || m == 0 || n == 0)
+    return st == IREE_MI355X_OK ? ok() : st;
+  void *ws = nullptr;
+  if ((st = scratch_address(&ws)) != IREE_MI355X_OK)
+    return st;
+  MatmulArgs args{a, b, c, m, n, k, lda, ldb, ldc,
+                  (flags & IREE_MI355X_MATMUL_B_TRANSPOSED) ? 1 : 0,
+                  (flags & IREE_MI355X_MATMUL_ACCUMULATE) ? 1 : 0, stream};
+  // A plan needing more than the scratch holds is refused by the workspace
+  // check (WORKSPACE_TOO_SMALL) before anything is launched.
+  return matmul_f16_run(who, args, flags, ws, kNoAllocScratchBytes);
 }
 
 int iree_mi355x_batch_matmul_f16(const void *a, const void *b, void *c,
