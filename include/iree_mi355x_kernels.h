@@ -15,7 +15,7 @@
 //    dimensions (in elements) and counts are int64_t.
 //  * `stream` is a hipStream_t (NULL = the legacy default stream). Work is
 //    enqueued and the call returns without waiting; calls on different
-//    streams are independent unless they share a workspace.
+//    streams are independent unless the caller gives them one workspace.
 //  * Return value is an iree_mi355x_status_t; preconditions are checked on
 //    the host before anything is launched, so an error never leaves work
 //    behind. The reference ABI has no error channel (its preconditions are
@@ -171,10 +171,15 @@ int iree_mi355x_attention_f16(const void *q, const void *k, const void *v,
 // partials and arrival counters), 0 if none. Mirrors the scratch query of the
 // reference's caller-scratch matmul, hexkl_matmul_f16f16_f32_scratch_bytes
 // (CG/Conversion/HexagonRuntimeLinking.h:35-38). Passing workspace == NULL
-// makes the library use its own per-device workspace (allocated once, grown on
-// demand); a caller workspace must be zero-filled before its first use and is
-// left zero-filled in its counter region (its first 256 KiB) after every call,
-// so one workspace serves any sequence of calls of any shapes.
+// makes the library use its own workspace of the call's stream (one per
+// stream, allocated by the first call that needs it, grown on demand, never
+// freed; a capturing stream never allocates and gets
+// IREE_MI355X_WORKSPACE_TOO_SMALL instead). A caller workspace must be
+// zero-filled before its first use and is left zero-filled in its counter
+// region (its first 256 KiB) after every call, so one workspace serves any
+// sequence of calls of any shapes; calls that overlap must not share one.
+// The value covers every layout the call may run with, the M = 1
+// transposed-A row included.
 size_t iree_mi355x_matmul_workspace_bytes(int64_t m, int64_t n, int64_t k,
                                           uint32_t flags);
 
