@@ -8,7 +8,15 @@ M=1 GEMV HBM GB/s), the roofline of the dominant kernel measured with HIP
 events on the stream it runs on, and the CPU baseline (the C oracle on the
 host cores, labelled "port": IREE is not installable here).
 
---suite prints one JSON line per BASELINE config (C1..C5 and the C3 sweep).
+The default line also times C3 M=2048 with row-major weights, C4 attention
+and C5 W8A16 (M=1, 512), and measures this box's ceilings with the
+calibration kernels: a register-only MFMA loop on random operands (the
+`ceiling` next to `peak`) and a pure HBM stream read of the GEMV's bytes.
+
+--suite prints one JSON line per BASELINE config (C1..C5 and the C3 sweep),
+each with the C oracle timed beside it on this host.
+--only <workload> runs one workload for profiler passes; --only stream and
+--only mfma_ceiling print the calibration ceilings alone.
 --tune times every compiled MFMA macro-tile on the 4096^3 shapes.
 """
 from __future__ import annotations
@@ -49,7 +57,8 @@ def parse():
     p.add_argument("--no-graph", action="store_true",
                    help="time eager launches instead of one captured graph")
     p.add_argument("--only", choices=["i8", "f16", "f16nn", "gemv", "attn",
-                                      "w8a16", "w8a16_gemm", "runtime"],
+                                      "w8a16", "w8a16_gemm", "runtime",
+                                      "stream", "mfma_ceiling"],
                    help="run one workload (for rocprof passes) and exit")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="with --only: first copy 256 MiB device-to-device "
@@ -137,12 +146,128 @@ def capture_stream():
     return _CAPTURE_STREAM
 
 
+_CAL = None
+
+
+def calibration():
+    """The benchmark's ceiling kernels (lib/libiree_mi355x_calibrate.so):
+    a pure HBM stream read and a register-only MFMA loop."""
+    import ctypes
+    global _CAL
+    if _CAL is None:
+        path = os.path.join(ROOT, "iree-hexagon-plugins_amd", "lib",
+                            "libiree_mi355x_calibrate.so")
+        if not os.path.exists(path):
+            raise ImportError(f"{path} is not built; run __graft_entry__.build()")
+        lib = ctypes.CDLL(path)
+        p, i64 = ctypes.c_void_p, ctypes.c_int64
+        lib.iree_mi355x_calibrate_stream_read.argtypes = [p, i64, p,
+                                                          ctypes.c_int, p]
+        lib.iree_mi355x_calibrate_mfma_loop.argtypes = [
+            ctypes.c_int, p, ctypes.c_int, p, ctypes.c_int, p]
+        _CAL = lib
+    return _CAL
+
+
+def stream_ceiling(dev, nbytes, steps, warmup):
+    """GB/s of a pure read of `nbytes`, rotating copies past the 256 MiB
+    Infinity Cache; the best over four grid sizes."""
+    import torch
+    lib = calibration()
+    copies = max(2, ROTATE_BYTES // nbytes + 1)
+    bufs = [torch.randint(-2 ** 31, 2 ** 31 - 1, (nbytes // 4,),
+                          dtype=torch.int32, device=dev) for _ in range(copies)]
+    best = None
+    for wgs in (512, 1024, 2048, 4096):
+        sink = torch.empty(wgs, dtype=torch.int32, device=dev)
+        it = [0]
+
+        def fn():
+            st = lib.iree_mi355x_calibrate_stream_read(
+                bufs[it[0] % copies].data_ptr(), nbytes, sink.data_ptr(), wgs,
+                torch.cuda.current_stream().cuda_stream)
+            assert st == 0
+            it[0] += 1
+        ms = timed(fn, max(steps, 4 * copies), warmup)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        if best is None or gbs > best[0]:
+            best = (gbs, wgs, ms)
+    del bufs
+    return {"gbs": round(best[0], 1), "us": round(best[2] * 1e3, 2),
+            "workgroups": best[1], "bytes": nbytes, "rotating_copies": copies}
+
+
+def mfma_ceiling(dev, kind, random_operands, steps=50, warmup=100,
+                 iters=4096):
+    """Dense TOPS (kind "i8") or TFLOP/s ("f16") of MFMAs on operands held
+    in registers (no memory traffic), 256 workgroups of 8 waves: the MFMA
+    pipe at the clock the operand data lets the chip hold."""
+    import torch
+    lib = calibration()
+    g = torch.Generator().manual_seed(5)
+    n = 64 * 256 * 16
+    if kind == "i8":
+        src = (torch.randint(-128, 128, (n,), generator=g, dtype=torch.int8)
+               if random_operands else torch.ones(n, dtype=torch.int8))
+        ops_per_mfma = 2 * 32 * 32 * 32
+    else:
+        src = (torch.randn(n // 2, generator=g).half() if random_operands
+               else torch.ones(n // 2, dtype=torch.float16))
+        ops_per_mfma = 2 * 32 * 32 * 16
+    src = src.to(dev)
+    wgs = 256
+    sink = torch.empty(wgs * 512, dtype=torch.int32, device=dev)
+
+    def fn():
+        st = lib.iree_mi355x_calibrate_mfma_loop(
+            0 if kind == "i8" else 1, src.data_ptr(), iters, sink.data_ptr(),
+            wgs, torch.cuda.current_stream().cuda_stream)
+        assert st == 0
+    ms = timed(fn, steps, warmup)
+    return ops_per_mfma * 4 * iters * wgs * 8 / (ms * 1e-3) / 1e12
+
+
+def cpu_info():
+    """nproc and the CPU model of this host (BASELINE's CPU baseline asks
+    for both next to the threads used)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "cpu_model": model}
+
+
+def cpu_threads():
+    """Host threads for the CPU baseline: this box's share (OMP_NUM_THREADS,
+    16 per GPU here), whatever nproc reports."""
+    try:
+        return max(1, int(os.environ.get("OMP_NUM_THREADS", "16")))
+    except ValueError:
+        return 16
+
+
+def cpu_time(fn, budget_s=2.0, max_runs=100):
+    """Seconds per run of fn() on the host, repeated to about `budget_s`:
+    (seconds per run, runs)."""
+    runs, t0 = 0, time.perf_counter()
+    while runs < max_runs and (runs == 0 or
+                               time.perf_counter() - t0 < budget_s):
+        fn()
+        runs += 1
+    return (time.perf_counter() - t0) / runs, runs
+
+
 def rotating(make, count):
     """`count` independent copies of a device tensor, to rotate through."""
     return [make() for _ in range(count)]
 
 
-def cpu_baseline_i8(a, bt, threads, budget_s=12.0, max_runs=40):
+def cpu_baseline_i8(a, bt, threads, budget_s=12.0, max_runs=400):
     """The C oracle on the host cores over the full C2 workload, repeated
     until about `budget_s` of CPU work: (TOPS, runs, seconds)."""
     import oracle
@@ -223,6 +348,45 @@ def main():
     gemv_gbs = gemv_bytes / (msv * 1e-3) / 1e9
     del ws
 
+    # ---- the other BASELINE configs the metric's kernels run on ----
+    # C3 M=2048 N=K=4096 with row-major weights (linalg.matmul's map, NN)
+    x, wn = (t.to(dev) for t in inputs.c3_linear_f16(2048, 4096, 4096))
+    yn = torch.empty(2048, 4096, dtype=torch.float16, device=dev)
+    ms_nn = timed(lambda: pkg.matmul(x, wn, yn), args.steps, args.warmup)
+    nn_tflops = 2.0 * 2048 * 4096 * 4096 / (ms_nn * 1e-3) / 1e12
+    del x, wn, yn
+    # C4 attention
+    q, kk, v = (t.to(dev) for t in inputs.c4_attention_f16())
+    o = torch.empty_like(q)
+    ms_att = timed(lambda: pkg.attention(q, kk, v, o, causal=True),
+                   min(args.steps, 200), min(args.warmup, 200))
+    att_flops = 4.0 * 32 * 2048 * 2048 * 128 / 2
+    att_tflops = att_flops / (ms_att * 1e-3) / 1e12
+    del q, kk, v, o
+    # C5 W8A16, M=1 (rotating int8 weights) and M=512
+    c5 = {}
+    for mm in (1, 512):
+        xq, wq, sq = inputs.c5_w8a16(mm)
+        cp = max(1, min(24, ROTATE_BYTES // wq.numel() + 1)) if mm == 1 else 1
+        wqs = [wq.to(dev)] + [wq.to(dev).clone() for _ in range(cp - 1)]
+        xq, sq = xq.to(dev), sq.to(dev)
+        yq = torch.empty(mm, wq.shape[1], dtype=torch.float16, device=dev)
+        itq = [0]
+
+        def w8_step():
+            pkg.quantized_matmul(xq, wqs[itq[0] % cp], sq, yq)
+            itq[0] += 1
+        c5[mm] = timed(w8_step, max(args.steps, 4 * cp), args.warmup)
+        del wqs
+    c5_m1_bytes = 4096 * 11008 + 2 * 11008 + 2 * 4096 + 2 * 11008
+    c5_m1_gbs = c5_m1_bytes / (c5[1] * 1e-3) / 1e9
+    c5_512_tflops = 2.0 * 512 * 11008 * 4096 / (c5[512] * 1e-3) / 1e12
+
+    # ---- ceilings measured on this box (calibration kernels) ----
+    ceil_i8 = mfma_ceiling(dev, "i8", True)
+    ceil_f16 = mfma_ceiling(dev, "f16", True)
+    stream32 = stream_ceiling(dev, 4096 * 4096 * 2, args.steps, args.warmup)
+
     out = {
         "metric": "int8/fp16 matmul TOPS/TFLOPS + % MFMA peak at 4096^3; "
                   "GEMV HBM GB/s",
@@ -243,34 +407,58 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(tops, 1),
                      "peak": PEAK_I8_TOPS, "unit": "TOPS",
                      "frac": round(tops / PEAK_I8_TOPS, 4),
-                     "traffic": profiled_traffic(plan.config_name.decode())},
+                     "traffic": profiled_traffic(plan.config_name.decode()),
+                     "ceiling": round(ceil_i8, 1),
+                     "ceiling_frac": round(tops / ceil_i8, 4),
+                     "ceiling_kind": "register-only int8 MFMA loop on random "
+                                     "operands, measured in this run"},
         "extra": {
             "fp16_4096_tflops": round(tflops16, 1),
             "fp16_4096_frac_peak": round(tflops16 / PEAK_F16_TFLOPS, 4),
             "fp16_4096_layout": "B [N,K] (transposed), f32 acc, f16 out",
+            "fp16_mfma_ceiling_tflops": round(ceil_f16, 1),
+            "c3_m2048_n4096_k4096_nn_tflops": round(nn_tflops, 1),
+            "c3_m2048_n4096_k4096_nn_frac_peak":
+                round(nn_tflops / PEAK_F16_TFLOPS, 4),
             "gemv_m1_4096_gbs": round(gemv_gbs, 1),
             "gemv_m1_4096_frac_hbm": round(gemv_gbs / PEAK_HBM_GBS, 4),
             "gemv_rotating_copies": copies,
+            "hbm_stream_read_32mib_gbs": stream32["gbs"],
+            "gemv_m1_4096_frac_stream": round(gemv_gbs / stream32["gbs"], 4),
+            "c4_attention_tflops": round(att_tflops, 1),
+            "c4_attention_us": round(ms_att * 1e3, 2),
+            "c4_attention_frac_peak": round(att_tflops / PEAK_F16_TFLOPS, 4),
+            "c5_w8a16_m1_gbs": round(c5_m1_gbs, 1),
+            "c5_w8a16_m1_us": round(c5[1] * 1e3, 2),
+            "c5_w8a16_m1_frac_hbm": round(c5_m1_gbs / PEAK_HBM_GBS, 4),
+            "c5_w8a16_m512_tflops": round(c5_512_tflops, 1),
+            "c5_w8a16_m512_frac_peak": round(c5_512_tflops / PEAK_F16_TFLOPS, 4),
         },
     }
     if not args.no_cpu_baseline:
-        threads = min(16, os.cpu_count() or 1)
+        threads = cpu_threads()
         cpu_tops, runs, dt = cpu_baseline_i8(a.numpy(), bt.numpy(), threads)
         out["cpu_baseline"] = {
             "value": round(cpu_tops, 4), "unit": "TOPS", "cores": threads,
-            "kind": "port",
+            "kind": "port", **cpu_info(),
             "sample": f"the full C2 4096^3 int8 matmul, {runs} runs in "
-                      f"{dt:.1f} s, by the C oracle (OpenMP, -O3 AVX2) on the "
-                      "same inputs; IREE llvm-cpu is not installable without "
+                      f"{dt:.1f} s, by the C oracle (OpenMP, -O3 AVX2, "
+                      f"{threads} threads: this box's share) on the same "
+                      "inputs; IREE llvm-cpu is not installable without "
                       "network"}
     print(json.dumps(out), flush=True)
 
 
 def suite(pkg, inputs, dev, args):
     import torch
+    import oracle
     steps, warm = args.steps, args.warmup
+    threads = cpu_threads()
+    host = cpu_info()
 
-    def emit(name, ms, flops, nbytes, bound, extra=None):
+    def emit(name, ms, flops, nbytes, bound, extra=None, cpu=None):
+        """One line per config; `cpu` = (fn, sample text, fraction of the
+        config's work one fn() call does) times the C oracle beside it."""
         rec = {"config": name, "ms": round(ms, 5),
                "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
                "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1), "bound": bound}
@@ -280,17 +468,38 @@ def suite(pkg, inputs, dev, args):
                             / peak, 4)
         if extra:
             rec.update(extra)
+        if cpu is not None and not args.no_cpu_baseline:
+            fn, sample, share = cpu
+            sec, runs = cpu_time(fn)
+            full = sec / share  # seconds for the whole config
+            rec["cpu_baseline"] = {
+                "ms": round(full * 1e3, 3),
+                "tflops": round(flops / full / 1e12, 4),
+                "gbs": round(nbytes / full / 1e9, 2),
+                "gpu_speedup": round(full * 1e3 / ms, 1),
+                "cores": threads, "kind": "port", **host,
+                "sample": f"{sample}, {runs} run(s), C oracle on {threads} "
+                          "threads"}
         print(json.dumps(rec), flush=True)
 
-    a, b = (t.to(dev) for t in inputs.c1_matmul_f16())
+    ah, bh = inputs.c1_matmul_f16()
+    a, b = ah.to(dev), bh.to(dev)
     c = torch.empty(128, 512, dtype=torch.float16, device=dev)
     ms = timed(lambda: pkg.matmul(a, b, c), steps, warm)
-    emit("C1 f16 128x512x256", ms, 2 * 128 * 512 * 256, 458752, "latency")
+    an, bn = ah.numpy(), bh.numpy()
+    emit("C1 f16 128x512x256", ms, 2 * 128 * 512 * 256, 458752, "latency",
+         cpu=(lambda: oracle.matmul_f16(an, bn, threads=threads),
+              "the full C1 matmul", 1.0))
 
-    a, bt = (t.to(dev) for t in inputs.c2_matmul_i8())
+    ah, bh = inputs.c2_matmul_i8()
+    a, bt = ah.to(dev), bh.to(dev)
     c = torch.empty(4096, 4096, dtype=torch.int32, device=dev)
     ms = timed(lambda: pkg.matmul(a, bt, c, b_transposed=True), steps, warm)
-    emit("C2 i8 4096^3", ms, 2 * 4096 ** 3, 100663296, "mfma")
+    an, bn = ah.numpy(), bh.numpy()
+    emit("C2 i8 4096^3", ms, 2 * 4096 ** 3, 100663296, "mfma",
+         cpu=(lambda: oracle.matmul_i8(an, bn, b_transposed=True,
+                                       threads=threads),
+              "the full C2 matmul", 1.0))
     del a, bt, c
 
     for m in (1, 16, 128, 2048):
@@ -308,16 +517,27 @@ def suite(pkg, inputs, dev, args):
                 it[0] += 1
             ms = timed(step, max(steps, 3 * copies), warm)
             fam = pkg.plan(pkg.make_desc(0, 0, 0, m, n, k, 0)).config_name.decode()
+            rows = min(m, 256)  # the oracle on a row sample of the big M
+            xn, wn = x[:rows].cpu().numpy(), w.numpy()
             emit(f"C3 f16 M={m} N={n} K={k}", ms, 2 * m * n * k,
                  2 * (m * k + k * n + m * n), "hbm" if m <= 16 else "mfma",
-                 {"kernel": fam, "rotating_copies": copies})
+                 {"kernel": fam, "rotating_copies": copies},
+                 cpu=(lambda: oracle.matmul_f16(xn, wn, threads=threads),
+                      f"{rows} of {m} rows, scaled by {m / rows:g}",
+                      rows / m))
             del ws
 
-    q, k_, v = (t.to(dev) for t in inputs.c4_attention_f16())
+    qh, kh, vh = inputs.c4_attention_f16()
+    q, k_, v = qh.to(dev), kh.to(dev), vh.to(dev)
     o = torch.empty_like(q)
     ms = timed(lambda: pkg.attention(q, k_, v, o, causal=True), steps, warm)
+    # the oracle on 4 of the 32 heads (every head costs the same)
+    q4, k4, v4 = (t[:, :4].contiguous().numpy() for t in (qh, kh, vh))
     emit("C4 attention causal B1 H32 S2048 D128", ms,
-         4 * 32 * 2048 * 2048 * 128 / 2, 4 * q.numel() * 2, "mfma")
+         4 * 32 * 2048 * 2048 * 128 / 2, 4 * q.numel() * 2, "mfma",
+         cpu=(lambda: oracle.attention_f16(q4, k4, v4, causal=True,
+                                           threads=threads),
+              "4 of the 32 heads, scaled by 8", 4 / 32))
     del q, k_, v, o
 
     for m in (1, 512):
@@ -334,9 +554,13 @@ def suite(pkg, inputs, dev, args):
             it[0] += 1
         ms = timed(step, max(steps, 3 * copies), warm)
         n, k = w.shape[1], w.shape[0]
+        rows = min(m, 128)
+        xn, wn, sn = x[:rows].cpu().numpy(), w.numpy(), s.cpu().numpy()
         emit(f"C5 w8a16 M={m} N={n} K={k}", ms, 2 * m * n * k,
              n * k + 2 * n + 2 * m * k + 2 * m * n, "hbm" if m == 1 else "mfma",
-             {"rotating_copies": copies})
+             {"rotating_copies": copies},
+             cpu=(lambda: oracle.w8a16(xn, wn, sn, threads=threads),
+                  f"{rows} of {m} rows, scaled by {m / rows:g}", rows / m))
         del ws
 
     runtime_suite(pkg, inputs, dev, emit, steps)
@@ -411,6 +635,26 @@ def only(pkg, inputs, dev, args):
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if w == "stream":
+        # the GEMV's 32 MiB, the C5 int8 weights (45 MB) and the 11008 x
+        # 4096 f16 weights (90 MB)
+        for nbytes in (4096 * 4096 * 2, 4096 * 11008, 11008 * 4096 * 2):
+            rec = stream_ceiling(dev, nbytes, args.steps, args.warmup)
+            rec["frac_hbm"] = round(rec["gbs"] / PEAK_HBM_GBS, 4)
+            print(json.dumps({"only": w, **rec}), flush=True)
+        return
+    if w == "mfma_ceiling":
+        for kind in ("i8", "f16"):
+            for rnd in (True, False):
+                v = mfma_ceiling(dev, kind, rnd)
+                peak = PEAK_I8_TOPS if kind == "i8" else PEAK_F16_TFLOPS
+                print(json.dumps({
+                    "only": w, "kind": kind,
+                    "operands": "random" if rnd else "constant",
+                    "value": round(v, 1),
+                    "unit": "TOPS" if kind == "i8" else "TFLOP/s",
+                    "frac_peak": round(v / peak, 4)}), flush=True)
+        return
     if w == "i8":
         a, bt = (t.to(dev) for t in inputs.c2_matmul_i8())
         c = torch.empty(4096, 4096, dtype=torch.int32, device=dev)
