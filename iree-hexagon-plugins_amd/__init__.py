@@ -74,6 +74,7 @@ EXPORTED_SYMBOLS = (
     "iree_mi355x_executable_load", "iree_mi355x_loaded_executable_library",
     "iree_mi355x_loaded_executable_release",
     "iree_mi355x_matmul_f16_no_alloc",
+    "iree_mi355x_match_linalg_op", "iree_mi355x_match_dispatch_region",
 )
 
 # Activations of the fused matmul epilogue (include/iree_mi355x_kernels.h).
@@ -189,6 +190,56 @@ class Binding(ctypes.Structure):
     _fields_ = [("buffer", ctypes.c_void_p), ("length", ctypes.c_uint64)]
 
 
+# Dispatch matcher (include/iree_mi355x_matcher.h).
+MAX_LOOPS, MAX_OPERANDS, MAX_BODY = 8, 6, 24
+OP_GENERIC, OP_MATMUL, OP_BATCH_MATMUL, OP_QUANTIZED_MATMUL = 0, 1, 2, 3
+OP_FILL, OP_TRANSPOSE, OP_ATTENTION = 4, 5, 6
+TYPES = {"f16": 1, "bf16": 2, "f32": 3, "f64": 4, "i1": 5, "i8": 6,
+         "i32": 7, "i64": 8, "index": 9}
+MAP_ZERO = -1
+FROM_ARGUMENT, FROM_CONSTANT = -1, -2
+BODY_OPS = {"yield": 0, "const": 1, "extf": 2, "truncf": 3, "extsi": 4,
+            "sitofp": 5, "mulf": 6, "addf": 7, "subf": 8, "divf": 9,
+            "maximumf": 10, "exp": 11, "muli": 12, "addi": 13, "subi": 14,
+            "index": 15, "index_cast": 16, "cmpf": 17, "cmpi": 18,
+            "select": 19, "andi": 20}
+PREDICATES = {"oeq": 1, "eq": 1, "ogt": 2, "sgt": 2, "ugt": 3}
+MATCH_NAMED_ONLY = 0x1
+
+
+class BodyOp(ctypes.Structure):
+    """iree_mi355x_body_op_t."""
+    _fields_ = [("opcode", ctypes.c_uint32), ("operands", ctypes.c_int32 * 3),
+                ("type", ctypes.c_int32), ("constant", ctypes.c_double)]
+
+
+class LinalgOp(ctypes.Structure):
+    """iree_mi355x_linalg_op_t."""
+    _fields_ = [("kind", ctypes.c_uint32), ("num_loops", ctypes.c_uint32),
+                ("reduction_loops", ctypes.c_uint32),
+                ("loop_extent", ctypes.c_int64 * MAX_LOOPS),
+                ("num_inputs", ctypes.c_uint32),
+                ("num_outputs", ctypes.c_uint32),
+                ("elem_type", ctypes.c_int32 * MAX_OPERANDS),
+                ("map_rank", ctypes.c_uint32 * MAX_OPERANDS),
+                ("map", (ctypes.c_int32 * MAX_LOOPS) * MAX_OPERANDS),
+                ("producer", ctypes.c_int32 * MAX_OPERANDS),
+                ("producer_result", ctypes.c_int32 * MAX_OPERANDS),
+                ("scalar", ctypes.c_double * MAX_OPERANDS),
+                ("num_body_ops", ctypes.c_uint32),
+                ("body", BodyOp * MAX_BODY)]
+
+
+class MatchResult(ctypes.Structure):
+    """iree_mi355x_match_t."""
+    _fields_ = [("taken", ctypes.c_int32), ("export_name", ctypes.c_char * 32),
+                ("flags", ctypes.c_uint32), ("batch_loop", ctypes.c_int32),
+                ("m_loop", ctypes.c_int32), ("n_loop", ctypes.c_int32),
+                ("k_loop", ctypes.c_int32), ("root", ctypes.c_int32),
+                ("scale", ctypes.c_float), ("head_loop", ctypes.c_int32),
+                ("reason", ctypes.c_char * 160)]
+
+
 _lib = None
 
 
@@ -285,6 +336,10 @@ def library():
     lib.iree_mi355x_loaded_executable_release.argtypes = [p]
     lib.iree_mi355x_executable_library_query.restype = ctypes.c_void_p
     lib.iree_mi355x_executable_library_query.argtypes = [u32, p]
+    lib.iree_mi355x_match_linalg_op.argtypes = [
+        ctypes.POINTER(LinalgOp), u32, ctypes.POINTER(MatchResult)]
+    lib.iree_mi355x_match_dispatch_region.argtypes = [
+        ctypes.POINTER(LinalgOp), u32, u32, ctypes.POINTER(MatchResult)]
     _lib = lib
     return lib
 
@@ -359,6 +414,127 @@ def mfma_configs() -> list[MfmaConfig]:
                               lds.value, th.value,
                               lib.iree_mi355x_mfma_config_layout_flags(i)))
     return out
+
+
+# ----------------------------------------------------------------- matcher --
+
+def linalg_op(kind, loops, maps, types, *, inputs, reductions=(),
+              extents=None, args=None, body=(), producers=None,
+              scalars=None) -> LinalgOp:
+    """Describe one linalg op for the matcher.
+
+    loops: loop names in order ("m n k" or a list); reductions: the
+    reduction loops' names; maps: one per operand (inputs, then outputs),
+    each the loop names of its dimensions with "0" for a broadcast
+    dimension ("m k", "b m 0"); types: element type names per operand;
+    inputs: how many operands are inputs; extents: {loop: extent}
+    (missing: dynamic); args: names of the body's block arguments (default:
+    in0.., out0..); body: SSA ops in order, each (name, op, operand names,
+    type[, attribute]) with the attribute a constant's value, an index op's
+    loop name or a comparison predicate, ending with ("yield", [names]);
+    producers: per operand, an earlier op's index (or (index, result)),
+    "arg" (default) or ("const", value).
+    """
+    loop_names = loops.split() if isinstance(loops, str) else list(loops)
+    pos = {n: i for i, n in enumerate(loop_names)}
+    op = LinalgOp()
+    op.kind = kind
+    op.num_loops = len(loop_names)
+    op.reduction_loops = sum(1 << pos[r] for r in reductions)
+    for i in range(MAX_LOOPS):
+        op.loop_extent[i] = -1
+    for name, ext in (extents or {}).items():
+        op.loop_extent[pos[name]] = ext
+    op.num_inputs = inputs
+    op.num_outputs = len(maps) - inputs
+    for i, (m, t) in enumerate(zip(maps, types)):
+        dims = m.split() if isinstance(m, str) else list(m)
+        op.elem_type[i] = TYPES[t]
+        op.map_rank[i] = len(dims)
+        for r, d in enumerate(dims):
+            op.map[i][r] = MAP_ZERO if d == "0" else pos[d]
+        op.producer[i] = FROM_ARGUMENT
+    for i, prod in enumerate(producers or ()):
+        if prod == "arg" or prod is None:
+            op.producer[i] = FROM_ARGUMENT
+        elif isinstance(prod, tuple) and prod[0] == "const":
+            op.producer[i] = FROM_CONSTANT
+            op.scalar[i] = prod[1]
+        elif isinstance(prod, tuple):
+            op.producer[i], op.producer_result[i] = prod
+        else:
+            op.producer[i] = prod
+    for i, v in (scalars or {}).items():
+        op.scalar[i] = v
+    values = {}
+    names = args or ([f"in{i}" for i in range(inputs)] +
+                     [f"out{i}" for i in range(len(maps) - inputs)])
+    for i, n in enumerate(names):
+        values[n] = i
+    op.num_body_ops = len(body)
+    for b, entry in enumerate(body):
+        if entry[0] == "yield":
+            bo = op.body[b]
+            bo.opcode = BODY_OPS["yield"]
+            ids = [values[n] for n in entry[1]] + [-1, -1, -1]
+            bo.operands[:] = ids[:3]
+            continue
+        name, code, operand_names, typ = entry[:4]
+        attr = entry[4] if len(entry) > 4 else 0.0
+        bo = op.body[b]
+        bo.opcode = BODY_OPS[code]
+        ids = [values[n] for n in operand_names] + [-1, -1, -1]
+        bo.operands[:] = ids[:3]
+        bo.type = TYPES[typ]
+        if code == "index":
+            bo.constant = pos[attr]
+        elif code in ("cmpf", "cmpi"):
+            bo.constant = PREDICATES[attr]
+        else:
+            bo.constant = float(attr)
+        values[name] = len(names) + b
+    return op
+
+
+@dataclass
+class Match:
+    taken: bool
+    export: str
+    flags: int
+    batch_loop: int
+    m_loop: int
+    n_loop: int
+    k_loop: int
+    root: int
+    scale: float
+    head_loop: int
+    reason: str
+
+
+def _match_result(r: MatchResult) -> Match:
+    return Match(bool(r.taken), r.export_name.decode(), r.flags, r.batch_loop,
+                 r.m_loop, r.n_loop, r.k_loop, r.root, r.scale, r.head_loop,
+                 r.reason.decode())
+
+
+def match(op: LinalgOp, *, named_only=False) -> Match:
+    """Which export computes one linalg op (iree_mi355x_match_linalg_op)."""
+    out = MatchResult()
+    _check(library().iree_mi355x_match_linalg_op(
+        ctypes.byref(op), MATCH_NAMED_ONLY if named_only else 0,
+        ctypes.byref(out)))
+    return _match_result(out)
+
+
+def match_region(ops, *, named_only=False) -> Match:
+    """Which export computes a dispatch region (ops in program order, the
+    last one's result is the region's)."""
+    arr = (LinalgOp * len(ops))(*ops)
+    out = MatchResult()
+    _check(library().iree_mi355x_match_dispatch_region(
+        arr, len(ops), MATCH_NAMED_ONLY if named_only else 0,
+        ctypes.byref(out)))
+    return _match_result(out)
 
 
 # ----------------------------------------------------------- library table --
