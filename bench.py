@@ -198,29 +198,36 @@ def stream_ceiling(dev, nbytes, steps, warmup):
 
 
 def mfma_ceiling(dev, kind, random_operands, steps=50, warmup=100,
-                 iters=4096):
+                 iters=4096, shape=32):
     """Dense TOPS (kind "i8") or TFLOP/s ("f16") of MFMAs on operands held
     in registers (no memory traffic), 256 workgroups of 8 waves: the MFMA
-    pipe at the clock the operand data lets the chip hold."""
+    pipe at the clock the operand data lets the chip hold. `shape` 32:
+    the 32x32 MFMAs the GEMM kernels issue; 16: the 16x16 ones."""
     import torch
     lib = calibration()
     g = torch.Generator().manual_seed(5)
     n = 64 * 256 * 16
+    per_lane_k = 32 if kind == "i8" else 16  # K of the 32x32 shape
     if kind == "i8":
         src = (torch.randint(-128, 128, (n,), generator=g, dtype=torch.int8)
                if random_operands else torch.ones(n, dtype=torch.int8))
-        ops_per_mfma = 2 * 32 * 32 * 32
     else:
         src = (torch.randn(n // 2, generator=g).half() if random_operands
                else torch.ones(n // 2, dtype=torch.float16))
-        ops_per_mfma = 2 * 32 * 32 * 16
+    if shape == 32:
+        ops_per_mfma = 2 * 32 * 32 * per_lane_k
+    else:
+        ops_per_mfma = 2 * 16 * 16 * 2 * per_lane_k
+        iters *= 2  # half the products per instruction
     src = src.to(dev)
     wgs = 256
     sink = torch.empty(wgs * 512, dtype=torch.int32, device=dev)
 
+    code = (0 if kind == "i8" else 1) + (2 if shape == 16 else 0)
+
     def fn():
         st = lib.iree_mi355x_calibrate_mfma_loop(
-            0 if kind == "i8" else 1, src.data_ptr(), iters, sink.data_ptr(),
+            code, src.data_ptr(), iters, sink.data_ptr(),
             wgs, torch.cuda.current_stream().cuda_stream)
         assert st == 0
     ms = timed(fn, steps, warmup)
@@ -645,11 +652,12 @@ def only(pkg, inputs, dev, args):
         return
     if w == "mfma_ceiling":
         for kind in ("i8", "f16"):
-            for rnd in (True, False):
-                v = mfma_ceiling(dev, kind, rnd)
+            for shape, rnd in ((32, True), (32, False), (16, True), (16, False)):
+                v = mfma_ceiling(dev, kind, rnd, shape=shape)
                 peak = PEAK_I8_TOPS if kind == "i8" else PEAK_F16_TFLOPS
                 print(json.dumps({
                     "only": w, "kind": kind,
+                    "mfma": f"{shape}x{shape}",
                     "operands": "random" if rnd else "constant",
                     "value": round(v, 1),
                     "unit": "TOPS" if kind == "i8" else "TFLOP/s",

@@ -11,6 +11,8 @@
 //    per SIMD, so the issue rate is the MFMA pipe's at whatever clock the
 //    operand data lets the chip hold. Random operands toggle more bits than
 //    constant ones; that difference is the power ceiling the GEMMs meet.
+//    The 32x32 and 16x16 shapes are both measured: they draw different
+//    power per product.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -46,11 +48,12 @@ __global__ __launch_bounds__(512) void stream_read_kernel(
 }
 
 // `iters` rounds of 4 independent MFMAs per wave on operands loaded once
-// from `src` (64 lanes x 4 operands x 16 bytes per wave).
-template <typename T>
+// from `src` (64 lanes x 4 operands x 16 bytes per wave); MF is the 32x32
+// or the 16x16 MFMA family (the same operand bytes per lane, half the
+// products per instruction for 16x16).
+template <typename MF>
 __global__ __launch_bounds__(512) void mfma_loop_kernel(
     const i32x4 *__restrict__ src, int iters, int32_t *__restrict__ sink) {
-  typedef Mfma32<T> MF;
   typedef typename MF::Acc Acc;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -69,7 +72,7 @@ __global__ __launch_bounds__(512) void mfma_loop_kernel(
   // vector element to zero and dropped the whole loop.
   uint32_t s = 0;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
+  for (int r = 0; r < (int)(sizeof(Acc) / 4); ++r) {
     const typename MF::AccScalar e0 = c0[r], e1 = c1[r], e2 = c2[r],
                                  e3 = c3[r];
     s ^= __builtin_bit_cast(uint32_t, e0) ^ __builtin_bit_cast(uint32_t, e1) ^
@@ -99,21 +102,35 @@ int iree_mi355x_calibrate_stream_read(const void *src, int64_t bytes,
 }
 
 // MFMA loop: `workgroups` x 8 waves, `iters` rounds of 4 MFMAs each;
-// kind 0: v_mfma_i32_32x32x32_i8, 1: v_mfma_f32_32x32x16_f16. `src` holds
+// kind 0: v_mfma_i32_32x32x32_i8, 1: v_mfma_f32_32x32x16_f16,
+// 2: v_mfma_i32_16x16x64_i8, 3: v_mfma_f32_16x16x32_f16. `src` holds
 // 64 x 256 x 16 bytes of operands, `sink` workgroups x 512 x 4 bytes.
 int iree_mi355x_calibrate_mfma_loop(int kind, const void *src, int iters,
                                     void *sink, int workgroups,
                                     void *stream) {
-  if (!src || !sink || iters <= 0 || workgroups <= 0)
+  if (!src || !sink || iters <= 0 || workgroups <= 0 || kind < 0 || kind > 3)
     return 1;
-  if (kind == 0)
-    hipLaunchKernelGGL(mfma_loop_kernel<int8_t>, dim3(workgroups), dim3(512),
-                       0, (hipStream_t)stream, (const i32x4 *)src, iters,
-                       (int32_t *)sink);
-  else
-    hipLaunchKernelGGL(mfma_loop_kernel<f16>, dim3(workgroups), dim3(512), 0,
-                       (hipStream_t)stream, (const i32x4 *)src, iters,
-                       (int32_t *)sink);
+  const dim3 grid(workgroups), block(512);
+  const hipStream_t s = (hipStream_t)stream;
+  const i32x4 *in = (const i32x4 *)src;
+  int32_t *out = (int32_t *)sink;
+  switch (kind) {
+    case 0:
+      hipLaunchKernelGGL(mfma_loop_kernel<Mfma32<int8_t>>, grid, block, 0, s,
+                         in, iters, out);
+      break;
+    case 1:
+      hipLaunchKernelGGL(mfma_loop_kernel<Mfma32<f16>>, grid, block, 0, s, in,
+                         iters, out);
+      break;
+    case 2:
+      hipLaunchKernelGGL(mfma_loop_kernel<Mfma16<int8_t>>, grid, block, 0, s,
+                         in, iters, out);
+      break;
+    default:
+      hipLaunchKernelGGL(mfma_loop_kernel<Mfma16<f16>>, grid, block, 0, s, in,
+                         iters, out);
+  }
   return hipGetLastError() == hipSuccess ? 0 : 4;
 }
 

@@ -62,6 +62,7 @@ struct Mfma16;
 template <>
 struct Mfma16<f16> {
   typedef f32x4 Acc;
+  typedef float AccScalar;
   static __device__ __forceinline__ Acc mma(i32x4 a, i32x4 b, Acc c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(
         __builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
@@ -72,6 +73,7 @@ struct Mfma16<f16> {
 template <>
 struct Mfma16<int8_t> {
   typedef i32x4 Acc;
+  typedef int AccScalar;
   static __device__ __forceinline__ Acc mma(i32x4 a, i32x4 b, Acc c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
   }

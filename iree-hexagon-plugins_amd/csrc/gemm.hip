@@ -119,8 +119,15 @@ __device__ __forceinline__ void lgkm_tie2(i32x2 &v) {
 // split over several runs is reduced the same way. M need not be a
 // multiple of BM: A rows past M are clamped to row M-1 on the copy side (rows
 // of C depend only on their own row of A) and never stored.
+//
+// MS: the MFMA shape, 32 (v_mfma_*_32x32x{16,32}) or 16
+// (v_mfma_*_16x16x{32,64}). Both read the same operand bytes per wave tile;
+// on random operands the 16x16 instructions sustain 11-15 % more products
+// per second on this chip (the calibration loop: int8 4075 against 3559
+// TOPS, f16 1950 against 1754 TFLOP/s), the power per product being lower.
+// The 16x16 form takes TN B operands without a transposed A.
 template <typename T, typename OutT, int BM, int BN, int BKB, int WM, int WN,
-          int STAGES, int BMODE, bool SPLIT, bool AT>
+          int STAGES, int BMODE, bool SPLIT, bool AT, int MS = 32>
 __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     const T *__restrict__ A, const void *__restrict__ Bv, OutT *__restrict__ C,
     const f16 *__restrict__ scale, int M, int N, int K, int64_t lda,
@@ -128,13 +135,20 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     typename Mfma32<T>::AccScalar *__restrict__ partials,
     unsigned *__restrict__ counters, int64_t sa, int64_t sb, int64_t sc,
     Epi epi, int64_t s_mul) {
-  typedef Mfma32<T> MF;
+  static_assert(MS == 32 || MS == 16, "MFMA shape");
+  static_assert(MS == 32 || (BMODE == kBTN && !AT), "16x16: TN operands");
+  typedef typename std::conditional<MS == 32, Mfma32<T>, Mfma16<T>>::type MF;
   typedef typename MF::Acc Acc;
+  // Accumulator registers per fragment, K bytes per MFMA step and the
+  // 16-byte chunks one step reads per row.
+  constexpr int AR = MS == 32 ? 16 : 4;
+  constexpr int KSB = MS == 32 ? 32 : 64;
+  constexpr int KCH = KSB / 16;
   constexpr bool kNN = BMODE != kBTN;
   constexpr int TBB = BMODE == kBW8 ? 1 : (int)sizeof(T);  // B element bytes
   constexpr int NT = 64 * WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int FM = WTM / 32, FN = WTN / 32;
+  constexpr int FM = WTM / MS, FN = WTN / MS;
   constexpr int KE = BKB / (int)sizeof(T);  // K elements per stage
   constexpr int CH = BKB / 16;              // chunks per staged A (TN B) row
   constexpr int ROWS_PER_WAVE = 64 / CH;
@@ -157,7 +171,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   constexpr int LOADS_PER_STAGE = A_PASSES + B_PASSES;
   constexpr int A_BYTES = BM * BKB;
   constexpr int STAGE_BYTES = A_BYTES + B_ROWS * BROW;
-  constexpr int KSTEPS = BKB / 32;
+  constexpr int KSTEPS = BKB / KSB;
   // LDS reads per K step: FM A fragments, FN B fragments (two transposed
   // reads each for f16 NN).
   constexpr int B_READS = BMODE == kBNN16 ? 2 * FN : FN;
@@ -293,14 +307,15 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   using First = std::integral_constant<int, 0>;
   using All = std::integral_constant<int, LOADS_PER_STAGE>;
 
-  // Read side, A (and TN B): lane reads row (lane % 32) of each 32-row
-  // fragment, logical chunk 2*ks + lane/32 of the staged row.
-  const int rd_row = lane & 31;
-  const int rd_sw = chunk_swizzle<CH>(rd_row) ^ (lane >> 5);
+  // Read side, A (and TN B): lane reads row (lane % MS) of each MS-row
+  // fragment, logical chunk KCH*ks + lane/MS of the staged row (the swizzle
+  // repeats every 16 rows, so it depends on the row in the fragment only).
+  const int rd_row = lane & (MS - 1);
+  const int rd_sw = chunk_swizzle<CH>(rd_row) ^ (lane / MS);
   int koff[KSTEPS];
 #pragma unroll
   for (int ks = 0; ks < KSTEPS; ++ks)
-    koff[ks] = ((2 * ks) ^ rd_sw) * 16;
+    koff[ks] = ((KCH * ks) ^ rd_sw) * 16;
   const int a_rd = (wm * WTM + rd_row) * BKB;
   const int b_rd = A_BYTES + (wn * WTN + rd_row) * BKB;
   // Read side, transposed A: the row-major B offsets below with M for N.
@@ -360,13 +375,13 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     } else {
       const IHP_LDS char *pa = st + a_rd + koff[ks];
       static_for<FM>([&](auto i) {
-        f.a[i] = lds_read_16_async<decltype(i)::value * 32 * BKB>(pa);
+        f.a[i] = lds_read_16_async<decltype(i)::value * MS * BKB>(pa);
       });
     }
     if constexpr (BMODE == kBTN) {
       const IHP_LDS char *pb = st + b_rd + koff[ks];
       static_for<FN>([&](auto j) {
-        f.b[j] = lds_read_16_async<decltype(j)::value * 32 * BKB>(pb);
+        f.b[j] = lds_read_16_async<decltype(j)::value * MS * BKB>(pb);
       });
     } else {
       const IHP_LDS char *pb = st + ks * 16 * BROW;
@@ -425,7 +440,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
 #pragma unroll
     for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
+      for (int r = 0; r < AR; ++r)
         acc[i][j][r] = 0;
 
   const int nk = (int)((k_len * (int64_t)sizeof(T)) / BKB);
@@ -504,9 +519,11 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     stage(kt, No(), No(), No());
 
   // Epilogue: C_out = [C_init +] acc (W8A16: acc * scale[n]), one rounding
-  // for f16 outputs.
-  const int col_l = lane & 31;
-  const int row_l = 4 * (lane >> 5);
+  // for f16 outputs. Lane l holds column l % MS of a fragment; register r
+  // holds row row_l + frow(r).
+  const int col_l = lane & (MS - 1);
+  const int row_l = 4 * (lane / MS);
+  auto frow = [](int r) { return MS == 32 ? 8 * (r >> 2) + (r & 3) : r; };
   constexpr bool kIntOut = std::is_same<OutT, int32_t>::value;
   if constexpr (!kIntOut) {
     if ((!SPLIT || parts == 1) && !epi_plain(epi)) {
@@ -515,7 +532,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
       // one rolled loop applies scale / bias / activation / multiplier and
       // stores whole rows, so the epilogue is instanced once per band
       // instead of once per accumulator register.
-      constexpr int PITCH = 33;
+      constexpr int PITCH = MS + 1;
       static_assert(WM * WN * WTN * PITCH * 4 <= STAGES * STAGE_BYTES,
                     "epilogue staging");
       float *stage = (float *)smem + wave * WTN * PITCH;
@@ -526,13 +543,13 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
-          for (int r = 0; r < 16; ++r)
-            stage[(j * 32 + col_l) * PITCH + row_l + 8 * (r >> 2) +
-                  (r & 3)] = (float)acc[i][j][r];
+          for (int r = 0; r < AR; ++r)
+            stage[(j * MS + col_l) * PITCH + row_l + frow(r)] =
+                (float)acc[i][j][r];
         __syncthreads();
-        for (int t = lane; t < 32 * WTN; t += 64) {
+        for (int t = lane; t < MS * WTN; t += 64) {
           const int rr = t / WTN, cc = t % WTN;
-          const int64_t row = row0 + i * 32 + rr, col = col0 + cc;
+          const int64_t row = row0 + i * MS + rr, col = col0 + cc;
           if (SPLIT && row >= M)
             continue;
           float v = stage[cc * PITCH + rr];
@@ -553,32 +570,30 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
       if (store_mode == kStoreThrough) {
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
-          OutT *crow = C + (m0 + wm * WTM + i * 32 + row_l) * ldc + n0 +
+          OutT *crow = C + (m0 + wm * WTM + i * MS + row_l) * ldc + n0 +
                        wn * WTN + col_l;
 #pragma unroll
           for (int j = 0; j < FN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-              store_through(crow + (8 * (r >> 2) + (r & 3)) * ldc + j * 32,
-                            acc[i][j][r]);
+            for (int r = 0; r < AR; ++r)
+              store_through(crow + frow(r) * ldc + j * MS, acc[i][j][r]);
         }
         return;
       }
     }
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
-      OutT *crow = C + (m0 + wm * WTM + i * 32 + row_l) * ldc + n0 +
+      OutT *crow = C + (m0 + wm * WTM + i * MS + row_l) * ldc + n0 +
                    wn * WTN + col_l;
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         float sc = 1.0f;
         if constexpr (BMODE == kBW8)
-          sc = (float)scale[n0 + wn * WTN + j * 32 + col_l];
+          sc = (float)scale[n0 + wn * WTN + j * MS + col_l];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          OutT *dst = crow + (8 * (r >> 2) + (r & 3)) * ldc + j * 32;
-          const int64_t row =
-              m0 + wm * WTM + i * 32 + row_l + 8 * (r >> 2) + (r & 3);
+        for (int r = 0; r < AR; ++r) {
+          OutT *dst = crow + frow(r) * ldc + j * MS;
+          const int64_t row = m0 + wm * WTM + i * MS + row_l + frow(r);
           if (SPLIT && row >= M)
             continue;
           if constexpr (kIntOut) {
@@ -603,11 +618,10 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
-        const int64_t col = n0 + wn * WTN + j * 32 + col_l;
+        const int64_t col = n0 + wn * WTN + j * MS + col_l;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t row =
-              m0 + wm * WTM + i * 32 + row_l + 8 * (r >> 2) + (r & 3);
+        for (int r = 0; r < AR; ++r) {
+          const int64_t row = m0 + wm * WTM + i * MS + row_l + frow(r);
           if (row < M)
             store_device(part_out + row * N + col, (P)acc[i][j][r]);
         }
@@ -867,7 +881,7 @@ __global__ __launch_bounds__(256) void gemm_general_kernel(
 // ----------------------------------------------------------------------------
 
 template <typename T, typename OutT, int BM, int BN, int BKB, int WM, int WN,
-          int STAGES, int BMODE, bool SPLIT, bool AT>
+          int STAGES, int BMODE, bool SPLIT, bool AT, int MS = 32>
 static hipError_t launch_fast(const MatmulArgs &a) {
   typedef typename Mfma32<T>::AccScalar P;
   const int64_t tiles_m = SPLIT ? (a.m + BM - 1) / BM : a.m / BM;
@@ -889,7 +903,7 @@ static hipError_t launch_fast(const MatmulArgs &a) {
           : kStorePlain;
   hipLaunchKernelGGL(
       (gemm_lds_kernel<T, OutT, BM, BN, BKB, WM, WN, STAGES, BMODE, SPLIT,
-                       AT>),
+                       AT, MS>),
       grid, dim3(64 * WM * WN), 0, (hipStream_t)a.stream, (const T *)a.a, a.b,
       (OutT *)a.c, (const f16 *)a.scale, (int)a.m, (int)a.n, (int)a.k, a.lda,
       a.ldb, a.ldc, store_mode, k_split, stream_k ? a.sk_steps : 0,
@@ -898,19 +912,21 @@ static hipError_t launch_fast(const MatmulArgs &a) {
 }
 
 #define IHP_FAST_CONFIG(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST)           \
-  IHP_FAST_CONFIG_X(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, false, false)
+  IHP_FAST_CONFIG_X(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, false, false, 32)
+#define IHP_FAST_CONFIG_16(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST)        \
+  IHP_FAST_CONFIG_X(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, false, false, 16)
 #define IHP_FAST_CONFIG_S(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, SPLIT)  \
-  IHP_FAST_CONFIG_X(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, SPLIT, false)
+  IHP_FAST_CONFIG_X(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, SPLIT, false, 32)
 #define IHP_FAST_CONFIG_AT(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST)        \
-  IHP_FAST_CONFIG_X(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, false, true)
+  IHP_FAST_CONFIG_X(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, false, true, 32)
 #define IHP_FAST_CONFIG_X(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, SPLIT,  \
-                          AT)                                                 \
+                          AT, MS)                                             \
   {NAME,                                                                      \
    MODE,                                                                      \
    SPLIT,                                                                     \
    AT,                                                                        \
    (const void *)&gemm_lds_kernel<T, OUT, BM, BN, BKB, WM, WN, ST, MODE,      \
-                                  SPLIT, AT>,                                 \
+                                  SPLIT, AT, MS>,                             \
    sizeof(T) == 1 ? kElemI8 : kElemF16,                                       \
    sizeof(OUT) == 4 && sizeof(T) == 2,                                        \
    BM,                                                                        \
@@ -921,7 +937,8 @@ static hipError_t launch_fast(const MatmulArgs &a) {
    ST * (BM * BKB + (MODE == kBTN ? BN * BKB                                  \
                                   : (BKB / (int)sizeof(T)) * BN *             \
                                         (MODE == kBW8 ? 1 : (int)sizeof(T)))),\
-   &launch_fast<T, OUT, BM, BN, BKB, WM, WN, ST, MODE, SPLIT, AT>}
+   &launch_fast<T, OUT, BM, BN, BKB, WM, WN, ST, MODE, SPLIT, AT, MS>,      \
+   MS}
 
 // Every compiled fast-path configuration. The planner picks among these by
 // its LDS-budget ranking or a measured table entry; bench.py --tune times
@@ -940,6 +957,13 @@ static const FastConfig kFastConfigs[] = {
     IHP_FAST_CONFIG("f16_tn_128x128x64_w2x2_s4", kBTN, f16, f16, 128, 128, 128, 2, 2, 4),
     IHP_FAST_CONFIG("f16f32_tn_256x256x64_w2x4_s2", kBTN, f16, float, 256, 256, 128, 2, 4, 2),
     IHP_FAST_CONFIG("f16f32_tn_128x128x64_w2x2_s4", kBTN, f16, float, 128, 128, 128, 2, 2, 4),
+    // 16x16 MFMA forms of the TN macro-tiles
+    IHP_FAST_CONFIG_16("i8_tn_256x256x128_w2x4_s2_m16", kBTN, int8_t, int32_t, 256, 256, 128, 2, 4, 2),
+    IHP_FAST_CONFIG_16("i8_tn_256x128x128_w2x4_s2_m16", kBTN, int8_t, int32_t, 256, 128, 128, 2, 4, 2),
+    IHP_FAST_CONFIG_16("f16_tn_256x256x64_w2x4_s2_m16", kBTN, f16, f16, 256, 256, 128, 2, 4, 2),
+    IHP_FAST_CONFIG_16("f16_tn_256x128x64_w2x4_s2_m16", kBTN, f16, f16, 256, 128, 128, 2, 4, 2),
+    IHP_FAST_CONFIG_16("f16_tn_128x128x64_w2x2_s4_m16", kBTN, f16, f16, 128, 128, 128, 2, 2, 4),
+    IHP_FAST_CONFIG_16("f16f32_tn_256x256x64_w2x4_s2_m16", kBTN, f16, float, 256, 256, 128, 2, 4, 2),
     IHP_FAST_CONFIG("f16_nn_256x256x64_w2x4_s2", kBNN16, f16, f16, 256, 256, 128, 2, 4, 2),
     IHP_FAST_CONFIG("f16_nn_256x256x64_w2x2_s2", kBNN16, f16, f16, 256, 256, 128, 2, 2, 2),
     IHP_FAST_CONFIG("f16_nn_256x128x64_w2x4_s2", kBNN16, f16, f16, 256, 128, 128, 2, 4, 2),

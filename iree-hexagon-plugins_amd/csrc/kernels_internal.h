@@ -140,6 +140,7 @@ struct FastConfig {
   int stages;    // LDS ring depth
   int lds_bytes; // static LDS per workgroup
   FastLaunchFn launch;
+  int mfma;      // MFMA shape: 32 (32x32) or 16 (16x16)
 };
 
 const FastConfig *fast_configs(int *count);

@@ -32,17 +32,19 @@ struct TunedEntry {
 };
 // Measured on MI355X with random inputs (bench.py --tune): the 8-wave
 // 256x256 tile wins for int8 and f16 (two waves per SIMD hide each other's
-// stage hand-off waits; int8 2098 against 1930 TOPS for the 4-wave tile).
+// stage hand-off waits; int8 2098 against 1930 TOPS for the 4-wave tile),
+// in its 16x16 MFMA form (int8 61.6 against 65.1 us, f16 109.9 against
+// 115.2 us on one box).
 const TunedEntry kTuned[] = {
     {IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_I32, 4096, 4096,
      4096,
-     IREE_MI355X_MATMUL_B_TRANSPOSED, "i8_tn_256x256x128_w2x4_s2", 0},
+     IREE_MI355X_MATMUL_B_TRANSPOSED, "i8_tn_256x256x128_w2x4_s2_m16", 0},
     {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 4096,
-     4096, 4096, IREE_MI355X_MATMUL_B_TRANSPOSED, "f16_tn_256x256x64_w2x4_s2",
-     0},
+     4096, 4096, IREE_MI355X_MATMUL_B_TRANSPOSED,
+     "f16_tn_256x256x64_w2x4_s2_m16", 0},
     {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F32, 4096,
      4096, 4096, IREE_MI355X_MATMUL_B_TRANSPOSED,
-     "f16f32_tn_256x256x64_w2x4_s2", 0},
+     "f16f32_tn_256x256x64_w2x4_s2_m16", 0},
     // Skinny shapes where the model's pick measured slower than a sweep of
     // every tile and split count (random inputs, rotating weights).
     {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 16,
@@ -159,6 +161,9 @@ struct Candidate {
 // about three quarters of its 8 TB/s peak.
 constexpr double kMacsPerCuNsF16 = 2048.0 * 2.4;  // 4096 flop/clk
 constexpr double kMacsPerCuNsI8 = 4096.0 * 2.4;   // 8192 op/clk
+// The 16x16 MFMAs sustain this much more on random operands (the
+// calibration loop: 1.145x int8, 1.112x f16).
+constexpr double kMfma16Speedup = 1.1;
 constexpr double kFeedBytesPerNs = 16000.0;
 constexpr double kHbmBytesPerNs = 6000.0;
 // Fixed latencies: each round of workgroups (one per CU) pays the pipeline
@@ -218,8 +223,10 @@ bool evaluate_stream_k(const iree_mi355x_matmul_desc_t &d, const FastConfig &c,
   r.workspace = layers > 1 ? (int64_t)split_counter_bytes(tiles) +
                                  layers * d.m * d.n * 4
                            : 0;
+  // stream-K runs fill every CU (its configurations are 32x32 MFMAs)
   const double macs_per_ns =
-      d.a_elem == IREE_MI355X_ELEM_I8 ? kMacsPerCuNsI8 : kMacsPerCuNsF16;
+      (d.a_elem == IREE_MI355X_ELEM_I8 ? kMacsPerCuNsI8 : kMacsPerCuNsF16) *
+      (c.mfma == 16 ? kMfma16Speedup : 1.0);
   double t = (double)r.critical / macs_per_ns;
   const double t_feed = (double)r.traffic / kFeedBytesPerNs;
   const double t_hbm =
@@ -308,8 +315,12 @@ bool evaluate(const iree_mi355x_matmul_desc_t &d, const FastConfig &c,
   }
   // time = the slowest of MFMA work on the busiest CU, the operand feed, and
   // HBM (each operand and C once, plus split partials written and read)
+  // The 16x16 rate only where the tiles fill every CU: the feed term is a
+  // whole-chip aggregate, which a half-empty grid does not reach.
+  const bool full = tiles * splits * batch >= cus;
   const double macs_per_ns =
-      d.a_elem == IREE_MI355X_ELEM_I8 ? kMacsPerCuNsI8 : kMacsPerCuNsF16;
+      (d.a_elem == IREE_MI355X_ELEM_I8 ? kMacsPerCuNsI8 : kMacsPerCuNsF16) *
+      (c.mfma == 16 && full ? kMfma16Speedup : 1.0);
   const double t_mfma = (double)r.critical / macs_per_ns;
   const double t_feed = (double)r.traffic / kFeedBytesPerNs;
   const double hbm = (double)(batch * (ab * d.m * d.k + bb * d.n * d.k +
