@@ -562,6 +562,77 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
       return;
     }
   }
+  // Full tiles, plain or written-through stores: each wave stages its
+  // WTM x WTN tile through its share of the idle LDS ring and stores whole
+  // 16-byte row chunks, a quarter of the store instructions of one store
+  // per accumulator element (issuing those took 4-7 us of the int8 4096^3
+  // kernel) and full row segments. 16-byte chunks are XOR-swizzled by row,
+  // so the fragment writes (16 lanes per row) and the chunk reads are
+  // conflict free. Needs a 16-byte aligned C and row pitch; otherwise, and
+  // when accumulating (one rounding of C_init + acc), the per-element
+  // stores below run.
+  if constexpr (!SPLIT && MS * WTN * sizeof(OutT) <=
+                              STAGES * STAGE_BYTES / (WM * WN)) {
+    constexpr int OB = (int)sizeof(OutT);
+    constexpr int ROWB = WTN * OB;  // bytes of one wave-tile row
+    constexpr int NCH = ROWB / 16;  // 16-byte chunks per row
+    constexpr int SHARE = STAGES * STAGE_BYTES / (WM * WN);
+    // fragment rows per band: the most that divide FM and fit the share
+    constexpr int BAND = [] {
+      int f = FM;
+      while (f > 1 && (f * MS * ROWB > SHARE || FM % f != 0))
+        --f;
+      return f;
+    }();
+    static_assert(NCH >= 1 && (NCH & (NCH - 1)) == 0, "row chunks");
+    if (store_mode != kStoreAccumulate && (uintptr_t)C % 16 == 0 &&
+        ((int64_t)ldc * OB) % 16 == 0) {
+      __syncthreads();  // every wave is done reading the ring
+      char *ws = smem + wave * SHARE;
+      const int64_t grow0 = m0 + wm * WTM, gcol0 = n0 + wn * WTN;
+#pragma unroll
+      for (int b = 0; b < FM; b += BAND) {
+#pragma unroll
+        for (int i = b; i < b + BAND; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) {
+            float sc = 1.0f;
+            if constexpr (BMODE == kBW8)
+              sc = (float)scale[gcol0 + j * MS + col_l];
+#pragma unroll
+            for (int r = 0; r < AR; ++r) {
+              const int row = (i - b) * MS + row_l + frow(r);
+              const int byte = (j * MS + col_l) * OB;
+              const int off = row * ROWB +
+                              (((byte >> 4) ^ (row & (NCH - 1))) << 4) +
+                              (byte & 15);
+              if constexpr (kIntOut) {
+                *(OutT *)(ws + off) = acc[i][j][r];
+              } else {
+                float v = (float)acc[i][j][r];
+                if constexpr (BMODE == kBW8)
+                  v *= sc;
+                *(OutT *)(ws + off) = (OutT)v;
+              }
+            }
+          }
+        for (int t = lane; t < BAND * MS * NCH; t += 64) {
+          const int row = t / NCH, ch = t % NCH;
+          const i32x4 v = *(const i32x4 *)(
+              ws + row * ROWB + ((ch ^ (row & (NCH - 1))) << 4));
+          char *dst = (char *)(C + (grow0 + b * MS + row) * ldc + gcol0) +
+                      ch * 16;
+          if (store_mode == kStoreThrough)
+            asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(dst),
+                         "v"(v)
+                         : "memory");
+          else
+            *(i32x4 *)dst = v;
+        }
+      }
+      return;
+    }
+  }
   // One split (a ragged-M shape whose tiles alone cover the CUs): store
   // directly, rows past M masked, no partials.
   if (!SPLIT || parts == 1) {
@@ -940,18 +1011,18 @@ static hipError_t launch_fast(const MatmulArgs &a) {
    &launch_fast<T, OUT, BM, BN, BKB, WM, WN, ST, MODE, SPLIT, AT, MS>,      \
    MS}
 
-// Every compiled fast-path configuration. The planner picks among these by
+// Every compiled fast-path configuration (none spills registers: the
+// 4-wave 256x256 tiles, 128 x 128 per wave, did and were dropped). The
+// planner picks among these by
 // its LDS-budget ranking or a measured table entry; bench.py --tune times
 // them. Names: <types>_<b form>_<BM>x<BN>x<BK in elements>_w<wave grid>_s<LDS
 // stages>.
 static const FastConfig kFastConfigs[] = {
-    IHP_FAST_CONFIG("i8_tn_256x256x128_w2x2_s2", kBTN, int8_t, int32_t, 256, 256, 128, 2, 2, 2),
     IHP_FAST_CONFIG("i8_tn_256x256x128_w2x4_s2", kBTN, int8_t, int32_t, 256, 256, 128, 2, 4, 2),
     IHP_FAST_CONFIG("i8_tn_256x256x64_w2x4_s4", kBTN, int8_t, int32_t, 256, 256, 64, 2, 4, 4),
     IHP_FAST_CONFIG("i8_tn_256x128x128_w2x4_s2", kBTN, int8_t, int32_t, 256, 128, 128, 2, 4, 2),
     IHP_FAST_CONFIG("i8_tn_128x128x128_w2x2_s4", kBTN, int8_t, int32_t, 128, 128, 128, 2, 2, 4),
     IHP_FAST_CONFIG("f16_tn_256x256x64_w2x4_s2", kBTN, f16, f16, 256, 256, 128, 2, 4, 2),
-    IHP_FAST_CONFIG("f16_tn_256x256x64_w2x2_s2", kBTN, f16, f16, 256, 256, 128, 2, 2, 2),
     IHP_FAST_CONFIG("f16_tn_256x256x32_w2x4_s4", kBTN, f16, f16, 256, 256, 64, 2, 4, 4),
     IHP_FAST_CONFIG("f16_tn_256x128x64_w2x4_s2", kBTN, f16, f16, 256, 128, 128, 2, 4, 2),
     IHP_FAST_CONFIG("f16_tn_128x128x64_w2x2_s4", kBTN, f16, f16, 128, 128, 128, 2, 2, 4),
@@ -965,7 +1036,6 @@ static const FastConfig kFastConfigs[] = {
     IHP_FAST_CONFIG_16("f16_tn_128x128x64_w2x2_s4_m16", kBTN, f16, f16, 128, 128, 128, 2, 2, 4),
     IHP_FAST_CONFIG_16("f16f32_tn_256x256x64_w2x4_s2_m16", kBTN, f16, float, 256, 256, 128, 2, 4, 2),
     IHP_FAST_CONFIG("f16_nn_256x256x64_w2x4_s2", kBNN16, f16, f16, 256, 256, 128, 2, 4, 2),
-    IHP_FAST_CONFIG("f16_nn_256x256x64_w2x2_s2", kBNN16, f16, f16, 256, 256, 128, 2, 2, 2),
     IHP_FAST_CONFIG("f16_nn_256x128x64_w2x4_s2", kBNN16, f16, f16, 256, 128, 128, 2, 4, 2),
     IHP_FAST_CONFIG("f16_nn_128x128x64_w2x2_s4", kBNN16, f16, f16, 128, 128, 128, 2, 2, 4),
     IHP_FAST_CONFIG("f16f32_nn_256x256x64_w2x4_s2", kBNN16, f16, float, 256, 256, 128, 2, 4, 2),
