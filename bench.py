@@ -17,7 +17,9 @@ calibration kernels: a register-only MFMA loop on random operands (the
 each with the C oracle timed beside it on this host.
 --only <workload> runs one workload for profiler passes; --only stream and
 --only mfma_ceiling print the calibration ceilings alone.
---tune times every compiled MFMA macro-tile on the 4096^3 shapes.
+--tune times every compiled MFMA macro-tile on the 4096^3 shapes;
+--tune --tune-counters profiles each one under rocprofv3 (SQ counters per
+wave: MFMA busy fraction, waits, LDS and VALU instructions).
 """
 from __future__ import annotations
 
@@ -58,8 +60,15 @@ def parse():
                    help="time eager launches instead of one captured graph")
     p.add_argument("--only", choices=["i8", "f16", "f16nn", "gemv", "attn",
                                       "w8a16", "w8a16_gemm", "runtime",
-                                      "stream", "mfma_ceiling"],
+                                      "stream", "mfma_ceiling", "config"],
                    help="run one workload (for rocprof passes) and exit")
+    p.add_argument("--config", default=None,
+                   help="with --only config: the MFMA configuration to run")
+    p.add_argument("--shape", default="4096,4096,4096",
+                   help="with --only config: M,N,K")
+    p.add_argument("--tune-counters", action="store_true",
+                   help="with --tune: profile every candidate on the 4096^3 "
+                        "shapes under rocprofv3 (SQ counters per wave)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="with --only: first copy 256 MiB device-to-device "
                         "once, the known-size reference for FETCH_SIZE / "
@@ -663,7 +672,10 @@ def only(pkg, inputs, dev, args):
                     "unit": "TOPS" if kind == "i8" else "TFLOP/s",
                     "frac_peak": round(v / peak, 4)}), flush=True)
         return
-    if w == "i8":
+    if w == "config":
+        fn = config_step(pkg, dev, args.config,
+                         [int(x) for x in args.shape.split(",")])
+    elif w == "i8":
         a, bt = (t.to(dev) for t in inputs.c2_matmul_i8())
         c = torch.empty(4096, 4096, dtype=torch.int32, device=dev)
         fn = lambda: pkg.matmul(a, bt, c, b_transposed=True)  # noqa: E731
@@ -728,6 +740,110 @@ def only(pkg, inputs, dev, args):
                       "steps": args.steps}), flush=True)
 
 
+def config_step(pkg, dev, name, shape):
+    """One launch of MFMA configuration `name` on random operands of
+    shape (M, N, K) in the layout the configuration reads."""
+    import torch
+    cfg = next(c for c in pkg.mfma_configs() if c.name == name)
+    m, n, k = shape
+    g = torch.Generator().manual_seed(0)
+    sc = None
+    if cfg.a_elem == pkg.ELEM_I8:
+        a = torch.randint(-128, 128, (m, k), generator=g).to(torch.int8)
+        b = torch.randint(-128, 128, (n, k), generator=g).to(torch.int8)
+        c = torch.empty(m, n, dtype=torch.int32, device=dev)
+    else:
+        a = torch.randn(*((k, m) if cfg.a_transposed else (m, k)),
+                        generator=g).half()
+        if cfg.b_form == pkg.B_FORM_TN:
+            b = torch.randn(n, k, generator=g).half()
+        elif cfg.b_form == pkg.B_FORM_NN:
+            b = torch.randn(k, n, generator=g).half()
+        else:
+            b = torch.randint(-128, 128, (k, n), generator=g).to(torch.int8)
+            sc = (torch.rand(n, generator=g) * 0.019 + 0.001).half().to(dev)
+        c = torch.empty(m, n, dtype=torch.float32 if cfg.c_elem == pkg.ELEM_F32
+                        else torch.float16, device=dev)
+    a, b = a.to(dev), b.to(dev)
+    return lambda: pkg.matmul_mfma_config(cfg.index, a, b, c, scale=sc)
+
+
+# SQ counters one rocprofv3 pass can hold (at most 8 SQ counters), and what
+# the tuner reads from them per wave.
+TUNE_COUNTERS = ("SQ_WAVES", "SQ_BUSY_CYCLES", "SQ_WAVE_CYCLES",
+                 "SQ_WAIT_ANY", "SQ_INSTS_MFMA", "SQ_VALU_MFMA_BUSY_CYCLES",
+                 "SQ_INSTS_LDS", "SQ_INSTS_VALU")
+
+
+def _find(root, name):
+    for d, _, files in os.walk(root):
+        if name in files:
+            yield os.path.join(d, name)
+
+
+def tune_counters(pkg, args):
+    """Every 4096^3 macro-tile candidate under rocprofv3, one child process
+    each: the kernel's median duration and, per wave, MFMA, LDS and VALU
+    instructions, the fraction of a wave's life spent waiting, and the MFMA
+    pipe's busy fraction. SQ counters come summed over the 32 shader
+    engines (8 XCDs x 4), each of 32 SIMDs; wave and wait cycles are in
+    quad-cycles, so their ratio is unit-free."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        print(json.dumps({"error": "rocprofv3 not found"}))
+        return
+    work = tempfile.mkdtemp(prefix="tune_counters_")
+    for cfg in pkg.mfma_configs():
+        if "_sk" in cfg.name or cfg.tile_m < 128:
+            continue  # split-K tiles are tuned on the skinny shapes
+        out = os.path.join(work, cfg.name)
+        cmd = ["timeout", "-s", "KILL", "90", prof, "--pmc", *TUNE_COUNTERS,
+               "--kernel-trace", "-d", out, "-o", "p", "--output-format", "csv",
+               "--", sys.executable, os.path.join(ROOT, "bench.py"), "--only",
+               "config", "--config", cfg.name, "--no-graph", "--steps", "20",
+               "--warmup", "200", "--no-cpu-baseline"]
+        r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                           cwd="/tmp", env={**os.environ, "TMPDIR": "/tmp"})
+        if r.returncode != 0:
+            print(json.dumps({"config": cfg.name, "error": r.returncode}),
+                  flush=True)
+            if r.returncode in (124, 137, 134, 139):
+                break  # a killed or crashed profiler run ends the sweep
+            continue
+        sums, durs = {}, []
+        for path in _find(out, "p_counter_collection.csv"):
+            for row in csv.DictReader(open(path)):
+                if "gemm_lds_kernel" in row["Kernel_Name"]:
+                    sums.setdefault(row["Counter_Name"], []).append(
+                        float(row["Counter_Value"]))
+        for path in _find(out, "p_kernel_trace.csv"):
+            for row in csv.DictReader(open(path)):
+                if "gemm_lds_kernel" in row["Kernel_Name"]:
+                    durs.append(int(row["End_Timestamp"]) -
+                                int(row["Start_Timestamp"]))
+        if not sums:
+            continue
+        avg = {k: sum(v) / len(v) for k, v in sums.items()}
+        waves = avg.get("SQ_WAVES", 0.0) or 1.0
+        busy = avg.get("SQ_BUSY_CYCLES", 0.0) or 1.0
+        durs.sort()
+        print(json.dumps({
+            "config": cfg.name,
+            "us_median": round(durs[len(durs) // 2] / 1000, 2) if durs else None,
+            "mfma_per_wave": round(avg.get("SQ_INSTS_MFMA", 0) / waves),
+            "lds_insts_per_wave": round(avg.get("SQ_INSTS_LDS", 0) / waves),
+            "valu_per_wave": round(avg.get("SQ_INSTS_VALU", 0) / waves),
+            "wait_frac": round(avg.get("SQ_WAIT_ANY", 0) /
+                               (avg.get("SQ_WAVE_CYCLES", 0) or 1), 3),
+            "mfma_busy_frac": round(avg.get("SQ_VALU_MFMA_BUSY_CYCLES", 0) /
+                                    (busy * 32), 3)}), flush=True)
+    shutil.rmtree(work, ignore_errors=True)
+
+
 def tune_skinny(pkg, dev, args):
     """Every eligible tile at every split count (1..16) and in stream-K runs
     on the skinny C3 / C5 shapes and two tile counts stream-K is planned
@@ -790,6 +906,8 @@ def tune(pkg, inputs, dev, args):
     import torch
     if args.tune_skinny:
         return tune_skinny(pkg, dev, args)
+    if args.tune_counters:
+        return tune_counters(pkg, args)
     m = n = k = 4096
     g = torch.Generator().manual_seed(0)
     a8 = torch.randint(-128, 128, (m, k), generator=g).to(torch.int8).to(dev)

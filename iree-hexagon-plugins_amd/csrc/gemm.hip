@@ -1033,7 +1033,6 @@ static const FastConfig kFastConfigs[] = {
     IHP_FAST_CONFIG_16("i8_tn_256x128x128_w2x4_s2_m16", kBTN, int8_t, int32_t, 256, 128, 128, 2, 4, 2),
     IHP_FAST_CONFIG_16("f16_tn_256x256x64_w2x4_s2_m16", kBTN, f16, f16, 256, 256, 128, 2, 4, 2),
     IHP_FAST_CONFIG_16("f16_tn_256x128x64_w2x4_s2_m16", kBTN, f16, f16, 256, 128, 128, 2, 4, 2),
-    IHP_FAST_CONFIG_16("f16_tn_128x128x64_w2x2_s4_m16", kBTN, f16, f16, 128, 128, 128, 2, 2, 4),
     IHP_FAST_CONFIG_16("f16f32_tn_256x256x64_w2x4_s2_m16", kBTN, f16, float, 256, 256, 128, 2, 4, 2),
     IHP_FAST_CONFIG("f16_nn_256x256x64_w2x4_s2", kBNN16, f16, f16, 256, 256, 128, 2, 4, 2),
     IHP_FAST_CONFIG("f16_nn_256x128x64_w2x4_s2", kBNN16, f16, f16, 256, 128, 128, 2, 4, 2),
