@@ -19,8 +19,13 @@
 //    (rounded to f16) and V^T read transposed from key-major LDS
 //    (ds_read_b64_tr_b16);
 //  * K and V blocks stream HBM -> LDS (global_load_lds) into per-group
-//    rings; S^T of the next block is computed on MFMA under the softmax of
-//    the current one;
+//    rings;
+//  * each wave alternates an M phase (PV of one block and S^T of the next:
+//    MFMA and LDS reads only) and a V phase (that block's softmax: VALU),
+//    one phase per workgroup barrier; group 1 runs one phase behind group 0,
+//    and wave w (group 0) shares its SIMD with wave w + 4 (group 1), so one
+//    wave of each SIMD feeds the matrix core while the other works on the
+//    VALU;
 //  * causal blocks above the diagonal are skipped, the diagonal blocks are
 //    masked, and the grid runs the heaviest query blocks first.
 #include <type_traits>
@@ -36,9 +41,12 @@ constexpr int kBKV = 64;   // keys per block
 constexpr int kGroups = 2;  // wave groups, each taking every other key block
 constexpr int kThreads = 256 * kGroups;
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 // Lazy running max: tolerated growth of a row's max (log2 units) before the
 // reference max moves and the output is rescaled.
 constexpr float kLazyMax = 8.0f;
+// K fragment reads in flight ahead of the S^T MFMA that takes them.
+constexpr int kKReadAhead = 3;
 
 template <int N, int I = 0, typename F>
 __device__ __forceinline__ void static_for(F &&f) {
@@ -89,8 +97,8 @@ __device__ __forceinline__ float pair_sum(float x) {
 }
 }  // namespace
 
-// K and V blocks are copied HBM -> LDS with global_load_lds into a two-slot
-// ring (block kb+1 streams in while block kb is computed). Both are stored
+// K and V blocks are copied HBM -> LDS with global_load_lds into two-slot
+// rings (a block streams in while the one before is computed). Both are stored
 // key-major as in HBM, 16-byte chunks XOR-swizzled on the copy side:
 //  * K rows are read by ds_read_b128, 16 lanes = 16 consecutive keys at one
 //    chunk: chunk ^ (key & 15) for 256-byte rows (D = 128),
@@ -152,17 +160,20 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
   const int64_t q_off = (int64_t)plane * seq_q * D;
   const int64_t kv_off = (int64_t)plane * seq_kv * D;
 
-  // Per query block: this wave's first row, this group's
-  // key blocks (local block i is key block 2 i + grp) and the steps of the
-  // longer group (group 0), which both groups' barriers follow.
-  int q0 = 0, n_mine = 0, n_steps = 0;
+  // Per query block: this wave's first row, this group's key blocks (local
+  // block i is key block 2 i + grp) and the barrier slots of the block's
+  // phase schedule. A group with n blocks runs 2 n + 1 phases (M, V, M, ...,
+  // M) and group 1 starts one slot after group 0, so the schedule takes
+  // 2 n0 + 1 slots, one more when group 1 has as many blocks as group 0.
+  int q0 = 0, n_mine = 0, n_slots = 0;
   auto setup = [&](int item) {
     const int qb = item == 0 ? q_blocks - 1 - pair : pair;
     q0 = qb * kBQ + wq * 32;
     const int kv_end = causal ? min(qb * kBQ + kBQ, seq_kv) : seq_kv;
     const int n_blocks = (kv_end + kBKV - 1) / kBKV;
     n_mine = (n_blocks - grp + 1) >> 1;
-    n_steps = (n_blocks + 1) >> 1;
+    const int n0 = (n_blocks + 1) >> 1, n1 = n_blocks >> 1;
+    n_slots = 2 * n0 + 1 + (n1 == n0 ? 1 : 0);
   };
 
   // Q fragments (B operand of S^T = K Q^T): lane holds query q0 + l32, d chunk
@@ -200,8 +211,32 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
                        dst + (p * 4 + wq) * ROWS_PER_INSN * ROW);
     }
   };
+  // Full key blocks take the saddr copy form: the lane's byte offset inside
+  // a block (its row and swizzled chunk) is the same for every block and
+  // pass (the swizzles repeat every 16 rows, a pass moves 4 * ROWS_PER_INSN
+  // rows), so it is computed once, and each copy adds only wave-uniform
+  // terms in SGPRs (the block's and the pass's rows): no vector instruction
+  // per copy. A tail block (keys past seq_kv, clamped per lane) takes
+  // copy_block.
+  const int f_row = wq * ROWS_PER_INSN + c_row;
+  const uint32_t k_voff =
+      (uint32_t)(f_row * ROW + 16 * (c_phys ^ k_swizzle<D>(f_row)));
+  const uint32_t v_voff =
+      (uint32_t)(f_row * ROW + 16 * (c_phys ^ v_swizzle<D>(f_row)));
+  auto copy_full = [&](const f16 *src, int kb, IHP_LDS char *dst,
+                       uint32_t voff) {
+    const char *base = (const char *)(src + kv_off) + (int64_t)kb * BLK;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p)
+      global_to_lds_16s(base + p * 4 * ROWS_PER_INSN * ROW, voff,
+                        dst + (p * 4 + wq) * ROWS_PER_INSN * ROW);
+  };
   auto copy_k = [&](int i) {
-    copy_block(K, 2 * i + grp, lds + (i & 1) * BLK, std::false_type());
+    const int kb = 2 * i + grp;
+    if ((kb + 1) * kBKV <= seq_kv)
+      copy_full(K, kb, lds + (i & 1) * BLK, k_voff);
+    else
+      copy_block(K, kb, lds + (i & 1) * BLK, std::false_type());
   };
   // The query block's rows into the V slots 1 (all 8 waves, PASSES
   // instructions each); rows past seq_q are clamped to the last row (their
@@ -221,7 +256,11 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
     }
   };
   auto copy_v = [&](int i) {
-    copy_block(V, 2 * i + grp, lds + (2 + (i & 1)) * BLK, std::true_type());
+    const int kb = 2 * i + grp;
+    if ((kb + 1) * kBKV <= seq_kv)
+      copy_full(V, kb, lds + (2 + (i & 1)) * BLK, v_voff);
+    else
+      copy_block(V, kb, lds + (2 + (i & 1)) * BLK, std::true_type());
   };
   // A query block's first key blocks (slots 0); K(1) goes out separately,
   // last, and the block's first barrier does not wait for it.
@@ -254,6 +293,10 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
   // c ^ w = 2 (s ^ w/2) + (g ^ w%2), so every step's address is one base
   // XOR 32 s (the key * ROW part has no bits below ROW).
   // S^T tiles of local block i: keys 32t..32t+31 x this wave's 32 queries.
+  // Read r = 2 s + t feeds MFMA r; reads run KW ahead of their MFMA in KW + 1
+  // rotating registers (read r + KW lands in the registers MFMA r - 1 took),
+  // so an MFMA waits for a read issued KW MFMAs earlier instead of for the
+  // LDS latency of one issued just before it.
   auto scores = [&](int i, f32x16 (&st)[2]) {
     const IHP_LDS char *ks = lds + (i & 1) * BLK;
     // Recomputed from an opaque copy of the lane id at each call, instead
@@ -263,55 +306,41 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
     const int kl = ln & 31, kg = ln >> 5;
     const int k_sw = k_swizzle<D>(kl);
     const int kaddr = kl * ROW + 16 * (kg ^ (k_sw & 1)) + 32 * (k_sw >> 1);
-#pragma unroll
-    for (int s = 0; s < DS; ++s)
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const i32x4 kf = *(const IHP_LDS i32x4 *)(ks + (kaddr ^ (32 * s)) +
-                                                  32 * t * ROW);
-        // The first step accumulates onto an inline zero.
-        st[t] = Mfma32<f16>::mma(kf, qf[s], s == 0 ? f32x16{} : st[t]);
-      }
+    constexpr int NR = 2 * DS, KW = kKReadAhead, NB = KW + 1;
+    i32x4 kb[NB];
+    auto issue = [&](auto r_c) {
+      constexpr int R = decltype(r_c)::value;
+      kb[R % NB] = lds_read_16_async<32 * (R % 2) * ROW>(
+          ks + (kaddr ^ (32 * (R / 2))));
+    };
+    static_for<KW>(issue);
+    static_for<NR>([&](auto r_c) {
+      constexpr int R = decltype(r_c)::value;
+      constexpr int S = R / 2, T = R % 2;
+      // Reads issued so far: min(NR, R + KW); read R is done when at most
+      // the ones after it are outstanding.
+      constexpr int AHEAD = (R + KW < NR ? R + KW : NR) - R - 1;
+      lgkm_wait<AHEAD>();
+      lgkm_tie(kb[R % NB]);
+      // The first step accumulates onto an inline zero.
+      st[T] = Mfma32<f16>::mma(kb[R % NB], qf[S], S == 0 ? f32x16{} : st[T]);
+      if constexpr (R + KW < NR)
+        issue(std::integral_constant<int, R + KW>());
+    });
   };
-  // Mask (causal diagonal, sequence tail) and row max of local block i, in
-  // the log2 domain. Off the diagonal the max is taken on the raw scores
-  // (scale_log2 > 0 keeps the order) and the scale goes into the exponent's
-  // FMA (*sc); masked blocks are scaled in place (*sc = 1).
-  auto mask_max = [&](int i, f32x16 (&st)[2], float &mx, float &sc) {
-    const int kv0 = (2 * i + grp) * kBKV;
-    const bool need_mask =
-        (causal && kv0 + kBKV - 1 > q0) || kv0 + kBKV > seq_kv;
-    mx = -INFINITY;
-    if (need_mask || scale_log2 <= 0.0f) {
-      // Element (t, r) holds key kv0 + 4 g + c, c = 32 t + 8 (r / 4) + r % 4;
-      // keys at or past min(seq_kv, q0 + l32 + 1) (causal) are masked, i.e.
-      // c >= thr: one compare against a constant and one select each.
-      // (Lane terms recomputed from an opaque lane id: not kept live.)
-      int ln = lane;
-      asm volatile("" : "+v"(ln));
-      const int row = q0 + (ln & 31);
-      const int lim = causal ? min(seq_kv, row + 1) : seq_kv;
-      const int thr = lim - kv0 - 4 * (ln >> 5);
+  // Max of a lane's 32 scores as 4 independent chains of 8 (the V phase
+  // runs alone on its wave: a single 32-long chain would be latency-bound),
+  // each seeded with -inf.
+  auto row_max = [](const f32x16 (&st)[2]) {
+    float m[4];
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+    for (int c = 0; c < 4; ++c) {
+      m[c] = -INFINITY;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int c = 32 * t + 8 * (r >> 2) + (r & 3);
-          const float s = c >= thr ? -INFINITY : st[t][r] * scale_log2;
-          st[t][r] = s;
-          mx = fmaxf(mx, s);
-        }
-      sc = 1.0f;
-    } else {
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          mx = fmaxf(mx, st[t][r]);
-      mx *= scale_log2;
-      sc = scale_log2;
+      for (int e = 0; e < 8; ++e)
+        m[c] = fmaxf(m[c], st[c >> 1][8 * (c & 1) + e]);
     }
-    mx = pair_max(mx);
+    return fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3]));
   };
 
   // Group 0's O^T tile of this wave, normalised to f16, into the staged
@@ -347,6 +376,161 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
 
   f32x16 o[DT];
   float m_run = -INFINITY, l_run = 0.0f;
+  // S^T of the block being scored (M phase) and turned into probabilities
+  // (V phase); P of the block awaiting its PV, as f16 pairs: word w of
+  // fragment st holds keys 16 st + 2 w, + 1.
+  f32x16 st[2];
+  i32x4 pw[4];
+
+  // O^T[d][q] += V^T[d][key] P^T[key][q] for local block i, 16 keys per
+  // MFMA. V^T fragments of key step ST in buffer ST % 2: the reads of step
+  // ST + 1 are issued before the MFMAs of step ST, which wait only for their
+  // own 2 DT reads.
+  auto pv = [&](int i) {
+    const IHP_LDS char *vs = lds + (2 + (i & 1)) * BLK;
+    i32x2 vr[2][DT][2];
+    auto read_v = [&](auto step_c) {
+      constexpr int ST = decltype(step_c)::value;
+      constexpr int KOFF = 16 * ST * ROW;
+      static_for<DT>([&](auto dt) {
+        constexpr int DTI = decltype(dt)::value;
+        vr[ST % 2][DTI][0] = lds_read_tr16_at<KOFF>(vs + v_off[DTI]);
+        vr[ST % 2][DTI][1] = lds_read_tr16_at<KOFF + 8 * ROW>(vs + v_off[DTI]);
+      });
+    };
+    read_v(std::integral_constant<int, 0>());
+    static_for<4>([&](auto step_c) {
+      constexpr int ST = decltype(step_c)::value;
+      if constexpr (ST < 3)
+        read_v(std::integral_constant<int, ST + 1>());
+      lgkm_wait<ST < 3 ? 2 * DT : 0>();
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        tie2(vr[ST % 2][dt][0]);
+        tie2(vr[ST % 2][dt][1]);
+        const i32x4 vf = i32x4{vr[ST % 2][dt][0][0], vr[ST % 2][dt][0][1],
+                               vr[ST % 2][dt][1][0], vr[ST % 2][dt][1][1]};
+        o[dt] = Mfma32<f16>::mma(vf, pw[ST], o[dt]);
+      }
+    });
+  };
+
+  // M phase: PV of block k - 1 (when DO_PV), then S^T of block k (when
+  // DO_S); MFMA and LDS reads only, at raised wave priority so its MFMAs
+  // issue ahead of the other group's VALU work on the same SIMD.
+  float alpha = 1.0f;     // output rescale pending from the V phase
+  bool rescale = false;   // wave-uniform
+  auto m_phase = [&](int k, auto do_pv, auto do_s) {
+    __builtin_amdgcn_s_setprio(1);
+    if constexpr (decltype(do_pv)::value) {
+      if (rescale) {
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            o[t][r] *= alpha;
+        rescale = false;
+      }
+      pv(k - 1);
+    }
+    if constexpr (decltype(do_s)::value)
+      scores(k, st);
+    __builtin_amdgcn_s_setprio(0);
+  };
+
+  // Block k's softmax. Off the diagonal the row max is taken on the raw
+  // scores (scale_log2 > 0 keeps the order) and the scale goes into the
+  // exponent's FMA; masked blocks (causal diagonal, sequence tail) are
+  // masked and scaled in place first. Two instances (MASKED true / false)
+  // so that neither path merges S^T values with the other.
+  auto softmax = [&](int k, auto masked_c) {
+    constexpr bool MASKED = decltype(masked_c)::value;
+    float mx, sc;
+    if constexpr (MASKED) {
+      // Element (t, r) holds key kv0 + 4 g + c, c = 32 t + 8 (r / 4) + r % 4;
+      // keys at or past min(seq_kv, q0 + l32 + 1) (causal) are masked, i.e.
+      // c >= thr: one compare against a constant and one select each.
+      const int kv0 = (2 * k + grp) * kBKV;
+      const int row = q0 + l32;
+      const int lim = causal ? min(seq_kv, row + 1) : seq_kv;
+      const int thr = lim - kv0 - 4 * g;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int c = 32 * t + 8 * (r >> 2) + (r & 3);
+          st[t][r] = c >= thr ? -INFINITY : st[t][r] * scale_log2;
+        }
+      mx = row_max(st);
+      sc = 1.0f;
+    } else {
+      mx = row_max(st) * scale_log2;
+      sc = scale_log2;
+    }
+    mx = pair_max(mx);
+    alpha = 1.0f;
+    if (!__all(mx <= m_run + kLazyMax)) {
+      const float m_new = fmaxf(m_run, mx);
+      // A row with every key masked so far keeps m = -inf; exp2 of a
+      // finite offset from it must not produce nan.
+      alpha =
+          __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.0f : m_new));
+      m_run = m_new;
+      // O is rescaled by the next M phase, before PV(k) adds to it.
+      rescale = true;
+    }
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+    // Probabilities rounded to f16 pairs; the row sum adds the rounded
+    // pairs (v_dot2 with (1, 1)) in 4 independent chains, one per P
+    // fragment, so the normaliser sums exactly the values PV multiplies.
+    float psum[4];
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      psum[f] = 0.0f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float p0 = __builtin_amdgcn_exp2f(
+            __builtin_fmaf(st[f >> 1][8 * (f & 1) + 2 * w], sc, -m_use));
+        const float p1 = __builtin_amdgcn_exp2f(
+            __builtin_fmaf(st[f >> 1][8 * (f & 1) + 2 * w + 1], sc, -m_use));
+        const f16x2 h = __builtin_convertvector(f32x2{p0, p1}, f16x2);
+        psum[f] = __builtin_amdgcn_fdot2(h, f16x2{1, 1}, psum[f], false);
+        pw[f][w] = __builtin_bit_cast(int, h);
+      }
+    }
+    l_run = l_run * alpha +
+            pair_sum((psum[0] + psum[1]) + (psum[2] + psum[3]));
+  };
+
+  // V phase k (k = 0 .. n_mine - 1): the copies of K(k + 2) into the K slot
+  // S(k) was read from and of V(k + 1) into the V slot PV(k - 1) was read
+  // from (both read in the M phase before, which every wave of the group
+  // has finished), then block k's softmax. The reference max m_run moves
+  // only when some row's block max exceeds it by more than kLazyMax (log2
+  // units), so probabilities stay at most 2^kLazyMax (exact in f16) and most
+  // blocks skip the output rescale (done by the M phase after, whose PV
+  // adds the first terms relative to the new reference). Ends by waiting
+  // for this wave's copies of K(k + 1) and V(k), which the next M phase
+  // reads (the ones issued here may stay in flight).
+  auto v_phase = [&](int k) {
+    const bool next_k = k + 2 < n_mine, next_v = k + 1 < n_mine;
+    if (next_k)
+      copy_k(k + 2);
+    if (next_v)
+      copy_v(k + 1);
+    const int kv0 = (2 * k + grp) * kBKV;
+    if ((causal && kv0 + kBKV - 1 > q0) || kv0 + kBKV > seq_kv ||
+        scale_log2 <= 0.0f)
+      softmax(k, std::true_type());
+    else
+      softmax(k, std::false_type());
+    if (next_k)
+      wait_vmcnt<2 * PASSES>();
+    else if (next_v)
+      wait_vmcnt<PASSES>();
+    else
+      wait_vmcnt<0>();
+  };
 
   setup(0);
   copy_q();
@@ -354,18 +538,19 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
   if (n_mine > 1)
     copy_k(1);
   for (int item = 0;;) {
-    // Q, K(0), V(0) of this block (and the previous block's output
-    // stores) have completed in every wave. K(1), when issued, is each
-    // wave's newest memory operation and may stay in flight.
+    // Q, K(0) of this block (and the previous block's output stores) have
+    // completed in every wave; so has V(0), issued before Q. K(1), when
+    // issued, is each wave's newest memory operation and may stay in flight.
     if (n_mine > 1)
       wait_vmcnt<PASSES>();
     else
       wait_vmcnt<0>();
     block_barrier();
     {
-      // This wave's 32 query rows, read like K rows (conflict-free). The V
-      // slots 1 are overwritten only after step 0's barrier, which every
-      // wave reaches after consuming qf in S(0).
+      // This wave's 32 query rows, read like K rows (conflict-free). They
+      // have landed before the barrier below: group 0 overwrites its V slot
+      // 1 with V(1) in the slot after it, while group 1 may not yet have
+      // used its copy.
       const IHP_LDS char *qs = staged_row(wq * 32, 3);
       int ln = lane;
       asm volatile("" : "+v"(ln));
@@ -375,6 +560,7 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
 #pragma unroll
       for (int s = 0; s < DS; ++s)
         qf[s] = *(const IHP_LDS i32x4 *)(qs + (qaddr ^ (32 * s)));
+      wait_lgkmcnt0();
     }
 #pragma unroll
     for (int t = 0; t < DT; ++t)
@@ -384,107 +570,36 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
     m_run = -INFINITY;
     l_run = 0.0f;
 
-    // Pipeline over this group's key blocks: iteration j computes S(j+1) on
-    // MFMA while the VALU turns the first half of block j's scores into
-    // probabilities, then O += V(j) P(j) on MFMA while the VALU finishes
-    // block j's probabilities and masks S(j+1). K and V have rings of their
-    // own, one block apart: at the top of iteration j (after the barrier) K
-    // slot j%2 (read by S(j)) and V slot (j+1)%2 (read by PV(j-1)) are free
-    // and receive K(j+2), V(j+1). The last iteration computes a discarded S
-    // from a stale, in-bounds slot. Every wave passes n_steps barriers here.
-    if (n_mine > 0) {
-      f32x16 sa[2], sb[2];
-      float mx_a, sc_a, mx_b, sc_b;
-      scores(0, sa);
-      mask_max(0, sa, mx_a, sc_a);
-
-      auto step = [&](int j, f32x16 (&cur)[2], float mx_cur, float sc_cur,
-                      f32x16 (&nxt)[2], float &mx_nxt, float &sc_nxt) {
-        wait_vmcnt<0>();
+    // Phase schedule: M(0), V(0), M(1), ..., V(n - 1), M(n), one phase per
+    // barrier slot (M(k): PV(k - 1) and S(k); M(0) has no PV, M(n) no S).
+    // Group 1 starts one slot after group 0, so the two waves sharing a
+    // SIMD (w and w + 4) are always in opposite phases: one issues MFMAs
+    // while the other works on the VALU. Every wave passes n_slots
+    // barriers: the schedule's 2 n_mine + 1 (+ 1 for group 1), then padding.
+    {
+      int pad = n_slots;
+      if (n_mine > 0) {
+        if (grp == 1)
+          block_barrier();
+        m_phase(0, std::false_type(), std::true_type());
         block_barrier();
-        if (j + 2 < n_mine)
-          copy_k(j + 2);
-        if (j + 1 < n_mine)
-          copy_v(j + 1);
-        // Phase A: reference max and output rescale, S(j+1) on MFMA with
-        // the first 32 keys' probabilities on the VALU. The reference max
-        // m_run moves only when some row's block max exceeds it by more
-        // than kLazyMax (log2 units), so probabilities stay at most
-        // 2^kLazyMax (exact in f16) and most blocks skip the rescale.
-        float alpha = 1.0f;
-        if (!__all(mx_cur <= m_run + kLazyMax)) {
-          const float m_new = fmaxf(m_run, mx_cur);
-          // A row with every key masked so far keeps m = -inf; exp2 of a
-          // finite offset from it must not produce nan.
-          alpha = __builtin_amdgcn_exp2f(
-              m_run - (m_new == -INFINITY ? 0.0f : m_new));
-          m_run = m_new;
-#pragma unroll
-          for (int t = 0; t < DT; ++t)
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-              o[t][r] *= alpha;
+        for (int k = 0; k + 1 < n_mine; ++k) {
+          v_phase(k);
+          block_barrier();
+          m_phase(k + 1, std::true_type(), std::true_type());
+          block_barrier();
         }
-        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-        scores(j + 1, nxt);
-        float psum = 0.0f;
-        // P fragment of key step st (keys 16 st .. 16 st + 15 of block j).
-        auto probs = [&](int st) {
-          f16x8 pf;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(
-                cur[st >> 1][8 * (st & 1) + e], sc_cur, -m_use));
-            psum += p;
-            pf[e] = (f16)p;
-          }
-          return __builtin_bit_cast(i32x4, pf);
-        };
-        i32x4 pb0 = probs(0), pb1 = probs(1);
-        // Phase B: O^T[d][q] += V^T[d][key] P^T[key][q], 16 keys per MFMA,
-        // with the other 32 keys' probabilities and the mask / max of S(j+1)
-        // on the VALU.
-        const IHP_LDS char *vs = lds + (2 + (j & 1)) * BLK;
-        static_for<4>([&](auto step_c) {
-          constexpr int ST = decltype(step_c)::value;
-          constexpr int KOFF = 16 * ST * ROW;
-          i32x2 vr[DT][2];
-          static_for<DT>([&](auto dt) {
-            constexpr int DTI = decltype(dt)::value;
-            vr[DTI][0] = lds_read_tr16_at<KOFF>(vs + v_off[DTI]);
-            vr[DTI][1] = lds_read_tr16_at<KOFF + 8 * ROW>(vs + v_off[DTI]);
-          });
-          const i32x4 pcur = ST == 0 ? pb0 : ST == 1 ? pb1 : probs(ST);
-          lgkm_wait<0>();
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            tie2(vr[dt][0]);
-            tie2(vr[dt][1]);
-            const i32x4 vf = i32x4{vr[dt][0][0], vr[dt][0][1], vr[dt][1][0],
-                                   vr[dt][1][1]};
-            o[dt] = Mfma32<f16>::mma(vf, pcur, o[dt]);
-          }
-        });
-        l_run = l_run * alpha + pair_sum(psum);
-        mask_max(j + 1, nxt, mx_nxt, sc_nxt);
-      };
-
-      int j = 0;
-      while (true) {
-        step(j, sa, mx_a, sc_a, sb, mx_b, sc_b);
-        if (++j == n_mine)
-          break;
-        step(j, sb, mx_b, sc_b, sa, mx_a, sc_a);
-        if (++j == n_mine)
-          break;
+        v_phase(n_mine - 1);
+        block_barrier();
+        m_phase(n_mine, std::true_type(), std::false_type());
+        block_barrier();
+        pad -= grp + 2 * n_mine + 1;
       }
+      for (; pad > 0; --pad)
+        block_barrier();
     }
-    // Group 1 has one block fewer when the block count is odd: it meets
-    // group 0's last barrier here.
-    if (n_mine < n_steps)
-      block_barrier();
-    // Every ring slot is free once all waves pass this barrier.
-    block_barrier();
+    // After the last slot's barrier every wave has finished its phases:
+    // every ring slot is free.
     const int qrow0 = q0 - wq * 32;  // this block's first row
     const bool more = item + 1 < n_items;
     // The next block's first key blocks stream into slots 0 during the
