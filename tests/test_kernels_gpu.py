@@ -320,7 +320,9 @@ def test_c3_linear_transposed_weights_full(pkg, oracle, inputs, dev):
 
 @pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (1, 11008, 4096),
                                    (1, 4096, 11008), (2, 520, 1000),
-                                   (4, 4096, 4096), (3, 8, 7), (1, 1024, 1024)])
+                                   (4, 4096, 4096), (3, 8, 7), (1, 1024, 1024),
+                                   (1, 2048, 4096), (3, 2048, 1000),
+                                   (2, 11008, 4100), (4, 4096, 11008)])
 def test_gemv_f16(pkg, oracle, dev, m, n, k):
     g = torch.Generator().manual_seed(m * 7 + n + k)
     x = (torch.randn(m, k, generator=g) * 0.02).half()
