@@ -375,6 +375,9 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
   };
 
   f32x16 o[DT];
+  // l_run is this lane's share of the row sum (the keys its lane half
+  // holds) until the key loop ends; both halves share m_run, so they are
+  // rescaled alike, and one pair_sum then gives the row's sum.
   float m_run = -INFINITY, l_run = 0.0f;
   // S^T of the block being scored (M phase) and turned into probabilities
   // (V phase); P of the block awaiting its PV, as f16 pairs: word w of
@@ -385,8 +388,28 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
   // O^T[d][q] += V^T[d][key] P^T[key][q] for local block i, 16 keys per
   // MFMA. V^T fragments of key step ST in buffer ST % 2: the reads of step
   // ST + 1 are issued before the MFMAs of step ST, which wait only for their
-  // own 2 DT reads.
+  // own 2 DT reads. The row sum of P (the f16 values PV multiplies, added
+  // with v_dot2 against (1, 1)) is taken here, between the MFMAs, by the
+  // wave whose SIMD partner is then on the VALU softmax: it depends on P
+  // only, and l_run needs it only at the end of the key loop.
+  // P fragment f (keys 16 f .. 16 f + 15 of the block) from the scores:
+  // exp2(s * sc - m) rounded to f16 pairs; word w holds keys 16 f + 2 w, + 1.
+  // The block's reference max and score scale are kept from its V phase.
+  float m_pend = 0.0f, sc_pend = 1.0f;
+  auto probs = [&](auto f_c) {
+    constexpr int F = decltype(f_c)::value;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float p0 = __builtin_amdgcn_exp2f(
+          __builtin_fmaf(st[F >> 1][8 * (F & 1) + 2 * w], sc_pend, -m_pend));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(
+          st[F >> 1][8 * (F & 1) + 2 * w + 1], sc_pend, -m_pend));
+      const f16x2 h = __builtin_convertvector(f32x2{p0, p1}, f16x2);
+      pw[F][w] = __builtin_bit_cast(int, h);
+    }
+  };
   auto pv = [&](int i) {
+    float psum[4];
     const IHP_LDS char *vs = lds + (2 + (i & 1)) * BLK;
     i32x2 vr[2][DT][2];
     auto read_v = [&](auto step_c) {
@@ -412,7 +435,21 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
                                vr[ST % 2][dt][1][0], vr[ST % 2][dt][1][1]};
         o[dt] = Mfma32<f16>::mma(vf, pw[ST], o[dt]);
       }
+      // Keys 32 .. 63 of the block (score tile 1) become P here, while
+      // the MFMAs of steps 0 and 1 run; steps 2 and 3 take them.
+      if constexpr (ST < 2)
+        probs(std::integral_constant<int, ST + 2>());
+      psum[ST] = 0.0f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        // Copied out first: __builtin_bit_cast of a vector element
+        // expression reads element 0 whatever the index (hipcc 7.2).
+        const int word = pw[ST][w];
+        psum[ST] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, word),
+                                          f16x2{1, 1}, psum[ST], false);
+      }
     });
+    l_run += (psum[0] + psum[1]) + (psum[2] + psum[3]);
   };
 
   // M phase: PV of block k - 1 (when DO_PV), then S^T of block k (when
@@ -479,27 +516,14 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
       // O is rescaled by the next M phase, before PV(k) adds to it.
       rescale = true;
     }
-    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-    // Probabilities rounded to f16 pairs; the row sum adds the rounded
-    // pairs (v_dot2 with (1, 1)) in 4 independent chains, one per P
-    // fragment, so the normaliser sums exactly the values PV multiplies.
-    float psum[4];
-#pragma unroll
-    for (int f = 0; f < 4; ++f) {
-      psum[f] = 0.0f;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float p0 = __builtin_amdgcn_exp2f(
-            __builtin_fmaf(st[f >> 1][8 * (f & 1) + 2 * w], sc, -m_use));
-        const float p1 = __builtin_amdgcn_exp2f(
-            __builtin_fmaf(st[f >> 1][8 * (f & 1) + 2 * w + 1], sc, -m_use));
-        const f16x2 h = __builtin_convertvector(f32x2{p0, p1}, f16x2);
-        psum[f] = __builtin_amdgcn_fdot2(h, f16x2{1, 1}, psum[f], false);
-        pw[f][w] = __builtin_bit_cast(int, h);
-      }
-    }
-    l_run = l_run * alpha +
-            pair_sum((psum[0] + psum[1]) + (psum[2] + psum[3]));
+    m_pend = m_run == -INFINITY ? 0.0f : m_run;
+    sc_pend = sc;
+    // Probabilities of keys 0 .. 31 (score tile 0); keys 32 .. 63 are
+    // turned into P by the next PV, between its first MFMAs. Their row sum
+    // is also added there; the sum so far is rescaled here, before it.
+    probs(std::integral_constant<int, 0>());
+    probs(std::integral_constant<int, 1>());
+    l_run *= alpha;
   };
 
   // V phase k (k = 0 .. n_mine - 1): the copies of K(k + 2) into the K slot
@@ -599,7 +623,9 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
         block_barrier();
     }
     // After the last slot's barrier every wave has finished its phases:
-    // every ring slot is free.
+    // every ring slot is free. The two lane halves' shares of each row
+    // sum are added.
+    l_run = pair_sum(l_run);
     const int qrow0 = q0 - wq * 32;  // this block's first row
     const bool more = item + 1 < n_items;
     // The next block's first key blocks stream into slots 0 during the

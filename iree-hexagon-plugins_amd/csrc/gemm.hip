@@ -57,10 +57,14 @@ __device__ __forceinline__ int chunk_swizzle(int row) {
 // read (ds_read_b64_tr_b16 / _b8) makes each 16-lane block read 4 (f16) or 8
 // (int8) consecutive k rows at one 32- or 16-byte column window; XORing the
 // chunk index with a multiple of the row index spreads the rows of two
-// neighbouring blocks over all 64 banks.
-template <int BMODE>
+// neighbouring blocks over all 64 banks. For the 32x32 MFMA those two
+// blocks read the same rows at neighbouring windows; for the 16x16 MFMA they
+// read one window at rows 8 apart, so row bit 3 also flips a chunk bit
+// (the swizzle then repeats every 16 rows).
+template <int BMODE, int MS = 32>
 __device__ __forceinline__ int nn_swizzle(int k) {
-  return BMODE == kBNN16 ? 4 * (k & 3) : 2 * (k & 7);
+  const int hi = MS == 16 ? (k >> 3) & 1 : 0;
+  return BMODE == kBNN16 ? 4 * (k & 3) ^ 2 * hi : 2 * (k & 7) ^ hi;
 }
 
 // 8 int8 weights (two dwords) -> 8 f16, exact: each byte b becomes the f16
@@ -125,7 +129,9 @@ __device__ __forceinline__ void lgkm_tie2(i32x2 &v) {
 // on random operands the 16x16 instructions sustain 11-15 % more products
 // per second on this chip (the calibration loop: int8 4075 against 3559
 // TOPS, f16 1950 against 1754 TFLOP/s), the power per product being lower.
-// The 16x16 form takes TN B operands without a transposed A.
+// For row-major B and transposed A the 16x16 operand (16 columns x 8 k per
+// 16-lane block) comes from the same transposed reads, each block taking
+// k rows 8 b .. 8 b + 7 of the 32-row K step.
 template <typename T, typename OutT, int BM, int BN, int BKB, int WM, int WN,
           int STAGES, int BMODE, bool SPLIT, bool AT, int MS = 32>
 __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
@@ -136,7 +142,6 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     unsigned *__restrict__ counters, int64_t sa, int64_t sb, int64_t sc,
     Epi epi, int64_t s_mul) {
   static_assert(MS == 32 || MS == 16, "MFMA shape");
-  static_assert(MS == 32 || (BMODE == kBTN && !AT), "16x16: TN operands");
   typedef typename std::conditional<MS == 32, Mfma32<T>, Mfma16<T>>::type MF;
   typedef typename MF::Acc Acc;
   // Accumulator registers per fragment, K bytes per MFMA step and the
@@ -188,9 +193,18 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   // that period, so a lane's swizzle depends only on its row in the pass.
   static_assert(ROWS_PER_PASS % 16 == 0 && (16 / CH) * CH == 16, "swz");
   static_assert(!kNN || (BCH >= 16 && B_RPP % 8 == 0 && B_RPW <= 8), "nn");
+  // Copy passes start on the row swizzle's period (16 rows for 16x16).
+  static_assert(MS == 32 || ((!kNN || B_RPP % 16 == 0) &&
+                             (!AT || A_RPP % 16 == 0)),
+                "16x16 swizzle period");
+  // k rows of a staged row-major operand per MFMA K step
+  constexpr int KROWS = MS == 32 ? 16 : 32;
   static_assert(STAGES >= 2 && (STAGES - 2) * LOADS_PER_STAGE < 64,
                 "vmcnt range");
-  static_assert(RD < 16, "lgkmcnt range");
+  // Reads allowed in flight while the previous step's are collected. LDS
+  // reads return in issue order and lgkmcnt has 4 bits: with more than 15
+  // new reads the wait also takes the oldest of them (still correct).
+  constexpr int RDW = RD < 16 ? RD : 15;
   static_assert(STAGES * STAGE_BYTES <= 160 * 1024, "LDS budget");
 
   __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE_BYTES];
@@ -241,7 +255,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   if constexpr (AT) {
     // Same copy shape as row-major B: lane -> (k row, swizzled chunk).
     const int krow = wave * A_RPW + lane / ACH;
-    const int chunk = (lane % ACH) ^ nn_swizzle<kBNN16>(krow);
+    const int chunk = (lane % ACH) ^ nn_swizzle<kBNN16, MS>(krow);
 #pragma unroll
     for (int p = 0; p < A_PASSES; ++p)
       a_lane[p] = (uint32_t)((p * A_RPP + krow) * lda_b + chunk * 16);
@@ -261,7 +275,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   const char *b_base;
   if constexpr (kNN) {
     const int krow = wave * B_RPW + lane / BCH;
-    const int chunk = (lane % BCH) ^ nn_swizzle<BMODE>(krow);
+    const int chunk = (lane % BCH) ^ nn_swizzle<BMODE, MS>(krow);
     b_lane = (uint32_t)(krow * ldb_b + chunk * 16);
     b_base = (const char *)Bv + n0 * TBB + k_begin * ldb_b;
   } else {
@@ -324,10 +338,14 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     const int blk = lane >> 4, jj = lane & 15;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
-      const int k = 8 * (blk >> 1) + (jj >> 2);
-      const int byte = 2 * (wm * WTM + i * 32 + 16 * (blk & 1) + 4 * (jj & 3));
+      // 32x32: block reads k rows 8 (blk / 2) + jj / 4, columns 16 (blk % 2)
+      // + 4 (jj % 4) .. +3; 16x16: k rows 8 blk + jj / 4, columns 4 (jj % 4)
+      const int k = MS == 32 ? 8 * (blk >> 1) + (jj >> 2) : 8 * blk + (jj >> 2);
+      const int byte =
+          2 * (wm * WTM + i * MS + (MS == 32 ? 16 * (blk & 1) : 0) +
+               4 * (jj & 3));
       a_nn[i] = k * AROW +
-                (((byte >> 4) ^ nn_swizzle<kBNN16>(k)) << 4) + (byte & 15);
+                (((byte >> 4) ^ nn_swizzle<kBNN16, MS>(k)) << 4) + (byte & 15);
     }
   }
   // Read side, NN B: per-lane byte offset of fragment j within a stage for
@@ -337,20 +355,26 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
     const int blk = lane >> 4, jj = lane & 15;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
+      // 32x32: the block's k rows start at 8 (blk / 2), its columns at
+      // 16 (blk % 2); 16x16: k rows from 8 blk, all 16 columns.
+      const int krow0 = MS == 32 ? 8 * (blk >> 1) : 8 * blk;
+      const int col0 = wn * WTN + j * MS + (MS == 32 ? 16 * (blk & 1) : 0);
       if constexpr (BMODE == kBNN16) {
-        // block reads k rows 8*(blk/2) + jj/4 (+4), columns 16*(blk%2) +
-        // 4*(jj%4) .. +3 of the fragment
-        const int k = 8 * (blk >> 1) + (jj >> 2);
-        const int byte = 2 * (wn * WTN + j * 32 + 16 * (blk & 1) + 4 * (jj & 3));
+        // block reads k rows krow0 + jj/4 (+4), columns col0 + 4*(jj%4) ..
+        // +3
+        const int k = krow0 + (jj >> 2);
+        const int byte = 2 * (col0 + 4 * (jj & 3));
         b_nn[j] = A_BYTES + k * BROW +
-                  (((byte >> 4) ^ nn_swizzle<BMODE>(k)) << 4) + (byte & 15);
+                  (((byte >> 4) ^ nn_swizzle<BMODE, MS>(k)) << 4) +
+                  (byte & 15);
       } else {
-        // block reads k rows 8*(blk/2) + jj/2, columns 16*(blk%2) +
-        // 8*(jj%2) .. +7 of the fragment (bytes)
-        const int k = 8 * (blk >> 1) + (jj >> 1);
-        const int byte = wn * WTN + j * 32 + 16 * (blk & 1) + 8 * (jj & 1);
+        // block reads k rows krow0 + jj/2, columns col0 + 8*(jj%2) .. +7
+        // (bytes)
+        const int k = krow0 + (jj >> 1);
+        const int byte = col0 + 8 * (jj & 1);
         b_nn[j] = A_BYTES + k * BROW +
-                  (((byte >> 4) ^ nn_swizzle<BMODE>(k)) << 4) + (byte & 15);
+                  (((byte >> 4) ^ nn_swizzle<BMODE, MS>(k)) << 4) +
+                  (byte & 15);
       }
     }
   }
@@ -366,7 +390,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   auto read_frags = [&](int slot, int ks, Frags &f) {
     const IHP_LDS char *st = lds + slot * STAGE_BYTES;
     if constexpr (AT) {
-      const IHP_LDS char *pa = st + ks * 16 * AROW;
+      const IHP_LDS char *pa = st + ks * KROWS * AROW;
       static_for<FM>([&](auto i) {
         constexpr int I = decltype(i)::value;
         f.ta[2 * I] = lds_read_tr16_async<0>(pa + a_nn[I]);
@@ -384,7 +408,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
         f.b[j] = lds_read_16_async<decltype(j)::value * MS * BKB>(pb);
       });
     } else {
-      const IHP_LDS char *pb = st + ks * 16 * BROW;
+      const IHP_LDS char *pb = st + ks * KROWS * BROW;
       static_for<FN>([&](auto j) {
         constexpr int J = decltype(j)::value;
         if constexpr (BMODE == kBNN16) {
@@ -474,7 +498,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
       const int cur = ks & 1, nxt = cur ^ 1;
       if (ks + 1 < KSTEPS) {
         read_frags(slot, ks + 1, fr[nxt]);
-        frags_ready(std::integral_constant<int, RD>(), fr[cur]);
+        frags_ready(std::integral_constant<int, RDW>(), fr[cur]);
       } else if constexpr (decltype(handoff)::value) {
         // Stage handoff: this step's fragments are in registers (all LDS
         // reads done), stage kt+1 must have landed for every wave, and every
@@ -990,6 +1014,8 @@ static hipError_t launch_fast(const MatmulArgs &a) {
   IHP_FAST_CONFIG_X(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, SPLIT, false, 32)
 #define IHP_FAST_CONFIG_AT(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST)        \
   IHP_FAST_CONFIG_X(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, false, true, 32)
+#define IHP_FAST_CONFIG_AT16(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST)      \
+  IHP_FAST_CONFIG_X(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, false, true, 16)
 #define IHP_FAST_CONFIG_X(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, SPLIT,  \
                           AT, MS)                                             \
   {NAME,                                                                      \
@@ -1042,6 +1068,11 @@ static const FastConfig kFastConfigs[] = {
     IHP_FAST_CONFIG("w8a16_nn_256x256x64_w2x4_s3", kBW8, f16, f16, 256, 256, 128, 2, 4, 3),
     IHP_FAST_CONFIG("w8a16_nn_128x256x64_w2x4_s4", kBW8, f16, f16, 128, 256, 128, 2, 4, 4),
     IHP_FAST_CONFIG("w8a16_nn_128x256x64_w2x2_s4", kBW8, f16, f16, 128, 256, 128, 2, 2, 4),
+    // 16x16 MFMA forms of the row-major f16 B macro-tiles (the W8A16 ones
+    // measured 0-5 % slower than their 32x32 forms and are not built)
+    IHP_FAST_CONFIG_16("f16_nn_256x256x64_w2x4_s2_m16", kBNN16, f16, f16, 256, 256, 128, 2, 4, 2),
+    IHP_FAST_CONFIG_16("f16_nn_256x128x64_w2x4_s2_m16", kBNN16, f16, f16, 256, 128, 128, 2, 4, 2),
+    IHP_FAST_CONFIG_16("f16f32_nn_256x256x64_w2x4_s2_m16", kBNN16, f16, float, 256, 256, 128, 2, 4, 2),
     // split-K skinny tiles (M < tile rows allowed; partials in workspace)
     // (measured on M = 16..128 with N, K in {4096, 11008}: 32x128 beats
     // 32x256 / 64x256 at every point, 64x128 is best for some M = 64..128)
@@ -1061,6 +1092,8 @@ static const FastConfig kFastConfigs[] = {
     IHP_FAST_CONFIG_AT("f16at_tn_128x128x64_w2x2_s4", kBTN, f16, f16, 128, 128, 128, 2, 2, 4),
     IHP_FAST_CONFIG_AT("f16f32at_nn_128x128x64_w2x2_s4", kBNN16, f16, float, 128, 128, 128, 2, 2, 4),
     IHP_FAST_CONFIG_AT("f16f32at_tn_128x128x64_w2x2_s4", kBTN, f16, float, 128, 128, 128, 2, 2, 4),
+    IHP_FAST_CONFIG_AT16("f16at_nn_256x256x64_w2x4_s2_m16", kBNN16, f16, f16, 256, 256, 128, 2, 4, 2),
+    IHP_FAST_CONFIG_AT16("f16at_tn_256x256x64_w2x4_s2_m16", kBTN, f16, f16, 256, 256, 128, 2, 4, 2),
 };
 
 const FastConfig *fast_configs(int *count) {

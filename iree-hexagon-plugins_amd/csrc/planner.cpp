@@ -453,7 +453,7 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
     // the split count that just covers the CUs and at a range of others
     // (more splits spread the work, fewer shorten the reduction).
     if (best.index < 0) {
-      std::tuple<int64_t, int64_t, int64_t, int64_t> best_rank;
+      std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t> best_rank;
       // Stream-K is not ranked: measured against the split counts it won
       // only where K is long (the partial tiles it publishes cost more
       // than the model prices); measured entries above select it.
@@ -467,7 +467,13 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
           Candidate c;
           if (!evaluate(*d, cfgs[i], i, cus, &c, false, forced))
             continue;
-          auto rank = std::make_tuple(c.est_ns, c.traffic, c.tiles,
+          // Between equal modeled times (feed- or HBM-bound models) the
+          // 16x16 MFMA form comes first where its tiles fill every CU: it
+          // measured faster on every such f16 shape (4096^3 TN 6-8 %, C3
+          // M = 2048 row-major B 1-4.5 %, transposed A 1-2 %).
+          const int64_t wgs = c.tiles * c.splits * (d->batch > 0 ? d->batch : 1);
+          const int64_t mfma16 = cfgs[i].mfma == 16 && wgs >= cus ? 1 : 0;
+          auto rank = std::make_tuple(c.est_ns, -mfma16, c.traffic, c.tiles,
                                       -(int64_t)cfgs[i].bn);
           if (best.index < 0 || rank < best_rank) {
             best = c;

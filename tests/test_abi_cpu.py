@@ -132,6 +132,24 @@ def test_planner_ranking_prefers_least_traffic(pkg):
     assert p.workgroups == 256
 
 
+@pytest.mark.parametrize("m,n,k,flags,want", [
+    (2048, 4096, 4096, 0, b"f16_nn_256x128x64_w2x4_s2_m16"),
+    (2048, 11008, 4096, 0, b"f16_nn_256x256x64_w2x4_s2_m16"),
+    (2048, 4096, 11008, 0, b"f16_nn_256x128x64_w2x4_s2_m16"),
+    (4096, 4096, 4096, 0, b"f16_nn_256x256x64_w2x4_s2_m16"),
+    (4096, 4096, 4096, 8, b"f16at_nn_256x256x64_w2x4_s2_m16"),
+])
+def test_planner_prefers_16x16_on_full_grids(pkg, m, n, k, flags, want):
+    # Feed-bound f16 shapes whose tiles fill every CU: the 16x16 MFMA form
+    # of the tile measured faster than the 32x32 one (same modeled time)
+    p = pkg.plan(pkg.make_desc(F16, F16, F16, m, n, k, flags))
+    assert p.config_name == want and p.splits == 1
+    # a grid that leaves CUs idle keeps the 32x32 form
+    p = pkg.plan(pkg.make_desc(F16, I8, F16, 512, 11008, 4096, 0,
+                               has_scale=True))
+    assert not p.config_name.endswith(b"_m16")
+
+
 def test_mfma_config_table(pkg):
     cfgs = pkg.mfma_configs()
     assert len(cfgs) >= 8
