@@ -287,6 +287,16 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
     v_off[dt] = (4 * g + v_row_in) * ROW +
                 (((b0 >> 4) ^ v_swizzle<D>(v_row_in)) << 4) + (b0 & 15);
   }
+  // K read base of this lane in ring slot 0 (absolute LDS address). The
+  // group's ring is 64 KiB aligned and a d step's swizzle flips address
+  // bits 5-7 only, so each step's address is this base XOR 32 s.
+  uint32_t ka;
+  {
+    const int kl = lane & 31, kg = lane >> 5;
+    const int k_sw = k_swizzle<D>(kl);
+    ka = (uint32_t)(uintptr_t)lds +
+         (uint32_t)(kl * ROW + 16 * (kg ^ (k_sw & 1)) + 32 * (k_sw >> 1));
+  }
 
   // K read side: step s reads chunk c = 2s + g of key l32 (+32 for the
   // second key tile, which has the same swizzle). With w = k_swizzle(key),
@@ -298,20 +308,13 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
   // so an MFMA waits for a read issued KW MFMAs earlier instead of for the
   // LDS latency of one issued just before it.
   auto scores = [&](int i, f32x16 (&st)[2]) {
-    const IHP_LDS char *ks = lds + (i & 1) * BLK;
-    // Recomputed from an opaque copy of the lane id at each call, instead
-    // of keeping the base (or DS per-step addresses) live across the loop.
-    int ln = lane;
-    asm volatile("" : "+v"(ln));
-    const int kl = ln & 31, kg = ln >> 5;
-    const int k_sw = k_swizzle<D>(kl);
-    const int kaddr = kl * ROW + 16 * (kg ^ (k_sw & 1)) + 32 * (k_sw >> 1);
+    const uint32_t kbase = ka + (uint32_t)((i & 1) * BLK);
     constexpr int NR = 2 * DS, KW = kKReadAhead, NB = KW + 1;
     i32x4 kb[NB];
     auto issue = [&](auto r_c) {
       constexpr int R = decltype(r_c)::value;
       kb[R % NB] = lds_read_16_async<32 * (R % 2) * ROW>(
-          ks + (kaddr ^ (32 * (R / 2))));
+          (const IHP_LDS char *)(uintptr_t)(kbase ^ (32u * (R / 2))));
     };
     static_for<KW>(issue);
     static_for<NR>([&](auto r_c) {
@@ -392,22 +395,6 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
   // with v_dot2 against (1, 1)) is taken here, between the MFMAs, by the
   // wave whose SIMD partner is then on the VALU softmax: it depends on P
   // only, and l_run needs it only at the end of the key loop.
-  // P fragment f (keys 16 f .. 16 f + 15 of the block) from the scores:
-  // exp2(s * sc - m) rounded to f16 pairs; word w holds keys 16 f + 2 w, + 1.
-  // The block's reference max and score scale are kept from its V phase.
-  float m_pend = 0.0f, sc_pend = 1.0f;
-  auto probs = [&](auto f_c) {
-    constexpr int F = decltype(f_c)::value;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float p0 = __builtin_amdgcn_exp2f(
-          __builtin_fmaf(st[F >> 1][8 * (F & 1) + 2 * w], sc_pend, -m_pend));
-      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(
-          st[F >> 1][8 * (F & 1) + 2 * w + 1], sc_pend, -m_pend));
-      const f16x2 h = __builtin_convertvector(f32x2{p0, p1}, f16x2);
-      pw[F][w] = __builtin_bit_cast(int, h);
-    }
-  };
   auto pv = [&](int i) {
     float psum[4];
     const IHP_LDS char *vs = lds + (2 + (i & 1)) * BLK;
@@ -435,10 +422,6 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
                                vr[ST % 2][dt][1][0], vr[ST % 2][dt][1][1]};
         o[dt] = Mfma32<f16>::mma(vf, pw[ST], o[dt]);
       }
-      // Keys 32 .. 63 of the block (score tile 1) become P here, while
-      // the MFMAs of steps 0 and 1 run; steps 2 and 3 take them.
-      if constexpr (ST < 2)
-        probs(std::integral_constant<int, ST + 2>());
       psum[ST] = 0.0f;
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
@@ -516,13 +499,21 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
       // O is rescaled by the next M phase, before PV(k) adds to it.
       rescale = true;
     }
-    m_pend = m_run == -INFINITY ? 0.0f : m_run;
-    sc_pend = sc;
-    // Probabilities of keys 0 .. 31 (score tile 0); keys 32 .. 63 are
-    // turned into P by the next PV, between its first MFMAs. Their row sum
-    // is also added there; the sum so far is rescaled here, before it.
-    probs(std::integral_constant<int, 0>());
-    probs(std::integral_constant<int, 1>());
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+    // Probabilities rounded to f16 pairs. Their row sum is added by the
+    // next PV (which multiplies exactly these values); the sum so far is
+    // rescaled here, before it.
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float p0 = __builtin_amdgcn_exp2f(
+            __builtin_fmaf(st[f >> 1][8 * (f & 1) + 2 * w], sc, -m_use));
+        const float p1 = __builtin_amdgcn_exp2f(
+            __builtin_fmaf(st[f >> 1][8 * (f & 1) + 2 * w + 1], sc, -m_use));
+        const f16x2 h = __builtin_convertvector(f32x2{p0, p1}, f16x2);
+        pw[f][w] = __builtin_bit_cast(int, h);
+      }
     l_run *= alpha;
   };
 
