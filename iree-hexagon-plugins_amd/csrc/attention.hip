@@ -129,16 +129,18 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
   constexpr int PASSES = kBKV / (4 * ROWS_PER_INSN);  // per wave, per tensor
   static_assert(PASSES * 4 * ROWS_PER_INSN == kBKV, "copy shape");
   // Per wave group: K ring (slots 0, 1) then V ring (slots 0, 1). After both
-  // groups' rings: the (max, sum) pairs of the merge, one per (wave, lane).
+  // groups' rings: the (max, sum) pairs of the merge, one per (group, wave,
+  // lane).
   // Slot 1 of the rings also stages, between key loops, the query block's
   // rows (Q in the V slots, rows 0-63 in group 0's, 64-127 in group 1's),
   // the merge's O hand-over, and the block's output rows (the K slots).
   constexpr int RING = 4 * BLK;
-  constexpr int XML = 4 * 64 * 8;
+  constexpr int XML = kGroups * 4 * 64 * 8;
   __shared__ __attribute__((aligned(1024))) char smem[kGroups * RING + XML];
-  // The merge hands one wave's O (DT tiles of 16 floats per lane) through
-  // one ring slot.
-  static_assert(DT * 4 * 64 * 16 == BLK, "one wave's O fills one ring slot");
+  // The merge hands half of a wave's O each way (DT / 2 tiles of 16 floats
+  // per lane); both halves of a wave pair fill one ring slot.
+  static_assert(DT * 4 * 64 * 16 == BLK, "a wave's O fills one ring slot");
+  static_assert(DT % 2 == 0, "O tiles split between the groups");
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -346,15 +348,17 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
     return fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3]));
   };
 
-  // Group 0's O^T tile of this wave, normalised to f16, into the staged
-  // output rows (the K slots 1): 4 d of row 32 wq + l32 per register
-  // quarter, 16-byte chunk 4 dt + rq swizzled as K rows are, half g.
-  auto stage_o = [&](const f32x16 (&acc)[DT], float inv) {
+  // Half H of this wave's merged O^T tiles (d tiles H DT/2 .. H DT/2 +
+  // DT/2 - 1), normalised to f16, into the staged output rows (the K slots
+  // 1): 4 d of row 32 wq + l32 per register quarter, 16-byte chunk 4 dt + rq
+  // swizzled as K rows are, half g.
+  auto stage_o = [&](const f32x16 (&acc)[DT], float inv, auto half_c) {
+    constexpr int H = decltype(half_c)::value;
     const int r = wq * 32 + l32;
     IHP_LDS char *dst = staged_row(r, 1);
     const int sw = k_swizzle<D>(r);
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+    for (int dt = H * DT / 2; dt < (H + 1) * DT / 2; ++dt)
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
         f16x4 v;
@@ -626,48 +630,76 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
       copy_first();
     }
 
-    // Merge: group 1 hands (O, m, l) to group 0. Wave wq's O goes through
-    // ring slot 1 (K, then V) of group wq / 2: float4 k of tile dt at
-    // (dt 4 + k) 64 + lane; (m, l) after the rings at wq 64 + lane.
+    // Merge: each group hands the other the half of its O tiles the other
+    // keeps (group 1 its d tiles 0 .. DT/2 - 1, group 0 the rest) and its
+    // (m, l); both then merge their kept half with the same weights, in the
+    // same arithmetic order (group 0's term first), and stage it. Wave wq's
+    // halves go through ring slot 1 (K, then V) of group wq / 2: float4 k
+    // of tile dt at (dt 4 + k) 64 + lane; (m, l) after the rings at
+    // (grp 4 + wq) 64 + lane.
     IHP_LDS f32x4 *xo = (IHP_LDS f32x4 *)(smem + (wq >> 1) * RING +
                                           (1 + 2 * (wq & 1)) * BLK);
     IHP_LDS f32x2 *xml = (IHP_LDS f32x2 *)(smem + kGroups * RING);
-    if (grp == 1) {
+    auto hand = [&](auto half_c) {
+      constexpr int H = decltype(half_c)::value;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
+      for (int dt = H * DT / 2; dt < (H + 1) * DT / 2; ++dt)
 #pragma unroll
         for (int k = 0; k < 4; ++k)
           xo[(dt * 4 + k) * 64 + lane] =
               f32x4{o[dt][4 * k], o[dt][4 * k + 1], o[dt][4 * k + 2],
                     o[dt][4 * k + 3]};
-      xml[wq * 64 + lane] = f32x2{m_run, l_run};
-      wait_lgkmcnt0();
-    }
+    };
+    if (grp == 1)
+      hand(std::integral_constant<int, 0>());
+    else
+      hand(std::integral_constant<int, 1>());
+    xml[(grp * 4 + wq) * 64 + lane] = f32x2{m_run, l_run};
+    wait_lgkmcnt0();
     block_barrier();
-    if (grp == 0) {
-      const f32x2 ml = xml[wq * 64 + lane];
-      const float m = fmaxf(m_run, ml[0]);
+    {
+      const f32x2 ml = xml[((grp ^ 1) * 4 + wq) * 64 + lane];
+      const float m0 = grp == 0 ? m_run : ml[0];
+      const float m1 = grp == 0 ? ml[0] : m_run;
+      const float l0 = grp == 0 ? l_run : ml[1];
+      const float l1 = grp == 0 ? ml[1] : l_run;
+      const float m = fmaxf(m0, m1);
       const float m_use = m == -INFINITY ? 0.0f : m;
-      const float a0 = __builtin_amdgcn_exp2f(m_run - m_use);
-      const float a1 = __builtin_amdgcn_exp2f(ml[0] - m_use);
-      l_run = l_run * a0 + ml[1] * a1;
+      const float a0 = __builtin_amdgcn_exp2f(m0 - m_use);
+      const float a1 = __builtin_amdgcn_exp2f(m1 - m_use);
+      l_run = l0 * a0 + l1 * a1;
+      auto merge = [&](auto half_c) {
+        constexpr int H = decltype(half_c)::value;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
+        for (int dt = H * DT / 2; dt < (H + 1) * DT / 2; ++dt)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const f32x4 x = xo[(dt * 4 + k) * 64 + lane];
+          for (int k = 0; k < 4; ++k) {
+            const f32x4 x = xo[(dt * 4 + k) * 64 + lane];
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            o[dt][4 * k + e] = o[dt][4 * k + e] * a0 + x[e] * a1;
-        }
+            for (int e = 0; e < 4; ++e) {
+              const float own = o[dt][4 * k + e];
+              o[dt][4 * k + e] = H == 0 ? own * a0 + x[e] * a1
+                                        : x[e] * a0 + own * a1;
+            }
+          }
+      };
+      if (grp == 0)
+        merge(std::integral_constant<int, 0>());
+      else
+        merge(std::integral_constant<int, 1>());
     }
     // The slots 1 are free again: the next block's rows stream into the V
     // slots, this block's output rows are staged in the K slots.
     block_barrier();
     if (more)
       copy_q();
-    if (grp == 0)
-      stage_o(o, l_run > 0.0f ? 1.0f / l_run : 0.0f);
+    {
+      const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+      if (grp == 0)
+        stage_o(o, inv, std::integral_constant<int, 0>());
+      else
+        stage_o(o, inv, std::integral_constant<int, 1>());
+    }
     wait_lgkmcnt0();
     block_barrier();
     store_rows(qrow0);

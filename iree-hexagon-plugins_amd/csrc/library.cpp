@@ -276,7 +276,7 @@ const iree_mi355x_executable_dispatch_attrs_t kAttrs[] = {
     {IREE_MI355X_DISPATCH_FLAG_RESOURCES_VALID |
          IREE_MI355X_DISPATCH_FLAG_USES_MFMA |
          IREE_MI355X_DISPATCH_FLAG_USES_LDS_DMA,
-     133120, 512},
+     135168, 512},
     {kF16Flags, 131072, 512},
 };
 
