@@ -66,7 +66,6 @@ def _load():
     lib.oracle_choose_static_tiling_factor.argtypes = [i64, i64, i64]
     lib.oracle_select_hmx_tile_sizes.argtypes = [p, p, ctypes.c_int, i64,
                                                  ctypes.c_int, i64, i64, p]
-    lib.oracle_hmx_pack_f16.argtypes = [p, p] + [ctypes.c_uint32] * 5
     for name in ("oracle_matmul_f16", "oracle_matmul_i8", "oracle_w8a16",
                  "oracle_batch_matmul_f16",
                  "oracle_attention_f16", "oracle_select_hmx_tile_sizes"):
@@ -255,17 +254,6 @@ def select_hmx_tile_sizes(m, n, k, *, elem_bytes=(2, 2, 4), b_transposed=False,
         _ptr(ranges), _ptr(eb), int(b_transposed), budget_bytes,
         int(double_buffering), hmx_m, hmx_n, _ptr(out))
     return [int(t) for t in out] if ok else None
-
-
-def hmx_pack_f16(src, row_tiles=None, col_tiles=None, stride=None):
-    src = np.ascontiguousarray(src, np.float16)
-    rows, cols = src.shape
-    row_tiles = row_tiles or -(-rows // 32)
-    col_tiles = col_tiles or -(-cols // 32)
-    out = np.empty(row_tiles * col_tiles * 1024, np.float16)
-    _load().oracle_hmx_pack_f16(_ptr(out), _ptr(src), stride or cols, rows,
-                                cols, row_tiles, col_tiles)
-    return out
 
 
 def fp16_parity(y, ref) -> float:

@@ -595,21 +595,3 @@ int oracle_select_hmx_tile_sizes(const int64_t ranges[3],
   return found;
 }
 
-/* --------------------------------------------------------------- pack ---- */
-
-void oracle_hmx_pack_f16(uint16_t *dest, const uint16_t *src,
-                         uint32_t src_stride, uint32_t rows, uint32_t cols,
-                         uint32_t row_tiles, uint32_t col_tiles) {
-  const uint32_t tile = 32, tile_elems = 1024;
-  memset(dest, 0, (size_t)row_tiles * col_tiles * tile_elems * 2);
-  for (uint32_t r = 0; r < rows; ++r) {
-    for (uint32_t c = 0; c < cols; ++c) {
-      uint32_t rt = r / tile, ct = c / tile;
-      if (rt >= row_tiles || ct >= col_tiles)
-        continue;
-      uint32_t tr = r % tile, tc = c % tile;
-      dest[(rt * col_tiles + ct) * tile_elems + (tr / 2u) * 64u + 2u * tc +
-           (tr & 1u)] = src[(size_t)r * src_stride + c];
-    }
-  }
-}

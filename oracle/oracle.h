@@ -22,7 +22,6 @@
  *                         micro attention model) in f32, causal invariants
  *   select_hmx_tile_sizes reference lit goldens
  *   choose_static_tiling  brute-force divisor search
- *   hmx_pack              reference closed form on the UK test cases
  *   batch_matmul_f16      per-batch equality with matmul_f16; bias / ReLU /
  *                         GELU / SiLU against numpy closed forms; epilogue
  *                         order (bias before act, multiplier after)
@@ -141,12 +140,6 @@ int oracle_select_hmx_tile_sizes(const int64_t ranges[3],
                                  int64_t budget_flag_bytes,
                                  int double_buffering, int64_t hmx_m,
                                  int64_t hmx_n, int64_t tiles[3]);
-
-/* iree_hexagon_hmx_pack_f16 closed form (UK/test/test_support.c:194-215):
- * packed[tile][(r/2)*64 + 2c + (r&1)] = src[r][c], zero padded. */
-void oracle_hmx_pack_f16(uint16_t *dest, const uint16_t *src,
-                         uint32_t src_stride, uint32_t rows, uint32_t cols,
-                         uint32_t row_tiles, uint32_t col_tiles);
 
 #ifdef __cplusplus
 }

@@ -11,9 +11,7 @@ Nothing here imports or runs the reference. The fixtures are:
   * matmul_i8.npz   int8 x int8 with an int64 numpy product;
   * tile_search.json the VTCM tile-search goldens of
                     plugins/compiler/hexagon/test/codegen/strategy/
-                    hexagon_vtcm_planning_hmx.mlir, transcribed as data;
-  * hmx_pack.npz    the UK pack test cases (UK/test/pack_test.c:98-103) with
-                    the closed-form layout of UK/test/test_support.c:194-240.
+                    hexagon_vtcm_planning_hmx.mlir, transcribed as data.
 Run: python tests/golden/make_golden.py
 """
 import json
@@ -100,40 +98,9 @@ def write_tile_search():
                    "double_buffering": True, "cases": cases}, f, indent=1)
 
 
-def pack_closed_form(src, stride, rows, cols, row_tiles, col_tiles):
-    out = np.zeros(row_tiles * col_tiles * 1024, np.float16)
-    flat = src.reshape(-1)
-    for r in range(rows):
-        for c in range(cols):
-            t = (r // 32) * col_tiles + c // 32
-            tr, tc = r % 32, c % 32
-            out[t * 1024 + (tr // 2) * 64 + 2 * tc + (tr & 1)] = flat[r * stride + c]
-    return out
-
-
-def pack_source(rows, cols, stride):
-    # UK/test/pack_test.c:input_value; the stride padding holds a marker that
-    # must never reach the packed tiles.
-    src = np.full((rows, stride), 99.0, np.float16)
-    for r in range(rows):
-        for c in range(cols):
-            src[r, c] = np.float16(((r * 7 + c * 3) % 23 - 11) / 4.0)
-    return src
-
-
-def write_pack():
-    full = pack_source(32, 32, 32)
-    ragged = pack_source(35, 37, 41)
-    np.savez(os.path.join(HERE, "hmx_pack.npz"),
-             full_src=full, full_packed=pack_closed_form(full, 32, 32, 32, 1, 1),
-             ragged_src=ragged,
-             ragged_packed=pack_closed_form(ragged, 41, 35, 37, 3, 3))
-
-
 if __name__ == "__main__":
     write_matmuls()
     write_attention()
     write_i8()
     write_tile_search()
-    write_pack()
     print("wrote", sorted(os.listdir(HERE)))

@@ -280,19 +280,6 @@ def test_choose_static_tiling_factor_brute_force(oracle):
     assert oracle.choose_static_tiling_factor(oracle.DYNAMIC, 8, 1) == 8
 
 
-def test_hmx_pack_reference_cases(oracle):
-    d = np.load(os.path.join(GOLDEN, "hmx_pack.npz"))
-    got = oracle.hmx_pack_f16(d["full_src"], 1, 1, stride=32)
-    assert np.array_equal(got.view(np.uint16), d["full_packed"].view(np.uint16))
-    src = d["ragged_src"]
-    out = np.empty(9 * 1024, np.float16)
-    lib = oracle._load()
-    lib.oracle_hmx_pack_f16(out.ctypes.data, np.ascontiguousarray(src).ctypes.data,
-                            41, 35, 37, 3, 3)
-    assert np.array_equal(out.view(np.uint16), d["ragged_packed"].view(np.uint16))
-    assert not (out == 99).any()
-
-
 # ------------------------------------------------ batch matmul / epilogue ----
 
 def test_batch_matmul_equals_per_batch_matmul(oracle):
