@@ -131,6 +131,34 @@ int iree_mi355x_command_buffer_submit(
 uint32_t iree_mi355x_command_buffer_count(
     const iree_mi355x_command_buffer_t *command_buffer);
 
+// One stream operation of a submission's lane schedule, in issue order.
+// Lane 0 is the caller's stream, lanes 1.. the runtime's lane streams.
+// Event 0 is the fork event (recorded on the caller's stream first); event
+// 1 + l is lane l's event.
+typedef enum iree_mi355x_lane_op_kind_e {
+  IREE_MI355X_LANE_OP_RECORD = 0,   // record `event` on `lane`
+  IREE_MI355X_LANE_OP_WAIT = 1,     // `lane` waits for `event`
+  IREE_MI355X_LANE_OP_ENQUEUE = 2,  // command `command` on `lane`
+} iree_mi355x_lane_op_kind_t;
+typedef struct iree_mi355x_lane_op_t {
+  uint32_t kind;
+  uint32_t lane;
+  uint32_t event;
+  uint32_t command;
+} iree_mi355x_lane_op_t;
+
+// The lane schedule a submission with this concurrency issues (the same
+// rules as iree_mi355x_command_buffer_submit: commands of a barrier segment
+// dealt round-robin over the lanes, each lane's first command of a segment
+// after a wait on the previous segment's other lanes, the other lanes
+// joined back into the caller's stream at the end). Writes at most
+// `capacity` operations to `ops` and returns how many the schedule has; no
+// device is touched. The reference's DSP scheduler has no such query
+// (RT/dsp/command_buffer.c:807-913 schedules inside its submit).
+uint32_t iree_mi355x_command_buffer_lane_schedule(
+    const iree_mi355x_command_buffer_t *command_buffer,
+    uint32_t max_concurrent, iree_mi355x_lane_op_t *ops, uint32_t capacity);
+
 #ifdef __cplusplus
 }  // extern "C"
 #endif

@@ -69,6 +69,7 @@ EXPORTED_SYMBOLS = (
     "iree_mi355x_command_buffer_end",
     "iree_mi355x_command_buffer_workspace_bytes",
     "iree_mi355x_command_buffer_submit", "iree_mi355x_command_buffer_count",
+    "iree_mi355x_command_buffer_lane_schedule",
     "iree_mi355x_kernel_count", "iree_mi355x_kernel_resources",
     "iree_mi355x_executable_serialize", "iree_mi355x_executable_verify",
     "iree_mi355x_executable_load", "iree_mi355x_loaded_executable_library",
@@ -177,6 +178,15 @@ BINDING_DIRECT = 0xFFFFFFFF
 WHOLE_BUFFER = (1 << 64) - 1
 DEFAULT_CONCURRENCY = 1
 MAX_CONCURRENCY = 8
+
+
+class LaneOp(ctypes.Structure):
+    """iree_mi355x_lane_op_t: one stream operation of a lane schedule."""
+    _fields_ = [("kind", ctypes.c_uint32), ("lane", ctypes.c_uint32),
+                ("event", ctypes.c_uint32), ("command", ctypes.c_uint32)]
+
+
+LANE_OP_RECORD, LANE_OP_WAIT, LANE_OP_ENQUEUE = 0, 1, 2
 
 
 class BufferRef(ctypes.Structure):
@@ -324,6 +334,9 @@ def library():
     lib.iree_mi355x_command_buffer_workspace_bytes.restype = sz
     lib.iree_mi355x_command_buffer_submit.argtypes = [
         cbp, ctypes.POINTER(Binding), u32, u32, p, sz, p]
+    lib.iree_mi355x_command_buffer_lane_schedule.argtypes = [
+        cbp, u32, ctypes.POINTER(LaneOp), u32]
+    lib.iree_mi355x_command_buffer_lane_schedule.restype = u32
     lib.iree_mi355x_kernel_resources.argtypes = [ctypes.c_int,
                                                  ctypes.POINTER(KernelResources)]
     lib.iree_mi355x_executable_serialize.restype = sz
@@ -990,6 +1003,19 @@ class CommandBuffer:
         arr, n = binding_table(list(table))
         return self._lib.iree_mi355x_command_buffer_workspace_bytes(
             self._h, arr, n, max_concurrent)
+
+    def lane_schedule(self, max_concurrent=0) -> list[tuple]:
+        """The stream operations a submission at this concurrency issues,
+        in order: (kind, lane, event, command) with kind one of LANE_OP_*;
+        lane 0 is the caller's stream, event 0 the fork event and event
+        1 + l lane l's event. Host-only: no device is touched."""
+        n = self._lib.iree_mi355x_command_buffer_lane_schedule(
+            self._h, max_concurrent, None, 0)
+        ops = (LaneOp * max(n, 1))()
+        got = self._lib.iree_mi355x_command_buffer_lane_schedule(
+            self._h, max_concurrent, ops, n)
+        assert got == n
+        return [(o.kind, o.lane, o.event, o.command) for o in ops[:n]]
 
     def submit(self, table=(), max_concurrent=0, workspace=None, stream=None):
         arr, n = binding_table(list(table))

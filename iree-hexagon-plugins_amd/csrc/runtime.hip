@@ -272,6 +272,67 @@ uint32_t lanes_for(const iree_mi355x_command_buffer_t *cb, uint32_t requested) {
 
 size_t slice_bytes(size_t need) { return (need + 255) & ~(size_t)255; }
 
+// The stream operations of a concurrent submission, in issue order: fork
+// record on the caller's stream; per barrier segment, each lane's first
+// command after waits on the previous segment's events of the other lanes
+// (a lane's own earlier work is already ahead of it in stream order), then
+// one record per lane used; at the end, each other lane used records its
+// event and the caller's stream waits on it.
+std::vector<iree_mi355x_lane_op_t> lane_schedule(
+    const iree_mi355x_command_buffer_t *cb, uint32_t lanes) {
+  std::vector<iree_mi355x_lane_op_t> ops;
+  auto op = [&](uint32_t kind, uint32_t lane, uint32_t event,
+                uint32_t command) {
+    ops.push_back({kind, lane, event, command});
+  };
+  const uint32_t n = (uint32_t)cb->commands.size();
+  if (lanes <= 1) {
+    for (uint32_t j = 0; j < n; ++j)
+      if (cb->commands[j].kind != kBarrier)
+        op(IREE_MI355X_LANE_OP_ENQUEUE, 0, 0, j);
+    return ops;
+  }
+  struct Prior {
+    uint32_t event, lane;
+  };
+  std::vector<Prior> prior = {{0, 0}};
+  bool used_ever[IREE_MI355X_MAX_CONCURRENCY] = {};
+  op(IREE_MI355X_LANE_OP_RECORD, 0, 0, 0);
+  uint32_t i = 0;
+  while (i < n) {
+    uint32_t end = i;
+    while (end < n && cb->commands[end].kind != kBarrier)
+      ++end;
+    bool used[IREE_MI355X_MAX_CONCURRENCY] = {};
+    for (uint32_t j = i; j < end; ++j) {
+      const uint32_t l = (j - i) % lanes;
+      if (!used[l]) {
+        used[l] = used_ever[l] = true;
+        for (const Prior &e : prior)
+          if (e.lane != l)
+            op(IREE_MI355X_LANE_OP_WAIT, l, e.event, 0);
+      }
+      op(IREE_MI355X_LANE_OP_ENQUEUE, l, 0, j);
+    }
+    if (end > i) {
+      prior.clear();
+      for (uint32_t l = 0; l < lanes; ++l)
+        if (used[l]) {
+          op(IREE_MI355X_LANE_OP_RECORD, l, 1 + l, 0);
+          prior.push_back({1 + l, l});
+        }
+    }
+    i = end + 1;  // past the barrier
+  }
+  for (uint32_t l = 1; l < lanes; ++l) {
+    if (!used_ever[l])
+      continue;
+    op(IREE_MI355X_LANE_OP_RECORD, l, 1 + l, 0);
+    op(IREE_MI355X_LANE_OP_WAIT, 0, 1 + l, 0);
+  }
+  return ops;
+}
+
 // Per device: the lane streams and events (default priority, non-blocking,
 // kept for the process), the runtime's own workspace, and a lock that makes
 // submissions on one device enqueue one at a time.
@@ -520,6 +581,19 @@ uint32_t iree_mi355x_command_buffer_count(
   return cb ? (uint32_t)cb->commands.size() : 0;
 }
 
+uint32_t iree_mi355x_command_buffer_lane_schedule(
+    const iree_mi355x_command_buffer_t *cb, uint32_t max_concurrent,
+    iree_mi355x_lane_op_t *ops, uint32_t capacity) {
+  if (!cb || max_concurrent > IREE_MI355X_MAX_CONCURRENCY)
+    return 0;
+  const uint32_t lanes = lanes_for(
+      cb, max_concurrent ? max_concurrent : IREE_MI355X_DEFAULT_CONCURRENCY);
+  const std::vector<iree_mi355x_lane_op_t> s = lane_schedule(cb, lanes);
+  for (uint32_t i = 0; i < capacity && i < s.size(); ++i)
+    ops[i] = s[i];
+  return (uint32_t)s.size();
+}
+
 size_t iree_mi355x_command_buffer_workspace_bytes(
     const iree_mi355x_command_buffer_t *cb,
     const iree_mi355x_binding_t *binding_table, uint32_t binding_count,
@@ -607,64 +681,34 @@ int iree_mi355x_command_buffer_submit(
     return st;
   }
   // Lane 0 is the caller's stream itself, lanes 1.. the device's lane
-  // streams. Fork: every lane's first command of a segment waits for the
-  // events of the previous barrier (initially the caller's prior work); a
-  // lane does not wait for its own event, which stream order already covers.
+  // streams; event 0 is the fork event, 1 + l lane l's event.
   hipStream_t lane_stream[IREE_MI355X_MAX_CONCURRENCY];
   lane_stream[0] = caller;
   for (uint32_t l = 1; l < lanes; ++l)
     lane_stream[l] = d->streams[l - 1];
-  struct Prior {
-    hipEvent_t event;
-    uint32_t lane;
-  };
-  std::vector<Prior> prior = {{d->fork, 0}};
-  bool used_ever[IREE_MI355X_MAX_CONCURRENCY] = {};
-  st = hip_ok(hipEventRecord(d->fork, caller), "fork record");
-  uint32_t i = 0;
-  while (i < n && !st) {
-    uint32_t end = i;
-    while (end < n && cb->commands[end].kind != kBarrier)
-      ++end;
-    bool used[IREE_MI355X_MAX_CONCURRENCY] = {};
-    for (uint32_t j = i; j < end && !st; ++j) {
-      const uint32_t l = (j - i) % lanes;
-      if (!used[l]) {
-        used[l] = used_ever[l] = true;
-        for (const Prior &e : prior)
-          if (e.lane != l &&
-              (st = hip_ok(hipStreamWaitEvent(lane_stream[l], e.event, 0),
-                           "lane wait")))
-            break;
-      }
-      if (!st)
-        st = enqueue(cb, j, ready[j], lane_stream[l],
-                     slice ? ws + (size_t)l * slice : nullptr, slice);
+  auto event = [&](uint32_t e) { return e == 0 ? d->fork : d->lane_done[e - 1]; };
+  // After a failure the remaining records and waits still run (no more
+  // commands), so every lane is joined back into the caller's stream; the
+  // first error is returned.
+  for (const iree_mi355x_lane_op_t &o : lane_schedule(cb, lanes)) {
+    int r = IREE_MI355X_OK;
+    switch (o.kind) {
+      case IREE_MI355X_LANE_OP_RECORD:
+        r = hip_ok(hipEventRecord(event(o.event), lane_stream[o.lane]),
+                   "lane record");
+        break;
+      case IREE_MI355X_LANE_OP_WAIT:
+        r = hip_ok(hipStreamWaitEvent(lane_stream[o.lane], event(o.event), 0),
+                   "lane wait");
+        break;
+      default:
+        if (st)
+          continue;
+        r = enqueue(cb, o.command, ready[o.command], lane_stream[o.lane],
+                    slice ? ws + (size_t)o.lane * slice : nullptr, slice);
     }
-    if (end > i && !st) {
-      // Barrier (or the end): the next segment waits for this one's lanes.
-      prior.clear();
-      for (uint32_t l = 0; l < lanes && !st; ++l)
-        if (used[l]) {
-          st = hip_ok(hipEventRecord(d->lane_done[l], lane_stream[l]),
-                      "lane record");
-          prior.push_back({d->lane_done[l], l});
-        }
-    }
-    i = end + 1;  // past the barrier
-  }
-  // Join: the caller's stream (lane 0) waits for every other lane this
-  // submission used (each lane's last event covers its work).
-  for (uint32_t l = 1; l < lanes; ++l) {
-    if (!used_ever[l])
-      continue;
-    const int rs =
-        hip_ok(hipEventRecord(d->lane_done[l], lane_stream[l]), "join record");
-    const int ws2 = rs ? rs
-                       : hip_ok(hipStreamWaitEvent(caller, d->lane_done[l], 0),
-                                "join wait");
-    if (!st)
-      st = ws2;
+    if (r && !st)
+      st = r;
   }
   roctxRangePop();
   return st;

@@ -146,3 +146,113 @@ def test_workspace_query_through_export(pkg):
                             [FAKE, FAKE, FAKE], [4096, 4096, 10],
                             stream=0, query=True)
     assert st == pkg.INVALID_ARGUMENT
+
+
+# ------------------------------------------------------- lane schedule ----
+
+def happens_before(pkg, ops):
+    """Simulate a lane schedule: stream order within each lane plus
+    record -> wait edges. Returns, per enqueued command, the set of
+    commands that finish before it starts, and the set the caller's stream
+    (lane 0) has waited for at the end. A wait takes the event's latest
+    record at the time of the wait (the HIP / CUDA event semantics)."""
+    lane_done = {}   # lane -> commands ordered before the lane's next op
+    event_set = {}   # event -> commands covered by its latest record
+    before = {}
+    for kind, lane, event, command in ops:
+        done = lane_done.setdefault(lane, set())
+        if kind == pkg.LANE_OP_RECORD:
+            event_set[event] = set(done)
+        elif kind == pkg.LANE_OP_WAIT:
+            assert event in event_set, f"wait on event {event} before a record"
+            done |= event_set[event]
+        else:
+            assert command not in before, f"command {command} enqueued twice"
+            before[command] = set(done)
+            done.add(command)
+    return before, lane_done.get(0, set())
+
+
+def segments_of(pkg, kinds):
+    """Command index -> barrier segment, for a list of 'd' / 'b' kinds."""
+    seg, out = 0, {}
+    for i, k in enumerate(kinds):
+        if k == "b":
+            seg += 1
+        else:
+            out[i] = seg
+    return out
+
+
+def build(pkg, kinds):
+    cb = pkg.CommandBuffer()
+    for k in kinds:
+        if k == "b":
+            cb.barrier()
+        else:
+            cb.fill(pkg.slot(0), b"\x00\x00")
+    return cb.end()
+
+
+@pytest.mark.parametrize("kinds", [
+    "ddddd", "ddddbddbd", "dbdbdbd", "dddddddddbdd", "ddbbddd", "bdddb",
+    "d", "ddddddddddddddddd",
+])
+@pytest.mark.parametrize("lanes", [1, 2, 3, 4, 8])
+def test_lane_schedule_orders_segments_and_joins_every_lane(pkg, kinds, lanes):
+    """The schedule a submission issues (the same one submit executes):
+    every command runs after every command of the earlier barrier
+    segments; the caller's stream ends after every command (each lane
+    joined back); no lane waits on its own event; each command is enqueued
+    once; every wait follows a record of its event."""
+    cb = build(pkg, kinds)
+    ops = cb.lane_schedule(lanes)
+    seg = segments_of(pkg, kinds)
+    before, caller_end = happens_before(pkg, ops)
+    assert set(before) == set(seg)
+    for c, s in seg.items():
+        for p_, ps in seg.items():
+            if ps < s:
+                assert p_ in before[c], (kinds, lanes, p_, c)
+    assert caller_end | {c for c in seg
+                         if any(o[0] == pkg.LANE_OP_ENQUEUE and o[1] == 0
+                                and o[3] == c for o in ops)} >= set(seg)
+    # every lane's last command is ordered before the caller's end
+    last_on_lane = {}
+    for kind, lane, _, command in ops:
+        if kind == pkg.LANE_OP_ENQUEUE:
+            last_on_lane[lane] = command
+    for lane, c in last_on_lane.items():
+        assert lane == 0 or c in caller_end, (kinds, lanes, lane)
+    # no self-waits: a lane never waits on the event it records
+    for kind, lane, event, _ in ops:
+        if kind == pkg.LANE_OP_WAIT:
+            assert event != 1 + lane
+    # lanes used: the request, capped by the widest barrier segment; a
+    # single lane runs in order with no events
+    widest = max(len(r) for r in kinds.split("b"))
+    eff = max(1, min(lanes, widest))
+    used = {o[1] for o in ops if o[0] == pkg.LANE_OP_ENQUEUE}
+    assert used == set(range(eff))
+    if eff == 1:
+        assert all(o[0] == pkg.LANE_OP_ENQUEUE for o in ops)
+    else:
+        assert ops[0][:3] == (pkg.LANE_OP_RECORD, 0, 0)
+
+
+def test_lane_schedule_in_order_has_no_events(pkg):
+    cb = build(pkg, "ddbdd")
+    ops = cb.lane_schedule(1)
+    assert [o[0] for o in ops] == [pkg.LANE_OP_ENQUEUE] * 4
+    assert [o[3] for o in ops] == [0, 1, 3, 4] and {o[1] for o in ops} == {0}
+
+
+def test_lane_schedule_deals_round_robin(pkg):
+    # 5 commands on 4 lanes: lanes 0..3 then lane 0 again; the fork event
+    # is waited on by lanes 1..3 only
+    ops = build(pkg, "ddddd").lane_schedule(4)
+    enq = [(o[1], o[3]) for o in ops if o[0] == pkg.LANE_OP_ENQUEUE]
+    assert enq == [(0, 0), (1, 1), (2, 2), (3, 3), (0, 4)]
+    fork_waits = sorted(o[1] for o in ops
+                        if o[0] == pkg.LANE_OP_WAIT and o[2] == 0)
+    assert fork_waits == [1, 2, 3]
