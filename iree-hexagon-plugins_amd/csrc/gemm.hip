@@ -518,11 +518,27 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
       } else {
         frags_ready(std::integral_constant<int, 0>(), fr[cur]);
       }
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
+      // Issue order. With 16x16 fragments and FN >= 4 the A index runs
+      // innermost, boustrophedon, so the B operand changes once per FM
+      // MFMAs and not on every one (the two waves of a SIMD hold the same B
+      // fragments): fewer operand bits switch in the matrix core, which on
+      // random data runs power-limited. Measured 1.5-2 % faster on the
+      // 256x256 TN tiles, ~0.7 % slower on 256x128 NN (FN = 2).
+      if constexpr (MS == 16 && FN >= 4) {
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          acc[i][j] = MF::mma(fr[cur].a[i], fr[cur].b[j], acc[i][j]);
+#pragma unroll
+          for (int ii = 0; ii < FM; ++ii) {
+            const int i = (j & 1) ? FM - 1 - ii : ii;
+            acc[i][j] = MF::mma(fr[cur].a[i], fr[cur].b[j], acc[i][j]);
+          }
+      } else {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = MF::mma(fr[cur].a[i], fr[cur].b[j], acc[i][j]);
+      }
     }
   };
   using Yes = std::true_type;
