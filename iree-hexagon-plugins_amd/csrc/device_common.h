@@ -158,6 +158,18 @@ __device__ __forceinline__ void lgkm_tie(i32x4 &v) {
   asm volatile("" : "+v"(v));
 }
 
+// 16 bytes written through. The compiler's hazard pass does not see inline
+// asm as a store, and on gfx950 a VALU write to the data registers of a
+// store wider than 8 bytes needs two wait states after it: without the
+// s_nop the compiler may reuse those registers at once and the store then
+// writes the new values (seen as wrong, run-to-run varying C2 outputs in an
+// experimental build; the shipped schedule had the slots by chance).
+__device__ __forceinline__ void store_through16(void *p, i32x4 v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(p),
+               "v"(v)
+               : "memory");
+}
+
 // Device-scope (sc1) 32-bit store / load for data one workgroup publishes and
 // another, possibly on another XCD, reads within the same kernel: the store
 // is written through past this XCD's L2 and the load bypasses it. They are

@@ -205,6 +205,12 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   // reads return in issue order and lgkmcnt has 4 bits: with more than 15
   // new reads the wait also takes the oldest of them (still correct).
   constexpr int RDW = RD < 16 ? RD : 15;
+  // Unsplit 16x16 tiles with an i32 output issue each MFMA with its operands
+  // swapped (B fragment as the row operand): the fragment then comes out
+  // transposed, lane l holding 4 consecutive columns of row l % 16, which
+  // the epilogue stores as one 16-byte chunk straight from registers.
+  constexpr bool kSwapAB = MS == 16 && !SPLIT &&
+                           std::is_same<OutT, int32_t>::value;
   static_assert(STAGES * STAGE_BYTES <= 160 * 1024, "LDS budget");
 
   __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE_BYTES];
@@ -530,14 +536,18 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
 #pragma unroll
           for (int ii = 0; ii < FM; ++ii) {
             const int i = (j & 1) ? FM - 1 - ii : ii;
-            acc[i][j] = MF::mma(fr[cur].a[i], fr[cur].b[j], acc[i][j]);
+            acc[i][j] = kSwapAB
+                            ? MF::mma(fr[cur].b[j], fr[cur].a[i], acc[i][j])
+                            : MF::mma(fr[cur].a[i], fr[cur].b[j], acc[i][j]);
           }
       } else {
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
           for (int j = 0; j < FN; ++j)
-            acc[i][j] = MF::mma(fr[cur].a[i], fr[cur].b[j], acc[i][j]);
+            acc[i][j] = kSwapAB
+                            ? MF::mma(fr[cur].b[j], fr[cur].a[i], acc[i][j])
+                            : MF::mma(fr[cur].a[i], fr[cur].b[j], acc[i][j]);
       }
     }
   };
@@ -565,6 +575,34 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   const int row_l = 4 * (lane / MS);
   auto frow = [](int r) { return MS == 32 ? 8 * (r >> 2) + (r & 3) : r; };
   constexpr bool kIntOut = std::is_same<OutT, int32_t>::value;
+  if constexpr (kSwapAB) {
+    // Transposed fragments: lane l holds C[row l % 16][4 (l / 16) .. +3] of
+    // each 16 x 16 fragment, so every fragment is one 16-byte store per
+    // lane (16 rows x 64 bytes per instruction), no LDS staging. Per-element
+    // stores serve accumulation and a C or pitch not 16-byte aligned.
+    const int64_t r0 = m0 + wm * WTM + (lane & 15);
+    const int64_t c0 = n0 + wn * WTN + 4 * (lane >> 4);
+    const bool vec = store_mode != kStoreAccumulate &&
+                     (uintptr_t)C % 16 == 0 && ldc % 4 == 0;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        OutT *dst = C + (r0 + i * MS) * ldc + c0 + j * MS;
+        if (vec) {
+          if (store_mode == kStoreThrough)
+            store_through16(dst, acc[i][j]);
+          else
+            *(i32x4 *)dst = acc[i][j];
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            store_out(dst + r, acc[i][j][r],
+                      store_mode == kStoreAccumulate ? 1 : 0);
+        }
+      }
+    return;
+  }
   if constexpr (!kIntOut) {
     if ((!SPLIT || parts == 1) && !epi_plain(epi)) {
       // Fused epilogue: each 32-row fragment band of a wave goes through
@@ -663,9 +701,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
           char *dst = (char *)(C + (grow0 + b * MS + row) * ldc + gcol0) +
                       ch * 16;
           if (store_mode == kStoreThrough)
-            asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(dst),
-                         "v"(v)
-                         : "memory");
+            store_through16(dst, v);
           else
             *(i32x4 *)dst = v;
         }
