@@ -205,12 +205,14 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   // reads return in issue order and lgkmcnt has 4 bits: with more than 15
   // new reads the wait also takes the oldest of them (still correct).
   constexpr int RDW = RD < 16 ? RD : 15;
-  // Unsplit 16x16 tiles with an i32 output issue each MFMA with its operands
-  // swapped (B fragment as the row operand): the fragment then comes out
-  // transposed, lane l holding 4 consecutive columns of row l % 16, which
-  // the epilogue stores as one 16-byte chunk straight from registers.
-  constexpr bool kSwapAB = MS == 16 && !SPLIT &&
-                           std::is_same<OutT, int32_t>::value;
+  // Unsplit 16x16 tiles issue each MFMA with its operands swapped (the B
+  // fragment as the row operand; both share one lane layout): the fragment
+  // then comes out transposed, lane l holding 4 consecutive columns of row
+  // l % 16. An i32 output stores that run as one 16-byte chunk straight from
+  // registers; f16 / f32 outputs stage it through LDS as one 8- / 16-byte
+  // write instead of four. (W8A16 and transposed-A tiles keep the plain
+  // order: not measured.)
+  constexpr bool kSwapAB = MS == 16 && !SPLIT && BMODE != kBW8 && !AT;
   static_assert(STAGES * STAGE_BYTES <= 160 * 1024, "LDS budget");
 
   __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE_BYTES];
@@ -574,8 +576,15 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   const int col_l = lane & (MS - 1);
   const int row_l = 4 * (lane / MS);
   auto frow = [](int r) { return MS == 32 ? 8 * (r >> 2) + (r & 3) : r; };
+  // Position of accumulator element r of fragment (i, j) in the wave tile.
+  auto fr_row = [&](int i, int r) {
+    return kSwapAB ? i * MS + (lane & 15) : i * MS + row_l + frow(r);
+  };
+  auto fr_col = [&](int j, int r) {
+    return kSwapAB ? j * MS + 4 * (lane >> 4) + r : j * MS + col_l;
+  };
   constexpr bool kIntOut = std::is_same<OutT, int32_t>::value;
-  if constexpr (kSwapAB) {
+  if constexpr (kSwapAB && kIntOut) {
     // Transposed fragments: lane l holds C[row l % 16][4 (l / 16) .. +3] of
     // each 16 x 16 fragment, so every fragment is one 16-byte store per
     // lane (16 rows x 64 bytes per instruction), no LDS staging. Per-element
@@ -622,8 +631,11 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
         for (int j = 0; j < FN; ++j)
 #pragma unroll
           for (int r = 0; r < AR; ++r)
-            stage[(j * MS + col_l) * PITCH + row_l + frow(r)] =
-                (float)acc[i][j][r];
+            if constexpr (kSwapAB)
+              stage[fr_col(j, r) * PITCH + (lane & 15)] = (float)acc[i][j][r];
+            else
+              stage[(j * MS + col_l) * PITCH + row_l + frow(r)] =
+                  (float)acc[i][j][r];
         __syncthreads();
         for (int t = lane; t < MS * WTN; t += 64) {
           const int rr = t / WTN, cc = t % WTN;
@@ -677,6 +689,24 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
             float sc = 1.0f;
             if constexpr (BMODE == kBW8)
               sc = (float)scale[gcol0 + j * MS + col_l];
+            if constexpr (kSwapAB && !kIntOut) {
+              // four consecutive columns of one row: one 8- or 16-byte write
+              const int row = (i - b) * MS + (lane & 15);
+              const int byte = fr_col(j, 0) * OB;
+              const int off = row * ROWB +
+                              (((byte >> 4) ^ (row & (NCH - 1))) << 4) +
+                              (byte & 15);
+              if constexpr (std::is_same<OutT, float>::value) {
+                *(f32x4 *)(ws + off) = acc[i][j];
+              } else {
+                f16x4 h;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                  h[r] = (f16)acc[i][j][r];
+                *(f16x4 *)(ws + off) = h;
+              }
+              continue;
+            }
 #pragma unroll
             for (int r = 0; r < AR; ++r) {
               const int row = (i - b) * MS + row_l + frow(r);
@@ -739,8 +769,10 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
           sc = (float)scale[n0 + wn * WTN + j * MS + col_l];
 #pragma unroll
         for (int r = 0; r < AR; ++r) {
-          OutT *dst = crow + frow(r) * ldc + j * MS;
-          const int64_t row = m0 + wm * WTM + i * MS + row_l + frow(r);
+          OutT *dst = kSwapAB ? C + (m0 + wm * WTM + fr_row(i, r)) * ldc + n0 +
+                                    wn * WTN + fr_col(j, r)
+                              : crow + frow(r) * ldc + j * MS;
+          const int64_t row = m0 + wm * WTM + fr_row(i, r);
           if (SPLIT && row >= M)
             continue;
           if constexpr (kIntOut) {
