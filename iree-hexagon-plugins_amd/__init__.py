@@ -873,14 +873,15 @@ def attention(q, k, v, o=None, *, causal=True, scale=None, stream=None):
     return o
 
 
-def matmul_mfma_config(index, a, b, c, *, scale=None, splits=0, stream=None):
+def matmul_mfma_config(index, a, b, c, *, scale=None, splits=0, accumulate=False,
+                       stream=None):
     """Run one compiled MFMA configuration (autotuner entry point).
 
     The configuration's B form decides how `b` is read: TN takes B [N, K],
     NN takes B [K, N] f16, W8A16 takes B [K, N] int8 plus `scale`; a
     transposed-A configuration takes A [K, M]. `splits` forces a split-K
     configuration's K split count (0: the planner's; SPLITS_STREAM_K:
-    stream-K runs)."""
+    stream-K runs). With `accumulate` the result is added into `c`."""
     import torch
     cfg = mfma_configs()[index]
     a_dtype = torch.int8 if cfg.a_elem == ELEM_I8 else torch.float16
@@ -911,6 +912,8 @@ def matmul_mfma_config(index, a, b, c, *, scale=None, splits=0, stream=None):
     _on_device((a, "a"), (b, "b"), (c, "c"), (scale, "scale"))
     if c.dtype == torch.float32 and a.dtype == torch.float16:
         flags |= OUT_F32
+    if accumulate:
+        flags |= ACCUMULATE
     _check(library().iree_mi355x_matmul_mfma_config_split(
         index, splits, a.data_ptr(), b.data_ptr(),
         scale.data_ptr() if scale is not None else None, c.data_ptr(), m, n,

@@ -420,6 +420,62 @@ def test_matmul_i8_general(pkg, oracle, dev, m, n, k, bt):
     check_canary(buf, m, n, 12345)
 
 
+def test_fast_tiles_accumulate_and_odd_pitch(pkg, oracle, dev):
+    """Every unsplit int8 / f16 macro-tile (not W8A16) through its two
+    per-element epilogue paths: C += A.B into a contiguous C, and a plain
+    store into a C view whose row pitch is not a multiple of 16 bytes.
+    The 16x16 tiles store transposed fragments; this covers their
+    non-vector paths, which the 4096^3 and sweep shapes do not reach."""
+    m, n, k = 256, 256, 128
+    g = torch.Generator().manual_seed(77)
+    ran = 0
+    for cfg in pkg.mfma_configs():
+        if "_sk" in cfg.name or cfg.b_form == pkg.B_FORM_W8A16:
+            continue
+        if m % cfg.tile_m or n % cfg.tile_n or k % cfg.tile_k:
+            continue
+        i8 = cfg.a_elem == pkg.ELEM_I8
+        tn = cfg.b_form == pkg.B_FORM_TN
+        if i8:
+            a = torch.randint(-128, 128, (m, k), generator=g).to(torch.int8)
+            b = torch.randint(-128, 128, (n, k), generator=g).to(torch.int8)
+            cdt = torch.int32
+            init = torch.randint(-10 ** 6, 10 ** 6, (m, n), generator=g,
+                                 dtype=torch.int32)
+            ref_acc = oracle.matmul_i8(a.numpy(), b.numpy(), init.numpy(),
+                                       b_transposed=True)
+            ref = oracle.matmul_i8(a.numpy(), b.numpy(), b_transposed=True)
+        else:
+            a = torch.randn(*((k, m) if cfg.a_transposed else (m, k)),
+                            generator=g).half()
+            b = torch.randn(*((n, k) if tn else (k, n)), generator=g).half()
+            f32 = cfg.c_elem == pkg.ELEM_F32
+            cdt = torch.float32 if f32 else torch.float16
+            init = torch.randn(m, n, generator=g).to(cdt)
+            kw = dict(b_transposed=tn, a_transposed=bool(cfg.a_transposed),
+                      out_f32=f32)
+            ref_acc = oracle.matmul_f16(a.numpy(), b.numpy(), init.numpy(), **kw)
+            ref = oracle.matmul_f16(a.numpy(), b.numpy(), **kw)
+        ad, bd = a.to(dev), b.to(dev)
+        c = init.to(dev).clone()
+        pkg.matmul_mfma_config(cfg.index, ad, bd, c, accumulate=True)
+        # odd pitch: one element past n, inside a canary-filled buffer
+        fill = 12345 if i8 else 3.0
+        buf = torch.full((m, n + 1), fill, dtype=cdt, device=dev)
+        cv = buf[:, :n]
+        pkg.matmul_mfma_config(cfg.index, ad, bd, cv)
+        got_acc, got = c.cpu().numpy(), cv.cpu().numpy()
+        if i8:
+            assert np.array_equal(got_acc, ref_acc), cfg.name
+            assert np.array_equal(got, ref), cfg.name
+        else:
+            fp16_ok(oracle, got_acc, ref_acc)
+            fp16_ok(oracle, got, ref)
+        assert bool((buf[:, n].cpu() == fill).all()), cfg.name
+        ran += 1
+    assert ran >= 8
+
+
 def test_c2_matmul_i8_4096_bit_exact(pkg, oracle, inputs, dev):
     a, bt = inputs.c2_matmul_i8()
     c = pkg.matmul(a.to(dev), bt.to(dev), b_transposed=True)
