@@ -53,6 +53,11 @@ const TunedEntry kTuned[] = {
      11008, 4096, 0, "w8a16_nn_32x256x64_w1x4_s4_sk", 1},
     {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 128,
      11008, 4096, 0, "f16_nn_64x128x64_w2x2_s4_sk", 1},
+    // C1 (128x512x256, latency-bound): 16 workgroups of 32x128 with one
+    // split (rows stored directly) beat 4 of 128x128 (4.0 against 5.7 us),
+    // each workgroup streaming a quarter of the operand bytes.
+    {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 128,
+     512, 256, 0, "f16_nn_32x128x64_w1x4_s4_sk", 1},
     // Stream-K (splits -1) where it measured fastest.
     {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_F16, 192,
      11008, 11008, 0, "w8a16_nn_128x256x64_w2x4_s4_sk", -1},

@@ -60,7 +60,8 @@ F16, I8, I32, F32 = 0, 1, 2, 3
     ((F16, F16, F16, 4096, 4096, 4096, 1), 1, (256, 256)),
     ((F16, F16, F32, 4096, 4096, 4096, 1), 1, (256, 256)),
     ((F16, F16, F16, 2048, 4096, 4096, 1), 1, (256, 128)),
-    ((F16, F16, F16, 128, 512, 256, 0), 1, (128, 128)),
+    # C1: a measured entry (16 workgroups of 32x128, one split)
+    ((F16, F16, F16, 128, 512, 256, 0), 1, (32, 128)),
     ((F16, F16, F16, 2048, 4096, 4096, 0), 1, (256, 128)),
     ((F16, F16, F16, 100, 512, 256, 0), 1, None),
     ((F16, F16, F16, 100, 500, 256, 0), 2, (64, 64)),
