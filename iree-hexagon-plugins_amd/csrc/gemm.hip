@@ -1139,6 +1139,14 @@ static hipError_t launch_fast(const MatmulArgs &a) {
   IHP_FAST_CONFIG_X(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, false, true, 16)
 #define IHP_FAST_CONFIG_X(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, SPLIT,  \
                           AT, MS)                                             \
+  IHP_FAST_CONFIG_XT(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, SPLIT, AT,  \
+                     MS, 0)
+// A split-K configuration the planner takes only from its measured table.
+#define IHP_FAST_CONFIG_S_TABLE(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST)   \
+  IHP_FAST_CONFIG_XT(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, true, false, \
+                     32, 1)
+#define IHP_FAST_CONFIG_XT(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, SPLIT, \
+                           AT, MS, TABLE)                                     \
   {NAME,                                                                      \
    MODE,                                                                      \
    SPLIT,                                                                     \
@@ -1156,7 +1164,8 @@ static hipError_t launch_fast(const MatmulArgs &a) {
                                   : (BKB / (int)sizeof(T)) * BN *             \
                                         (MODE == kBW8 ? 1 : (int)sizeof(T)))),\
    &launch_fast<T, OUT, BM, BN, BKB, WM, WN, ST, MODE, SPLIT, AT, MS>,      \
-   MS}
+   MS,                                                                        \
+   TABLE}
 
 // Every compiled fast-path configuration (none spills registers: the
 // 4-wave 256x256 tiles, 128 x 128 per wave, did and were dropped). The
@@ -1215,6 +1224,11 @@ static const FastConfig kFastConfigs[] = {
     IHP_FAST_CONFIG_AT("f16f32at_tn_128x128x64_w2x2_s4", kBTN, f16, float, 128, 128, 128, 2, 2, 4),
     IHP_FAST_CONFIG_AT16("f16at_nn_256x256x64_w2x4_s2_m16", kBNN16, f16, f16, 256, 256, 128, 2, 4, 2),
     IHP_FAST_CONFIG_AT16("f16at_tn_256x256x64_w2x4_s2_m16", kBTN, f16, f16, 256, 256, 128, 2, 4, 2),
+    // 8-wave skinny split-K tile (512-byte weight rows, twice the copies in
+    // flight of the 4-wave 32x128 tile per CU). Measured ahead only on the
+    // shape the planner's table names it for (slower at M = 16 with N =
+    // 4096, M = 128 and K = 11008), so the cost model does not rank it.
+    IHP_FAST_CONFIG_S_TABLE("f16_nn_64x256x64_w2x4_s4_sk", kBNN16, f16, f16, 64, 256, 128, 2, 4, 4),
 };
 
 const FastConfig *fast_configs(int *count) {

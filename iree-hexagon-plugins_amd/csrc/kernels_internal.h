@@ -141,6 +141,7 @@ struct FastConfig {
   int lds_bytes; // static LDS per workgroup
   FastLaunchFn launch;
   int mfma;      // MFMA shape: 32 (32x32) or 16 (16x16)
+  int table_only;  // chosen only by a measured planner entry, never ranked
 };
 
 const FastConfig *fast_configs(int *count);

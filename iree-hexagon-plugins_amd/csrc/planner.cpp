@@ -49,6 +49,10 @@ const TunedEntry kTuned[] = {
     // every tile and split count (random inputs, rotating weights).
     {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 16,
      4096, 11008, 0, "f16_nn_32x128x64_w1x4_s4_sk", 8},
+    // C3 M=16 N=11008: the 8-wave 64x256 tile, 4 splits (172 workgroups),
+    // 20.7 against 22.3 us for the best 32x128 split count.
+    {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 16,
+     11008, 4096, 0, "f16_nn_64x256x64_w2x4_s4_sk", 4},
     {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_F16, 128,
      11008, 4096, 0, "w8a16_nn_32x256x64_w1x4_s4_sk", 1},
     {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 128,
@@ -394,7 +398,7 @@ int32_t iree_mi355x_classify_matmul(const iree_mi355x_matmul_desc_t *d) {
   const int64_t cus = d->num_cus > 0 ? d->num_cus : kDefaultCus;
   for (int i = 0; i < count; ++i) {
     Candidate c;
-    if (cfgs[i].lds_bytes <= d->lds_budget_bytes &&
+    if (!cfgs[i].table_only && cfgs[i].lds_bytes <= d->lds_budget_bytes &&
         evaluate(*d, cfgs[i], i, cus, &c))
       return IREE_MI355X_FAMILY_MFMA;
   }
@@ -464,7 +468,7 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
       // than the model prices); measured entries above select it.
       static const int kSplitChoices[] = {0, 1, 2, 3, 4, 5, 6, 8, 10, 12, 16};
       for (int i = 0; i < count; ++i) {
-        if (cfgs[i].lds_bytes > budget)
+        if (cfgs[i].lds_bytes > budget || cfgs[i].table_only)
           continue;
         for (int forced : kSplitChoices) {
           if (forced && !cfgs[i].split_k)
