@@ -182,6 +182,24 @@ def test_planner_split_k_for_skinny_shapes(pkg):
     assert p.splits == 1 and p.workspace_bytes == 0
 
 
+def test_table_only_tile_runs_only_where_measured(pkg):
+    # The 8-wave 64x256 split-K tile measured ahead only at C3 M=16
+    # N=11008 K=4096; the cost model would rank it first at other skinny
+    # shapes where it measured slower, so only its measured entry selects
+    # it.
+    name = b"f16_nn_64x256x64_w2x4_s4_sk"
+    assert name.decode() in [c.name for c in pkg.mfma_configs()]
+    p = pkg.plan(pkg.make_desc(F16, F16, F16, 16, 11008, 4096, 0))
+    assert p.config_name == name and p.from_tuned_table and p.splits == 4
+    for m in (8, 16, 24, 32, 48, 64, 128, 192, 256):
+        for n, k in ((4096, 4096), (11008, 4096), (4096, 11008),
+                     (11008, 11008), (512, 256), (8192, 4096)):
+            if (m, n, k) == (16, 11008, 4096):
+                continue
+            p = pkg.plan(pkg.make_desc(F16, F16, F16, m, n, k, 0))
+            assert p.config_name != name, (m, n, k)
+
+
 def test_planner_stream_k(pkg):
     # W8A16 192 x 11008 x 11008 on 128x256 tiles: 86 tiles for 256 CUs.
     # Stream-K runs (equal runs of (tile, K stage) pairs) measured fastest
