@@ -1229,6 +1229,8 @@ static const FastConfig kFastConfigs[] = {
     // shape the planner's table names it for (slower at M = 16 with N =
     // 4096, M = 128 and K = 11008), so the cost model does not rank it.
     IHP_FAST_CONFIG_S_TABLE("f16_nn_64x256x64_w2x4_s4_sk", kBNN16, f16, f16, 64, 256, 128, 2, 4, 4),
+    // The same for C3 M=128 N=11008: 8 waves of 64x32 on a 128x128 tile.
+    IHP_FAST_CONFIG_S_TABLE("f16_nn_128x128x64_w2x4_s4_sk", kBNN16, f16, f16, 128, 128, 128, 2, 4, 4),
 };
 
 const FastConfig *fast_configs(int *count) {

@@ -53,10 +53,14 @@ const TunedEntry kTuned[] = {
     // 20.7 against 22.3 us for the best 32x128 split count.
     {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 16,
      11008, 4096, 0, "f16_nn_64x256x64_w2x4_s4_sk", 4},
+    // C5 W8A16 M=128: stream-K runs of the 32x256 tile, 37.8 / 38.4 against
+    // 42.9 / 43.3 us for its single split in two sweeps.
     {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_F16, 128,
-     11008, 4096, 0, "w8a16_nn_32x256x64_w1x4_s4_sk", 1},
+     11008, 4096, 0, "w8a16_nn_32x256x64_w1x4_s4_sk", -1},
+    // C3 M=128 N=11008: the 8-wave 128x128 tile, 2 splits (172 workgroups),
+    // 32.8 against 37.8 us for 64x128 x1 and 35.5 us for the 4-wave 128x128.
     {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 128,
-     11008, 4096, 0, "f16_nn_64x128x64_w2x2_s4_sk", 1},
+     11008, 4096, 0, "f16_nn_128x128x64_w2x4_s4_sk", 2},
     // C1 (128x512x256, latency-bound): 16 workgroups of 32x128 with one
     // split (rows stored directly) beat 4 of 128x128 (4.0 against 5.7 us),
     // each workgroup streaming a quarter of the operand bytes.

@@ -182,22 +182,27 @@ def test_planner_split_k_for_skinny_shapes(pkg):
     assert p.splits == 1 and p.workspace_bytes == 0
 
 
-def test_table_only_tile_runs_only_where_measured(pkg):
-    # The 8-wave 64x256 split-K tile measured ahead only at C3 M=16
-    # N=11008 K=4096; the cost model would rank it first at other skinny
-    # shapes where it measured slower, so only its measured entry selects
-    # it.
-    name = b"f16_nn_64x256x64_w2x4_s4_sk"
-    assert name.decode() in [c.name for c in pkg.mfma_configs()]
-    p = pkg.plan(pkg.make_desc(F16, F16, F16, 16, 11008, 4096, 0))
-    assert p.config_name == name and p.from_tuned_table and p.splits == 4
+def test_table_only_tiles_run_only_where_measured(pkg):
+    # The 8-wave 64x256 and 128x128 split-K tiles measured ahead only at C3
+    # M=16 and M=128 with N=11008, K=4096; the cost model would rank the
+    # first at other skinny shapes where it measured slower, so only their
+    # measured entries select them.
+    home = {(16, 11008, 4096): (b"f16_nn_64x256x64_w2x4_s4_sk", 4),
+            (128, 11008, 4096): (b"f16_nn_128x128x64_w2x4_s4_sk", 2)}
+    names = [c.name for c in pkg.mfma_configs()]
+    for shape, (name, splits) in home.items():
+        assert name.decode() in names
+        p = pkg.plan(pkg.make_desc(F16, F16, F16, *shape, 0))
+        assert p.config_name == name and p.from_tuned_table
+        assert p.splits == splits
+    table_only = {name for name, _ in home.values()}
     for m in (8, 16, 24, 32, 48, 64, 128, 192, 256):
         for n, k in ((4096, 4096), (11008, 4096), (4096, 11008),
                      (11008, 11008), (512, 256), (8192, 4096)):
-            if (m, n, k) == (16, 11008, 4096):
+            if (m, n, k) in home:
                 continue
             p = pkg.plan(pkg.make_desc(F16, F16, F16, m, n, k, 0))
-            assert p.config_name != name, (m, n, k)
+            assert p.config_name not in table_only, (m, n, k)
 
 
 def test_planner_stream_k(pkg):

@@ -647,13 +647,14 @@ def test_batch_matmul_epilogue_paths(pkg, oracle, dev, z, m, n, k, bt, shared_b,
     fp16_ok(oracle, y.cpu().numpy(), ref)
 
 
-def test_stream_k_planned(pkg, oracle, dev):
-    """A shape the planner runs in stream-K (a measured entry), through the
-    quantized_matmul entry point, twice in a row (re-armed counters)."""
-    m, n, k = 192, 11008, 11008
+@pytest.mark.parametrize("m,n,k", [(192, 11008, 11008), (128, 11008, 4096)])
+def test_stream_k_planned(pkg, oracle, dev, m, n, k):
+    """Shapes the planner runs in stream-K (measured entries; the second is
+    BASELINE's C5 W8A16 M=128), through the quantized_matmul entry point,
+    whole outputs, twice in a row (re-armed counters)."""
     assert pkg.plan(pkg.make_desc(0, 1, 0, m, n, k, 0,
                                   has_scale=True)).stream_k_steps > 0
-    g = torch.Generator().manual_seed(192)
+    g = torch.Generator().manual_seed(m)
     x = (torch.randn(m, k, generator=g) * 0.5).half()
     w = torch.randint(-128, 128, (k, n), generator=g).to(torch.int8)
     s = (torch.rand(n, generator=g) * 0.019 + 0.001).half()
