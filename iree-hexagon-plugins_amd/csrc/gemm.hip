@@ -1231,6 +1231,8 @@ static const FastConfig kFastConfigs[] = {
     IHP_FAST_CONFIG_S_TABLE("f16_nn_64x256x64_w2x4_s4_sk", kBNN16, f16, f16, 64, 256, 128, 2, 4, 4),
     // The same for C3 M=128 N=11008: 8 waves of 64x32 on a 128x128 tile.
     IHP_FAST_CONFIG_S_TABLE("f16_nn_128x128x64_w2x4_s4_sk", kBNN16, f16, f16, 128, 128, 128, 2, 4, 4),
+    // And 8 waves of 32x32 on a 64x128 tile (4 stages of 24 KiB).
+    IHP_FAST_CONFIG_S_TABLE("f16_nn_64x128x64_w2x4_s4_sk", kBNN16, f16, f16, 64, 128, 128, 2, 4, 4),
 };
 
 const FastConfig *fast_configs(int *count) {

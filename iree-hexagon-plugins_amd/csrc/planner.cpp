@@ -48,7 +48,7 @@ const TunedEntry kTuned[] = {
     // Skinny shapes where the model's pick measured slower than a sweep of
     // every tile and split count (random inputs, rotating weights).
     {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 16,
-     4096, 11008, 0, "f16_nn_32x128x64_w1x4_s4_sk", 8},
+     4096, 11008, 0, "f16_nn_64x128x64_w2x4_s4_sk", 8},
     // C3 M=16 N=11008: the 8-wave 64x256 tile, 4 splits (172 workgroups),
     // 20.7 against 22.3 us for the best 32x128 split count.
     {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 16,
@@ -57,6 +57,16 @@ const TunedEntry kTuned[] = {
     // 42.9 / 43.3 us for its single split in two sweeps.
     {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_F16, 128,
      11008, 4096, 0, "w8a16_nn_32x256x64_w1x4_s4_sk", -1},
+    // C3 M=16 and M=128 at N=K=4096 and M=128 at K=11008: the 8-wave 64x128
+    // tile, 12.2 against 12.9 us (x6), 18.5 against 21.2 us (x4) and 33.1
+    // against 35.2 us (x4) for the model's picks; at M=16 K=11008 (the
+    // entry above) 21.3 against 21.8 us for the 4-wave 32x128 tile, x8.
+    {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 16,
+     4096, 4096, 0, "f16_nn_64x128x64_w2x4_s4_sk", 6},
+    {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 128,
+     4096, 4096, 0, "f16_nn_64x128x64_w2x4_s4_sk", 4},
+    {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 128,
+     4096, 11008, 0, "f16_nn_64x128x64_w2x4_s4_sk", 4},
     // C3 M=128 N=11008: the 8-wave 128x128 tile, 2 splits (172 workgroups),
     // 32.8 against 37.8 us for 64x128 x1 and 35.5 us for the 4-wave 128x128.
     {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 128,
@@ -66,6 +76,10 @@ const TunedEntry kTuned[] = {
     // each workgroup streaming a quarter of the operand bytes.
     {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 128,
      512, 256, 0, "f16_nn_32x128x64_w1x4_s4_sk", 1},
+    // M=192 N=11008 (86 tiles of 128x128): the 8-wave tile, one split,
+    // 39.7 / 40.5 against 41.3 / 41.9 us for the 4-wave one in two sweeps.
+    {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, 192,
+     11008, 4096, 0, "f16_nn_128x128x64_w2x4_s4_sk", 1},
     // Stream-K (splits -1) where it measured fastest.
     {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_F16, 192,
      11008, 11008, 0, "w8a16_nn_128x256x64_w2x4_s4_sk", -1},
@@ -445,9 +459,11 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
     int count = 0;
     const FastConfig *cfgs = fast_configs(&count);
     Candidate best;
-    // A measured entry wins when it fits.
+    // A measured entry wins when it fits. Entries were timed on one matrix:
+    // a batch multiplies the grid, so batched calls take the model's pick.
     for (const TunedEntry &t : kTuned) {
-      if (!t.config || t.a_elem != d->a_elem || t.b_elem != d->b_elem ||
+      if (!t.config || d->batch > 1 || t.a_elem != d->a_elem ||
+          t.b_elem != d->b_elem ||
           t.c_elem != d->c_elem ||
           t.m != d->m || t.n != d->n || t.k != d->k || t.flags != d->flags)
         continue;

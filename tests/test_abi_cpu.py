@@ -183,12 +183,17 @@ def test_planner_split_k_for_skinny_shapes(pkg):
 
 
 def test_table_only_tiles_run_only_where_measured(pkg):
-    # The 8-wave 64x256 and 128x128 split-K tiles measured ahead only at C3
-    # M=16 and M=128 with N=11008, K=4096; the cost model would rank the
-    # first at other skinny shapes where it measured slower, so only their
+    # The 8-wave 64x256, 128x128 and 64x128 split-K tiles measured ahead
+    # only at the C3 shapes named here; the cost model would rank the first
+    # at other skinny shapes where it measured slower, so only their
     # measured entries select them.
     home = {(16, 11008, 4096): (b"f16_nn_64x256x64_w2x4_s4_sk", 4),
-            (128, 11008, 4096): (b"f16_nn_128x128x64_w2x4_s4_sk", 2)}
+            (128, 11008, 4096): (b"f16_nn_128x128x64_w2x4_s4_sk", 2),
+            (16, 4096, 4096): (b"f16_nn_64x128x64_w2x4_s4_sk", 6),
+            (128, 4096, 4096): (b"f16_nn_64x128x64_w2x4_s4_sk", 4),
+            (128, 4096, 11008): (b"f16_nn_64x128x64_w2x4_s4_sk", 4),
+            (16, 4096, 11008): (b"f16_nn_64x128x64_w2x4_s4_sk", 8),
+            (192, 11008, 4096): (b"f16_nn_128x128x64_w2x4_s4_sk", 1)}
     names = [c.name for c in pkg.mfma_configs()]
     for shape, (name, splits) in home.items():
         assert name.decode() in names
@@ -196,6 +201,10 @@ def test_table_only_tiles_run_only_where_measured(pkg):
         assert p.config_name == name and p.from_tuned_table
         assert p.splits == splits
     table_only = {name for name, _ in home.values()}
+    # entries were timed on one matrix: a batch takes the model's pick
+    for shape in home:
+        p = pkg.plan(pkg.make_desc(F16, F16, F16, *shape, 0, batch=2))
+        assert not p.from_tuned_table and p.config_name not in table_only
     for m in (8, 16, 24, 32, 48, 64, 128, 192, 256):
         for n, k in ((4096, 4096), (11008, 4096), (4096, 11008),
                      (11008, 11008), (512, 256), (8192, 4096)):
