@@ -315,9 +315,12 @@ bool evaluate(const iree_mi355x_matmul_desc_t &d, const FastConfig &c,
       want = 1;
     k_split = ((d.k + want - 1) / want + c.bk - 1) / c.bk * c.bk;
     splits = (int)((d.k + k_split - 1) / k_split);
-    // One split stores directly (rows past M masked): worth it only where
-    // M is ragged, else an unsplit configuration covers the shape better.
-    if (splits < 2 && !explicit_config && d.m % c.bm == 0)
+    // One split stores directly (rows past M masked): worth it where M is
+    // ragged, or where the shape's unsplit grid would leave most CUs idle
+    // (short K: many small tiles, each a short chain); else an unsplit
+    // configuration covers the shape better.
+    if (splits < 2 && !explicit_config && d.m % c.bm == 0 &&
+        tiles * batch * 2 >= cus)
       return false;
   }
   const int64_t ab = elem_bytes(d.a_elem), bb = elem_bytes(d.b_elem);
@@ -361,7 +364,13 @@ bool evaluate(const iree_mi355x_matmul_desc_t &d, const FastConfig &c,
   // apart once the ring's lookahead is spent.
   const int64_t rounds = (tiles * splits * batch + cus - 1) / cus;
   const double t_chain = (double)rounds * (double)(k_split / c.bk) * kStageNs;
-  if (t_chain > t)
+  // An unsplit grid filling under half the CUs never reaches the copy /
+  // MFMA overlap of a long K loop: its few stages pay both in turn. (Split
+  // grids keep the overlapped form, so the split count is not pushed
+  // across the half-grid boundary.)
+  if (splits == 1 && tiles * batch * 2 < cus)
+    t = t_mfma + t_chain > t ? t_mfma + t_chain : t;
+  else if (t_chain > t)
     t = t_chain;
   t += (double)rounds * kRoundNs;
   if (c.split_k && splits > 1) {

@@ -214,6 +214,26 @@ def test_table_only_tiles_run_only_where_measured(pkg):
             assert p.config_name not in table_only, (m, n, k)
 
 
+def test_short_k_fills_the_cus(pkg):
+    # Short K on a grid of few large tiles never overlaps its copies with
+    # its MFMAs: the planner prefers more, smaller workgroups there
+    # (2048x512x256: 32 workgroups of 256x128 measured 6.7 us, 64 of
+    # 128x128 6.2 us; 512x512x256: 6.4 us against 4.3 us for 64 of 32x128
+    # at one split; 256x11008x4096: 70.6 against 43.8 us).
+    p = pkg.plan(pkg.make_desc(F16, F16, F16, 2048, 512, 256, 0))
+    assert p.workgroups >= 64 and (p.tile_m, p.tile_n) != (256, 128)
+    p = pkg.plan(pkg.make_desc(F16, F16, F16, 512, 512, 256, 0))
+    assert p.config_name == b"f16_nn_32x128x64_w1x4_s4_sk" and p.splits == 1
+    assert p.workgroups == 64 and p.workspace_bytes == 0
+    p = pkg.plan(pkg.make_desc(F16, F16, F16, 256, 11008, 4096, 0))
+    assert p.workgroups >= 128
+    # a split grid keeps the overlapped pricing, so the split count is not
+    # pushed past half the CUs (W8A16 96x2048x2048: x4 16.7 us, x8 20.4 us)
+    p = pkg.plan(pkg.make_desc(F16, I8, F16, 96, 2048, 2048, 0,
+                               has_scale=True))
+    assert p.splits == 4
+
+
 def test_planner_stream_k(pkg):
     # W8A16 192 x 11008 x 11008 on 128x256 tiles: 86 tiles for 256 CUs.
     # Stream-K runs (equal runs of (tile, K stage) pairs) measured fastest
