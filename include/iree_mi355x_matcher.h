@@ -136,6 +136,15 @@ typedef struct iree_mi355x_match_t {
   float scale;
   int32_t head_loop;
   char reason[160];        // why not taken (empty when taken)
+  // Contractions compute init + A.B. A zero init (a splat 0 or a
+  // linalg.fill of 0) gives the overwriting export; a region argument gives
+  // IREE_MI355X_MATMUL_ACCUMULATE, reading the output buffer as the init. A
+  // fill of another constant also gives ACCUMULATE with init_fill = 1: the
+  // caller first fills the output with init_value (a command-buffer fill),
+  // as the reference unpacks HMX tiles into the filled init
+  // (test/codegen/transforms/convert_matmul_to_hmx.mlir:40-55).
+  int32_t init_fill;
+  double init_value;
 } iree_mi355x_match_t;
 
 // Options.

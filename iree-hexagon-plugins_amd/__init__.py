@@ -247,7 +247,8 @@ class MatchResult(ctypes.Structure):
                 ("m_loop", ctypes.c_int32), ("n_loop", ctypes.c_int32),
                 ("k_loop", ctypes.c_int32), ("root", ctypes.c_int32),
                 ("scale", ctypes.c_float), ("head_loop", ctypes.c_int32),
-                ("reason", ctypes.c_char * 160)]
+                ("reason", ctypes.c_char * 160),
+                ("init_fill", ctypes.c_int32), ("init_value", ctypes.c_double)]
 
 
 _lib = None
@@ -522,12 +523,15 @@ class Match:
     scale: float
     head_loop: int
     reason: str
+    # ACCUMULATE over a constant fill: fill the output with init_value first
+    init_fill: bool = False
+    init_value: float = 0.0
 
 
 def _match_result(r: MatchResult) -> Match:
     return Match(bool(r.taken), r.export_name.decode(), r.flags, r.batch_loop,
                  r.m_loop, r.n_loop, r.k_loop, r.root, r.scale, r.head_loop,
-                 r.reason.decode())
+                 r.reason.decode(), bool(r.init_fill), r.init_value)
 
 
 def match(op: LinalgOp, *, named_only=False) -> Match:

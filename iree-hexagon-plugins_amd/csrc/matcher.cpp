@@ -36,6 +36,8 @@ typedef iree_mi355x_match_t Match;
 void reject(Match *out, const char *fmt, ...) {
   out->taken = 0;
   out->export_name[0] = 0;
+  out->init_fill = 0;
+  out->init_value = 0.0;
   va_list args;
   va_start(args, fmt);
   vsnprintf(out->reason, sizeof(out->reason), fmt, args);
@@ -378,6 +380,99 @@ struct Types {
   int a, b, c;
 };
 
+struct Region {
+  const Op *ops;
+  int count;
+};
+
+// What a destination operand (a contraction's init, a reduction's start
+// value) holds before the op runs. A linalg contraction computes
+// init + A.B (examples/matmul/matmul.mlir; the HMX unpack adds every tile
+// into the init, UK/hmx.c:328-357,426-450), so the init decides between an
+// overwriting and an accumulating dispatch.
+enum InitKind { kInitConstant, kInitArgument, kInitOther };
+struct Init {
+  InitKind kind = kInitOther;
+  double value = 0.0;  // kInitConstant
+  char why[96] = {0};  // kInitOther
+};
+
+// The init of operand `operand` of op `index` (of region `rg`, or of a lone
+// op when rg is null): a region argument, a splat constant, a linalg.fill
+// of a constant in the region, or something else.
+Init init_of(const Region *rg, const Op &op, int index, int operand) {
+  Init init;
+  const int producer = op.producer[operand];
+  if (producer == IREE_MI355X_FROM_ARGUMENT) {
+    init.kind = kInitArgument;
+    return init;
+  }
+  if (producer == IREE_MI355X_FROM_CONSTANT) {
+    init.kind = kInitConstant;
+    init.value = op.scalar[operand];
+    return init;
+  }
+  if (!rg || producer < 0 || producer >= index) {
+    snprintf(init.why, sizeof(init.why),
+             "the init is produced by an op outside the description");
+    return init;
+  }
+  const Op &p = rg->ops[producer];
+  if (p.kind == IREE_MI355X_LINALG_FILL && p.num_inputs == 1) {
+    if (p.producer[0] == IREE_MI355X_FROM_CONSTANT) {
+      init.kind = kInitConstant;
+      init.value = p.scalar[0];
+      return init;
+    }
+    snprintf(init.why, sizeof(init.why),
+             "the init is a fill of a value that is not a constant");
+    return init;
+  }
+  snprintf(init.why, sizeof(init.why),
+           "the init is produced by op %d, which is not a fill", producer);
+  return init;
+}
+
+bool init_is(const Init &init, double value) {
+  return init.kind == kInitConstant && init.value == value;
+}
+
+// Applies the output init to an accepted contraction: a zero init keeps the
+// overwriting export; a region argument, or a fill of another constant,
+// adds ACCUMULATE (C_out = C_init + A.B) where the export has that form
+// (the constant is returned for the caller to fill first); anything else
+// is not taken. `truncated`: the contraction accumulates in f32 and a
+// truncation after it writes the result, so an init would have to be read
+// in f32.
+void apply_init(const Init &init, bool truncated, Match *out) {
+  if (!out->taken)
+    return;
+  if (init_is(init, 0.0))
+    return;
+  if (init.kind == kInitOther) {
+    reject(out, "%s", init.why);
+    return;
+  }
+  const char *what = init.kind == kInitConstant ? "a nonzero fill"
+                                                : "a region argument";
+  if (truncated) {
+    reject(out, "the init is %s, accumulated in f32 before a truncation: "
+           "no kernel (the accumulating exports read the init in the "
+           "output type)", what);
+    return;
+  }
+  if (strcmp(out->export_name, "w8a16_matmul") == 0) {
+    reject(out, "the init is %s, and w8a16_matmul has no accumulating form",
+           what);
+    return;
+  }
+  out->flags |= IREE_MI355X_MATMUL_ACCUMULATE;
+  if (init.kind == kInitConstant) {
+    out->init_fill = 1;
+    out->init_value = init.value;
+  }
+}
+
 // A (possibly batched) contraction with two inputs, optionally a per-column
 // scale (W8A16), or linalg.quantized_matmul's zero points.
 void match_contraction(const Op &op, uint32_t options, Types t, Match *out) {
@@ -545,12 +640,16 @@ bool valid_op(const Op &op) {
   return true;
 }
 
-int match_one(const Op &op, uint32_t options, Types t, Match *out) {
+// `init` is what the op's output holds before it runs (contractions only);
+// `truncated` as for apply_init.
+int match_one(const Op &op, uint32_t options, Types t, const Init &init,
+              bool truncated, Match *out) {
   switch (op.kind) {
     case IREE_MI355X_LINALG_MATMUL:
     case IREE_MI355X_LINALG_BATCH_MATMUL:
     case IREE_MI355X_LINALG_QUANTIZED_MATMUL:
       match_contraction(op, options, t, out);
+      apply_init(init, truncated, out);
       return IREE_MI355X_OK;
     case IREE_MI355X_LINALG_GENERIC: {
       if (op.reduction_loops == 0) {
@@ -559,6 +658,7 @@ int match_one(const Op &op, uint32_t options, Types t, Match *out) {
         return IREE_MI355X_OK;
       }
       match_contraction(op, options, t, out);
+      apply_init(init, truncated, out);
       return IREE_MI355X_OK;
     }
     case IREE_MI355X_LINALG_ATTENTION: {
@@ -588,11 +688,6 @@ int match_one(const Op &op, uint32_t options, Types t, Match *out) {
 }
 
 // --------------------------------------------------------------- regions --
-
-struct Region {
-  const Op *ops;
-  int count;
-};
 
 bool identity_map(const Op &op, int i) {
   const int rank = (int)op.map_rank[i];
@@ -818,9 +913,11 @@ int guard_input(const Region &rg, int index) {
     return -1;
   if (op.producer[1] != IREE_MI355X_FROM_CONSTANT || op.scalar[1] != 0.0)
     return -1;
-  // condition: a row AND-reduction of (x == -inf)
+  // condition: a row AND-reduction of (x == -inf), starting from true
   const int cond = op.producer[0];
-  if (cond < 0 || cond >= index || !row_reduction(rg.ops[cond], IREE_MI355X_BODY_ANDI))
+  if (cond < 0 || cond >= index ||
+      !row_reduction(rg.ops[cond], IREE_MI355X_BODY_ANDI) ||
+      !init_is(init_of(&rg, rg.ops[cond], cond, 1), 1.0))
     return -1;
   const int eq = rg.ops[cond].producer[0];
   if (eq < 0 || eq >= cond)
@@ -839,10 +936,23 @@ int guard_input(const Region &rg, int index) {
   return op.producer[2];
 }
 
+// A batch_matmul of the attention chain written as a linalg.generic must
+// have the multiply-accumulate body, as a single contraction must.
+bool chain_contraction_body(const Op &op) {
+  if (op.kind != IREE_MI355X_LINALG_GENERIC)
+    return true;
+  double zp[2];
+  char why[120];
+  return contraction_body(op, 0, 1, -1, 2, false, zp, why, sizeof(why));
+}
+
 // The decomposed attention of examples/attention_layer/attention_layer.mlir:
 // S = (Q.a) . (K.b)^T [masked]; P = exp(S - rowmax S) / rowsum(...) [guarded];
-// O = P . V [truncated to f16].
-bool match_attention_chain(const Region &rg, int root, Match *out) {
+// O = P . V [truncated to f16]. The two batch_matmuls start from zero
+// fills, the row max from -inf and the row sum from 0
+// (attention_layer.mlir:47,52,80,102).
+bool match_attention_chain(const Region &rg, int root, uint32_t options,
+                           Match *out) {
   int pv = root;
   bool truncated = false;
   {
@@ -865,7 +975,7 @@ bool match_attention_chain(const Region &rg, int root, Match *out) {
   Roles r2;
   char why[120];
   if (!contraction_roles(bmm2, 0, 1, 2, &r2, why, sizeof(why)) ||
-      r2.a_t || r2.b_t)
+      r2.a_t || r2.b_t || !chain_contraction_body(bmm2))
     return false;
   // V: an f16 region argument (through extensions)
   const Source v = trace(rg, pv, 1);
@@ -885,6 +995,7 @@ bool match_attention_chain(const Region &rg, int root, Match *out) {
   if (ex < 0 || sum < 0 || !row_reduction(rg.ops[sum], IREE_MI355X_BODY_ADDF) ||
       rg.ops[sum].producer[0] != ex)
     return false;
+  const Init sum_init = init_of(&rg, rg.ops[sum], sum, 1);
   uint32_t code;
   double c;
   if (!unary_elementwise(rg.ops[ex], &code, &c) || code != IREE_MI355X_BODY_EXP)
@@ -897,6 +1008,7 @@ bool match_attention_chain(const Region &rg, int root, Match *out) {
   if (mx < 0 || !row_reduction(rg.ops[mx], IREE_MI355X_BODY_MAXF) ||
       rg.ops[mx].producer[0] != s)
     return false;
+  const Init max_init = init_of(&rg, rg.ops[mx], mx, 1);
   // S: [causal mask] [scale] bmm1
   bool causal = false;
   double score_factor = 1.0;
@@ -923,7 +1035,8 @@ bool match_attention_chain(const Region &rg, int root, Match *out) {
       bmm1.num_inputs != 2 || bmm1.num_outputs != 1)
     return false;
   Roles r1;
-  if (!contraction_roles(bmm1, 0, 1, 2, &r1, why, sizeof(why)) || r1.a_t)
+  if (!contraction_roles(bmm1, 0, 1, 2, &r1, why, sizeof(why)) || r1.a_t ||
+      !chain_contraction_body(bmm1))
     return false;
   const Source q = trace(rg, s, 0), k = trace(rg, s, 1);
   if (!q.arg || !k.arg || q.transposed || q.type != IREE_MI355X_TYPE_F16 ||
@@ -933,6 +1046,29 @@ bool match_attention_chain(const Region &rg, int root, Match *out) {
   // transposed by the map.
   if (k.transposed == r1.b_t)
     return false;
+  // The chain is attention's; what follows decides whether the kernel
+  // computes it.
+  out->root = root;
+  if ((options & IREE_MI355X_MATCH_NAMED_ONLY) &&
+      (bmm1.kind == IREE_MI355X_LINALG_GENERIC ||
+       bmm2.kind == IREE_MI355X_LINALG_GENERIC)) {
+    reject(out, "matmul-like 'linalg.generic' in the attention chain is not "
+           "lowered: only named batch_matmuls are");
+    return true;
+  }
+  if (!init_is(init_of(&rg, bmm1, s, 2), 0.0) ||
+      !init_is(init_of(&rg, bmm2, pv, 2), 0.0)) {
+    reject(out, "an attention batch_matmul does not start from a zero fill");
+    return true;
+  }
+  if (!init_is(sum_init, 0.0)) {
+    reject(out, "the softmax row sum does not start from 0");
+    return true;
+  }
+  if (max_init.kind != kInitConstant || !(max_init.value <= -3.4028234663852886e38)) {
+    reject(out, "the softmax row max does not start from -inf");
+    return true;
+  }
   const int64_t head = bmm1.loop_extent[r1.k];
   if (head != bmm2.loop_extent[r2.n] || (head != 64 && head != 128)) {
     reject(out, "attention head dims %lld / %lld (64 or 128 are taken)",
@@ -1007,7 +1143,9 @@ int iree_mi355x_match_linalg_op(const iree_mi355x_linalg_op_t *op,
   Types t{op->elem_type[0], op->num_inputs > 1 ? op->elem_type[1] : 0,
           op->num_outputs > 0 ? op->elem_type[c] : 0};
   out->root = 0;
-  return match_one(*op, options, t, out);
+  return match_one(*op, options, t,
+                   op->num_outputs > 0 ? init_of(nullptr, *op, 0, c) : Init(),
+                   false, out);
 }
 
 int iree_mi355x_match_dispatch_region(const iree_mi355x_linalg_op_t *ops,
@@ -1032,7 +1170,7 @@ int iree_mi355x_match_dispatch_region(const iree_mi355x_linalg_op_t *ops,
   const Region rg{ops, (int)count};
   const int root = (int)count - 1;
   // The attention chain, or an attention op (possibly behind a causal mask).
-  if (match_attention_chain(rg, root, out))
+  if (match_attention_chain(rg, root, options, out))
     return IREE_MI355X_OK;
   clear(out);
   const Op &r = ops[root];
@@ -1050,14 +1188,14 @@ int iree_mi355x_match_dispatch_region(const iree_mi355x_linalg_op_t *ops,
         plain.producer[i] = r.producer[i + 1];
       }
       Types t{r.elem_type[0], r.elem_type[1], r.elem_type[5]};
-      match_one(plain, options, t, out);
+      match_one(plain, options, t, Init(), false, out);
       if (out->taken)
         out->flags |= IREE_MI355X_ATTENTION_CAUSAL;
       out->root = root;
       return IREE_MI355X_OK;
     }
     Types t{r.elem_type[0], r.elem_type[1], r.elem_type[r.num_inputs]};
-    match_one(r, options, t, out);
+    match_one(r, options, t, Init(), false, out);
     out->root = root;
     return IREE_MI355X_OK;
   }
@@ -1080,6 +1218,7 @@ int iree_mi355x_match_dispatch_region(const iree_mi355x_linalg_op_t *ops,
     match_one(m, options,
               Types{m.elem_type[0], m.num_inputs > 1 ? m.elem_type[1] : 0,
                     m.num_outputs ? m.elem_type[c] : 0},
+              m.num_outputs ? init_of(&rg, m, mm, c) : Init(), out_type >= 0,
               out);
     out->root = root;
     return IREE_MI355X_OK;
@@ -1097,13 +1236,34 @@ int iree_mi355x_match_dispatch_region(const iree_mi355x_linalg_op_t *ops,
     out->root = root;
     return IREE_MI355X_OK;
   }
+  const Init init = init_of(&rg, m, mm, c);
   // A matmul whose B is the output of a dequantization generic: W8A16.
   if (!b.arg && b.op >= 0 && dequant_generic(ops[b.op]) &&
       ops[b.op].producer[0] == IREE_MI355X_FROM_ARGUMENT) {
-    const Op &dq = ops[b.op];
     Roles rr;
     char why[120];
-    if (!contraction_roles(m, 0, 1, c, &rr, why, sizeof(why))) {
+    double zp[2];
+    if (!a.arg) {
+      // Only extensions fold into the kernel's A read; any other producer
+      // (an activation, a second matmul) would be dropped.
+      reject(out, "matmul input produced by an op the region cannot fold");
+    } else if (m.kind != IREE_MI355X_LINALG_MATMUL &&
+               m.kind != IREE_MI355X_LINALG_GENERIC) {
+      reject(out, "dequantized B feeds a %s, not a matmul",
+             m.kind == IREE_MI355X_LINALG_BATCH_MATMUL ? "batch_matmul"
+                                                       : "non-contraction");
+    } else if (m.kind == IREE_MI355X_LINALG_GENERIC &&
+               (options & IREE_MI355X_MATCH_NAMED_ONLY)) {
+      reject(out,
+             "matmul-like 'linalg.generic' is not lowered: only named "
+             "linalg.matmul and linalg.batch_matmul with an MxN output are");
+    } else if (m.num_inputs != 2) {
+      reject(out, "contraction with %u inputs", m.num_inputs);
+    } else if (!contraction_roles(m, 0, 1, c, &rr, why, sizeof(why))) {
+      reject(out, "%s", why);
+    } else if (m.kind == IREE_MI355X_LINALG_GENERIC &&
+               !contraction_body(m, 0, 1, -1, c, false, zp, why,
+                                 sizeof(why))) {
       reject(out, "%s", why);
     } else if (rr.b_t || rr.a_t || rr.batch >= 0) {
       reject(out, "dequantized B must be [K, N] of a plain matmul");
@@ -1112,16 +1272,16 @@ int iree_mi355x_match_dispatch_region(const iree_mi355x_linalg_op_t *ops,
       reject(out, "dequantized matmul (%s, int8) -> %s has no kernel",
              type_name(a.type), type_name(t.c));
     } else {
-      (void)dq;
       out->m_loop = rr.m;
       out->n_loop = rr.n;
       out->k_loop = rr.k;
       accept(out, "w8a16_matmul", 0);
+      apply_init(init, out_type >= 0, out);
     }
     out->root = root;
     return IREE_MI355X_OK;
   }
-  if ((!a.arg && a.op >= 0) || (!b.arg && b.op >= 0)) {
+  if (!a.arg || !b.arg) {
     reject(out, "matmul input produced by an op the region cannot fold");
     out->root = root;
     return IREE_MI355X_OK;
@@ -1129,7 +1289,7 @@ int iree_mi355x_match_dispatch_region(const iree_mi355x_linalg_op_t *ops,
   // The extensions looked through are exactly what a mixed-precision body
   // does inside a contraction, so the contraction's own body and types are
   // judged with the source types.
-  match_one(m, options, t, out);
+  match_one(m, options, t, init, out_type >= 0, out);
   out->root = root;
   return IREE_MI355X_OK;
 }

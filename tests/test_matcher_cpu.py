@@ -38,9 +38,21 @@ def generic(pkg, loops, red, maps, types, body, extents=None, inputs=2,
                          extents=extents, producers=producers)
 
 
-def named(pkg, kind, loops, red, maps, types, extents=None):
+def named(pkg, kind, loops, red, maps, types, extents=None, producers=None):
     return pkg.linalg_op(kind, loops, maps, types, inputs=len(maps) - 1,
-                         reductions=red, extents=extents)
+                         reductions=red, extents=extents, producers=producers)
+
+
+def fill(pkg, loops, typ, value):
+    """linalg.fill ins(%value) outs(%empty) over all of `loops`."""
+    return pkg.linalg_op(pkg.OP_FILL, loops, ["", loops], [typ, typ],
+                         inputs=1, producers=[("const", value)])
+
+
+# The init of a contraction's output as a zero splat constant, what a
+# linalg.fill of 0 amounts to. Cases that transcribe a lit function with a
+# fill op describe the fill as an op of a region instead.
+ZERO_INIT = ("const", 0.0)
 
 
 # ----------------------------------------- specialize_hmx_contractions.mlir --
@@ -51,7 +63,9 @@ def test_f16_mixed_precision_transposed_rhs(pkg):
                  {"d0": 64, "d1": 128, "d2": 96})
     m = pkg.match(op)
     assert m.taken and m.export == "matmul_f16", m.reason
-    assert m.flags == pkg.B_TRANSPOSED | pkg.OUT_F32
+    # outs(%init), a function argument: the contraction adds into it
+    assert m.flags == pkg.B_TRANSPOSED | pkg.OUT_F32 | pkg.ACCUMULATE
+    assert not m.init_fill
     assert (m.m_loop, m.n_loop, m.k_loop, m.batch_loop) == (0, 1, 2, -1)
 
 
@@ -60,7 +74,7 @@ def test_f16_batch_contraction(pkg):
                  ["d0 d1 d3", "d0 d3 d2", "d0 d1 d2"], ["f16"] * 3, F16_BODY)
     m = pkg.match(op)
     assert m.taken and m.export == "batch_matmul_f16", m.reason
-    assert m.flags == 0
+    assert m.flags == pkg.ACCUMULATE  # outs(%init), an argument
     assert (m.batch_loop, m.m_loop, m.n_loop, m.k_loop) == (0, 1, 2, 3)
 
 
@@ -96,20 +110,26 @@ def test_elementwise_is_kept(pkg):
 # ------------------------- hexagon_strategy_hmx_generic_contraction.mlir --
 
 def test_strategy_generic_contraction_planned_without_mfma(pkg):
+    # %init = linalg.fill ins(%zero : f32) outs(%empty), then the generic
+    init = fill(pkg, "d0 d1", "f32", 0.0)
     op = generic(pkg, "d0 d1 d2", ["d2"], ["d0 d2", "d1 d2", "d0 d1"],
                  ["f16", "f16", "f32"], MIXED_BODY,
-                 {"d0": 256, "d1": 1024, "d2": 1536})
-    alone = pkg.match(op, named_only=True)
+                 {"d0": 256, "d1": 1024, "d2": 1536},
+                 producers=["arg", "arg", 0])
+    alone = pkg.match_region([init, op], named_only=True)
     assert not alone.taken and "only named" in alone.reason
     # the configuration pipeline specializes it first: then it is taken
-    full = pkg.match(op)
+    full = pkg.match_region([init, op])
     assert full.taken and full.flags == pkg.B_TRANSPOSED | pkg.OUT_F32
+    assert full.root == 1 and not full.init_fill
 
 
 def test_strategy_named_contraction(pkg):
+    init = fill(pkg, "d0 d1", "f32", 0.0)
     op = named(pkg, pkg.OP_MATMUL, "d0 d1 d2", ["d2"],
-               ["d0 d2", "d1 d2", "d0 d1"], ["f16", "f16", "f32"])
-    m = pkg.match(op, named_only=True)
+               ["d0 d2", "d1 d2", "d0 d1"], ["f16", "f16", "f32"],
+               producers=["arg", "arg", 0])
+    m = pkg.match_region([init, op], named_only=True)
     assert m.taken and m.export == "matmul_f16", m.reason
     assert m.flags == pkg.B_TRANSPOSED | pkg.OUT_F32
 
@@ -130,28 +150,34 @@ def test_strategy_named_unsupported_output_type(pkg):
 
 # ------------------------------------------------ convert_matmul_to_hmx.mlir --
 
-@pytest.mark.parametrize("maps,out,flags", [
-    # @convert_f32_output / @convert_f16_output / @convert_ragged
-    (["m k", "k n", "m n"], "f32", "OUT_F32"),
-    (["m k", "k n", "m n"], "f16", ""),
+@pytest.mark.parametrize("maps,out,init,flags", [
+    # @convert_f32_output / @convert_ragged: a fill of 0
+    (["m k", "k n", "m n"], "f32", 0.0, "OUT_F32"),
+    # @convert_f16_output: a fill of 5.0 kept as the accumulation's init
+    (["m k", "k n", "m n"], "f16", 5.0, "ACCUMULATE"),
     # @convert_both_inputs_transposed
-    (["k m", "n k", "m n"], "f32", "A_TRANSPOSED B_TRANSPOSED OUT_F32"),
+    (["k m", "n k", "m n"], "f32", 0.0, "A_TRANSPOSED B_TRANSPOSED OUT_F32"),
 ])
-def test_convert_matmul_layouts(pkg, maps, out, flags):
+def test_convert_matmul_layouts(pkg, maps, out, init, flags):
+    filled = fill(pkg, "m n", out, init)
     op = named(pkg, pkg.OP_MATMUL, "m n k", ["k"], maps, ["f16", "f16", out],
-               {"m": 1537, "n": 1539, "k": 257})
-    m = pkg.match(op)
+               {"m": 1537, "n": 1539, "k": 257}, producers=["arg", "arg", 0])
+    m = pkg.match_region([filled, op])
     want = 0
     for f in flags.split():
         want |= getattr(pkg, f)
     assert m.taken and m.export == "matmul_f16" and m.flags == want, m.reason
+    # the caller fills the output with the constant before an accumulating
+    # dispatch; a zero fill needs none
+    assert m.init_fill == (init != 0.0) and m.init_value == init
 
 
 def test_convert_unit_batch_transpose_b(pkg):
+    filled = fill(pkg, "b m n", "f32", 0.0)
     op = named(pkg, pkg.OP_BATCH_MATMUL, "b m n k", ["k"],
                ["b m k", "b n k", "b m n"], ["f16", "f16", "f32"],
-               {"b": 1, "m": 32, "n": 32, "k": 64})
-    m = pkg.match(op)
+               {"b": 1, "m": 32, "n": 32, "k": 64}, producers=["arg", "arg", 0])
+    m = pkg.match_region([filled, op])
     assert m.taken and m.export == "batch_matmul_f16", m.reason
     assert m.flags == pkg.B_TRANSPOSED | pkg.OUT_F32 and m.batch_loop == 0
 
@@ -179,9 +205,10 @@ def test_int8_generic_and_named(pkg):
     op = generic(pkg, "m n k", ["k"], ["m k", "n k", "m n"],
                  ["i8", "i8", "i32"], I8_BODY)
     m = pkg.match(op)
-    assert m.taken and m.export == "matmul_i8" and m.flags == pkg.B_TRANSPOSED
+    assert m.taken and m.export == "matmul_i8", m.reason
+    assert m.flags == pkg.B_TRANSPOSED | pkg.ACCUMULATE
     op = named(pkg, pkg.OP_MATMUL, "m n k", ["k"], ["m k", "k n", "m n"],
-               ["i8", "i8", "i32"])
+               ["i8", "i8", "i32"], producers=["arg", "arg", ZERO_INIT])
     m = pkg.match(op)
     assert m.taken and m.export == "matmul_i8" and m.flags == 0
     # int8 kernels have no transposed-A or batched form
@@ -252,8 +279,10 @@ def test_w8a16_fused_dequant_generic(pkg, order):
         body = [("wf", "sitofp", ["w"], "f16"), ("p", "mulf", ["x", "wf"], "f16"),
                 ("q", "mulf", ["p", "s"], "f16"),
                 ("r", "addf", ["y", "q"], "f16"), ("yield", ["r"])]
+    prods = ["arg", "arg", "arg", ZERO_INIT]
     op = generic(pkg, "m n k", ["k"], ["m k", "k n", "n", "m n"],
-                 ["f16", "i8", "f16", "f16"], body, inputs=3, args=W8_ARGS)
+                 ["f16", "i8", "f16", "f16"], body, inputs=3, args=W8_ARGS,
+                 producers=prods)
     m = pkg.match(op)
     if order == "dequant_then_mul":
         # a truncation of the accumulation inside the body is not the
@@ -261,28 +290,140 @@ def test_w8a16_fused_dequant_generic(pkg, order):
         assert not m.taken
     else:
         assert m.taken and m.export == "w8a16_matmul", m.reason
+        # accumulating into an argument: the W8A16 export has no such form
+        op = generic(pkg, "m n k", ["k"], ["m k", "k n", "n", "m n"],
+                     ["f16", "i8", "f16", "f16"], body, inputs=3,
+                     args=W8_ARGS)
+        m = pkg.match(op)
+        assert not m.taken and "no accumulating form" in m.reason
     # a per-row (K) scale is not the per-output-channel dequantization
     op = generic(pkg, "m n k", ["k"], ["m k", "k n", "k", "m n"],
-                 ["f16", "i8", "f16", "f16"], body, inputs=3, args=W8_ARGS)
+                 ["f16", "i8", "f16", "f16"], body, inputs=3, args=W8_ARGS,
+                 producers=prods)
     assert not pkg.match(op).taken
 
 
+def dequant(pkg):
+    return generic(pkg, "k n", [], ["k n", "n", "k n"], ["i8", "f16", "f16"],
+                   [("wf", "sitofp", ["w"], "f16"),
+                    ("d", "mulf", ["wf", "s"], "f16"), ("yield", ["d"])],
+                   args=["w", "s", "o"])
+
+
 def test_w8a16_dequant_generic_feeding_matmul(pkg):
-    dq = generic(pkg, "k n", [], ["k n", "n", "k n"], ["i8", "f16", "f16"],
-                 [("wf", "sitofp", ["w"], "f16"),
-                  ("d", "mulf", ["wf", "s"], "f16"), ("yield", ["d"])],
-                 args=["w", "s", "o"])
+    dq = dequant(pkg)
     mm = named(pkg, pkg.OP_MATMUL, "m n k", ["k"], ["m k", "k n", "m n"],
-               ["f16", "f16", "f16"], {"m": 1, "n": 11008, "k": 4096})
-    mm.producer[1] = 0
+               ["f16", "f16", "f16"], {"m": 1, "n": 11008, "k": 4096},
+               producers=["arg", 0, ZERO_INIT])
     m = pkg.match_region([dq, mm])
     assert m.taken and m.export == "w8a16_matmul" and m.root == 1, m.reason
-    assert (m.m_loop, m.n_loop, m.k_loop) == (0, 1, 2)
+    assert (m.m_loop, m.n_loop, m.k_loop) == (0, 1, 2) and m.flags == 0
+    # the same with the init a fill op of the region
+    filled = fill(pkg, "m n", "f16", 0.0)
+    mm_f = named(pkg, pkg.OP_MATMUL, "m n k", ["k"], ["m k", "k n", "m n"],
+                 ["f16", "f16", "f16"], producers=["arg", 0, 1])
+    m = pkg.match_region([dq, filled, mm_f])
+    assert m.taken and m.export == "w8a16_matmul" and m.root == 2, m.reason
     # the weight transposed by the matmul's map: no kernel
     mm2 = named(pkg, pkg.OP_MATMUL, "m n k", ["k"], ["m k", "n k", "m n"],
-                ["f16", "f16", "f16"])
-    mm2.producer[1] = 0
+                ["f16", "f16", "f16"], producers=["arg", 0, ZERO_INIT])
     assert not pkg.match_region([dq, mm2]).taken
+
+
+def test_w8a16_region_keeps_every_producer_of_a(pkg):
+    # relu(x) feeding the matmul's A: the kernel reads x itself, so the
+    # region is not taken (without the dequantization it is not either)
+    relu = generic(pkg, "m k", [], ["m k", "m k"], ["f16", "f16"],
+                   [("z", "const", [], "f16", 0.0),
+                    ("r", "maximumf", ["i", "z"], "f16"), ("yield", ["r"])],
+                   inputs=1, args=["i", "o"])
+    dq = dequant(pkg)
+    mm = named(pkg, pkg.OP_MATMUL, "m n k", ["k"], ["m k", "k n", "m n"],
+               ["f16", "f16", "f16"], producers=[0, 1, ZERO_INIT])
+    m = pkg.match_region([relu, dq, mm])
+    assert not m.taken and "cannot fold" in m.reason
+    plain = named(pkg, pkg.OP_MATMUL, "m n k", ["k"], ["m k", "k n", "m n"],
+                  ["f16", "f16", "f16"], producers=[0, "arg", ZERO_INIT])
+    assert not pkg.match_region([relu, plain]).taken
+
+
+def test_w8a16_region_generic_matmul_rules(pkg):
+    dq = dequant(pkg)
+    gm = generic(pkg, "m n k", ["k"], ["m k", "k n", "m n"],
+                 ["f16", "f16", "f16"], F16_BODY,
+                 producers=["arg", 0, ZERO_INIT])
+    m = pkg.match_region([dq, gm])
+    assert m.taken and m.export == "w8a16_matmul", m.reason
+    # strategy selection alone takes named matmuls only
+    m = pkg.match_region([dq, gm], named_only=True)
+    assert not m.taken and "only named" in m.reason
+    # a generic whose body is not the multiply-accumulate
+    wrong = generic(pkg, "m n k", ["k"], ["m k", "k n", "m n"],
+                    ["f16", "f16", "f16"],
+                    [("m", "addf", ["a", "b"], "f16"),
+                     ("s", "addf", ["c", "m"], "f16"), ("yield", ["s"])],
+                    producers=["arg", 0, ZERO_INIT])
+    m = pkg.match_region([dq, wrong])
+    assert not m.taken and "product" in m.reason
+
+
+# ------------------------------------------------------------ output init ----
+
+def test_output_init_forms(pkg):
+    maps = ["m k", "k n", "m n"]
+
+    def mm(init_producer, out="f16"):
+        return named(pkg, pkg.OP_MATMUL, "m n k", ["k"], maps,
+                     ["f16", "f16", out], producers=["arg", "arg",
+                                                     init_producer])
+    # outs from a region argument: C_out = C_init + A.B
+    m = pkg.match_region([mm("arg")])
+    assert m.taken and m.flags == pkg.ACCUMULATE and not m.init_fill
+    # a fill of 0 (an op, or a splat): overwrite
+    m = pkg.match_region([fill(pkg, "m n", "f16", 0.0), mm(0)])
+    assert m.taken and m.flags == 0 and not m.init_fill
+    m = pkg.match(mm(ZERO_INIT))
+    assert m.taken and m.flags == 0
+    # a fill of 1.0: accumulate into the filled output
+    m = pkg.match_region([fill(pkg, "m n", "f16", 1.0), mm(0)])
+    assert m.taken and m.flags == pkg.ACCUMULATE
+    assert m.init_fill and m.init_value == 1.0
+    m = pkg.match(mm(("const", -2.5)))
+    assert m.taken and m.init_fill and m.init_value == -2.5
+    # a fill of a value that is not a constant
+    dyn = pkg.linalg_op(pkg.OP_FILL, "m n", ["", "m n"], ["f16", "f16"],
+                        inputs=1)
+    m = pkg.match_region([dyn, mm(0)])
+    assert not m.taken and "not a constant" in m.reason
+    # an init computed by another op (an elementwise generic)
+    neg = generic(pkg, "m n", [], ["m n", "m n"], ["f16", "f16"],
+                  [("z", "const", [], "f16", -1.0),
+                   ("r", "mulf", ["i", "z"], "f16"), ("yield", ["r"])],
+                  inputs=1, args=["i", "o"])
+    m = pkg.match_region([neg, mm(0)])
+    assert not m.taken and "not a fill" in m.reason
+    # a lone op whose init an undescribed op produces
+    m = pkg.match(mm(3))
+    assert not m.taken and "outside the description" in m.reason
+
+
+def test_output_init_with_truncation(pkg):
+    # f32 accumulation, then truncf to f16: a zero init is taken, an init
+    # accumulated in f32 is not (the exports read an init in the output type)
+    def region(init_producer):
+        mm = named(pkg, pkg.OP_MATMUL, "m n k", ["k"], ["m k", "k n", "m n"],
+                   ["f16", "f16", "f32"],
+                   producers=["arg", "arg", init_producer])
+        tr = generic(pkg, "m n", [], ["m n", "m n"], ["f32", "f16"],
+                     [("t", "truncf", ["i"], "f16"), ("yield", ["t"])],
+                     inputs=1, args=["i", "o"], producers=[0])
+        return [mm, tr]
+    m = pkg.match_region(region(ZERO_INIT))
+    assert m.taken and m.export == "matmul_f16" and m.flags == 0, m.reason
+    m = pkg.match_region(region("arg"))
+    assert not m.taken and "truncation" in m.reason
+    m = pkg.match_region(region(("const", 2.0)))
+    assert not m.taken and "truncation" in m.reason
 
 
 # ------------------------------------------------------------- attention ----
@@ -300,7 +441,8 @@ def ew(pkg, types, body, producers, args=("i", "o"), loops="d0 d1 d2",
 
 
 def attention_chain(pkg, *, head=128, causal=False, guard=True, exp=True,
-                    out="f16", q_scale=SCALE):
+                    out="f16", q_scale=SCALE, bmm_init=("const", 0.0),
+                    max_init=-INF, sum_init=0.0, bmm1_body=None):
     """The ops of attention_layer.mlir:48-105 in program order (reshapes are
     views and so not ops: a consumer of an expand_shape names the op whose
     result it reshapes)."""
@@ -322,11 +464,19 @@ def attention_chain(pkg, *, head=128, causal=False, guard=True, exp=True,
                            ["d0 d2 d1", "d0 d1 d2"], ["f32", "f32"], inputs=1,
                            producers=[k32]))
     ks = add(ew(pkg, ["f32", "f32"], scale_body(SCALE), [kt]))
-    s = add(pkg.linalg_op(pkg.OP_BATCH_MATMUL, "b m n k",
-                          ["b m k", "b k n", "b m n"], ["f32"] * 3, inputs=2,
-                          reductions=["k"],
-                          extents={"b": 4, "m": 1024, "n": 1024, "k": head},
-                          producers=[qs, ks, ("const", 0.0)]))
+    if bmm1_body is None:
+        s = add(pkg.linalg_op(pkg.OP_BATCH_MATMUL, "b m n k",
+                              ["b m k", "b k n", "b m n"], ["f32"] * 3,
+                              inputs=2, reductions=["k"],
+                              extents={"b": 4, "m": 1024, "n": 1024, "k": head},
+                              producers=[qs, ks, bmm_init]))
+    else:
+        s = add(pkg.linalg_op(pkg.OP_GENERIC, "b m n k",
+                              ["b m k", "b k n", "b m n"], ["f32"] * 3,
+                              inputs=2, reductions=["k"], body=bmm1_body,
+                              args=ABC,
+                              extents={"b": 4, "m": 1024, "n": 1024, "k": head},
+                              producers=[qs, ks, bmm_init]))
     if causal:
         s = add(ew(pkg, ["f32", "f32"], [
             ("q", "index", [], "index", "d1"), ("k", "index", [], "index", "d2"),
@@ -338,7 +488,9 @@ def attention_chain(pkg, *, head=128, causal=False, guard=True, exp=True,
     mx = add(pkg.linalg_op(pkg.OP_GENERIC, "d0 d1 d2",
                            ["d0 d1 d2", "d0 d1", "d0 d1"],
                            ["f32", "f32", "i64"], inputs=1, reductions=red,
-                           args=["i", "o", "idx"], producers=[s],
+                           args=["i", "o", "idx"],
+                           producers=[s, ("const", max_init),
+                                      ("const", 0.0)],
                            body=[("j", "index", [], "index", "d2"),
                                  ("ji", "index_cast", ["j"], "i64"),
                                  ("mx", "maximumf", ["i", "o"], "f32"),
@@ -354,7 +506,8 @@ def attention_chain(pkg, *, head=128, causal=False, guard=True, exp=True,
                [sub]))
     total = add(pkg.linalg_op(pkg.OP_GENERIC, "d0 d1 d2",
                               ["d0 d1 d2", "d0 d1 0"], ["f32", "f32"],
-                              inputs=1, reductions=red, producers=[e],
+                              inputs=1, reductions=red,
+                              producers=[e, ("const", sum_init)],
                               args=["i", "o"],
                               body=[("a", "addf", ["i", "o"], "f32"),
                                     ("yield", ["a"])]))
@@ -369,7 +522,8 @@ def attention_chain(pkg, *, head=128, causal=False, guard=True, exp=True,
         allinf = add(pkg.linalg_op(pkg.OP_GENERIC, "d0 d1 d2",
                                    ["d0 d1 d2", "d0 d1 0"], ["i1", "i1"],
                                    inputs=1, reductions=red,
-                                   producers=[isinf], args=["i", "o"],
+                                   producers=[isinf, ("const", 1.0)],
+                                   args=["i", "o"],
                                    body=[("a", "andi", ["i", "o"], "i1"),
                                          ("yield", ["a"])]))
         p = add(pkg.linalg_op(pkg.OP_GENERIC, "d0 d1 d2",
@@ -416,6 +570,36 @@ def test_attention_chain_variants(pkg):
     assert not m.taken and "head dims" in m.reason
     m = pkg.match_region(attention_chain(pkg, out="f32"))
     assert not m.taken and "f32" in m.reason
+
+
+def test_attention_chain_inits(pkg):
+    # attention_layer.mlir starts both batch_matmuls from a zero fill, the
+    # row max from -inf (0xFF800000) and the row sum from 0
+    m = pkg.match_region(attention_chain(pkg, bmm_init="arg"))
+    assert not m.taken and "zero fill" in m.reason
+    m = pkg.match_region(attention_chain(pkg, bmm_init=("const", 1.0)))
+    assert not m.taken and "zero fill" in m.reason
+    m = pkg.match_region(attention_chain(pkg, sum_init=1.0))
+    assert not m.taken and "row sum" in m.reason
+    m = pkg.match_region(attention_chain(pkg, max_init=0.0))
+    assert not m.taken and "row max" in m.reason
+    # the lowest finite f32 is as good a start as -inf
+    m = pkg.match_region(attention_chain(pkg, max_init=-3.4028234663852886e38))
+    assert m.taken, m.reason
+
+
+def test_attention_chain_generic_contraction_bodies(pkg):
+    # Q.K^T written as a linalg.generic with the multiply-accumulate body
+    m = pkg.match_region(attention_chain(pkg, bmm1_body=F32_BODY))
+    assert m.taken and m.export == "attention_f16", m.reason
+    # strategy selection alone takes named batch_matmuls only
+    m = pkg.match_region(attention_chain(pkg, bmm1_body=F32_BODY),
+                         named_only=True)
+    assert not m.taken and "only named" in m.reason
+    # a reduction body other than the multiply-accumulate is not attention
+    maxbody = [("m", "mulf", ["a", "b"], "f32"),
+               ("s", "maximumf", ["c", "m"], "f32"), ("yield", ["s"])]
+    assert not pkg.match_region(attention_chain(pkg, bmm1_body=maxbody)).taken
 
 
 def test_linalg_ext_attention_op(pkg):

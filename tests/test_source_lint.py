@@ -36,6 +36,24 @@ def _asm_strings(text):
         yield text.count("\n", 0, m.start()) + 1, "".join(lits)
 
 
+# `s_nop N` waits N + 1 states: two need N >= 1.
+NOP = re.compile(r"s_nop\s+(0x[0-9a-fA-F]+|\d+)")
+
+
+def _uncovered_stores(tmpl):
+    """The wide stores of one asm template whose next instruction is not an
+    s_nop of at least two wait states."""
+    bad = []
+    for m in WIDE_STORE.finditer(tmpl):
+        rest = re.split(r"\\n|\n|;", tmpl[m.end():], maxsplit=1)
+        following = rest[1].strip().lstrip("\\t").strip() if len(rest) > 1 \
+            else ""
+        nop = NOP.match(following)
+        if not nop or int(nop.group(1), 0) < 1:
+            bad.append(m.group(0))
+    return bad
+
+
 def test_inline_asm_wide_stores_carry_wait_states():
     offenders = []
     for name in sorted(os.listdir(CSRC)):
@@ -44,20 +62,22 @@ def test_inline_asm_wide_stores_carry_wait_states():
         with open(os.path.join(CSRC, name)) as f:
             text = f.read()
         for line, tmpl in _asm_strings(text):
-            for m in WIDE_STORE.finditer(tmpl):
-                if "s_nop" not in tmpl[m.end():]:
-                    offenders.append(f"{name}:{line}: {tmpl!r}")
-    assert not offenders, "wide inline-asm stores without s_nop:\n" + \
-        "\n".join(offenders)
+            if _uncovered_stores(tmpl):
+                offenders.append(f"{name}:{line}: {tmpl!r}")
+    assert not offenders, ("wide inline-asm stores not followed by s_nop 1 "
+                           "or more:\n" + "\n".join(offenders))
 
 
 def test_lint_flags_a_bare_wide_store():
-    # The checker itself: a bare dwordx4 store is found, one with the
-    # trailing s_nop is not.
-    bad = 'asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v));'
-    good = ('asm volatile("global_store_dwordx4 %0, %1, off sc1\\n\\ts_nop 1"'
-            ' ::"v"(p), "v"(v));')
-    (_, t_bad), = _asm_strings(bad)
-    (_, t_good), = _asm_strings(good)
-    assert WIDE_STORE.search(t_bad) and "s_nop" not in t_bad
-    assert WIDE_STORE.search(t_good) and "s_nop" in t_good
+    # The checker itself: a bare dwordx4 store, and one followed by s_nop 0
+    # (a single wait state), are found; s_nop 1 and more are not.
+    def tmpl(tail):
+        (_, t), = _asm_strings('asm volatile("global_store_dwordx4 %0, %1, '
+                               'off sc1' + tail + '" ::"v"(p), "v"(v));')
+        return t
+    assert _uncovered_stores(tmpl(""))
+    assert _uncovered_stores(tmpl("\\n\\ts_nop 0"))
+    assert _uncovered_stores(tmpl("\\n\\tv_mov_b32 v0, 0\\n\\ts_nop 1"))
+    assert not _uncovered_stores(tmpl("\\n\\ts_nop 1"))
+    assert not _uncovered_stores(tmpl("\\n s_nop 2"))
+    assert not _uncovered_stores(tmpl("\\n\\ts_nop 0x3"))
