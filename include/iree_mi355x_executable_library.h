@@ -146,7 +146,10 @@ int iree_mi355x_kernel_resources(int index,
 //  "matmul_i8"    same constants and bindings as matmul_f16
 //  "w8a16_matmul" same constants   bindings: x w scale y
 //  "attention_f16" constants: batch heads seq_q seq_kv head_dim
-//                 scale_bits(f32) flags   bindings: q k v o
+//                 scale_bits(f32) flags [kv_heads q_stride_batch_lo/hi
+//                 q_stride_head_lo/hi q_stride_row_lo/hi, then the same
+//                 three for k, v and o] (7 or 32 words)
+//                 bindings: q k v o
 //  "batch_matmul_f16" constants: the matmul_f16 ones, then batch_lo batch_hi
 //                 stride_a_lo/hi stride_b_lo/hi stride_c_lo/hi activation
 //                 epilogue_bindings (bit 0 bias, bit 1 multiplier)

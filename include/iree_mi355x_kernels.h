@@ -167,6 +167,35 @@ int iree_mi355x_attention_f16(const void *q, const void *k, const void *v,
                               int64_t seq_q, int64_t seq_kv, int64_t head_dim,
                               float scale, uint32_t flags, void *stream);
 
+// Where each attention operand lives: the element strides of its batch,
+// head and row (sequence) dimensions; its head_dim elements are contiguous.
+// k and v are indexed by KV head.
+typedef struct iree_mi355x_attention_strides_t {
+  int64_t q[3];
+  int64_t k[3];
+  int64_t v[3];
+  int64_t o[3];
+} iree_mi355x_attention_strides_t;
+
+// iree_mi355x_attention_f16 over strided operands with grouped-query heads:
+// query head h (of `heads`) attends with KV head h / (heads / kv_heads).
+// K / V may be the first seq_kv rows of a longer KV cache and O may be laid
+// out [B, Sq, H, D]: the attention of
+// integration_tests/models/micro/attention-cache-slice-f16/model.py:10-29
+// (9 query heads over 3 KV heads, the first 64 of 128 cache rows, the
+// output permuted to [batch, seq, heads, dim]). heads must be a multiple of
+// kv_heads; every stride a multiple of 8 elements and every pointer 16-byte
+// aligned; each head's q, k and v rows must lie within 4 GiB of its first
+// row. o's row stride must be at least head_dim, and distinct (batch, head,
+// row) must not share o elements (not checked beyond the row stride).
+// iree_mi355x_attention_f16 is this call with contiguous strides and
+// kv_heads == heads.
+int iree_mi355x_attention_f16_strided(
+    const void *q, const void *k, const void *v, void *o, int64_t batch,
+    int64_t heads, int64_t kv_heads, int64_t seq_q, int64_t seq_kv,
+    int64_t head_dim, float scale, uint32_t flags,
+    const iree_mi355x_attention_strides_t *strides, void *stream);
+
 // Workspace a matmul_f16 / w8a16_matmul call of this shape needs (split-K
 // partials and arrival counters), 0 if none. Mirrors the scratch query of the
 // reference's caller-scratch matmul, hexkl_matmul_f16f16_f32_scratch_bytes

@@ -54,6 +54,7 @@ EXECUTABLE_LIBRARY_VERSION = 0x4D490001
 EXPORTED_SYMBOLS = (
     "iree_mi355x_matmul_f16", "iree_mi355x_matmul_i8",
     "iree_mi355x_w8a16_matmul", "iree_mi355x_attention_f16",
+    "iree_mi355x_attention_f16_strided",
     "iree_mi355x_matmul_workspace_bytes", "iree_mi355x_last_error",
     "iree_mi355x_version", "iree_mi355x_device_count",
     "iree_mi355x_matmul_desc_init", "iree_mi355x_classify_matmul",
@@ -286,6 +287,8 @@ def library():
                                              i64, i64, u32, p, sz, p]
     lib.iree_mi355x_attention_f16.argtypes = [p, p, p, p, i64, i64, i64, i64,
                                               i64, ctypes.c_float, u32, p]
+    lib.iree_mi355x_attention_f16_strided.argtypes = [
+        p, p, p, p, i64, i64, i64, i64, i64, i64, ctypes.c_float, u32, p, p]
     lib.iree_mi355x_matmul_workspace_bytes.restype = sz
     lib.iree_mi355x_matmul_workspace_bytes.argtypes = [i64, i64, i64, u32]
     lib.iree_mi355x_batch_matmul_f16.argtypes = [
@@ -608,9 +611,17 @@ def batch_matmul_constants(m, n, k, lda, ldb, ldc, flags, batch, stride_a,
     return words
 
 
-def attention_constants(batch, heads, seq_q, seq_kv, head_dim, scale, flags):
+def attention_constants(batch, heads, seq_q, seq_kv, head_dim, scale, flags,
+                        kv_heads=None, strides=None):
+    """Push constants of "attention_f16"; with `strides` (12 element strides:
+    batch, head, row of q, k, v, o) the 32-word strided form."""
     scale_bits = struct.unpack("<I", struct.pack("<f", scale))[0]
-    return [batch, heads, seq_q, seq_kv, head_dim, scale_bits, flags]
+    words = [batch, heads, seq_q, seq_kv, head_dim, scale_bits, flags]
+    if strides is not None:
+        words.append(heads if kv_heads is None else kv_heads)
+        for v in strides:
+            words += [v & 0xFFFFFFFF, (v >> 32) & 0xFFFFFFFF]
+    return words
 
 
 # --------------------------------------------------------------- operators --
@@ -849,20 +860,34 @@ def quantized_matmul(x, w, scale, y=None, *, w_transposed=False, stream=None):
     return y
 
 
+class AttentionStrides(ctypes.Structure):
+    """iree_mi355x_attention_strides_t: (batch, head, row) element strides of
+    q, k, v and o."""
+    _fields_ = [("q", ctypes.c_int64 * 3), ("k", ctypes.c_int64 * 3),
+                ("v", ctypes.c_int64 * 3), ("o", ctypes.c_int64 * 3)]
+
+
 def attention(q, k, v, o=None, *, causal=True, scale=None, stream=None):
-    """Fused attention forward on contiguous f16 tensors: q, o [B, H, Sq, D];
-    k, v [B, H, Skv, D]."""
+    """Fused attention forward on f16 tensors: q, o [B, Hq, Sq, D]; k, v
+    [B, Hkv, Skv, D] with Hq a multiple of Hkv (query head h reads KV head
+    h // (Hq // Hkv)). Any of them may be a strided view whose last
+    dimension is contiguous: a slice of a longer KV cache, or o as a
+    permuted view of a [B, Sq, Hq, D] buffer."""
     import torch
     for t, nm in ((q, "q"), (k, "k"), (v, "v"), (o, "o")):
         if t is None:
             continue
         if (not isinstance(t, torch.Tensor) or t.dtype != torch.float16
-                or not t.is_contiguous() or t.dim() != 4):
-            raise TypeError(f"{nm} must be a contiguous 4-D f16 tensor")
+                or t.dim() != 4 or not _unit_col(t)):
+            raise TypeError(f"{nm} must be a 4-D f16 tensor with unit "
+                            "stride along head_dim")
     b, h, sq, d = q.shape
-    skv = k.shape[2]
-    _shape(k, (b, h, skv, d), "k")
-    _shape(v, (b, h, skv, d), "v")
+    hkv, skv = k.shape[1], k.shape[2]
+    if hkv < 1 or h % hkv:
+        raise ValueError(f"k must be [{b}, Hkv, Skv, {d}] with Hkv dividing "
+                         f"the {h} query heads, got {list(k.shape)}")
+    _shape(k, (b, hkv, skv, d), "k")
+    _shape(v, (b, hkv, skv, d), "v")
     if o is not None:
         _shape(o, (b, h, sq, d), "o")
     _on_device((q, "q"), (k, "k"), (v, "v"), (o, "o"))
@@ -870,10 +895,20 @@ def attention(q, k, v, o=None, *, causal=True, scale=None, stream=None):
     if scale is None:
         scale = d ** -0.5
     if o is None:
-        o = torch.empty_like(q)
-    _check(lib.iree_mi355x_attention_f16(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), b, h, sq, skv,
-        d, float(scale), CAUSAL if causal else 0, _stream_ptr(stream)))
+        o = torch.empty_like(q, memory_format=torch.contiguous_format)
+    flags = CAUSAL if causal else 0
+    contiguous = all(t.is_contiguous() for t in (q, k, v, o))
+    if contiguous and hkv == h:
+        _check(lib.iree_mi355x_attention_f16(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), b, h, sq,
+            skv, d, float(scale), flags, _stream_ptr(stream)))
+        return o
+    st = AttentionStrides()
+    for field, t in (("q", q), ("k", k), ("v", v), ("o", o)):
+        getattr(st, field)[:] = list(t.stride()[:3])
+    _check(lib.iree_mi355x_attention_f16_strided(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), b, h, hkv, sq,
+        skv, d, float(scale), flags, ctypes.byref(st), _stream_ptr(stream)))
     return o
 
 

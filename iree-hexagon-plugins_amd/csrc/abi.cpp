@@ -571,45 +571,114 @@ int iree_mi355x_w8a16_matmul(const void *x, const int8_t *w, const void *scale,
                        "gemm_general_w8a16");
 }
 
+int iree_mi355x_attention_f16_strided(
+    const void *q, const void *k, const void *v, void *o, int64_t batch,
+    int64_t heads, int64_t kv_heads, int64_t seq_q, int64_t seq_kv,
+    int64_t head_dim, float scale, uint32_t flags,
+    const iree_mi355x_attention_strides_t *strides, void *stream) {
+  const char *who = "attention_f16";
+  if (flags & ~IREE_MI355X_ATTENTION_CAUSAL)
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: unknown flag bits 0x%x",
+                who, flags);
+  if (batch < 0 || heads < 0 || kv_heads < 0 || seq_q < 0 || seq_kv < 0 ||
+      head_dim < 0)
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: negative extent", who);
+  if (!std::isfinite(scale))
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: scale not finite", who);
+  if (!strides)
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: null strides", who);
+  if (batch == 0 || heads == 0 || seq_q == 0)
+    return ok();
+  if (kv_heads == 0 || heads % kv_heads != 0)
+    return fail(IREE_MI355X_INVALID_ARGUMENT,
+                "%s: %lld query heads are not a multiple of %lld KV heads",
+                who, (long long)heads, (long long)kv_heads);
+  if (head_dim != 64 && head_dim != 128)
+    return fail(IREE_MI355X_UNSUPPORTED,
+                "%s: head_dim %lld (64 or 128 supported)", who,
+                (long long)head_dim);
+  if (!q || !o || (seq_kv > 0 && (!k || !v)))
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: null pointer", who);
+  const int64_t *st[4] = {strides->q, strides->k, strides->v, strides->o};
+  for (int t = 0; t < 4; ++t)
+    for (int i = 0; i < 3; ++i)
+      if (st[t][i] < 0)
+        return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: negative stride", who);
+  if (strides->o[2] < head_dim)
+    return fail(IREE_MI355X_INVALID_ARGUMENT,
+                "%s: o row stride %lld overlaps its rows", who,
+                (long long)strides->o[2]);
+  // The copies and stores move 16-byte chunks of rows: every base, and
+  // every stride (in bytes), must keep them aligned.
+  for (int t = 0; t < 4; ++t)
+    for (int i = 0; i < 3; ++i)
+      if (st[t][i] % 8 != 0)
+        return fail(IREE_MI355X_MISALIGNED,
+                    "%s: strides must be multiples of 8 elements", who);
+  if (!aligned(q, 16) || !aligned(o, 16) || (k && !aligned(k, 16)) ||
+      (v && !aligned(v, 16)))
+    return fail(IREE_MI355X_MISALIGNED,
+                "%s: q/k/v/o must be 16-byte aligned", who);
+  const int64_t q_blocks = (seq_q + 127) / 128;
+  if (batch >= kMaxExtent || heads >= kMaxExtent || seq_q >= kMaxExtent ||
+      seq_kv >= kMaxExtent || batch * heads * q_blocks >= kMaxExtent)
+    return fail(IREE_MI355X_UNSUPPORTED, "%s: problem too large", who);
+  // Q, K and V rows are copied with a 32-bit byte offset from their head's
+  // first row.
+  const int64_t row_bytes = head_dim * 2;
+  auto head_span = [&](const int64_t *s, int64_t rows) -> int64_t {
+    if (rows <= 1)
+      return rows == 1 ? row_bytes : 0;
+    const uint64_t pitch = (uint64_t)s[2] * 2;
+    if (s[2] > (int64_t)UINT32_MAX ||
+        (pitch > 0 &&
+         (uint64_t)(rows - 1) > (UINT32_MAX - (uint64_t)row_bytes) / pitch))
+      return INT64_MAX;
+    return (int64_t)((uint64_t)(rows - 1) * pitch) + row_bytes;
+  };
+  if (head_span(strides->q, seq_q) > (int64_t)UINT32_MAX ||
+      head_span(strides->k, seq_kv) > (int64_t)UINT32_MAX ||
+      head_span(strides->v, seq_kv) > (int64_t)UINT32_MAX)
+    return fail(IREE_MI355X_UNSUPPORTED,
+                "%s: a head's rows span more than 4 GiB", who);
+  if (dry_run(0))
+    return ok();
+  AttentionLayout layout;
+  for (int i = 0; i < 3; ++i) {
+    layout.q[i] = strides->q[i];
+    layout.k[i] = strides->k[i];
+    layout.v[i] = strides->v[i];
+    layout.o[i] = strides->o[i];
+  }
+  layout.heads = (int)heads;
+  layout.group = (int)(heads / kv_heads);
+  layout.seq_q = (int)seq_q;
+  layout.seq_kv = (int)seq_kv;
+  return launch_status(
+      launch_attention(q, k, v, o, batch, layout, head_dim, scale,
+                       (flags & IREE_MI355X_ATTENTION_CAUSAL) ? 1 : 0, stream),
+      "attention_fwd");
+}
+
 int iree_mi355x_attention_f16(const void *q, const void *k, const void *v,
                               void *o, int64_t batch, int64_t heads,
                               int64_t seq_q, int64_t seq_kv, int64_t head_dim,
                               float scale, uint32_t flags, void *stream) {
-  if (flags & ~IREE_MI355X_ATTENTION_CAUSAL)
-    return fail(IREE_MI355X_INVALID_ARGUMENT,
-                "attention_f16: unknown flag bits 0x%x", flags);
-  if (batch < 0 || heads < 0 || seq_q < 0 || seq_kv < 0 || head_dim < 0)
-    return fail(IREE_MI355X_INVALID_ARGUMENT, "attention_f16: negative extent");
-  if (!std::isfinite(scale))
-    return fail(IREE_MI355X_INVALID_ARGUMENT, "attention_f16: scale not finite");
-  if (batch == 0 || heads == 0 || seq_q == 0)
-    return ok();
-  if (head_dim != 64 && head_dim != 128)
-    return fail(IREE_MI355X_UNSUPPORTED,
-                "attention_f16: head_dim %lld (64 or 128 supported)",
-                (long long)head_dim);
-  if (!q || !o || (seq_kv > 0 && (!k || !v)))
-    return fail(IREE_MI355X_INVALID_ARGUMENT, "attention_f16: null pointer");
-  if (!aligned(q, 16) || !aligned(o, 16) || (k && !aligned(k, 16)) ||
-      (v && !aligned(v, 16)))
-    return fail(IREE_MI355X_MISALIGNED,
-                "attention_f16: q/k/v/o must be 16-byte aligned");
-  const int64_t q_blocks = (seq_q + 127) / 128;
-  if (batch * heads * q_blocks >= kMaxExtent || seq_q >= kMaxExtent ||
-      seq_kv >= kMaxExtent || batch * heads * (seq_q > seq_kv ? seq_q : seq_kv) *
-                                      head_dim >= ((int64_t)1 << 62))
+  // Contiguous [B, H, S, D] operands, one KV head per query head.
+  if (heads >= kMaxExtent || seq_q >= kMaxExtent || seq_kv >= kMaxExtent ||
+      head_dim >= kMaxExtent)
     return fail(IREE_MI355X_UNSUPPORTED, "attention_f16: problem too large");
-  // The Q / K / V copies address a plane with a 32-bit byte offset.
-  if ((seq_q > seq_kv ? seq_q : seq_kv) * head_dim * 2 > (int64_t)UINT32_MAX)
-    return fail(IREE_MI355X_UNSUPPORTED,
-                "attention_f16: seq %lld x head_dim exceeds 4 GiB per head",
-                (long long)(seq_q > seq_kv ? seq_q : seq_kv));
-  if (dry_run(0))
-    return ok();
-  return launch_status(
-      launch_attention(q, k, v, o, batch, heads, seq_q, seq_kv, head_dim, scale,
-                       (flags & IREE_MI355X_ATTENTION_CAUSAL) ? 1 : 0, stream),
-      "attention_fwd");
+  iree_mi355x_attention_strides_t s;
+  const int64_t qs[3] = {heads * seq_q * head_dim, seq_q * head_dim, head_dim};
+  const int64_t ks[3] = {heads * seq_kv * head_dim, seq_kv * head_dim,
+                         head_dim};
+  for (int i = 0; i < 3; ++i) {
+    s.q[i] = s.o[i] = qs[i];
+    s.k[i] = s.v[i] = ks[i];
+  }
+  return iree_mi355x_attention_f16_strided(q, k, v, o, batch, heads, heads,
+                                           seq_q, seq_kv, head_dim, scale,
+                                           flags, &s, stream);
 }
 
 }  // extern "C"

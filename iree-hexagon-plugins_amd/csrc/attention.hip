@@ -115,11 +115,16 @@ __device__ __forceinline__ int v_swizzle(int key) {
   return D == 128 ? 4 * (key & 3) : 4 * ((key >> 1) & 1);
 }
 
-template <int D>
+// CONTIG: every operand is contiguous [B, H, S, D] with one KV head per
+// query head (the layout's strides are then not read): rows are one
+// compile-time row size apart and a plane's base is its index times its
+// size, so the copies add no scalar arithmetic.
+template <int D, bool CONTIG>
 __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
     const f16 *__restrict__ Q, const f16 *__restrict__ K,
-    const f16 *__restrict__ V, f16 *__restrict__ O, int heads, int seq_q,
-    int seq_kv, float scale_log2, int causal) {
+    const f16 *__restrict__ V, f16 *__restrict__ O, AttentionLayout L,
+    float scale_log2, int causal) {
+  const int heads = L.heads, seq_q = L.seq_q, seq_kv = L.seq_kv;
   constexpr int DS = D / 16;       // 16-wide d steps of S^T = K Q^T
   constexpr int DT = D / 32;       // 32-row d tiles of O^T
   constexpr int ROW = D * 2;       // bytes per staged K / V row
@@ -159,8 +164,30 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
   const int pair = (int)(blockIdx.x / (unsigned)planes);
   const int plane = (int)(blockIdx.x % (unsigned)planes);
   const int n_items = q_blocks - 1 - pair == pair ? 1 : 2;
-  const int64_t q_off = (int64_t)plane * seq_q * D;
-  const int64_t kv_off = (int64_t)plane * seq_kv * D;
+  // The plane's (batch, query head) and the KV head it reads; its rows of
+  // Q, K, V and O start at these bases, one row pitch (bytes) apart.
+  const char *Qp, *Kp, *Vp;
+  f16 *Op;
+  uint32_t q_pitch, k_pitch, v_pitch;
+  int64_t o_row;
+  if constexpr (CONTIG) {
+    Qp = (const char *)(Q + (int64_t)plane * seq_q * D);
+    Kp = (const char *)(K + (int64_t)plane * seq_kv * D);
+    Vp = (const char *)(V + (int64_t)plane * seq_kv * D);
+    Op = O + (int64_t)plane * seq_q * D;
+    q_pitch = k_pitch = v_pitch = ROW;
+    o_row = D;
+  } else {
+    const int pb = plane / heads, ph = plane - pb * heads, pk = ph / L.group;
+    Qp = (const char *)(Q + pb * L.q[0] + ph * L.q[1]);
+    Kp = (const char *)(K + pb * L.k[0] + pk * L.k[1]);
+    Vp = (const char *)(V + pb * L.v[0] + pk * L.v[1]);
+    Op = O + pb * L.o[0] + ph * L.o[1];
+    q_pitch = (uint32_t)(2 * L.q[2]);
+    k_pitch = (uint32_t)(2 * L.k[2]);
+    v_pitch = (uint32_t)(2 * L.v[2]);
+    o_row = L.o[2];
+  }
 
   // Per query block: this wave's first row, this group's key blocks (local
   // block i is key block 2 i + grp) and the barrier slots of the block's
@@ -193,8 +220,8 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
   // block copy is PASSES instructions per wave.
   const int c_row = lane / CH, c_phys = lane % CH;
   IHP_LDS char *lds = (IHP_LDS char *)smem + grp * RING;
-  auto copy_block = [&](const f16 *src, int kb, IHP_LDS char *dst,
-                        auto is_v) {
+  auto copy_block = [&](const char *src, uint32_t pitch, int kb,
+                        IHP_LDS char *dst, auto is_v) {
     const int kv0 = kb * kBKV;
     // Opaque copies: the per-pass addresses are recomputed at each copy
     // instead of being hoisted into live registers.
@@ -207,10 +234,9 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
       key = key < seq_kv ? key : seq_kv - 1;
       const int sw = decltype(is_v)::value ? v_swizzle<D>(row)
                                            : k_swizzle<D>(row);
-      // Uniform plane base + 32-bit lane offset: one VGPR per address.
-      const uint32_t off = (uint32_t)key * ROW + 16u * (lane_chunk ^ sw);
-      global_to_lds_16((const char *)(src + kv_off) + off,
-                       dst + (p * 4 + wq) * ROWS_PER_INSN * ROW);
+      // Uniform head base + 32-bit lane offset: one VGPR per address.
+      const uint32_t off = (uint32_t)key * pitch + 16u * (lane_chunk ^ sw);
+      global_to_lds_16(src + off, dst + (p * 4 + wq) * ROWS_PER_INSN * ROW);
     }
   };
   // Full key blocks take the saddr copy form: the lane's byte offset inside
@@ -222,23 +248,23 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
   // copy_block.
   const int f_row = wq * ROWS_PER_INSN + c_row;
   const uint32_t k_voff =
-      (uint32_t)(f_row * ROW + 16 * (c_phys ^ k_swizzle<D>(f_row)));
+      (uint32_t)f_row * k_pitch + 16u * (c_phys ^ k_swizzle<D>(f_row));
   const uint32_t v_voff =
-      (uint32_t)(f_row * ROW + 16 * (c_phys ^ v_swizzle<D>(f_row)));
-  auto copy_full = [&](const f16 *src, int kb, IHP_LDS char *dst,
-                       uint32_t voff) {
-    const char *base = (const char *)(src + kv_off) + (int64_t)kb * BLK;
+      (uint32_t)f_row * v_pitch + 16u * (c_phys ^ v_swizzle<D>(f_row));
+  auto copy_full = [&](const char *src, uint32_t pitch, int kb,
+                       IHP_LDS char *dst, uint32_t voff) {
+    const char *base = src + (int64_t)kb * kBKV * pitch;
 #pragma unroll
     for (int p = 0; p < PASSES; ++p)
-      global_to_lds_16s(base + p * 4 * ROWS_PER_INSN * ROW, voff,
+      global_to_lds_16s(base + (int64_t)p * 4 * ROWS_PER_INSN * pitch, voff,
                         dst + (p * 4 + wq) * ROWS_PER_INSN * ROW);
   };
   auto copy_k = [&](int i) {
     const int kb = 2 * i + grp;
     if ((kb + 1) * kBKV <= seq_kv)
-      copy_full(K, kb, lds + (i & 1) * BLK, k_voff);
+      copy_full(Kp, k_pitch, kb, lds + (i & 1) * BLK, k_voff);
     else
-      copy_block(K, kb, lds + (i & 1) * BLK, std::false_type());
+      copy_block(Kp, k_pitch, kb, lds + (i & 1) * BLK, std::false_type());
   };
   // The query block's rows into the V slots 1 (all 8 waves, PASSES
   // instructions each); rows past seq_q are clamped to the last row (their
@@ -253,16 +279,16 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
       const int r = r0 + lane_row;
       const int row = min(qrow0 + r, seq_q - 1);
       const uint32_t off =
-          (uint32_t)row * ROW + 16u * (lane_chunk ^ k_swizzle<D>(r));
-      global_to_lds_16((const char *)(Q + q_off) + off, staged_row(r0, 3));
+          (uint32_t)row * q_pitch + 16u * (lane_chunk ^ k_swizzle<D>(r));
+      global_to_lds_16(Qp + off, staged_row(r0, 3));
     }
   };
   auto copy_v = [&](int i) {
     const int kb = 2 * i + grp;
     if ((kb + 1) * kBKV <= seq_kv)
-      copy_full(V, kb, lds + (2 + (i & 1)) * BLK, v_voff);
+      copy_full(Vp, v_pitch, kb, lds + (2 + (i & 1)) * BLK, v_voff);
     else
-      copy_block(V, kb, lds + (2 + (i & 1)) * BLK, std::true_type());
+      copy_block(Vp, v_pitch, kb, lds + (2 + (i & 1)) * BLK, std::true_type());
   };
   // A query block's first key blocks (slots 0); K(1) goes out separately,
   // last, and the block's first barrier does not wait for it.
@@ -377,7 +403,7 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
       const i32x4 v = *(const IHP_LDS i32x4 *)(
           staged_row(r, 1) + 16 * (c_phys ^ k_swizzle<D>(r)));
       if (qrow0 + r < seq_q)
-        *(i32x4 *)(O + q_off + (int64_t)(qrow0 + r) * D + 8 * c_phys) = v;
+        *(i32x4 *)(Op + (int64_t)(qrow0 + r) * o_row + 8 * c_phys) = v;
     }
   };
 
@@ -715,27 +741,38 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
 }
 
 hipError_t launch_attention(const void *q, const void *k, const void *v,
-                            void *o, int64_t batch, int64_t heads,
-                            int64_t seq_q, int64_t seq_kv, int64_t head_dim,
+                            void *o, int64_t batch,
+                            const AttentionLayout &layout, int64_t head_dim,
                             float scale, int causal, void *stream) {
-  const int64_t q_blocks = (seq_q + kBQ - 1) / kBQ;
-  const int64_t planes = batch * heads;
+  const int64_t q_blocks = (layout.seq_q + kBQ - 1) / kBQ;
+  const int64_t planes = batch * layout.heads;
   // One workgroup per pair of query blocks (q_blocks - 1 - k, k).
   dim3 grid((unsigned)((q_blocks + 1) / 2 * planes));
   const float scale_log2 = scale * 1.4426950408889634f;  // log2(e)
+  const int64_t d = head_dim, sq = layout.seq_q, skv = layout.seq_kv,
+                h = layout.heads;
+  const bool contig =
+      layout.group == 1 && layout.q[2] == d && layout.o[2] == d &&
+      layout.k[2] == d && layout.v[2] == d && layout.q[1] == sq * d &&
+      layout.o[1] == sq * d && layout.k[1] == skv * d &&
+      layout.v[1] == skv * d && layout.q[0] == h * sq * d &&
+      layout.o[0] == h * sq * d && layout.k[0] == h * skv * d &&
+      layout.v[0] == h * skv * d;
+  const void *kernel;
   if (head_dim == 128)
-    hipLaunchKernelGGL((attention_fwd_kernel<128>), grid, dim3(kThreads), 0,
-                       (hipStream_t)stream, (const f16 *)q, (const f16 *)k,
-                       (const f16 *)v, (f16 *)o, (int)heads, (int)seq_q,
-                       (int)seq_kv, scale_log2, causal);
+    kernel = contig ? (const void *)&attention_fwd_kernel<128, true>
+                    : (const void *)&attention_fwd_kernel<128, false>;
   else if (head_dim == 64)
-    hipLaunchKernelGGL((attention_fwd_kernel<64>), grid, dim3(kThreads), 0,
-                       (hipStream_t)stream, (const f16 *)q, (const f16 *)k,
-                       (const f16 *)v, (f16 *)o, (int)heads, (int)seq_q,
-                       (int)seq_kv, scale_log2, causal);
+    kernel = contig ? (const void *)&attention_fwd_kernel<64, true>
+                    : (const void *)&attention_fwd_kernel<64, false>;
   else
     return hipErrorInvalidValue;
-  return hipGetLastError();
+  const f16 *qp = (const f16 *)q, *kp = (const f16 *)k, *vp = (const f16 *)v;
+  f16 *op = (f16 *)o;
+  AttentionLayout l = layout;
+  void *args[] = {&qp, &kp, &vp, &op, &l, (void *)&scale_log2, &causal};
+  return hipLaunchKernel(kernel, grid, dim3(kThreads), args, 0,
+                         (hipStream_t)stream);
 }
 
 }  // namespace ihp
@@ -744,8 +781,10 @@ namespace ihp {
 
 const KernelEntry *attention_kernels(int *count) {
   static const KernelEntry all[] = {
-      {"attention_fwd_d128", (const void *)&attention_fwd_kernel<128>, kThreads, kExportAttention},
-      {"attention_fwd_d64", (const void *)&attention_fwd_kernel<64>, kThreads, kExportAttention},
+      {"attention_fwd_d128", (const void *)&attention_fwd_kernel<128, true>, kThreads, kExportAttention},
+      {"attention_fwd_d64", (const void *)&attention_fwd_kernel<64, true>, kThreads, kExportAttention},
+      {"attention_fwd_d128_strided", (const void *)&attention_fwd_kernel<128, false>, kThreads, kExportAttention},
+      {"attention_fwd_d64_strided", (const void *)&attention_fwd_kernel<64, false>, kThreads, kExportAttention},
   };
   *count = (int)(sizeof(all) / sizeof(all[0]));
   return all;

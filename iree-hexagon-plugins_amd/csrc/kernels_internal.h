@@ -175,9 +175,19 @@ size_t gemv_workspace_bytes(int64_t m, int64_t n, int64_t k, int w_bytes,
 hipError_t launch_gemv(const MatmulArgs &a, int w_bytes, const void *scale,
                        int out_f32, void *workspace);
 
+// Where attention's operands live: element strides of the batch, head and
+// row dimensions of each (d is contiguous), and the query heads that share
+// one K / V head (query head h reads KV head h / group). Checked on the host:
+// every stride a multiple of 8 elements, every row of K and V within 4 GiB
+// of its head's base (the copies address a head with 32-bit offsets).
+struct AttentionLayout {
+  int64_t q[3], k[3], v[3], o[3];  // batch, head, row
+  int heads, group, seq_q, seq_kv;
+};
+
 hipError_t launch_attention(const void *q, const void *k, const void *v,
-                            void *o, int64_t batch, int64_t heads,
-                            int64_t seq_q, int64_t seq_kv, int64_t head_dim,
+                            void *o, int64_t batch,
+                            const AttentionLayout &layout, int64_t head_dim,
                             float scale, int causal, void *stream);
 
 #ifdef __HIP_DEVICE_COMPILE__

@@ -153,31 +153,56 @@ int dispatch_w8a16(const iree_mi355x_executable_environment_t *,
       c.ldc, c.flags, s->workspace, s->workspace_bytes, s->stream);
 }
 
+// "attention_f16": batch heads seq_q seq_kv head_dim scale_bits flags, then
+// optionally kv_heads and the (batch, head, row) element strides of q, k, v
+// and o as lo/hi pairs (32 words in all); without them the operands are
+// contiguous [B, H, S, D] with one KV head per query head.
 int dispatch_attention(const iree_mi355x_executable_environment_t *,
                        const iree_mi355x_executable_dispatch_state_t *s) {
   DryRunScope dry(s);
+  const char *who = "attention_f16";
   if (!s || s->constant_count < 7 || !s->constants || s->binding_count < 4 ||
       !s->binding_ptrs || !s->binding_lengths)
     return fail(IREE_MI355X_INVALID_ARGUMENT,
-                "attention_f16: constants or bindings missing");
+                "%s: constants or bindings missing", who);
   const uint32_t *c = s->constants;
   const int64_t batch = c[0], heads = c[1], sq = c[2], skv = c[3], d = c[4];
   float scale;
   memcpy(&scale, &c[5], 4);
-  const int64_t planes = mul_checked(batch, heads);
-  const int64_t q_bytes = mul_checked(mul_checked(mul_checked(planes, sq), d), 2);
-  const int64_t kv_bytes =
-      mul_checked(mul_checked(mul_checked(planes, skv), d), 2);
-  int st;
-  if ((st = check_binding(s, 0, q_bytes, "attention_f16")) ||
-      (st = check_binding(s, 1, kv_bytes, "attention_f16")) ||
-      (st = check_binding(s, 2, kv_bytes, "attention_f16")) ||
-      (st = check_binding(s, 3, q_bytes, "attention_f16")))
-    return st;
-  return iree_mi355x_attention_f16(s->binding_ptrs[0], s->binding_ptrs[1],
-                                   s->binding_ptrs[2], s->binding_ptrs[3],
-                                   batch, heads, sq, skv, d, scale, c[6],
-                                   s->stream);
+  const bool strided = s->constant_count >= 32;
+  int64_t kv_heads = heads;
+  iree_mi355x_attention_strides_t st;
+  int64_t *dst[4] = {st.q, st.k, st.v, st.o};
+  for (int t = 0; t < 4; ++t) {
+    const bool kv = t == 1 || t == 2;
+    const int64_t rows = kv ? skv : sq;
+    const int64_t one[3] = {mul_checked(mul_checked(heads, rows), d),
+                            mul_checked(rows, d), d};
+    for (int i = 0; i < 3; ++i)
+      dst[t][i] = strided ? u64(c, 8 + 2 * (3 * t + i)) : one[i];
+  }
+  if (strided)
+    kv_heads = c[7];
+  // Bytes from an operand's first element to the end of its last row.
+  auto reach = [&](const int64_t *sd, int64_t planes_heads, int64_t rows) {
+    if (batch <= 0 || planes_heads <= 0 || rows <= 0)
+      return (int64_t)0;
+    const int64_t last = add_checked(
+        add_checked(mul_checked(batch - 1, sd[0]),
+                    mul_checked(planes_heads - 1, sd[1])),
+        mul_checked(rows - 1, sd[2]));
+    return mul_checked(add_checked(last, d), 2);
+  };
+  int st_ok;
+  if ((st_ok = check_binding(s, 0, reach(st.q, heads, sq), who)) ||
+      (st_ok = check_binding(s, 1, reach(st.k, kv_heads, skv), who)) ||
+      (st_ok = check_binding(s, 2, reach(st.v, kv_heads, skv), who)) ||
+      (st_ok = check_binding(s, 3, reach(st.o, heads, sq), who)))
+    return st_ok;
+  return iree_mi355x_attention_f16_strided(
+      s->binding_ptrs[0], s->binding_ptrs[1], s->binding_ptrs[2],
+      s->binding_ptrs[3], batch, heads, kv_heads, sq, skv, d, scale, c[6],
+      &st, s->stream);
 }
 
 // "batch_matmul_f16": the matmul_f16 constants, then batch, stride_a,

@@ -62,13 +62,17 @@ def _load():
     lib.oracle_attention_f16.argtypes = [p, p, p, p, i64, i64, i64, i64, i64,
                                          ctypes.c_float, ctypes.c_int,
                                          ctypes.c_int]
+    lib.oracle_attention_f16_strided.argtypes = [
+        p, p, p, p, i64, i64, i64, i64, i64, i64, ctypes.POINTER(i64),
+        ctypes.c_float, ctypes.c_int, ctypes.c_int]
     lib.oracle_choose_static_tiling_factor.restype = i64
     lib.oracle_choose_static_tiling_factor.argtypes = [i64, i64, i64]
     lib.oracle_select_hmx_tile_sizes.argtypes = [p, p, ctypes.c_int, i64,
                                                  ctypes.c_int, i64, i64, p]
     for name in ("oracle_matmul_f16", "oracle_matmul_i8", "oracle_w8a16",
                  "oracle_batch_matmul_f16",
-                 "oracle_attention_f16", "oracle_select_hmx_tile_sizes"):
+                 "oracle_attention_f16", "oracle_attention_f16_strided",
+                 "oracle_select_hmx_tile_sizes"):
         getattr(lib, name).restype = ctypes.c_int
     _lib = lib
     return lib
@@ -217,19 +221,34 @@ def w8a16(x, w, scale, *, w_transposed=False, threads=None) -> np.ndarray:
     return y
 
 
-def attention_f16(q, k, v, *, scale=None, causal=True, threads=None):
-    """softmax(QK^T*scale + causal mask) V for [B,H,S,D] f16 tensors."""
-    q = np.ascontiguousarray(q, np.float16)
-    k = np.ascontiguousarray(k, np.float16)
-    v = np.ascontiguousarray(v, np.float16)
+def _rows_view(a):
+    """An f16 array whose last dimension is contiguous (a strided view is
+    kept as it is) and its first three element strides."""
+    if a.dtype != np.float16 or a.strides[-1] != 2:
+        a = np.ascontiguousarray(a, np.float16)
+    return a, [st // 2 for st in a.strides[:3]]
+
+
+def attention_f16(q, k, v, *, scale=None, causal=True, out=None, threads=None):
+    """softmax(QK^T*scale + causal mask) V for q [B,Hq,Sq,D] and k, v
+    [B,Hkv,Skv,D] f16 arrays (strided views allowed: the last dimension
+    contiguous). Hq is a multiple of Hkv and query head h reads KV head
+    h // (Hq // Hkv). The result goes into `out` ([B,Hq,Sq,D], possibly a
+    strided view) or a new contiguous array."""
+    q, qs = _rows_view(q)
+    k, ks = _rows_view(k)
+    v, vs = _rows_view(v)
     b, h, sq, d = q.shape
-    skv = k.shape[2]
+    hkv, skv = k.shape[1], k.shape[2]
     if scale is None:
         scale = 1.0 / float(np.sqrt(d))
-    o = np.empty_like(q)
-    rc = _load().oracle_attention_f16(_ptr(q), _ptr(k), _ptr(v), _ptr(o), b, h,
-                                      sq, skv, d, float(scale), int(causal),
-                                      threads or default_threads())
+    o = np.empty_like(q, order="C") if out is None else out
+    assert o.dtype == np.float16 and o.shape == q.shape and o.strides[-1] == 2
+    os_ = [st // 2 for st in o.strides[:3]]
+    strides = (ctypes.c_int64 * 12)(*(qs + ks + vs + os_))
+    rc = _load().oracle_attention_f16_strided(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(o), b, h, hkv, sq, skv, d, strides,
+        float(scale), int(causal), threads or default_threads())
     assert rc == 0, rc
     return o
 

@@ -435,23 +435,29 @@ int oracle_w8a16(const uint16_t *x, const int8_t *w, const uint16_t *scale,
 
 /* ---------------------------------------------------------- attention ---- */
 
-int oracle_attention_f16(const uint16_t *q, const uint16_t *k,
-                         const uint16_t *v, uint16_t *o, int64_t batch,
-                         int64_t heads, int64_t seq_q, int64_t seq_kv,
-                         int64_t head_dim, float scale, int causal,
-                         int threads) {
-  if (batch < 0 || heads < 0 || seq_q < 0 || seq_kv < 0 || head_dim < 0)
+int oracle_attention_f16_strided(const uint16_t *q, const uint16_t *k,
+                                 const uint16_t *v, uint16_t *o,
+                                 int64_t batch, int64_t heads,
+                                 int64_t kv_heads, int64_t seq_q,
+                                 int64_t seq_kv, int64_t head_dim,
+                                 const int64_t strides[12], float scale,
+                                 int causal, int threads) {
+  if (batch < 0 || heads < 0 || kv_heads <= 0 || seq_q < 0 || seq_kv < 0 ||
+      head_dim < 0 || heads % kv_heads != 0)
     return 1;
-  const int64_t planes = batch * heads;
+  const int64_t group = heads / kv_heads;
+  const int64_t *qs = strides, *ks = strides + 3, *vs = strides + 6,
+                *os = strides + 9;
   if (threads < 1)
     threads = 1;
 #pragma omp parallel for num_threads(threads) schedule(dynamic)
-  for (int64_t row = 0; row < planes * seq_q; ++row) {
+  for (int64_t row = 0; row < batch * heads * seq_q; ++row) {
     const int64_t plane = row / seq_q;
     const int64_t i = row % seq_q;
-    const uint16_t *qi = q + (plane * seq_q + i) * head_dim;
-    const uint16_t *kp = k + plane * seq_kv * head_dim;
-    const uint16_t *vp = v + plane * seq_kv * head_dim;
+    const int64_t b = plane / heads, h = plane % heads, hk = h / group;
+    const uint16_t *qi = q + b * qs[0] + h * qs[1] + i * qs[2];
+    const uint16_t *kp = k + b * ks[0] + hk * ks[1];
+    const uint16_t *vp = v + b * vs[0] + hk * vs[1];
     float *qf = (float *)malloc(sizeof(float) * (size_t)(head_dim + 1));
     float *s = (float *)malloc(sizeof(float) * (size_t)(seq_kv + 1));
     float *acc = (float *)calloc((size_t)head_dim + 1, sizeof(float));
@@ -462,7 +468,7 @@ int oracle_attention_f16(const uint16_t *q, const uint16_t *k,
     for (int64_t j = 0; j <= last; ++j) {
       float dot = 0.0f;
       for (int64_t d = 0; d < head_dim; ++d) {
-        float prod = qf[d] * oracle_f16_to_f32(kp[j * head_dim + d]);
+        float prod = qf[d] * oracle_f16_to_f32(kp[j * ks[2] + d]);
         dot = dot + prod;
       }
       s[j] = dot * scale;
@@ -474,11 +480,11 @@ int oracle_attention_f16(const uint16_t *q, const uint16_t *k,
       float p = expf(s[j] - mx);
       sum = sum + p;
       for (int64_t d = 0; d < head_dim; ++d) {
-        float prod = p * oracle_f16_to_f32(vp[j * head_dim + d]);
+        float prod = p * oracle_f16_to_f32(vp[j * vs[2] + d]);
         acc[d] = acc[d] + prod;
       }
     }
-    uint16_t *oi = o + (plane * seq_q + i) * head_dim;
+    uint16_t *oi = o + b * os[0] + h * os[1] + i * os[2];
     for (int64_t d = 0; d < head_dim; ++d)
       oi[d] = oracle_f32_to_f16(last >= 0 ? acc[d] / sum : 0.0f);
     free(qf);
@@ -486,6 +492,26 @@ int oracle_attention_f16(const uint16_t *q, const uint16_t *k,
     free(acc);
   }
   return 0;
+}
+
+int oracle_attention_f16(const uint16_t *q, const uint16_t *k,
+                         const uint16_t *v, uint16_t *o, int64_t batch,
+                         int64_t heads, int64_t seq_q, int64_t seq_kv,
+                         int64_t head_dim, float scale, int causal,
+                         int threads) {
+  if (batch < 0 || heads < 0 || seq_q < 0 || seq_kv < 0 || head_dim < 0)
+    return 1;
+  if (heads == 0)
+    return 0;
+  const int64_t st[12] = {heads * seq_q * head_dim,  seq_q * head_dim,
+                          head_dim,                  heads * seq_kv * head_dim,
+                          seq_kv * head_dim,         head_dim,
+                          heads * seq_kv * head_dim, seq_kv * head_dim,
+                          head_dim,                  heads * seq_q * head_dim,
+                          seq_q * head_dim,          head_dim};
+  return oracle_attention_f16_strided(q, k, v, o, batch, heads, heads, seq_q,
+                                      seq_kv, head_dim, st, scale, causal,
+                                      threads);
 }
 
 /* ------------------------------------------------------------ planner ---- */

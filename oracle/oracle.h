@@ -119,6 +119,19 @@ int oracle_attention_f16(const uint16_t *q, const uint16_t *k,
                          int64_t head_dim, float scale, int causal,
                          int threads);
 
+/* The same over strided operands with grouped-query heads: strides holds
+ * the (batch, head, row) element strides of q, k, v and o in that order (d
+ * contiguous), and query head h reads KV head h / (heads / kv_heads), as the
+ * query heads sharing a KV head form one matmul's rows in
+ * IT/models/micro/attention-cache-slice-f16/model.py:17-29. */
+int oracle_attention_f16_strided(const uint16_t *q, const uint16_t *k,
+                                 const uint16_t *v, uint16_t *o,
+                                 int64_t batch, int64_t heads,
+                                 int64_t kv_heads, int64_t seq_q,
+                                 int64_t seq_kv, int64_t head_dim,
+                                 const int64_t strides[12], float scale,
+                                 int causal, int threads);
+
 /* chooseStaticTilingFactor, CG/Strategy/Planning/Strategies/
  * StrategySupport.cpp:38-69. dynamic bound is passed as INT64_MIN. */
 int64_t oracle_choose_static_tiling_factor(int64_t static_bound,

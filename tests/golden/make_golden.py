@@ -8,6 +8,9 @@ Nothing here imports or runs the reference. The fixtures are:
                     model.py, tolerances copied from their model.yaml;
   * attention_*.npz F.scaled_dot_product_attention in f32 on small shapes (the
                     function of IT/models/micro/attention-4x1024x128-f16);
+  * attention_cache_slice.npz the grouped-query attention over a KV-cache
+                    slice of IT/models/micro/attention-cache-slice-f16: its
+                    shapes, seeds, tolerances, and its forward restated here;
   * matmul_i8.npz   int8 x int8 with an int64 numpy product;
   * tile_search.json the VTCM tile-search goldens of
                     plugins/compiler/hexagon/test/codegen/strategy/
@@ -61,6 +64,42 @@ def write_attention():
                  causal=np.array(causal), tol=np.array([5e-2, 5e-2, 1.0]))
 
 
+def write_attention_cache_slice():
+    # IT/models/micro/attention-cache-slice-f16/model.{py,yaml}: query
+    # [1, 9, 64, 64] normal seed 0, K / V caches [1, 3, 128, 64] normal seeds
+    # 1 and 2, attention over the first 64 cache rows, 3 query heads per KV
+    # head, output [batch, seq, heads, dim]. The model's forward restated:
+    # the query heads sharing a KV head become one matmul's rows, scores in
+    # f16 then scaled in f32, softmax in f32, weights back to f16. Run in
+    # f16 as written ("expected", what the reference harness compares with
+    # under the model.yaml tolerances) and in f32 ("expected_f32").
+    q, kc, vc = (normal(shape, s) for s, shape in
+                 enumerate([(1, 9, 64, 64), (1, 3, 128, 64), (1, 3, 128, 64)]))
+    context = 64
+
+    def forward(query, k_cache, v_cache):
+        key = k_cache[:, :, :context, :]
+        value = v_cache[:, :, :context, :]
+        batch, q_heads, q_len, head_dim = query.shape
+        kv_heads = key.shape[1]
+        group = q_heads // kv_heads
+        query = query.reshape(batch, kv_heads, group * q_len, head_dim)
+        scores = torch.matmul(query, key.transpose(2, 3)).float() \
+            * head_dim ** -0.5
+        weights = torch.softmax(scores, dim=-1).to(query.dtype)
+        out = torch.matmul(weights, value)
+        out = out.view(batch, kv_heads, group, q_len, head_dim)
+        return out.permute(0, 3, 1, 2, 4).reshape(batch, q_len, q_heads,
+                                                  head_dim)
+    expected = forward(q, kc, vc).float()
+    expected_f32 = forward(q.float(), kc.float(), vc.float())
+    np.savez(os.path.join(HERE, "attention_cache_slice.npz"), q=q.numpy(),
+             k_cache=kc.numpy(), v_cache=vc.numpy(),
+             context=np.array(context), expected=expected.numpy(),
+             expected_f32=expected_f32.numpy(),
+             tol=np.array([5e-2, 5e-2, 1.0]))
+
+
 def write_i8():
     g = torch.Generator().manual_seed(0)
     a = torch.randint(-128, 128, (37, 91), generator=g).to(torch.int8)
@@ -101,6 +140,7 @@ def write_tile_search():
 if __name__ == "__main__":
     write_matmuls()
     write_attention()
+    write_attention_cache_slice()
     write_i8()
     write_tile_search()
     print("wrote", sorted(os.listdir(HERE)))

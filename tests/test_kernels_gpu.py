@@ -546,6 +546,103 @@ def test_c4_attention_full(pkg, oracle, inputs, dev):
     fp16_ok(oracle, got, ref)
 
 
+# Sequence lengths that differ (seq_q against seq_kv, both ways, a single
+# query row) and scales other than 1/sqrt(d): the product of
+# attention_layer.mlir's two 128^-1/4 factors at d = 64, 0.5, 0.297.
+@pytest.mark.parametrize("sq,skv,d,causal,scale", [
+    (128, 2048, 128, True, 0.297), (128, 2048, 128, False, 0.5),
+    (1, 2048, 128, True, 0.297), (1, 2048, 64, False, 0.5),
+    (2048, 128, 128, True, 0.5), (300, 1000, 64, True,
+                                  0.29730177875068026 ** 2),
+    (1000, 300, 64, False, 0.297), (64, 64, 128, True, 0.5),
+    # scale <= 0 takes the kernel's masked-scaling softmax on every block
+    (200, 300, 64, False, -0.3), (100, 100, 128, True, 0.0)])
+def test_attention_lengths_and_scales(pkg, oracle, dev, sq, skv, d, causal,
+                                      scale):
+    print(f"attention sq={sq} skv={skv} d={d} causal={causal} "
+          f"scale={scale}", flush=True)
+    g = torch.Generator().manual_seed(sq + 7 * skv + d)
+    q = torch.randn(1, 4, sq, d, generator=g).half()
+    k = torch.randn(1, 4, skv, d, generator=g).half()
+    v = torch.randn(1, 4, skv, d, generator=g).half()
+    o = pkg.attention(q.to(dev), k.to(dev), v.to(dev), causal=causal,
+                      scale=scale)
+    got = o.cpu().numpy()
+    ref = oracle.attention_f16(q.numpy(), k.numpy(), v.numpy(), scale=scale,
+                               causal=causal)
+    fp16_ok(oracle, got, ref)
+    if causal:
+        # query 0 sees key 0 only, whatever the scale
+        assert np.array_equal(got[:, :, 0], v.numpy()[:, :, 0])
+    elif abs(scale - d ** -0.5) > 1e-2:
+        # the scale reached the kernel: the default one gives another answer
+        other = oracle.attention_f16(q.numpy(), k.numpy(), v.numpy(),
+                                     causal=causal)
+        assert oracle.fp16_parity(got, other) > 1e-2
+
+
+def test_attention_cache_slice_model(pkg, oracle, dev):
+    # integration_tests/models/micro/attention-cache-slice-f16: 9 query heads
+    # over 3 KV heads, the first 64 of 128 cache rows, output [B, S, H, D],
+    # against its golden under its model.yaml tolerances
+    d = np.load(os.path.join(GOLDEN, "attention_cache_slice.npz"))
+    ctx = int(d["context"])
+    q = torch.from_numpy(d["q"]).to(dev)
+    kc = torch.from_numpy(d["k_cache"]).to(dev)
+    vc = torch.from_numpy(d["v_cache"]).to(dev)
+    b, hq, sq, dim = q.shape
+    out = torch.full((b, sq, hq, dim), float("nan"), dtype=torch.float16,
+                     device=dev)
+    pkg.attention(q, kc[:, :, :ctx], vc[:, :, :ctx], out.permute(0, 2, 1, 3),
+                  causal=False)
+    got = out.cpu().numpy()
+    atol, rtol, rel_l2 = d["tol"]
+    for key in ("expected", "expected_f32"):
+        rel, _, close = oracle.compare_arrays(d[key], got, atol, rtol)
+        assert close and rel <= rel_l2, (key, rel)
+    fp16_ok(oracle, got, d["expected_f32"])
+
+
+@pytest.mark.parametrize("hq,hkv,s,dim,causal", [(16, 4, 1024, 128, True),
+                                                 (8, 1, 700, 64, False),
+                                                 (6, 3, 1, 128, True)])
+def test_attention_grouped_strided(pkg, oracle, dev, hq, hkv, s, dim, causal):
+    # K / V: the first s rows of a cache twice as long; Q read from and O
+    # written to [B, S, H, D] buffers
+    print(f"gqa hq={hq} hkv={hkv} s={s} d={dim} causal={causal}", flush=True)
+    g = torch.Generator().manual_seed(hq * 100 + hkv + s)
+    q_bshd = torch.randn(2, s, hq, dim, generator=g).half()
+    kc = torch.randn(2, hkv, 2 * s, dim, generator=g).half()
+    vc = torch.randn(2, hkv, 2 * s, dim, generator=g).half()
+    q_d, kc_d, vc_d = q_bshd.to(dev), kc.to(dev), vc.to(dev)
+    out = torch.full((2, s, hq, dim), float("nan"), dtype=torch.float16,
+                     device=dev)
+    pkg.attention(q_d.permute(0, 2, 1, 3), kc_d[:, :, :s], vc_d[:, :, :s],
+                  out.permute(0, 2, 1, 3), causal=causal)
+    got = out.permute(0, 2, 1, 3).cpu().numpy()
+    ref = oracle.attention_f16(q_bshd.numpy().transpose(0, 2, 1, 3),
+                               kc.numpy()[:, :, :s], vc.numpy()[:, :, :s],
+                               causal=causal)
+    fp16_ok(oracle, got, ref)
+
+
+def test_attention_strided_argument_checks(pkg, dev):
+    q = torch.zeros(1, 4, 64, 64, dtype=torch.float16, device=dev)
+    k = torch.zeros(1, 3, 64, 64, dtype=torch.float16, device=dev)
+    with pytest.raises(ValueError, match="dividing"):
+        pkg.attention(q, k, k)  # 4 query heads over 3 KV heads
+    st = pkg.AttentionStrides()
+    for f, t in (("q", q), ("k", k), ("v", k), ("o", q)):
+        getattr(st, f)[:] = list(t.stride()[:3])
+    assert pkg.library().iree_mi355x_attention_f16_strided(
+        q.data_ptr(), k.data_ptr(), k.data_ptr(), q.data_ptr(), 1, 4, 3, 64,
+        64, 64, 0.125, 0, ctypes.byref(st), None) == pkg.INVALID_ARGUMENT
+    kc = torch.zeros(1, 2, 64, 68, dtype=torch.float16, device=dev)
+    with pytest.raises(pkg.MI355XError) as e:
+        pkg.attention(q, kc[..., :64], kc[..., :64])  # row pitch 68
+    assert e.value.status == pkg.MISALIGNED
+
+
 # ------------------------------------------------------ executable library --
 
 def test_dispatch_through_export_table(pkg, oracle, dev):
@@ -574,6 +671,34 @@ def test_dispatch_through_export_table(pkg, oracle, dev):
     ref = oracle.attention_f16(q.cpu().numpy(), kk.cpu().numpy(),
                                v.cpu().numpy(), scale=0.125, causal=True)
     fp16_ok(oracle, o.cpu().numpy(), ref)
+    # the strided, grouped form: 4 query heads over 2 KV heads, K / V the
+    # first 96 rows of 160-row caches, O written [B, S, H, D]
+    q4 = torch.randn(1, 4, 128, 64, generator=g).half().to(dev)
+    kc, vc = (torch.randn(1, 2, 160, 64, generator=g).half().to(dev)
+              for _ in range(2))
+    o4 = torch.zeros(1, 128, 4, 64, dtype=torch.float16, device=dev)
+    o4v = o4.permute(0, 2, 1, 3)
+    strides = (list(q4.stride()[:3]) + list(kc.stride()[:3]) +
+               list(vc.stride()[:3]) + list(o4v.stride()[:3]))
+    consts = pkg.attention_constants(1, 4, 128, 96, 64, 0.5, 0, kv_heads=2,
+                                     strides=strides)
+    assert len(consts) == 32
+    ptrs = [q4.data_ptr(), kc.data_ptr(), vc.data_ptr(), o4.data_ptr()]
+    lens = [q4.numel() * 2, kc.numel() * 2, vc.numel() * 2, o4.numel() * 2]
+    # K is read up to the end of row 95 of KV head 1: a binding of that many
+    # bytes is enough, two bytes fewer is refused before launch
+    k_reach = ((2 - 1) * kc.stride(1) + 95 * kc.stride(2) + 64) * 2
+    assert k_reach == 32768 < lens[1]
+    st = pkg.call_export("attention_f16", consts, ptrs,
+                         [lens[0], k_reach - 2] + lens[2:], s)
+    assert st == pkg.INVALID_ARGUMENT
+    lens[1] = k_reach
+    st = pkg.call_export("attention_f16", consts, ptrs, lens, s)
+    assert st == pkg.OK, pkg.last_error()
+    ref = oracle.attention_f16(q4.cpu().numpy(), kc.cpu().numpy()[:, :, :96],
+                               vc.cpu().numpy()[:, :, :96], scale=0.5,
+                               causal=False)
+    fp16_ok(oracle, o4v.cpu().numpy(), ref)
     # batched matmul with a SiLU-gated epilogue through the export table
     z, m, n, k = 3, 64, 256, 128
     a = (torch.randn(z, m, k, generator=g) * 0.5).half()

@@ -442,7 +442,8 @@ def ew(pkg, types, body, producers, args=("i", "o"), loops="d0 d1 d2",
 
 def attention_chain(pkg, *, head=128, causal=False, guard=True, exp=True,
                     out="f16", q_scale=SCALE, bmm_init=("const", 0.0),
-                    max_init=-INF, sum_init=0.0, bmm1_body=None):
+                    max_init=-INF, sum_init=0.0, bmm1_body=None, batch=4,
+                    seq=1024):
     """The ops of attention_layer.mlir:48-105 in program order (reshapes are
     views and so not ops: a consumer of an expand_shape names the op whose
     result it reshapes)."""
@@ -468,14 +469,16 @@ def attention_chain(pkg, *, head=128, causal=False, guard=True, exp=True,
         s = add(pkg.linalg_op(pkg.OP_BATCH_MATMUL, "b m n k",
                               ["b m k", "b k n", "b m n"], ["f32"] * 3,
                               inputs=2, reductions=["k"],
-                              extents={"b": 4, "m": 1024, "n": 1024, "k": head},
+                              extents={"b": batch, "m": seq, "n": seq,
+                                       "k": head},
                               producers=[qs, ks, bmm_init]))
     else:
         s = add(pkg.linalg_op(pkg.OP_GENERIC, "b m n k",
                               ["b m k", "b k n", "b m n"], ["f32"] * 3,
                               inputs=2, reductions=["k"], body=bmm1_body,
                               args=ABC,
-                              extents={"b": 4, "m": 1024, "n": 1024, "k": head},
+                              extents={"b": batch, "m": seq, "n": seq,
+                                       "k": head},
                               producers=[qs, ks, bmm_init]))
     if causal:
         s = add(ew(pkg, ["f32", "f32"], [
@@ -536,7 +539,7 @@ def attention_chain(pkg, *, head=128, causal=False, guard=True, exp=True,
     o = add(pkg.linalg_op(pkg.OP_BATCH_MATMUL, "b m n k",
                           ["b m k", "b k n", "b m n"], ["f32"] * 3, inputs=2,
                           reductions=["k"],
-                          extents={"b": 4, "m": 1024, "n": head, "k": 1024},
+                          extents={"b": batch, "m": seq, "n": head, "k": seq},
                           producers=[p, v32, ("const", 0.0)]))
     if out == "f16":
         add(ew(pkg, ["f32", "f16"], [("t", "truncf", ["i"], "f16"),

@@ -234,6 +234,138 @@ def test_attention_vs_torch_sdpa_nonsquare(oracle):
     assert oracle.fp16_parity(got, want.numpy()) < 1e-3
 
 
+# The scales a matched region hands over besides 1/sqrt(d): the product of
+# attention_layer.mlir's two 128^-1/4 factors with d = 64 (0.297...^2 is not
+# 1/8), an explicit 0.5, and a scale so small the softmax is nearly uniform.
+def sdpa_f64(q, k, v, scale, causal):
+    """softmax(q k^T scale + top-left causal mask) v in float64 numpy, for
+    scales torch's sdpa cannot take (its math path multiplies q and k by
+    sqrt(scale) each, so a negative scale gives nan)."""
+    s = np.einsum("bhqd,bhkd->bhqk", q.astype(np.float64),
+                  k.astype(np.float64)) * scale
+    if causal:
+        sq, skv = s.shape[-2:]
+        s = np.where(np.arange(skv)[None, :] > np.arange(sq)[:, None],
+                     -np.inf, s)
+    s = np.exp(s - s.max(axis=-1, keepdims=True))
+    return np.einsum("bhqk,bhkd->bhqd", s / s.sum(axis=-1, keepdims=True),
+                     v.astype(np.float64))
+
+
+@pytest.mark.parametrize("scale", [0.29730177875068026 ** 2, 0.5, 0.297,
+                                   1e-3, -0.3])
+@pytest.mark.parametrize("sq,skv,causal", [(40, 72, False), (40, 72, True),
+                                           (72, 40, True), (1, 96, False),
+                                           (1, 96, True), (33, 33, True)])
+def test_attention_scale_and_lengths_vs_sdpa(oracle, scale, sq, skv, causal):
+    # F.sdpa(scale=, is_causal=) is the pin: its causal mask is top-left
+    # aligned (key j hidden from query i when j > i) for any Sq, Skv.
+    g = torch.Generator().manual_seed(sq * 1000 + skv)
+    q = torch.randn(1, 2, sq, 64, generator=g).half()
+    k = torch.randn(1, 2, skv, 64, generator=g).half()
+    v = torch.randn(1, 2, skv, 64, generator=g).half()
+    if scale > 0:
+        want = F.scaled_dot_product_attention(
+            q.float(), k.float(), v.float(), is_causal=causal,
+            scale=scale).numpy()
+    else:
+        want = sdpa_f64(q.numpy(), k.numpy(), v.numpy(), scale, causal)
+    got = oracle.attention_f16(q.numpy(), k.numpy(), v.numpy(), scale=scale,
+                               causal=causal)
+    assert oracle.fp16_parity(got, want) < 1e-3
+    # a wrong scale is caught: the oracle at 1/sqrt(d) differs here
+    if abs(scale - 0.125) > 1e-2:
+        other = oracle.attention_f16(q.numpy(), k.numpy(), v.numpy(),
+                                     causal=causal)
+        if not (causal and sq == 1):  # one visible key: scale-independent
+            assert oracle.fp16_parity(other, want) > 1e-2
+
+
+@pytest.mark.parametrize("sq,skv,causal", [(40, 72, True), (72, 40, False)])
+def test_attention_zero_scale_is_the_mean(oracle, sq, skv, causal):
+    # scale 0: every visible key weighs the same, row i is the mean of the
+    # V rows it sees (torch's sdpa returns nan here under a causal mask)
+    rng = np.random.default_rng(sq + skv)
+    q = rng.standard_normal((1, 2, sq, 64)).astype(np.float16)
+    k, v = (rng.standard_normal((1, 2, skv, 64)).astype(np.float16)
+            for _ in range(2))
+    o = oracle.attention_f16(q, k, v, scale=0.0, causal=causal)
+    vf = v.astype(np.float64)
+    for i in range(sq):
+        last = min(i, skv - 1) if causal else skv - 1
+        want = vf[:, :, :last + 1].mean(axis=2)
+        assert np.abs(o[:, :, i].astype(np.float64) - want).max() < 2e-3
+
+
+def test_attention_single_query_row_causal(oracle):
+    # seq_q = 1 under a top-left causal mask sees key 0 only: O = V[0]
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal((1, 2, 1, 128)).astype(np.float16)
+    k, v = (rng.standard_normal((1, 2, 300, 128)).astype(np.float16)
+            for _ in range(2))
+    o = oracle.attention_f16(q, k, v, causal=True, scale=0.7)
+    assert np.array_equal(o[:, :, 0], v[:, :, 0])
+
+
+@pytest.mark.parametrize("hq,hkv,causal", [(8, 2, False), (6, 3, True),
+                                           (4, 1, True)])
+def test_attention_grouped_heads_vs_sdpa(oracle, hq, hkv, causal):
+    g = torch.Generator().manual_seed(hq * 10 + hkv)
+    q = torch.randn(2, hq, 70, 64, generator=g).half()
+    k = torch.randn(2, hkv, 90, 64, generator=g).half()
+    v = torch.randn(2, hkv, 90, 64, generator=g).half()
+    want = F.scaled_dot_product_attention(q.float(), k.float(), v.float(),
+                                          is_causal=causal, enable_gqa=True)
+    got = oracle.attention_f16(q.numpy(), k.numpy(), v.numpy(), causal=causal)
+    assert oracle.fp16_parity(got, want.numpy()) < 1e-3
+    # the same as repeating each KV head over its query heads
+    rep = hq // hkv
+    got2 = oracle.attention_f16(q.numpy(), np.repeat(k.numpy(), rep, axis=1),
+                                np.repeat(v.numpy(), rep, axis=1),
+                                causal=causal)
+    assert np.array_equal(got, got2)
+    # and not the same as interleaving them (head h reading KV head h % hkv)
+    if hkv > 1:
+        got3 = oracle.attention_f16(q.numpy(), np.tile(k.numpy(), (1, rep, 1, 1)),
+                                    np.tile(v.numpy(), (1, rep, 1, 1)),
+                                    causal=causal)
+        assert not np.array_equal(got, got3)
+
+
+def test_attention_strided_views(oracle):
+    # K, V a slice of a longer cache, Q a head-major view of a [B, S, H, D]
+    # buffer, O written into a [B, S, H, D] buffer: the same values as the
+    # contiguous call
+    rng = np.random.default_rng(11)
+    q_bshd = rng.standard_normal((2, 50, 4, 64)).astype(np.float16)
+    kc, vc = (rng.standard_normal((2, 2, 130, 64)).astype(np.float16)
+              for _ in range(2))
+    q = q_bshd.transpose(0, 2, 1, 3)
+    k, v = kc[:, :, :77], vc[:, :, :77]
+    o_bshd = np.full((2, 50, 4, 64), np.nan, np.float16)
+    oracle.attention_f16(q, k, v, causal=True, out=o_bshd.transpose(0, 2, 1, 3))
+    want = oracle.attention_f16(np.ascontiguousarray(q), np.ascontiguousarray(k),
+                                np.ascontiguousarray(v), causal=True)
+    assert np.array_equal(o_bshd.transpose(0, 2, 1, 3), want)
+
+
+def test_attention_cache_slice_golden(oracle):
+    # the reference's grouped-query KV-cache micro model, its tolerances
+    d = np.load(os.path.join(GOLDEN, "attention_cache_slice.npz"))
+    ctx = int(d["context"])
+    k, v = d["k_cache"][:, :, :ctx], d["v_cache"][:, :, :ctx]
+    q = d["q"]
+    b, hq, sq, dim = q.shape
+    out = np.empty((b, sq, hq, dim), np.float16)
+    oracle.attention_f16(q, k, v, causal=False,
+                         out=out.transpose(0, 2, 1, 3))
+    atol, rtol, rel_l2 = d["tol"]
+    for key in ("expected", "expected_f32"):
+        rel, _, close = oracle.compare_arrays(d[key], out, atol, rtol)
+        assert close and rel <= rel_l2, (key, rel)
+    assert oracle.fp16_parity(out, d["expected_f32"]) < 2e-3
+
+
 # --------------------------------------------------------------- planner ---
 
 def test_select_hmx_tile_sizes_lit_goldens(oracle):
