@@ -98,8 +98,9 @@ def profiled_traffic(kernel):
 def timed(fn, steps, warmup):
     """Average ms per step of fn() over exactly `steps` steps.
 
-    `warmup` eager steps first (they also size the library workspace, so the
-    timed steps allocate nothing). The `steps` launches are then captured into
+    `warmup` eager steps first (they also size the wrapper's workspace of
+    the capture stream, so the timed steps allocate nothing). The `steps`
+    launches are then captured into
     one HIP graph (no memset nodes: the kernels re-arm their own counters) and
     replayed once untimed and once between HIP events recorded on the capture
     stream, with a device synchronize on both sides. Without the graph a

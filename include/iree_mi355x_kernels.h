@@ -16,6 +16,8 @@
 //  * `stream` is a hipStream_t (NULL = the legacy default stream). Work is
 //    enqueued and the call returns without waiting; calls on different
 //    streams are independent unless the caller gives them one workspace.
+//  * No entry point allocates, frees or synchronizes device memory: scratch
+//    comes from a caller workspace (the workspace queries size it).
 //  * Return value is an iree_mi355x_status_t; preconditions are checked on
 //    the host before anything is launched, so an error never leaves work
 //    behind. The reference ABI has no error channel (its preconditions are
@@ -132,13 +134,15 @@ size_t iree_mi355x_batch_matmul_workspace_bytes(int64_t batch, int64_t m,
                                                 uint32_t flags);
 
 // i8 x i8 -> i32 matmul, exact (linalg.matmul i8,i8->i32 or
-// linalg.quantized_matmul with zero points 0). Same layouts and flags as
-// iree_mi355x_matmul_f16 except OUT_F32. The reference has no accelerator
-// kernel for it (ContractionStrategy.cpp:138-150, int8 TODO at :141); it runs
-// the generic HVX path, whose semantics this keeps bit for bit.
+// linalg.quantized_matmul with zero points 0). Same layouts, flags and
+// workspace rules as iree_mi355x_matmul_f16 except OUT_F32 and
+// A_TRANSPOSED. The reference has no accelerator kernel for it
+// (ContractionStrategy.cpp:138-150, int8 TODO at :141); it runs the generic
+// HVX path, whose semantics this keeps bit for bit.
 int iree_mi355x_matmul_i8(const int8_t *a, const int8_t *b, int32_t *c,
                           int64_t m, int64_t n, int64_t k, int64_t lda,
                           int64_t ldb, int64_t ldc, uint32_t flags,
+                          void *workspace, size_t workspace_bytes,
                           void *stream);
 
 // W8A16 linear: y[m,n] = f16((sum_k f32(x[m,k]) * f32(w[k,n])) * f32(s[n])),
@@ -196,26 +200,25 @@ int iree_mi355x_attention_f16_strided(
     int64_t head_dim, float scale, uint32_t flags,
     const iree_mi355x_attention_strides_t *strides, void *stream);
 
-// Workspace a matmul_f16 / w8a16_matmul call of this shape needs (split-K
+// Workspace a matmul_f16 / matmul_i8 / w8a16_matmul call of this shape
+// needs (split-K
 // partials and arrival counters), 0 if none. Mirrors the scratch query of the
 // reference's caller-scratch matmul, hexkl_matmul_f16f16_f32_scratch_bytes
-// (CG/Conversion/HexagonRuntimeLinking.h:35-38). Passing workspace == NULL
-// makes the library use its own workspace of the call's stream (one per
-// stream, allocated by the first call that needs it, grown on demand, never
-// freed; a capturing stream never allocates and gets
-// IREE_MI355X_WORKSPACE_TOO_SMALL instead). A caller workspace must be
-// zero-filled before its first use and is left zero-filled in its counter
-// region (its first 256 KiB) after every call, so one workspace serves any
-// sequence of calls of any shapes; calls that overlap must not share one.
-// The value covers every layout the call may run with, the M = 1
-// transposed-A row included.
+// (CG/Conversion/HexagonRuntimeLinking.h:35-38). The library allocates no
+// device memory: a call whose plan needs a workspace and gets none, or a
+// smaller one, returns IREE_MI355X_WORKSPACE_TOO_SMALL before anything is
+// launched. A workspace must be zero-filled before its first use and is left
+// zero-filled in its counter region (its first 256 KiB) after every call, so
+// one workspace serves any sequence of calls of any shapes; calls that
+// overlap must not share one. The value covers every layout the call may run
+// with, the M = 1 transposed-A row included.
 size_t iree_mi355x_matmul_workspace_bytes(int64_t m, int64_t n, int64_t k,
                                           uint32_t flags);
 
 // iree_mi355x_matmul_f16 without any allocation: the split-K partials and
 // arrival counters live in the library's own device scratch (32 MiB per GPU,
-// a static device array held until the process ends) instead of a caller or
-// library workspace, so the call never allocates, frees or synchronizes.
+// a static device array held until the process ends) instead of a caller
+// workspace, so the caller needs no device memory of its own for them.
 // No counterpart in the reference: it is for callers that cannot allocate
 // (code under HIP graph capture, tight serving loops, harnesses that forbid
 // hipMalloc). A shape whose plan needs more scratch than that returns

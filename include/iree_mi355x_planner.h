@@ -112,12 +112,16 @@ int32_t iree_mi355x_mfma_config_layout_flags(int index);
 // Launch one compiled MFMA configuration by index on an eligible shape
 // (autotuner entry). Arguments as iree_mi355x_matmul_f16 / _i8 /
 // _w8a16_matmul (scale is read only by the W8A16 form); flags must match the
-// configuration's B form. Returns IREE_MI355X_UNSUPPORTED if the shape does
-// not tile exactly.
+// configuration's B form. A split-K run takes its partials and counters
+// from `workspace` (sized by iree_mi355x_matmul_mfma_config_workspace_bytes,
+// zero-filled before its first use; IREE_MI355X_WORKSPACE_TOO_SMALL when
+// absent or short). Returns IREE_MI355X_UNSUPPORTED if the shape does not
+// tile exactly.
 int iree_mi355x_matmul_mfma_config(int index, const void *a, const void *b,
                                    const void *scale, void *c, int64_t m,
                                    int64_t n, int64_t k, int64_t lda,
                                    int64_t ldb, int64_t ldc, uint32_t flags,
+                                   void *workspace, size_t workspace_bytes,
                                    void *stream);
 
 // As iree_mi355x_matmul_mfma_config, with the K split count of a split-K
@@ -128,7 +132,18 @@ int iree_mi355x_matmul_mfma_config(int index, const void *a, const void *b,
 int iree_mi355x_matmul_mfma_config_split(
     int index, int32_t splits, const void *a, const void *b, const void *scale,
     void *c, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb,
-    int64_t ldc, uint32_t flags, void *stream);
+    int64_t ldc, uint32_t flags, void *workspace, size_t workspace_bytes,
+    void *stream);
+
+// Workspace bytes a configuration run of this shape and split count needs
+// with 16-byte aligned operands of natural pitch (0: none, or the run is
+// refused). No counterpart in the reference, whose tile search has no
+// run-time scratch; it sizes the autotuner's workspace.
+size_t iree_mi355x_matmul_mfma_config_workspace_bytes(int index,
+                                                      int32_t splits,
+                                                      int64_t m, int64_t n,
+                                                      int64_t k,
+                                                      uint32_t flags);
 
 #ifdef __cplusplus
 }  // extern "C"

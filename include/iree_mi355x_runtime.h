@@ -117,10 +117,17 @@ size_t iree_mi355x_command_buffer_workspace_bytes(
 // binding table, validates every command (a failing one enqueues nothing),
 // then enqueues. max_concurrent: 0 = IREE_MI355X_DEFAULT_CONCURRENCY, 1 = in
 // order on `stream` alone, at most IREE_MI355X_MAX_CONCURRENCY. `workspace`
-// (zero-filled before its first use; the kernels leave it zero) holds the
-// lane slices; NULL lets the runtime use its own, which submissions on
-// different streams must not use at the same time. Work is stream-ordered
-// after `stream`'s prior work, and `stream`'s later work is ordered after it.
+// holds the lane slices, sized by iree_mi355x_command_buffer_workspace_bytes
+// (one slice is that query at concurrency 1); a submission that needs one
+// and has none, or a short one, returns IREE_MI355X_WORKSPACE_TOO_SMALL
+// before enqueueing anything (the runtime allocates no device memory). Lane
+// l's slice starts at l slices and opens with its arrival counters: a
+// workspace must be zero-filled before its first use and then serve
+// submissions of one slice size only (its flat calls' counters likewise sit
+// at its start), after each of which the kernels leave every lane's
+// counters zero again. Submissions that overlap must not share a
+// workspace. Work is stream-ordered after `stream`'s prior work, and
+// `stream`'s later work is ordered after it.
 int iree_mi355x_command_buffer_submit(
     const iree_mi355x_command_buffer_t *command_buffer,
     const iree_mi355x_binding_t *binding_table, uint32_t binding_count,

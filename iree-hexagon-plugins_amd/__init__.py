@@ -12,6 +12,7 @@ binding raises, and every call goes to the HIP kernels.
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 import struct
 from dataclasses import dataclass
@@ -62,6 +63,7 @@ EXPORTED_SYMBOLS = (
     "iree_mi355x_mfma_config_info", "iree_mi355x_matmul_mfma_config",
     "iree_mi355x_executable_library_query", "iree_mi355x_batch_matmul_f16",
     "iree_mi355x_batch_matmul_workspace_bytes",
+    "iree_mi355x_matmul_mfma_config_workspace_bytes",
     "iree_mi355x_mfma_config_layout_flags",
     "iree_mi355x_matmul_mfma_config_split",
     "iree_mi355x_command_buffer_create", "iree_mi355x_command_buffer_release",
@@ -280,7 +282,7 @@ def library():
     lib.iree_mi355x_matmul_f16.argtypes = [p, p, p, i64, i64, i64, i64, i64,
                                            i64, u32, p, sz, p]
     lib.iree_mi355x_matmul_i8.argtypes = [p, p, p, i64, i64, i64, i64, i64,
-                                          i64, u32, p]
+                                          i64, u32, p, sz, p]
     lib.iree_mi355x_matmul_f16_no_alloc.argtypes = [p, p, p, i64, i64, i64,
                                                     i64, i64, i64, u32, p]
     lib.iree_mi355x_w8a16_matmul.argtypes = [p, p, p, p, i64, i64, i64, i64,
@@ -316,10 +318,13 @@ def library():
     lib.iree_mi355x_mfma_config_layout_flags.argtypes = [ctypes.c_int]
     lib.iree_mi355x_matmul_mfma_config_split.argtypes = [
         ctypes.c_int, ctypes.c_int32, p, p, p, p, i64, i64, i64, i64, i64, i64,
-        u32, p]
+        u32, p, sz, p]
     lib.iree_mi355x_matmul_mfma_config.argtypes = [ctypes.c_int, p, p, p, p,
                                                    i64, i64, i64, i64, i64,
-                                                   i64, u32, p]
+                                                   i64, u32, p, sz, p]
+    lib.iree_mi355x_matmul_mfma_config_workspace_bytes.restype = sz
+    lib.iree_mi355x_matmul_mfma_config_workspace_bytes.argtypes = [
+        ctypes.c_int, ctypes.c_int32, i64, i64, i64, u32]
     cbp = ctypes.c_void_p
     lib.iree_mi355x_command_buffer_create.argtypes = [p, ctypes.POINTER(cbp)]
     lib.iree_mi355x_command_buffer_release.argtypes = [cbp]
@@ -624,6 +629,73 @@ def attention_constants(batch, heads, seq_q, seq_kv, head_dim, scale, flags,
     return words
 
 
+# --------------------------------------------------------------- workspace --
+
+# The C-ABI allocates no device memory: calls whose plan splits K take their
+# partials and arrival counters from a workspace. For calls made without
+# one, the wrapper keeps one zero-filled buffer per (device, stream),
+# allocated through torch's allocator in that stream's order, grown
+# geometrically and never released: a graph captured earlier may hold an
+# older buffer, so the ones a larger buffer replaces stay alive too. Two
+# streams never share a buffer (their arrival counters would collide).
+_STREAM_WORKSPACES: dict = {}
+_MIN_WORKSPACE = 64 << 20
+
+
+def _torch_stream(stream, dev):
+    import torch
+    if stream is None:
+        return torch.cuda.current_stream(dev)
+    if isinstance(stream, int):
+        return (torch.cuda.ExternalStream(stream, device=dev) if stream
+                else torch.cuda.default_stream(dev))
+    return stream
+
+
+def stream_workspace(need: int, device=None, stream=None, layout=None):
+    """(pointer, bytes) of the wrapper's workspace for `stream` (None: the
+    current one; an int: a raw hipStream_t) on `device`, holding at least
+    `need` bytes; (None, 0) when `need` is 0. `layout` keeps apart buffers
+    whose arrival counters sit at different offsets (a command buffer's lane
+    slices): None for flat calls, whose counters open the buffer. Under graph
+    capture a buffer that is too small is not grown:
+    MI355XError(WORKSPACE_TOO_SMALL)."""
+    import torch
+    if need <= 0:
+        return None, 0
+    dev = torch.device("cuda") if device is None else torch.device(device)
+    if dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    s = _torch_stream(stream, dev)
+    bufs = _STREAM_WORKSPACES.setdefault((dev.index, s.cuda_stream, layout),
+                                         [])
+    have = bufs[-1].numel() if bufs else 0
+    if have >= need:
+        return bufs[-1].data_ptr(), have
+    if torch.cuda.is_current_stream_capturing():
+        raise MI355XError(
+            WORKSPACE_TOO_SMALL,
+            f"the stream is capturing and its workspace holds {have} < "
+            f"{need} bytes: make one call of this shape on the stream "
+            "before capture, or pass a workspace")
+    size = max(_MIN_WORKSPACE, 2 * have, need)
+    with torch.cuda.stream(s):
+        buf = torch.zeros(size, dtype=torch.uint8, device=dev)
+    bufs.append(buf)
+    return buf.data_ptr(), size
+
+
+@functools.lru_cache(maxsize=4096)
+def _matmul_workspace_need(m, n, k, flags) -> int:
+    return library().iree_mi355x_matmul_workspace_bytes(m, n, k, flags)
+
+
+@functools.lru_cache(maxsize=4096)
+def _batch_workspace_need(batch, m, n, k, flags) -> int:
+    return library().iree_mi355x_batch_matmul_workspace_bytes(batch, m, n, k,
+                                                              flags)
+
+
 # --------------------------------------------------------------- operators --
 
 def _stream_ptr(stream=None):
@@ -716,17 +788,20 @@ def matmul(a, b, c=None, *, b_transposed=False, accumulate=False,
              (ACCUMULATE if accumulate else 0) |
              (A_TRANSPOSED if a_transposed else 0))
     s = _stream_ptr(stream)
+    if a.dtype != torch.int8 and out_dtype == torch.float32:
+        flags |= OUT_F32
+    ws, wsb = stream_workspace(_matmul_workspace_need(m, n, k, flags),
+                               a.device, s)
     if a.dtype == torch.int8:
         _check(lib.iree_mi355x_matmul_i8(a.data_ptr(), b.data_ptr(),
                                          c.data_ptr(), m, n, k, a.stride(0),
-                                         b.stride(0), c.stride(0), flags, s))
+                                         b.stride(0), c.stride(0), flags, ws,
+                                         wsb, s))
     else:
-        if out_dtype == torch.float32:
-            flags |= OUT_F32
         _check(lib.iree_mi355x_matmul_f16(a.data_ptr(), b.data_ptr(),
                                           c.data_ptr(), m, n, k, a.stride(0),
                                           b.stride(0), c.stride(0), flags,
-                                          None, 0, s))
+                                          ws, wsb, s))
     return c
 
 
@@ -815,11 +890,13 @@ def batch_matmul(a, b, c=None, *, b_transposed=False, accumulate=False,
              (ACCUMULATE if accumulate else 0) |
              (OUT_F32 if out_dtype == torch.float32 else 0) |
              (A_TRANSPOSED if a_transposed else 0))
+    st = _stream_ptr(stream)
+    ws, wsb = stream_workspace(_batch_workspace_need(batch, m, n, k, flags),
+                               a.device, st)
     _check(lib.iree_mi355x_batch_matmul_f16(
         a3.data_ptr(), b3.data_ptr(), c3.data_ptr(), batch, m, n, k,
         a3.stride(1), b3.stride(1), c3.stride(1), sa, sb, sc, flags,
-        ctypes.byref(e) if e is not None else None, None, 0,
-        _stream_ptr(stream)))
+        ctypes.byref(e) if e is not None else None, ws, wsb, st))
     return c
 
 
@@ -853,10 +930,13 @@ def quantized_matmul(x, w, scale, y=None, *, w_transposed=False, stream=None):
     lib = library()
     if y is None:
         y = torch.empty((m, n), dtype=torch.float16, device=x.device)
+    flags = B_TRANSPOSED if w_transposed else 0
+    st = _stream_ptr(stream)
+    ws, wsb = stream_workspace(_matmul_workspace_need(m, n, k, flags),
+                               x.device, st)
     _check(lib.iree_mi355x_w8a16_matmul(
         x.data_ptr(), w.data_ptr(), scale.data_ptr(), y.data_ptr(), m, n, k,
-        x.stride(0), w.stride(0), y.stride(0),
-        B_TRANSPOSED if w_transposed else 0, None, 0, _stream_ptr(stream)))
+        x.stride(0), w.stride(0), y.stride(0), flags, ws, wsb, st))
     return y
 
 
@@ -953,10 +1033,16 @@ def matmul_mfma_config(index, a, b, c, *, scale=None, splits=0, accumulate=False
         flags |= OUT_F32
     if accumulate:
         flags |= ACCUMULATE
-    _check(library().iree_mi355x_matmul_mfma_config_split(
+    lib = library()
+    s = _stream_ptr(stream)
+    ws, wsb = stream_workspace(
+        lib.iree_mi355x_matmul_mfma_config_workspace_bytes(index, splits, m, n,
+                                                           k, flags),
+        a.device, s)
+    _check(lib.iree_mi355x_matmul_mfma_config_split(
         index, splits, a.data_ptr(), b.data_ptr(),
         scale.data_ptr() if scale is not None else None, c.data_ptr(), m, n,
-        k, a.stride(0), b.stride(0), c.stride(0), flags, _stream_ptr(stream)))
+        k, a.stride(0), b.stride(0), c.stride(0), flags, ws, wsb, s))
     return c
 
 
@@ -1060,10 +1146,21 @@ class CommandBuffer:
         return [(o.kind, o.lane, o.event, o.command) for o in ops[:n]]
 
     def submit(self, table=(), max_concurrent=0, workspace=None, stream=None):
+        """Submit on `stream`; without a `workspace` the lane slices come
+        from the wrapper's workspace of that stream for this slice size
+        (lane l's counters sit at l slices: a buffer serves one slice size)."""
         arr, n = binding_table(list(table))
-        ws, wsb = (None, 0) if workspace is None else _ptr_len(workspace)
+        s = _stream_ptr(stream)
+        if workspace is None:
+            need = self._lib.iree_mi355x_command_buffer_workspace_bytes(
+                self._h, arr, n, max_concurrent)
+            slice_ = self._lib.iree_mi355x_command_buffer_workspace_bytes(
+                self._h, arr, n, 1) if need else 0
+            ws, wsb = stream_workspace(need, None, s, ("lanes", slice_))
+        else:
+            ws, wsb = _ptr_len(workspace)
         _check(self._lib.iree_mi355x_command_buffer_submit(
-            self._h, arr, n, max_concurrent, ws, wsb, _stream_ptr(stream)))
+            self._h, arr, n, max_concurrent, ws, wsb, s))
 
 
 def kernel_resources(device: bool = True) -> list[dict]:

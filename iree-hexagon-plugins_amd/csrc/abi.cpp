@@ -58,96 +58,21 @@ static bool aligned(const void *p, size_t a) {
 
 static const int64_t kMaxExtent = (int64_t)1 << 31;
 
-// The library's own workspace, for calls made with workspace == NULL: one
-// buffer per (device, stream), so calls on different streams never share
-// arrival counters or partials. A buffer is allocated outside stream capture
-// only, its counter region zero-filled in stream order; it grows
-// geometrically and is never freed: a graph captured earlier, or a launch
-// another thread is still queueing, may hold a smaller one, and freeing it
-// would turn that launch into a use of freed memory. Streams are told apart
-// by hipStreamGetId (where the runtime has it) as well as their handle, so a
-// new stream that reuses a destroyed one's handle gets a buffer of its own.
-struct StreamWorkspace {
-  int device;
-  uintptr_t handle;
-  unsigned long long id;
-  void *ptr;
-  size_t bytes;
-};
-static std::mutex g_ws_mutex;
-static std::vector<StreamWorkspace> g_ws;
-
-// hipStreamGetId, looked up at run time: the HIP runtime this process runs
-// on (torch's, when loaded from Python) may predate it, and then streams are
-// told apart by their handle alone.
-typedef hipError_t (*StreamIdFn)(hipStream_t, unsigned long long *);
-static StreamIdFn stream_id_fn() {
-  static const StreamIdFn fn =
-      (StreamIdFn)dlsym(RTLD_DEFAULT, "hipStreamGetId");
-  return fn;
-}
-
-int library_workspace(size_t need, void *stream, void **out) {
-  *out = nullptr;
-  if (need == 0)
+// The split-K partials and arrival counters of a call come from the
+// caller's workspace: the library allocates no device memory. A call whose
+// plan needs `need` bytes and has none, or fewer, is refused before
+// anything is launched.
+int require_workspace(const char *who, size_t need, const void *workspace,
+                      size_t workspace_bytes) {
+  if (need == 0 || (workspace && workspace_bytes >= need))
     return IREE_MI355X_OK;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess)
-    return fail(IREE_MI355X_NO_DEVICE, "hipGetDevice failed");
-  unsigned long long id = 0;
-  if (stream_id_fn() &&
-      stream_id_fn()((hipStream_t)stream, &id) != hipSuccess) {
-    (void)hipGetLastError();
-    id = 0;
-  }
-  std::lock_guard<std::mutex> lock(g_ws_mutex);
-  StreamWorkspace *ws = nullptr;
-  for (StreamWorkspace &w : g_ws)
-    if (w.device == dev && w.handle == (uintptr_t)stream && w.id == id)
-      ws = &w;
-  if (ws && ws->bytes >= need) {
-    *out = ws->ptr;
-    return IREE_MI355X_OK;
-  }
-  const size_t have = ws ? ws->bytes : 0;
-  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing((hipStream_t)stream, &capture) != hipSuccess) {
-    (void)hipGetLastError();
-    capture = hipStreamCaptureStatusActive;  // unknown: do not allocate
-  }
-  if (capture != hipStreamCaptureStatusNone)
+  if (!workspace)
     return fail(IREE_MI355X_WORKSPACE_TOO_SMALL,
-                "the stream is capturing and its library workspace holds "
-                "%zu < %zu bytes: pass a workspace sized by the workspace "
-                "query, or make one call on this stream before capture",
-                have, need);
-  size_t grow = (size_t)64 << 20;
-  if (grow < 2 * have)
-    grow = 2 * have;
-  if (grow < need)
-    grow = need;
-  void *p = nullptr;
-  if (hipMalloc(&p, grow) != hipSuccess) {
-    (void)hipGetLastError();
-    return fail(IREE_MI355X_LAUNCH_FAILED, "workspace hipMalloc(%zu) failed",
-                grow);
-  }
-  // Only the arrival counters must start at zero; partials are written
-  // before they are read. Stream order puts the fill before the kernel.
-  if (hipMemsetAsync(p, 0, kWorkspaceCounterBytes, (hipStream_t)stream) !=
-      hipSuccess) {
-    (void)hipGetLastError();
-    (void)hipFree(p);
-    return fail(IREE_MI355X_LAUNCH_FAILED, "workspace fill failed");
-  }
-  if (ws) {
-    ws->ptr = p;  // the old buffer is retired, not freed
-    ws->bytes = grow;
-  } else {
-    g_ws.push_back({dev, (uintptr_t)stream, id, p, grow});
-  }
-  *out = p;
-  return IREE_MI355X_OK;
+                "%s: the plan needs a workspace of %zu bytes (size it with "
+                "the workspace query) and none was passed",
+                who, need);
+  return fail(IREE_MI355X_WORKSPACE_TOO_SMALL, "%s: workspace %zu < %zu", who,
+              workspace_bytes, need);
 }
 
 // Scratch of the allocation-free entry point: device memory of the
@@ -205,16 +130,11 @@ static int launch_mfma(MatmulArgs &args, const iree_mi355x_matmul_plan_t &plan,
   args.sk_workgroups = plan.stream_k_steps > 0 ? (int)plan.workgroups : 0;
   args.workspace = nullptr;
   if (plan.workspace_bytes > 0) {
-    if (workspace && workspace_bytes < (size_t)plan.workspace_bytes)
-      return fail(IREE_MI355X_WORKSPACE_TOO_SMALL, "%s: workspace %zu < %lld",
-                  who, workspace_bytes, (long long)plan.workspace_bytes);
+    const int st = require_workspace(who, (size_t)plan.workspace_bytes,
+                                     workspace, workspace_bytes);
+    if (st != IREE_MI355X_OK)
+      return st;
     args.workspace = workspace;
-    if (!args.workspace) {
-      const int st = library_workspace((size_t)plan.workspace_bytes,
-                                       args.stream, &args.workspace);
-      if (st != IREE_MI355X_OK)
-        return st;
-    }
   }
   return launch_status(cfgs[plan.config_index].launch(args),
                        cfgs[plan.config_index].name);
@@ -280,21 +200,22 @@ size_t iree_mi355x_matmul_workspace_bytes(int64_t m, int64_t n, int64_t k,
                                           uint32_t flags) {
   if (m <= 0 || n <= 0 || k <= 0)
     return 0;
-  // The largest workspace any f16 or W8A16 plan of this shape uses (plans
+  // The largest workspace any f16, int8 or W8A16 plan of this shape uses (plans
   // assume 16-byte aligned operands, the case that can pick split-K), over
   // both layouts a call may take: one row of a transposed A with unit pitch
   // runs as the untransposed row (see m1_row_layout).
   size_t most = 0;
-  const int32_t forms[3][3] = {
+  const int32_t forms[4][3] = {
       {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16},
       {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_F32},
-      {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_F16}};
+      {IREE_MI355X_ELEM_F16, IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_F16},
+      {IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_I8, IREE_MI355X_ELEM_I32}};
   for (int layout = 0; layout < 2; ++layout) {
     const uint32_t lf =
         layout == 0 ? flags : m1_row_layout(m, 1, flags);
     if (layout == 1 && lf == flags)
       break;
-    for (int f = 0; f < 3; ++f) {
+    for (int f = 0; f < 4; ++f) {
       iree_mi355x_matmul_desc_t d;
       iree_mi355x_matmul_desc_init(&d, forms[f][0], forms[f][1], forms[f][2],
                                    m, n, k, lf & ~IREE_MI355X_MATMUL_OUT_F32);
@@ -341,20 +262,13 @@ static int matmul_f16_run(const char *who, MatmulArgs &args, uint32_t flags,
     return ok();
   int st;
   switch (plan.family) {
-    case IREE_MI355X_FAMILY_GEMV: {
-      void *ws = workspace;
-      if (plan.workspace_bytes > 0) {
-        if (ws && workspace_bytes < (size_t)plan.workspace_bytes)
-          return fail(IREE_MI355X_WORKSPACE_TOO_SMALL,
-                      "%s: workspace %zu < %zu", who, workspace_bytes,
-                      (size_t)plan.workspace_bytes);
-        if (!ws && (st = library_workspace(plan.workspace_bytes, args.stream,
-                                           &ws)) != IREE_MI355X_OK)
-          return st;
-      }
-      return launch_status(launch_gemv(args, 2, nullptr, out_f32, ws),
+    case IREE_MI355X_FAMILY_GEMV:
+      if ((st = require_workspace(who, (size_t)plan.workspace_bytes,
+                                  workspace, workspace_bytes)) !=
+          IREE_MI355X_OK)
+        return st;
+      return launch_status(launch_gemv(args, 2, nullptr, out_f32, workspace),
                            "gemv_f16");
-    }
     case IREE_MI355X_FAMILY_MFMA:
       return launch_mfma(args, plan, workspace, workspace_bytes, who);
     default:
@@ -499,6 +413,7 @@ size_t iree_mi355x_batch_matmul_workspace_bytes(int64_t batch, int64_t m,
 int iree_mi355x_matmul_i8(const int8_t *a, const int8_t *b, int32_t *c,
                           int64_t m, int64_t n, int64_t k, int64_t lda,
                           int64_t ldb, int64_t ldc, uint32_t flags,
+                          void *workspace, size_t workspace_bytes,
                           void *stream) {
   int st = check_matmul("matmul_i8", a, b, c, m, n, k, lda, ldb, ldc, flags,
                         IREE_MI355X_MATMUL_B_TRANSPOSED |
@@ -520,7 +435,7 @@ int iree_mi355x_matmul_i8(const int8_t *a, const int8_t *b, int32_t *c,
   if (dry_run(plan.workspace_bytes))
     return ok();
   if (plan.family == IREE_MI355X_FAMILY_MFMA)
-    return launch_mfma(args, plan, nullptr, 0, "matmul_i8");
+    return launch_mfma(args, plan, workspace, workspace_bytes, "matmul_i8");
   return launch_status(launch_general(args, kGeneralI8I32, nullptr),
                        "gemm_general_i8");
 }
@@ -553,17 +468,11 @@ int iree_mi355x_w8a16_matmul(const void *x, const int8_t *w, const void *scale,
   if (dry_run(plan.workspace_bytes))
     return ok();
   if (plan.family == IREE_MI355X_FAMILY_GEMV) {
-    void *ws = workspace;
-    if (plan.workspace_bytes > 0) {
-      if (ws && workspace_bytes < plan.workspace_bytes)
-        return fail(IREE_MI355X_WORKSPACE_TOO_SMALL,
-                    "w8a16_matmul: workspace %zu < %zu", workspace_bytes,
-                    (size_t)plan.workspace_bytes);
-      if (!ws && (st = library_workspace(plan.workspace_bytes, stream,
-                                         &ws)) != IREE_MI355X_OK)
-        return st;
-    }
-    return launch_status(launch_gemv(args, 1, scale, 0, ws), "gemv_w8a16");
+    if ((st = require_workspace("w8a16_matmul", (size_t)plan.workspace_bytes,
+                                workspace, workspace_bytes)) != IREE_MI355X_OK)
+      return st;
+    return launch_status(launch_gemv(args, 1, scale, 0, workspace),
+                         "gemv_w8a16");
   }
   if (plan.family == IREE_MI355X_FAMILY_MFMA)
     return launch_mfma(args, plan, workspace, workspace_bytes, "w8a16_matmul");

@@ -133,7 +133,8 @@ int dispatch_matmul_i8(const iree_mi355x_executable_environment_t *,
   return iree_mi355x_matmul_i8((const int8_t *)s->binding_ptrs[0],
                                (const int8_t *)s->binding_ptrs[1],
                                (int32_t *)s->binding_ptrs[2], c.m, c.n, c.k,
-                               c.lda, c.ldb, c.ldc, c.flags, s->stream);
+                               c.lda, c.ldb, c.ldc, c.flags, s->workspace,
+                               s->workspace_bytes, s->stream);
 }
 
 int dispatch_w8a16(const iree_mi355x_executable_environment_t *,

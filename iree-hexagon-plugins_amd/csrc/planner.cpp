@@ -14,7 +14,8 @@
 namespace ihp {
 
 int fail(int status, const char *fmt, ...);
-int library_workspace(size_t need, void *stream, void **out);
+int require_workspace(const char *who, size_t need, const void *workspace,
+                      size_t workspace_bytes);
 
 namespace {
 
@@ -610,10 +611,16 @@ int32_t iree_mi355x_mfma_config_layout_flags(int index) {
                                         : 0u));
 }
 
-int iree_mi355x_matmul_mfma_config_split(
-    int index, int32_t splits, const void *a, const void *b, const void *scale,
-    void *c, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb,
-    int64_t ldc, uint32_t flags, void *stream) {
+}  // extern "C"
+
+namespace {
+
+// The checks and the plan of one configuration run (the candidate it would
+// launch), shared by the run and its workspace query.
+int config_candidate(int index, int32_t splits, const void *a, const void *b,
+                     const void *scale, const void *c, int64_t m, int64_t n,
+                     int64_t k, int64_t lda, int64_t ldb, int64_t ldc,
+                     uint32_t flags, Candidate *out) {
   int count = 0;
   const FastConfig *cfgs = fast_configs(&count);
   if (index < 0 || index >= count)
@@ -643,23 +650,57 @@ int iree_mi355x_matmul_mfma_config_split(
       n >= ((int64_t)1 << 31) || k >= ((int64_t)1 << 31) ||
       (d.has_scale && (!scale || (uintptr_t)scale % 2 != 0)))
     return fail(IREE_MI355X_INVALID_ARGUMENT, "mfma_config: bad arguments");
-  Candidate cand;
   if (splits < kStreamK || ((splits > 1 || splits == kStreamK) &&
                             !cfg.split_k))
     return fail(IREE_MI355X_INVALID_ARGUMENT,
                 "mfma_config %s: %d splits", cfg.name, splits);
-  if (!evaluate(d, cfg, index, kDefaultCus, &cand, true, splits))
+  if (!evaluate(d, cfg, index, kDefaultCus, out, true, splits))
     return fail(IREE_MI355X_UNSUPPORTED,
                 "mfma_config %s: shape or layout does not fit", cfg.name);
-  void *ws = nullptr;
-  if (cand.workspace > 0) {
-    int st = library_workspace((size_t)cand.workspace, stream, &ws);
-    if (st != IREE_MI355X_OK)
-      return st;
-  }
+  return IREE_MI355X_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t iree_mi355x_matmul_mfma_config_workspace_bytes(int index,
+                                                      int32_t splits,
+                                                      int64_t m, int64_t n,
+                                                      int64_t k,
+                                                      uint32_t flags) {
+  // Any 256-byte aligned operands with natural pitches plan alike.
+  const void *p = (const void *)(uintptr_t)256;
+  const bool bt = flags & IREE_MI355X_MATMUL_B_TRANSPOSED;
+  const bool at = flags & IREE_MI355X_MATMUL_A_TRANSPOSED;
+  Candidate cand;
+  if (config_candidate(index, splits, p, p, p, p, m, n, k, at ? m : k,
+                       bt ? k : n, n, flags, &cand) != IREE_MI355X_OK)
+    return 0;
+  return cand.workspace > 0 ? (size_t)cand.workspace : 0;
+}
+
+int iree_mi355x_matmul_mfma_config_split(
+    int index, int32_t splits, const void *a, const void *b, const void *scale,
+    void *c, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb,
+    int64_t ldc, uint32_t flags, void *workspace, size_t workspace_bytes,
+    void *stream) {
+  Candidate cand;
+  int st = config_candidate(index, splits, a, b, scale, c, m, n, k, lda, ldb,
+                            ldc, flags, &cand);
+  if (st != IREE_MI355X_OK)
+    return st;
+  int count = 0;
+  const FastConfig &cfg = fast_configs(&count)[index];
+  if ((st = require_workspace(cfg.name, (size_t)cand.workspace, workspace,
+                              workspace_bytes)) != IREE_MI355X_OK)
+    return st;
+  const bool bt = flags & IREE_MI355X_MATMUL_B_TRANSPOSED;
+  const bool at = flags & IREE_MI355X_MATMUL_A_TRANSPOSED;
   MatmulArgs args{a, b, c, m, n, k, lda, ldb, ldc, bt ? 1 : 0,
                   (flags & IREE_MI355X_MATMUL_ACCUMULATE) ? 1 : 0, stream,
-                  scale, cand.splits, cand.k_split, ws};
+                  scale, cand.splits, cand.k_split,
+                  cand.workspace > 0 ? workspace : nullptr};
   args.a_transposed = at ? 1 : 0;
   args.sk_steps = cand.sk_steps;
   args.sk_workgroups = (int)cand.sk_wgs;
@@ -674,9 +715,12 @@ int iree_mi355x_matmul_mfma_config(int index, const void *a, const void *b,
                                    const void *scale, void *c, int64_t m,
                                    int64_t n, int64_t k, int64_t lda,
                                    int64_t ldb, int64_t ldc, uint32_t flags,
+                                   void *workspace, size_t workspace_bytes,
                                    void *stream) {
   return iree_mi355x_matmul_mfma_config_split(index, 0, a, b, scale, c, m, n,
-                                              k, lda, ldb, ldc, flags, stream);
+                                              k, lda, ldb, ldc, flags,
+                                              workspace, workspace_bytes,
+                                              stream);
 }
 
 }  // extern "C"

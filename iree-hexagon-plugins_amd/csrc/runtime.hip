@@ -334,15 +334,13 @@ std::vector<iree_mi355x_lane_op_t> lane_schedule(
 }
 
 // Per device: the lane streams and events (default priority, non-blocking,
-// kept for the process), the runtime's own workspace, and a lock that makes
+// kept for the process), and a lock that makes
 // submissions on one device enqueue one at a time.
 struct DeviceLanes {
   std::mutex lock;
   hipStream_t streams[IREE_MI355X_MAX_CONCURRENCY] = {};
   hipEvent_t lane_done[IREE_MI355X_MAX_CONCURRENCY] = {};
   hipEvent_t fork = nullptr;
-  void *workspace = nullptr;
-  size_t workspace_bytes = 0;
 };
 
 std::mutex g_devices_lock;
@@ -373,31 +371,6 @@ int ensure_lanes(DeviceLanes *d, uint32_t lanes) {
             hipSuccess)
       return fail(IREE_MI355X_LAUNCH_FAILED, "submit: hipEventCreate failed");
   }
-  return IREE_MI355X_OK;
-}
-
-// The runtime's workspace: grow-only, zero-filled when (re)allocated.
-int runtime_workspace(DeviceLanes *d, size_t need, void **out) {
-  if (d->workspace_bytes < need) {
-    if (d->workspace) {
-      // Work on any stream may still use the old buffer.
-      if (hipDeviceSynchronize() != hipSuccess ||
-          hipFree(d->workspace) != hipSuccess)
-        return fail(IREE_MI355X_LAUNCH_FAILED,
-                    "submit: workspace release failed");
-      d->workspace = nullptr;
-      d->workspace_bytes = 0;
-    }
-    if (hipMalloc(&d->workspace, need) != hipSuccess)
-      return fail(IREE_MI355X_LAUNCH_FAILED,
-                  "submit: workspace hipMalloc(%zu) failed (inside a graph "
-                  "capture, pass a workspace or submit once before)",
-                  need);
-    if (hipMemset(d->workspace, 0, need) != hipSuccess)
-      return fail(IREE_MI355X_LAUNCH_FAILED, "submit: workspace zero failed");
-    d->workspace_bytes = need;
-  }
-  *out = d->workspace;
   return IREE_MI355X_OK;
 }
 
@@ -634,10 +607,14 @@ int iree_mi355x_command_buffer_submit(
   const uint32_t lanes = lanes_for(
       cb, max_concurrent ? max_concurrent : IREE_MI355X_DEFAULT_CONCURRENCY);
   const size_t slice = need ? slice_bytes(need) : 0;
-  if (workspace && slice && workspace_bytes < slice * lanes)
+  // The caller provides the lane slices: the runtime allocates no device
+  // memory.
+  if (slice && (!workspace || workspace_bytes < slice * lanes))
     return fail(IREE_MI355X_WORKSPACE_TOO_SMALL,
-                "submit: workspace %zu < %zu (%u lanes x %zu)",
-                workspace_bytes, slice * lanes, lanes, slice);
+                "submit: workspace %zu < %zu (%u lanes x %zu; size it with "
+                "iree_mi355x_command_buffer_workspace_bytes)",
+                workspace ? workspace_bytes : (size_t)0, slice * lanes, lanes,
+                slice);
 
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess)
@@ -645,12 +622,6 @@ int iree_mi355x_command_buffer_submit(
   DeviceLanes *d = device_lanes(dev);
   std::lock_guard<std::mutex> guard(d->lock);
   char *ws = (char *)workspace;
-  if (slice && !ws) {
-    void *own = nullptr;
-    if ((st = runtime_workspace(d, slice * lanes, &own)))
-      return st;
-    ws = (char *)own;
-  }
   hipStream_t caller = (hipStream_t)stream;
   roctxRangePushA("iree_mi355x submit");
   const uint32_t n = (uint32_t)cb->commands.size();

@@ -29,6 +29,57 @@ def test_library_exports_every_declared_symbol(pkg):
         assert getattr(lib, name) is not None
 
 
+# Device-memory allocators, frees and fills of the HIP runtime: the C-ABI
+# imports none of them (scratch comes from a caller workspace, or, for the
+# allocation-free entry point, from a static device array).
+ALLOCATING = ("hipMalloc", "hipMallocAsync", "hipMallocManaged",
+              "hipMallocPitch", "hipExtMallocWithFlags", "hipHostMalloc",
+              "hipMallocFromPoolAsync", "hipFree", "hipFreeAsync",
+              "hipHostFree", "hipMemset", "hipMemsetAsync", "hipMemsetD32",
+              "hipMemsetD32Async", "hipDeviceSynchronize")
+
+
+def test_library_imports_no_allocator(pkg):
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--undefined-only", pkg.LIB_PATH],
+                         check=True, capture_output=True, text=True).stdout
+    imported = {line.split()[-1].split("@")[0] for line in out.splitlines()
+                if line.strip()}
+    assert "hipLaunchKernel" in imported  # the listing is the real one
+    assert not imported & set(ALLOCATING), imported & set(ALLOCATING)
+
+
+def test_missing_workspace_is_refused_before_launch(pkg):
+    # split-K and GEMV plans need a workspace: none, or a short one, is
+    # refused on the host (no device here: nothing could have launched)
+    lib = pkg.library()
+    for m, n, k in [(16, 4096, 4096), (1, 4096, 4096)]:
+        need = lib.iree_mi355x_matmul_workspace_bytes(m, n, k, 0)
+        assert need > 0
+        st = lib.iree_mi355x_matmul_f16(FAKE, FAKE, FAKE, m, n, k, k, n, n, 0,
+                                        None, 0, None)
+        assert st == pkg.WORKSPACE_TOO_SMALL, pkg.last_error()
+        assert str(need) in pkg.last_error() or "workspace" in pkg.last_error()
+        # the query bounds every form; the f16 plan itself needs this much
+        exact = pkg.plan(pkg.make_desc(0, 0, 0, m, n, k, 0)).workspace_bytes
+        assert 0 < exact <= need
+        st = lib.iree_mi355x_matmul_f16(FAKE, FAKE, FAKE, m, n, k, k, n, n, 0,
+                                        FAKE, exact - 1, None)
+        assert st == pkg.WORKSPACE_TOO_SMALL
+        st = lib.iree_mi355x_w8a16_matmul(FAKE, FAKE, FAKE, FAKE, m, n, k, k,
+                                          n, n, 0, None, 0, None)
+        assert st == pkg.WORKSPACE_TOO_SMALL
+    # an autotuner run of a split-K configuration likewise
+    cfg = next(c for c in pkg.mfma_configs()
+               if c.name == "f16_nn_64x128x64_w2x2_s4_sk")
+    need = lib.iree_mi355x_matmul_mfma_config_workspace_bytes(
+        cfg.index, 4, 64, 4096, 4096, 0)
+    assert need > 0
+    assert lib.iree_mi355x_matmul_mfma_config_split(
+        cfg.index, 4, FAKE, FAKE, None, FAKE, 64, 4096, 4096, 4096, 4096,
+        4096, 0, None, 0, None) == pkg.WORKSPACE_TOO_SMALL
+
+
 def test_version_and_no_device_here(pkg):
     lib = pkg.library()
     assert b"gfx950" in lib.iree_mi355x_version()
@@ -288,9 +339,10 @@ def test_matmul_argument_errors(pkg):
     assert call_f16(lib, m=0) == pkg.OK
     assert call_f16(lib, n=0, a=None, b=None) == pkg.OK
     assert lib.iree_mi355x_matmul_i8(FAKE, FAKE, FAKE + 2, 8, 8, 8, 8, 8, 8, 0,
-                                     None) == pkg.MISALIGNED
+                                     None, 0, None) == pkg.MISALIGNED
     assert lib.iree_mi355x_matmul_i8(FAKE, FAKE, FAKE, 8, 8, 8, 8, 8, 8,
-                                     pkg.OUT_F32, None) == pkg.INVALID_ARGUMENT
+                                     pkg.OUT_F32, None, 0,
+                                     None) == pkg.INVALID_ARGUMENT
     assert lib.iree_mi355x_w8a16_matmul(FAKE, FAKE, None, FAKE, 1, 64, 64, 64,
                                         64, 64, 0, None, 0,
                                         None) == pkg.INVALID_ARGUMENT
@@ -454,7 +506,7 @@ def test_transposed_a_argument_checks(pkg):
     assert call_f16(lib, flags=AT, lda=32) == pkg.INVALID_ARGUMENT
     # integer and W8A16 entry points take no transposed A
     assert lib.iree_mi355x_matmul_i8(FAKE, FAKE, FAKE, 8, 8, 8, 8, 8, 8, AT,
-                                     None) == pkg.INVALID_ARGUMENT
+                                     None, 0, None) == pkg.INVALID_ARGUMENT
     assert lib.iree_mi355x_w8a16_matmul(FAKE, FAKE, FAKE, FAKE, 1, 64, 64, 64,
                                         64, 64, AT, None, 0,
                                         None) == pkg.INVALID_ARGUMENT
@@ -463,7 +515,7 @@ def test_transposed_a_argument_checks(pkg):
               if c.a_transposed and c.b_form == pkg.B_FORM_NN][0]
     f = lib.iree_mi355x_matmul_mfma_config
     assert f(at_cfg.index, FAKE, FAKE, None, FAKE, 256, 256, 256, 256, 256,
-             256, 0, None) == pkg.UNSUPPORTED
+             256, 0, None, 0, None) == pkg.UNSUPPORTED
 
 
 def test_fast_path_pitch_limit(pkg):
@@ -474,9 +526,9 @@ def test_fast_path_pitch_limit(pkg):
     f = lib.iree_mi355x_matmul_mfma_config
     big = (1 << 22)  # f16 elements: an 8 MiB row
     assert f(cfg.index, FAKE, FAKE, None, FAKE, 128, 128, 64, big, 128, 128, 0,
-             None) == pkg.UNSUPPORTED
+             None, 0, None) == pkg.UNSUPPORTED
     assert f(cfg.index, FAKE, FAKE, None, FAKE, 128, 128, 64, 128, big, 128, 0,
-             None) == pkg.UNSUPPORTED
+             None, 0, None) == pkg.UNSUPPORTED
 
 
 # ------------------------------------------------------ kernel resources ----

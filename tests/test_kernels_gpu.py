@@ -963,12 +963,38 @@ def test_export_attributes_cover_their_kernels(pkg):
             assert k["lds_bytes"] == cfg_lds[k["name"]], k
 
 
-# ----------------------------------------------- library workspace, streams --
+# ----------------------------------------------- workspace, streams --------
+
+def test_c_abi_refuses_a_missing_workspace(pkg, oracle, dev):
+    """The C-ABI allocates nothing: a split-K or GEMV plan without a
+    workspace is refused before launch (the output is untouched); with one
+    sized by the query it runs."""
+    lib = pkg.library()
+    g = torch.Generator().manual_seed(23)
+    s = torch.cuda.current_stream().cuda_stream
+    for m, n, k in [(16, 4096, 4096), (1, 4096, 4096)]:
+        x = (torch.randn(m, k, generator=g) * 0.5).half()
+        w = (torch.randn(k, n, generator=g) * 0.02).half()
+        xd, wd = x.to(dev), w.to(dev)
+        y = torch.full((m, n), 3.0, dtype=torch.float16, device=dev)
+        args = (xd.data_ptr(), wd.data_ptr(), y.data_ptr(), m, n, k, k, n, n,
+                0)
+        assert lib.iree_mi355x_matmul_f16(*args, None, 0, s) == \
+            pkg.WORKSPACE_TOO_SMALL
+        torch.cuda.synchronize()
+        assert bool((y == 3.0).all())
+        need = lib.iree_mi355x_matmul_workspace_bytes(m, n, k, 0)
+        ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+        assert lib.iree_mi355x_matmul_f16(*args, ws.data_ptr(), need, s) == \
+            pkg.OK, pkg.last_error()
+        ref = oracle.matmul_f16(x.numpy(), w.numpy())
+        fp16_ok(oracle, y.cpu().numpy(), ref)
+
 
 def test_split_k_on_two_streams_library_workspace(pkg, oracle, dev):
-    """workspace == NULL on two streams at once: each stream has its own
-    library workspace, so the two split-K reductions (and two GEMVs) cannot
-    share arrival counters or partials."""
+    """Calls without a workspace on two streams at once: the wrapper gives
+    each stream its own workspace, so the two split-K reductions (and two
+    GEMVs) cannot share arrival counters or partials."""
     g = torch.Generator().manual_seed(21)
     cases = [(16, 4096, 4096), (1, 4096, 4096)]
     for m, n, k in cases:
@@ -992,10 +1018,10 @@ def test_split_k_on_two_streams_library_workspace(pkg, oracle, dev):
 
 
 def test_library_workspace_under_capture(pkg, oracle, dev):
-    """A capturing stream never allocates: with no library workspace yet the
-    call is refused (WORKSPACE_TOO_SMALL, nothing captured); after one eager
-    call on that stream the workspace exists and the captured split-K
-    matmul replays correctly, with eager work between replays."""
+    """A capturing stream never allocates: with no workspace for it yet the
+    wrapper refuses the call (WORKSPACE_TOO_SMALL, nothing captured); after
+    one eager call on that stream the workspace exists and the captured
+    split-K matmul replays correctly, with eager work between replays."""
     m, n, k = 16, 4096, 4096
     g = torch.Generator().manual_seed(22)
     x = (torch.randn(m, k, generator=g) * 0.5).half()

@@ -33,9 +33,17 @@ def extent(op, loop):
 
 
 def dispatch(pkg, name, constants, tensors, stream=None):
+    """A plugin's dispatch: validate and size the workspace with a query,
+    then run with a zeroed workspace of that size."""
     s = torch.cuda.current_stream().cuda_stream if stream is None else stream
-    st = pkg.call_export(name, constants, [t.data_ptr() for t in tensors],
-                         [t.numel() * t.element_size() for t in tensors], s)
+    ptrs = [t.data_ptr() for t in tensors]
+    lens = [t.numel() * t.element_size() for t in tensors]
+    st, need = pkg.call_export(name, constants, ptrs, lens, s, query=True)
+    assert st == pkg.OK, pkg.last_error()
+    ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=tensors[0].device)
+    st = pkg.call_export(name, constants, ptrs, lens, s,
+                         workspace=ws.data_ptr() if need else None,
+                         workspace_bytes=need)
     assert st == pkg.OK, pkg.last_error()
     torch.cuda.synchronize()
 

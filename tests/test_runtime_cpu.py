@@ -121,6 +121,11 @@ def test_workspace_sizing(pkg):
     with pytest.raises(pkg.MI355XError) as e:
         cb.submit(table, max_concurrent=4, workspace=(FAKE, slice_), stream=0)
     assert e.value.status == pkg.WORKSPACE_TOO_SMALL
+    # and so is none at all: the runtime allocates no workspace of its own
+    arr, n = pkg.binding_table(table)
+    assert pkg.library().iree_mi355x_command_buffer_submit(
+        cb._h, arr, n, 2, None, 0, None) == pkg.WORKSPACE_TOO_SMALL
+    assert "workspace" in pkg.last_error()
     # full tiles: no workspace at all
     cb = pkg.CommandBuffer()
     cb.dispatch("matmul_f16", matmul_consts(pkg, 2048, 4096, 4096),

@@ -80,6 +80,46 @@ def test_program_every_concurrency(pkg, oracle, dev, lanes):
     p.check(oracle)
 
 
+def test_lane_slices_of_different_sizes_on_one_stream(pkg, oracle, dev):
+    """Two command buffers whose lane slices differ, submitted at 2 lanes
+    between flat split-K calls on one stream: lane l's counters sit at l
+    slices, where a buffer used with another slice (or by flat calls) holds
+    partials, so each slice size needs its own zeroed workspace.
+    (Regression: sharing one buffer gave the second lane dirty counters.)"""
+    g = torch.Generator().manual_seed(41)
+    k = 4096
+    x = (torch.randn(16, k, generator=g) * 0.5).half()
+    xd = x.to(dev)
+    progs = []
+    for n in (4096, 11008):
+        ws = [(torch.randn(k, n, generator=g) * 0.02).half() for _ in range(2)]
+        ys = [torch.empty(16, n, dtype=torch.float16, device=dev)
+              for _ in range(2)]
+        cb = pkg.CommandBuffer()
+        for i in range(2):
+            cb.dispatch("matmul_f16", consts(pkg, 16, n, k),
+                        [pkg.slot(0), pkg.slot(1 + i), pkg.slot(3 + i)])
+        cb.end()
+        table = [xd] + [w.to(dev) for w in ws] + ys
+        refs = [oracle.matmul_f16(x.numpy(), w.numpy()) for w in ws]
+        progs.append((cb, table, ys, refs))
+    slices = {p[0].workspace_bytes(p[1], 1) for p in progs}
+    assert len(slices) == 2, slices
+    wf = (torch.randn(k, 11008, generator=g) * 0.02).half()
+    ref_f = oracle.matmul_f16(x.numpy(), wf.numpy())
+    wfd = wf.to(dev)
+    for order in (0, 1, 0, 1):
+        cb, table, ys, refs = progs[order]
+        for y in ys:
+            y.fill_(7.0)
+        cb.submit(table, max_concurrent=2)
+        yf = pkg.matmul(xd, wfd)  # flat split-K on the stream's own buffer
+        torch.cuda.synchronize()
+        for y, ref in zip(ys, refs):
+            assert oracle.fp16_parity(y.cpu().numpy(), ref) <= FP16_BOUND
+        assert oracle.fp16_parity(yf.cpu().numpy(), ref_f) <= FP16_BOUND
+
+
 def test_program_caller_workspace(pkg, oracle, dev):
     p = Program(pkg, dev, seed=11)
     need = p.cb.workspace_bytes(p.table(), 4)

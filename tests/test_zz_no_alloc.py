@@ -12,14 +12,18 @@ pytestmark = pytest.mark.gpu
 FP16_BOUND = 2e-3
 
 
-def _call(lib, fn, x, w, y, stream):
+def _call(pkg, fn, x, w, y, stream):
+    lib = pkg.library()
     m, k = x.shape
     n = w.shape[1]
     args = (x.data_ptr(), w.data_ptr(), y.data_ptr(), m, n, k, x.stride(0),
             w.stride(0), y.stride(0), 0)
     if fn == "no_alloc":
         return lib.iree_mi355x_matmul_f16_no_alloc(*args, stream)
-    return lib.iree_mi355x_matmul_f16(*args, None, 0, stream)
+    # the existing entry point takes its scratch from a caller workspace
+    ws, wsb = pkg.stream_workspace(
+        lib.iree_mi355x_matmul_workspace_bytes(m, n, k, 0), x.device, stream)
+    return lib.iree_mi355x_matmul_f16(*args, ws, wsb, stream)
 
 
 def test_no_alloc_matches_matmul_f16(pkg, oracle, dev):
@@ -44,12 +48,12 @@ def test_no_alloc_matches_matmul_f16(pkg, oracle, dev):
                        device=dev)
         print(f"no_alloc m={x.shape[0]} n={w.shape[1]} k={x.shape[1]}",
               flush=True)
-        assert _call(lib, "no_alloc", x, w, y, s) == pkg.OK, pkg.last_error()
+        assert _call(pkg, "no_alloc", x, w, y, s) == pkg.OK, pkg.last_error()
         outs.append(y)
     torch.cuda.synchronize()
     for (x, w), (xh, wh), y in zip(dev_in, host, outs):
         y_ref = torch.empty_like(y)
-        assert _call(lib, "workspace", x, w, y_ref, s) == pkg.OK
+        assert _call(pkg, "workspace", x, w, y_ref, s) == pkg.OK
         torch.cuda.synchronize()
         got = y.cpu().numpy()
         assert np.array_equal(got.view(np.uint16),
@@ -70,7 +74,7 @@ def test_no_alloc_repeated_and_rejects_oversized_plans(pkg, oracle, dev):
     ref = oracle.matmul_f16(x.numpy(), w.numpy())
     ys = [torch.empty(m, n, dtype=torch.float16, device=dev) for _ in range(4)]
     for y in ys:
-        assert _call(lib, "no_alloc", xd, wd, y, s) == pkg.OK
+        assert _call(pkg, "no_alloc", xd, wd, y, s) == pkg.OK
     torch.cuda.synchronize()
     for y in ys:
         assert oracle.fp16_parity(y.cpu().numpy(), ref) <= FP16_BOUND
@@ -80,7 +84,7 @@ def test_no_alloc_repeated_and_rejects_oversized_plans(pkg, oracle, dev):
     x = torch.zeros(m, k, dtype=torch.float16, device=dev)
     w = torch.zeros(k, n, dtype=torch.float16, device=dev)
     y = torch.full((m, n), 5.0, dtype=torch.float16, device=dev)
-    assert _call(lib, "no_alloc", x, w, y, s) == pkg.WORKSPACE_TOO_SMALL
+    assert _call(pkg, "no_alloc", x, w, y, s) == pkg.WORKSPACE_TOO_SMALL
     assert "workspace" in pkg.last_error()
     torch.cuda.synchronize()
     assert bool((y == 5.0).all())
