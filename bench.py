@@ -341,9 +341,12 @@ def main():
 
     # ---- fp16 4096^3 (B transposed: the TN MFMA path) ----
     g = torch.Generator().manual_seed(0)
-    x16 = (torch.randn(m, k, generator=g) * 0.02).half().to(dev)
-    w16 = (torch.randn(n, k, generator=g) * 0.02).half().to(dev)
+    x16_h = (torch.randn(m, k, generator=g) * 0.02).half()
+    w16_h = (torch.randn(n, k, generator=g) * 0.02).half()
+    x16, w16 = x16_h.to(dev), w16_h.to(dev)
     y16 = torch.empty(m, n, dtype=torch.float16, device=dev)
+    plan16 = pkg.plan(pkg.make_desc(pkg.ELEM_F16, pkg.ELEM_F16, pkg.ELEM_F16,
+                                    m, n, k, pkg.B_TRANSPOSED))
     ms16 = timed(lambda: pkg.matmul(x16, w16, y16, b_transposed=True),
                  args.steps, args.warmup)
     tflops16 = ops / (ms16 * 1e-3) / 1e12
@@ -367,7 +370,8 @@ def main():
 
     # ---- the other BASELINE configs the metric's kernels run on ----
     # C3 M=2048 N=K=4096 with row-major weights (linalg.matmul's map, NN)
-    x, wn = (t.to(dev) for t in inputs.c3_linear_f16(2048, 4096, 4096))
+    c3_h = inputs.c3_linear_f16(2048, 4096, 4096)
+    x, wn = (t.to(dev) for t in c3_h)
     yn = torch.empty(2048, 4096, dtype=torch.float16, device=dev)
     ms_nn = timed(lambda: pkg.matmul(x, wn, yn), args.steps, args.warmup)
     nn_tflops = 2.0 * 2048 * 4096 * 4096 / (ms_nn * 1e-3) / 1e12
@@ -400,8 +404,15 @@ def main():
     c5_512_tflops = 2.0 * 512 * 11008 * 4096 / (c5[512] * 1e-3) / 1e12
 
     # ---- ceilings measured on this box (calibration kernels) ----
-    ceil_i8 = mfma_ceiling(dev, "i8", True)
-    ceil_f16 = mfma_ceiling(dev, "f16", True)
+    # The register-only loop issues the MFMA shape the timed kernel issues:
+    # the _m16 tiles run 16x16 MFMAs, which sustain more products per
+    # second on random operands than the 32x32 ones.
+    def mfma_shape(cfg):
+        return 16 if cfg.endswith("_m16") else 32
+    shape_i8 = mfma_shape(plan.config_name.decode())
+    shape_f16 = mfma_shape(plan16.config_name.decode())
+    ceil_i8 = mfma_ceiling(dev, "i8", True, shape=shape_i8)
+    ceil_f16 = mfma_ceiling(dev, "f16", True, shape=shape_f16)
     stream32 = stream_ceiling(dev, 4096 * 4096 * 2, args.steps, args.warmup)
 
     out = {
@@ -427,13 +438,18 @@ def main():
                      "traffic": profiled_traffic(plan.config_name.decode()),
                      "ceiling": round(ceil_i8, 1),
                      "ceiling_frac": round(tops / ceil_i8, 4),
-                     "ceiling_kind": "register-only int8 MFMA loop on random "
-                                     "operands, measured in this run"},
+                     "ceiling_kind": f"register-only int8 {shape_i8}x"
+                                     f"{shape_i8} MFMA loop (the shape the "
+                                     "kernel issues) on random operands, "
+                                     "measured in this run"},
         "extra": {
             "fp16_4096_tflops": round(tflops16, 1),
             "fp16_4096_frac_peak": round(tflops16 / PEAK_F16_TFLOPS, 4),
             "fp16_4096_layout": "B [N,K] (transposed), f32 acc, f16 out",
+            "fp16_4096_kernel": plan16.config_name.decode(),
             "fp16_mfma_ceiling_tflops": round(ceil_f16, 1),
+            "fp16_mfma_ceiling_shape": f"{shape_f16}x{shape_f16}",
+            "fp16_4096_frac_ceiling": round(tflops16 / ceil_f16, 4),
             "c3_m2048_n4096_k4096_nn_tflops": round(nn_tflops, 1),
             "c3_m2048_n4096_k4096_nn_frac_peak":
                 round(nn_tflops / PEAK_F16_TFLOPS, 4),
@@ -454,6 +470,8 @@ def main():
     }
     if not args.no_cpu_baseline:
         threads = cpu_threads()
+        out["extra"]["cpu_baselines"] = cpu_baselines_extra(
+            inputs, threads, x16_h, w16_h, c3_h)
         cpu_tops, runs, dt = cpu_baseline_i8(a.numpy(), bt.numpy(), threads)
         out["cpu_baseline"] = {
             "value": round(cpu_tops, 4), "unit": "TOPS", "cores": threads,
@@ -464,6 +482,59 @@ def main():
                       "inputs; IREE llvm-cpu is not installable without "
                       "network"}
     print(json.dumps(out), flush=True)
+
+
+def cpu_baselines_extra(inputs, threads, x16, w16, c3, budget_s=1.5):
+    """The C oracle on the host cores beside each extra workload of the
+    default line: a bounded sample of the same inputs (rows of the output,
+    or one attention head), each repeated to about `budget_s`, reported in
+    the workload's own unit and labelled with the sample."""
+    import oracle
+    import numpy as np
+    res = {}
+
+    def rec(name, value, unit, sample):
+        res[name] = {"value": round(value, 4), "unit": unit, "cores": threads,
+                     "kind": "port", "sample": sample}
+
+    rows = 256
+    xs, wt = x16.numpy()[:rows], w16.numpy()
+    sec, runs = cpu_time(lambda: oracle.matmul_f16(
+        xs, wt, b_transposed=True, threads=threads), budget_s)
+    rec("fp16_4096", 2.0 * rows * 4096 * 4096 / sec / 1e12, "TFLOP/s",
+        f"{rows} of the 4096 output rows of the fp16 4096^3 TN matmul, "
+        f"{runs} runs")
+    xs, wn = c3[0].numpy()[:rows], c3[1].numpy()
+    sec, runs = cpu_time(lambda: oracle.matmul_f16(xs, wn, threads=threads),
+                         budget_s)
+    rec("c3_m2048_n4096_k4096_nn", 2.0 * rows * 4096 * 4096 / sec / 1e12,
+        "TFLOP/s", f"{rows} of the 2048 output rows of C3 M=2048 N=K=4096 NN, "
+        f"{runs} runs")
+    xv, wv = c3[0].numpy()[:1], c3[1].numpy()
+    sec, runs = cpu_time(lambda: oracle.matmul_f16(xv, wv, threads=threads),
+                         budget_s)
+    rec("gemv_m1_4096", (4096 * 4096 * 2 + 4 * 4096) / sec / 1e9, "GB/s",
+        f"the whole C3 M=1 N=K=4096 GEMV, {runs} runs")
+    q, k, v = (t.numpy()[:, :1] for t in inputs.c4_attention_f16())
+    sec, runs = cpu_time(lambda: oracle.attention_f16(
+        q, k, v, causal=True, threads=threads), budget_s)
+    rec("c4_attention", 4.0 * 2048 * 2048 * 128 / 2 / sec / 1e12, "TFLOP/s",
+        f"1 of the 32 heads of C4 (causal, S=2048, D=128), {runs} runs")
+    for mm, sample_rows in ((1, 1), (512, 64)):
+        xq, wq, sq = (t.numpy() for t in inputs.c5_w8a16(mm))
+        xq = np.ascontiguousarray(xq[:sample_rows])
+        sec, runs = cpu_time(lambda: oracle.w8a16(xq, wq, sq,
+                                                  threads=threads), budget_s)
+        if mm == 1:
+            rec("c5_w8a16_m1",
+                (4096 * 11008 + 2 * 11008 + 4 * 4096) / sec / 1e9, "GB/s",
+                f"the whole C5 M=1 W8A16 GEMV, {runs} runs")
+        else:
+            rec("c5_w8a16_m512",
+                2.0 * sample_rows * 11008 * 4096 / sec / 1e12, "TFLOP/s",
+                f"{sample_rows} of the 512 output rows of C5 M=512, "
+                f"{runs} runs")
+    return res
 
 
 def suite(pkg, inputs, dev, args):
