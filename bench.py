@@ -822,7 +822,9 @@ def config_step(pkg, dev, name, shape):
     sc = None
     if cfg.a_elem == pkg.ELEM_I8:
         a = torch.randint(-128, 128, (m, k), generator=g).to(torch.int8)
-        b = torch.randint(-128, 128, (n, k), generator=g).to(torch.int8)
+        b = torch.randint(-128, 128,
+                          (n, k) if cfg.b_form == pkg.B_FORM_TN else (k, n),
+                          generator=g).to(torch.int8)
         c = torch.empty(m, n, dtype=torch.int32, device=dev)
     else:
         a = torch.randn(*((k, m) if cfg.a_transposed else (m, k)),

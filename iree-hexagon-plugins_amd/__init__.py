@@ -45,7 +45,7 @@ CAUSAL = 0x1
 # Element kinds (iree_mi355x_elem_t) and kernel families.
 ELEM_F16, ELEM_I8, ELEM_I32, ELEM_F32 = 0, 1, 2, 3
 FAMILY_NONE, FAMILY_MFMA, FAMILY_GENERAL, FAMILY_GEMV = 0, 1, 2, 3
-B_FORM_TN, B_FORM_NN, B_FORM_W8A16 = 0, 1, 2
+B_FORM_TN, B_FORM_NN, B_FORM_W8A16, B_FORM_NN8 = 0, 1, 2, 3
 FAMILY_NAMES = {FAMILY_NONE: "none", FAMILY_MFMA: "mfma",
                 FAMILY_GENERAL: "general", FAMILY_GEMV: "gemv"}
 
@@ -997,7 +997,8 @@ def matmul_mfma_config(index, a, b, c, *, scale=None, splits=0, accumulate=False
     """Run one compiled MFMA configuration (autotuner entry point).
 
     The configuration's B form decides how `b` is read: TN takes B [N, K],
-    NN takes B [K, N] f16, W8A16 takes B [K, N] int8 plus `scale`; a
+    NN takes B [K, N] of the A type (f16, or int8 for the int8 row-major
+    form), W8A16 takes B [K, N] int8 plus `scale`; a
     transposed-A configuration takes A [K, M]. `splits` forces a split-K
     configuration's K split count (0: the planner's; SPLITS_STREAM_K:
     stream-K runs). With `accumulate` the result is added into `c`."""

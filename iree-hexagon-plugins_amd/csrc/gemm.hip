@@ -40,6 +40,8 @@ __device__ __forceinline__ void static_for(F &&f) {
 //   kBNN16 B [K,N] f16 (N-contiguous, row-major weights)
 //   kBW8   B [K,N] int8 with a per-column f16 scale (W8A16), dequantized to
 //          f16 in registers after the LDS read, scale applied in the epilogue
+//   kBNN8  B [K,N] int8 with int8 A (row-major int8 weights: the default map
+//          of linalg.matmul and quantized_matmul), int32 accumulation
 // ----------------------------------------------------------------------------
 
 template <int CH>
@@ -60,11 +62,22 @@ __device__ __forceinline__ int chunk_swizzle(int row) {
 // neighbouring blocks over all 64 banks. For the 32x32 MFMA those two
 // blocks read the same rows at neighbouring windows; for the 16x16 MFMA they
 // read one window at rows 8 apart, so row bit 3 also flips a chunk bit
-// (the swizzle then repeats every 16 rows).
+// (the swizzle then repeats every 16 rows). int8 operands of the int8
+// MFMA take 16 k rows per 16-lane block (two 8-row transposed reads); in the
+// 16x16 form the two blocks served together read rows 16 apart, so row bit
+// 4 flips the chunk's low bit (period 32 rows).
 template <int BMODE, int MS = 32>
 __device__ __forceinline__ int nn_swizzle(int k) {
+  if constexpr (BMODE == kBNN8)
+    return 2 * (k & 7) ^ (MS == 16 ? (k >> 4) & 1 : 0);
   const int hi = MS == 16 ? (k >> 3) & 1 : 0;
   return BMODE == kBNN16 ? 4 * (k & 3) ^ 2 * hi : 2 * (k & 7) ^ hi;
+}
+// Rows after which nn_swizzle repeats.
+template <int BMODE, int MS>
+constexpr int nn_swizzle_period() {
+  return BMODE == kBNN8 ? (MS == 16 ? 32 : 8)
+                        : (MS == 16 ? 16 : (BMODE == kBNN16 ? 4 : 8));
 }
 
 // 8 int8 weights (two dwords) -> 8 f16, exact: each byte b becomes the f16
@@ -178,8 +191,9 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   constexpr int STAGE_BYTES = A_BYTES + B_ROWS * BROW;
   constexpr int KSTEPS = BKB / KSB;
   // LDS reads per K step: FM A fragments, FN B fragments (two transposed
-  // reads each for f16 NN).
-  constexpr int B_READS = BMODE == kBNN16 ? 2 * FN : FN;
+  // reads each for f16 and int8 NN).
+  constexpr bool kTwoReadB = BMODE == kBNN16 || BMODE == kBNN8;
+  constexpr int B_READS = kTwoReadB ? 2 * FN : FN;
   constexpr int A_READS = AT ? 2 * FM : FM;
   constexpr int RD = A_READS + B_READS;
   static_assert(A_ROWS % A_RPP == 0 && B_ROWS % B_RPP == 0, "tile");
@@ -193,12 +207,14 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   // that period, so a lane's swizzle depends only on its row in the pass.
   static_assert(ROWS_PER_PASS % 16 == 0 && (16 / CH) * CH == 16, "swz");
   static_assert(!kNN || (BCH >= 16 && B_RPP % 8 == 0 && B_RPW <= 8), "nn");
-  // Copy passes start on the row swizzle's period (16 rows for 16x16).
-  static_assert(MS == 32 || ((!kNN || B_RPP % 16 == 0) &&
-                             (!AT || A_RPP % 16 == 0)),
-                "16x16 swizzle period");
+  // Copy passes start on the row swizzle's period (16 rows for 16x16, 32
+  // for the int8 16x16 form).
+  static_assert(!kNN || B_RPP % nn_swizzle_period<BMODE, MS>() == 0,
+                "B swizzle period");
+  static_assert(MS == 32 || !AT || A_RPP % 16 == 0, "16x16 swizzle period");
+  static_assert(BMODE != kBNN8 || sizeof(T) == 1, "int8 NN takes int8 A");
   // k rows of a staged row-major operand per MFMA K step
-  constexpr int KROWS = MS == 32 ? 16 : 32;
+  constexpr int KROWS = KSB / (int)sizeof(T);
   // Reads allowed in flight while the previous step's are collected. LDS
   // reads return in issue order and lgkmcnt has 4 bits: with more than 15
   // new reads the wait also takes the oldest of them (still correct).
@@ -412,6 +428,15 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
         b_nn[j] = A_BYTES + k * BROW +
                   (((byte >> 4) ^ nn_swizzle<BMODE, MS>(k)) << 4) +
                   (byte & 15);
+      } else if constexpr (BMODE == kBNN8) {
+        // int8 MFMA: 16 k rows per block (k rows 16 (blk / 2) for 32x32,
+        // 16 blk for 16x16), read as rows krow0 + jj/2 and krow0 + 8 + jj/2,
+        // columns col0 + 8*(jj%2) .. +7 (bytes)
+        const int k = (MS == 32 ? 16 * (blk >> 1) : 16 * blk) + (jj >> 1);
+        const int byte = col0 + 8 * (jj & 1);
+        b_nn[j] = A_BYTES + k * BROW +
+                  (((byte >> 4) ^ nn_swizzle<BMODE, MS>(k)) << 4) +
+                  (byte & 15);
       } else {
         // block reads k rows krow0 + jj/2, columns col0 + 8*(jj%2) .. +7
         // (bytes)
@@ -429,7 +454,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
   struct Frags {
     i32x4 a[FM];
     i32x4 b[FN];
-    i32x2 t[BMODE == kBNN16 ? 2 * FN : FN];
+    i32x2 t[kTwoReadB ? 2 * FN : FN];
     i32x2 ta[AT ? 2 * FM : 1];
   };
   auto read_frags = [&](int slot, int ks, Frags &f) {
@@ -459,6 +484,9 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
         if constexpr (BMODE == kBNN16) {
           f.t[2 * J] = lds_read_tr16_async<0>(pb + b_nn[J]);
           f.t[2 * J + 1] = lds_read_tr16_async<4 * BROW>(pb + b_nn[J]);
+        } else if constexpr (BMODE == kBNN8) {
+          f.t[2 * J] = lds_read_tr8_async<0>(pb + b_nn[J]);
+          f.t[2 * J + 1] = lds_read_tr8_async<8 * BROW>(pb + b_nn[J]);
         } else {
           f.t[J] = lds_read_tr8_async<0>(pb + b_nn[J]);
         }
@@ -486,7 +514,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
 #pragma unroll
       for (int j = 0; j < FN; ++j)
         lgkm_tie(f.b[j]);
-    } else if constexpr (BMODE == kBNN16) {
+    } else if constexpr (kTwoReadB) {
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         lgkm_tie2(f.t[2 * j]);
@@ -1214,6 +1242,16 @@ static const FastConfig kFastConfigs[] = {
     IHP_FAST_CONFIG_S("f16_tn_128x128x64_w2x2_s4_sk", kBTN, f16, f16, 128, 128, 128, 2, 2, 4, true),
     IHP_FAST_CONFIG_S("w8a16_nn_32x256x64_w1x4_s4_sk", kBW8, f16, f16, 32, 256, 128, 1, 4, 4, true),
     IHP_FAST_CONFIG_S("w8a16_nn_128x256x64_w2x4_s4_sk", kBW8, f16, f16, 128, 256, 128, 2, 4, 4, true),
+    // int8 with row-major B ([K,N], linalg.matmul's default map): the int8
+    // weights are staged as they lie and read with ds_read_b64_tr_b8
+    IHP_FAST_CONFIG("i8_nn_256x256x128_w2x4_s2", kBNN8, int8_t, int32_t, 256, 256, 128, 2, 4, 2),
+    IHP_FAST_CONFIG_16("i8_nn_256x256x128_w2x4_s2_m16", kBNN8, int8_t, int32_t, 256, 256, 128, 2, 4, 2),
+    IHP_FAST_CONFIG("i8_nn_128x256x128_w2x4_s2", kBNN8, int8_t, int32_t, 128, 256, 128, 2, 4, 2),
+    // int8 split-K tiles for skinny and ragged M, either B form
+    IHP_FAST_CONFIG_S("i8_tn_32x128x128_w1x4_s4_sk", kBTN, int8_t, int32_t, 32, 128, 128, 1, 4, 4, true),
+    IHP_FAST_CONFIG_S("i8_tn_128x128x128_w2x2_s4_sk", kBTN, int8_t, int32_t, 128, 128, 128, 2, 2, 4, true),
+    IHP_FAST_CONFIG_S("i8_nn_32x256x128_w1x4_s4_sk", kBNN8, int8_t, int32_t, 32, 256, 128, 1, 4, 4, true),
+    IHP_FAST_CONFIG_S("i8_nn_128x256x128_w2x4_s3_sk", kBNN8, int8_t, int32_t, 128, 256, 128, 2, 4, 3, true),
     // transposed A ([K,M], M-contiguous), either B form
     IHP_FAST_CONFIG_AT("f16at_nn_256x256x64_w2x4_s2", kBNN16, f16, f16, 256, 256, 128, 2, 4, 2),
     IHP_FAST_CONFIG_AT("f16at_nn_256x128x64_w2x4_s2", kBNN16, f16, f16, 256, 128, 128, 2, 4, 2),

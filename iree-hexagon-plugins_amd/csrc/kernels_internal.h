@@ -16,6 +16,7 @@ enum BMode {
   kBTN = 0,    // B [N,K], same type as A
   kBNN16 = 1,  // B [K,N] f16
   kBW8 = 2,    // B [K,N] int8 with per-column f16 scale (W8A16)
+  kBNN8 = 3,   // B [K,N] int8, int8 A (row-major int8 weights)
 };
 
 // One matmul launch: C[M,N] = [C +] A[M,K] . B (B [K,N] or [N,K]).

@@ -283,7 +283,8 @@ const iree_mi355x_executable_dispatch_fn_t kPtrs[] = {
 
 // Largest static LDS and workgroup of any kernel an export can launch (the
 // GPU tests compare them with what the loaded kernels report): the int8
-// MFMA rings (128 KiB: 2 x 64 KiB or 4 x 32 KiB, 512 threads), the f16 ones
+// MFMA rings (up to the row-major-B split-K tiles' 4 x 36 / 3 x 48 KiB,
+// 512 threads; split-K tiles use a workspace), the f16 ones
 // up to the 64x256 split-K tile's 4 x 40 KiB (all of a CU's LDS), the
 // W8A16 256x256 ring (3 x 48 KiB), the GEMV (512 threads, its 8-wave
 // reduction buffer at most 128 KiB), the attention K/V rings (two wave
@@ -295,10 +296,7 @@ constexpr uint64_t kF16Flags = IREE_MI355X_DISPATCH_FLAG_RESOURCES_VALID |
                                IREE_MI355X_DISPATCH_FLAG_USES_WORKSPACE;
 const iree_mi355x_executable_dispatch_attrs_t kAttrs[] = {
     {kF16Flags, 163840, 512},
-    {IREE_MI355X_DISPATCH_FLAG_RESOURCES_VALID |
-         IREE_MI355X_DISPATCH_FLAG_USES_MFMA |
-         IREE_MI355X_DISPATCH_FLAG_USES_LDS_DMA,
-     131072, 512},
+    {kF16Flags, 147456, 512},
     {kF16Flags, 147456, 512},
     {IREE_MI355X_DISPATCH_FLAG_RESOURCES_VALID |
          IREE_MI355X_DISPATCH_FLAG_USES_MFMA |

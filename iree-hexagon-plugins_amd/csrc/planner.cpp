@@ -147,7 +147,7 @@ int wanted_b_mode(const iree_mi355x_matmul_desc_t &d) {
     return -1;
   if (bt)
     return kBTN;
-  return d.a_elem == IREE_MI355X_ELEM_F16 ? kBNN16 : -1;
+  return d.a_elem == IREE_MI355X_ELEM_F16 ? kBNN16 : kBNN8;
 }
 
 // Fast-kernel candidates for the shape: N and K tile exactly; M tiles

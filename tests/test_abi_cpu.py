@@ -121,7 +121,10 @@ F16, I8, I32, F32 = 0, 1, 2, 3
     ((F16, F16, F16, 4, 11008, 4096, 0), 3, (4, 512)),
     ((F16, F16, F16, 5, 4096, 4096, 0), 1, None),
     ((F16, F16, F16, 5, 4090, 4096, 0), 2, (64, 64)),
-    ((I8, I8, I32, 1, 4096, 4096, 0), 2, (64, 64)),
+    # int8 with row-major B: macro-tiles, and split-K tiles for skinny M
+    ((I8, I8, I32, 4096, 4096, 4096, 0), 1, (256, 256)),
+    ((I8, I8, I32, 1, 4096, 4096, 0), 1, None),
+    ((I8, I8, I32, 16, 4096, 4096, 1), 1, None),
 ])
 def test_planner_classification(pkg, case, family, tile):
     a, b, c, m, n, k, flags = case

@@ -384,22 +384,32 @@ def test_matmul_i8_golden(pkg, dev):
 
 
 @pytest.mark.parametrize("shape", [(256, 256, 128), (512, 512, 512),
-                                   (256, 1024, 384)])
-def test_matmul_i8_tn_configs(pkg, oracle, dev, shape):
+                                   (256, 1024, 384), (37, 768, 1024)])
+@pytest.mark.parametrize("form", ["tn", "nn"])
+def test_matmul_i8_configs(pkg, oracle, dev, shape, form):
+    """Every int8 configuration of the B form (macro-tiles where the shape
+    tiles, split-K tiles also at a ragged M), bit-exact, twice in a row
+    (the split-K counters re-armed)."""
     m, n, k = shape
-    g = torch.Generator().manual_seed(m + 2 * n + k)
+    tn = form == "tn"
+    g = torch.Generator().manual_seed(m + 2 * n + k + tn)
     a = torch.randint(-128, 128, (m, k), generator=g).to(torch.int8)
-    bt = torch.randint(-128, 128, (n, k), generator=g).to(torch.int8)
-    ref = oracle.matmul_i8(a.numpy(), bt.numpy(), b_transposed=True)
+    b = torch.randint(-128, 128, (n, k) if tn else (k, n),
+                      generator=g).to(torch.int8)
+    ref = oracle.matmul_i8(a.numpy(), b.numpy(), b_transposed=tn)
+    want_form = pkg.B_FORM_TN if tn else pkg.B_FORM_NN8
     ran = 0
     for cfg in pkg.mfma_configs():
-        if cfg.a_elem != pkg.ELEM_I8:
+        if cfg.a_elem != pkg.ELEM_I8 or cfg.b_form != want_form:
             continue
-        if m % cfg.tile_m or n % cfg.tile_n or k % cfg.tile_k:
+        split = "_sk" in cfg.name
+        if (not split and m % cfg.tile_m) or n % cfg.tile_n or k % cfg.tile_k:
             continue
-        c = torch.empty(m, n, dtype=torch.int32, device=dev)
-        pkg.matmul_mfma_config(cfg.index, a.to(dev), bt.to(dev), c)
-        assert np.array_equal(c.cpu().numpy(), ref), cfg.name
+        for _ in range(2):
+            buf, c = canary_out((m, n), torch.int32, dev, 12345)
+            pkg.matmul_mfma_config(cfg.index, a.to(dev), b.to(dev), c)
+            assert np.array_equal(c.cpu().numpy(), ref), cfg.name
+            check_canary(buf, m, n, 12345)
         ran += 1
     assert ran > 0
 
@@ -438,13 +448,14 @@ def test_fast_tiles_accumulate_and_odd_pitch(pkg, oracle, dev):
         tn = cfg.b_form == pkg.B_FORM_TN
         if i8:
             a = torch.randint(-128, 128, (m, k), generator=g).to(torch.int8)
-            b = torch.randint(-128, 128, (n, k), generator=g).to(torch.int8)
+            b = torch.randint(-128, 128, (n, k) if tn else (k, n),
+                              generator=g).to(torch.int8)
             cdt = torch.int32
             init = torch.randint(-10 ** 6, 10 ** 6, (m, n), generator=g,
                                  dtype=torch.int32)
             ref_acc = oracle.matmul_i8(a.numpy(), b.numpy(), init.numpy(),
-                                       b_transposed=True)
-            ref = oracle.matmul_i8(a.numpy(), b.numpy(), b_transposed=True)
+                                       b_transposed=tn)
+            ref = oracle.matmul_i8(a.numpy(), b.numpy(), b_transposed=tn)
         else:
             a = torch.randn(*((k, m) if cfg.a_transposed else (m, k)),
                             generator=g).half()
@@ -474,6 +485,45 @@ def test_fast_tiles_accumulate_and_odd_pitch(pkg, oracle, dev):
         assert bool((buf[:, n].cpu() == fill).all()), cfg.name
         ran += 1
     assert ran >= 8
+
+
+def test_matmul_i8_nn_4096_bit_exact(pkg, oracle, inputs, dev):
+    """C2's operands with B row-major ([K, N], linalg.matmul's default map):
+    a row-major int8 macro-tile, bit-exact."""
+    a, bt = inputs.c2_matmul_i8()
+    b = bt.t().contiguous()
+    p = pkg.plan(pkg.make_desc(pkg.ELEM_I8, pkg.ELEM_I8, pkg.ELEM_I32, 4096,
+                               4096, 4096, 0))
+    assert p.config_name.startswith(b"i8_nn_"), p.config_name
+    c = pkg.matmul(a.to(dev), b.to(dev))
+    got = c.cpu().numpy()
+    row_sums = a.numpy().astype(np.int64) @ b.numpy().astype(np.int64).sum(1)
+    assert np.array_equal(got.astype(np.int64).sum(1), row_sums)
+    ref = oracle.matmul_i8(a.numpy(), bt.numpy(), b_transposed=True)
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("m", [1, 16, 128])
+@pytest.mark.parametrize("bt", [False, True])
+def test_matmul_i8_skinny(pkg, oracle, dev, m, bt):
+    """Skinny int8 at N = K = 4096 through the planner: a split-K MFMA tile
+    (never the general kernel), bit-exact, with the C-ABI's workspace from
+    the wrapper; twice, so the re-armed counters are reused."""
+    n = k = 4096
+    p = pkg.plan(pkg.make_desc(pkg.ELEM_I8, pkg.ELEM_I8, pkg.ELEM_I32, m, n,
+                               k, pkg.B_TRANSPOSED if bt else 0))
+    assert p.family == pkg.FAMILY_MFMA, p.config_name
+    g = torch.Generator().manual_seed(m + bt)
+    a = torch.randint(-128, 128, (m, k), generator=g).to(torch.int8)
+    b = torch.randint(-128, 128, (n, k) if bt else (k, n),
+                      generator=g).to(torch.int8)
+    ref = oracle.matmul_i8(a.numpy(), b.numpy(), b_transposed=bt)
+    ad, bd = a.to(dev), b.to(dev)
+    for _ in range(2):
+        buf, c = canary_out((m, n), torch.int32, dev, -5)
+        pkg.matmul(ad, bd, c, b_transposed=bt)
+        assert np.array_equal(c.cpu().numpy(), ref)
+        check_canary(buf, m, n, -5)
 
 
 def test_c2_matmul_i8_4096_bit_exact(pkg, oracle, inputs, dev):
