@@ -45,10 +45,12 @@ typedef struct iree_mi355x_executable_environment_t {
 // Per-dispatch state. `constants` are the push constants (u32), whose layout
 // each export documents below; 64-bit extents are passed as lo/hi pairs.
 //
-// `workspace` is the split-K / GEMV scratch of this dispatch (NULL: the
-// library's per-device one, which dispatches on different streams must not
-// share); its counter region must be zero before first use, and the kernels
-// leave it zero. Dispatches that may run concurrently need disjoint ones.
+// `workspace` is the split-K / GEMV scratch of this dispatch, sized by a
+// workspace query (below); a dispatch that needs one and gets NULL, or a
+// short one, returns IREE_MI355X_WORKSPACE_TOO_SMALL before anything is
+// enqueued (the library allocates no device memory). Its counter region
+// must be zero before first use, and the kernels leave it zero. Dispatches
+// that may run concurrently need disjoint ones.
 //
 // `workspace_query`, when non-NULL, turns the call into a validation: every
 // check and the plan run, nothing is allocated or enqueued, and the bytes of
