@@ -150,8 +150,11 @@ int iree_mi355x_kernel_resources(int index,
 //  "attention_f16" constants: batch heads seq_q seq_kv head_dim
 //                 scale_bits(f32) flags [kv_heads q_stride_batch_lo/hi
 //                 q_stride_head_lo/hi q_stride_row_lo/hi, then the same
-//                 three for k, v and o] (7 or 32 words)
-//                 bindings: q k v o
+//                 three for k, v and o [head_dim_v mask_stride_batch_lo/hi
+//                 mask_stride_head_lo/hi mask_stride_row_lo/hi
+//                 mask_stride_key_lo/hi]] (7, 32 or 41 words); flags
+//                 IREE_MI355X_ATTENTION_CAUSAL, _OUT_F32, _MASK (41 words)
+//                 bindings: q k v o [mask]
 //  "batch_matmul_f16" constants: the matmul_f16 ones, then batch_lo batch_hi
 //                 stride_a_lo/hi stride_b_lo/hi stride_c_lo/hi activation
 //                 epilogue_bindings (bit 0 bias, bit 1 multiplier)

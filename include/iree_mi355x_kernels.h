@@ -70,6 +70,12 @@ typedef enum iree_mi355x_status_e {
 
 // Attention flags.
 #define IREE_MI355X_ATTENTION_CAUSAL 0x1u
+// iree_mi355x_attention only: write f32 o instead of f16.
+#define IREE_MI355X_ATTENTION_OUT_F32 0x2u
+// iree_mi355x_attention only: an additive mask is given (set exactly when
+// the mask pointer is not NULL; in the executable library's attention_f16
+// dispatch, the mask is binding 4).
+#define IREE_MI355X_ATTENTION_MASK 0x4u
 
 // f16 x f16 matmul with f32 accumulation (inputs widened with arith.extf, as
 // in examples/matmul/matmul.mlir:1-14), f16 or f32 output rounded once at the
@@ -199,6 +205,39 @@ int iree_mi355x_attention_f16_strided(
     int64_t heads, int64_t kv_heads, int64_t seq_q, int64_t seq_kv,
     int64_t head_dim, float scale, uint32_t flags,
     const iree_mi355x_attention_strides_t *strides, void *stream);
+
+// Attention in general form: iree_linalg_ext.attention with any head dims,
+// an optional additive mask and an f16 or f32 output, as the reference
+// lowers it (CG/Pipelines/LoweringPipelines.cpp:561-595; the online_attention
+// of its pipeline test test/codegen/pipelines/
+// hexagon_lower_executable_target.mlir:195-233 has a Q/K head dim of 4, a V
+// head dim of 5, an f16 scale of 0.5 and an f32 accumulator):
+//   o = softmax(q k^T * scale + mask [+ causal]) v
+// q [B, H, Sq, head_dim], k [B, H_kv, Skv, head_dim], v [B, H_kv, Skv,
+// head_dim_v], o [B, H, Sq, head_dim_v] (f32 with OUT_F32), each through its
+// (batch, head, row) strides in elements, the head dim contiguous; mask, if
+// not NULL, an f16 [B, H, Sq, Skv] view through its (batch, head, row, key)
+// strides (0 broadcasts a dimension) added to the scaled scores. A row whose
+// keys are all masked (-inf) writes 0, as the all-masked guard of the
+// decomposed softmax does (examples/attention_layer/attention_layer.mlir:
+// 80-102). head_dim and head_dim_v are 1..256, heads a multiple of
+// kv_heads, heads and batch at most 65535. Shapes the MFMA kernel takes
+// (equal head dims of 64 or 128, no mask, f16 output, the alignment of
+// iree_mi355x_attention_f16_strided) run there; the rest run a general
+// kernel (32-key blocks in LDS, f32 online softmax). _f16 and _f16_strided
+// are this call.
+typedef struct iree_mi355x_attention_t {
+  const void *q, *k, *v;
+  void *o;
+  const void *mask;  // f16 additive mask (with ATTENTION_MASK), or NULL
+  int64_t batch, heads, kv_heads, seq_q, seq_kv;
+  int64_t head_dim, head_dim_v;
+  float scale;
+  uint32_t flags;  // IREE_MI355X_ATTENTION_CAUSAL | _OUT_F32 | _MASK
+  iree_mi355x_attention_strides_t strides;
+  int64_t mask_strides[4];  // batch, head, row, key
+} iree_mi355x_attention_t;
+int iree_mi355x_attention(const iree_mi355x_attention_t *args, void *stream);
 
 // Workspace a matmul_f16 / matmul_i8 / w8a16_matmul call of this shape
 // needs (split-K

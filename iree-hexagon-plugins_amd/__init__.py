@@ -41,6 +41,8 @@ OUT_F32 = 0x4
 A_TRANSPOSED = 0x8
 SPLITS_STREAM_K = -1  # matmul_mfma_config: stream-K runs of (tile, K stage)
 CAUSAL = 0x1
+ATTENTION_OUT_F32 = 0x2
+ATTENTION_MASK = 0x4
 
 # Element kinds (iree_mi355x_elem_t) and kernel families.
 ELEM_F16, ELEM_I8, ELEM_I32, ELEM_F32 = 0, 1, 2, 3
@@ -55,7 +57,7 @@ EXECUTABLE_LIBRARY_VERSION = 0x4D490001
 EXPORTED_SYMBOLS = (
     "iree_mi355x_matmul_f16", "iree_mi355x_matmul_i8",
     "iree_mi355x_w8a16_matmul", "iree_mi355x_attention_f16",
-    "iree_mi355x_attention_f16_strided",
+    "iree_mi355x_attention_f16_strided", "iree_mi355x_attention",
     "iree_mi355x_matmul_workspace_bytes", "iree_mi355x_last_error",
     "iree_mi355x_version", "iree_mi355x_device_count",
     "iree_mi355x_matmul_desc_init", "iree_mi355x_classify_matmul",
@@ -291,6 +293,7 @@ def library():
                                               i64, ctypes.c_float, u32, p]
     lib.iree_mi355x_attention_f16_strided.argtypes = [
         p, p, p, p, i64, i64, i64, i64, i64, i64, ctypes.c_float, u32, p, p]
+    lib.iree_mi355x_attention.argtypes = [p, p]
     lib.iree_mi355x_matmul_workspace_bytes.restype = sz
     lib.iree_mi355x_matmul_workspace_bytes.argtypes = [i64, i64, i64, u32]
     lib.iree_mi355x_batch_matmul_f16.argtypes = [
@@ -617,14 +620,30 @@ def batch_matmul_constants(m, n, k, lda, ldb, ldc, flags, batch, stride_a,
 
 
 def attention_constants(batch, heads, seq_q, seq_kv, head_dim, scale, flags,
-                        kv_heads=None, strides=None):
+                        kv_heads=None, strides=None, head_dim_v=None,
+                        mask_strides=None):
     """Push constants of "attention_f16"; with `strides` (12 element strides:
-    batch, head, row of q, k, v, o) the 32-word strided form."""
+    batch, head, row of q, k, v, o) the 32-word strided form; with
+    `head_dim_v` or `mask_strides` (batch, head, row, key of the mask,
+    binding 4, flag ATTENTION_MASK) the 41-word general form, whose strides
+    default to contiguous ones."""
     scale_bits = struct.unpack("<I", struct.pack("<f", scale))[0]
     words = [batch, heads, seq_q, seq_kv, head_dim, scale_bits, flags]
+    general = head_dim_v is not None or mask_strides is not None
+    dv = head_dim if head_dim_v is None else head_dim_v
+    if general and strides is None:
+        hk = heads if kv_heads is None else kv_heads
+        strides = [heads * seq_q * head_dim, seq_q * head_dim, head_dim,
+                   hk * seq_kv * head_dim, seq_kv * head_dim, head_dim,
+                   hk * seq_kv * dv, seq_kv * dv, dv,
+                   heads * seq_q * dv, seq_q * dv, dv]
     if strides is not None:
         words.append(heads if kv_heads is None else kv_heads)
         for v in strides:
+            words += [v & 0xFFFFFFFF, (v >> 32) & 0xFFFFFFFF]
+    if general:
+        words.append(dv)
+        for v in (mask_strides or (0, 0, 0, 0)):
             words += [v & 0xFFFFFFFF, (v >> 32) & 0xFFFFFFFF]
     return words
 
@@ -947,38 +966,76 @@ class AttentionStrides(ctypes.Structure):
                 ("v", ctypes.c_int64 * 3), ("o", ctypes.c_int64 * 3)]
 
 
-def attention(q, k, v, o=None, *, causal=True, scale=None, stream=None):
-    """Fused attention forward on f16 tensors: q, o [B, Hq, Sq, D]; k, v
-    [B, Hkv, Skv, D] with Hq a multiple of Hkv (query head h reads KV head
-    h // (Hq // Hkv)). Any of them may be a strided view whose last
-    dimension is contiguous: a slice of a longer KV cache, or o as a
-    permuted view of a [B, Sq, Hq, D] buffer."""
+class AttentionArgs(ctypes.Structure):
+    """iree_mi355x_attention_t."""
+    _fields_ = [("q", ctypes.c_void_p), ("k", ctypes.c_void_p),
+                ("v", ctypes.c_void_p), ("o", ctypes.c_void_p),
+                ("mask", ctypes.c_void_p), ("batch", ctypes.c_int64),
+                ("heads", ctypes.c_int64), ("kv_heads", ctypes.c_int64),
+                ("seq_q", ctypes.c_int64), ("seq_kv", ctypes.c_int64),
+                ("head_dim", ctypes.c_int64), ("head_dim_v", ctypes.c_int64),
+                ("scale", ctypes.c_float), ("flags", ctypes.c_uint32),
+                ("strides", AttentionStrides),
+                ("mask_strides", ctypes.c_int64 * 4)]
+
+
+def attention(q, k, v, o=None, *, causal=True, scale=None, mask=None,
+              out_dtype=None, stream=None):
+    """Fused attention forward: q [B, Hq, Sq, D], k [B, Hkv, Skv, D],
+    v [B, Hkv, Skv, Dv] f16 with Hq a multiple of Hkv (query head h reads KV
+    head h // (Hq // Hkv)); o [B, Hq, Sq, Dv], f16 or f32 (``out_dtype``
+    when o is not given). ``mask``, an f16 tensor that broadcasts to
+    [B, Hq, Sq, Skv], is added to the scaled scores; a row whose keys are all
+    -inf is 0. Any operand may be a strided view whose last dimension is
+    contiguous (a slice of a longer KV cache, o a permuted view of a
+    [B, Sq, Hq, Dv] buffer). Equal head dims of 64 or 128 with no mask and
+    an f16 o run the MFMA kernel; the rest the general one (head dims up to
+    256)."""
     import torch
-    for t, nm in ((q, "q"), (k, "k"), (v, "v"), (o, "o")):
-        if t is None:
-            continue
+    for t, nm in ((q, "q"), (k, "k"), (v, "v")):
         if (not isinstance(t, torch.Tensor) or t.dtype != torch.float16
                 or t.dim() != 4 or not _unit_col(t)):
             raise TypeError(f"{nm} must be a 4-D f16 tensor with unit "
                             "stride along head_dim")
+    if o is not None:
+        if (not isinstance(o, torch.Tensor)
+                or o.dtype not in (torch.float16, torch.float32)
+                or o.dim() != 4 or not _unit_col(o)):
+            raise TypeError("o must be a 4-D f16 or f32 tensor with unit "
+                            "stride along head_dim")
+        if out_dtype is not None and out_dtype != o.dtype:
+            raise TypeError(f"o is {o.dtype}, out_dtype {out_dtype}")
+    out_dtype = o.dtype if o is not None else (out_dtype or torch.float16)
+    if out_dtype not in (torch.float16, torch.float32):
+        raise TypeError("out_dtype must be torch.float16 or torch.float32")
     b, h, sq, d = q.shape
     hkv, skv = k.shape[1], k.shape[2]
+    dv = v.shape[3]
     if hkv < 1 or h % hkv:
         raise ValueError(f"k must be [{b}, Hkv, Skv, {d}] with Hkv dividing "
                          f"the {h} query heads, got {list(k.shape)}")
     _shape(k, (b, hkv, skv, d), "k")
-    _shape(v, (b, hkv, skv, d), "v")
+    _shape(v, (b, hkv, skv, dv), "v")
     if o is not None:
-        _shape(o, (b, h, sq, d), "o")
-    _on_device((q, "q"), (k, "k"), (v, "v"), (o, "o"))
+        _shape(o, (b, h, sq, dv), "o")
+    if mask is not None:
+        if not isinstance(mask, torch.Tensor) or mask.dtype != torch.float16:
+            raise TypeError("mask must be an f16 tensor")
+        try:
+            mask = mask.expand(b, h, sq, skv)
+        except RuntimeError:
+            raise ValueError(f"mask {list(mask.shape)} does not broadcast to "
+                             f"{[b, h, sq, skv]}") from None
+    _on_device((q, "q"), (k, "k"), (v, "v"), (o, "o"), (mask, "mask"))
     lib = library()
     if scale is None:
         scale = d ** -0.5
     if o is None:
-        o = torch.empty_like(q, memory_format=torch.contiguous_format)
+        o = torch.empty(b, h, sq, dv, dtype=out_dtype, device=q.device)
     flags = CAUSAL if causal else 0
-    contiguous = all(t.is_contiguous() for t in (q, k, v, o))
-    if contiguous and hkv == h:
+    fast = (mask is None and out_dtype == torch.float16 and d == dv
+            and d in (64, 128))
+    if fast and hkv == h and all(t.is_contiguous() for t in (q, k, v, o)):
         _check(lib.iree_mi355x_attention_f16(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), b, h, sq,
             skv, d, float(scale), flags, _stream_ptr(stream)))
@@ -986,9 +1043,24 @@ def attention(q, k, v, o=None, *, causal=True, scale=None, stream=None):
     st = AttentionStrides()
     for field, t in (("q", q), ("k", k), ("v", v), ("o", o)):
         getattr(st, field)[:] = list(t.stride()[:3])
-    _check(lib.iree_mi355x_attention_f16_strided(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), b, h, hkv, sq,
-        skv, d, float(scale), flags, ctypes.byref(st), _stream_ptr(stream)))
+    if fast:
+        _check(lib.iree_mi355x_attention_f16_strided(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), b, h,
+            hkv, sq, skv, d, float(scale), flags, ctypes.byref(st),
+            _stream_ptr(stream)))
+        return o
+    a = AttentionArgs(q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(),
+                      o=o.data_ptr(), batch=b, heads=h, kv_heads=hkv,
+                      seq_q=sq, seq_kv=skv, head_dim=d, head_dim_v=dv,
+                      scale=float(scale), strides=st)
+    if out_dtype == torch.float32:
+        flags |= ATTENTION_OUT_F32
+    if mask is not None:
+        flags |= ATTENTION_MASK
+        a.mask = mask.data_ptr()
+        a.mask_strides[:] = list(mask.stride())
+    a.flags = flags
+    _check(lib.iree_mi355x_attention(ctypes.byref(a), _stream_ptr(stream)))
     return o
 
 

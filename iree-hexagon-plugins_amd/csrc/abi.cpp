@@ -569,6 +569,114 @@ int iree_mi355x_attention_f16_strided(
       "attention_fwd");
 }
 
+int iree_mi355x_attention(const iree_mi355x_attention_t *a, void *stream) {
+  const char *who = "attention";
+  if (!a)
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: null arguments", who);
+  if (a->flags & ~(IREE_MI355X_ATTENTION_CAUSAL | IREE_MI355X_ATTENTION_OUT_F32 |
+                   IREE_MI355X_ATTENTION_MASK))
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: unknown flag bits 0x%x",
+                who, a->flags);
+  if (!(a->flags & IREE_MI355X_ATTENTION_MASK) != !a->mask)
+    return fail(IREE_MI355X_INVALID_ARGUMENT,
+                "%s: the MASK flag and the mask pointer disagree", who);
+  if (a->batch < 0 || a->heads < 0 || a->kv_heads < 0 || a->seq_q < 0 ||
+      a->seq_kv < 0 || a->head_dim < 0 || a->head_dim_v < 0)
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: negative extent", who);
+  if (!std::isfinite(a->scale))
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: scale not finite", who);
+  if (a->batch == 0 || a->heads == 0 || a->seq_q == 0 || a->head_dim_v == 0)
+    return ok();
+  if (a->kv_heads == 0 || a->heads % a->kv_heads != 0)
+    return fail(IREE_MI355X_INVALID_ARGUMENT,
+                "%s: %lld query heads are not a multiple of %lld KV heads",
+                who, (long long)a->heads, (long long)a->kv_heads);
+  if (a->head_dim < 1 || a->head_dim > 256 || a->head_dim_v > 256)
+    return fail(IREE_MI355X_UNSUPPORTED,
+                "%s: head dims %lld / %lld (1..256 supported)", who,
+                (long long)a->head_dim, (long long)a->head_dim_v);
+  // Grid (query blocks, heads, batch) and 32-bit row and key counters.
+  if (a->batch > 65535 || a->heads > 65535 || a->seq_q >= kMaxExtent / 2 ||
+      a->seq_kv >= kMaxExtent / 2)
+    return fail(IREE_MI355X_UNSUPPORTED, "%s: problem too large", who);
+  if (!a->q || !a->o || (a->seq_kv > 0 && (!a->k || !a->v)))
+    return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: null pointer", who);
+  const iree_mi355x_attention_strides_t &st = a->strides;
+  const int64_t *all[5] = {st.q, st.k, st.v, st.o, a->mask_strides};
+  for (int t = 0; t < 5; ++t)
+    for (int i = 0; i < (t == 4 ? 4 : 3); ++i)
+      if (all[t][i] < 0)
+        return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: negative stride", who);
+  if (st.o[2] < a->head_dim_v)
+    return fail(IREE_MI355X_INVALID_ARGUMENT,
+                "%s: o row stride %lld overlaps its rows", who,
+                (long long)st.o[2]);
+  const bool out_f32 = a->flags & IREE_MI355X_ATTENTION_OUT_F32;
+  if (!aligned(a->q, 2) || !aligned(a->o, out_f32 ? 4 : 2) ||
+      (a->k && !aligned(a->k, 2)) || (a->v && !aligned(a->v, 2)) ||
+      (a->mask && !aligned(a->mask, 2)))
+    return fail(IREE_MI355X_MISALIGNED,
+                "%s: operands must be aligned to their element size", who);
+  const bool causal = a->flags & IREE_MI355X_ATTENTION_CAUSAL;
+
+  // The MFMA kernel: equal head dims of 64 or 128, no mask, f16 output,
+  // 16-byte rows and strides, each head's rows within 4 GiB (32-bit copy
+  // offsets), and a grid of pairs of 128-row query blocks.
+  bool fast = a->head_dim == a->head_dim_v &&
+              (a->head_dim == 64 || a->head_dim == 128) && !a->mask &&
+              !out_f32 && aligned(a->q, 16) && aligned(a->o, 16) &&
+              (!a->k || aligned(a->k, 16)) && (!a->v || aligned(a->v, 16));
+  for (int t = 0; t < 4 && fast; ++t)
+    for (int i = 0; i < 3; ++i)
+      if (all[t][i] % 8 != 0)
+        fast = false;
+  const int64_t row_bytes = a->head_dim * 2;
+  auto head_span = [&](const int64_t *s, int64_t rows) -> int64_t {
+    if (rows <= 1)
+      return rows == 1 ? row_bytes : 0;
+    const uint64_t pitch = (uint64_t)s[2] * 2;
+    if (s[2] > (int64_t)UINT32_MAX ||
+        (pitch > 0 &&
+         (uint64_t)(rows - 1) > (UINT32_MAX - (uint64_t)row_bytes) / pitch))
+      return INT64_MAX;
+    return (int64_t)((uint64_t)(rows - 1) * pitch) + row_bytes;
+  };
+  if (fast && (head_span(st.q, a->seq_q) > (int64_t)UINT32_MAX ||
+               head_span(st.k, a->seq_kv) > (int64_t)UINT32_MAX ||
+               head_span(st.v, a->seq_kv) > (int64_t)UINT32_MAX ||
+               a->batch * a->heads * ((a->seq_q + 127) / 128) >= kMaxExtent))
+    fast = false;
+  if (fast)
+    return iree_mi355x_attention_f16_strided(
+        a->q, a->k, a->v, a->o, a->batch, a->heads, a->kv_heads, a->seq_q,
+        a->seq_kv, a->head_dim, a->scale, a->flags & IREE_MI355X_ATTENTION_CAUSAL,
+        &a->strides, stream);
+  if (dry_run(0))
+    return ok();
+  AttentionGeneralLayout g;
+  for (int i = 0; i < 3; ++i) {
+    g.q[i] = st.q[i];
+    g.k[i] = st.k[i];
+    g.v[i] = st.v[i];
+    g.o[i] = st.o[i];
+  }
+  for (int i = 0; i < 4; ++i)
+    g.mask[i] = a->mask_strides[i];
+  g.heads = (int)a->heads;
+  g.group = (int)(a->heads / a->kv_heads);
+  g.seq_q = (int)a->seq_q;
+  g.seq_kv = (int)a->seq_kv;
+  g.dqk = (int)a->head_dim;
+  g.dv = (int)a->head_dim_v;
+  g.scale = a->scale;
+  g.causal = causal ? 1 : 0;
+  return launch_status(
+      launch_attention_general(a->q, a->k, a->v, a->o, a->mask, a->batch, g,
+                               out_f32 ? 1 : 0, stream),
+      "attention_general");
+}
+
+
 int iree_mi355x_attention_f16(const void *q, const void *k, const void *v,
                               void *o, int64_t batch, int64_t heads,
                               int64_t seq_q, int64_t seq_kv, int64_t head_dim,

@@ -191,6 +191,24 @@ hipError_t launch_attention(const void *q, const void *k, const void *v,
                             const AttentionLayout &layout, int64_t head_dim,
                             float scale, int causal, void *stream);
 
+// The general attention kernel's view (attention_general.hip): strides as
+// AttentionLayout plus the mask's (batch, head, row, key) element strides
+// (0 broadcasts), the two head dims, the scale and the causal flag. Host
+// checks: head dims 1..256, heads and batch at most 65535.
+struct AttentionGeneralLayout {
+  int64_t q[3], k[3], v[3], o[3];
+  int64_t mask[4];
+  int heads, group, seq_q, seq_kv, dqk, dv;
+  float scale;
+  int causal;
+};
+hipError_t launch_attention_general(const void *q, const void *k,
+                                    const void *v, void *o, const void *mask,
+                                    int64_t batch,
+                                    const AttentionGeneralLayout &layout,
+                                    int out_f32, void *stream);
+const KernelEntry *attention_general_kernels(int *count);
+
 #ifdef __HIP_DEVICE_COMPILE__
 #define IHP_HD __device__
 #else

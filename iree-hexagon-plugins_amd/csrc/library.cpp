@@ -156,8 +156,12 @@ int dispatch_w8a16(const iree_mi355x_executable_environment_t *,
 
 // "attention_f16": batch heads seq_q seq_kv head_dim scale_bits flags, then
 // optionally kv_heads and the (batch, head, row) element strides of q, k, v
-// and o as lo/hi pairs (32 words in all); without them the operands are
-// contiguous [B, H, S, D] with one KV head per query head.
+// and o as lo/hi pairs (32 words in all), then optionally head_dim_v and the
+// (batch, head, row, key) element strides of the mask as lo/hi pairs (41
+// words). Without strides the operands are contiguous [B, H, S, D] with one
+// KV head per query head; without the last part head_dim_v is head_dim and
+// there is no mask. Bindings: q k v o [mask]; flags take CAUSAL, OUT_F32 and
+// (41 words only) MASK.
 int dispatch_attention(const iree_mi355x_executable_environment_t *,
                        const iree_mi355x_executable_dispatch_state_t *s) {
   DryRunScope dry(s);
@@ -167,43 +171,80 @@ int dispatch_attention(const iree_mi355x_executable_environment_t *,
     return fail(IREE_MI355X_INVALID_ARGUMENT,
                 "%s: constants or bindings missing", who);
   const uint32_t *c = s->constants;
-  const int64_t batch = c[0], heads = c[1], sq = c[2], skv = c[3], d = c[4];
-  float scale;
-  memcpy(&scale, &c[5], 4);
+  iree_mi355x_attention_t a = {};
+  a.batch = c[0];
+  a.heads = c[1];
+  a.seq_q = c[2];
+  a.seq_kv = c[3];
+  a.head_dim = a.head_dim_v = c[4];
+  memcpy(&a.scale, &c[5], 4);
+  a.flags = c[6];
+  a.kv_heads = a.heads;
   const bool strided = s->constant_count >= 32;
-  int64_t kv_heads = heads;
-  iree_mi355x_attention_strides_t st;
-  int64_t *dst[4] = {st.q, st.k, st.v, st.o};
+  const bool general = s->constant_count >= 41;
+  if (general)
+    a.head_dim_v = c[32];
+  const bool has_mask = a.flags & IREE_MI355X_ATTENTION_MASK;
+  if (has_mask && (!general || s->binding_count < 5))
+    return fail(IREE_MI355X_INVALID_ARGUMENT,
+                "%s: a mask needs the 41-word constants and binding 4", who);
+  int64_t *dst[4] = {a.strides.q, a.strides.k, a.strides.v, a.strides.o};
   for (int t = 0; t < 4; ++t) {
     const bool kv = t == 1 || t == 2;
-    const int64_t rows = kv ? skv : sq;
-    const int64_t one[3] = {mul_checked(mul_checked(heads, rows), d),
+    const int64_t rows = kv ? a.seq_kv : a.seq_q;
+    const int64_t d = t < 2 ? a.head_dim : a.head_dim_v;
+    const int64_t one[3] = {mul_checked(mul_checked(a.heads, rows), d),
                             mul_checked(rows, d), d};
     for (int i = 0; i < 3; ++i)
       dst[t][i] = strided ? u64(c, 8 + 2 * (3 * t + i)) : one[i];
   }
   if (strided)
-    kv_heads = c[7];
+    a.kv_heads = c[7];
+  for (int i = 0; i < 4 && general; ++i)
+    a.mask_strides[i] = u64(c, 33 + 2 * i);
   // Bytes from an operand's first element to the end of its last row.
-  auto reach = [&](const int64_t *sd, int64_t planes_heads, int64_t rows) {
-    if (batch <= 0 || planes_heads <= 0 || rows <= 0)
+  auto reach = [&](const int64_t *sd, int64_t planes_heads, int64_t rows,
+                   int64_t d, int64_t elem) {
+    if (a.batch <= 0 || planes_heads <= 0 || rows <= 0 || d <= 0)
       return (int64_t)0;
     const int64_t last = add_checked(
-        add_checked(mul_checked(batch - 1, sd[0]),
+        add_checked(mul_checked(a.batch - 1, sd[0]),
                     mul_checked(planes_heads - 1, sd[1])),
         mul_checked(rows - 1, sd[2]));
-    return mul_checked(add_checked(last, d), 2);
+    return mul_checked(add_checked(last, d), elem);
   };
+  const int64_t ob = (a.flags & IREE_MI355X_ATTENTION_OUT_F32) ? 4 : 2;
   int st_ok;
-  if ((st_ok = check_binding(s, 0, reach(st.q, heads, sq), who)) ||
-      (st_ok = check_binding(s, 1, reach(st.k, kv_heads, skv), who)) ||
-      (st_ok = check_binding(s, 2, reach(st.v, kv_heads, skv), who)) ||
-      (st_ok = check_binding(s, 3, reach(st.o, heads, sq), who)))
+  if ((st_ok = check_binding(s, 0, reach(a.strides.q, a.heads, a.seq_q,
+                                         a.head_dim, 2), who)) ||
+      (st_ok = check_binding(s, 1, reach(a.strides.k, a.kv_heads, a.seq_kv,
+                                         a.head_dim, 2), who)) ||
+      (st_ok = check_binding(s, 2, reach(a.strides.v, a.kv_heads, a.seq_kv,
+                                         a.head_dim_v, 2), who)) ||
+      (st_ok = check_binding(s, 3, reach(a.strides.o, a.heads, a.seq_q,
+                                         a.head_dim_v, ob), who)))
     return st_ok;
-  return iree_mi355x_attention_f16_strided(
-      s->binding_ptrs[0], s->binding_ptrs[1], s->binding_ptrs[2],
-      s->binding_ptrs[3], batch, heads, kv_heads, sq, skv, d, scale, c[6],
-      &st, s->stream);
+  if (has_mask) {
+    // The mask's rows are seq_kv long with key stride mask_strides[3].
+    int64_t need = 0;
+    if (a.batch > 0 && a.heads > 0 && a.seq_q > 0 && a.seq_kv > 0) {
+      const int64_t *m = a.mask_strides;
+      const int64_t last = add_checked(
+          add_checked(mul_checked(a.batch - 1, m[0]),
+                      mul_checked(a.heads - 1, m[1])),
+          add_checked(mul_checked(a.seq_q - 1, m[2]),
+                      mul_checked(a.seq_kv - 1, m[3])));
+      need = mul_checked(add_checked(last, 1), 2);
+    }
+    if ((st_ok = check_binding(s, 4, need, who)))
+      return st_ok;
+    a.mask = s->binding_ptrs[4];
+  }
+  a.q = s->binding_ptrs[0];
+  a.k = s->binding_ptrs[1];
+  a.v = s->binding_ptrs[2];
+  a.o = s->binding_ptrs[3];
+  return iree_mi355x_attention(&a, s->stream);
 }
 
 // "batch_matmul_f16": the matmul_f16 constants, then batch, stride_a,
@@ -336,7 +377,7 @@ namespace {
 const ihp::KernelEntry *kernel_at(int index) {
   const ihp::KernelEntry *(*lists[])(int *) = {
       ihp::gemm_kernels, ihp::gemv_kernels, ihp::attention_kernels,
-      ihp::runtime_kernels};
+      ihp::attention_general_kernels, ihp::runtime_kernels};
   for (auto list : lists) {
     int n = 0;
     const ihp::KernelEntry *e = list(&n);
@@ -356,6 +397,8 @@ extern "C" int iree_mi355x_kernel_count(void) {
   ihp::gemv_kernels(&n);
   total += n;
   ihp::attention_kernels(&n);
+  total += n;
+  ihp::attention_general_kernels(&n);
   total += n;
   ihp::runtime_kernels(&n);
   return total + n;

@@ -65,6 +65,10 @@ def _load():
     lib.oracle_attention_f16_strided.argtypes = [
         p, p, p, p, i64, i64, i64, i64, i64, i64, ctypes.POINTER(i64),
         ctypes.c_float, ctypes.c_int, ctypes.c_int]
+    lib.oracle_attention.argtypes = [
+        p, p, p, p, p, i64, i64, i64, i64, i64, i64, i64, ctypes.POINTER(i64),
+        ctypes.POINTER(i64), ctypes.c_float, ctypes.c_int, ctypes.c_int,
+        ctypes.c_int]
     lib.oracle_choose_static_tiling_factor.restype = i64
     lib.oracle_choose_static_tiling_factor.argtypes = [i64, i64, i64]
     lib.oracle_select_hmx_tile_sizes.argtypes = [p, p, ctypes.c_int, i64,
@@ -72,6 +76,7 @@ def _load():
     for name in ("oracle_matmul_f16", "oracle_matmul_i8", "oracle_w8a16",
                  "oracle_batch_matmul_f16",
                  "oracle_attention_f16", "oracle_attention_f16_strided",
+                 "oracle_attention",
                  "oracle_select_hmx_tile_sizes"):
         getattr(lib, name).restype = ctypes.c_int
     _lib = lib
@@ -249,6 +254,43 @@ def attention_f16(q, k, v, *, scale=None, causal=True, out=None, threads=None):
     rc = _load().oracle_attention_f16_strided(
         _ptr(q), _ptr(k), _ptr(v), _ptr(o), b, h, hkv, sq, skv, d, strides,
         float(scale), int(causal), threads or default_threads())
+    assert rc == 0, rc
+    return o
+
+
+def attention(q, k, v, *, scale=None, causal=False, mask=None,
+              out_f32=False, out=None, threads=None):
+    """The general form: softmax(QK^T*scale + mask [+ causal]) V for q
+    [B,Hq,Sq,Dqk], k [B,Hkv,Skv,Dqk], v [B,Hkv,Skv,Dv] f16 arrays (strided
+    views allowed, the last dimension contiguous); mask an f16 array that
+    broadcasts to [B,Hq,Sq,Skv] (numpy broadcasting; its strides are read,
+    0 for a broadcast dimension). Masked (-inf) keys weigh 0 and a row with
+    no other key is 0. The result is f16, or f32 with `out_f32`, in `out`
+    or a new contiguous [B,Hq,Sq,Dv] array."""
+    q, qs = _rows_view(q)
+    k, ks = _rows_view(k)
+    v, vs = _rows_view(v)
+    b, h, sq, d = q.shape
+    hkv, skv, dv = k.shape[1], k.shape[2], v.shape[3]
+    if scale is None:
+        scale = 1.0 / float(np.sqrt(d))
+    dt = np.float32 if out_f32 else np.float16
+    o = np.empty((b, h, sq, dv), dt) if out is None else out
+    assert o.dtype == dt and o.shape == (b, h, sq, dv)
+    assert o.strides[-1] == o.itemsize
+    os_ = [st // o.itemsize for st in o.strides[:3]]
+    strides = (ctypes.c_int64 * 12)(*(qs + ks + vs + os_))
+    mptr, mst = None, (ctypes.c_int64 * 4)(0, 0, 0, 0)
+    if mask is not None:
+        mask = np.asarray(mask)
+        assert mask.dtype == np.float16
+        mask = np.broadcast_to(mask, (b, h, sq, skv))
+        mst = (ctypes.c_int64 * 4)(*[st // 2 for st in mask.strides])
+        mptr = mask.ctypes.data
+    rc = _load().oracle_attention(
+        _ptr(q), _ptr(k), _ptr(v), o.ctypes.data, mptr, b, h, hkv, sq, skv, d,
+        dv, strides, mst, float(scale), int(causal), int(out_f32),
+        threads or default_threads())
     assert rc == 0, rc
     return o
 

@@ -435,15 +435,14 @@ int oracle_w8a16(const uint16_t *x, const int8_t *w, const uint16_t *scale,
 
 /* ---------------------------------------------------------- attention ---- */
 
-int oracle_attention_f16_strided(const uint16_t *q, const uint16_t *k,
-                                 const uint16_t *v, uint16_t *o,
-                                 int64_t batch, int64_t heads,
-                                 int64_t kv_heads, int64_t seq_q,
-                                 int64_t seq_kv, int64_t head_dim,
-                                 const int64_t strides[12], float scale,
-                                 int causal, int threads) {
+int oracle_attention(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                     void *o, const uint16_t *mask, int64_t batch,
+                     int64_t heads, int64_t kv_heads, int64_t seq_q,
+                     int64_t seq_kv, int64_t head_dim, int64_t head_dim_v,
+                     const int64_t strides[12], const int64_t mask_strides[4],
+                     float scale, int causal, int out_f32, int threads) {
   if (batch < 0 || heads < 0 || kv_heads <= 0 || seq_q < 0 || seq_kv < 0 ||
-      head_dim < 0 || heads % kv_heads != 0)
+      head_dim < 0 || head_dim_v < 0 || heads % kv_heads != 0)
     return 1;
   const int64_t group = heads / kv_heads;
   const int64_t *qs = strides, *ks = strides + 3, *vs = strides + 6,
@@ -458,11 +457,16 @@ int oracle_attention_f16_strided(const uint16_t *q, const uint16_t *k,
     const uint16_t *qi = q + b * qs[0] + h * qs[1] + i * qs[2];
     const uint16_t *kp = k + b * ks[0] + hk * ks[1];
     const uint16_t *vp = v + b * vs[0] + hk * vs[1];
+    const uint16_t *mi =
+        mask ? mask + b * mask_strides[0] + h * mask_strides[1] +
+                   i * mask_strides[2]
+             : NULL;
     float *qf = (float *)malloc(sizeof(float) * (size_t)(head_dim + 1));
     float *s = (float *)malloc(sizeof(float) * (size_t)(seq_kv + 1));
-    float *acc = (float *)calloc((size_t)head_dim + 1, sizeof(float));
+    float *acc = (float *)calloc((size_t)head_dim_v + 1, sizeof(float));
     for (int64_t d = 0; d < head_dim; ++d)
       qf[d] = oracle_f16_to_f32(qi[d]);
+    /* top-left causal: key j is seen by query i when j <= i */
     const int64_t last = causal ? (i < seq_kv ? i : seq_kv - 1) : seq_kv - 1;
     float mx = -INFINITY;
     for (int64_t j = 0; j <= last; ++j) {
@@ -472,26 +476,50 @@ int oracle_attention_f16_strided(const uint16_t *q, const uint16_t *k,
         dot = dot + prod;
       }
       s[j] = dot * scale;
+      if (mi)
+        s[j] = s[j] + oracle_f16_to_f32(mi[j * mask_strides[3]]);
       if (s[j] > mx)
         mx = s[j];
     }
+    /* keys whose score is -inf (masked) weigh 0; a row with no other key
+     * writes 0 (the all-masked guard, attention_layer.mlir:80-102) */
     float sum = 0.0f;
-    for (int64_t j = 0; j <= last; ++j) {
+    for (int64_t j = 0; j <= last && mx != -INFINITY; ++j) {
+      if (s[j] == -INFINITY)
+        continue;
       float p = expf(s[j] - mx);
       sum = sum + p;
-      for (int64_t d = 0; d < head_dim; ++d) {
+      for (int64_t d = 0; d < head_dim_v; ++d) {
         float prod = p * oracle_f16_to_f32(vp[j * vs[2] + d]);
         acc[d] = acc[d] + prod;
       }
     }
-    uint16_t *oi = o + b * os[0] + h * os[1] + i * os[2];
-    for (int64_t d = 0; d < head_dim; ++d)
-      oi[d] = oracle_f32_to_f16(last >= 0 ? acc[d] / sum : 0.0f);
+    const int64_t at = b * os[0] + h * os[1] + i * os[2];
+    for (int64_t d = 0; d < head_dim_v; ++d) {
+      const float val = sum > 0.0f ? acc[d] / sum : 0.0f;
+      if (out_f32)
+        ((float *)o)[at + d] = val;
+      else
+        ((uint16_t *)o)[at + d] = oracle_f32_to_f16(val);
+    }
     free(qf);
     free(s);
     free(acc);
   }
   return 0;
+}
+
+int oracle_attention_f16_strided(const uint16_t *q, const uint16_t *k,
+                                 const uint16_t *v, uint16_t *o,
+                                 int64_t batch, int64_t heads,
+                                 int64_t kv_heads, int64_t seq_q,
+                                 int64_t seq_kv, int64_t head_dim,
+                                 const int64_t strides[12], float scale,
+                                 int causal, int threads) {
+  const int64_t none[4] = {0, 0, 0, 0};
+  return oracle_attention(q, k, v, o, NULL, batch, heads, kv_heads, seq_q,
+                          seq_kv, head_dim, head_dim, strides, none, scale,
+                          causal, 0, threads);
 }
 
 int oracle_attention_f16(const uint16_t *q, const uint16_t *k,

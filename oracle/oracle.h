@@ -20,6 +20,11 @@
  *   w8a16                 per-element-dequant form, exact power-of-two cases
  *   attention             torch F.scaled_dot_product_attention (the reference
  *                         micro attention model) in f32, causal invariants
+ *   attention (general)   SDPA with attn_mask and unequal head dims, a
+ *                         float64 closed form with causal + mask + grouped
+ *                         heads, brute force at the pipeline test's shapes,
+ *                         masked keys = dropped keys (bits), f16 out = f32
+ *                         out rounded (bits), fully masked rows = 0
  *   select_hmx_tile_sizes reference lit goldens
  *   choose_static_tiling  brute-force divisor search
  *   batch_matmul_f16      per-batch equality with matmul_f16; bias / ReLU /
@@ -131,6 +136,23 @@ int oracle_attention_f16_strided(const uint16_t *q, const uint16_t *k,
                                  int64_t seq_kv, int64_t head_dim,
                                  const int64_t strides[12], float scale,
                                  int causal, int threads);
+
+/* General form: iree_linalg_ext.attention with head dims head_dim (Q, K)
+ * and head_dim_v (V, O), an optional f16 additive mask read through its
+ * (batch, head, row, key) element strides (0 broadcasts), added after the
+ * scale, and f16 (out_f32 = 0) or f32 output. Keys whose score is -inf weigh
+ * 0 and a row with no other key writes 0, as the all-masked-row guard of
+ * examples/attention_layer/attention_layer.mlir:80-102 does. The head dims and f32 output follow the online_attention
+ * of test/codegen/pipelines/hexagon_lower_executable_target.mlir:195-233
+ * (Q/K dim 4, V dim 5, scale 0.5, f32 accumulator); the mask follows the
+ * optional mask operand of iree_linalg_ext.attention that
+ * CG/Pipelines/LoweringPipelines.cpp:561-595 lowers. */
+int oracle_attention(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                     void *o, const uint16_t *mask, int64_t batch,
+                     int64_t heads, int64_t kv_heads, int64_t seq_q,
+                     int64_t seq_kv, int64_t head_dim, int64_t head_dim_v,
+                     const int64_t strides[12], const int64_t mask_strides[4],
+                     float scale, int causal, int out_f32, int threads);
 
 /* chooseStaticTilingFactor, CG/Strategy/Planning/Strategies/
  * StrategySupport.cpp:38-69. dynamic bound is passed as INT64_MIN. */

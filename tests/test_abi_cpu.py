@@ -395,6 +395,102 @@ def test_dispatch_rejects_short_bindings(pkg):
                            [q, q, q - 2, q]) == pkg.INVALID_ARGUMENT
 
 
+def general_args(pkg, **kw):
+    """An iree_mi355x_attention_t over contiguous operands (FAKE pointers:
+    only checks that fail before any launch may use it)."""
+    b, h, hkv, sq, skv, d, dv = (kw.pop(n, dflt) for n, dflt in (
+        ("batch", 1), ("heads", 2), ("kv_heads", 2), ("seq_q", 64),
+        ("seq_kv", 64), ("head_dim", 32), ("head_dim_v", 48)))
+    a = pkg.AttentionArgs(q=FAKE, k=FAKE, v=FAKE, o=FAKE, batch=b, heads=h,
+                          kv_heads=hkv, seq_q=sq, seq_kv=skv, head_dim=d,
+                          head_dim_v=dv, scale=0.5, flags=0)
+    a.strides.q[:] = [h * sq * d, sq * d, d]
+    a.strides.k[:] = [hkv * skv * d, skv * d, d]
+    a.strides.v[:] = [hkv * skv * dv, skv * dv, dv]
+    a.strides.o[:] = [h * sq * dv, sq * dv, dv]
+    for key, val in kw.items():
+        setattr(a, key, val)
+    return a
+
+
+def test_general_attention_argument_errors(pkg):
+    lib = pkg.library()
+
+    def call(**kw):
+        return lib.iree_mi355x_attention(ctypes.byref(general_args(pkg, **kw)),
+                                         None)
+
+    assert lib.iree_mi355x_attention(None, None) == pkg.INVALID_ARGUMENT
+    assert call(flags=0x8) == pkg.INVALID_ARGUMENT
+    assert "unknown flag" in pkg.last_error()
+    # the MASK flag and the mask pointer go together
+    assert call(flags=pkg.ATTENTION_MASK) == pkg.INVALID_ARGUMENT
+    assert call(mask=FAKE) == pkg.INVALID_ARGUMENT
+    assert "disagree" in pkg.last_error()
+    assert call(head_dim=257) == pkg.UNSUPPORTED
+    assert call(head_dim_v=300) == pkg.UNSUPPORTED
+    assert call(head_dim=0) == pkg.UNSUPPORTED
+    assert call(heads=6, kv_heads=4) == pkg.INVALID_ARGUMENT
+    assert call(scale=float("inf")) == pkg.INVALID_ARGUMENT
+    assert call(seq_q=-1) == pkg.INVALID_ARGUMENT
+    assert call(batch=70000) == pkg.UNSUPPORTED
+    assert call(q=None) == pkg.INVALID_ARGUMENT
+    a = general_args(pkg, flags=pkg.ATTENTION_MASK, mask=FAKE)
+    a.mask_strides[:] = [0, 0, -64, 1]
+    assert lib.iree_mi355x_attention(ctypes.byref(a), None) \
+        == pkg.INVALID_ARGUMENT
+    assert "negative stride" in pkg.last_error()
+    a = general_args(pkg)
+    a.strides.o[2] = 47  # below head_dim_v
+    assert lib.iree_mi355x_attention(ctypes.byref(a), None) \
+        == pkg.INVALID_ARGUMENT
+    # element alignment: f16 operands on 2 bytes, an f32 o on 4
+    assert call(q=FAKE + 1) == pkg.MISALIGNED
+    assert call(o=FAKE + 2, flags=pkg.ATTENTION_OUT_F32) == pkg.MISALIGNED
+    assert call(mask=FAKE + 1, flags=pkg.ATTENTION_MASK) == pkg.MISALIGNED
+    # nothing to write: succeeds without touching a device
+    assert call(batch=0) == pkg.OK
+    assert call(seq_q=0) == pkg.OK
+    assert call(head_dim_v=0) == pkg.OK
+    # the strict entry points keep their contract: head dims 64 / 128
+    assert lib.iree_mi355x_attention_f16(FAKE, FAKE, FAKE, FAKE, 1, 1, 64, 64,
+                                         96, 0.1, 0, None) == pkg.UNSUPPORTED
+
+
+def test_general_attention_dispatch_bindings(pkg):
+    # the 41-word form: head_dim_v, mask strides and the mask binding are
+    # all checked against the bindings before any launch
+    b, h, sq, skv, d, dv = 2, 3, 40, 50, 24, 40
+    flags = pkg.ATTENTION_MASK | pkg.ATTENTION_OUT_F32
+    row_mask = [0, 0, skv, 1]  # one [Sq, Skv] mask for every (batch, head)
+    att = pkg.attention_constants(b, h, sq, skv, d, 0.5, flags,
+                                  head_dim_v=dv, mask_strides=row_mask)
+    assert len(att) == 41
+    q = b * h * sq * d * 2
+    kk = b * h * skv * d * 2
+    vv = b * h * skv * dv * 2
+    o = b * h * sq * dv * 4
+    m = sq * skv * 2
+    ok = [q, kk, vv, o, m]
+    st, need = pkg.call_export("attention_f16", att, [FAKE] * 5, ok,
+                               query=True)
+    assert st == pkg.OK and need == 0, pkg.last_error()
+    for i in range(5):
+        short = list(ok)
+        short[i] -= 2
+        assert pkg.call_export("attention_f16", att, [FAKE] * 5, short,
+                               query=True)[0] == pkg.INVALID_ARGUMENT
+        assert f"binding {i}" in pkg.last_error()
+    # a mask needs the 41-word form and its binding
+    assert pkg.call_export("attention_f16", att, [FAKE] * 4, ok[:4],
+                           query=True)[0] == pkg.INVALID_ARGUMENT
+    short_form = pkg.attention_constants(b, h, sq, skv, d, 0.5,
+                                         pkg.ATTENTION_MASK)
+    assert pkg.call_export("attention_f16", short_form, [FAKE] * 5, ok,
+                           query=True)[0] == pkg.INVALID_ARGUMENT
+    assert "41-word" in pkg.last_error()
+
+
 def test_batch_dispatch_rejects_short_bindings(pkg):
     """batch_matmul_f16 export: every binding, the batched spans included,
     is checked before anything launches."""

@@ -366,6 +366,148 @@ def test_attention_cache_slice_golden(oracle):
     assert oracle.fp16_parity(out, d["expected_f32"]) < 2e-3
 
 
+# ------------------------------------------------ attention, general form ---
+
+def attention_f64(q, k, v, scale, causal=False, mask=None):
+    """softmax(q k^T scale + mask [+ top-left causal]) v in float64 with
+    numpy broadcasting of the mask and grouped KV heads; a row with no
+    unmasked key is 0."""
+    rep = q.shape[1] // k.shape[1]
+    k = np.repeat(k.astype(np.float64), rep, axis=1)
+    v = np.repeat(v.astype(np.float64), rep, axis=1)
+    s = np.einsum("bhqd,bhkd->bhqk", q.astype(np.float64), k) * scale
+    if mask is not None:
+        s = s + mask.astype(np.float64)
+    if causal:
+        sq, skv = s.shape[-2:]
+        s = np.where(np.arange(skv)[None, :] > np.arange(sq)[:, None],
+                     -np.inf, s)
+    mx = s.max(axis=-1, keepdims=True)
+    dead = mx == -np.inf
+    p = np.where(dead, 0.0, np.exp(s - np.where(dead, 0.0, mx)))
+    den = p.sum(axis=-1, keepdims=True)
+    return np.einsum("bhqk,bhkd->bhqd", p / np.where(den > 0, den, 1.0), v)
+
+
+def random_mask(rng, shape, dead_frac=0.2):
+    """An f16 additive mask: N(0, 2) values with some keys at -inf."""
+    m = (2 * rng.standard_normal(shape)).astype(np.float16)
+    m[rng.random(shape) < dead_frac] = -np.inf
+    return m
+
+
+@pytest.mark.parametrize("dqk,dv,mask_shape", [
+    (24, 40, (2, 1, 37, 53)), (4, 5, (1, 3, 1, 53)), (64, 64, (2, 3, 37, 53)),
+    (96, 32, (1, 53))])
+def test_attention_general_vs_sdpa_mask(oracle, dqk, dv, mask_shape):
+    # torch's SDPA adds attn_mask after the scale, as iree_linalg_ext
+    # attention does; a broadcast mask (batch, head or row of 1) reads with
+    # stride 0
+    rng = np.random.default_rng(dqk * 100 + dv)
+    b, h, sq, skv = 2, 3, 37, 53
+    q = rng.standard_normal((b, h, sq, dqk)).astype(np.float16)
+    k = rng.standard_normal((b, h, skv, dqk)).astype(np.float16)
+    v = rng.standard_normal((b, h, skv, dv)).astype(np.float16)
+    mask = random_mask(rng, mask_shape, 0.1)
+    full = np.broadcast_to(mask, (b, h, sq, skv))
+    assert not (full == -np.inf).all(axis=-1).any()
+    scale = 0.37
+    want = F.scaled_dot_product_attention(
+        torch.from_numpy(q).float(), torch.from_numpy(k).float(),
+        torch.from_numpy(v).float(), attn_mask=torch.from_numpy(mask).float(),
+        scale=scale).numpy()
+    got32 = oracle.attention(q, k, v, scale=scale, mask=mask, out_f32=True)
+    assert got32.dtype == np.float32 and got32.shape == (b, h, sq, dv)
+    assert oracle.fp16_parity(got32, want) < 1e-5
+    got16 = oracle.attention(q, k, v, scale=scale, mask=mask)
+    # the f16 output is the f32 one rounded once
+    assert np.array_equal(got16, got32.astype(np.float16))
+    # the mask added before the scale would be a different function
+    wrong = attention_f64(q, k, v, 1.0, mask=mask.astype(np.float64) / scale)
+    assert oracle.fp16_parity(got32, wrong * 1.0) > 1e-2 or scale == 1.0
+
+
+def test_attention_general_reference_fixture_shape(oracle):
+    # the shapes of hexagon_lower_executable_target.mlir:195-233: Q 1x2x4,
+    # K 1x3x4, V 1x3x5 f16, scale 0.5, f32 result; against the float64
+    # closed form (no mask, not causal)
+    rng = np.random.default_rng(0)
+    q = rng.standard_normal((1, 1, 2, 4)).astype(np.float16)
+    k = rng.standard_normal((1, 1, 3, 4)).astype(np.float16)
+    v = rng.standard_normal((1, 1, 3, 5)).astype(np.float16)
+    got = oracle.attention(q, k, v, scale=0.5, out_f32=True)
+    want = attention_f64(q, k, v, 0.5)
+    assert np.abs(got - want).max() < 1e-6
+    # brute force of the first row, term by term
+    s = [0.5 * sum(float(q[0, 0, 0, d]) * float(k[0, 0, j, d])
+                   for d in range(4)) for j in range(3)]
+    e = [np.exp(x - max(s)) for x in s]
+    row = [sum(e[j] * float(v[0, 0, j, n]) for j in range(3)) / sum(e)
+           for n in range(5)]
+    assert np.abs(got[0, 0, 0] - row).max() < 1e-6
+
+
+def test_attention_general_masked_keys_drop_out(oracle):
+    # a -inf key weighs exactly 0: the same bits as the call without it
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal((1, 2, 9, 16)).astype(np.float16)
+    k = rng.standard_normal((1, 2, 30, 16)).astype(np.float16)
+    v = rng.standard_normal((1, 2, 30, 24)).astype(np.float16)
+    keep = np.ones(30, bool)
+    keep[[0, 7, 8, 29]] = False
+    mask = np.where(keep, 0.0, -np.inf).astype(np.float16)
+    got = oracle.attention(q, k, v, scale=0.25, mask=mask)
+    want = oracle.attention(q, np.ascontiguousarray(k[:, :, keep]),
+                            np.ascontiguousarray(v[:, :, keep]), scale=0.25)
+    assert np.array_equal(got, want)
+    # a zero mask is no mask
+    zero = np.zeros(30, np.float16)
+    assert np.array_equal(oracle.attention(q, k, v, scale=0.25, mask=zero),
+                          oracle.attention(q, k, v, scale=0.25))
+
+
+def test_attention_general_fully_masked_rows_are_zero(oracle):
+    # the all-masked guard of attention_layer.mlir:80-102 writes 0 (as the
+    # SDPA of this torch does; earlier releases wrote nan)
+    rng = np.random.default_rng(9)
+    q = rng.standard_normal((1, 1, 6, 8)).astype(np.float16)
+    k = rng.standard_normal((1, 1, 10, 8)).astype(np.float16)
+    v = rng.standard_normal((1, 1, 10, 8)).astype(np.float16)
+    mask = np.zeros((6, 10), np.float16)
+    mask[[1, 4]] = -np.inf
+    got = oracle.attention(q, k, v, scale=0.5, mask=mask, out_f32=True)
+    assert (got[0, 0, [1, 4]] == 0).all()
+    want = attention_f64(q, k, v, 0.5, mask=mask)
+    assert np.abs(got - want).max() < 1e-6
+    sdpa = F.scaled_dot_product_attention(
+        torch.from_numpy(q).float(), torch.from_numpy(k).float(),
+        torch.from_numpy(v).float(), attn_mask=torch.from_numpy(mask).float(),
+        scale=0.5).numpy()
+    assert np.abs(got - sdpa).max() < 1e-5
+
+
+@pytest.mark.parametrize("hq,hkv", [(6, 2), (4, 4)])
+def test_attention_general_causal_mask_gqa(oracle, hq, hkv):
+    # causal and a mask together, grouped KV heads, unequal head dims
+    rng = np.random.default_rng(hq + hkv)
+    q = rng.standard_normal((2, hq, 45, 20)).astype(np.float16)
+    k = rng.standard_normal((2, hkv, 60, 20)).astype(np.float16)
+    v = rng.standard_normal((2, hkv, 60, 12)).astype(np.float16)
+    mask = random_mask(rng, (2, hq, 45, 60), 0.3)
+    got = oracle.attention(q, k, v, scale=-0.4, causal=True, mask=mask,
+                           out_f32=True)
+    want = attention_f64(q, k, v, -0.4, causal=True, mask=mask)
+    assert np.abs(got - want).max() < 1e-5
+    # the general form without mask is the attention_f16 routine
+    if hkv == hq:
+        q2 = q[..., :16].copy()
+        k2 = k[..., :16].copy()
+        v2 = v[..., :12].copy()
+        v2 = np.concatenate([v2, v2[..., :4]], axis=-1)
+        assert np.array_equal(oracle.attention(q2, k2, v2, causal=True),
+                              oracle.attention_f16(q2, k2, v2, causal=True))
+
+
 # --------------------------------------------------------------- planner ---
 
 def test_select_hmx_tile_sizes_lit_goldens(oracle):
