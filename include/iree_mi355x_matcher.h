@@ -145,6 +145,12 @@ typedef struct iree_mi355x_match_t {
   // (test/codegen/transforms/convert_matmul_to_hmx.mlir:40-55).
   int32_t init_fill;
   double init_value;
+  // Attention: the loop of Q's and K's head dim (n_loop is V's and O's); in
+  // the decomposed chain, whose loops are those of P.V, the two are equal
+  // and this is n_loop. With IREE_MI355X_ATTENTION_MASK the op's mask input
+  // is a region argument whose map selects, in order, some of (batch_loop,
+  // head_loop, m_loop, k_loop); the dimensions it leaves out broadcast.
+  int32_t head_dim_loop;
 } iree_mi355x_match_t;
 
 // Options.

@@ -253,7 +253,8 @@ class MatchResult(ctypes.Structure):
                 ("k_loop", ctypes.c_int32), ("root", ctypes.c_int32),
                 ("scale", ctypes.c_float), ("head_loop", ctypes.c_int32),
                 ("reason", ctypes.c_char * 160),
-                ("init_fill", ctypes.c_int32), ("init_value", ctypes.c_double)]
+                ("init_fill", ctypes.c_int32), ("init_value", ctypes.c_double),
+                ("head_dim_loop", ctypes.c_int32)]
 
 
 _lib = None
@@ -537,12 +538,15 @@ class Match:
     # ACCUMULATE over a constant fill: fill the output with init_value first
     init_fill: bool = False
     init_value: float = 0.0
+    # attention: the loop of Q's / K's head dim (n_loop is V's)
+    head_dim_loop: int = -1
 
 
 def _match_result(r: MatchResult) -> Match:
     return Match(bool(r.taken), r.export_name.decode(), r.flags, r.batch_loop,
                  r.m_loop, r.n_loop, r.k_loop, r.root, r.scale, r.head_loop,
-                 r.reason.decode(), bool(r.init_fill), r.init_value)
+                 r.reason.decode(), bool(r.init_fill), r.init_value,
+                 r.head_dim_loop)
 
 
 def match(op: LinalgOp, *, named_only=False) -> Match:

@@ -54,7 +54,7 @@ void accept(Match *out, const char *export_name, uint32_t flags) {
 void clear(Match *out) {
   memset(out, 0, sizeof(*out));
   out->batch_loop = out->m_loop = out->n_loop = out->k_loop = -1;
-  out->head_loop = -1;
+  out->head_loop = out->head_dim_loop = -1;
   out->root = -1;
   out->scale = 1.0f;
 }
@@ -581,8 +581,10 @@ void match_contraction(const Op &op, uint32_t options, Types t, Match *out) {
 }
 
 // iree_linalg_ext.attention: Q [.., M, K1], K [.., K2, K1], V [.., K2, N],
-// a scale, an optional mask, O [.., M, N]; K1 and K2 are reductions.
-bool attention_shape(const Op &op, Match *out) {
+// a scale, an optional mask, O [.., M, N]; K1 and K2 are reductions. At
+// most two batch loops (batch, head). Q, K, V are f16 and O f16 or f32
+// (*flags gains OUT_F32); head dims K1 and N are 1..256.
+bool attention_shape(const Op &op, Match *out, uint32_t *flags) {
   const int q = 0, k = 1, v = 2, o = (int)op.num_inputs;
   const uint32_t rank = op.map_rank[q];
   if (rank < 2 || op.map_rank[k] != rank || op.map_rank[v] != rank ||
@@ -591,6 +593,11 @@ bool attention_shape(const Op &op, Match *out) {
     return false;
   }
   const int nb = (int)rank - 2;
+  if (nb > 2) {
+    reject(out, "attention with %d batch loops (batch and head are taken)",
+           nb);
+    return false;
+  }
   for (int i = 0; i < nb; ++i) {
     const int l = op.map[q][i];
     if (l < 0 || is_reduction(op, l) || op.map[k][i] != l ||
@@ -609,15 +616,22 @@ bool attention_shape(const Op &op, Match *out) {
            "V[.., K2, N] O[.., M, N]");
     return false;
   }
-  for (int i : {q, k, v, o})
+  for (int i : {q, k, v})
     if (op.elem_type[i] != IREE_MI355X_TYPE_F16) {
       reject(out, "attention operand %d is %s (f16 is taken)", i,
              type_name(op.elem_type[i]));
       return false;
     }
+  if (op.elem_type[o] == IREE_MI355X_TYPE_F32) {
+    *flags |= IREE_MI355X_ATTENTION_OUT_F32;
+  } else if (op.elem_type[o] != IREE_MI355X_TYPE_F16) {
+    reject(out, "attention output is %s (f16 and f32 are taken)",
+           type_name(op.elem_type[o]));
+    return false;
+  }
   const int64_t d1 = op.loop_extent[k1], dn = op.loop_extent[n];
-  if (d1 != dn || (d1 != 64 && d1 != 128)) {
-    reject(out, "head dims %lld / %lld (64 or 128 are taken)",
+  if (d1 < 1 || d1 > 256 || dn < 1 || dn > 256) {
+    reject(out, "head dims %lld / %lld (static 1..256 are taken)",
            (long long)d1, (long long)dn);
     return false;
   }
@@ -626,6 +640,33 @@ bool attention_shape(const Op &op, Match *out) {
   out->m_loop = m;
   out->n_loop = n;
   out->k_loop = k2;
+  out->head_dim_loop = k1;
+  return true;
+}
+
+// An attention mask read from a region argument: f16 (added to the scaled
+// scores), its map an ordered selection of (batch loops, M, K2), the
+// dimensions it leaves out broadcast.
+bool attention_mask(const Op &op, int index, const Match &shape, Match *out) {
+  if (op.elem_type[index] != IREE_MI355X_TYPE_F16) {
+    reject(out, "attention mask is %s (an f16 additive mask is taken)",
+           type_name(op.elem_type[index]));
+    return false;
+  }
+  const int order[4] = {shape.batch_loop, shape.head_loop, shape.m_loop,
+                        shape.k_loop};
+  int next = 0;
+  for (uint32_t r = 0; r < op.map_rank[index]; ++r) {
+    const int l = op.map[index][r];
+    while (next < 4 && order[next] != l)
+      ++next;
+    if (l < 0 || next == 4) {
+      reject(out, "attention mask map is not a selection of (batch, head, "
+             "M, K2) in order");
+      return false;
+    }
+    ++next;
+  }
   return true;
 }
 
@@ -670,15 +711,21 @@ int match_one(const Op &op, uint32_t options, Types t, const Init &init,
         reject(out, "attention scale is not a constant");
         return IREE_MI355X_OK;
       }
+      uint32_t flags = 0;
+      if (!attention_shape(op, out, &flags))
+        return IREE_MI355X_OK;
       if (op.num_inputs == 5) {
-        reject(out, "attention mask of unknown content (a causal mask "
-               "generic in the region is taken)");
-        return IREE_MI355X_OK;
+        if (op.producer[4] != IREE_MI355X_FROM_ARGUMENT) {
+          reject(out, "attention mask of unknown content (a region argument "
+                 "or a causal mask generic is taken)");
+          return IREE_MI355X_OK;
+        }
+        if (!attention_mask(op, 4, *out, out))
+          return IREE_MI355X_OK;
+        flags |= IREE_MI355X_ATTENTION_MASK;
       }
-      if (!attention_shape(op, out))
-        return IREE_MI355X_OK;
       out->scale = (float)op.scalar[3];
-      accept(out, "attention_f16", 0);
+      accept(out, "attention_f16", flags);
       return IREE_MI355X_OK;
     }
     default:
@@ -1069,17 +1116,19 @@ bool match_attention_chain(const Region &rg, int root, uint32_t options,
     reject(out, "the softmax row max does not start from -inf");
     return true;
   }
+  // The match reports bmm2's loops, so Q.K's head dim must be V's.
   const int64_t head = bmm1.loop_extent[r1.k];
-  if (head != bmm2.loop_extent[r2.n] || (head != 64 && head != 128)) {
-    reject(out, "attention head dims %lld / %lld (64 or 128 are taken)",
-           (long long)head, (long long)bmm2.loop_extent[r2.n]);
+  if (head != bmm2.loop_extent[r2.n] || head < 1 || head > 256) {
+    reject(out, "attention head dims %lld / %lld (equal, static, 1..256 are "
+           "taken)", (long long)head, (long long)bmm2.loop_extent[r2.n]);
     out->root = root;
     return true;
   }
   const int out_type = truncated ? rg.ops[root].elem_type[1]
                                  : bmm2.elem_type[2];
-  if (out_type != IREE_MI355X_TYPE_F16) {
-    reject(out, "attention output is %s (f16 is taken)", type_name(out_type));
+  if (out_type != IREE_MI355X_TYPE_F16 && out_type != IREE_MI355X_TYPE_F32) {
+    reject(out, "attention output is %s (f16 and f32 are taken)",
+           type_name(out_type));
     out->root = root;
     return true;
   }
@@ -1088,8 +1137,12 @@ bool match_attention_chain(const Region &rg, int root, uint32_t options,
   out->m_loop = r2.m;
   out->n_loop = r2.n;
   out->k_loop = r2.k;
+  out->head_dim_loop = r2.n;
   out->scale = (float)(q.factor * k.factor * score_factor);
-  accept(out, "attention_f16", causal ? IREE_MI355X_ATTENTION_CAUSAL : 0u);
+  accept(out, "attention_f16",
+         (causal ? IREE_MI355X_ATTENTION_CAUSAL : 0u) |
+             (out_type == IREE_MI355X_TYPE_F32 ? IREE_MI355X_ATTENTION_OUT_F32
+                                               : 0u));
   return true;
 }
 

@@ -16,14 +16,19 @@ Regions (each as the reference writes it):
     specialize_hmx_contractions.mlir:20-32 over a zero fill, over its
     argument init, and over a fill of 5.0 as in convert_matmul_to_hmx.mlir:
     40-55;
-  * linalg.quantized_matmul with zero points 0.
+  * linalg.quantized_matmul with zero points 0;
+  * iree_linalg_ext.attention ops the general kernel takes: the shapes of
+    test/codegen/pipelines/hexagon_lower_executable_target.mlir:195-233 (Q
+    1x2x4, K 1x3x4, V 1x3x5, scale 0.5, f32 result), unequal head dims with
+    an f16 mask from a region argument broadcast over batch and heads, and
+    the decomposed chain at head dim 96 with an f32 result.
 """
 import numpy as np
 import pytest
 import torch
 
-from test_matcher_cpu import (MIXED_BODY, ZERO_INIT, attention_chain, dequant,
-                              fill, generic, named)
+from test_matcher_cpu import (MIXED_BODY, ZERO_INIT, att_op, attention_chain,
+                              dequant, fill, generic, named)
 
 pytestmark = pytest.mark.gpu
 
@@ -163,3 +168,91 @@ def test_quantized_matmul_region(pkg, oracle, dev):
              [a.to(dev), bt.to(dev), c])
     ref = oracle.matmul_i8(a.numpy(), bt.numpy(), b_transposed=True)
     assert np.array_equal(c.cpu().numpy(), ref)
+
+
+def mask_strides(op, index, m, sizes):
+    """Element strides (batch, head, row, key) of a contiguous mask whose map
+    selects some of the match's (batch, head, M, K2) loops; 0 where it
+    broadcasts."""
+    loops = [op.map[index][r] for r in range(op.map_rank[index])]
+    strides, acc = {}, 1
+    for l in reversed(loops):
+        strides[l] = acc
+        acc *= sizes[l]
+    return [strides.get(l, 0) for l in (m.batch_loop, m.head_loop, m.m_loop,
+                                        m.k_loop)]
+
+
+@pytest.mark.parametrize("case", ["pipeline_fixture", "mask_rows",
+                                  "mask_full_causal"])
+def test_attention_op_general_region(pkg, oracle, dev, case):
+    print(f"attention op {case}", flush=True)
+    if case == "pipeline_fixture":
+        op = att_op(pkg, 4, head_v=5, out="f32", batch_dims="b",
+                    sizes={"b": 1, "m": 2, "k2": 3}, scale=0.5)
+        mshape = None
+    elif case == "mask_rows":
+        op = att_op(pkg, 96, head_v=64, mask="m k2",
+                    sizes={"b": 2, "h": 3, "m": 100, "k2": 150}, scale=0.1)
+        mshape = (100, 150)
+    else:
+        op = att_op(pkg, 40, mask="b h m k2", out="f32",
+                    sizes={"b": 1, "h": 2, "m": 64, "k2": 64}, scale=0.2)
+        mshape = (1, 2, 64, 64)
+    m = pkg.match_region([op])
+    assert m.taken and m.export == "attention_f16", m.reason
+    sizes = [int(x) for x in op.loop_extent[:op.num_loops]]
+    b = sizes[m.batch_loop]
+    h = sizes[m.head_loop] if m.head_loop >= 0 else 1
+    sq, skv = sizes[m.m_loop], sizes[m.k_loop]
+    d, dv = sizes[m.head_dim_loop], sizes[m.n_loop]
+    out_f32 = bool(m.flags & pkg.ATTENTION_OUT_F32)
+    causal = case == "mask_full_causal"
+    flags = m.flags | (pkg.CAUSAL if causal else 0)
+    g = torch.Generator().manual_seed(len(case))
+    q = torch.randn(b, h, sq, d, generator=g).half()
+    k = torch.randn(b, h, skv, d, generator=g).half()
+    v = torch.randn(b, h, skv, dv, generator=g).half()
+    o = torch.full((b, h, sq, dv), float("nan"),
+                   dtype=torch.float32 if out_f32 else torch.float16)
+    tensors = [q, k, v, o]
+    ms = [0, 0, 0, 0]
+    mask = None
+    if mshape is not None:
+        mask = (2 * torch.randn(*mshape, generator=g)).half()
+        mask[torch.rand(*mshape, generator=g) < 0.2] = float("-inf")
+        ms = mask_strides(op, 4, m, sizes)
+        tensors.append(mask)
+    dev_t = [t.to(dev) for t in tensors]
+    dispatch(pkg, "attention_f16",
+             pkg.attention_constants(b, h, sq, skv, d, m.scale, flags,
+                                     head_dim_v=dv, mask_strides=ms),
+             dev_t)
+    got = dev_t[3].cpu().numpy()
+    ref = oracle.attention(q.numpy(), k.numpy(), v.numpy(), scale=m.scale,
+                           causal=causal, out_f32=out_f32,
+                           mask=None if mask is None else mask.numpy())
+    fp16_ok(oracle, got, ref, bound=2e-5 if out_f32 else 2e-3)
+
+
+def test_attention_chain_head96_f32(pkg, oracle, dev):
+    # the decomposed chain of attention_layer.mlir at head dim 96, without
+    # its final truncation: an f32 result
+    batch, seq, head = 2, 200, 96
+    ops = attention_chain(pkg, head=head, batch=batch, seq=seq, out="f32")
+    m = pkg.match_region(ops)
+    assert m.taken and m.flags == pkg.ATTENTION_OUT_F32, m.reason
+    pv = ops[m.root]
+    d = extent(pv, m.head_dim_loop)
+    assert d == extent(pv, m.n_loop) == head
+    g = torch.Generator().manual_seed(96)
+    q, k, v = (torch.randn(batch, 1, seq, head, generator=g).half()
+               for _ in range(3))
+    o = torch.empty(batch, 1, seq, head, dtype=torch.float32, device=dev)
+    dispatch(pkg, "attention_f16",
+             pkg.attention_constants(batch, 1, seq, seq, head, m.scale,
+                                     m.flags, head_dim_v=head),
+             [q.to(dev), k.to(dev), v.to(dev), o])
+    ref = oracle.attention(q.numpy(), k.numpy(), v.numpy(), scale=m.scale,
+                           out_f32=True)
+    fp16_ok(oracle, o.cpu().numpy(), ref, bound=2e-5)

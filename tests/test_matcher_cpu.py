@@ -17,6 +17,7 @@ pipeline decides for it, restated for this library's exports:
   * examples/attention_layer/attention_layer.mlir:48-105, the decomposed
     attention, and variants of it.
 """
+import functools
 import math
 
 import pytest
@@ -569,10 +570,14 @@ def test_attention_chain_variants(pkg):
     # not attention, or not a kernel of this library
     m = pkg.match_region(attention_chain(pkg, exp=False))
     assert not m.taken
+    # other head dims and an f32 result take the general kernel
     m = pkg.match_region(attention_chain(pkg, head=96))
-    assert not m.taken and "head dims" in m.reason
+    assert m.taken and m.flags == 0, m.reason
+    assert m.head_dim_loop == m.n_loop
     m = pkg.match_region(attention_chain(pkg, out="f32"))
-    assert not m.taken and "f32" in m.reason
+    assert m.taken and m.flags == pkg.ATTENTION_OUT_F32, m.reason
+    m = pkg.match_region(attention_chain(pkg, head=300))
+    assert not m.taken and "head dims" in m.reason
 
 
 def test_attention_chain_inits(pkg):
@@ -605,28 +610,76 @@ def test_attention_chain_generic_contraction_bodies(pkg):
     assert not pkg.match_region(attention_chain(pkg, bmm1_body=maxbody)).taken
 
 
+def att_op(pkg, head, scale_const=True, mask=None, head_v=None, out="f16",
+           mask_type="f16", mask_from="arg", batch_dims="b h", sizes=None,
+           scale=0.125):
+    """iree_linalg_ext.attention over (batch dims) M K1 K2 N; `mask` is the
+    mask's map (None: no mask); `sizes` overrides loop extents."""
+    bd = batch_dims.split()
+    pre = " ".join(bd)
+    maps = [f"{pre} m k1", f"{pre} k2 k1", f"{pre} k2 n", ""]
+    types = ["f16", "f16", "f16", "f16"]
+    prods = ["arg", "arg", "arg", ("const", scale) if scale_const else "arg"]
+    if mask is not None:
+        maps.append(mask)
+        types.append(mask_type)
+        prods.append(mask_from)
+    ext = {"b": 1, "h": 32, "g": 2, "m": 2048, "n": head_v or head, "k1": head,
+           "k2": 2048}
+    ext.update(sizes or {})
+    return pkg.linalg_op(pkg.OP_ATTENTION, f"{pre} m n k1 k2",
+                         maps + [f"{pre} m n"], types + [out],
+                         inputs=len(maps), reductions=["k1", "k2"],
+                         extents={d: ext[d] for d in bd + ["m", "n", "k1",
+                                                           "k2"]},
+                         producers=prods)
+
+
 def test_linalg_ext_attention_op(pkg):
-    def att(head, scale_const=True, mask=False):
-        maps = ["b h m k1", "b h k2 k1", "b h k2 n", ""]
-        types = ["f16", "f16", "f16", "f16"]
-        prods = ["arg", "arg", "arg", ("const", 0.125) if scale_const else "arg"]
-        if mask:
-            maps.append("b h m k2")
-            types.append("f16")
-            prods.append("arg")
-        return pkg.linalg_op(pkg.OP_ATTENTION, "b h m n k1 k2",
-                             maps + ["b h m n"], types + ["f16"],
-                             inputs=len(maps), reductions=["k1", "k2"],
-                             extents={"b": 1, "h": 32, "m": 2048, "n": head,
-                                      "k1": head, "k2": 2048},
-                             producers=prods)
+    att = functools.partial(att_op, pkg)
     m = pkg.match(att(128))
     assert m.taken and m.export == "attention_f16" and m.scale == 0.125
-    assert (m.batch_loop, m.head_loop, m.m_loop, m.n_loop, m.k_loop) == \
-        (0, 1, 2, 3, 5)
-    assert not pkg.match(att(80)).taken
+    assert (m.batch_loop, m.head_loop, m.m_loop, m.n_loop, m.k_loop,
+            m.head_dim_loop) == (0, 1, 2, 3, 5, 4)
+    assert m.flags == 0
     assert not pkg.match(att(128, scale_const=False)).taken
-    assert "mask" in pkg.match(att(128, mask=True)).reason
+    # head dims 1..256, Q/K and V apart, f16 or f32 output
+    m = pkg.match(att(80))
+    assert m.taken and m.flags == 0, m.reason
+    m = pkg.match(att(4, head_v=5, out="f32"))
+    assert m.taken and m.flags == pkg.ATTENTION_OUT_F32, m.reason
+    assert m.head_dim_loop == 4 and m.n_loop == 3
+    m = pkg.match(att(257))
+    assert not m.taken and "head dims" in m.reason
+    m = pkg.match(att(64, out="bf16"))
+    assert not m.taken and "output" in m.reason
+    m = pkg.match(att(64, batch_dims="b g h"))
+    assert not m.taken and "batch loops" in m.reason
+
+
+@pytest.mark.parametrize("mask_map", ["b h m k2", "m k2", "b m k2", "h k2",
+                                      "k2", "b h m"])
+def test_linalg_ext_attention_argument_mask(pkg, mask_map):
+    # an f16 mask from a region argument, full or broadcast along the
+    # dimensions its map leaves out
+    m = pkg.match(att_op(pkg, 64, mask=mask_map))
+    assert m.taken, m.reason
+    assert m.flags == pkg.ATTENTION_MASK
+
+
+@pytest.mark.parametrize("mask_map,mask_type,mask_from,why", [
+    ("b h m k2", "i1", "arg", "f16 additive"),
+    ("b h m k2", "f32", "arg", "f16 additive"),
+    ("b h m k2", "f16", ("const", 0.0), "unknown content"),
+    ("b h k2 m", "f16", "arg", "selection"),
+    ("b h m k1", "f16", "arg", "selection"),
+    ("m b k2", "f16", "arg", "selection"),
+])
+def test_linalg_ext_attention_mask_rejects(pkg, mask_map, mask_type,
+                                           mask_from, why):
+    m = pkg.match(att_op(pkg, 64, mask=mask_map, mask_type=mask_type,
+                         mask_from=mask_from))
+    assert not m.taken and why in m.reason, m.reason
 
 
 def test_malformed_descriptions_are_errors(pkg):
