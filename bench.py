@@ -20,6 +20,9 @@ each with the C oracle timed beside it on this host.
 --tune times every compiled MFMA macro-tile on the 4096^3 shapes;
 --tune --tune-counters profiles each one under rocprofv3 (SQ counters per
 wave: MFMA busy fraction, waits, LDS and VALU instructions).
+--tune --tune-skinny sweeps tiles x split counts on the skinny shapes; with
+--tune-counters it profiles the planner's pick and the fastest candidates of
+each shape under rocprofv3 (SQ counters and HBM bytes).
 """
 from __future__ import annotations
 
@@ -66,6 +69,12 @@ def parse():
                    help="with --only config: the MFMA configuration to run")
     p.add_argument("--shape", default="4096,4096,4096",
                    help="with --only config: M,N,K")
+    p.add_argument("--splits", type=int, default=0,
+                   help="with --only config: K splits of a split-K tile "
+                        "(0: the planner's; -1: stream-K)")
+    p.add_argument("--rotate", action="store_true",
+                   help="with --only config: rotate copies of B past the "
+                        "Infinity Cache, as the skinny sweep does")
     p.add_argument("--tune-counters", action="store_true",
                    help="with --tune: profile every candidate on the 4096^3 "
                         "shapes under rocprofv3 (SQ counters per wave)")
@@ -746,7 +755,8 @@ def only(pkg, inputs, dev, args):
         return
     if w == "config":
         fn = config_step(pkg, dev, args.config,
-                         [int(x) for x in args.shape.split(",")])
+                         [int(x) for x in args.shape.split(",")],
+                         splits=args.splits, rotate=args.rotate)
     elif w == "i8":
         a, bt = (t.to(dev) for t in inputs.c2_matmul_i8())
         c = torch.empty(4096, 4096, dtype=torch.int32, device=dev)
@@ -812,9 +822,11 @@ def only(pkg, inputs, dev, args):
                       "steps": args.steps}), flush=True)
 
 
-def config_step(pkg, dev, name, shape):
+def config_step(pkg, dev, name, shape, splits=0, rotate=False):
     """One launch of MFMA configuration `name` on random operands of
-    shape (M, N, K) in the layout the configuration reads."""
+    shape (M, N, K) in the layout the configuration reads, with `splits`
+    K splits (split-K tiles); with `rotate`, each launch reads the next of
+    enough copies of B to pass the Infinity Cache."""
     import torch
     cfg = next(c for c in pkg.mfma_configs() if c.name == name)
     m, n, k = shape
@@ -839,7 +851,18 @@ def config_step(pkg, dev, name, shape):
         c = torch.empty(m, n, dtype=torch.float32 if cfg.c_elem == pkg.ELEM_F32
                         else torch.float16, device=dev)
     a, b = a.to(dev), b.to(dev)
-    return lambda: pkg.matmul_mfma_config(cfg.index, a, b, c, scale=sc)
+    copies = 1
+    if rotate:
+        copies = max(1, min(24, ROTATE_BYTES // (b.numel() * b.element_size())
+                            + 1))
+    bs = [b] + [b.clone() for _ in range(copies - 1)]
+    it = [0]
+
+    def step():
+        pkg.matmul_mfma_config(cfg.index, a, bs[it[0] % copies], c, scale=sc,
+                               splits=splits)
+        it[0] += 1
+    return step
 
 
 # SQ counters one rocprofv3 pass can hold (at most 8 SQ counters), and what
@@ -918,66 +941,189 @@ def tune_counters(pkg, args):
     shutil.rmtree(work, ignore_errors=True)
 
 
-def tune_skinny(pkg, dev, args):
-    """Every eligible tile at every split count (1..16) and in stream-K runs
-    on the skinny C3 / C5 shapes and two tile counts stream-K is planned
-    for, with rotating weights: the sweep the planner's skinny tuned
-    entries, its split enumeration and its stream-K choice were checked
-    against."""
-    import torch
-    shapes = [("f16", 16, 4096, 4096), ("f16", 16, 11008, 4096),
-              ("f16", 16, 4096, 11008), ("f16", 128, 4096, 4096),
-              ("f16", 128, 11008, 4096), ("f16", 128, 4096, 11008),
-              ("w8a16", 512, 11008, 4096), ("w8a16", 128, 11008, 4096),
-              # tile counts stream-K is planned for
-              ("f16", 192, 11008, 4096), ("w8a16", 192, 11008, 11008)]
-    cfgs = pkg.mfma_configs()
-    for kind, m, n, k in shapes:
-        g = torch.Generator().manual_seed(m + n + k)
-        x = (torch.randn(m, k, generator=g) * 0.5).half().to(dev)
-        if kind == "f16":
-            w0 = (torch.randn(k, n, generator=g) * 0.02).half().to(dev)
-            sc, form = None, pkg.B_FORM_NN
-            desc = pkg.make_desc(pkg.ELEM_F16, pkg.ELEM_F16, pkg.ELEM_F16, m, n, k)
-        else:
-            w0 = torch.randint(-128, 128, (k, n), generator=g).to(torch.int8).to(dev)
-            sc = (torch.rand(n, generator=g) * 0.019 + 0.001).half().to(dev)
-            form = pkg.B_FORM_W8A16
-            desc = pkg.make_desc(pkg.ELEM_F16, pkg.ELEM_I8, pkg.ELEM_F16, m, n,
-                                 k, has_scale=True)
-        copies = max(1, min(24, ROTATE_BYTES // (w0.numel() * w0.element_size()) + 1))
-        ws = [w0] + [w0.clone() for _ in range(copies - 1)]
-        y = torch.empty(m, n, dtype=torch.float16, device=dev)
-        plan = pkg.plan(desc)
-        for c in cfgs:
-            if (c.b_form != form or c.a_transposed or c.c_elem != pkg.ELEM_F16
-                    or n % c.tile_n or k % c.tile_k):
-                continue
-            split = "_sk" in c.name
-            if not split and m % c.tile_m:
-                continue
-            for sp in ((1, 2, 3, 4, 6, 8, 12, 16, pkg.SPLITS_STREAM_K)
-                       if split else (0,)):
-                if split and sp > 0 and k // sp < c.tile_k:
-                    continue
-                it = [0]
+SKINNY_SHAPES = [("f16", 16, 4096, 4096), ("f16", 16, 11008, 4096),
+                 ("f16", 16, 4096, 11008), ("f16", 128, 4096, 4096),
+                 ("f16", 128, 11008, 4096), ("f16", 128, 4096, 11008),
+                 ("w8a16", 512, 11008, 4096), ("w8a16", 128, 11008, 4096),
+                 # tile counts stream-K is planned for
+                 ("f16", 192, 11008, 4096), ("w8a16", 192, 11008, 11008)]
 
-                def fn():
-                    pkg.matmul_mfma_config(c.index, x, ws[it[0] % copies], y,
-                                           scale=sc, splits=sp)
-                    it[0] += 1
-                ms = timed(fn, args.steps, args.warmup)
-                print(json.dumps({"shape": [kind, m, n, k], "config": c.name,
-                                  "splits": sp, "us": round(ms * 1000, 2),
-                                  "planned": c.index == plan.config_index and
-                                  (not split or
-                                   (sp == pkg.SPLITS_STREAM_K
-                                    if plan.stream_k_steps > 0
-                                    else sp == plan.splits))}), flush=True)
+
+def skinny_sweep(pkg, dev, args, kind, m, n, k):
+    """Every eligible tile at every split count (1..16) and in stream-K runs
+    on one skinny shape, with rotating weights: a list of records."""
+    import torch
+    g = torch.Generator().manual_seed(m + n + k)
+    x = (torch.randn(m, k, generator=g) * 0.5).half().to(dev)
+    if kind == "f16":
+        w0 = (torch.randn(k, n, generator=g) * 0.02).half().to(dev)
+        sc, form = None, pkg.B_FORM_NN
+        desc = pkg.make_desc(pkg.ELEM_F16, pkg.ELEM_F16, pkg.ELEM_F16, m, n, k)
+    else:
+        w0 = torch.randint(-128, 128, (k, n), generator=g).to(torch.int8).to(dev)
+        sc = (torch.rand(n, generator=g) * 0.019 + 0.001).half().to(dev)
+        form = pkg.B_FORM_W8A16
+        desc = pkg.make_desc(pkg.ELEM_F16, pkg.ELEM_I8, pkg.ELEM_F16, m, n,
+                             k, has_scale=True)
+    copies = max(1, min(24, ROTATE_BYTES // (w0.numel() * w0.element_size()) + 1))
+    ws = [w0] + [w0.clone() for _ in range(copies - 1)]
+    y = torch.empty(m, n, dtype=torch.float16, device=dev)
+    plan = pkg.plan(desc)
+    out = []
+    for c in pkg.mfma_configs():
+        if (c.b_form != form or c.a_transposed or c.c_elem != pkg.ELEM_F16
+                or n % c.tile_n or k % c.tile_k):
+            continue
+        split = "_sk" in c.name
+        if not split and m % c.tile_m:
+            continue
+        for sp in ((1, 2, 3, 4, 6, 8, 12, 16, pkg.SPLITS_STREAM_K)
+                   if split else (0,)):
+            if split and sp > 0 and k // sp < c.tile_k:
+                continue
+            it = [0]
+
+            def fn():
+                pkg.matmul_mfma_config(c.index, x, ws[it[0] % copies], y,
+                                       scale=sc, splits=sp)
+                it[0] += 1
+            ms = timed(fn, args.steps, args.warmup)
+            out.append({"shape": [kind, m, n, k], "config": c.name,
+                        "splits": sp, "us": round(ms * 1000, 2),
+                        "planned": c.index == plan.config_index and
+                        (not split or
+                         (sp == pkg.SPLITS_STREAM_K
+                          if plan.stream_k_steps > 0
+                          else sp == plan.splits))})
+    del ws, x, y
+    torch.cuda.empty_cache()
+    return out
+
+
+def tune_skinny(pkg, dev, args):
+    """The sweep the planner's skinny tuned entries, its split enumeration
+    and its stream-K choice were checked against (skinny_sweep on every
+    skinny C3 / C5 shape and two tile counts stream-K is planned for)."""
+    for kind, m, n, k in SKINNY_SHAPES:
+        for rec in skinny_sweep(pkg, dev, args, kind, m, n, k):
+            print(json.dumps(rec), flush=True)
+
+
+# One pass each: FETCH_SIZE takes 3 of a pass's 4 TCC counters and
+# WRITE_SIZE 2, so they cannot share one.
+SKINNY_TRAFFIC = ("FETCH_SIZE", "WRITE_SIZE")
+
+
+def _profile_config(prof, work, tag, counters, rec, steps=20, warmup=100,
+                    calibrate=False):
+    """One rocprofv3 --pmc pass over `bench.py --only config` for record
+    `rec`: {counter: mean per gemm dispatch}, gemm durations (ns) and, with
+    `calibrate`, the largest value each counter read for another kernel
+    (the 256 MiB calibration copy)."""
+    import csv
+    import subprocess
+    kind, m, n, k = rec["shape"]
+    out = os.path.join(work, tag)
+    cmd = ["timeout", "-s", "KILL", "90", prof, "--pmc", *counters,
+           "--kernel-trace", "-d", out, "-o", "p", "--output-format", "csv",
+           "--", sys.executable, os.path.join(ROOT, "bench.py"), "--only",
+           "config", "--config", rec["config"], "--shape", f"{m},{n},{k}",
+           "--splits", str(rec["splits"]), "--rotate", "--no-graph",
+           "--steps", str(steps), "--warmup", str(warmup),
+           "--no-cpu-baseline"] + (["--calibrate-copy"] if calibrate else [])
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                       cwd="/tmp", env={**os.environ, "TMPDIR": "/tmp"})
+    if r.returncode != 0:
+        return None, r.returncode
+    sums, other, durs = {}, {}, []
+    for path in _find(out, "p_counter_collection.csv"):
+        for row in csv.DictReader(open(path)):
+            v = float(row["Counter_Value"])
+            name = row["Counter_Name"]
+            if "gemm_lds_kernel" in row["Kernel_Name"]:
+                sums.setdefault(name, []).append(v)
+            else:
+                other[name] = max(other.get(name, 0.0), v)
+    for path in _find(out, "p_kernel_trace.csv"):
+        for row in csv.DictReader(open(path)):
+            if "gemm_lds_kernel" in row["Kernel_Name"]:
+                durs.append(int(row["End_Timestamp"]) -
+                            int(row["Start_Timestamp"]))
+    avg = {k2: sum(v) / len(v) for k2, v in sums.items()}
+    return (avg, sorted(durs), other), 0
+
+
+def tune_skinny_counters(pkg, dev, args):
+    """For each skinny shape: the sweep, then the planner's pick and the
+    three fastest other candidates under rocprofv3, in three passes (SQ
+    counters; FETCH_SIZE; WRITE_SIZE, each scaled by a 256 MiB copy
+    measured in the same run). One JSON line per candidate: sweep and profiled
+    durations, HBM bytes read and written per dispatch, the rate they
+    imply, the fraction of wave cycles spent waiting and the MFMA pipe's
+    busy fraction."""
+    import shutil
+    import tempfile
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        print(json.dumps({"error": "rocprofv3 not found"}))
+        return
+    work = tempfile.mkdtemp(prefix="skinny_counters_")
+    calib = 256 << 20
+    for kind, m, n, k in SKINNY_SHAPES:
+        recs = skinny_sweep(pkg, dev, args, kind, m, n, k)
+        recs.sort(key=lambda r: r["us"])
+        pick = [r for r in recs if r["planned"]][:1]
+        cands = pick + [r for r in recs if not r["planned"]][:3]
+        for i, rec in enumerate(cands):
+            tag = f"{kind}_{m}_{n}_{k}_{i}"
+            sq, rc = _profile_config(prof, work, tag + "_sq", TUNE_COUNTERS,
+                                     rec)
+            if sq is None:
+                print(json.dumps({**rec, "error": rc}), flush=True)
+                if rc in (124, 137, 134, 139):
+                    shutil.rmtree(work, ignore_errors=True)
+                    return
+                continue
+            avg, durs, _ = sq
+            waves = avg.get("SQ_WAVES", 0.0) or 1.0
+            busy = avg.get("SQ_BUSY_CYCLES", 0.0) or 1.0
+            us = durs[len(durs) // 2] / 1000 if durs else None
+            moved = {}
+            for cn in SKINNY_TRAFFIC:
+                tr, rc = _profile_config(prof, work, f"{tag}_{cn}", (cn,),
+                                         rec, calibrate=True)
+                if tr is None:
+                    print(json.dumps({**rec, "counter": cn, "error": rc}),
+                          flush=True)
+                    if rc in (124, 137, 134, 139):
+                        shutil.rmtree(work, ignore_errors=True)
+                        return
+                    moved[cn] = None
+                    continue
+                tavg, _, other = tr
+                ref = other.get(cn, 0.0)
+                moved[cn] = (tavg.get(cn, 0.0) * calib / ref if ref > 0
+                             else None)
+            tot = (moved["FETCH_SIZE"] or 0) + (moved["WRITE_SIZE"] or 0)
+            print(json.dumps({
+                **rec, "us_profiled": round(us, 2) if us else None,
+                "fetch_mb": round(moved["FETCH_SIZE"] / 1e6, 2)
+                if moved["FETCH_SIZE"] else None,
+                "write_mb": round(moved["WRITE_SIZE"] / 1e6, 2)
+                if moved["WRITE_SIZE"] else None,
+                "hbm_gbs": round(tot / (us * 1e3), 1) if us and tot else None,
+                "waves": round(waves),
+                "wait_frac": round(avg.get("SQ_WAIT_ANY", 0) /
+                                   (avg.get("SQ_WAVE_CYCLES", 0) or 1), 3),
+                "mfma_busy_frac": round(avg.get("SQ_VALU_MFMA_BUSY_CYCLES", 0)
+                                        / (busy * 32), 3)}), flush=True)
+    shutil.rmtree(work, ignore_errors=True)
 
 
 def tune(pkg, inputs, dev, args):
     import torch
+    if args.tune_skinny and args.tune_counters:
+        return tune_skinny_counters(pkg, dev, args)
     if args.tune_skinny:
         return tune_skinny(pkg, dev, args)
     if args.tune_counters:
