@@ -558,6 +558,7 @@ int iree_mi355x_attention_f16_strided(
     layout.k[i] = strides->k[i];
     layout.v[i] = strides->v[i];
     layout.o[i] = strides->o[i];
+    layout.m[i] = 0;
   }
   layout.heads = (int)heads;
   layout.group = (int)(heads / kv_heads);
@@ -619,13 +620,19 @@ int iree_mi355x_attention(const iree_mi355x_attention_t *a, void *stream) {
                 "%s: operands must be aligned to their element size", who);
   const bool causal = a->flags & IREE_MI355X_ATTENTION_CAUSAL;
 
-  // The MFMA kernel: equal head dims of 64 or 128, no mask, f16 output,
-  // 16-byte rows and strides, each head's rows within 4 GiB (32-bit copy
-  // offsets), and a grid of pairs of 128-row query blocks.
+  // The MFMA kernel: equal head dims of 64 or 128, f16 output, 16-byte rows
+  // and strides, each head's rows within 4 GiB (32-bit copy offsets), and a
+  // grid of pairs of 128-row query blocks; a mask with contiguous keys read
+  // 4 keys (8 bytes) at a time: strides and base 8-byte aligned, seq_kv a
+  // multiple of 4.
   bool fast = a->head_dim == a->head_dim_v &&
-              (a->head_dim == 64 || a->head_dim == 128) && !a->mask &&
-              !out_f32 && aligned(a->q, 16) && aligned(a->o, 16) &&
+              (a->head_dim == 64 || a->head_dim == 128) && !out_f32 &&
+              aligned(a->q, 16) && aligned(a->o, 16) &&
               (!a->k || aligned(a->k, 16)) && (!a->v || aligned(a->v, 16));
+  if (fast && a->mask)
+    fast = a->mask_strides[3] == 1 && a->mask_strides[0] % 4 == 0 &&
+           a->mask_strides[1] % 4 == 0 && a->mask_strides[2] % 4 == 0 &&
+           aligned(a->mask, 8) && a->seq_kv % 4 == 0;
   for (int t = 0; t < 4 && fast; ++t)
     for (int i = 0; i < 3; ++i)
       if (all[t][i] % 8 != 0)
@@ -646,13 +653,32 @@ int iree_mi355x_attention(const iree_mi355x_attention_t *a, void *stream) {
                head_span(st.v, a->seq_kv) > (int64_t)UINT32_MAX ||
                a->batch * a->heads * ((a->seq_q + 127) / 128) >= kMaxExtent))
     fast = false;
-  if (fast)
+  if (fast && !a->mask)
     return iree_mi355x_attention_f16_strided(
         a->q, a->k, a->v, a->o, a->batch, a->heads, a->kv_heads, a->seq_q,
         a->seq_kv, a->head_dim, a->scale, a->flags & IREE_MI355X_ATTENTION_CAUSAL,
         &a->strides, stream);
   if (dry_run(0))
     return ok();
+  if (fast) {
+    AttentionLayout layout;
+    for (int i = 0; i < 3; ++i) {
+      layout.q[i] = st.q[i];
+      layout.k[i] = st.k[i];
+      layout.v[i] = st.v[i];
+      layout.o[i] = st.o[i];
+      layout.m[i] = a->mask_strides[i];
+    }
+    layout.heads = (int)a->heads;
+    layout.group = (int)(a->heads / a->kv_heads);
+    layout.seq_q = (int)a->seq_q;
+    layout.seq_kv = (int)a->seq_kv;
+    return launch_status(
+        launch_attention(a->q, a->k, a->v, a->o, a->batch, layout,
+                         a->head_dim, a->scale, causal ? 1 : 0, stream,
+                         a->mask),
+        "attention_fwd_mask");
+  }
   AttentionGeneralLayout g;
   for (int i = 0; i < 3; ++i) {
     g.q[i] = st.q[i];

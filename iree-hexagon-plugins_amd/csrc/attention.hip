@@ -119,11 +119,15 @@ __device__ __forceinline__ int v_swizzle(int key) {
 // query head (the layout's strides are then not read): rows are one
 // compile-time row size apart and a plane's base is its index times its
 // size, so the copies add no scalar arithmetic.
-template <int D, bool CONTIG>
+// MASK: an additive f16 mask M (strided instances only), read through the
+// layout's (batch, head, row) strides with keys contiguous, scaled by log2(e)
+// and added to the log2-domain scores of every block.
+template <int D, bool CONTIG, bool MASK = false>
 __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
     const f16 *__restrict__ Q, const f16 *__restrict__ K,
-    const f16 *__restrict__ V, f16 *__restrict__ O, AttentionLayout L,
-    float scale_log2, int causal) {
+    const f16 *__restrict__ V, f16 *__restrict__ O, const f16 *__restrict__ M,
+    AttentionLayout L, float scale_log2, int causal) {
+  static_assert(!(CONTIG && MASK), "masks take the strided instance");
   const int heads = L.heads, seq_q = L.seq_q, seq_kv = L.seq_kv;
   constexpr int DS = D / 16;       // 16-wide d steps of S^T = K Q^T
   constexpr int DT = D / 32;       // 32-row d tiles of O^T
@@ -168,6 +172,7 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
   // Q, K, V and O start at these bases, one row pitch (bytes) apart.
   const char *Qp, *Kp, *Vp;
   f16 *Op;
+  const f16 *Mp = nullptr;
   uint32_t q_pitch, k_pitch, v_pitch;
   int64_t o_row;
   if constexpr (CONTIG) {
@@ -183,6 +188,8 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
     Kp = (const char *)(K + pb * L.k[0] + pk * L.k[1]);
     Vp = (const char *)(V + pb * L.v[0] + pk * L.v[1]);
     Op = O + pb * L.o[0] + ph * L.o[1];
+    if constexpr (MASK)
+      Mp = M + pb * L.m[0] + ph * L.m[1];
     q_pitch = (uint32_t)(2 * L.q[2]);
     k_pitch = (uint32_t)(2 * L.k[2]);
     v_pitch = (uint32_t)(2 * L.v[2]);
@@ -465,12 +472,34 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
     l_run += (psum[0] + psum[1]) + (psum[2] + psum[3]);
   };
 
+  // The mask values of block k this lane's scores need (MASK): element
+  // (t, r) of S^T is key kv0 + 4 g + 32 t + 8 (r / 4) + r % 4 of row
+  // q0 + l32, so register quarter (t, r / 4) is one 8-byte load of 4
+  // consecutive keys. Groups past seq_kv (a multiple of 4) load key 0
+  // instead (those scores are masked anyway); rows past seq_q the last row.
+  // Issued by the M phase that computes S^T(k); the V phase after it waits
+  // for them before its copies.
+  i32x2 mk[2][4];
+  auto load_mask = [&](int k) {
+    const int kv0 = (2 * k + grp) * kBKV;
+    const f16 *mrow = Mp + (int64_t)min(q0 + l32, seq_q - 1) * L.m[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int key = kv0 + 4 * g + 32 * t + 8 * rq;
+        mk[t][rq] = *(const i32x2 *)(mrow + (key + 3 < seq_kv ? key : 0));
+      }
+  };
+
   // M phase: PV of block k - 1 (when DO_PV), then S^T of block k (when
   // DO_S); MFMA and LDS reads only, at raised wave priority so its MFMAs
   // issue ahead of the other group's VALU work on the same SIMD.
   float alpha = 1.0f;     // output rescale pending from the V phase
   bool rescale = false;   // wave-uniform
   auto m_phase = [&](int k, auto do_pv, auto do_s) {
+    if constexpr (MASK && decltype(do_s)::value)
+      load_mask(k);
     __builtin_amdgcn_s_setprio(1);
     if constexpr (decltype(do_pv)::value) {
       if (rescale) {
@@ -509,7 +538,13 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int c = 32 * t + 8 * (r >> 2) + (r & 3);
-          st[t][r] = c >= thr ? -INFINITY : st[t][r] * scale_log2;
+          float v = st[t][r] * scale_log2;
+          if constexpr (MASK) {
+            const i32x2 w = mk[t][r >> 2];
+            const f16x4 h = __builtin_bit_cast(f16x4, w);
+            v = __builtin_fmaf((float)h[r & 3], 1.4426950408889634f, v);
+          }
+          st[t][r] = c >= thr ? -INFINITY : v;
         }
       mx = row_max(st);
       sc = 1.0f;
@@ -559,12 +594,22 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
   // reads (the ones issued here may stay in flight).
   auto v_phase = [&](int k) {
     const bool next_k = k + 2 < n_mine, next_v = k + 1 < n_mine;
+    if constexpr (MASK) {
+      // Block k's mask values, and the copies issued before them, have
+      // landed before this phase's copies go out.
+      wait_vmcnt<0>();
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq)
+          tie2(mk[t][rq]);
+    }
     if (next_k)
       copy_k(k + 2);
     if (next_v)
       copy_v(k + 1);
     const int kv0 = (2 * k + grp) * kBKV;
-    if ((causal && kv0 + kBKV - 1 > q0) || kv0 + kBKV > seq_kv ||
+    if (MASK || (causal && kv0 + kBKV - 1 > q0) || kv0 + kBKV > seq_kv ||
         scale_log2 <= 0.0f)
       softmax(k, std::true_type());
     else
@@ -743,7 +788,8 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
 hipError_t launch_attention(const void *q, const void *k, const void *v,
                             void *o, int64_t batch,
                             const AttentionLayout &layout, int64_t head_dim,
-                            float scale, int causal, void *stream) {
+                            float scale, int causal, void *stream,
+                            const void *mask) {
   const int64_t q_blocks = (layout.seq_q + kBQ - 1) / kBQ;
   const int64_t planes = batch * layout.heads;
   // One workgroup per pair of query blocks (q_blocks - 1 - k, k).
@@ -752,7 +798,7 @@ hipError_t launch_attention(const void *q, const void *k, const void *v,
   const int64_t d = head_dim, sq = layout.seq_q, skv = layout.seq_kv,
                 h = layout.heads;
   const bool contig =
-      layout.group == 1 && layout.q[2] == d && layout.o[2] == d &&
+      !mask && layout.group == 1 && layout.q[2] == d && layout.o[2] == d &&
       layout.k[2] == d && layout.v[2] == d && layout.q[1] == sq * d &&
       layout.o[1] == sq * d && layout.k[1] == skv * d &&
       layout.v[1] == skv * d && layout.q[0] == h * sq * d &&
@@ -760,17 +806,20 @@ hipError_t launch_attention(const void *q, const void *k, const void *v,
       layout.v[0] == h * skv * d;
   const void *kernel;
   if (head_dim == 128)
-    kernel = contig ? (const void *)&attention_fwd_kernel<128, true>
-                    : (const void *)&attention_fwd_kernel<128, false>;
+    kernel = mask     ? (const void *)&attention_fwd_kernel<128, false, true>
+             : contig ? (const void *)&attention_fwd_kernel<128, true>
+                      : (const void *)&attention_fwd_kernel<128, false>;
   else if (head_dim == 64)
-    kernel = contig ? (const void *)&attention_fwd_kernel<64, true>
-                    : (const void *)&attention_fwd_kernel<64, false>;
+    kernel = mask     ? (const void *)&attention_fwd_kernel<64, false, true>
+             : contig ? (const void *)&attention_fwd_kernel<64, true>
+                      : (const void *)&attention_fwd_kernel<64, false>;
   else
     return hipErrorInvalidValue;
   const f16 *qp = (const f16 *)q, *kp = (const f16 *)k, *vp = (const f16 *)v;
+  const f16 *mp = (const f16 *)mask;
   f16 *op = (f16 *)o;
   AttentionLayout l = layout;
-  void *args[] = {&qp, &kp, &vp, &op, &l, (void *)&scale_log2, &causal};
+  void *args[] = {&qp, &kp, &vp, &op, &mp, &l, (void *)&scale_log2, &causal};
   return hipLaunchKernel(kernel, grid, dim3(kThreads), args, 0,
                          (hipStream_t)stream);
 }
@@ -785,6 +834,8 @@ const KernelEntry *attention_kernels(int *count) {
       {"attention_fwd_d64", (const void *)&attention_fwd_kernel<64, true>, kThreads, kExportAttention},
       {"attention_fwd_d128_strided", (const void *)&attention_fwd_kernel<128, false>, kThreads, kExportAttention},
       {"attention_fwd_d64_strided", (const void *)&attention_fwd_kernel<64, false>, kThreads, kExportAttention},
+      {"attention_fwd_d128_mask", (const void *)&attention_fwd_kernel<128, false, true>, kThreads, kExportAttention},
+      {"attention_fwd_d64_mask", (const void *)&attention_fwd_kernel<64, false, true>, kThreads, kExportAttention},
   };
   *count = (int)(sizeof(all) / sizeof(all[0]));
   return all;

@@ -184,12 +184,17 @@ hipError_t launch_gemv(const MatmulArgs &a, int w_bytes, const void *scale,
 struct AttentionLayout {
   int64_t q[3], k[3], v[3], o[3];  // batch, head, row
   int heads, group, seq_q, seq_kv;
+  // An additive f16 mask (launches given one): (batch, head, row) element
+  // strides, keys contiguous. Checked on the host: strides multiples of 4,
+  // the base 8-byte aligned, seq_kv a multiple of 4.
+  int64_t m[3];
 };
 
 hipError_t launch_attention(const void *q, const void *k, const void *v,
                             void *o, int64_t batch,
                             const AttentionLayout &layout, int64_t head_dim,
-                            float scale, int causal, void *stream);
+                            float scale, int causal, void *stream,
+                            const void *mask = nullptr);
 
 // The general attention kernel's view (attention_general.hip): strides as
 // AttentionLayout plus the mask's (batch, head, row, key) element strides

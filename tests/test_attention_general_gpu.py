@@ -124,8 +124,11 @@ def test_attention_general_strided_views(pkg, oracle, dev):
 
 def test_attention_general_routing(pkg, oracle, dev):
     # equal head dims of 64 / 128, no mask, f16 out: the MFMA kernel, the
-    # same bits through the descriptor as through attention_f16; a zero mask
-    # takes the general kernel, within the fp16 bound of it
+    # same bits through the descriptor as through attention_f16. A zero mask
+    # with contiguous keys takes the MFMA kernel's mask instance; the same
+    # zeros read with a key stride of 2 take the general kernel: both within
+    # the fp16 bound of the unmasked result, and not the same bits (two
+    # kernels ran)
     g = torch.Generator().manual_seed(12)
     q, k, v = (rand(g, 2, 4, 256, 128).to(dev) for _ in range(3))
     fast = pkg.attention(q, k, v, causal=True)
@@ -143,10 +146,13 @@ def test_attention_general_routing(pkg, oracle, dev):
     torch.cuda.synchronize()
     assert torch.equal(o, fast)
     zero = torch.zeros(1, 256, dtype=torch.float16, device=dev)
-    general = pkg.attention(q, k, v, causal=True, mask=zero)
-    assert oracle.fp16_parity(general.cpu().numpy(),
-                              fast.cpu().numpy()) <= F16_BOUND
-    assert not torch.equal(general, fast)  # another kernel ran
+    masked = pkg.attention(q, k, v, causal=True, mask=zero)
+    zero2 = torch.zeros(1, 512, dtype=torch.float16, device=dev)[:, ::2]
+    general = pkg.attention(q, k, v, causal=True, mask=zero2)
+    for got in (masked, general):
+        assert oracle.fp16_parity(got.cpu().numpy(),
+                                  fast.cpu().numpy()) <= F16_BOUND
+    assert not torch.equal(general, masked)
 
 
 def test_attention_general_through_export_table(pkg, oracle, dev):
@@ -187,3 +193,61 @@ def test_attention_general_wrapper_checks(pkg, dev):
         big = torch.zeros(1, 1, 4, 300, dtype=torch.float16, device=dev)
         pkg.attention(big, big, big)
     assert e.value.status == pkg.UNSUPPORTED
+
+
+MFMA_MASK_CASES = [
+    # b, hq, hkv, sq, skv, d, mask shape, causal
+    (1, 4, 4, 256, 256, 128, (256, 256), True),
+    (2, 4, 2, 200, 300, 128, (2, 1, 200, 300), False),
+    (1, 2, 2, 130, 516, 64, (1, 2, 130, 516), True),
+    (2, 3, 3, 64, 64, 64, (64,), False),
+    (1, 8, 2, 1, 1024, 128, (1, 8, 1, 1024), False),
+    (1, 2, 2, 333, 128, 128, (333, 128), True),
+]
+
+
+@pytest.mark.parametrize("case", MFMA_MASK_CASES, ids=[
+    "b{}h{}/{}q{}k{}d{}_m{}_c{}".format(*c[:6], "x".join(map(str, c[6])),
+                                        int(c[7])) for c in MFMA_MASK_CASES])
+def test_attention_mask_mfma_path(pkg, oracle, dev, case):
+    # head dims 64 / 128 with an additive mask whose keys are contiguous run
+    # the MFMA kernel's mask instance: ragged lengths (tails of query rows and
+    # key blocks), grouped heads, masks broadcast over batch, heads or rows,
+    # -inf entries, with and without the causal mask
+    b, hq, hkv, sq, skv, d, mshape, causal = case
+    print(f"attention mask mfma {case}", flush=True)
+    g = torch.Generator().manual_seed(sq + skv + d + hq)
+    q, k, v = rand(g, b, hq, sq, d), rand(g, b, hkv, skv, d), rand(g, b, hkv, skv, d)
+    mask = random_mask(g, mshape, 0.15)
+    o = pkg.attention(q.to(dev), k.to(dev), v.to(dev), causal=causal,
+                      mask=mask.to(dev), scale=0.11)
+    torch.cuda.synchronize()
+    ref = oracle.attention(q.numpy(), k.numpy(), v.numpy(), scale=0.11,
+                           causal=causal, mask=mask.numpy())
+    got = o.cpu().numpy()
+    assert np.isfinite(got).all()
+    err = oracle.fp16_parity(got, ref)
+    assert err <= F16_BOUND, err
+
+
+def test_attention_mask_mfma_rows_and_views(pkg, oracle, dev):
+    # fully masked rows write 0; a mask that is a view of a wider buffer
+    # (row stride past seq_kv) over a KV-cache slice, o in [B, S, H, D]
+    g = torch.Generator().manual_seed(31)
+    b, h, sq, ctx, cache, d = 2, 4, 160, 192, 256, 128
+    q = rand(g, b, h, sq, d).to(dev)
+    kc, vc = rand(g, b, h, cache, d).to(dev), rand(g, b, h, cache, d).to(dev)
+    wide = random_mask(g, (b, 1, sq, cache), 0.1)
+    wide[:, :, [0, 77, 159]] = float("-inf")
+    wide = wide.to(dev)
+    mask = wide[..., :ctx]
+    out = torch.full((b, sq, h, d), float("nan"), dtype=torch.float16,
+                     device=dev)
+    pkg.attention(q, kc[:, :, :ctx], vc[:, :, :ctx], out.permute(0, 2, 1, 3),
+                  causal=False, mask=mask)
+    got = out.permute(0, 2, 1, 3).cpu().numpy()
+    assert (got[:, :, [0, 77, 159]] == 0).all()
+    ref = oracle.attention(q.cpu().numpy(), kc[:, :, :ctx].cpu().numpy(),
+                           vc[:, :, :ctx].cpu().numpy(), scale=d ** -0.5,
+                           mask=mask.cpu().numpy())
+    assert oracle.fp16_parity(got, ref) <= F16_BOUND
