@@ -122,15 +122,23 @@ __device__ __forceinline__ int v_swizzle(int key) {
 // MASK: an additive f16 mask M (strided instances only), read through the
 // layout's (batch, head, row) strides with keys contiguous, scaled by log2(e)
 // and added to the log2-domain scores of every block.
-template <int D, bool CONTIG, bool MASK = false>
+// DV: the head dim when it is a multiple of 16 below D (the LDS layout's):
+// copies skip the chunks past it (those LDS bytes are never read as K or Q:
+// S^T takes DV / 16 d steps), PV runs over all D / 32 tiles of O^T and the
+// rows past DV it produces from the unwritten V chunks are not stored.
+template <int D, bool CONTIG, bool MASK = false, int DV = D>
 __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
     const f16 *__restrict__ Q, const f16 *__restrict__ K,
     const f16 *__restrict__ V, f16 *__restrict__ O, const f16 *__restrict__ M,
     AttentionLayout L, float scale_log2, int causal) {
   static_assert(!(CONTIG && MASK), "masks take the strided instance");
+  static_assert(DV % 16 == 0 && DV > 0 && DV <= D && (DV == D || !CONTIG),
+                "head dim");
   const int heads = L.heads, seq_q = L.seq_q, seq_kv = L.seq_kv;
   constexpr int DS = D / 16;       // 16-wide d steps of S^T = K Q^T
   constexpr int DT = D / 32;       // 32-row d tiles of O^T
+  constexpr int DSV = DV / 16;     // d steps of S^T over the head dim
+  constexpr int CHV = DV / 8;      // 16-byte chunks of a row within it
   constexpr int ROW = D * 2;       // bytes per staged K / V row
   constexpr int CH = ROW / 16;     // 16-byte chunks per row
   constexpr int BLK = kBKV * ROW;  // bytes of one staged K (or V) block
@@ -243,7 +251,8 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
                                            : k_swizzle<D>(row);
       // Uniform head base + 32-bit lane offset: one VGPR per address.
       const uint32_t off = (uint32_t)key * pitch + 16u * (lane_chunk ^ sw);
-      global_to_lds_16(src + off, dst + (p * 4 + wq) * ROWS_PER_INSN * ROW);
+      if (DV == D || (lane_chunk ^ sw) < CHV)
+        global_to_lds_16(src + off, dst + (p * 4 + wq) * ROWS_PER_INSN * ROW);
     }
   };
   // Full key blocks take the saddr copy form: the lane's byte offset inside
@@ -258,8 +267,14 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
       (uint32_t)f_row * k_pitch + 16u * (c_phys ^ k_swizzle<D>(f_row));
   const uint32_t v_voff =
       (uint32_t)f_row * v_pitch + 16u * (c_phys ^ v_swizzle<D>(f_row));
+  // The lane's logical chunk is the same in every pass: whether it lies
+  // within the head dim.
+  const bool k_in = DV == D || (c_phys ^ k_swizzle<D>(f_row)) < CHV;
+  const bool v_in = DV == D || (c_phys ^ v_swizzle<D>(f_row)) < CHV;
   auto copy_full = [&](const char *src, uint32_t pitch, int kb,
-                       IHP_LDS char *dst, uint32_t voff) {
+                       IHP_LDS char *dst, uint32_t voff, bool in) {
+    if (DV < D && !in)
+      return;
     const char *base = src + (int64_t)kb * kBKV * pitch;
 #pragma unroll
     for (int p = 0; p < PASSES; ++p)
@@ -269,7 +284,7 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
   auto copy_k = [&](int i) {
     const int kb = 2 * i + grp;
     if ((kb + 1) * kBKV <= seq_kv)
-      copy_full(Kp, k_pitch, kb, lds + (i & 1) * BLK, k_voff);
+      copy_full(Kp, k_pitch, kb, lds + (i & 1) * BLK, k_voff, k_in);
     else
       copy_block(Kp, k_pitch, kb, lds + (i & 1) * BLK, std::false_type());
   };
@@ -285,15 +300,16 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
       const int r0 = (p * 8 + wave) * ROWS_PER_INSN;
       const int r = r0 + lane_row;
       const int row = min(qrow0 + r, seq_q - 1);
-      const uint32_t off =
-          (uint32_t)row * q_pitch + 16u * (lane_chunk ^ k_swizzle<D>(r));
-      global_to_lds_16(Qp + off, staged_row(r0, 3));
+      const int chunk = lane_chunk ^ k_swizzle<D>(r);
+      const uint32_t off = (uint32_t)row * q_pitch + 16u * chunk;
+      if (DV == D || chunk < CHV)
+        global_to_lds_16(Qp + off, staged_row(r0, 3));
     }
   };
   auto copy_v = [&](int i) {
     const int kb = 2 * i + grp;
     if ((kb + 1) * kBKV <= seq_kv)
-      copy_full(Vp, v_pitch, kb, lds + (2 + (i & 1)) * BLK, v_voff);
+      copy_full(Vp, v_pitch, kb, lds + (2 + (i & 1)) * BLK, v_voff, v_in);
     else
       copy_block(Vp, v_pitch, kb, lds + (2 + (i & 1)) * BLK, std::true_type());
   };
@@ -344,7 +360,7 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
   // LDS latency of one issued just before it.
   auto scores = [&](int i, f32x16 (&st)[2]) {
     const uint32_t kbase = ka + (uint32_t)((i & 1) * BLK);
-    constexpr int NR = 2 * DS, KW = kKReadAhead, NB = KW + 1;
+    constexpr int NR = 2 * DSV, KW = kKReadAhead, NB = KW + 1;
     i32x4 kb[NB];
     auto issue = [&](auto r_c) {
       constexpr int R = decltype(r_c)::value;
@@ -409,7 +425,7 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
       const int r = (p * 8 + wave) * ROWS_PER_INSN + c_row;
       const i32x4 v = *(const IHP_LDS i32x4 *)(
           staged_row(r, 1) + 16 * (c_phys ^ k_swizzle<D>(r)));
-      if (qrow0 + r < seq_q)
+      if (qrow0 + r < seq_q && (DV == D || c_phys < CHV))
         *(i32x4 *)(Op + (int64_t)(qrow0 + r) * o_row + 8 * c_phys) = v;
     }
   };
@@ -648,7 +664,7 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
       const int k_sw = k_swizzle<D>(kl);
       const int qaddr = kl * ROW + 16 * (kg ^ (k_sw & 1)) + 32 * (k_sw >> 1);
 #pragma unroll
-      for (int s = 0; s < DS; ++s)
+      for (int s = 0; s < DSV; ++s)
         qf[s] = *(const IHP_LDS i32x4 *)(qs + (qaddr ^ (32 * s)));
       wait_lgkmcnt0();
     }
@@ -805,16 +821,31 @@ hipError_t launch_attention(const void *q, const void *k, const void *v,
       layout.o[0] == h * sq * d && layout.k[0] == h * skv * d &&
       layout.v[0] == h * skv * d;
   const void *kernel;
-  if (head_dim == 128)
-    kernel = mask     ? (const void *)&attention_fwd_kernel<128, false, true>
-             : contig ? (const void *)&attention_fwd_kernel<128, true>
-                      : (const void *)&attention_fwd_kernel<128, false>;
-  else if (head_dim == 64)
-    kernel = mask     ? (const void *)&attention_fwd_kernel<64, false, true>
-             : contig ? (const void *)&attention_fwd_kernel<64, true>
-                      : (const void *)&attention_fwd_kernel<64, false>;
-  else
-    return hipErrorInvalidValue;
+#define IHP_ATT_PICK(DVV, DD)                                                  \
+  kernel = mask ? (const void *)&attention_fwd_kernel<DD, false, true, DVV>    \
+                : (const void *)&attention_fwd_kernel<DD, false, false, DVV>; \
+  break;
+  switch (head_dim) {
+    case 128:
+      kernel = mask     ? (const void *)&attention_fwd_kernel<128, false, true>
+               : contig ? (const void *)&attention_fwd_kernel<128, true>
+                        : (const void *)&attention_fwd_kernel<128, false>;
+      break;
+    case 64:
+      kernel = mask     ? (const void *)&attention_fwd_kernel<64, false, true>
+               : contig ? (const void *)&attention_fwd_kernel<64, true>
+                        : (const void *)&attention_fwd_kernel<64, false>;
+      break;
+    case 16: IHP_ATT_PICK(16, 64)
+    case 32: IHP_ATT_PICK(32, 64)
+    case 48: IHP_ATT_PICK(48, 64)
+    case 80: IHP_ATT_PICK(80, 128)
+    case 96: IHP_ATT_PICK(96, 128)
+    case 112: IHP_ATT_PICK(112, 128)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef IHP_ATT_PICK
   const f16 *qp = (const f16 *)q, *kp = (const f16 *)k, *vp = (const f16 *)v;
   const f16 *mp = (const f16 *)mask;
   f16 *op = (f16 *)o;
@@ -836,6 +867,18 @@ const KernelEntry *attention_kernels(int *count) {
       {"attention_fwd_d64_strided", (const void *)&attention_fwd_kernel<64, false>, kThreads, kExportAttention},
       {"attention_fwd_d128_mask", (const void *)&attention_fwd_kernel<128, false, true>, kThreads, kExportAttention},
       {"attention_fwd_d64_mask", (const void *)&attention_fwd_kernel<64, false, true>, kThreads, kExportAttention},
+      {"attention_fwd_d16", (const void *)&attention_fwd_kernel<64, false, false, 16>, kThreads, kExportAttention},
+      {"attention_fwd_d32", (const void *)&attention_fwd_kernel<64, false, false, 32>, kThreads, kExportAttention},
+      {"attention_fwd_d48", (const void *)&attention_fwd_kernel<64, false, false, 48>, kThreads, kExportAttention},
+      {"attention_fwd_d80", (const void *)&attention_fwd_kernel<128, false, false, 80>, kThreads, kExportAttention},
+      {"attention_fwd_d96", (const void *)&attention_fwd_kernel<128, false, false, 96>, kThreads, kExportAttention},
+      {"attention_fwd_d112", (const void *)&attention_fwd_kernel<128, false, false, 112>, kThreads, kExportAttention},
+      {"attention_fwd_d16_mask", (const void *)&attention_fwd_kernel<64, false, true, 16>, kThreads, kExportAttention},
+      {"attention_fwd_d32_mask", (const void *)&attention_fwd_kernel<64, false, true, 32>, kThreads, kExportAttention},
+      {"attention_fwd_d48_mask", (const void *)&attention_fwd_kernel<64, false, true, 48>, kThreads, kExportAttention},
+      {"attention_fwd_d80_mask", (const void *)&attention_fwd_kernel<128, false, true, 80>, kThreads, kExportAttention},
+      {"attention_fwd_d96_mask", (const void *)&attention_fwd_kernel<128, false, true, 96>, kThreads, kExportAttention},
+      {"attention_fwd_d112_mask", (const void *)&attention_fwd_kernel<128, false, true, 112>, kThreads, kExportAttention},
   };
   *count = (int)(sizeof(all) / sizeof(all[0]));
   return all;

@@ -251,3 +251,45 @@ def test_attention_mask_mfma_rows_and_views(pkg, oracle, dev):
                            vc[:, :, :ctx].cpu().numpy(), scale=d ** -0.5,
                            mask=mask.cpu().numpy())
     assert oracle.fp16_parity(got, ref) <= F16_BOUND
+
+
+HEAD_DIM_CASES = [
+    # b, hq, hkv, sq, skv, d, mask shape (None: none), causal
+    (1, 4, 4, 256, 256, 96, None, True),
+    (2, 4, 2, 200, 300, 80, (300,), False),
+    (1, 2, 2, 130, 516, 32, (1, 2, 130, 516), True),
+    (2, 3, 3, 64, 64, 16, None, False),
+    (1, 8, 2, 1, 1024, 112, None, False),
+    (1, 2, 2, 333, 128, 48, (333, 128), True),
+    (1, 6, 3, 512, 512, 96, (512, 512), True),
+]
+
+
+@pytest.mark.parametrize("case", HEAD_DIM_CASES, ids=[
+    "b{}h{}/{}q{}k{}d{}_m{}_c{}".format(
+        *c[:6], "x".join(map(str, c[6])) if c[6] else "none", int(c[7]))
+    for c in HEAD_DIM_CASES])
+def test_attention_head_dims_mfma_path(pkg, oracle, dev, case):
+    # head dims that are multiples of 16 up to 128 run the MFMA kernel with
+    # the 64- or 128-wide LDS layout, reading only their own chunks: with
+    # and without masks, grouped heads, ragged lengths, causal or not; the
+    # columns past the head dim of the output's buffer stay untouched
+    b, hq, hkv, sq, skv, d, mshape, causal = case
+    print(f"attention head dim {case}", flush=True)
+    g = torch.Generator().manual_seed(sq * 3 + skv + d)
+    q, k, v = rand(g, b, hq, sq, d), rand(g, b, hkv, skv, d), rand(g, b, hkv, skv, d)
+    mask = random_mask(g, mshape, 0.1) if mshape else None
+    # o inside a wider buffer: a canary past the head dim of every row
+    wide = torch.full((b, hq, sq, d + 16), 7.0, dtype=torch.float16,
+                      device=dev)
+    o = wide[..., :d]
+    pkg.attention(q.to(dev), k.to(dev), v.to(dev), o, causal=causal,
+                  mask=None if mask is None else mask.to(dev))
+    torch.cuda.synchronize()
+    ref = oracle.attention(q.numpy(), k.numpy(), v.numpy(), scale=d ** -0.5,
+                           causal=causal,
+                           mask=None if mask is None else mask.numpy())
+    got = o.cpu().numpy()
+    assert np.isfinite(got).all()
+    assert oracle.fp16_parity(got, ref) <= F16_BOUND
+    assert (wide[..., d:].cpu() == 7.0).all()
