@@ -222,8 +222,8 @@ int iree_mi355x_attention_f16_strided(
 // decomposed softmax does (examples/attention_layer/attention_layer.mlir:
 // 80-102). head_dim and head_dim_v are 1..256, heads a multiple of
 // kv_heads, heads and batch at most 65535. Shapes the MFMA kernel takes
-// (equal head dims that are multiples of 16 up to 128, f16 output, the
-// alignment of iree_mi355x_attention_f16_strided, and a mask if any with
+// (equal head dims that are multiples of 16 up to 128, f16 or f32 output,
+// the alignment of iree_mi355x_attention_f16_strided, and a mask if any with
 // contiguous keys, its other strides and base 8-byte aligned and seq_kv a
 // multiple of 4) run there; the rest run a general kernel (32-key blocks in
 // LDS, f32 online softmax). _f16 and _f16_strided take head dims 64 and

@@ -621,12 +621,12 @@ int iree_mi355x_attention(const iree_mi355x_attention_t *a, void *stream) {
   const bool causal = a->flags & IREE_MI355X_ATTENTION_CAUSAL;
 
   // The MFMA kernel: equal head dims that are multiples of 16 up to 128,
-  // f16 output, 16-byte rows and strides, each head's rows within 4 GiB
-  // (32-bit copy offsets), and a grid of pairs of 128-row query blocks; a
-  // mask with contiguous keys read 4 keys (8 bytes) at a time: strides and
-  // base 8-byte aligned, seq_kv a multiple of 4.
+  // 16-byte rows and strides, each head's rows within 4 GiB (32-bit copy
+  // offsets), and a grid of pairs of 128-row query blocks; a mask with
+  // contiguous keys read 4 keys (8 bytes) at a time: strides and base
+  // 8-byte aligned, seq_kv a multiple of 4.
   bool fast = a->head_dim == a->head_dim_v && a->head_dim % 16 == 0 &&
-              a->head_dim <= 128 && !out_f32 &&
+              a->head_dim <= 128 &&
               aligned(a->q, 16) && aligned(a->o, 16) &&
               (!a->k || aligned(a->k, 16)) && (!a->v || aligned(a->v, 16));
   if (fast && a->mask)
@@ -653,7 +653,8 @@ int iree_mi355x_attention(const iree_mi355x_attention_t *a, void *stream) {
                head_span(st.v, a->seq_kv) > (int64_t)UINT32_MAX ||
                a->batch * a->heads * ((a->seq_q + 127) / 128) >= kMaxExtent))
     fast = false;
-  if (fast && !a->mask && (a->head_dim == 64 || a->head_dim == 128))
+  if (fast && !a->mask && !out_f32 &&
+      (a->head_dim == 64 || a->head_dim == 128))
     return iree_mi355x_attention_f16_strided(
         a->q, a->k, a->v, a->o, a->batch, a->heads, a->kv_heads, a->seq_q,
         a->seq_kv, a->head_dim, a->scale, a->flags & IREE_MI355X_ATTENTION_CAUSAL,
@@ -676,7 +677,7 @@ int iree_mi355x_attention(const iree_mi355x_attention_t *a, void *stream) {
     return launch_status(
         launch_attention(a->q, a->k, a->v, a->o, a->batch, layout,
                          a->head_dim, a->scale, causal ? 1 : 0, stream,
-                         a->mask),
+                         a->mask, out_f32 ? 1 : 0),
         a->mask ? "attention_fwd_mask" : "attention_fwd");
   }
   AttentionGeneralLayout g;

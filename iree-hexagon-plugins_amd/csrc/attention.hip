@@ -126,12 +126,16 @@ __device__ __forceinline__ int v_swizzle(int key) {
 // copies skip the chunks past it (those LDS bytes are never read as K or Q:
 // S^T takes DV / 16 d steps), PV runs over all D / 32 tiles of O^T and the
 // rows past DV it produces from the unwritten V chunks are not stored.
-template <int D, bool CONTIG, bool MASK = false, int DV = D>
+// OF32: O is f32 (strided instances only), stored from the merged
+// registers, 16 bytes (4 d of one row) per lane and register quarter.
+template <int D, bool CONTIG, bool MASK = false, int DV = D, bool OF32 = false>
 __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
     const f16 *__restrict__ Q, const f16 *__restrict__ K,
-    const f16 *__restrict__ V, f16 *__restrict__ O, const f16 *__restrict__ M,
+    const f16 *__restrict__ V, void *__restrict__ O, const f16 *__restrict__ M,
     AttentionLayout L, float scale_log2, int causal) {
-  static_assert(!(CONTIG && MASK), "masks take the strided instance");
+  typedef typename std::conditional<OF32, float, f16>::type OutT;
+  static_assert(!(CONTIG && (MASK || OF32)),
+                "masks and f32 outputs take the strided instance");
   static_assert(DV % 16 == 0 && DV > 0 && DV <= D && (DV == D || !CONTIG),
                 "head dim");
   const int heads = L.heads, seq_q = L.seq_q, seq_kv = L.seq_kv;
@@ -179,7 +183,7 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
   // The plane's (batch, query head) and the KV head it reads; its rows of
   // Q, K, V and O start at these bases, one row pitch (bytes) apart.
   const char *Qp, *Kp, *Vp;
-  f16 *Op;
+  OutT *Op;
   const f16 *Mp = nullptr;
   uint32_t q_pitch, k_pitch, v_pitch;
   int64_t o_row;
@@ -187,7 +191,7 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
     Qp = (const char *)(Q + (int64_t)plane * seq_q * D);
     Kp = (const char *)(K + (int64_t)plane * seq_kv * D);
     Vp = (const char *)(V + (int64_t)plane * seq_kv * D);
-    Op = O + (int64_t)plane * seq_q * D;
+    Op = (OutT *)O + (int64_t)plane * seq_q * D;
     q_pitch = k_pitch = v_pitch = ROW;
     o_row = D;
   } else {
@@ -195,7 +199,7 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
     Qp = (const char *)(Q + pb * L.q[0] + ph * L.q[1]);
     Kp = (const char *)(K + pb * L.k[0] + pk * L.k[1]);
     Vp = (const char *)(V + pb * L.v[0] + pk * L.v[1]);
-    Op = O + pb * L.o[0] + ph * L.o[1];
+    Op = (OutT *)O + pb * L.o[0] + ph * L.o[1];
     if constexpr (MASK)
       Mp = M + pb * L.m[0] + ph * L.m[1];
     q_pitch = (uint32_t)(2 * L.q[2]);
@@ -426,7 +430,7 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
       const i32x4 v = *(const IHP_LDS i32x4 *)(
           staged_row(r, 1) + 16 * (c_phys ^ k_swizzle<D>(r)));
       if (qrow0 + r < seq_q && (DV == D || c_phys < CHV))
-        *(i32x4 *)(Op + (int64_t)(qrow0 + r) * o_row + 8 * c_phys) = v;
+        *(i32x4 *)((f16 *)Op + (int64_t)(qrow0 + r) * o_row + 8 * c_phys) = v;
     }
   };
 
@@ -782,14 +786,39 @@ __global__ __launch_bounds__(kThreads, 1) void attention_fwd_kernel(
       copy_q();
     {
       const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-      if (grp == 0)
+      if constexpr (OF32) {
+        // This group's half of the d tiles of this wave's row l32 of the
+        // block (q0 already names the next block's rows), straight to O:
+        // register quarter rq of tile dt is d = 32 dt + 8 rq + 4 g .. + 3.
+        const int row = qrow0 + wq * 32 + l32;
+        if (row < seq_q) {
+          float *dst = (float *)Op + (int64_t)row * o_row + 4 * g;
+          auto put = [&](auto half_c) {
+            constexpr int H = decltype(half_c)::value;
+#pragma unroll
+            for (int dt = H * DT / 2; dt < (H + 1) * DT / 2; ++dt)
+#pragma unroll
+              for (int rq = 0; rq < 4; ++rq)
+                if (DV == D || 32 * dt + 8 * rq < DV)
+                  *(f32x4 *)(dst + 32 * dt + 8 * rq) =
+                      f32x4{o[dt][4 * rq] * inv, o[dt][4 * rq + 1] * inv,
+                            o[dt][4 * rq + 2] * inv, o[dt][4 * rq + 3] * inv};
+          };
+          if (grp == 0)
+            put(std::integral_constant<int, 0>());
+          else
+            put(std::integral_constant<int, 1>());
+        }
+      } else if (grp == 0) {
         stage_o(o, inv, std::integral_constant<int, 0>());
-      else
+      } else {
         stage_o(o, inv, std::integral_constant<int, 1>());
+      }
     }
     wait_lgkmcnt0();
     block_barrier();
-    store_rows(qrow0);
+    if constexpr (!OF32)
+      store_rows(qrow0);
     if (!more)
       return;
     // The staged rows have been read: K(1) of the next block may land.
@@ -805,7 +834,7 @@ hipError_t launch_attention(const void *q, const void *k, const void *v,
                             void *o, int64_t batch,
                             const AttentionLayout &layout, int64_t head_dim,
                             float scale, int causal, void *stream,
-                            const void *mask) {
+                            const void *mask, int out_f32) {
   const int64_t q_blocks = (layout.seq_q + kBQ - 1) / kBQ;
   const int64_t planes = batch * layout.heads;
   // One workgroup per pair of query blocks (q_blocks - 1 - k, k).
@@ -814,28 +843,33 @@ hipError_t launch_attention(const void *q, const void *k, const void *v,
   const int64_t d = head_dim, sq = layout.seq_q, skv = layout.seq_kv,
                 h = layout.heads;
   const bool contig =
-      !mask && layout.group == 1 && layout.q[2] == d && layout.o[2] == d &&
+      !mask && !out_f32 && layout.group == 1 && layout.q[2] == d && layout.o[2] == d &&
       layout.k[2] == d && layout.v[2] == d && layout.q[1] == sq * d &&
       layout.o[1] == sq * d && layout.k[1] == skv * d &&
       layout.v[1] == skv * d && layout.q[0] == h * sq * d &&
       layout.o[0] == h * sq * d && layout.k[0] == h * skv * d &&
       layout.v[0] == h * skv * d;
   const void *kernel;
+  // The strided instances: (mask, f32 output) of head dim DVV in layout DD.
 #define IHP_ATT_PICK(DVV, DD)                                                  \
-  kernel = mask ? (const void *)&attention_fwd_kernel<DD, false, true, DVV>    \
-                : (const void *)&attention_fwd_kernel<DD, false, false, DVV>; \
+  kernel = mask ? (out_f32 ? (const void *)&attention_fwd_kernel<DD, false, true, DVV, true>   \
+                           : (const void *)&attention_fwd_kernel<DD, false, true, DVV>)        \
+                : (out_f32 ? (const void *)&attention_fwd_kernel<DD, false, false, DVV, true>  \
+                           : (const void *)&attention_fwd_kernel<DD, false, false, DVV>);      \
   break;
   switch (head_dim) {
     case 128:
-      kernel = mask     ? (const void *)&attention_fwd_kernel<128, false, true>
-               : contig ? (const void *)&attention_fwd_kernel<128, true>
-                        : (const void *)&attention_fwd_kernel<128, false>;
-      break;
+      if (contig) {
+        kernel = (const void *)&attention_fwd_kernel<128, true>;
+        break;
+      }
+      IHP_ATT_PICK(128, 128)
     case 64:
-      kernel = mask     ? (const void *)&attention_fwd_kernel<64, false, true>
-               : contig ? (const void *)&attention_fwd_kernel<64, true>
-                        : (const void *)&attention_fwd_kernel<64, false>;
-      break;
+      if (contig) {
+        kernel = (const void *)&attention_fwd_kernel<64, true>;
+        break;
+      }
+      IHP_ATT_PICK(64, 64)
     case 16: IHP_ATT_PICK(16, 64)
     case 32: IHP_ATT_PICK(32, 64)
     case 48: IHP_ATT_PICK(48, 64)
@@ -848,7 +882,7 @@ hipError_t launch_attention(const void *q, const void *k, const void *v,
 #undef IHP_ATT_PICK
   const f16 *qp = (const f16 *)q, *kp = (const f16 *)k, *vp = (const f16 *)v;
   const f16 *mp = (const f16 *)mask;
-  f16 *op = (f16 *)o;
+  void *op = o;
   AttentionLayout l = layout;
   void *args[] = {&qp, &kp, &vp, &op, &mp, &l, (void *)&scale_log2, &causal};
   return hipLaunchKernel(kernel, grid, dim3(kThreads), args, 0,
@@ -879,6 +913,13 @@ const KernelEntry *attention_kernels(int *count) {
       {"attention_fwd_d80_mask", (const void *)&attention_fwd_kernel<128, false, true, 80>, kThreads, kExportAttention},
       {"attention_fwd_d96_mask", (const void *)&attention_fwd_kernel<128, false, true, 96>, kThreads, kExportAttention},
       {"attention_fwd_d112_mask", (const void *)&attention_fwd_kernel<128, false, true, 112>, kThreads, kExportAttention},
+#define IHP_ATT_F32(NAME, DD, DVV)                                                                               \
+      {"attention_fwd_" NAME "_f32", (const void *)&attention_fwd_kernel<DD, false, false, DVV, true>, kThreads, kExportAttention}, \
+      {"attention_fwd_" NAME "_mask_f32", (const void *)&attention_fwd_kernel<DD, false, true, DVV, true>, kThreads, kExportAttention},
+      IHP_ATT_F32("d16", 64, 16) IHP_ATT_F32("d32", 64, 32) IHP_ATT_F32("d48", 64, 48)
+      IHP_ATT_F32("d64", 64, 64) IHP_ATT_F32("d80", 128, 80) IHP_ATT_F32("d96", 128, 96)
+      IHP_ATT_F32("d112", 128, 112) IHP_ATT_F32("d128", 128, 128)
+#undef IHP_ATT_F32
   };
   *count = (int)(sizeof(all) / sizeof(all[0]));
   return all;

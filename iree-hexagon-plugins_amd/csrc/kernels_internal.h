@@ -194,7 +194,7 @@ hipError_t launch_attention(const void *q, const void *k, const void *v,
                             void *o, int64_t batch,
                             const AttentionLayout &layout, int64_t head_dim,
                             float scale, int causal, void *stream,
-                            const void *mask = nullptr);
+                            const void *mask = nullptr, int out_f32 = 0);
 
 // The general attention kernel's view (attention_general.hip): strides as
 // AttentionLayout plus the mask's (batch, head, row, key) element strides

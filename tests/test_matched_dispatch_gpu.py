@@ -255,4 +255,5 @@ def test_attention_chain_head96_f32(pkg, oracle, dev):
              [q.to(dev), k.to(dev), v.to(dev), o])
     ref = oracle.attention(q.numpy(), k.numpy(), v.numpy(), scale=m.scale,
                            out_f32=True)
-    fp16_ok(oracle, o.cpu().numpy(), ref, bound=2e-5)
+    # the MFMA kernel takes head dim 96: f16 probabilities before PV
+    fp16_ok(oracle, o.cpu().numpy(), ref, bound=4e-4)
