@@ -635,7 +635,40 @@ def suite(pkg, inputs, dev, args):
          cpu=(lambda: oracle.attention_f16(q4, k4, v4, causal=True,
                                            threads=threads),
               "4 of the 32 heads, scaled by 8", 4 / 32))
-    del q, k_, v, o
+    # The same shape through the general form (not BASELINE configs): an
+    # additive [S, S] mask shared by every head (the MFMA kernel's mask
+    # instance), an f32 result, and head dim 96 (the 128-wide layout
+    # reading 96 columns). The oracle on 4 heads beside each.
+    g = torch.Generator().manual_seed(5)
+    mh = (2 * torch.randn(2048, 2048, generator=g)).half()
+    md = mh.to(dev)
+    o32 = torch.empty(q.shape, dtype=torch.float32, device=dev)
+    for name, fn, oracle_fn, nbytes in (
+            ("C4 shape, additive mask [S, S], causal",
+             lambda: pkg.attention(q, k_, v, o, causal=True, mask=md),
+             lambda: oracle.attention(q4, k4, v4, causal=True, mask=mh.numpy(),
+                                      threads=threads),
+             4 * q.numel() * 2 + md.numel() * 2),
+            ("C4 shape, f32 result, causal",
+             lambda: pkg.attention(q, k_, v, o32, causal=True),
+             lambda: oracle.attention(q4, k4, v4, causal=True, out_f32=True,
+                                      threads=threads),
+             3 * q.numel() * 2 + o32.numel() * 4)):
+        ms = timed(fn, steps, warm)
+        emit(name, ms, 4 * 32 * 2048 * 2048 * 128 / 2, nbytes, "mfma",
+             cpu=(oracle_fn, "4 of the 32 heads, scaled by 8", 4 / 32))
+    q96, k96, v96 = (t[..., :96].contiguous() for t in (qh, kh, vh))
+    q96d, k96d, v96d = q96.to(dev), k96.to(dev), v96.to(dev)
+    o96 = torch.empty_like(q96d)
+    ms = timed(lambda: pkg.attention(q96d, k96d, v96d, o96, causal=True),
+               steps, warm)
+    q4, k4, v4 = (t[:, :4].contiguous().numpy() for t in (q96, k96, v96))
+    emit("C4 shape, head dim 96, causal", ms, 4 * 32 * 2048 * 2048 * 96 / 2,
+         4 * q96d.numel() * 2, "mfma",
+         cpu=(lambda: oracle.attention(q4, k4, v4, causal=True,
+                                       threads=threads),
+              "4 of the 32 heads, scaled by 8", 4 / 32))
+    del q, k_, v, o, md, o32, q96d, k96d, v96d, o96
 
     for m in (1, 512):
         x, w, s = inputs.c5_w8a16(m)

@@ -697,6 +697,10 @@ int iree_mi355x_attention(const iree_mi355x_attention_t *a, void *stream) {
   g.dv = (int)a->head_dim_v;
   g.scale = a->scale;
   g.causal = causal ? 1 : 0;
+  g.vec_k = a->head_dim % 8 == 0 && st.k[0] % 8 == 0 && st.k[1] % 8 == 0 &&
+            st.k[2] % 8 == 0 && aligned(a->k, 16);
+  g.vec_v = a->head_dim_v % 8 == 0 && st.v[0] % 8 == 0 &&
+            st.v[1] % 8 == 0 && st.v[2] % 8 == 0 && aligned(a->v, 16);
   return launch_status(
       launch_attention_general(a->q, a->k, a->v, a->o, a->mask, a->batch, g,
                                out_f32 ? 1 : 0, stream),

@@ -206,6 +206,9 @@ struct AttentionGeneralLayout {
   int heads, group, seq_q, seq_kv, dqk, dv;
   float scale;
   int causal;
+  // K (V) rows start 16-byte aligned and their head dim is a multiple of 8:
+  // the kernel fills LDS 16 bytes at a time.
+  int vec_k, vec_v;
 };
 hipError_t launch_attention_general(const void *q, const void *k,
                                     const void *v, void *o, const void *mask,
