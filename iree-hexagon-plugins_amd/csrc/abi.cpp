@@ -603,8 +603,9 @@ int iree_mi355x_attention(const iree_mi355x_attention_t *a, void *stream) {
   if (!a->q || !a->o || (a->seq_kv > 0 && (!a->k || !a->v)))
     return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: null pointer", who);
   const iree_mi355x_attention_strides_t &st = a->strides;
+  // Mask strides are read only with a mask.
   const int64_t *all[5] = {st.q, st.k, st.v, st.o, a->mask_strides};
-  for (int t = 0; t < 5; ++t)
+  for (int t = 0; t < (a->mask ? 5 : 4); ++t)
     for (int i = 0; i < (t == 4 ? 4 : 3); ++i)
       if (all[t][i] < 0)
         return fail(IREE_MI355X_INVALID_ARGUMENT, "%s: negative stride", who);
