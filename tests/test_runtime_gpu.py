@@ -175,6 +175,46 @@ def test_direct_references_and_attention(pkg, oracle, dev):
                               oracle.matmul_f16(a.numpy(), b.numpy())) <= FP16_BOUND
 
 
+def test_general_attention_in_a_command_buffer(pkg, oracle, dev):
+    """The 41-word attention_f16 form through a command buffer: a mask in
+    binding 4 taken from the binding table, head dims 96 / 96 with an f32
+    result (the MFMA kernel's f32 mask instance) and 24 / 40 (the general
+    kernel), in one segment on two lanes."""
+    g = torch.Generator().manual_seed(9)
+    b, h, s = 1, 2, 192
+    cases = []
+    for d, dv in ((96, 96), (24, 40)):
+        q, k_ = (torch.randn(b, h, s, d, generator=g).half() for _ in range(2))
+        v = torch.randn(b, h, s, dv, generator=g).half()
+        o = torch.full((b, h, s, dv), float("nan"), device=dev)
+        cases.append((d, dv, q, k_, v, o))
+    mask = (2 * torch.randn(s, s, generator=g)).half()
+    mask[torch.rand(s, s, generator=g) < 0.1] = float("-inf")
+    dm = mask.to(dev)
+    flags = pkg.ATTENTION_MASK | pkg.ATTENTION_OUT_F32 | pkg.CAUSAL
+    cb = pkg.CommandBuffer()
+    table = [dm]
+    held = []  # the device copies must outlive the submission
+    for d, dv, q, k_, v, o in cases:
+        consts = pkg.attention_constants(b, h, s, s, d, 0.25, flags,
+                                         head_dim_v=dv,
+                                         mask_strides=[0, 0, s, 1])
+        dq, dk, dvv = q.to(dev), k_.to(dev), v.to(dev)
+        held += [dq, dk, dvv]
+        cb.dispatch("attention_f16", consts,
+                    [pkg.direct(dq), pkg.direct(dk), pkg.direct(dvv),
+                     pkg.direct(o), pkg.slot(0)])
+    cb.end()
+    cb.submit(table, max_concurrent=2)
+    torch.cuda.synchronize()
+    for d, dv, q, k_, v, o in cases:
+        ref = oracle.attention(q.numpy(), k_.numpy(), v.numpy(), scale=0.25,
+                               causal=True, mask=mask.numpy(), out_f32=True)
+        # the MFMA kernel's f16 probabilities: 4e-4; the general kernel 2e-5
+        bound = 4e-4 if d == dv else 2e-5
+        assert oracle.fp16_parity(o.cpu().numpy(), ref) <= bound, (d, dv)
+
+
 @pytest.mark.skip(reason="a 4-lane submission captured into a HIP graph ended "
                   "in a host segmentation fault in hipStreamEndCapture; the "
                   "cause is not established, so the runtime refuses "
