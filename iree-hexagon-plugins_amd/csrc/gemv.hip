@@ -9,10 +9,14 @@
 // kernel, not an MFMA kernel:
 //  * each lane streams one 16-byte column segment of W (8 f16 or 16 int8
 //    weights) down a run of rows, 16 loads in flight, and accumulates in
-//    f32; x is read through the scalar cache, nothing is staged first;
+//    f32; x is read once per lane and broadcast, nothing is staged first;
+//  * a wave covers 64 segments of one row, or (half-wave form) 32 segments
+//    of two rows, each 32-lane half streaming its own run: half the columns
+//    per workgroup, so fewer K splits and a smaller final sum per column
+//    block;
 //  * K is split over a 2-D grid (column block x K split) sized to about one
-//    workgroup per CU; each workgroup sums its 8 waves through LDS and writes
-//    an f32 partial;
+//    workgroup per CU; each workgroup sums its waves' runs through LDS and
+//    writes an f32 partial;
 //  * the last workgroup to finish a column block (device-scope arrival
 //    counter) sums the partials, applies the per-column scale (W8A16), adds
 //    the DPS init if asked, rounds once and re-arms the counter, so the
@@ -67,13 +71,15 @@ __device__ __forceinline__ void store_y(f16 *p, float v, int acc) {
 
 }  // namespace
 
-// Grid: (column blocks, K splits). A workgroup owns 64 * kCols columns
-// (512 f16 / 1024 int8: one 16-byte segment per lane of a row) and k_chunk
-// rows, which its 8 waves split into contiguous runs of rows_per_wave. Each
-// lane streams its column segment down its wave's rows, two batches of
-// kBatch loads in flight, and accumulates in f32; x[r][k] is wave-uniform and
-// comes through the scalar cache.
-template <typename WT, int MR, typename OutT>
+// Grid: (column blocks, K splits). A workgroup owns (64 / H) * kCols columns
+// (H = 1: 512 f16 / 1024 int8, one 16-byte segment per lane of a row; H = 2:
+// half that, one segment per lane of a 32-lane half) and k_chunk rows, which
+// its 8 waves split into contiguous runs of rows_per_wave, and each wave's H
+// lane groups into runs of rows_per_wave / H. Each lane streams its column
+// segment down its group's rows, two batches of kBatch loads in flight, and
+// accumulates in f32; x[r][k] is uniform across a lane group and broadcast
+// with readlane.
+template <typename WT, int MR, typename OutT, int H>
 __global__ __launch_bounds__(kThreads, 1) void gemv_splitk_kernel(
     const f16 *__restrict__ X, const WT *__restrict__ W,
     const f16 *__restrict__ scale, OutT *__restrict__ Y, int N, int K,
@@ -82,9 +88,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemv_splitk_kernel(
     unsigned *__restrict__ counters, int64_t sx, int64_t sw, int64_t sy,
     Epi epi, int64_t s_mul) {
   typedef WTraits<WT> Tr;
+  static_assert(H == 1 || H == 2, "one or two lane groups per wave");
   constexpr int CPT = Tr::kCols;
-  constexpr int BNC = 64 * CPT;
-  __shared__ float red[kWaves][MR][BNC];
+  constexpr int LPR = 64 / H;  // lanes per row
+  constexpr int BNC = LPR * CPT;
+  __shared__ float red[kWaves * H][MR][BNC];
   __shared__ unsigned last_flag;
 
   // Batch z: this workgroup's x, W, y, partials and counters.
@@ -99,15 +107,26 @@ __global__ __launch_bounds__(kThreads, 1) void gemv_splitk_kernel(
   }
   const int tid = threadIdx.x;
   const int lane = tid & 63;
+  const int half = H == 2 ? lane / LPR : 0;  // this lane's group
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int split = blockIdx.y, splits = gridDim.y;
   const int64_t n_base = (int64_t)blockIdx.x * BNC;
-  const int64_t n0 = n_base + lane * CPT;
+  const int64_t n0 = n_base + (lane % LPR) * CPT;
   const bool col_ok = n0 < N;  // N is a multiple of CPT
   const int64_t kc0 = (int64_t)split * k_chunk;
   const int64_t kc1 = kc0 + k_chunk < K ? kc0 + k_chunk : K;
   const int64_t kw0 = kc0 + (int64_t)wave * rows_per_wave;
   const int64_t kw1 = kw0 + rows_per_wave < kc1 ? kw0 + rows_per_wave : kc1;
+  // The wave's run of nrows rows: group 0 owns the first cnt0 and group 1
+  // the other cnt1 (<= cnt0). Both stream cnt0 steps, group 1 over the cnt0
+  // rows that end the run, whose first cnt0 - cnt1 (group 0's) it re-reads
+  // and skips: every step is a row of the run for both groups, and the step
+  // count is wave-uniform.
+  const int hr = rows_per_wave / H;
+  const int nrows = kw1 > kw0 ? (int)(kw1 - kw0) : 0;
+  const int cnt0 = nrows < hr ? nrows : hr;
+  const int skip1 = H == 1 ? 0 : 2 * cnt0 - nrows;  // cnt0 - cnt1
+  const int64_t hk0 = half ? kw1 - cnt0 : kw0;
 
   float acc[MR][CPT];
 #pragma unroll
@@ -116,41 +135,54 @@ __global__ __launch_bounds__(kThreads, 1) void gemv_splitk_kernel(
     for (int c = 0; c < CPT; ++c)
       acc[r][c] = 0.0f;
 
-  // x[r][kw0 + lane] for this wave's rows (at most 64), loaded before any
+  // x[r][k] for this lane group's steps (at most 64), loaded before any
   // weight so that the in-order return of vector loads lets the weights stay
-  // in flight while it is read; row u of the run is then lane u's value,
-  // broadcast with readlane.
-  int xl[MR];  // raw f16 bits, widened when broadcast
+  // in flight while it is read. Lane s holds step s of each group as f16
+  // bits, group 1's in the upper half; a step's value is broadcast with
+  // readlane and each group shifts its half down.
+  int xl[MR];
   const unsigned short *xbits = (const unsigned short *)X;
 #pragma unroll
-  for (int r = 0; r < MR; ++r)
-    xl[r] = kw0 + lane < kw1 ? (int)xbits[r * ldx + kw0 + lane] : 0;
+  for (int r = 0; r < MR; ++r) {
+    int v = lane < cnt0 ? (int)xbits[r * ldx + kw0 + lane] : 0;
+    if constexpr (H == 2)
+      if (lane < cnt0)
+        v |= (int)xbits[r * ldx + kw1 - cnt0 + lane] << 16;
+    xl[r] = v;
+  }
+  const int x_shift = 16 * half;
+  auto x_at = [&](int r, int idx) {
+    const int bits = __builtin_amdgcn_readlane(xl[r], idx);
+    return (float)__builtin_bit_cast(
+        f16, (unsigned short)(H == 2 ? bits >> x_shift : bits));
+  };
 
   // Lanes past N read column 0 instead (never stored), so every load of a
-  // batch is unpredicated and only the wave-uniform row bound branches.
-  const char *wcol = (const char *)(W + (col_ok ? n0 : 0));
+  // batch is unpredicated and only the wave-uniform step bound branches.
   const int64_t ldw_b = ldw * (int64_t)sizeof(WT);
-  // Rows past the run re-read its last row (their products are skipped), so
-  // a batch is 8 unconditional loads the wait counter can track exactly.
-  auto load_batch = [&](int64_t kb, i32x4 *v) {
+  const char *wrow = (const char *)(W + (col_ok ? n0 : 0)) + hk0 * ldw_b;
+  // Steps past the run re-read its last step (their products are skipped),
+  // so a batch is 8 unconditional loads the wait counter can track exactly.
+  auto load_batch = [&](int sb, i32x4 *v) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const int64_t k = kb + u < kw1 ? kb + u : kw1 - 1;
-      v[u] = __builtin_nontemporal_load((const i32x4 *)(wcol + k * ldw_b));
+      const int st = sb + u < cnt0 ? sb + u : cnt0 - 1;
+      v[u] = __builtin_nontemporal_load(
+          (const i32x4 *)(wrow + (int64_t)st * ldw_b));
     }
   };
-  auto consume = [&](int64_t kb, const i32x4 *v) {
+  auto consume = [&](int sb, const i32x4 *v) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const int64_t k = kb + u;
-      if (k < kw1) {  // wave-uniform
+      const int st = sb + u;
+      // Wave-uniform except in the half-wave form's ragged runs, whose
+      // first steps group 1 skips.
+      if (st < cnt0 && (H == 1 || st >= skip1 || half == 0)) {
         float w[CPT];
         Tr::widen(v[u], w);
-        const int idx = (int)(k - kw0);
 #pragma unroll
         for (int r = 0; r < MR; ++r) {
-          const float xv = (float)__builtin_bit_cast(
-              f16, (unsigned short)__builtin_amdgcn_readlane(xl[r], idx));
+          const float xv = x_at(r, st);
 #pragma unroll
           for (int c = 0; c < CPT; ++c)
             acc[r][c] += xv * w[c];
@@ -158,30 +190,38 @@ __global__ __launch_bounds__(kThreads, 1) void gemv_splitk_kernel(
       }
     }
   };
-  if (kw0 < kw1) {
-    i32x4 cur[kBatch], nxt[kBatch];
-    int64_t kb = kw0;
-    load_batch(kb, cur);
+  // Two register batches in turn, the loop unrolled by two, so that no
+  // batch is copied (a copy would wait for its loads) and every consume
+  // follows a known sequence of loads: the next batch stays in flight while
+  // the current one is consumed.
+  if (cnt0 > 0) {
+    i32x4 va[kBatch], vb[kBatch];
+    int sb = 0;
+    load_batch(sb, va);
     while (true) {
-      const bool more = kb + kBatch < kw1;
-      if (more)
-        load_batch(kb + kBatch, nxt);
-      consume(kb, cur);
-      if (!more)
+      if (sb + kBatch >= cnt0) {
+        consume(sb, va);
         break;
-      kb += kBatch;
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u)
-        cur[u] = nxt[u];
+      }
+      load_batch(sb + kBatch, vb);
+      consume(sb, va);
+      sb += kBatch;
+      if (sb + kBatch >= cnt0) {
+        consume(sb, vb);
+        break;
+      }
+      load_batch(sb + kBatch, va);
+      consume(sb, vb);
+      sb += kBatch;
     }
   }
 
-  // Sum the 8 waves' row runs through LDS, in wave order.
+  // Sum the waves' (and groups') row runs through LDS, in row order.
 #pragma unroll
   for (int r = 0; r < MR; ++r)
 #pragma unroll
     for (int c = 0; c < CPT; ++c)
-      red[wave][r][lane * CPT + c] = acc[r][c];
+      red[wave * H + half][r][(lane % LPR) * CPT + c] = acc[r][c];
   __syncthreads();
 
   // Output of one element: scale, fused epilogue (chosen once per
@@ -203,7 +243,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemv_splitk_kernel(
         continue;
       float s = red[0][r][col];
 #pragma unroll
-      for (int w = 1; w < kWaves; ++w)
+      for (int w = 1; w < kWaves * H; ++w)
         s += red[w][r][col];
       if (direct) {
         finish(with_epi, s, r, n);
@@ -257,34 +297,59 @@ __global__ __launch_bounds__(kThreads, 1) void gemv_splitk_kernel(
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
-GemvPlan gemv_plan(int64_t m, int64_t n, int64_t k, int w_bytes,
-                   int64_t batch) {
-  (void)m;
-  const int cpt = w_bytes == 2 ? 8 : 16;
+// The plan with h lane groups per wave.
+static GemvPlan gemv_plan_h(int64_t n, int64_t k, int cpt, int64_t batch,
+                            int h) {
   GemvPlan p;
-  p.cols_per_wg = 64 * cpt;
+  p.halves = h;
+  p.cols_per_wg = 64 / h * cpt;
   const int64_t col_blocks = (n + p.cols_per_wg - 1) / p.cols_per_wg;
   // About one workgroup per CU (256): measured over 128..1024 workgroups on
   // the C3 / C5 shapes, fewer and longer K runs shorten the split-K tail (the
   // partial publish, arrival count and final sum are three memory round
   // trips) but leave CUs idle, more add tail latency. Split K so that
-  // col_blocks x splits is about that, each wave's run of rows a multiple of
-  // the load batch.
+  // col_blocks x splits is about that, each lane group's run of rows a
+  // multiple of the load batch.
   const int64_t per_batch = (kGemvTargetWgs + batch - 1) / batch;
   int64_t want = (per_batch + col_blocks / 2) / col_blocks;
   if (want < 1)
     want = 1;
+  const int64_t unit = (int64_t)h * kBatch;
   int64_t rpw = (k + want * kWaves - 1) / (want * kWaves);
-  rpw = (rpw + kBatch - 1) / kBatch * kBatch;
-  if (rpw < kBatch)
-    rpw = kBatch;
-  if (rpw > kMaxRowsPerWave)  // x of a run is one value per lane
-    rpw = kMaxRowsPerWave;
+  rpw = (rpw + unit - 1) / unit * unit;
+  if (rpw < unit)
+    rpw = unit;
+  if (rpw > (int64_t)h * kMaxRowsPerWave)  // x of a run: one value per lane
+    rpw = (int64_t)h * kMaxRowsPerWave;
   p.rows_per_wave = (int)rpw;
   p.k_chunk = (int)(rpw * kWaves);
   p.splits = k > 0 ? (int)((k + p.k_chunk - 1) / p.k_chunk) : 1;
   p.col_blocks = col_blocks;
   return p;
+}
+
+GemvPlan gemv_plan(int64_t m, int64_t n, int64_t k, int w_bytes,
+                   int64_t batch) {
+  (void)m;
+  const int cpt = w_bytes == 2 ? 8 : 16;
+  const GemvPlan one = gemv_plan_h(n, k, cpt, batch, 1);
+  const GemvPlan two = gemv_plan_h(n, k, cpt, batch, 2);
+  // The last workgroup of a column block reads splits x columns partials
+  // alone: the half-wave form halves the columns and about halves the
+  // splits. Taken when it shrinks that read and keeps the grid within 1/16
+  // of the full-wave one (and its column blocks within the workspace's
+  // arrival counters, which the full-wave form's eligibility checked).
+  const int64_t wgs1 = one.col_blocks * one.splits;
+  const int64_t wgs2 = two.col_blocks * two.splits;
+  const int64_t read1 = (int64_t)one.splits * one.cols_per_wg;
+  const int64_t read2 =
+      two.splits > 1 ? (int64_t)two.splits * two.cols_per_wg : 0;
+  const bool counters_fit =
+      two.splits == 1 || two.col_blocks * batch <= kMaxWorkspaceCounters;
+  if (one.splits > 1 && read2 < read1 && wgs2 <= wgs1 + wgs1 / 16 &&
+      counters_fit)
+    return two;
+  return one;
 }
 
 // Workspace layout: [the fixed counter region, one counter per column block]
@@ -312,13 +377,17 @@ static hipError_t launch_gemv_t(const MatmulArgs &a, const void *scale,
       workspace ? (float *)((char *)workspace + counter_bytes(p.col_blocks))
                 : nullptr;
   dim3 grid((unsigned)p.col_blocks, (unsigned)p.splits, (unsigned)a.batch);
-  hipLaunchKernelGGL((gemv_splitk_kernel<WT, MR, OutT>), grid, dim3(kThreads),
-                     0, (hipStream_t)a.stream, (const f16 *)a.a,
-                     (const WT *)a.b, (const f16 *)scale, (OutT *)a.c,
-                     (int)a.n, (int)a.k, a.lda, a.ldb, a.ldc, p.k_chunk,
-                     p.rows_per_wave, a.accumulate, partials, counters, a.sa,
-                     a.sb, a.sc, make_epi(a), epi_batch_stride(a));
-  return hipGetLastError();
+  auto run = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0,
+                       (hipStream_t)a.stream, (const f16 *)a.a,
+                       (const WT *)a.b, (const f16 *)scale, (OutT *)a.c,
+                       (int)a.n, (int)a.k, a.lda, a.ldb, a.ldc, p.k_chunk,
+                       p.rows_per_wave, a.accumulate, partials, counters,
+                       a.sa, a.sb, a.sc, make_epi(a), epi_batch_stride(a));
+    return hipGetLastError();
+  };
+  return p.halves == 2 ? run(gemv_splitk_kernel<WT, MR, OutT, 2>)
+                       : run(gemv_splitk_kernel<WT, MR, OutT, 1>);
 }
 
 template <typename WT, typename OutT>
@@ -350,22 +419,35 @@ hipError_t launch_gemv(const MatmulArgs &a, int w_bytes, const void *scale,
 
 namespace ihp {
 
-// Every GEMV kernel: rows 1..4 for f16 weights (f16 / f32 out) and W8A16.
+// Every GEMV kernel: rows 1..4 for f16 weights (f16 / f32 out) and W8A16,
+// in the full-wave and the half-wave (_h2) form.
 const KernelEntry *gemv_kernels(int *count) {
   const uint32_t f16x = kExportMatmulF16 | kExportBatchMatmulF16;
   static const KernelEntry all[] = {
-      {"gemv_f16_r1", (const void *)&gemv_splitk_kernel<f16, 1, f16>, kThreads, f16x},
-      {"gemv_f16_r2", (const void *)&gemv_splitk_kernel<f16, 2, f16>, kThreads, f16x},
-      {"gemv_f16_r3", (const void *)&gemv_splitk_kernel<f16, 3, f16>, kThreads, f16x},
-      {"gemv_f16_r4", (const void *)&gemv_splitk_kernel<f16, 4, f16>, kThreads, f16x},
-      {"gemv_f16f32_r1", (const void *)&gemv_splitk_kernel<f16, 1, float>, kThreads, f16x},
-      {"gemv_f16f32_r2", (const void *)&gemv_splitk_kernel<f16, 2, float>, kThreads, f16x},
-      {"gemv_f16f32_r3", (const void *)&gemv_splitk_kernel<f16, 3, float>, kThreads, f16x},
-      {"gemv_f16f32_r4", (const void *)&gemv_splitk_kernel<f16, 4, float>, kThreads, f16x},
-      {"gemv_w8a16_r1", (const void *)&gemv_splitk_kernel<int8_t, 1, f16>, kThreads, kExportW8A16},
-      {"gemv_w8a16_r2", (const void *)&gemv_splitk_kernel<int8_t, 2, f16>, kThreads, kExportW8A16},
-      {"gemv_w8a16_r3", (const void *)&gemv_splitk_kernel<int8_t, 3, f16>, kThreads, kExportW8A16},
-      {"gemv_w8a16_r4", (const void *)&gemv_splitk_kernel<int8_t, 4, f16>, kThreads, kExportW8A16},
+      {"gemv_f16_r1", (const void *)&gemv_splitk_kernel<f16, 1, f16, 1>, kThreads, f16x},
+      {"gemv_f16_r2", (const void *)&gemv_splitk_kernel<f16, 2, f16, 1>, kThreads, f16x},
+      {"gemv_f16_r3", (const void *)&gemv_splitk_kernel<f16, 3, f16, 1>, kThreads, f16x},
+      {"gemv_f16_r4", (const void *)&gemv_splitk_kernel<f16, 4, f16, 1>, kThreads, f16x},
+      {"gemv_f16f32_r1", (const void *)&gemv_splitk_kernel<f16, 1, float, 1>, kThreads, f16x},
+      {"gemv_f16f32_r2", (const void *)&gemv_splitk_kernel<f16, 2, float, 1>, kThreads, f16x},
+      {"gemv_f16f32_r3", (const void *)&gemv_splitk_kernel<f16, 3, float, 1>, kThreads, f16x},
+      {"gemv_f16f32_r4", (const void *)&gemv_splitk_kernel<f16, 4, float, 1>, kThreads, f16x},
+      {"gemv_w8a16_r1", (const void *)&gemv_splitk_kernel<int8_t, 1, f16, 1>, kThreads, kExportW8A16},
+      {"gemv_w8a16_r2", (const void *)&gemv_splitk_kernel<int8_t, 2, f16, 1>, kThreads, kExportW8A16},
+      {"gemv_w8a16_r3", (const void *)&gemv_splitk_kernel<int8_t, 3, f16, 1>, kThreads, kExportW8A16},
+      {"gemv_w8a16_r4", (const void *)&gemv_splitk_kernel<int8_t, 4, f16, 1>, kThreads, kExportW8A16},
+      {"gemv_f16_r1_h2", (const void *)&gemv_splitk_kernel<f16, 1, f16, 2>, kThreads, f16x},
+      {"gemv_f16_r2_h2", (const void *)&gemv_splitk_kernel<f16, 2, f16, 2>, kThreads, f16x},
+      {"gemv_f16_r3_h2", (const void *)&gemv_splitk_kernel<f16, 3, f16, 2>, kThreads, f16x},
+      {"gemv_f16_r4_h2", (const void *)&gemv_splitk_kernel<f16, 4, f16, 2>, kThreads, f16x},
+      {"gemv_f16f32_r1_h2", (const void *)&gemv_splitk_kernel<f16, 1, float, 2>, kThreads, f16x},
+      {"gemv_f16f32_r2_h2", (const void *)&gemv_splitk_kernel<f16, 2, float, 2>, kThreads, f16x},
+      {"gemv_f16f32_r3_h2", (const void *)&gemv_splitk_kernel<f16, 3, float, 2>, kThreads, f16x},
+      {"gemv_f16f32_r4_h2", (const void *)&gemv_splitk_kernel<f16, 4, float, 2>, kThreads, f16x},
+      {"gemv_w8a16_r1_h2", (const void *)&gemv_splitk_kernel<int8_t, 1, f16, 2>, kThreads, kExportW8A16},
+      {"gemv_w8a16_r2_h2", (const void *)&gemv_splitk_kernel<int8_t, 2, f16, 2>, kThreads, kExportW8A16},
+      {"gemv_w8a16_r3_h2", (const void *)&gemv_splitk_kernel<int8_t, 3, f16, 2>, kThreads, kExportW8A16},
+      {"gemv_w8a16_r4_h2", (const void *)&gemv_splitk_kernel<int8_t, 4, f16, 2>, kThreads, kExportW8A16},
   };
   *count = (int)(sizeof(all) / sizeof(all[0]));
   return all;

@@ -163,6 +163,7 @@ constexpr int kGemvThreads = 512;
 constexpr int kGemvTargetWgs = 256;
 struct GemvPlan {
   int splits;          // K split count (grid y)
+  int halves;          // 1: a wave streams one row; 2: two 32-lane halves
   int cols_per_wg;     // output columns per workgroup
   int k_chunk;         // rows of W per workgroup
   int rows_per_wave;   // contiguous rows each of the 8 waves streams

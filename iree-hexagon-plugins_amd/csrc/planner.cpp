@@ -451,8 +451,9 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
     const int wb = elem_bytes(d->b_elem);
     const int64_t batch = d->batch > 0 ? d->batch : 1;
     GemvPlan g = gemv_plan(d->m, d->n, d->k, wb, batch);
-    snprintf(plan->config_name, sizeof(plan->config_name), "gemv_%s_r%lld",
-             wb == 1 ? "w8a16" : "f16", (long long)d->m);
+    snprintf(plan->config_name, sizeof(plan->config_name), "gemv_%s_r%lld%s",
+             wb == 1 ? "w8a16" : "f16", (long long)d->m,
+             g.halves == 2 ? "_h2" : "");
     plan->tile_m = d->m;
     plan->tile_n = g.cols_per_wg;
     plan->tile_k = g.k_chunk;

@@ -117,7 +117,9 @@ F16, I8, I32, F32 = 0, 1, 2, 3
     ((F16, F16, F16, 100, 512, 256, 0), 1, None),
     ((F16, F16, F16, 100, 500, 256, 0), 2, (64, 64)),
     ((F16, F16, F16, 17, 19, 23, 1), 2, (64, 64)),
-    ((F16, F16, F16, 1, 4096, 4096, 0), 3, (1, 512)),
+    # GEMV: the half-wave form (32 lanes x 8 f16 per row) where it shrinks
+    # the final sum, the full-wave form (64 lanes) otherwise
+    ((F16, F16, F16, 1, 4096, 4096, 0), 3, (1, 256)),
     ((F16, F16, F16, 4, 11008, 4096, 0), 3, (4, 512)),
     ((F16, F16, F16, 5, 4096, 4096, 0), 1, None),
     ((F16, F16, F16, 5, 4090, 4096, 0), 2, (64, 64)),
@@ -152,7 +154,9 @@ def test_planner_classification(pkg, case, family, tile):
 def test_planner_w8a16_and_unsupported_types(pkg):
     d = pkg.make_desc(F16, I8, F16, 1, 11008, 4096, 0, has_scale=True)
     p = pkg.plan(d)
-    assert p.family == pkg.FAMILY_GEMV and p.tile_n == 1024  # 64 lanes x 16 int8
+    # half-wave form: 32 lanes x 16 int8 per row
+    assert p.family == pkg.FAMILY_GEMV and p.tile_n == 512
+    assert p.config_name == b"gemv_w8a16_r1_h2"
     assert p.workspace_bytes > 0 and p.splits > 1
     d = pkg.make_desc(F16, I8, F16, 512, 11008, 4096, 0, has_scale=True)
     p = pkg.plan(d)

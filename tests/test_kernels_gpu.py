@@ -342,6 +342,39 @@ def test_gemv_f16(pkg, oracle, dev, m, n, k):
     fp16_ok(oracle, y32.cpu().numpy(), ref32)
 
 
+@pytest.mark.parametrize("m,n,k,w8,form", [
+    (1, 4096, 4096, False, "_h2"),     # 16 column blocks x 16 splits
+    (1, 11008, 4096, False, ""),       # the full-wave form keeps 242 groups
+    (2, 1000, 3004, False, "_h2"),     # last split: a wave of 12 rows (8 + 4)
+    (2, 1000, 3000, False, "_h2"),     # last split: a wave of 8 rows (8 + 0)
+    (3, 1024, 3004, True, "_h2"),
+    (1, 11008, 4096, True, "_h2"),
+    (1, 4096, 100, False, "_h2"),      # one split: no partials at all
+])
+def test_gemv_lane_group_forms(pkg, oracle, dev, m, n, k, w8, form):
+    """Both GEMV forms (a wave streams one row, or its two 32-lane halves
+    stream runs of their own), including the last split's ragged runs, where
+    the second half has fewer rows than the first or none."""
+    g = torch.Generator().manual_seed(m * 13 + n + k)
+    x = (torch.randn(m, k, generator=g) * 0.5).half()
+    p = pkg.plan(pkg.make_desc(0, 1 if w8 else 0, 0, m, n, k, 0,
+                               has_scale=w8))
+    assert p.family == pkg.FAMILY_GEMV
+    assert p.config_name.decode().endswith(f"_r{m}{form}"), p.config_name
+    buf, y = canary_out((m, n), torch.float16, dev, 3.0)
+    if w8:
+        w = torch.randint(-128, 128, (k, n), generator=g).to(torch.int8)
+        s = (torch.rand(n, generator=g) * 0.01 + 0.001).half()
+        pkg.quantized_matmul(x.to(dev), w.to(dev), s.to(dev), y)
+        ref = oracle.w8a16(x.numpy(), w.numpy(), s.numpy())
+    else:
+        w = (torch.randn(k, n, generator=g) * 0.05).half()
+        pkg.matmul(x.to(dev), w.to(dev), y)
+        ref = oracle.matmul_f16(x.numpy(), w.numpy())
+    check_canary(buf, m, n, 3.0)
+    fp16_ok(oracle, y.cpu().numpy(), ref)
+
+
 def test_gemv_repeated_calls_rearm_counters(pkg, oracle, dev):
     g = torch.Generator().manual_seed(11)
     for n, k in ((4096, 4096), (2048, 8192), (4096, 4096), (512, 300)):
