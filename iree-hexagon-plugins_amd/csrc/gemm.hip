@@ -671,8 +671,7 @@ __global__ __launch_bounds__(64 * WM *WN, 1) void gemm_lds_kernel(
         } else {
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            store_out(dst + r, acc[i][j][r],
-                      store_mode == kStoreAccumulate ? 1 : 0);
+            store_out(dst + r, acc[i][j][r], store_mode);
         }
       }
     return;
@@ -1103,18 +1102,18 @@ __global__ __launch_bounds__(256) void gemm_general_kernel(
   float s = 1.0f;
   if (kScale)
     s = (float)scale[col];
+  const int mode = accumulate ? kStoreAccumulate : kStorePlain;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int64_t row = m0 + wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
     if (row < M) {
       if constexpr (std::is_same<OutT, int32_t>::value) {
-        store_out(C + row * ldc + col, acc[r], accumulate);
+        store_out(C + row * ldc + col, acc[r], mode);
       } else {
         float v = (float)acc[r];
         if (kScale)
           v *= s;
-        store_out(C + row * ldc + col, epi_apply(v, row, col, epi),
-                  accumulate);
+        store_out(C + row * ldc + col, epi_apply(v, row, col, epi), mode);
       }
     }
   }
@@ -1141,7 +1140,7 @@ static hipError_t launch_fast(const MatmulArgs &a) {
                              : dim3(tiles, splits, (unsigned)a.batch);
   const int store_mode =
       a.accumulate ? kStoreAccumulate
-      : !SPLIT && std::is_same<OutT, int32_t>::value &&
+      : !SPLIT &&
               a.m * a.n * a.batch * (int64_t)sizeof(OutT) >= kStoreThroughBytes
           ? kStoreThrough
           : kStorePlain;

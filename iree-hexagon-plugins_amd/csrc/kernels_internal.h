@@ -272,13 +272,15 @@ __device__ __forceinline__ bool epi_plain(const Epi &e) {
 }
 
 // Output store modes (the MFMA kernel's `store_mode` argument): plain store,
-// C += result, or (i32 outputs of unsplit tiles only) a store written through
+// C += result, or (outputs of unsplit tiles only) a store written through
 // past this XCD's L2 (sc1). The kernel does not read its output again, and
 // written through it leaves no dirty lines for the L2 write-back at the end
 // of the kernel: measured 0.7-2.5 % on the int8 4096^3 matmul, whose 64 MiB
-// i32 output otherwise sat dirty in the L2s. The launcher chooses it for i32
-// outputs of at least kStoreThroughBytes; the kernel tests it once, outside
-// its store loop (a per-element three-way test slowed the f16 kernels ~5 %).
+// i32 output otherwise sat dirty in the L2s, and 0.6 % on the f16 4096^3
+// and 2048 x 4096 x 4096 matmuls. The launcher chooses it for outputs of at
+// least kStoreThroughBytes; the kernel tests it once, outside its store loop
+// (a per-element three-way test slowed the f16 kernels ~5 %), and paths that
+// store element by element treat it as a plain store.
 constexpr int kStorePlain = 0;
 constexpr int kStoreAccumulate = 1;
 constexpr int kStoreThrough = 2;
@@ -290,16 +292,17 @@ __device__ __forceinline__ void store_through(int32_t *p, int32_t v) {
                : "memory");
 }
 
-// Plain or accumulating store (`acc`: kStorePlain or kStoreAccumulate).
-__device__ __forceinline__ void store_out(float *p, float v, int acc) {
-  *p = acc ? *p + v : v;
+// Accumulating store when `mode` is kStoreAccumulate, plain otherwise
+// (kStoreThrough included: element stores are not written through).
+__device__ __forceinline__ void store_out(float *p, float v, int mode) {
+  *p = mode == kStoreAccumulate ? *p + v : v;
 }
-__device__ __forceinline__ void store_out(_Float16 *p, float v, int acc) {
-  *p = (_Float16)(acc ? (float)*p + v : v);
+__device__ __forceinline__ void store_out(_Float16 *p, float v, int mode) {
+  *p = (_Float16)(mode == kStoreAccumulate ? (float)*p + v : v);
 }
-__device__ __forceinline__ void store_out(int32_t *p, int v, int acc) {
+__device__ __forceinline__ void store_out(int32_t *p, int v, int mode) {
   // two's-complement wrap, like the i32 adds of the CPU path
-  *p = acc ? (int32_t)((uint32_t)*p + (uint32_t)v) : v;
+  *p = mode == kStoreAccumulate ? (int32_t)((uint32_t)*p + (uint32_t)v) : v;
 }
 
 }  // namespace ihp
