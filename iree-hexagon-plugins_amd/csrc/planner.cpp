@@ -123,7 +123,8 @@ bool gemv_eligible(const iree_mi355x_matmul_desc_t &d) {
   if (d.n % cols != 0)
     return false;
   // one arrival counter per column block of 64 lanes x `cols` columns, per
-  // batch
+  // batch (the full-wave form; the half-wave form's twice as many blocks are
+  // planned only where they fit too)
   const int64_t batch = d.batch > 0 ? d.batch : 1;
   if ((d.n + 64 * cols - 1) / (64 * cols) * batch > kMaxWorkspaceCounters)
     return false;

@@ -990,6 +990,37 @@ def test_matmul_transposed_a(pkg, oracle, dev, m, n, k, bt, out32):
     check_canary(buf, m, n, -7.0)
 
 
+def test_large_outputs_written_through_on_every_store_path(pkg, oracle, dev):
+    """Unsplit tiles with an output of at least 8 MiB store it written
+    through past the L2. The paths that store element by element (a row
+    pitch not a multiple of 16 bytes, a fused epilogue) must treat that
+    mode as a plain store: over a canary-filled buffer, the result equals
+    the product, not the product added to the canary."""
+    g = torch.Generator().manual_seed(23)
+    m = n = 2048  # 8 MiB of f16: the smallest output written through
+    k = 256
+    a = (torch.randn(m, k, generator=g) * 0.5).half()
+    b = (torch.randn(k, n, generator=g) * 0.5).half()
+    ref = oracle.matmul_f16(a.numpy(), b.numpy())
+    ad, bd = a.to(dev), b.to(dev)
+    p = pkg.plan(pkg.make_desc(0, 0, 0, m, n, k, 0))
+    assert p.family == pkg.FAMILY_MFMA and p.splits == 1
+    for pitch in (n, n + 4):  # staged 16-byte rows; odd pitch: per element
+        buf = torch.full((m, pitch), 3.0, dtype=torch.float16, device=dev)
+        y = buf[:, :n]
+        pkg.matmul(ad, bd, y)
+        fp16_ok(oracle, y.cpu().numpy(), ref)
+        if pitch > n:
+            assert bool((buf[:, n:] == 3.0).all())
+    # fused epilogue (bias): per-element stores of the epilogue path
+    bias = (torch.randn(n, generator=g) * 0.5).half()
+    y = torch.full((m, n), 3.0, dtype=torch.float16, device=dev)
+    pkg.batch_matmul(ad, bd, y, bias=bias.to(dev))
+    ref_b = oracle.batch_matmul_f16(a.numpy()[None], b.numpy()[None],
+                                    bias=bias.numpy())[0]
+    fp16_ok(oracle, y.cpu().numpy(), ref_b)
+
+
 def test_matmul_transposed_a_accumulate_and_pitch(pkg, oracle, dev):
     """Accumulate into the init, with A [K, M] a view of a wider buffer
     (lda > M) on the fast path."""
