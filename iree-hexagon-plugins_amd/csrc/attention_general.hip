@@ -1,26 +1,28 @@
-// General attention forward: any head dims (Q/K and V/O may differ, up to
-// 256), an optional additive mask, f16 or f32 output, strided operands and
-// grouped KV heads.
+// General attention forward on the matrix cores: any head dims (Q/K and V/O
+// may differ, up to 256), an optional additive mask, f16 or f32 output,
+// strided operands and grouped KV heads.
 //
 // The reference lowers iree_linalg_ext.attention whatever its head dims,
 // mask or output type, through online attention
 // (CG/Pipelines/LoweringPipelines.cpp:561-595; the online_attention of the
 // pipeline test test/codegen/pipelines/hexagon_lower_executable_target.mlir:
 // 195-233 has a QK head dim of 4, a V head dim of 5, scale 0.5 and an f32
-// accumulator). The
-// MFMA kernel (attention.hip) takes the common shapes; this one takes the
-// rest, with the same semantics:
-//  * a workgroup owns 64 query rows of one (batch, head) (under the causal
-//    mask two such blocks, x and the mirror one, for an even load); four
-//    lanes share a row, each holding a quarter of its Q slice (f16 pairs)
-//    and of its O accumulator (f32) in registers;
-//  * 32-key blocks of K and V are staged in LDS (bounds-checked element
-//    loads, zero past the sequence and head dims); a row's score is its four
-//    lanes' partial dot products summed across the quad;
-//  * scores are scaled, the mask added, causal and out-of-range keys set to
-//    -inf, then an online softmax in f32 rescales the accumulator block by
-//    block; a row that sees no key (fully masked) writes 0, as the
-//    all-masked-row guard of the decomposed softmax does
+// accumulator). The fused kernel (attention.hip) takes the common shapes at
+// full speed; this one takes the rest, with the same semantics:
+//  * a workgroup of 4 waves owns 64 query rows of one (batch, head), 16 per
+//    wave (under the causal mask two such blocks, x and the mirror one, for
+//    an even load); a wave keeps its Q rows as 16x16x32 MFMA fragments
+//    (zero past the head dim) and its O rows as f32 accumulators;
+//  * 64-key blocks of K (row-major) and V (transposed, so that a lane reads
+//    8 consecutive keys of one V column) are staged in LDS, zero past the
+//    sequence and the head dims; 16-byte fills where rows allow them;
+//  * S = Q K^T on v_mfma_f32_16x16x32_f16; scores are scaled, the mask
+//    added, causal and out-of-range keys set to -inf; an online softmax in
+//    f32 (row max and sum over a lane's 16-lane group) rescales O block by
+//    block; the probabilities, rounded to f16, go through the wave's own LDS
+//    tile into the A operand of O += P V;
+//  * a row that sees no key (fully masked) writes 0, as the all-masked-row
+//    guard of the decomposed softmax does
 //    (examples/attention_layer/attention_layer.mlir:80-102).
 #include <type_traits>
 
@@ -31,50 +33,61 @@ namespace ihp {
 
 namespace {
 
-constexpr int kGenThreads = 256;
-constexpr int kGenRows = kGenThreads / 4;  // query rows per workgroup
-constexpr int kGenKeys = 32;               // keys per LDS block
+constexpr int kGenThreads = 256;           // 4 waves
+constexpr int kGenRows = 64;               // query rows per workgroup
+constexpr int kGenKeys = 64;               // keys per LDS block
+constexpr int kGenPad = 8;                 // f16 padding per LDS row
 
-__device__ __forceinline__ float quad_sum(float x) {
+// Max / sum over the 16 lanes of a lane's group (lanes sharing lane / 16):
+// the lanes that hold one query row's scores.
+__device__ __forceinline__ float group16_max(float x) {
+  x = fmaxf(x, __shfl_xor(x, 1, 64));
+  x = fmaxf(x, __shfl_xor(x, 2, 64));
+  x = fmaxf(x, __shfl_xor(x, 4, 64));
+  return fmaxf(x, __shfl_xor(x, 8, 64));
+}
+__device__ __forceinline__ float group16_sum(float x) {
   x += __shfl_xor(x, 1, 64);
   x += __shfl_xor(x, 2, 64);
-  return x;
+  x += __shfl_xor(x, 4, 64);
+  return x + __shfl_xor(x, 8, 64);
 }
-
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ void store_o(f16 *p, float v) { *p = (f16)v; }
 __device__ __forceinline__ void store_o(float *p, float v) { *p = v; }
 
 }  // namespace
 
-// MAXD: the head-dim bucket (a power of two >= both head dims); each of a
-// row's four lanes holds MAXD / 4 elements of Q (as f16 pairs) and of the O
-// accumulator (f32). Scores are v_dot2_f32_f16 sums of those pairs (f16
-// products are exact in f32); PV multiplies the f16 V values into f32 (the
-// widening folds into v_fma_mix).
-template <int MAXD, typename OutT>
+// DP: the head-dim bucket (32, 64, 128 or 256, at least both head dims).
+// MFMA operand layout (v_mfma_f32_16x16x32_f16): lane l supplies row l % 16
+// and the 8 consecutive k of chunk l / 16; the result holds column l % 16 in
+// lane l, row 4 (l / 16) + r in register r. S uses Q as the row operand and
+// K as the column operand (k = head dim); O uses P (k = keys) and V^T.
+template <int DP, typename OutT>
 __global__ __launch_bounds__(kGenThreads) void attention_general_kernel(
     const f16 *__restrict__ Q, const f16 *__restrict__ K,
     const f16 *__restrict__ V, OutT *__restrict__ O,
     const f16 *__restrict__ Mask, AttentionGeneralLayout L) {
-  constexpr int QC = MAXD / 4;
-  constexpr int QP = QC / 2;    // f16 pairs a lane holds
-  constexpr int PAD = 8;        // keeps the four quarters of a row off one bank
-  constexpr int RS = MAXD + PAD;  // LDS row stride (elements; 16-byte rows)
-  constexpr int CPR = MAXD / 8;   // 16-byte chunks of a row
-  static_assert(QC % 2 == 0 && (RS * 2) % 16 == 0, "layout");
-  __shared__ __attribute__((aligned(16))) f16 ks[kGenKeys][RS];
-  __shared__ __attribute__((aligned(16))) f16 vs[kGenKeys][RS];
+  constexpr int QS = DP / 32;            // 32-wide head-dim steps of S
+  constexpr int DB = DP / 16;            // 16-wide column blocks of O
+  constexpr int KR = DP + kGenPad;       // K row in LDS (halves)
+  constexpr int VR = kGenKeys + kGenPad; // V^T row (halves)
+  constexpr int PR = kGenKeys + kGenPad; // P row (halves)
+  constexpr int C8 = DP / 8;             // 16-byte chunks of a head-dim row
+  static_assert(DP % 32 == 0, "head-dim bucket");
+  __shared__ __attribute__((aligned(16))) f16 ks[kGenKeys * KR];
+  __shared__ __attribute__((aligned(16))) f16 vt[DP * VR];
+  __shared__ __attribute__((aligned(16))) f16 ps[kGenThreads / 64][16 * PR];
   __shared__ f16 ms[kGenRows][kGenKeys + 2];  // this block's mask values
 
   const int t = threadIdx.x;
-  const int r = t >> 2, qd = t & 3;
+  const int lane = t & 63, wave = t >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
   const int64_t b = blockIdx.z, h = blockIdx.y, hk = h / L.group;
   const f16 *kp = K + b * L.k[0] + hk * L.k[1];
   const f16 *vp = V + b * L.v[0] + hk * L.v[1];
   const f16 *mbase = Mask ? Mask + b * L.mask[0] + h * L.mask[1] : nullptr;
-  const int d0 = qd * QC;
+  f16 *pw = ps[wave];
   // Under the causal mask row block x costs x + 1 key blocks: a workgroup
   // takes blocks x and nb - 1 - x (one when they coincide), so every
   // workgroup carries about the same keys; otherwise one block each.
@@ -83,57 +96,82 @@ __global__ __launch_bounds__(kGenThreads) void attention_general_kernel(
   const int n_items = L.causal && nb - 1 - x != x ? 2 : 1;
   for (int item = 0; item < n_items; ++item) {
     const int row0 = (item == 0 ? x : nb - 1 - x) * kGenRows;
-    const int i = row0 + r;
-    const bool row_ok = i < L.seq_q;
-    const int ic = row_ok ? i : L.seq_q - 1;
-    const f16 *qp = Q + b * L.q[0] + h * L.q[1] + (int64_t)ic * L.q[2];
+    const int wrow0 = row0 + 16 * wave;  // this wave's first query row
 
-    f16x2 q2[QP];
-    float acc[QC];
+    // Q fragments: row wrow0 + lr, head dims 32 s + 8 lg .. + 7.
+    i32x4 qf[QS];
+    {
+      const int qi = wrow0 + lr;
+      const bool q_ok = qi < L.seq_q;
+      const f16 *qp = Q + b * L.q[0] + h * L.q[1] +
+                      (int64_t)(q_ok ? qi : 0) * L.q[2];
 #pragma unroll
-    for (int c = 0; c < QP; ++c) {
-      const int d = d0 + 2 * c;
-      q2[c] = f16x2{d < L.dqk ? qp[d] : (f16)0,
-                    d + 1 < L.dqk ? qp[d + 1] : (f16)0};
-    }
+      for (int st = 0; st < QS; ++st) {
+        f16x8 v;
 #pragma unroll
-    for (int c = 0; c < QC; ++c)
-      acc[c] = 0.0f;
-    float m_run = -INFINITY, l_run = 0.0f;
-
-    // 16-byte fills when every K (V) row starts 16-byte aligned and its head
-    // dim is a multiple of 8 (decided on the host, uniform); element fills
-    // with bounds checks otherwise. Both write zeros past the sequence and
-    // the head dim.
-    auto fill = [&](f16 (*dst)[RS], const f16 *src, int64_t pitch, int dim,
-                    int vec, int kb0) {
-      if (vec) {
-        for (int e = t; e < kGenKeys * CPR; e += kGenThreads) {
-          const int j = e / CPR, c8 = (e % CPR) * 8;
-          const int key = kb0 + j;
-          i32x4 v = i32x4{0, 0, 0, 0};
-          if (key < L.seq_kv && c8 < dim)
-            v = *(const i32x4 *)(src + (int64_t)key * pitch + c8);
-          *(i32x4 *)&dst[j][c8] = v;
+        for (int e = 0; e < 8; ++e) {
+          const int d = 32 * st + 8 * lg + e;
+          v[e] = q_ok && d < L.dqk ? qp[d] : (f16)0;
         }
-      } else {
-        for (int e = t; e < kGenKeys * MAXD; e += kGenThreads) {
-          const int j = e / MAXD, d = e % MAXD;
-          const int key = kb0 + j;
-          dst[j][d] = key < L.seq_kv && d < dim
-                          ? src[(int64_t)key * pitch + d]
-                          : (f16)0;
-        }
+        qf[st] = __builtin_bit_cast(i32x4, v);
       }
-    };
+    }
+    f32x4 o[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+      o[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // Rows 4 lg + r of the wave: running max (shared by the row's 16 lanes)
+    // and this lane's share of the row sum.
+    float m_run[4], l_run[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      m_run[r] = -INFINITY;
+      l_run[r] = 0.0f;
+    }
 
     // Keys this workgroup's rows may see.
     const int last_row = min(row0 + kGenRows, L.seq_q) - 1;
     const int kv_end = L.causal ? min(L.seq_kv, last_row + 1) : L.seq_kv;
     for (int kb0 = 0; kb0 < kv_end; kb0 += kGenKeys) {
-      __syncthreads();  // the previous block's K, V and mask are no longer read
-      fill(ks, kp, L.k[2], L.dqk, L.vec_k, kb0);
-      fill(vs, vp, L.v[2], L.dv, L.vec_v, kb0);
+      __syncthreads();  // the previous block's K, V, mask and P are read
+      // K block, row-major, and V block, transposed; zeros past the
+      // sequence and the head dims.
+      if (L.vec_k) {
+        for (int e = t; e < kGenKeys * C8; e += kGenThreads) {
+          const int j = e / C8, c8 = (e % C8) * 8, key = kb0 + j;
+          i32x4 v = i32x4{0, 0, 0, 0};
+          if (key < L.seq_kv && c8 < L.dqk)
+            v = *(const i32x4 *)(kp + (int64_t)key * L.k[2] + c8);
+          *(i32x4 *)&ks[j * KR + c8] = v;
+        }
+      } else {
+        for (int e = t; e < kGenKeys * DP; e += kGenThreads) {
+          const int j = e / DP, d = e % DP, key = kb0 + j;
+          ks[j * KR + d] = key < L.seq_kv && d < L.dqk
+                               ? kp[(int64_t)key * L.k[2] + d]
+                               : (f16)0;
+        }
+      }
+      if (L.vec_v) {
+        for (int e = t; e < kGenKeys * C8; e += kGenThreads) {
+          const int j = e % kGenKeys, c8 = (e / kGenKeys) * 8,
+                    key = kb0 + j;
+          i32x4 v = i32x4{0, 0, 0, 0};
+          if (key < L.seq_kv && c8 < L.dv)
+            v = *(const i32x4 *)(vp + (int64_t)key * L.v[2] + c8);
+          const f16x8 hv = __builtin_bit_cast(f16x8, v);
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+            vt[(c8 + u) * VR + j] = hv[u];
+        }
+      } else {
+        for (int e = t; e < kGenKeys * DP; e += kGenThreads) {
+          const int j = e % kGenKeys, d = e / kGenKeys, key = kb0 + j;
+          vt[d * VR + j] = key < L.seq_kv && d < L.dv
+                               ? vp[(int64_t)key * L.v[2] + d]
+                               : (f16)0;
+        }
+      }
       if (mbase) {
         for (int e = t; e < kGenRows * kGenKeys; e += kGenThreads) {
           const int rr = e / kGenKeys, j = e % kGenKeys;
@@ -145,49 +183,81 @@ __global__ __launch_bounds__(kGenThreads) void attention_general_kernel(
         }
       }
       __syncthreads();
-      float s[kGenKeys];
-      float blk_max = -INFINITY;
+
+      // S for the block's four 16-key groups.
+      f32x4 s[4];
 #pragma unroll
-      for (int j = 0; j < kGenKeys; ++j) {
-        float part = 0.0f;
+      for (int kg = 0; kg < 4; ++kg) {
+        s[kg] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        const f16 *krow = &ks[(16 * kg + lr) * KR + 8 * lg];
 #pragma unroll
-        for (int c = 0; c < QP; ++c)
-          part = __builtin_amdgcn_fdot2(
-              q2[c], *(const f16x2 *)&ks[j][d0 + 2 * c], part, false);
-        const float dot = quad_sum(part);
-        const int key = kb0 + j;
-        const bool valid = key < L.seq_kv && (!L.causal || key <= ic);
-        float v = dot * L.scale;
-        if (mbase)
-          v += (float)ms[r][j];
-        s[j] = valid ? v : -INFINITY;
-        blk_max = fmaxf(blk_max, s[j]);
+        for (int st = 0; st < QS; ++st)
+          s[kg] = Mfma16<f16>::mma(qf[st], *(const i32x4 *)(krow + 32 * st),
+                                   s[kg]);
       }
-      const float m_new = fmaxf(m_run, blk_max);
-      if (m_new == -INFINITY)
-        continue;  // every key so far masked: nothing to accumulate
-      const float alpha = m_run == -INFINITY ? 0.0f : __expf(m_run - m_new);
-      l_run *= alpha;
+      // Scale, mask and bounds; this block's row max.
+      float mx[4];
 #pragma unroll
-      for (int c = 0; c < QC; ++c)
-        acc[c] *= alpha;
+      for (int r = 0; r < 4; ++r) {
+        const int qrow = wrow0 + 4 * lg + r;
+        mx[r] = -INFINITY;
 #pragma unroll
-      for (int j = 0; j < kGenKeys; ++j) {
-        const float p = s[j] == -INFINITY ? 0.0f : __expf(s[j] - m_new);
-        l_run += p;
-#pragma unroll
-        for (int c = 0; c < QC; ++c)
-          acc[c] = __builtin_fmaf((float)vs[j][d0 + c], p, acc[c]);
+        for (int kg = 0; kg < 4; ++kg) {
+          const int key = kb0 + 16 * kg + lr;
+          const bool valid = key < L.seq_kv && (!L.causal || key <= qrow);
+          float v = s[kg][r] * L.scale;
+          if (mbase)
+            v += (float)ms[16 * wave + 4 * lg + r][16 * kg + lr];
+          s[kg][r] = valid ? v : -INFINITY;
+          mx[r] = fmaxf(mx[r], s[kg][r]);
+        }
+        mx[r] = group16_max(mx[r]);
       }
-      m_run = m_new;
+      // Online softmax: rescale, probabilities (rounded to f16 once, the
+      // values PV multiplies and the row sum adds) into the wave's P tile.
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float m_new = fmaxf(m_run[r], mx[r]);
+        const float alpha =
+            m_run[r] == -INFINITY ? 0.0f : __expf(m_run[r] - m_new);
+        l_run[r] *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+          o[db][r] *= alpha;
+        m_run[r] = m_new;
+#pragma unroll
+        for (int kg = 0; kg < 4; ++kg) {
+          const float sv = s[kg][r];
+          const f16 p = (f16)(sv == -INFINITY ? 0.0f : __expf(sv - m_new));
+          l_run[r] += (float)p;
+          pw[(4 * lg + r) * PR + 16 * kg + lr] = p;
+        }
+      }
+      // O += P V, 32 keys a step (the wave reads only its own P tile, so
+      // its in-order LDS accesses need no barrier).
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const i32x4 pf = *(const i32x4 *)&pw[lr * PR + 32 * kt + 8 * lg];
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+          o[db] = Mfma16<f16>::mma(
+              pf, *(const i32x4 *)&vt[(16 * db + lr) * VR + 32 * kt + 8 * lg],
+              o[db]);
+      }
     }
-    if (row_ok) {
-      const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-      OutT *op = O + b * L.o[0] + h * L.o[1] + (int64_t)i * L.o[2];
+    // O / l for the wave's rows; columns past the V head dim are padding.
 #pragma unroll
-      for (int c = 0; c < QC; ++c)
-        if (d0 + c < L.dv)
-          store_o(op + d0 + c, acc[c] * inv);
+    for (int r = 0; r < 4; ++r) {
+      const float l = group16_sum(l_run[r]);
+      const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+      const int qrow = wrow0 + 4 * lg + r;
+      if (qrow < L.seq_q) {
+        OutT *op = O + b * L.o[0] + h * L.o[1] + (int64_t)qrow * L.o[2];
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+          if (16 * db + lr < L.dv)
+            store_o(op + 16 * db + lr, o[db][r] * inv);
+      }
     }
   }
 }
@@ -210,8 +280,6 @@ hipError_t launch_general_t(const void *q, const void *k, const void *v,
                        (hipStream_t)stream, qp, kp, vp, op, mp, l);
     return hipGetLastError();
   };
-  if (d <= 16)
-    return run(attention_general_kernel<16, OutT>);
   if (d <= 32)
     return run(attention_general_kernel<32, OutT>);
   if (d <= 64)
@@ -238,12 +306,10 @@ hipError_t launch_attention_general(const void *q, const void *k,
 
 const KernelEntry *attention_general_kernels(int *count) {
   static const KernelEntry all[] = {
-      {"attention_general_d16", (const void *)&attention_general_kernel<16, f16>, kGenThreads, kExportAttention},
       {"attention_general_d32", (const void *)&attention_general_kernel<32, f16>, kGenThreads, kExportAttention},
       {"attention_general_d64", (const void *)&attention_general_kernel<64, f16>, kGenThreads, kExportAttention},
       {"attention_general_d128", (const void *)&attention_general_kernel<128, f16>, kGenThreads, kExportAttention},
       {"attention_general_d256", (const void *)&attention_general_kernel<256, f16>, kGenThreads, kExportAttention},
-      {"attention_general_d16_f32", (const void *)&attention_general_kernel<16, float>, kGenThreads, kExportAttention},
       {"attention_general_d32_f32", (const void *)&attention_general_kernel<32, float>, kGenThreads, kExportAttention},
       {"attention_general_d64_f32", (const void *)&attention_general_kernel<64, float>, kGenThreads, kExportAttention},
       {"attention_general_d128_f32", (const void *)&attention_general_kernel<128, float>, kGenThreads, kExportAttention},

@@ -232,7 +232,7 @@ def test_attention_op_general_region(pkg, oracle, dev, case):
     ref = oracle.attention(q.numpy(), k.numpy(), v.numpy(), scale=m.scale,
                            causal=causal, out_f32=out_f32,
                            mask=None if mask is None else mask.numpy())
-    fp16_ok(oracle, got, ref, bound=2e-5 if out_f32 else 2e-3)
+    fp16_ok(oracle, got, ref, bound=4e-4 if out_f32 else 2e-3)
 
 
 def test_attention_chain_head96_f32(pkg, oracle, dev):
