@@ -95,6 +95,16 @@ def test_attention_general_fully_masked_rows(pkg, oracle, dev):
                        causal=True, scale=0.3)
     assert np.array_equal(o2.cpu().numpy(),
                           np.broadcast_to(v[:, :, :1].numpy(), (1, 2, 70, 32)))
+    # no keys at all: every row sees none and writes 0, over a NaN-filled
+    # output (head dims 24 / 40 take the general kernel)
+    for out_dtype in (torch.float16, torch.float32):
+        o3 = torch.full((1, 2, 70, 40), float("nan"), dtype=out_dtype,
+                        device=dev)
+        pkg.attention(q[..., :24].contiguous().to(dev),
+                      torch.empty(1, 2, 0, 24, dtype=torch.float16, device=dev),
+                      torch.empty(1, 2, 0, 40, dtype=torch.float16, device=dev),
+                      o3)
+        assert (o3.cpu() == 0).all()
 
 
 def test_attention_general_strided_views(pkg, oracle, dev):
