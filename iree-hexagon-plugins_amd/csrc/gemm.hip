@@ -1154,6 +1154,40 @@ static hipError_t launch_fast(const MatmulArgs &a) {
   return hipGetLastError();
 }
 
+// Column split: the head configuration's grid over columns [0, n_head),
+// whole rounds of the chip's CUs, then the tail configuration's grid over
+// the rest, as two launches on the caller's stream. The tail launch sees a
+// plain M x (N - n_head) product: every column-indexed operand (B, C, the
+// W8A16 scale, the epilogue's bias and multiplier) starts n_head columns
+// on, pitches unchanged. Each output element is computed by one tile of
+// either grid in the same K order, so the result is that of the head
+// configuration alone.
+template <typename T, typename OutT, int BMODE, FastLaunchFn HEAD,
+          FastLaunchFn TAIL, int HBM, int HBN, int TBM, int TBN>
+static hipError_t launch_column_split(const MatmulArgs &a) {
+  const int64_t n_head =
+      column_split_head(a.m, a.n, HBM, HBN, TBM, TBN, kColumnSplitCus);
+  if (n_head <= 0 || a.batch != 1)
+    return hipErrorInvalidValue;
+  MatmulArgs h = a;
+  h.n = n_head;
+  const hipError_t e = HEAD(h);
+  if (e != hipSuccess)
+    return e;
+  constexpr int64_t TBB = BMODE == kBW8 ? 1 : (int64_t)sizeof(T);
+  MatmulArgs t = a;
+  t.n = a.n - n_head;
+  t.b = (const char *)a.b + (BMODE == kBTN ? n_head * a.ldb : n_head) * TBB;
+  t.c = (OutT *)a.c + n_head;
+  if (a.scale)
+    t.scale = (const f16 *)a.scale + n_head;
+  if (a.bias)
+    t.bias = (const f16 *)a.bias + n_head;
+  if (a.mul)
+    t.mul = (const f16 *)a.mul + n_head;
+  return TAIL(t);
+}
+
 #define IHP_FAST_CONFIG(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST)           \
   IHP_FAST_CONFIG_X(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST, false, false, 32)
 #define IHP_FAST_CONFIG_16(NAME, MODE, T, OUT, BM, BN, BKB, WM, WN, ST)        \
@@ -1193,6 +1227,39 @@ static hipError_t launch_fast(const MatmulArgs &a) {
    &launch_fast<T, OUT, BM, BN, BKB, WM, WN, ST, MODE, SPLIT, AT, MS>,      \
    MS,                                                                        \
    TABLE}
+
+// A column split of two listed 8-wave configurations (head H*, tail T*,
+// both unsplit, one K stage size), named "<head>+<tail>". Its tile is the
+// head's rows by the tail's columns (the shape's divisibility), its LDS the
+// head's (the larger ring), its kernel entry the head's.
+#define IHP_COLUMN_SPLIT(HEAD, TAIL, MODE, T, OUT, BKB, AT, HBM, HBN, HST,     \
+                         HMS, TBM, TBN, TST, TMS)                             \
+  {HEAD "+" TAIL,                                                             \
+   MODE,                                                                      \
+   false,                                                                     \
+   AT,                                                                        \
+   (const void *)&gemm_lds_kernel<T, OUT, HBM, HBN, BKB, 2, 4, HST, MODE,     \
+                                  false, AT, HMS>,                            \
+   sizeof(T) == 1 ? kElemI8 : kElemF16,                                       \
+   sizeof(OUT) == 4 && sizeof(T) == 2,                                        \
+   HBM,                                                                       \
+   TBN,                                                                       \
+   BKB / (int)sizeof(T),                                                      \
+   512,                                                                       \
+   HST,                                                                       \
+   HST * (HBM * BKB + (MODE == kBTN ? HBN * BKB                               \
+                                    : (BKB / (int)sizeof(T)) * HBN *          \
+                                          (MODE == kBW8 ? 1                   \
+                                                        : (int)sizeof(T)))),  \
+   &launch_column_split<                                                      \
+       T, OUT, MODE,                                                          \
+       &launch_fast<T, OUT, HBM, HBN, BKB, 2, 4, HST, MODE, false, AT, HMS>,  \
+       &launch_fast<T, OUT, TBM, TBN, BKB, 2, 4, TST, MODE, false, AT, TMS>,  \
+       HBM, HBN, TBM, TBN>,                                                   \
+   HMS,                                                                       \
+   0,                                                                         \
+   HEAD,                                                                      \
+   TAIL}
 
 // Every compiled fast-path configuration (none spills registers: the
 // 4-wave 256x256 tiles, 128 x 128 per wave, did and were dropped). The
@@ -1270,6 +1337,21 @@ static const FastConfig kFastConfigs[] = {
     IHP_FAST_CONFIG_S_TABLE("f16_nn_128x128x64_w2x4_s4_sk", kBNN16, f16, f16, 128, 128, 128, 2, 4, 4),
     // And 8 waves of 32x32 on a 64x128 tile (4 stages of 24 KiB).
     IHP_FAST_CONFIG_S_TABLE("f16_nn_64x128x64_w2x4_s4_sk", kBNN16, f16, f16, 64, 128, 128, 2, 4, 4),
+    // Column splits: a ragged last round of 256x256 tiles (C3 M=2048
+    // N=11008: 344 tiles, a round of 256 and one of 88) re-tiled as one
+    // round of half-size tiles after the whole rounds.
+    IHP_COLUMN_SPLIT("f16_nn_256x256x64_w2x4_s2_m16", "f16_nn_256x128x64_w2x4_s2_m16",
+                     kBNN16, f16, f16, 128, false, 256, 256, 2, 16, 256, 128, 2, 16),
+    IHP_COLUMN_SPLIT("f16_tn_256x256x64_w2x4_s2_m16", "f16_tn_256x128x64_w2x4_s2_m16",
+                     kBTN, f16, f16, 128, false, 256, 256, 2, 16, 256, 128, 2, 16),
+    IHP_COLUMN_SPLIT("i8_tn_256x256x128_w2x4_s2_m16", "i8_tn_256x128x128_w2x4_s2_m16",
+                     kBTN, int8_t, int32_t, 128, false, 256, 256, 2, 16, 256, 128, 2, 16),
+    IHP_COLUMN_SPLIT("i8_nn_256x256x128_w2x4_s2_m16", "i8_nn_128x256x128_w2x4_s2",
+                     kBNN8, int8_t, int32_t, 128, false, 256, 256, 2, 16, 128, 256, 2, 32),
+    IHP_COLUMN_SPLIT("w8a16_nn_256x256x64_w2x4_s3", "w8a16_nn_128x256x64_w2x4_s4",
+                     kBW8, f16, f16, 128, false, 256, 256, 3, 32, 128, 256, 4, 32),
+    IHP_COLUMN_SPLIT("f16at_nn_256x256x64_w2x4_s2_m16", "f16at_nn_256x128x64_w2x4_s2",
+                     kBNN16, f16, f16, 128, true, 256, 256, 2, 16, 256, 128, 2, 32),
 };
 
 const FastConfig *fast_configs(int *count) {
@@ -1283,6 +1365,8 @@ const KernelEntry *gemm_kernels(int *count) {
   static const std::vector<KernelEntry> all = [] {
     std::vector<KernelEntry> v;
     for (const FastConfig &c : kFastConfigs) {
+      if (c.head)
+        continue;  // a column split launches two listed kernels
       const uint32_t ex = c.elem == kElemI8 ? kExportMatmulI8
                           : c.b_mode == kBW8
                               ? kExportW8A16

@@ -143,7 +143,34 @@ struct FastConfig {
   FastLaunchFn launch;
   int mfma;      // MFMA shape: 32 (32x32) or 16 (16x16)
   int table_only;  // chosen only by a measured planner entry, never ranked
+  // Column split (unsplit, batch 1): the configuration named `head` runs
+  // over columns [0, n_head) in whole rounds of the chip's CUs, then `tail`
+  // over [n_head, N) as a second grid on the same stream
+  // (column_split_head). Null for a single-grid configuration.
+  const char *head = nullptr;
+  const char *tail = nullptr;
 };
+
+// The CUs a column split's head grid fills in whole rounds (MI355X: 256).
+constexpr int64_t kColumnSplitCus = 256;
+
+// Columns [0, n_head) of an M x N output that head tiles (hbm x hbn) cover
+// in whole rounds of `cus` workgroups, when the remaining columns fit one
+// round of tail tiles (tbm x tbn): 0 where no such split exists (M not
+// tiled by either, the head grid not a whole number of rounds, no
+// remainder, or a remainder of more than one tail round).
+inline int64_t column_split_head(int64_t m, int64_t n, int64_t hbm,
+                                 int64_t hbn, int64_t tbm, int64_t tbn,
+                                 int64_t cus) {
+  if (m <= 0 || m % hbm != 0 || m % tbm != 0 || cus % (m / hbm) != 0)
+    return 0;
+  const int64_t round_cols = cus / (m / hbm) * hbn;
+  const int64_t head = n / round_cols * round_cols;
+  if (head == 0 || head == n || (n - head) % tbn != 0 ||
+      (m / tbm) * ((n - head) / tbn) > cus)
+    return 0;
+  return head;
+}
 
 const FastConfig *fast_configs(int *count);
 

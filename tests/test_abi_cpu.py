@@ -193,7 +193,8 @@ def test_planner_ranking_prefers_least_traffic(pkg):
 
 @pytest.mark.parametrize("m,n,k,flags,want", [
     (2048, 4096, 4096, 0, b"f16_nn_256x128x64_w2x4_s2_m16"),
-    (2048, 11008, 4096, 0, b"f16_nn_256x256x64_w2x4_s2_m16"),
+    (2048, 11008, 4096, 0,
+     b"f16_nn_256x256x64_w2x4_s2_m16+f16_nn_256x128x64_w2x4_s2_m16"),
     (2048, 4096, 11008, 0, b"f16_nn_256x128x64_w2x4_s2_m16"),
     (4096, 4096, 4096, 0, b"f16_nn_256x256x64_w2x4_s2_m16"),
     (4096, 4096, 4096, 8, b"f16at_nn_256x256x64_w2x4_s2_m16"),
@@ -207,6 +208,58 @@ def test_planner_prefers_16x16_on_full_grids(pkg, m, n, k, flags, want):
     p = pkg.plan(pkg.make_desc(F16, I8, F16, 512, 11008, 4096, 0,
                                has_scale=True))
     assert not p.config_name.endswith(b"_m16")
+
+
+COLUMN_SPLITS = [
+    ((F16, F16, F16), 0, b"f16_nn_256x256x64_w2x4_s2_m16",
+     b"f16_nn_256x128x64_w2x4_s2_m16", 8 * 22),
+    ((F16, F16, F16), 1, b"f16_tn_256x256x64_w2x4_s2_m16",
+     b"f16_tn_256x128x64_w2x4_s2_m16", 8 * 22),
+    ((F16, F16, F16), 8, b"f16at_nn_256x256x64_w2x4_s2_m16",
+     b"f16at_nn_256x128x64_w2x4_s2", 8 * 22),
+    ((I8, I8, I32), 1, b"i8_tn_256x256x128_w2x4_s2_m16",
+     b"i8_tn_256x128x128_w2x4_s2_m16", 8 * 22),
+    ((I8, I8, I32), 0, b"i8_nn_256x256x128_w2x4_s2_m16",
+     b"i8_nn_128x256x128_w2x4_s2", 16 * 11),
+]
+
+
+@pytest.mark.parametrize("types,flags,head,tail,tail_wgs", COLUMN_SPLITS)
+def test_planner_column_split(pkg, types, flags, head, tail, tail_wgs):
+    """C3 M=2048 N=11008: 344 tiles of 256x256 end in a round of 88; the
+    plan runs the head over 8192 columns (one round of 256 tiles) and the
+    tail tile over the last 2816 columns, with no workspace."""
+    for k in (4096, 11008):
+        p = pkg.plan(pkg.make_desc(*types, 2048, 11008, k, flags))
+        assert p.config_name == head + b"+" + tail
+        assert p.workgroups == 256 + tail_wgs
+        assert p.splits == 1 and p.workspace_bytes == 0
+    # the head alone where its grid ends in whole rounds, or where the rest
+    # needs more than one round of tail tiles (4096 x 11008: 352 tiles)
+    for m, n in ((4096, 4096), (4096, 11008)):
+        p = pkg.plan(pkg.make_desc(*types, m, n, 4096, flags))
+        assert b"+" not in p.config_name, (m, n)
+    # batched calls, and a chip of another CU count, take no column split
+    p = pkg.plan(pkg.make_desc(*types, 2048, 11008, 4096, flags, batch=2))
+    assert b"+" not in p.config_name
+    d = pkg.make_desc(*types, 2048, 11008, 4096, flags)
+    d.num_cus = 128
+    assert b"+" not in pkg.plan(d).config_name
+
+
+def test_column_split_head_rule_on_the_cpu(pkg):
+    """The composite runs only where its launcher can split: the named
+    configuration with a shape it cannot split is refused before launch."""
+    cfgs = {c.name: c for c in pkg.mfma_configs()}
+    name = "f16_nn_256x256x64_w2x4_s2_m16+f16_nn_256x128x64_w2x4_s2_m16"
+    idx = cfgs[name].index
+    lib = pkg.library()
+    # 4096^3: whole rounds of 256x256 tiles, nothing left for the tail
+    assert lib.iree_mi355x_matmul_mfma_config_workspace_bytes(
+        idx, 0, 4096, 4096, 4096, 0) == 0
+    assert lib.iree_mi355x_matmul_mfma_config_split(
+        idx, 0, 256, 256, None, 256, 4096, 4096, 4096, 4096, 4096, 4096, 0,
+        None, 0, None) == pkg.UNSUPPORTED
 
 
 def test_mfma_config_table(pkg):
@@ -643,7 +696,8 @@ def test_kernel_registry_without_device(pkg):
     names = [k["name"] for k in ks]
     assert len(names) == len(set(names)) == pkg.library().iree_mi355x_kernel_count()
     for cfg in pkg.mfma_configs():
-        assert cfg.name in names
+        # a column split "<head>+<tail>" launches two listed kernels
+        assert all(part in names for part in cfg.name.split("+"))
     for export in pkg.export_names():
         assert any(export in k["exports"] for k in ks), export
     by = {k["name"]: k for k in ks}
@@ -667,7 +721,7 @@ def test_export_attributes_cover_mfma_configs(pkg):
     names = pkg.export_names()
     by_name = {k["name"]: k for k in pkg.kernel_resources(device=False)}
     for cfg in pkg.mfma_configs():
-        for export in by_name[cfg.name]["exports"]:
+        for export in by_name[cfg.name.split("+")[0]]["exports"]:
             attrs = lib.exports.attrs[names.index(export)]
             assert attrs.lds_bytes >= cfg.lds_bytes, (export, cfg.name)
             assert attrs.threads >= cfg.threads, (export, cfg.name)
