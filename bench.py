@@ -928,8 +928,10 @@ def tune_counters(pkg, args):
         return
     work = tempfile.mkdtemp(prefix="tune_counters_")
     for cfg in pkg.mfma_configs():
-        if "_sk" in cfg.name or cfg.tile_m < 128:
-            continue  # split-K tiles are tuned on the skinny shapes
+        if "_sk" in cfg.name or cfg.tile_m < 128 or "+" in cfg.name:
+            # split-K tiles are tuned on the skinny shapes; a column split
+            # ("<head>+<tail>") has no ragged round to fill at 4096^3
+            continue
         out = os.path.join(work, cfg.name)
         cmd = ["timeout", "-s", "KILL", "90", prof, "--pmc", *TUNE_COUNTERS,
                "--kernel-trace", "-d", out, "-o", "p", "--output-format", "csv",
@@ -1186,7 +1188,8 @@ def tune(pkg, inputs, dev, args):
             ms = timed(lambda: pkg.matmul_mfma_config(cfg.index, a, b, c,
                                                       scale=sc),
                        args.steps, args.warmup)
-        except pkg.MI355XError as ex:  # a skinny split-K tile: not 4096^3
+        except pkg.MI355XError as ex:  # a skinny split-K tile or a column
+            # split: neither runs at 4096^3
             print(json.dumps({"config": cfg.name, "skipped": str(ex)}),
                   flush=True)
             continue
