@@ -564,9 +564,10 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
       }
       // A ranked unsplit pick whose grid ends in a ragged round takes the
       // column split headed by it where one applies: one round of
-      // half-size tiles in place of the ragged round measured 8-9 % faster
-      // at 2048 x 11008 (f16 row-major and transposed B, int8 transposed
-      // B; K = 4096 and 11008), with identical results. The cost model's
+      // half-size tiles in place of the ragged round measured 8-11 %
+      // faster at 2048 x 11008 (f16 with either B form or transposed A,
+      // int8 with either B form; K = 4096 and 11008) and 2 % at M = 8192
+      // (f16, W8A16), with identical results. The cost model's
       // aggregate operand feed cannot see that gain (the tail grid fills
       // 176 of the 256 CUs), so the rule is measured, not modeled.
       if (best.index >= 0 && !cfgs[best.index].split_k) {
