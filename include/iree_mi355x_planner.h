@@ -59,7 +59,9 @@ typedef struct iree_mi355x_matmul_plan_t {
   int32_t config_index;  // MFMA: index into the compiled config table
   // "<head>+<tail>": a column split, two launches on the call's stream (the
   // head configuration over whole rounds of the CUs, then the tail over the
-  // remaining columns); `workgroups` counts both grids.
+  // remaining columns); the tail is named without the type and B form
+  // prefix it shares with the head ("f16_nn_256x256x64_w2x4_s2_m16+
+  // 256x128x64_w2x4_s2_m16"); `workgroups` counts both grids.
   char config_name[64];
   int64_t tile_m, tile_n, tile_k;  // workgroup macro-tile (the VTCM tile)
   int64_t lds_bytes;               // LDS per workgroup

@@ -1229,12 +1229,14 @@ static hipError_t launch_column_split(const MatmulArgs &a) {
    TABLE}
 
 // A column split of two listed 8-wave configurations (head H*, tail T*,
-// both unsplit, one K stage size), named "<head>+<tail>". Its tile is the
-// head's rows by the tail's columns (the shape's divisibility), its LDS the
-// head's (the larger ring), its kernel entry the head's.
-#define IHP_COLUMN_SPLIT(HEAD, TAIL, MODE, T, OUT, BKB, AT, HBM, HBN, HST,     \
-                         HMS, TBM, TBN, TST, TMS)                             \
-  {HEAD "+" TAIL,                                                             \
+// both unsplit, one K stage size, one type and B form prefix PRE), named
+// "<head>+<tail without PRE>" (within the plan's 63-character name). Its
+// tile is the head's rows by the tail's columns (the shape's
+// divisibility), its LDS the head's (the larger ring), its kernel entry
+// the head's.
+#define IHP_COLUMN_SPLIT(PRE, HEAD, TAIL, MODE, T, OUT, BKB, AT, HBM, HBN,    \
+                         HST, HMS, TBM, TBN, TST, TMS)                        \
+  {PRE HEAD "+" TAIL,                                                         \
    MODE,                                                                      \
    false,                                                                     \
    AT,                                                                        \
@@ -1258,8 +1260,8 @@ static hipError_t launch_column_split(const MatmulArgs &a) {
        HBM, HBN, TBM, TBN>,                                                   \
    HMS,                                                                       \
    0,                                                                         \
-   HEAD,                                                                      \
-   TAIL}
+   PRE HEAD,                                                                  \
+   PRE TAIL}
 
 // Every compiled fast-path configuration (none spills registers: the
 // 4-wave 256x256 tiles, 128 x 128 per wave, did and were dropped). The
@@ -1284,6 +1286,7 @@ static const FastConfig kFastConfigs[] = {
     IHP_FAST_CONFIG_16("f16_tn_256x256x64_w2x4_s2_m16", kBTN, f16, f16, 256, 256, 128, 2, 4, 2),
     IHP_FAST_CONFIG_16("f16_tn_256x128x64_w2x4_s2_m16", kBTN, f16, f16, 256, 128, 128, 2, 4, 2),
     IHP_FAST_CONFIG_16("f16f32_tn_256x256x64_w2x4_s2_m16", kBTN, f16, float, 256, 256, 128, 2, 4, 2),
+    IHP_FAST_CONFIG_16("f16f32_tn_256x128x64_w2x4_s2_m16", kBTN, f16, float, 256, 128, 128, 2, 4, 2),
     IHP_FAST_CONFIG("f16_nn_256x256x64_w2x4_s2", kBNN16, f16, f16, 256, 256, 128, 2, 4, 2),
     IHP_FAST_CONFIG("f16_nn_256x128x64_w2x4_s2", kBNN16, f16, f16, 256, 128, 128, 2, 4, 2),
     IHP_FAST_CONFIG("f16_nn_128x128x64_w2x2_s4", kBNN16, f16, f16, 128, 128, 128, 2, 2, 4),
@@ -1297,6 +1300,7 @@ static const FastConfig kFastConfigs[] = {
     IHP_FAST_CONFIG_16("f16_nn_256x256x64_w2x4_s2_m16", kBNN16, f16, f16, 256, 256, 128, 2, 4, 2),
     IHP_FAST_CONFIG_16("f16_nn_256x128x64_w2x4_s2_m16", kBNN16, f16, f16, 256, 128, 128, 2, 4, 2),
     IHP_FAST_CONFIG_16("f16f32_nn_256x256x64_w2x4_s2_m16", kBNN16, f16, float, 256, 256, 128, 2, 4, 2),
+    IHP_FAST_CONFIG_16("f16f32_nn_256x128x64_w2x4_s2_m16", kBNN16, f16, float, 256, 128, 128, 2, 4, 2),
     // split-K skinny tiles (M < tile rows allowed; partials in workspace)
     // (measured on M = 16..128 with N, K in {4096, 11008}: 32x128 beats
     // 32x256 / 64x256 at every point, 64x128 is best for some M = 64..128)
@@ -1340,18 +1344,22 @@ static const FastConfig kFastConfigs[] = {
     // Column splits: a ragged last round of 256x256 tiles (C3 M=2048
     // N=11008: 344 tiles, a round of 256 and one of 88) re-tiled as one
     // round of half-size tiles after the whole rounds.
-    IHP_COLUMN_SPLIT("f16_nn_256x256x64_w2x4_s2_m16", "f16_nn_256x128x64_w2x4_s2_m16",
+    IHP_COLUMN_SPLIT("f16_nn_", "256x256x64_w2x4_s2_m16", "256x128x64_w2x4_s2_m16",
                      kBNN16, f16, f16, 128, false, 256, 256, 2, 16, 256, 128, 2, 16),
-    IHP_COLUMN_SPLIT("f16_tn_256x256x64_w2x4_s2_m16", "f16_tn_256x128x64_w2x4_s2_m16",
+    IHP_COLUMN_SPLIT("f16_tn_", "256x256x64_w2x4_s2_m16", "256x128x64_w2x4_s2_m16",
                      kBTN, f16, f16, 128, false, 256, 256, 2, 16, 256, 128, 2, 16),
-    IHP_COLUMN_SPLIT("i8_tn_256x256x128_w2x4_s2_m16", "i8_tn_256x128x128_w2x4_s2_m16",
+    IHP_COLUMN_SPLIT("i8_tn_", "256x256x128_w2x4_s2_m16", "256x128x128_w2x4_s2_m16",
                      kBTN, int8_t, int32_t, 128, false, 256, 256, 2, 16, 256, 128, 2, 16),
-    IHP_COLUMN_SPLIT("i8_nn_256x256x128_w2x4_s2_m16", "i8_nn_128x256x128_w2x4_s2",
+    IHP_COLUMN_SPLIT("i8_nn_", "256x256x128_w2x4_s2_m16", "128x256x128_w2x4_s2",
                      kBNN8, int8_t, int32_t, 128, false, 256, 256, 2, 16, 128, 256, 2, 32),
-    IHP_COLUMN_SPLIT("w8a16_nn_256x256x64_w2x4_s3", "w8a16_nn_128x256x64_w2x4_s4",
+    IHP_COLUMN_SPLIT("w8a16_nn_", "256x256x64_w2x4_s3", "128x256x64_w2x4_s4",
                      kBW8, f16, f16, 128, false, 256, 256, 3, 32, 128, 256, 4, 32),
-    IHP_COLUMN_SPLIT("f16at_nn_256x256x64_w2x4_s2_m16", "f16at_nn_256x128x64_w2x4_s2",
+    IHP_COLUMN_SPLIT("f16at_nn_", "256x256x64_w2x4_s2_m16", "256x128x64_w2x4_s2",
                      kBNN16, f16, f16, 128, true, 256, 256, 2, 16, 256, 128, 2, 32),
+    IHP_COLUMN_SPLIT("f16f32_nn_", "256x256x64_w2x4_s2_m16", "256x128x64_w2x4_s2_m16",
+                     kBNN16, f16, float, 128, false, 256, 256, 2, 16, 256, 128, 2, 16),
+    IHP_COLUMN_SPLIT("f16f32_tn_", "256x256x64_w2x4_s2_m16", "256x128x64_w2x4_s2_m16",
+                     kBTN, f16, float, 128, false, 256, 256, 2, 16, 256, 128, 2, 16),
 };
 
 const FastConfig *fast_configs(int *count) {

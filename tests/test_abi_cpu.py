@@ -194,7 +194,7 @@ def test_planner_ranking_prefers_least_traffic(pkg):
 @pytest.mark.parametrize("m,n,k,flags,want", [
     (2048, 4096, 4096, 0, b"f16_nn_256x128x64_w2x4_s2_m16"),
     (2048, 11008, 4096, 0,
-     b"f16_nn_256x256x64_w2x4_s2_m16+f16_nn_256x128x64_w2x4_s2_m16"),
+     b"f16_nn_256x256x64_w2x4_s2_m16+256x128x64_w2x4_s2_m16"),
     (2048, 4096, 11008, 0, b"f16_nn_256x128x64_w2x4_s2_m16"),
     (4096, 4096, 4096, 0, b"f16_nn_256x256x64_w2x4_s2_m16"),
     (4096, 4096, 4096, 8, b"f16at_nn_256x256x64_w2x4_s2_m16"),
@@ -210,6 +210,25 @@ def test_planner_prefers_16x16_on_full_grids(pkg, m, n, k, flags, want):
     assert not p.config_name.endswith(b"_m16")
 
 
+def column_split_parts(name):
+    """Head and tail configuration names of a column split, named
+    "<head>+<tail without the head's type and B form prefix>"."""
+    head, tail = name.split("+")
+    pre = head[:head.index("_", head.index("_") + 1) + 1]
+    return head, pre + tail
+
+
+def test_config_names_fit_the_plan(pkg):
+    """Every configuration name, column splits included, fits the plan's
+    63-character config_name, and each split's parts are listed."""
+    names = [c.name for c in pkg.mfma_configs()]
+    for name in names:
+        assert len(name) <= 63, name
+        if "+" in name:
+            head, tail = column_split_parts(name)
+            assert head in names and tail in names, name
+
+
 COLUMN_SPLITS = [
     ((F16, F16, F16), 0, b"f16_nn_256x256x64_w2x4_s2_m16",
      b"f16_nn_256x128x64_w2x4_s2_m16", 8 * 22),
@@ -221,6 +240,10 @@ COLUMN_SPLITS = [
      b"i8_tn_256x128x128_w2x4_s2_m16", 8 * 22),
     ((I8, I8, I32), 0, b"i8_nn_256x256x128_w2x4_s2_m16",
      b"i8_nn_128x256x128_w2x4_s2", 16 * 11),
+    ((F16, F16, F32), 0, b"f16f32_nn_256x256x64_w2x4_s2_m16",
+     b"f16f32_nn_256x128x64_w2x4_s2_m16", 8 * 22),
+    ((F16, F16, F32), 1, b"f16f32_tn_256x256x64_w2x4_s2_m16",
+     b"f16f32_tn_256x128x64_w2x4_s2_m16", 8 * 22),
 ]
 
 
@@ -231,7 +254,8 @@ def test_planner_column_split(pkg, types, flags, head, tail, tail_wgs):
     tail tile over the last 2816 columns, with no workspace."""
     for k in (4096, 11008):
         p = pkg.plan(pkg.make_desc(*types, 2048, 11008, k, flags))
-        assert p.config_name == head + b"+" + tail
+        pre = head[:head.index(b"_", head.index(b"_") + 1) + 1]
+        assert p.config_name == head + b"+" + tail[len(pre):]
         assert p.workgroups == 256 + tail_wgs
         assert p.splits == 1 and p.workspace_bytes == 0
     # the head alone where its grid ends in whole rounds, or where the rest
@@ -251,7 +275,7 @@ def test_column_split_head_rule_on_the_cpu(pkg):
     """The composite runs only where its launcher can split: the named
     configuration with a shape it cannot split is refused before launch."""
     cfgs = {c.name: c for c in pkg.mfma_configs()}
-    name = "f16_nn_256x256x64_w2x4_s2_m16+f16_nn_256x128x64_w2x4_s2_m16"
+    name = "f16_nn_256x256x64_w2x4_s2_m16+256x128x64_w2x4_s2_m16"
     idx = cfgs[name].index
     lib = pkg.library()
     # 4096^3: whole rounds of 256x256 tiles, nothing left for the tail
@@ -696,8 +720,9 @@ def test_kernel_registry_without_device(pkg):
     names = [k["name"] for k in ks]
     assert len(names) == len(set(names)) == pkg.library().iree_mi355x_kernel_count()
     for cfg in pkg.mfma_configs():
-        # a column split "<head>+<tail>" launches two listed kernels
-        assert all(part in names for part in cfg.name.split("+"))
+        # a column split launches two listed kernels
+        parts = column_split_parts(cfg.name) if "+" in cfg.name else [cfg.name]
+        assert all(part in names for part in parts)
     for export in pkg.export_names():
         assert any(export in k["exports"] for k in ks), export
     by = {k["name"]: k for k in ks}

@@ -50,6 +50,10 @@ CASES = [
     ("i8_tn", "i8_tn_256x256x128_w2x4_s2_m16", "i8_tn_256x128x128_w2x4_s2_m16"),
     ("i8_nn", "i8_nn_256x256x128_w2x4_s2_m16", "i8_nn_128x256x128_w2x4_s2"),
     ("w8a16", "w8a16_nn_256x256x64_w2x4_s3", "w8a16_nn_128x256x64_w2x4_s4"),
+    ("f16f32_nn", "f16f32_nn_256x256x64_w2x4_s2_m16",
+     "f16f32_nn_256x128x64_w2x4_s2_m16"),
+    ("f16f32_tn", "f16f32_tn_256x256x64_w2x4_s2_m16",
+     "f16f32_tn_256x128x64_w2x4_s2_m16"),
 ]
 
 
@@ -73,15 +77,19 @@ def test_column_split_planned(pkg, oracle, dev, kind, head, tail):
                              0, has_scale=True)
         fill, dt = 3.0, torch.float16
     else:
-        bt, at = kind == "f16_tn", kind == "f16_at"
+        bt, at = kind.endswith("_tn"), kind == "f16_at"
+        f32 = kind.startswith("f16f32")
         a = (torch.randn(*((K, M) if at else (M, K)), generator=g) * 0.5).half()
         b = (torch.randn(*((N, K) if bt else (K, N)), generator=g) * 0.5).half()
-        desc = pkg.make_desc(pkg.ELEM_F16, pkg.ELEM_F16, pkg.ELEM_F16, M, N, K,
+        desc = pkg.make_desc(pkg.ELEM_F16, pkg.ELEM_F16,
+                             pkg.ELEM_F32 if f32 else pkg.ELEM_F16, M, N, K,
                              (pkg.B_TRANSPOSED if bt else 0) |
                              (pkg.A_TRANSPOSED if at else 0))
-        fill, dt = 3.0, torch.float16
+        fill, dt = 3.0, torch.float32 if f32 else torch.float16
     plan = pkg.plan(desc)
-    assert plan.config_name.decode() == f"{head}+{tail}"
+    # "<head>+<tail without the head's type and B form prefix>"
+    pre = head[:head.index("_", head.index("_") + 1) + 1]
+    assert plan.config_name.decode() == f"{head}+{tail[len(pre):]}"
     assert plan.workspace_bytes == 0
     ad, bd = a.to(dev), b.to(dev)
     buf, c = canary_out((M, N), dt, dev, fill)
@@ -96,10 +104,11 @@ def test_column_split_planned(pkg, oracle, dev, kind, head, tail):
         pkg.matmul_mfma_config(cfg_index(pkg, head), ad, bd, solo)
         ref = oracle.matmul_i8(a.numpy(), b.numpy(), b_transposed=bt)
     else:
-        pkg.matmul(ad, bd, c, b_transposed=bt, a_transposed=at)
+        pkg.matmul(ad, bd, c, b_transposed=bt, a_transposed=at,
+                   out_dtype=dt)
         pkg.matmul_mfma_config(cfg_index(pkg, head), ad, bd, solo)
         ref = oracle.matmul_f16(a.numpy(), b.numpy(), b_transposed=bt,
-                                a_transposed=at)
+                                a_transposed=at, out_f32=f32)
     torch.cuda.synchronize()
     check_canary(buf, M, N, fill)
     assert torch.equal(c, solo), "column split differs from its head alone"
