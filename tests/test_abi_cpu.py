@@ -236,6 +236,8 @@ COLUMN_SPLITS = [
      b"f16_tn_256x128x64_w2x4_s2_m16", 8 * 22),
     ((F16, F16, F16), 8, b"f16at_nn_256x256x64_w2x4_s2_m16",
      b"f16at_nn_256x128x64_w2x4_s2", 8 * 22),
+    ((F16, F16, F16), 9, b"f16at_tn_256x256x64_w2x4_s2_m16",
+     b"f16at_tn_256x128x64_w2x4_s2", 8 * 22),
     ((I8, I8, I32), 1, b"i8_tn_256x256x128_w2x4_s2_m16",
      b"i8_tn_256x128x128_w2x4_s2_m16", 8 * 22),
     ((I8, I8, I32), 0, b"i8_nn_256x256x128_w2x4_s2_m16",

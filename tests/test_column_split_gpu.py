@@ -47,6 +47,7 @@ CASES = [
     ("f16_nn", "f16_nn_256x256x64_w2x4_s2_m16", "f16_nn_256x128x64_w2x4_s2_m16"),
     ("f16_tn", "f16_tn_256x256x64_w2x4_s2_m16", "f16_tn_256x128x64_w2x4_s2_m16"),
     ("f16_at", "f16at_nn_256x256x64_w2x4_s2_m16", "f16at_nn_256x128x64_w2x4_s2"),
+    ("f16_at_tn", "f16at_tn_256x256x64_w2x4_s2_m16", "f16at_tn_256x128x64_w2x4_s2"),
     ("i8_tn", "i8_tn_256x256x128_w2x4_s2_m16", "i8_tn_256x128x128_w2x4_s2_m16"),
     ("i8_nn", "i8_nn_256x256x128_w2x4_s2_m16", "i8_nn_128x256x128_w2x4_s2"),
     ("w8a16", "w8a16_nn_256x256x64_w2x4_s3", "w8a16_nn_128x256x64_w2x4_s4"),
@@ -77,7 +78,7 @@ def test_column_split_planned(pkg, oracle, dev, kind, head, tail):
                              0, has_scale=True)
         fill, dt = 3.0, torch.float16
     else:
-        bt, at = kind.endswith("_tn"), kind == "f16_at"
+        bt, at = kind.endswith("_tn"), kind.startswith("f16_at")
         f32 = kind.startswith("f16f32")
         a = (torch.randn(*((K, M) if at else (M, K)), generator=g) * 0.5).half()
         b = (torch.randn(*((N, K) if bt else (K, N)), generator=g) * 0.5).half()
