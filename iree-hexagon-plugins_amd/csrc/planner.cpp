@@ -562,19 +562,20 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
           }
         }
       }
-      // A ranked unsplit pick whose grid ends in a ragged round takes the
-      // column split headed by it where one applies: one round of
-      // half-size tiles in place of the ragged round measured 8-11 %
-      // faster at 2048 x 11008 (f16 with either B form or transposed A,
-      // int8 with either B form; K = 4096 and 11008) and 2 % at M = 8192
-      // (f16, W8A16), with identical results. The cost model's
-      // aggregate operand feed cannot see that gain (the tail grid fills
-      // 176 of the 256 CUs), so the rule is measured, not modeled.
+      // A ranked unsplit pick gives way to the column split of its form
+      // wherever one applies (the shape's 256x256 grid ends in a ragged
+      // round that one round of half-size tiles covers): measured 7-11 %
+      // faster at 2048 x 11008 than the head alone in every form (K = 4096
+      // and 11008) and 2 % at M = 8192; for W8A16 at 2048 x 11008 also 7 %
+      // faster than the ranked 128x256 tile (171.6 against 185.2 us). The
+      // results are identical to the head's alone. The cost model's
+      // aggregate operand feed
+      // cannot see that gain (the tail grid fills 176 of the 256 CUs), so
+      // the rule is measured, not modeled.
       if (best.index >= 0 && !cfgs[best.index].split_k) {
         for (int i = 0; i < count; ++i) {
           Candidate c;
-          if (cfgs[i].head && strcmp(cfgs[i].head, cfgs[best.index].name) == 0 &&
-              cfgs[i].lds_bytes <= budget &&
+          if (cfgs[i].head && cfgs[i].lds_bytes <= budget &&
               evaluate(*d, cfgs[i], i, cus, &c)) {
             best = c;
             break;

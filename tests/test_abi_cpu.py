@@ -266,11 +266,29 @@ def test_planner_column_split(pkg, types, flags, head, tail, tail_wgs):
         p = pkg.plan(pkg.make_desc(*types, m, n, 4096, flags))
         assert b"+" not in p.config_name, (m, n)
     # batched calls, and a chip of another CU count, take no column split
+    # (W8A16 below: the model ranks the 128x256 tile first there, and the
+    # split replaces it too)
     p = pkg.plan(pkg.make_desc(*types, 2048, 11008, 4096, flags, batch=2))
     assert b"+" not in p.config_name
     d = pkg.make_desc(*types, 2048, 11008, 4096, flags)
     d.num_cus = 128
     assert b"+" not in pkg.plan(d).config_name
+
+
+def test_planner_column_split_w8a16(pkg):
+    """W8A16 at 2048 x 11008: the model ranks 688 tiles of 128x256 first;
+    the column split (one round of 256x256, one of 176 128x256 tiles)
+    replaces it."""
+    for k in (4096, 11008):
+        p = pkg.plan(pkg.make_desc(F16, I8, F16, 2048, 11008, k, 0,
+                                   has_scale=True))
+        assert p.config_name == (b"w8a16_nn_256x256x64_w2x4_s3+"
+                                 b"128x256x64_w2x4_s4")
+        assert p.workgroups == 256 + 176 and p.workspace_bytes == 0
+    # C5 M=512 has no whole round of 256x256 tiles: no split
+    p = pkg.plan(pkg.make_desc(F16, I8, F16, 512, 11008, 4096, 0,
+                               has_scale=True))
+    assert b"+" not in p.config_name
 
 
 def test_column_split_head_rule_on_the_cpu(pkg):
