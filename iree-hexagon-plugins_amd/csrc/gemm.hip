@@ -1331,8 +1331,12 @@ static const FastConfig kFastConfigs[] = {
     IHP_FAST_CONFIG_AT("f16at_tn_128x128x64_w2x2_s4", kBTN, f16, f16, 128, 128, 128, 2, 2, 4),
     IHP_FAST_CONFIG_AT("f16f32at_nn_128x128x64_w2x2_s4", kBNN16, f16, float, 128, 128, 128, 2, 2, 4),
     IHP_FAST_CONFIG_AT("f16f32at_tn_128x128x64_w2x2_s4", kBTN, f16, float, 128, 128, 128, 2, 2, 4),
+    IHP_FAST_CONFIG_AT("f16f32at_nn_256x128x64_w2x4_s2", kBNN16, f16, float, 256, 128, 128, 2, 4, 2),
+    IHP_FAST_CONFIG_AT("f16f32at_tn_256x128x64_w2x4_s2", kBTN, f16, float, 256, 128, 128, 2, 4, 2),
     IHP_FAST_CONFIG_AT16("f16at_nn_256x256x64_w2x4_s2_m16", kBNN16, f16, f16, 256, 256, 128, 2, 4, 2),
     IHP_FAST_CONFIG_AT16("f16at_tn_256x256x64_w2x4_s2_m16", kBTN, f16, f16, 256, 256, 128, 2, 4, 2),
+    IHP_FAST_CONFIG_AT16("f16f32at_nn_256x256x64_w2x4_s2_m16", kBNN16, f16, float, 256, 256, 128, 2, 4, 2),
+    IHP_FAST_CONFIG_AT16("f16f32at_tn_256x256x64_w2x4_s2_m16", kBTN, f16, float, 256, 256, 128, 2, 4, 2),
     // 8-wave skinny split-K tile (512-byte weight rows, twice the copies in
     // flight of the 4-wave 32x128 tile per CU). Measured ahead only on the
     // shape the planner's table names it for (slower at M = 16 with N =
@@ -1359,6 +1363,10 @@ static const FastConfig kFastConfigs[] = {
                      kBNN16, f16, f16, 128, true, 256, 256, 2, 16, 256, 128, 2, 32),
     IHP_COLUMN_SPLIT("f16at_tn_", "256x256x64_w2x4_s2_m16", "256x128x64_w2x4_s2",
                      kBTN, f16, f16, 128, true, 256, 256, 2, 16, 256, 128, 2, 32),
+    IHP_COLUMN_SPLIT("f16f32at_nn_", "256x256x64_w2x4_s2_m16", "256x128x64_w2x4_s2",
+                     kBNN16, f16, float, 128, true, 256, 256, 2, 16, 256, 128, 2, 32),
+    IHP_COLUMN_SPLIT("f16f32at_tn_", "256x256x64_w2x4_s2_m16", "256x128x64_w2x4_s2",
+                     kBTN, f16, float, 128, true, 256, 256, 2, 16, 256, 128, 2, 32),
     IHP_COLUMN_SPLIT("f16f32_nn_", "256x256x64_w2x4_s2_m16", "256x128x64_w2x4_s2_m16",
                      kBNN16, f16, float, 128, false, 256, 256, 2, 16, 256, 128, 2, 16),
     IHP_COLUMN_SPLIT("f16f32_tn_", "256x256x64_w2x4_s2_m16", "256x128x64_w2x4_s2_m16",

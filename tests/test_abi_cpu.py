@@ -246,6 +246,10 @@ COLUMN_SPLITS = [
      b"f16f32_nn_256x128x64_w2x4_s2_m16", 8 * 22),
     ((F16, F16, F32), 1, b"f16f32_tn_256x256x64_w2x4_s2_m16",
      b"f16f32_tn_256x128x64_w2x4_s2_m16", 8 * 22),
+    ((F16, F16, F32), 8, b"f16f32at_nn_256x256x64_w2x4_s2_m16",
+     b"f16f32at_nn_256x128x64_w2x4_s2", 8 * 22),
+    ((F16, F16, F32), 9, b"f16f32at_tn_256x256x64_w2x4_s2_m16",
+     b"f16f32at_tn_256x128x64_w2x4_s2", 8 * 22),
 ]
 
 

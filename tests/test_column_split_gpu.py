@@ -55,6 +55,10 @@ CASES = [
      "f16f32_nn_256x128x64_w2x4_s2_m16"),
     ("f16f32_tn", "f16f32_tn_256x256x64_w2x4_s2_m16",
      "f16f32_tn_256x128x64_w2x4_s2_m16"),
+    ("f16f32_at", "f16f32at_nn_256x256x64_w2x4_s2_m16",
+     "f16f32at_nn_256x128x64_w2x4_s2"),
+    ("f16f32_at_tn", "f16f32at_tn_256x256x64_w2x4_s2_m16",
+     "f16f32at_tn_256x128x64_w2x4_s2"),
 ]
 
 
@@ -78,7 +82,7 @@ def test_column_split_planned(pkg, oracle, dev, kind, head, tail):
                              0, has_scale=True)
         fill, dt = 3.0, torch.float16
     else:
-        bt, at = kind.endswith("_tn"), kind.startswith("f16_at")
+        bt, at = kind.endswith("_tn"), "_at" in kind
         f32 = kind.startswith("f16f32")
         a = (torch.randn(*((K, M) if at else (M, K)), generator=g) * 0.5).half()
         b = (torch.randn(*((N, K) if bt else (K, N)), generator=g) * 0.5).half()
