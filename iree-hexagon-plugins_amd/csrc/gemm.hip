@@ -80,25 +80,6 @@ constexpr int nn_swizzle_period() {
                         : (MS == 16 ? 16 : (BMODE == kBNN16 ? 4 : 8));
 }
 
-// 8 int8 weights (two dwords) -> 8 f16, exact: each byte b becomes the f16
-// with exponent 2^10 and mantissa (b ^ 0x80), i.e. 1024 + (b + 128), and
-// subtracting 1152 leaves b. Two v_perm_b32 and one packed f16 subtract per
-// four weights.
-__device__ __forceinline__ i32x4 i8x8_to_f16x8(i32x2 q) {
-  i32x4 out;
-#pragma unroll
-  for (int d = 0; d < 2; ++d) {
-    const unsigned y = (unsigned)q[d] ^ 0x80808080u;
-    const unsigned lo = __builtin_amdgcn_perm(0x64646464u, y, 0x05010400u);
-    const unsigned hi = __builtin_amdgcn_perm(0x64646464u, y, 0x07030602u);
-    const f16x2 bias = {(f16)1152.0f, (f16)1152.0f};
-    out[2 * d] = __builtin_bit_cast(int, __builtin_bit_cast(f16x2, lo) - bias);
-    out[2 * d + 1] =
-        __builtin_bit_cast(int, __builtin_bit_cast(f16x2, hi) - bias);
-  }
-  return out;
-}
-
 template <int OFF>
 __device__ __forceinline__ i32x2 lds_read_tr16_async(const IHP_LDS char *p) {
   static_assert(OFF >= 0 && OFF < 65536, "ds offset range");

@@ -1,6 +1,7 @@
-// HBM-streaming skinny matmul (M <= 4 rows of activations) for B = W [K,N]
-// row-major: the decode-shaped linear (M = 1 GEMV) and the W8A16 linear with
-// int8 weights dequantized in-kernel.
+// HBM-streaming skinny matmul (M <= 4 rows of activations): the
+// decode-shaped linear (M = 1 GEMV) and the W8A16 linear with int8 weights
+// dequantized in-kernel, for B = W [K,N] row-major (the split-K kernel
+// below) and for W [N,K] (the row-dot kernel, further down).
 //
 // In the reference such a dispatch is still an HMX matmul: M is padded to the
 // 32-row HMX tile (CG/Transforms/HexagonConvertMatmulToHmx.cpp:51-70) and the
@@ -297,6 +298,130 @@ __global__ __launch_bounds__(kThreads, 1) void gemv_splitk_kernel(
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Row-dot form for W [N,K] (K contiguous: the B_TRANSPOSED layout, a torch
+// Linear's weight): y[r][n] = sum_k x[r][k] W[n][k]. Workgroup g owns the
+// output columns [g P, g P + P) (P = ceil(N / grid)); its waves take them
+// one at a time from an LDS counter. A wave streams column n's row of W in
+// 16-byte segments (lane l: segments l, l + 64, ...; kBatch loads in flight)
+// against x, staged whole in LDS once per workgroup, and sums the row
+// wave-wide; lane 0 then scales (W8A16), applies the epilogue and stores
+// y[r][n] for each r. K is never split: nothing is published and the launch
+// takes no workspace.
+template <typename WT, int MR, typename OutT>
+__global__ __launch_bounds__(kThreads) void gemv_rowdot_kernel(
+    const f16 *__restrict__ X, const WT *__restrict__ W,
+    const f16 *__restrict__ scale, OutT *__restrict__ Y, int N, int K,
+    int64_t ldx, int64_t ldw, int64_t ldy, int accumulate, int64_t sx,
+    int64_t sw, int64_t sy, Epi epi, int64_t s_mul) {
+  extern __shared__ __attribute__((aligned(16))) f16 xs[];  // [MR][K]
+  __shared__ unsigned next_col;
+  constexpr int EPS = 16 / (int)sizeof(WT);  // weights per 16-byte segment
+  {
+    const int64_t z = blockIdx.z;
+    X += z * sx;
+    W += z * sw;
+    Y += z * sy;
+    epi.mul += z * s_mul;
+  }
+  const int tid = threadIdx.x, lane = tid & 63;
+  // x rows into LDS, 16 bytes a step (K is a multiple of 8 and each x row
+  // 16-byte aligned, both checked by the planner).
+  const int xc = K / 8;
+  for (int i = tid; i < MR * xc; i += kThreads) {
+    const int r = i / xc, c = i - r * xc;
+    *(i32x4 *)(xs + (int64_t)r * K + 8 * c) =
+        *(const i32x4 *)(X + r * ldx + 8 * c);
+  }
+  const int per = (N + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int n_begin = (int)blockIdx.x * per;
+  const int n_end = min(N, n_begin + per);
+  if (tid == 0)
+    next_col = (unsigned)n_begin;
+  __syncthreads();
+  const int segs = K / EPS;  // 16-byte segments of a row of W
+  while (true) {
+    int n = 0;
+    if (lane == 0)
+      n = (int)atomicAdd(&next_col, 1u);
+    n = __builtin_amdgcn_readfirstlane(n);
+    if (n >= n_end)
+      break;
+    const WT *wrow = W + (int64_t)n * ldw;
+    float acc[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r)
+      acc[r] = 0.0f;
+    for (int s0 = 0; s0 < segs; s0 += 64 * kBatch) {
+      i32x4 v[kBatch];
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        const int s = s0 + 64 * b + lane;
+        if (s < segs)
+          v[b] = __builtin_nontemporal_load(
+              (const i32x4 *)(wrow + (int64_t)s * EPS));
+      }
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        const int s = s0 + 64 * b + lane;
+        if (s >= segs)
+          continue;
+        const int k0 = s * EPS;
+        // Vector elements are copied out before __builtin_bit_cast: a bit
+        // cast of a vector element expression reads element 0 whatever the
+        // index (hipcc 7.2).
+        auto dot = [](float a, int w, int x) {
+          return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w),
+                                        __builtin_bit_cast(f16x2, x), a,
+                                        false);
+        };
+        if constexpr (sizeof(WT) == 2) {
+#pragma unroll
+          for (int r = 0; r < MR; ++r) {
+            const i32x4 xv = *(const i32x4 *)(xs + (int64_t)r * K + k0);
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+              const int wd = v[b][d], xd = xv[d];
+              acc[r] = dot(acc[r], wd, xd);
+            }
+          }
+        } else {
+          // 16 int8 weights as 16 exact f16 values, in k order
+          const i32x4 w0 = i8x8_to_f16x8(i32x2{v[b][0], v[b][1]});
+          const i32x4 w1 = i8x8_to_f16x8(i32x2{v[b][2], v[b][3]});
+#pragma unroll
+          for (int r = 0; r < MR; ++r) {
+            const i32x4 x0 = *(const i32x4 *)(xs + (int64_t)r * K + k0);
+            const i32x4 x1 = *(const i32x4 *)(xs + (int64_t)r * K + k0 + 8);
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+              const int wa = w0[d], xa = x0[d], wb = w1[d], xb = x1[d];
+              acc[r] = dot(acc[r], wa, xa);
+              acc[r] = dot(acc[r], wb, xb);
+            }
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+      float t = acc[r];
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1)
+        t += __shfl_xor(t, off);
+      acc[r] = t;
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < MR; ++r) {
+        float t = acc[r];
+        if constexpr (sizeof(WT) == 1)
+          t *= (float)scale[n];
+        store_y(Y + r * ldy + n, epi_apply(t, r, n, epi), accumulate);
+      }
+    }
+  }
+}
+
 // The plan with h lane groups per wave.
 static GemvPlan gemv_plan_h(int64_t n, int64_t k, int cpt, int64_t batch,
                             int h) {
@@ -406,8 +531,43 @@ static hipError_t launch_gemv_rows(const MatmulArgs &a, const void *scale,
   return hipErrorInvalidValue;
 }
 
+template <typename WT, int MR, typename OutT>
+static hipError_t launch_rowdot_t(const MatmulArgs &a, const void *scale) {
+  const dim3 grid((unsigned)rowdot_workgroups(a.n), 1, (unsigned)a.batch);
+  const size_t x_bytes = (size_t)MR * (size_t)a.k * sizeof(f16);
+  hipLaunchKernelGGL((gemv_rowdot_kernel<WT, MR, OutT>), grid, dim3(kThreads),
+                     x_bytes, (hipStream_t)a.stream, (const f16 *)a.a,
+                     (const WT *)a.b, (const f16 *)scale, (OutT *)a.c,
+                     (int)a.n, (int)a.k, a.lda, a.ldb, a.ldc, a.accumulate,
+                     a.sa, a.sb, a.sc, make_epi(a), epi_batch_stride(a));
+  return hipGetLastError();
+}
+
+template <typename WT, typename OutT>
+static hipError_t launch_rowdot(const MatmulArgs &a, const void *scale) {
+  switch (a.m) {
+    case 1:
+      return launch_rowdot_t<WT, 1, OutT>(a, scale);
+    case 2:
+      return launch_rowdot_t<WT, 2, OutT>(a, scale);
+    case 3:
+      return launch_rowdot_t<WT, 3, OutT>(a, scale);
+    case 4:
+      return launch_rowdot_t<WT, 4, OutT>(a, scale);
+  }
+  return hipErrorInvalidValue;
+}
+
 hipError_t launch_gemv(const MatmulArgs &a, int w_bytes, const void *scale,
                        int out_f32, void *workspace) {
+  if (a.b_transposed) {
+    if (a.m * a.k * (int64_t)sizeof(f16) > kRowdotMaxXBytes || a.k % 16 != 0)
+      return hipErrorInvalidValue;
+    if (w_bytes == 2)
+      return out_f32 ? launch_rowdot<f16, float>(a, nullptr)
+                     : launch_rowdot<f16, f16>(a, nullptr);
+    return launch_rowdot<int8_t, f16>(a, scale);
+  }
   const GemvPlan p = gemv_plan(a.m, a.n, a.k, w_bytes, a.batch);
   if (w_bytes == 2)
     return out_f32 ? launch_gemv_rows<f16, float>(a, nullptr, workspace, p)
@@ -420,7 +580,8 @@ hipError_t launch_gemv(const MatmulArgs &a, int w_bytes, const void *scale,
 namespace ihp {
 
 // Every GEMV kernel: rows 1..4 for f16 weights (f16 / f32 out) and W8A16,
-// in the full-wave and the half-wave (_h2) form.
+// in the full-wave and the half-wave (_h2) form for W [K,N], and the
+// row-dot form for W [N,K].
 const KernelEntry *gemv_kernels(int *count) {
   const uint32_t f16x = kExportMatmulF16 | kExportBatchMatmulF16;
   static const KernelEntry all[] = {
@@ -448,6 +609,18 @@ const KernelEntry *gemv_kernels(int *count) {
       {"gemv_w8a16_r2_h2", (const void *)&gemv_splitk_kernel<int8_t, 2, f16, 2>, kThreads, kExportW8A16},
       {"gemv_w8a16_r3_h2", (const void *)&gemv_splitk_kernel<int8_t, 3, f16, 2>, kThreads, kExportW8A16},
       {"gemv_w8a16_r4_h2", (const void *)&gemv_splitk_kernel<int8_t, 4, f16, 2>, kThreads, kExportW8A16},
+      {"gemv_rowdot_f16_r1", (const void *)&gemv_rowdot_kernel<f16, 1, f16>, kThreads, f16x},
+      {"gemv_rowdot_f16_r2", (const void *)&gemv_rowdot_kernel<f16, 2, f16>, kThreads, f16x},
+      {"gemv_rowdot_f16_r3", (const void *)&gemv_rowdot_kernel<f16, 3, f16>, kThreads, f16x},
+      {"gemv_rowdot_f16_r4", (const void *)&gemv_rowdot_kernel<f16, 4, f16>, kThreads, f16x},
+      {"gemv_rowdot_f16f32_r1", (const void *)&gemv_rowdot_kernel<f16, 1, float>, kThreads, f16x},
+      {"gemv_rowdot_f16f32_r2", (const void *)&gemv_rowdot_kernel<f16, 2, float>, kThreads, f16x},
+      {"gemv_rowdot_f16f32_r3", (const void *)&gemv_rowdot_kernel<f16, 3, float>, kThreads, f16x},
+      {"gemv_rowdot_f16f32_r4", (const void *)&gemv_rowdot_kernel<f16, 4, float>, kThreads, f16x},
+      {"gemv_rowdot_w8a16_r1", (const void *)&gemv_rowdot_kernel<int8_t, 1, f16>, kThreads, kExportW8A16},
+      {"gemv_rowdot_w8a16_r2", (const void *)&gemv_rowdot_kernel<int8_t, 2, f16>, kThreads, kExportW8A16},
+      {"gemv_rowdot_w8a16_r3", (const void *)&gemv_rowdot_kernel<int8_t, 3, f16>, kThreads, kExportW8A16},
+      {"gemv_rowdot_w8a16_r4", (const void *)&gemv_rowdot_kernel<int8_t, 4, f16>, kThreads, kExportW8A16},
   };
   *count = (int)(sizeof(all) / sizeof(all[0]));
   return all;

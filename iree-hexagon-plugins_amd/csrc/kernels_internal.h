@@ -201,8 +201,21 @@ GemvPlan gemv_plan(int64_t m, int64_t n, int64_t k, int w_bytes,
 size_t gemv_workspace_bytes(int64_t m, int64_t n, int64_t k, int w_bytes,
                             int64_t batch = 1);
 // w_bytes = 2: f16 weights (scale == NULL); 1: int8 weights with f16 scale.
+// With a.b_transposed (W [N,K], K contiguous) the row-dot kernel runs: no K
+// split, no workspace.
 hipError_t launch_gemv(const MatmulArgs &a, int w_bytes, const void *scale,
                        int out_f32, void *workspace);
+
+// Row-dot form (W [N,K]): x rows staged whole in LDS, at most this many
+// bytes of them (m x k x 2), so that a workgroup's LDS (x and the column
+// counter) stays under 64 KiB; workgroups per launch (columns dealt in equal
+// runs, taken by the waves one at a time).
+constexpr int64_t kRowdotMaxXBytes = 60 * 1024;
+constexpr int kRowdotMaxWgs = 512;
+inline int64_t rowdot_workgroups(int64_t n) {
+  const int64_t w = (n + 7) / 8;
+  return w < kRowdotMaxWgs ? w : kRowdotMaxWgs;
+}
 
 // Where attention's operands live: element strides of the batch, head and
 // row dimensions of each (d is contiguous), and the query heads that share

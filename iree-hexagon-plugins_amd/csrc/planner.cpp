@@ -115,10 +115,18 @@ bool types_supported(const iree_mi355x_matmul_desc_t &d) {
 
 bool gemv_eligible(const iree_mi355x_matmul_desc_t &d) {
   if (d.m < 1 || d.m > kGemvMaxRows || d.k < 1 ||
-      (d.flags & (IREE_MI355X_MATMUL_B_TRANSPOSED |
-                  IREE_MI355X_MATMUL_A_TRANSPOSED)) ||
-      !d.b_aligned16)
+      (d.flags & IREE_MI355X_MATMUL_A_TRANSPOSED) || !d.b_aligned16)
     return false;
+  if (d.flags & IREE_MI355X_MATMUL_B_TRANSPOSED) {
+    // Row-dot form (W [N,K]): whole 16-byte segments of each row of W (K a
+    // multiple of 16 covers f16 and int8), x rows copied into LDS in
+    // 16-byte pieces, all of x within the LDS it stages in. int8 weights
+    // only in the W8A16 form.
+    if (d.k % 16 != 0 || !d.a_aligned16 ||
+        d.m * d.k * 2 > kRowdotMaxXBytes)
+      return false;
+    return d.b_elem == IREE_MI355X_ELEM_I8 ? d.has_scale != 0 : true;
+  }
   const int cols = 16 / elem_bytes(d.b_elem);
   if (d.n % cols != 0)
     return false;
@@ -486,6 +494,27 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
       d->lds_budget_bytes > 0 ? d->lds_budget_bytes : kDefaultLdsBudget;
   const int64_t cus = d->num_cus > 0 ? d->num_cus : kDefaultCus;
 
+  if (family == IREE_MI355X_FAMILY_GEMV &&
+      (d->flags & IREE_MI355X_MATMUL_B_TRANSPOSED)) {
+    // Row-dot form: one wave per output column at a time, K whole.
+    const int wb = elem_bytes(d->b_elem);
+    const int64_t batch = d->batch > 0 ? d->batch : 1;
+    snprintf(plan->config_name, sizeof(plan->config_name),
+             "gemv_rowdot_%s_r%lld",
+             wb == 1 ? "w8a16"
+                     : (d->c_elem == IREE_MI355X_ELEM_F32 ? "f16f32" : "f16"),
+             (long long)d->m);
+    plan->tile_m = d->m;
+    plan->tile_n = 1;
+    plan->tile_k = d->k;
+    plan->lds_bytes = d->m * d->k * 2;
+    plan->workgroups = rowdot_workgroups(d->n) * batch;
+    plan->threads = kGemvThreads;
+    plan->splits = 1;
+    plan->workspace_bytes = 0;
+    plan->traffic_bytes = batch * (d->n * d->k * wb + d->m * d->k * 2);
+    return IREE_MI355X_OK;
+  }
   if (family == IREE_MI355X_FAMILY_GEMV) {
     const int wb = elem_bytes(d->b_elem);
     const int64_t batch = d->batch > 0 ? d->batch : 1;

@@ -310,6 +310,34 @@ def test_column_split_head_rule_on_the_cpu(pkg):
         None, 0, None) == pkg.UNSUPPORTED
 
 
+def test_planner_rowdot_gemv(pkg):
+    """Weights [N, K] (B_TRANSPOSED) with M <= 4: the row-dot GEMV, no
+    workspace, where whole 16-byte segments tile K and x fits the LDS it is
+    staged in (M x K x 2 <= 60 KiB); otherwise the MFMA or general path."""
+    for (a, b, c), kw, tag in (((F16, F16, F16), {}, b"f16"),
+                               ((F16, F16, F32), {}, b"f16f32"),
+                               ((F16, I8, F16), {"has_scale": True},
+                                b"w8a16")):
+        for m, n, k in ((1, 11008, 4096), (4, 11008, 4096), (2, 4096, 11008),
+                        (1, 1000, 1040)):
+            p = pkg.plan(pkg.make_desc(a, b, c, m, n, k, pkg.B_TRANSPOSED,
+                                       **kw))
+            assert p.family == pkg.FAMILY_GEMV
+            assert p.config_name == b"gemv_rowdot_" + tag + b"_r%d" % m
+            assert p.workspace_bytes == 0 and p.splits == 1
+            assert p.workgroups == min((n + 7) // 8, 512)
+        for m, n, k in ((3, 4096, 11008),   # x 66 KB: past the LDS it uses
+                        (1, 1000, 1000),    # K not a multiple of 16
+                        (5, 4096, 4096)):   # more than 4 rows
+            p = pkg.plan(pkg.make_desc(a, b, c, m, n, k, pkg.B_TRANSPOSED,
+                                       **kw))
+            assert b"rowdot" not in p.config_name, (m, n, k)
+    # x rows must be 16-byte aligned to be staged
+    d = pkg.make_desc(F16, F16, F16, 1, 4096, 4096, pkg.B_TRANSPOSED)
+    d.a_aligned16 = 0
+    assert b"rowdot" not in pkg.plan(d).config_name
+
+
 def test_mfma_config_table(pkg):
     cfgs = pkg.mfma_configs()
     assert len(cfgs) >= 8
