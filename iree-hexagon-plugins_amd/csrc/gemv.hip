@@ -561,12 +561,28 @@ static hipError_t launch_rowdot(const MatmulArgs &a, const void *scale) {
 hipError_t launch_gemv(const MatmulArgs &a, int w_bytes, const void *scale,
                        int out_f32, void *workspace) {
   if (a.b_transposed) {
-    if (a.m * a.k * (int64_t)sizeof(f16) > kRowdotMaxXBytes || a.k % 16 != 0)
+    const int64_t rows = a.m < kGemvMaxRows ? a.m : kGemvMaxRows;
+    if (rows * a.k * (int64_t)sizeof(f16) > kRowdotMaxXBytes ||
+        a.k % 16 != 0 ||
+        a.m > (w_bytes == 1 ? kRowdotMaxRowsW8A16 : kGemvMaxRows))
       return hipErrorInvalidValue;
     if (w_bytes == 2)
       return out_f32 ? launch_rowdot<f16, float>(a, nullptr)
                      : launch_rowdot<f16, f16>(a, nullptr);
-    return launch_rowdot<int8_t, f16>(a, scale);
+    // W8A16: blocks of at most 4 rows of x (and of y and the multiplier),
+    // one launch each
+    for (int64_t r0 = 0; r0 < a.m; r0 += kGemvMaxRows) {
+      MatmulArgs b = a;
+      b.m = a.m - r0 < kGemvMaxRows ? a.m - r0 : kGemvMaxRows;
+      b.a = (const f16 *)a.a + r0 * a.lda;
+      b.c = (f16 *)a.c + r0 * a.ldc;
+      if (a.mul)
+        b.mul = (const f16 *)a.mul + r0 * a.ld_mul;
+      const hipError_t e = launch_rowdot<int8_t, f16>(b, scale);
+      if (e != hipSuccess)
+        return e;
+    }
+    return hipSuccess;
   }
   const GemvPlan p = gemv_plan(a.m, a.n, a.k, w_bytes, a.batch);
   if (w_bytes == 2)

@@ -211,6 +211,10 @@ hipError_t launch_gemv(const MatmulArgs &a, int w_bytes, const void *scale,
 // counter) stays under 64 KiB; workgroups per launch (columns dealt in equal
 // runs, taken by the waves one at a time).
 constexpr int64_t kRowdotMaxXBytes = 60 * 1024;
+// W8A16 with W [N,K] and 4 < M <= this runs as ceil(M / 4) row-dot launches
+// of at most 4 rows of x each (each re-reads W): the MFMA tiles take int8
+// weights only as [K,N], and the general kernel is several times slower.
+constexpr int kRowdotMaxRowsW8A16 = 16;
 constexpr int kRowdotMaxWgs = 512;
 inline int64_t rowdot_workgroups(int64_t n) {
   const int64_t w = (n + 7) / 8;

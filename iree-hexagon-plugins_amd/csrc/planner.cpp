@@ -114,19 +114,24 @@ bool types_supported(const iree_mi355x_matmul_desc_t &d) {
 }
 
 bool gemv_eligible(const iree_mi355x_matmul_desc_t &d) {
-  if (d.m < 1 || d.m > kGemvMaxRows || d.k < 1 ||
-      (d.flags & IREE_MI355X_MATMUL_A_TRANSPOSED) || !d.b_aligned16)
+  if (d.m < 1 || d.k < 1 || (d.flags & IREE_MI355X_MATMUL_A_TRANSPOSED) ||
+      !d.b_aligned16)
     return false;
   if (d.flags & IREE_MI355X_MATMUL_B_TRANSPOSED) {
     // Row-dot form (W [N,K]): whole 16-byte segments of each row of W (K a
     // multiple of 16 covers f16 and int8), x rows copied into LDS in
-    // 16-byte pieces, all of x within the LDS it stages in. int8 weights
-    // only in the W8A16 form.
-    if (d.k % 16 != 0 || !d.a_aligned16 ||
-        d.m * d.k * 2 > kRowdotMaxXBytes)
+    // 16-byte pieces, a launch's x (at most 4 rows) within the LDS it
+    // stages in. int8 weights only in the W8A16 form, which also takes up
+    // to kRowdotMaxRowsW8A16 rows as launches of 4.
+    const bool w8 = d.b_elem == IREE_MI355X_ELEM_I8;
+    const int64_t rows = d.m < kGemvMaxRows ? d.m : kGemvMaxRows;
+    if (d.m > (w8 ? kRowdotMaxRowsW8A16 : kGemvMaxRows) || d.k % 16 != 0 ||
+        !d.a_aligned16 || rows * d.k * 2 > kRowdotMaxXBytes)
       return false;
-    return d.b_elem == IREE_MI355X_ELEM_I8 ? d.has_scale != 0 : true;
+    return w8 ? d.has_scale != 0 : true;
   }
+  if (d.m > kGemvMaxRows)
+    return false;
   const int cols = 16 / elem_bytes(d.b_elem);
   if (d.n % cols != 0)
     return false;
@@ -507,12 +512,14 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
     plan->tile_m = d->m;
     plan->tile_n = 1;
     plan->tile_k = d->k;
-    plan->lds_bytes = d->m * d->k * 2;
-    plan->workgroups = rowdot_workgroups(d->n) * batch;
+    const int64_t launches = (d->m + kGemvMaxRows - 1) / kGemvMaxRows;
+    plan->lds_bytes = (d->m < kGemvMaxRows ? d->m : kGemvMaxRows) * d->k * 2;
+    plan->workgroups = rowdot_workgroups(d->n) * batch * launches;
     plan->threads = kGemvThreads;
     plan->splits = 1;
     plan->workspace_bytes = 0;
-    plan->traffic_bytes = batch * (d->n * d->k * wb + d->m * d->k * 2);
+    plan->traffic_bytes =
+        batch * (launches * d->n * d->k * wb + d->m * d->k * 2);
     return IREE_MI355X_OK;
   }
   if (family == IREE_MI355X_FAMILY_GEMV) {

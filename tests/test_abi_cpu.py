@@ -328,10 +328,17 @@ def test_planner_rowdot_gemv(pkg):
             assert p.workgroups == min((n + 7) // 8, 512)
         for m, n, k in ((3, 4096, 11008),   # x 66 KB: past the LDS it uses
                         (1, 1000, 1000),    # K not a multiple of 16
-                        (5, 4096, 4096)):   # more than 4 rows
+                        (5 if tag != b"w8a16" else 17, 4096, 4096)):
             p = pkg.plan(pkg.make_desc(a, b, c, m, n, k, pkg.B_TRANSPOSED,
                                        **kw))
             assert b"rowdot" not in p.config_name, (m, n, k)
+    # W8A16 up to 16 rows: launches of at most 4 rows each
+    for m in (5, 8, 16):
+        p = pkg.plan(pkg.make_desc(F16, I8, F16, m, 11008, 4096,
+                                   pkg.B_TRANSPOSED, has_scale=True))
+        assert p.config_name == b"gemv_rowdot_w8a16_r%d" % m
+        assert p.workgroups == 512 * ((m + 3) // 4)
+        assert p.lds_bytes == 4 * 4096 * 2
     # x rows must be 16-byte aligned to be staged
     d = pkg.make_desc(F16, F16, F16, 1, 4096, 4096, pkg.B_TRANSPOSED)
     d.a_aligned16 = 0

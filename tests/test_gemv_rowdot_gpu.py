@@ -1,6 +1,7 @@
-"""Row-dot GEMV: skinny matmuls (M <= 4) with the weights stored [N, K]
-(B_TRANSPOSED, a torch Linear's layout), f16 and W8A16 (csrc/gemv.hip
-gemv_rowdot_kernel). One wave reduces a whole row of W, so K is never split.
+"""Row-dot GEMV: skinny matmuls (M <= 4; W8A16 up to 16 as launches of 4
+rows) with the weights stored [N, K] (B_TRANSPOSED, a torch Linear's
+layout), f16 and W8A16 (csrc/gemv.hip gemv_rowdot_kernel). One wave reduces
+a whole row of W, so K is never split.
 
 Bars: f16 and f32 results max|y - y_cpu| / max|y_cpu| <= 2e-3 (the
 BASELINE fp16 rule) against the oracle; nothing outside the output view is
@@ -63,6 +64,28 @@ def test_rowdot_planned(pkg, oracle, dev, kind, m, n, k):
         pkg.matmul(xd, wd, y, b_transposed=True, out_dtype=dt)
         ref = oracle.matmul_f16(x.numpy(), w.numpy(), b_transposed=True,
                                 out_f32=dt == torch.float32)
+    torch.cuda.synchronize()
+    check_canary(buf, m, n, 3.0)
+    err = oracle.fp16_parity(y.cpu().numpy(), ref)
+    assert err <= FP16_BOUND, f"fp16 parity {err:.3e}"
+
+
+@pytest.mark.parametrize("m", [5, 8, 13, 16])
+def test_rowdot_w8a16_row_blocks(pkg, oracle, dev, m):
+    """W8A16 with W [N, K] and 4 < M <= 16: launches of at most 4 rows of x
+    and y each."""
+    n, k = 2048, 4096
+    print(f"rowdot w8a16 blocks m={m}", flush=True)
+    g = torch.Generator().manual_seed(40 + m)
+    x = (torch.randn(m, k, generator=g) * 0.5).half()
+    w = torch.randint(-128, 128, (n, k), generator=g).to(torch.int8)
+    sc = (torch.rand(n, generator=g) * 0.019 + 0.001).half()
+    d = pkg.make_desc(pkg.ELEM_F16, pkg.ELEM_I8, pkg.ELEM_F16, m, n, k,
+                      pkg.B_TRANSPOSED, has_scale=True)
+    assert pkg.plan(d).config_name.decode() == f"gemv_rowdot_w8a16_r{m}"
+    buf, y = canary_out((m, n), torch.float16, dev, 3.0)
+    pkg.quantized_matmul(x.to(dev), w.to(dev), sc.to(dev), y, w_transposed=True)
+    ref = oracle.w8a16(x.numpy(), w.numpy(), sc.numpy(), w_transposed=True)
     torch.cuda.synchronize()
     check_canary(buf, m, n, 3.0)
     err = oracle.fp16_parity(y.cpu().numpy(), ref)
