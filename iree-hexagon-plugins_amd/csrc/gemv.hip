@@ -555,25 +555,38 @@ static hipError_t launch_rowdot(const MatmulArgs &a, const void *scale) {
     case 4:
       return launch_rowdot_t<WT, 4, OutT>(a, scale);
   }
+  if constexpr (sizeof(WT) == 1) {  // W8A16 launches of up to 8 rows
+    switch (a.m) {
+      case 5:
+        return launch_rowdot_t<WT, 5, OutT>(a, scale);
+      case 6:
+        return launch_rowdot_t<WT, 6, OutT>(a, scale);
+      case 7:
+        return launch_rowdot_t<WT, 7, OutT>(a, scale);
+      case 8:
+        return launch_rowdot_t<WT, 8, OutT>(a, scale);
+    }
+  }
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemv(const MatmulArgs &a, int w_bytes, const void *scale,
                        int out_f32, void *workspace) {
   if (a.b_transposed) {
-    const int64_t rows = a.m < kGemvMaxRows ? a.m : kGemvMaxRows;
-    if (rows * a.k * (int64_t)sizeof(f16) > kRowdotMaxXBytes ||
+    const int64_t rows =
+        w_bytes == 1 ? rowdot_w8a16_rows(a.m, a.k) : a.m;
+    if (rows < 1 || rows * a.k * (int64_t)sizeof(f16) > kRowdotMaxXBytes ||
         a.k % 16 != 0 ||
         a.m > (w_bytes == 1 ? kRowdotMaxRowsW8A16 : kGemvMaxRows))
       return hipErrorInvalidValue;
     if (w_bytes == 2)
       return out_f32 ? launch_rowdot<f16, float>(a, nullptr)
                      : launch_rowdot<f16, f16>(a, nullptr);
-    // W8A16: blocks of at most 4 rows of x (and of y and the multiplier),
-    // one launch each
-    for (int64_t r0 = 0; r0 < a.m; r0 += kGemvMaxRows) {
+    // W8A16: blocks of `rows` rows of x (and of y and the multiplier), one
+    // launch each
+    for (int64_t r0 = 0; r0 < a.m; r0 += rows) {
       MatmulArgs b = a;
-      b.m = a.m - r0 < kGemvMaxRows ? a.m - r0 : kGemvMaxRows;
+      b.m = a.m - r0 < rows ? a.m - r0 : rows;
       b.a = (const f16 *)a.a + r0 * a.lda;
       b.c = (f16 *)a.c + r0 * a.ldc;
       if (a.mul)
@@ -637,6 +650,10 @@ const KernelEntry *gemv_kernels(int *count) {
       {"gemv_rowdot_w8a16_r2", (const void *)&gemv_rowdot_kernel<int8_t, 2, f16>, kThreads, kExportW8A16},
       {"gemv_rowdot_w8a16_r3", (const void *)&gemv_rowdot_kernel<int8_t, 3, f16>, kThreads, kExportW8A16},
       {"gemv_rowdot_w8a16_r4", (const void *)&gemv_rowdot_kernel<int8_t, 4, f16>, kThreads, kExportW8A16},
+      {"gemv_rowdot_w8a16_r5", (const void *)&gemv_rowdot_kernel<int8_t, 5, f16>, kThreads, kExportW8A16},
+      {"gemv_rowdot_w8a16_r6", (const void *)&gemv_rowdot_kernel<int8_t, 6, f16>, kThreads, kExportW8A16},
+      {"gemv_rowdot_w8a16_r7", (const void *)&gemv_rowdot_kernel<int8_t, 7, f16>, kThreads, kExportW8A16},
+      {"gemv_rowdot_w8a16_r8", (const void *)&gemv_rowdot_kernel<int8_t, 8, f16>, kThreads, kExportW8A16},
   };
   *count = (int)(sizeof(all) / sizeof(all[0]));
   return all;

@@ -211,10 +211,22 @@ hipError_t launch_gemv(const MatmulArgs &a, int w_bytes, const void *scale,
 // counter) stays under 64 KiB; workgroups per launch (columns dealt in equal
 // runs, taken by the waves one at a time).
 constexpr int64_t kRowdotMaxXBytes = 60 * 1024;
-// W8A16 with W [N,K] and 4 < M <= this runs as ceil(M / 4) row-dot launches
-// of at most 4 rows of x each (each re-reads W): the MFMA tiles take int8
-// weights only as [K,N], and the general kernel is several times slower.
+// W8A16 with W [N,K] and M <= this runs as row-dot launches of at most 8
+// rows of x each (each re-reads W): the MFMA tiles take int8 weights only as
+// [K,N], and the general kernel is several times slower.
 constexpr int kRowdotMaxRowsW8A16 = 16;
+// Rows of x per W8A16 row-dot launch: as many as the LDS limit allows (at
+// most 8), dealt evenly over the launches M needs; 0 if one row of x does
+// not fit.
+inline int rowdot_w8a16_rows(int64_t m, int64_t k) {
+  int64_t cap = k > 0 ? kRowdotMaxXBytes / (2 * k) : 0;
+  if (cap > 8)
+    cap = 8;
+  if (cap < 1 || m < 1)
+    return 0;
+  const int64_t launches = (m + cap - 1) / cap;
+  return (int)((m + launches - 1) / launches);
+}
 constexpr int kRowdotMaxWgs = 512;
 inline int64_t rowdot_workgroups(int64_t n) {
   const int64_t w = (n + 7) / 8;

@@ -124,9 +124,9 @@ bool gemv_eligible(const iree_mi355x_matmul_desc_t &d) {
     // stages in. int8 weights only in the W8A16 form, which also takes up
     // to kRowdotMaxRowsW8A16 rows as launches of 4.
     const bool w8 = d.b_elem == IREE_MI355X_ELEM_I8;
-    const int64_t rows = d.m < kGemvMaxRows ? d.m : kGemvMaxRows;
+    const int64_t rows = w8 ? rowdot_w8a16_rows(d.m, d.k) : d.m;
     if (d.m > (w8 ? kRowdotMaxRowsW8A16 : kGemvMaxRows) || d.k % 16 != 0 ||
-        !d.a_aligned16 || rows * d.k * 2 > kRowdotMaxXBytes)
+        !d.a_aligned16 || rows < 1 || rows * d.k * 2 > kRowdotMaxXBytes)
       return false;
     return w8 ? d.has_scale != 0 : true;
   }
@@ -512,8 +512,9 @@ int iree_mi355x_plan_matmul(const iree_mi355x_matmul_desc_t *d,
     plan->tile_m = d->m;
     plan->tile_n = 1;
     plan->tile_k = d->k;
-    const int64_t launches = (d->m + kGemvMaxRows - 1) / kGemvMaxRows;
-    plan->lds_bytes = (d->m < kGemvMaxRows ? d->m : kGemvMaxRows) * d->k * 2;
+    const int64_t rows = wb == 1 ? rowdot_w8a16_rows(d->m, d->k) : d->m;
+    const int64_t launches = (d->m + rows - 1) / rows;
+    plan->lds_bytes = rows * d->k * 2;
     plan->workgroups = rowdot_workgroups(d->n) * batch * launches;
     plan->threads = kGemvThreads;
     plan->splits = 1;

@@ -326,19 +326,26 @@ def test_planner_rowdot_gemv(pkg):
             assert p.config_name == b"gemv_rowdot_" + tag + b"_r%d" % m
             assert p.workspace_bytes == 0 and p.splits == 1
             assert p.workgroups == min((n + 7) // 8, 512)
-        for m, n, k in ((3, 4096, 11008),   # x 66 KB: past the LDS it uses
-                        (1, 1000, 1000),    # K not a multiple of 16
+        # x 66 KB past the LDS it uses (W8A16 splits it over launches of 2
+        # rows), K not a multiple of 16, too many rows
+        for m, n, k in ((3, 4096, 11008 if tag != b"w8a16" else 40960),
+                        (1, 1000, 1000),
                         (5 if tag != b"w8a16" else 17, 4096, 4096)):
             p = pkg.plan(pkg.make_desc(a, b, c, m, n, k, pkg.B_TRANSPOSED,
                                        **kw))
             assert b"rowdot" not in p.config_name, (m, n, k)
-    # W8A16 up to 16 rows: launches of at most 4 rows each
-    for m in (5, 8, 16):
+    # W8A16 up to 16 rows: launches of at most 8 rows each, as many as x's
+    # LDS limit allows (7 at K = 4096), dealt evenly
+    p = pkg.plan(pkg.make_desc(F16, I8, F16, 3, 4096, 11008,
+                               pkg.B_TRANSPOSED, has_scale=True))
+    assert p.config_name == b"gemv_rowdot_w8a16_r3"
+    assert p.workgroups == 512 * 2 and p.lds_bytes == 2 * 11008 * 2
+    for m, rows in ((5, 5), (7, 7), (8, 4), (12, 6), (16, 6)):
         p = pkg.plan(pkg.make_desc(F16, I8, F16, m, 11008, 4096,
                                    pkg.B_TRANSPOSED, has_scale=True))
         assert p.config_name == b"gemv_rowdot_w8a16_r%d" % m
-        assert p.workgroups == 512 * ((m + 3) // 4)
-        assert p.lds_bytes == 4 * 4096 * 2
+        assert p.workgroups == 512 * ((m + rows - 1) // rows)
+        assert p.lds_bytes == rows * 4096 * 2
     # x rows must be 16-byte aligned to be staged
     d = pkg.make_desc(F16, F16, F16, 1, 4096, 4096, pkg.B_TRANSPOSED)
     d.a_aligned16 = 0

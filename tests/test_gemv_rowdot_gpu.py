@@ -1,5 +1,5 @@
-"""Row-dot GEMV: skinny matmuls (M <= 4; W8A16 up to 16 as launches of 4
-rows) with the weights stored [N, K] (B_TRANSPOSED, a torch Linear's
+"""Row-dot GEMV: skinny matmuls (M <= 4; W8A16 up to 16 in launches of up
+to 8 rows) with the weights stored [N, K] (B_TRANSPOSED, a torch Linear's
 layout), f16 and W8A16 (csrc/gemv.hip gemv_rowdot_kernel). One wave reduces
 a whole row of W, so K is never split.
 
@@ -70,12 +70,14 @@ def test_rowdot_planned(pkg, oracle, dev, kind, m, n, k):
     assert err <= FP16_BOUND, f"fp16 parity {err:.3e}"
 
 
-@pytest.mark.parametrize("m", [5, 8, 13, 16])
-def test_rowdot_w8a16_row_blocks(pkg, oracle, dev, m):
-    """W8A16 with W [N, K] and 4 < M <= 16: launches of at most 4 rows of x
-    and y each."""
-    n, k = 2048, 4096
-    print(f"rowdot w8a16 blocks m={m}", flush=True)
+@pytest.mark.parametrize("m,k", [(5, 4096), (8, 4096), (13, 4096),
+                                 (16, 4096), (8, 2048), (3, 11008)])
+def test_rowdot_w8a16_row_blocks(pkg, oracle, dev, m, k):
+    """W8A16 with W [N, K] in launches of up to 8 rows of x and y, as many
+    as x's LDS allows (7 at K = 4096, 8 at 2048, 2 at 11008), dealt
+    evenly."""
+    n = 2048
+    print(f"rowdot w8a16 blocks m={m} k={k}", flush=True)
     g = torch.Generator().manual_seed(40 + m)
     x = (torch.randn(m, k, generator=g) * 0.5).half()
     w = torch.randint(-128, 128, (n, k), generator=g).to(torch.int8)
