@@ -8,7 +8,7 @@ Each case runs at a shape the planner gives a column split and checks:
     the whole shape (every element is computed by one tile of either grid,
     in the same K order);
   - the output matches the oracle: int8 bit-exact, f16 within the
-    BASELINE fp16 bound (max|y - y_cpu| / max|y_cpu| <= 2e-3);
+    fp16 parity bound (max|y - y_cpu| / max|y_cpu| <= 2e-3);
   - nothing outside the output view is written.
 The column-indexed operands of the tail launch (B, C, the W8A16 scale, the
 epilogue's bias and multiplier) start n_head columns on; the epilogue and

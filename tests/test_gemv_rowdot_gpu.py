@@ -4,7 +4,7 @@ layout), f16 and W8A16 (csrc/gemv.hip gemv_rowdot_kernel). One wave reduces
 a whole row of W, so K is never split.
 
 Bars: f16 and f32 results max|y - y_cpu| / max|y_cpu| <= 2e-3 (the
-BASELINE fp16 rule) against the oracle; nothing outside the output view is
+fp16 parity bound) against the oracle; nothing outside the output view is
 written.
 """
 import pytest
