@@ -62,8 +62,9 @@ def parse():
     p.add_argument("--no-graph", action="store_true",
                    help="time eager launches instead of one captured graph")
     p.add_argument("--only", choices=["i8", "f16", "f16nn", "gemv", "attn",
-                                      "w8a16", "w8a16_gemm", "runtime",
-                                      "stream", "mfma_ceiling", "config"],
+                                      "w8a16", "w8a16_gemm", "w8a16_nk",
+                                      "runtime", "stream", "mfma_ceiling",
+                                      "config"],
                    help="run one workload (for rocprof passes) and exit")
     p.add_argument("--config", default=None,
                    help="with --only config: the MFMA configuration to run")
@@ -845,6 +846,20 @@ def only(pkg, inputs, dev, args):
         print(json.dumps({"only": w, "ms_per_step": round(ms, 5),
                           "steps": args.steps}), flush=True)
         return
+    elif w == "w8a16_nk":
+        # C5 M=1 with the int8 weights stored [N, K] (a torch Linear's
+        # layout: the row-dot GEMV), rotating copies past the Infinity Cache
+        x, wq, s = (t.to(dev) for t in inputs.c5_w8a16(1))
+        wt = wq.t().contiguous()
+        copies = ROTATE_BYTES // wt.numel() + 1
+        ws = [wt] + [wt.clone() for _ in range(copies - 1)]
+        y = torch.empty(1, wt.shape[0], dtype=torch.float16, device=dev)
+        it = [0]
+
+        def fn():
+            pkg.quantized_matmul(x, ws[it[0] % copies], s, y,
+                                 w_transposed=True)
+            it[0] += 1
     else:
         m = 1 if w == "w8a16" else 512
         x, wq, s = (t.to(dev) for t in inputs.c5_w8a16(m))
