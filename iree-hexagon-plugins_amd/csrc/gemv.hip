@@ -301,12 +301,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemv_splitk_kernel(
 // Row-dot form for W [N,K] (K contiguous: the B_TRANSPOSED layout, a torch
 // Linear's weight): y[r][n] = sum_k x[r][k] W[n][k]. Workgroup g owns the
 // output columns [g P, g P + P) (P = ceil(N / grid)); its waves take them
-// one at a time from an LDS counter. A wave streams column n's row of W in
-// 16-byte segments (lane l: segments l, l + 64, ...; kBatch loads in flight)
-// against x, staged whole in LDS once per workgroup, and sums the row
-// wave-wide; lane 0 then scales (W8A16), applies the epilogue and stores
-// y[r][n] for each r. K is never split: nothing is published and the launch
-// takes no workspace.
+// from an LDS counter, one (f16 weights) or two (int8) at a time. A wave
+// streams those columns' rows of W in 16-byte segments (lane l: segments
+// l, l + 64, ...; kBatch loads a row in flight) against x, staged whole in
+// LDS once per workgroup, and sums each row wave-wide; lane 0 then scales
+// (W8A16), applies the epilogue and stores y[r][n] for each r. K is never
+// split: nothing is published and the launch takes no workspace.
 template <typename WT, int MR, typename OutT>
 __global__ __launch_bounds__(kThreads) void gemv_rowdot_kernel(
     const f16 *__restrict__ X, const WT *__restrict__ W,
@@ -339,26 +339,48 @@ __global__ __launch_bounds__(kThreads) void gemv_rowdot_kernel(
     next_col = (unsigned)n_begin;
   __syncthreads();
   const int segs = K / EPS;  // 16-byte segments of a row of W
+  // Vector elements are copied out before __builtin_bit_cast: a bit cast of
+  // a vector element expression reads element 0 whatever the index (hipcc
+  // 7.2).
+  auto dot = [](float a, int w, int x) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w),
+                                  __builtin_bit_cast(f16x2, x), a, false);
+  };
+  // A wave takes COLS columns at a time: their rows' loads are in flight
+  // together and each x value read from LDS serves all of them. An odd last
+  // column re-reads its own row as the second (its sums are not stored).
+  // Two for int8 weights (C5 M=1 N=11008: 11.9 against 13.9 us for one);
+  // f16 rows, twice the bytes, measured 2-7 % slower with two.
+  constexpr int COLS = sizeof(WT) == 1 ? 2 : 1;
   while (true) {
     int n = 0;
     if (lane == 0)
-      n = (int)atomicAdd(&next_col, 1u);
+      n = (int)atomicAdd(&next_col, (unsigned)COLS);
     n = __builtin_amdgcn_readfirstlane(n);
     if (n >= n_end)
       break;
-    const WT *wrow = W + (int64_t)n * ldw;
-    float acc[MR];
+    const bool two = COLS == 2 && n + 1 < n_end;
+    const WT *wrow[COLS];
+    wrow[0] = W + (int64_t)n * ldw;
+    if constexpr (COLS == 2)
+      wrow[1] = two ? wrow[0] + ldw : wrow[0];
+    float acc[COLS][MR];
 #pragma unroll
-    for (int r = 0; r < MR; ++r)
-      acc[r] = 0.0f;
+    for (int c = 0; c < COLS; ++c)
+#pragma unroll
+      for (int r = 0; r < MR; ++r)
+        acc[c][r] = 0.0f;
     for (int s0 = 0; s0 < segs; s0 += 64 * kBatch) {
-      i32x4 v[kBatch];
+      i32x4 v[COLS][kBatch];
 #pragma unroll
       for (int b = 0; b < kBatch; ++b) {
         const int s = s0 + 64 * b + lane;
-        if (s < segs)
-          v[b] = __builtin_nontemporal_load(
-              (const i32x4 *)(wrow + (int64_t)s * EPS));
+        if (s < segs) {
+#pragma unroll
+          for (int c = 0; c < COLS; ++c)
+            v[c][b] = __builtin_nontemporal_load(
+                (const i32x4 *)(wrow[c] + (int64_t)s * EPS));
+        }
       }
 #pragma unroll
       for (int b = 0; b < kBatch; ++b) {
@@ -366,57 +388,69 @@ __global__ __launch_bounds__(kThreads) void gemv_rowdot_kernel(
         if (s >= segs)
           continue;
         const int k0 = s * EPS;
-        // Vector elements are copied out before __builtin_bit_cast: a bit
-        // cast of a vector element expression reads element 0 whatever the
-        // index (hipcc 7.2).
-        auto dot = [](float a, int w, int x) {
-          return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w),
-                                        __builtin_bit_cast(f16x2, x), a,
-                                        false);
-        };
         if constexpr (sizeof(WT) == 2) {
 #pragma unroll
           for (int r = 0; r < MR; ++r) {
             const i32x4 xv = *(const i32x4 *)(xs + (int64_t)r * K + k0);
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
-              const int wd = v[b][d], xd = xv[d];
-              acc[r] = dot(acc[r], wd, xd);
+              const int xd = xv[d];
+#pragma unroll
+              for (int c = 0; c < COLS; ++c) {
+                const int wd = v[c][b][d];
+                acc[c][r] = dot(acc[c][r], wd, xd);
+              }
             }
           }
         } else {
           // 16 int8 weights as 16 exact f16 values, in k order
-          const i32x4 w0 = i8x8_to_f16x8(i32x2{v[b][0], v[b][1]});
-          const i32x4 w1 = i8x8_to_f16x8(i32x2{v[b][2], v[b][3]});
+          i32x4 w0[COLS], w1[COLS];
+#pragma unroll
+          for (int c = 0; c < COLS; ++c) {
+            w0[c] = i8x8_to_f16x8(i32x2{v[c][b][0], v[c][b][1]});
+            w1[c] = i8x8_to_f16x8(i32x2{v[c][b][2], v[c][b][3]});
+          }
 #pragma unroll
           for (int r = 0; r < MR; ++r) {
             const i32x4 x0 = *(const i32x4 *)(xs + (int64_t)r * K + k0);
             const i32x4 x1 = *(const i32x4 *)(xs + (int64_t)r * K + k0 + 8);
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
-              const int wa = w0[d], xa = x0[d], wb = w1[d], xb = x1[d];
-              acc[r] = dot(acc[r], wa, xa);
-              acc[r] = dot(acc[r], wb, xb);
+              const int xa = x0[d], xb = x1[d];
+#pragma unroll
+              for (int c = 0; c < COLS; ++c) {
+                const int wa = w0[c][d], wb = w1[c][d];
+                acc[c][r] = dot(acc[c][r], wa, xa);
+                acc[c][r] = dot(acc[c][r], wb, xb);
+              }
             }
           }
         }
       }
     }
 #pragma unroll
-    for (int r = 0; r < MR; ++r) {
-      float t = acc[r];
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1)
-        t += __shfl_xor(t, off);
-      acc[r] = t;
-    }
-    if (lane == 0) {
+    for (int c = 0; c < COLS; ++c)
 #pragma unroll
       for (int r = 0; r < MR; ++r) {
-        float t = acc[r];
-        if constexpr (sizeof(WT) == 1)
-          t *= (float)scale[n];
-        store_y(Y + r * ldy + n, epi_apply(t, r, n, epi), accumulate);
+        float t = acc[c][r];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1)
+          t += __shfl_xor(t, off);
+        acc[c][r] = t;
+      }
+    if (lane == 0) {
+#pragma unroll
+      for (int c = 0; c < COLS; ++c) {
+        if (c == 1 && !two)
+          break;
+        const int col = n + c;
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+          float t = acc[c][r];
+          if constexpr (sizeof(WT) == 1)
+            t *= (float)scale[col];
+          store_y(Y + r * ldy + col, epi_apply(t, r, col, epi), accumulate);
+        }
       }
     }
   }
